@@ -1,0 +1,129 @@
+/* C ABI of the MI355X (gfx950) decode-step library, libtfdecode_gfx950.so.
+ *
+ * Conventions for every entry:
+ *   - pointers are device pointers (HBM) unless stated; sizes are plain ints;
+ *   - `stream` is a hipStream_t passed as void*; work is enqueued on it and the
+ *     entry returns without synchronising;
+ *   - nothing is allocated: outputs and workspaces belong to the caller, so any
+ *     sequence of calls can be captured in a HIP graph;
+ *   - the return value is 0 on success, a negative code for a rejected argument
+ *     (-1 bad pointer/argument, -2 bad shape, -3 unsupported size) or a positive
+ *     hipError_t if the launch failed; tfd_last_error() gives the text;
+ *   - values the kernels index memory with (token ids, positions, page-table
+ *     entries) are checked on the device: a bad one sets a bit in `err`
+ *     (TFD_ERR_*) and the access is skipped, never performed out of bounds.
+ *
+ * bf16 tensors are raw 16-bit bfloat16; weight matrices are row-major
+ * [out][in].  The reference these entries replace is TileFoundry's Qwen3-1.7B
+ * runtime, examples/qwen3_1_7b-tilelang/fast/kernels.py (tilelang kernels called
+ * by fast/engine.py:189-217 and wrapped by fast/twin.py:112-226); the citation on
+ * each entry names the reference kernel and the authored @func
+ * (ref_src/model.py) whose semantics it computes.
+ */
+#ifndef TF_DECODE_H
+#define TF_DECODE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TFD_ABI_VERSION 1
+
+/* gemv prologues / epilogues */
+#define TFD_PRO_PLAIN 0  /* x used as given */
+#define TFD_PRO_NORM 1   /* x := Qwen3 RMSNorm(x) * gamma first */
+#define TFD_EPI_STORE 0  /* out[n] = bf16(W[n].x) */
+#define TFD_EPI_RESID 1  /* out[n] = bf16(resid[n] + bf16(W[n].x)) */
+#define TFD_EPI_SWIGLU 2 /* rows are (gate_i, up_i) pairs: out[i] = bf16(bf16(silu(g)) * u) */
+
+/* device error bits */
+#define TFD_ERR_TOKEN_RANGE 1
+#define TFD_ERR_POS_RANGE 2
+#define TFD_ERR_PAGE_RANGE 4
+#define TFD_ERR_STEP_RANGE 8
+
+/* KV paging: a page holds 16 positions; a layer's pool is [pages][kv_heads][16][head_dim]
+ * bf16 and position p of a sequence lives in page page_table[p / 16], row p % 16. */
+#define TFD_PAGE_SIZE 16
+/* context positions owned by one attention block */
+#define TFD_ATTN_SPLIT 64
+
+const char* tfd_last_error(void);
+int tfd_abi_version(void);
+
+/* RMSNorm with the Qwen3 rounding order: out = bf16(bf16(x*rsqrt(mean(x^2)+eps))*gamma).
+ * Replaces fast/kernels.py:58-79 (rms_norm); semantics ref_src/model.py:125-137
+ * (input_rms_norm) and :289-298 (final_rms_norm).  n % 8 == 0, n <= 8192. */
+int tfd_rmsnorm_bf16(const void* x, const void* gamma, void* out, int n, float eps, void* stream);
+
+/* out[0:hidden] = table[ids[0]].  Replaces fast/kernels.py:579-588 (embed);
+ * semantics ref_src/model.py:279-287.  An id outside [0, vocab) sets TFD_ERR_TOKEN_RANGE. */
+int tfd_embed_bf16(const void* table, const int64_t* ids, void* out, int hidden, int vocab,
+                   int32_t* err, void* stream);
+
+/* y = W x over N rows of length K, with an optional RMSNorm prologue and a fused
+ * epilogue (TFD_PRO_*, TFD_EPI_*).  Replaces fast/kernels.py:123-145 (gemv),
+ * :154-207 (gemv_attn_combine, minus the merge, which tfd_attn_pv_combine_paged
+ * owns), :210-257 (gemv_silu) and :82-116 (resid_rms_norm, folded into the
+ * prologue/epilogue); semantics ref_src/model.py:159-171, 213-215, 227-234, 264-266.
+ * K % 8 == 0, K <= 8192; gamma only with TFD_PRO_NORM; resid only with TFD_EPI_RESID. */
+int tfd_gemv_bf16(const void* x, const void* gamma, const void* w, const void* resid, void* out,
+                  int K, int N, int prologue, int epilogue, float eps, void* stream);
+
+/* Final norm, logits = bf16(W xn) for V rows (written as f32), and each of the
+ * `nblocks` blocks' largest logit with the lowest index on ties.  Replaces
+ * fast/kernels.py:260-321 (lm_head); semantics ref_src/model.py:300-305 and
+ * generation.py:24-26.  block_val / block_idx hold nblocks entries. */
+int tfd_lm_head_argmax_bf16(const void* x, const void* gamma, const void* w, float* logits,
+                            float* block_val, int32_t* block_idx, int K, int V, int nblocks,
+                            float eps, void* stream);
+
+/* Greedy pick over the block partials (lowest index on ties); sam[pos] = pick;
+ * ids[0] = inp[pos+1] while pos+1 < prompt_len, else the pick; pos += 1; and
+ * hid = table[ids[0]] (the next step's embedding).  Replaces fast/kernels.py:591-637
+ * (sample_step) plus the next step's embed. */
+int tfd_argmax_finalize(const float* block_val, const int32_t* block_idx, int nblocks,
+                        const int32_t* inp, const int32_t* prompt_len, int64_t* ids,
+                        int32_t* pos, int32_t* sam, int nsteps, const void* table, void* hid,
+                        int hidden, int vocab, int32_t* err, void* stream);
+
+/* Attention part 1 over a paged cache.  From the bf16 [q | k | v] projection:
+ * per-head q/k RMSNorm (gamma_q, gamma_k), RoPE at *rope_pos from the bf16 cos/sin
+ * tables [rope_rows][head_dim], q_s = bf16(q_rope * scale); writes this token's
+ * k_rope and v at position *cache_len of the cache; scores every prior position
+ * j < *cache_len: scores[h][j] = bf16(sum_d bf16(q_s[h][d] * K[j][d])), the max per
+ * TFD_ATTN_SPLIT split (split_max[nsplit][heads]) and the new key's score
+ * (score_new[heads]).  Grid is nsplit x kv_heads; nsplit * 64 >= max_pages * 16.
+ * Replaces fast/kernels.py:328-411 (qk_rope_cache) and the score half of :418-501
+ * (attn_partial); semantics ref_src/model.py:172-198. */
+int tfd_attn_rope_scores_paged(const void* qkv, const void* gamma_q, const void* gamma_k,
+                               const void* cos_table, const void* sin_table, int rope_rows,
+                               const int32_t* rope_pos, const int32_t* cache_len,
+                               const int32_t* page_table, int max_pages, void* k_pool,
+                               void* v_pool, int num_pages, int heads, int kv_heads,
+                               int head_dim, float scale, float eps, float* scores,
+                               int score_stride, float* split_max, float* score_new, int nsplit,
+                               int32_t* err, void* stream);
+
+/* Attention part 2: joint peak M, p_j = bf16(exp(bf16(s_j - M))), per-split sums of
+ * p and bf16(p * V) in f32 (part_sum[nsplit][heads], part_out[nsplit][heads][head_dim]);
+ * the last block per kv head (counted in counters[kv_heads], which must start at 0
+ * and are left at 0) merges the splits with the new token's term:
+ * attn = bf16(bf16(bf16(sum pV) + bf16(p_new v_new)) / bf16(bf16(sum p) + p_new)).
+ * Replaces the softmax/PV half of fast/kernels.py:418-501 (attn_partial) and the
+ * merge of :504-540 / :154-207; semantics ref_src/model.py:200-212. */
+int tfd_attn_pv_combine_paged(const void* qkv, const int32_t* cache_len,
+                              const int32_t* page_table, int max_pages, const void* v_pool,
+                              int num_pages, int heads, int kv_heads, int head_dim,
+                              const float* scores, int score_stride, const float* split_max,
+                              const float* score_new, float* part_sum, float* part_out,
+                              int nsplit, int32_t* counters, void* attn_out, int32_t* err,
+                              void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TF_DECODE_H */

@@ -1,0 +1,96 @@
+"""ctypes binding of ``libtfdecode_gfx950.so`` (the C ABI in ``include/tf_decode.h``).
+
+There is no fallback: if the library is missing, or was built for an older ABI,
+every caller gets a ``RuntimeError`` naming the build command.  A call that
+returns non-zero raises ``TFDError`` carrying the library's own message.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_void_p
+from functools import lru_cache
+from pathlib import Path
+
+from .build import LIB
+
+ABI_VERSION = 1
+
+PRO_PLAIN, PRO_NORM = 0, 1
+EPI_STORE, EPI_RESID, EPI_SWIGLU = 0, 1, 2
+ERR_TOKEN_RANGE, ERR_POS_RANGE, ERR_PAGE_RANGE, ERR_STEP_RANGE = 1, 2, 4, 8
+PAGE_SIZE = 16
+ATTN_SPLIT = 64
+
+P = c_void_p
+I = c_int
+F = c_float
+
+#: argtypes of every entry, in header order (restype is int unless named here)
+SIGNATURES: dict[str, list] = {
+    "tfd_abi_version": [],
+    "tfd_last_error": [],
+    "tfd_rmsnorm_bf16": [P, P, P, I, F, P],
+    "tfd_embed_bf16": [P, P, P, I, I, P, P],
+    "tfd_gemv_bf16": [P, P, P, P, P, I, I, I, I, F, P],
+    "tfd_lm_head_argmax_bf16": [P, P, P, P, P, P, I, I, I, F, P],
+    "tfd_argmax_finalize": [P, P, I, P, P, P, P, P, I, P, P, I, I, P, P],
+    "tfd_attn_rope_scores_paged": [P, P, P, P, P, I, P, P, P, I, P, P, I, I, I, I, F, F, P, I,
+                                   P, P, I, P, P],
+    "tfd_attn_pv_combine_paged": [P, P, P, I, P, I, I, I, I, P, I, P, P, P, P, I, P, P, P, P],
+}
+RESTYPES = {"tfd_last_error": ctypes.c_char_p}
+
+
+class TFDError(RuntimeError):
+    """A library entry rejected its arguments or failed to launch."""
+
+    def __init__(self, name: str, code: int, message: str):
+        super().__init__(f"{name} returned {code}: {message}")
+        self.code = code
+
+
+class _Checked:
+    """Wraps the CDLL so every int-returning entry raises on a non-zero result."""
+
+    def __init__(self, dll: ctypes.CDLL):
+        self._dll = dll
+        for name, args in SIGNATURES.items():
+            fn = getattr(dll, name)
+            fn.argtypes = args
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
+
+    def last_error(self) -> str:
+        return self._dll.tfd_last_error().decode(errors="replace")
+
+    def __getattr__(self, name):
+        fn = getattr(self._dll, name)
+        if name in RESTYPES or name == "tfd_abi_version":
+            return fn
+
+        def call(*args):
+            rc = fn(*args)
+            if rc != 0:
+                raise TFDError(name, rc, self.last_error())
+            return rc
+
+        return call
+
+
+@lru_cache(maxsize=1)
+def lib() -> _Checked:
+    """The loaded library (loaded once per process)."""
+    path = Path(LIB)
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is not built: run `python -m tilefoundry_amd.build` "
+            "(or __graft_entry__.build()) first; there is no non-HIP fallback")
+    dll = ctypes.CDLL(str(path))
+    got = dll.tfd_abi_version()
+    if got != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI {got}, this package expects {ABI_VERSION}: rebuild it")
+    return _Checked(dll)
+
+
+def ptr(t) -> int:
+    """Device address of a torch tensor (0 for None)."""
+    return 0 if t is None else t.data_ptr()

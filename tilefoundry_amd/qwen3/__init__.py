@@ -1,0 +1,6 @@
+"""Qwen3 dense decoder on the gfx950 kernels."""
+from .config import QWEN3_1_7B, TINY, Qwen3Config
+from .weights import declared_shapes, synthetic_weights, validate
+
+__all__ = ["Qwen3Config", "QWEN3_1_7B", "TINY", "declared_shapes", "synthetic_weights",
+           "validate"]

@@ -1,0 +1,297 @@
+"""One captured batch-1 decode step over a paged KV cache, replayed per token.
+
+The same shape as the reference's fast engine
+(``examples/qwen3_1_7b-tilelang/fast/engine.py:69-301``): a fixed-capacity cache
+whose write position advances, the position in a one-element device tensor, and
+the whole step -- every layer, the head, the greedy pick and the next token's
+embedding -- recorded once into a HIP graph (``torch.cuda.graph``) and replayed.
+The last kernel writes the pick back as the next input, or the next prompt
+token while the prompt lasts, so walking the prompt and continuing past it need
+no host round trip.
+
+What differs, MI355X-first:
+
+* the KV cache is paged: per layer a pool ``[pages][HKV][16][D]`` bf16 and a
+  device page table; a position's row is ``table[p // 16] * 16 + p % 16``;
+* six kernels per layer instead of eight, the norms folded into the
+  projections that consume them (see ``csrc/qwen3_decode.hip``);
+* every kernel is hand-written HIP for gfx950 reached through the C ABI in
+  ``include/tf_decode.h``; there is no torch compute on the step.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from time import perf_counter
+
+import torch
+
+from .. import _lib
+from .._lib import lib, ptr
+from .config import Qwen3Config
+from .weights import head_rows, pack_layer, validate
+
+
+@dataclass(frozen=True)
+class Generated:
+    """A continuation and the timing of the part that produced it (engine.py:55-66)."""
+
+    tokens: list[int]
+    seconds: float
+    prefill_seconds: float
+    prompt_steps: int
+    logits: torch.Tensor | None = None   # [len(tokens), V] f32, when recorded
+
+    @property
+    def tokens_per_second(self) -> float:
+        return len(self.tokens) / self.seconds if self.seconds > 0 else float("inf")
+
+
+def _round_up(n: int, m: int) -> int:
+    return (n + m - 1) // m * m
+
+
+def bf16_scale(head_dim: int) -> float:
+    """``head_dim ** -0.5`` as the bf16 value the reference feeds (model.py:384-386)."""
+    return torch.tensor(head_dim ** -0.5, dtype=torch.bfloat16).item()
+
+
+class Engine:
+    """A loaded Qwen3 dense decoder and one captured decode step over it."""
+
+    def __init__(self, cfg: Qwen3Config, weights: dict[str, torch.Tensor], *,
+                 device: str = "cuda:0", max_new: int = 2048, prompt_room: int = 512,
+                 page_seed: int | None = 0, graph: bool = True,
+                 lm_head_blocks: int = 2048):
+        if cfg.dtype != torch.bfloat16:
+            raise ValueError(f"the HIP engine runs bf16 weights; config has {cfg.dtype}")
+        validate(cfg, weights)
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.L = cfg.num_hidden_layers
+        self.H, self.V = cfg.hidden_size, cfg.vocab_size
+        self.HQ, self.HKV, self.D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        self.I = cfg.intermediate_size
+        self.eps = float(cfg.rms_norm_eps)
+        self.scale = bf16_scale(self.D)
+
+        self.nsteps = max_new + prompt_room
+        self.cap = _round_up(self.nsteps, _lib.ATTN_SPLIT)
+        self.max_pages = self.cap // _lib.PAGE_SIZE
+        self.nsplit = self.cap // _lib.ATTN_SPLIT
+        if self.cap > cfg.max_position_embeddings:
+            raise ValueError(f"capacity {self.cap} exceeds the rope table "
+                             f"({cfg.max_position_embeddings} positions)")
+        self.nb = lm_head_blocks
+        self._lib = lib()
+        self._pack(weights, page_seed)
+        self._buffers()
+        self.graph = None
+        if graph:
+            self._capture()
+
+    # ---------------------------------------------------------------- weights
+    def _pack(self, weights, page_seed):
+        dev = self.device
+        self.layers = [pack_layer(weights, i, dev) for i in range(self.L)]
+        self.w_embed, self.w_head = head_rows(weights, dev)
+        self.gamma_final = weights["gamma_final"].to(dev).contiguous()
+        # the rope tables exactly as _generation_rope builds them (model.py:107-120)
+        d = self.D
+        inv = 1.0 / (self.cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+        ph = torch.outer(torch.arange(self.cap, dtype=torch.float32), inv)
+        ph = torch.cat((ph, ph), dim=-1)
+        self.cos = ph.cos().to(torch.bfloat16).to(dev).contiguous()
+        self.sin = ph.sin().to(torch.bfloat16).to(dev).contiguous()
+        # a page table: a seeded permutation of the pool, so every read goes
+        # through the indirection (page_seed=None keeps pages in order)
+        if page_seed is None:
+            table = torch.arange(self.max_pages, dtype=torch.int32)
+        else:
+            g = torch.Generator().manual_seed(page_seed)
+            table = torch.randperm(self.max_pages, generator=g).to(torch.int32)
+        self.page_table = table.to(dev)
+
+    # ---------------------------------------------------------------- buffers
+    def _buffers(self):
+        dev, bf, f32, i32 = self.device, torch.bfloat16, torch.float32, torch.int32
+
+        def z(*shape, dtype=bf):
+            return torch.zeros(*shape, device=dev, dtype=dtype)
+
+        self.hid = z(self.H)
+        self.h1 = z(self.H)
+        self.qkv = z(self.cfg.qkv_size)
+        self.attn = z(self.HQ * self.D)
+        self.hmid = z(self.I)
+        self.kpool = z(self.L, self.max_pages, self.HKV, _lib.PAGE_SIZE, self.D)
+        self.vpool = z(self.L, self.max_pages, self.HKV, _lib.PAGE_SIZE, self.D)
+        self.scores = z(self.HQ, self.cap, dtype=f32)
+        self.smax = z(self.nsplit, self.HQ, dtype=f32)
+        self.snew = z(self.HQ, dtype=f32)
+        self.psum = z(self.nsplit, self.HQ, dtype=f32)
+        self.pout = z(self.nsplit, self.HQ, self.D, dtype=f32)
+        self.counters = z(self.HKV, dtype=i32)
+        self.logits = z(self.V, dtype=f32)
+        self.bv = z(self.nb, dtype=f32)
+        self.bi = z(self.nb, dtype=i32)
+        self.pos = z(1, dtype=i32)
+        self.ids = z(1, dtype=torch.int64)
+        self.inp = z(self.nsteps, dtype=i32)
+        self.sam = z(self.nsteps, dtype=i32)
+        self.plen = z(1, dtype=i32)
+        self.err = z(1, dtype=i32)
+
+    # ---------------------------------------------------------------- the step
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _layer(self, i: int, s: int):
+        """One decoder layer (model.py:236-266) as six launches."""
+        L, w = self._lib, self.layers[i]
+        H, I, D = self.H, self.I, self.D
+        kp, vp = self.kpool[i], self.vpool[i]
+        L.tfd_gemv_bf16(ptr(self.hid), ptr(w["gamma_in"]), ptr(w["w_qkv"]), None, ptr(self.qkv),
+                        H, self.cfg.qkv_size, _lib.PRO_NORM, _lib.EPI_STORE, self.eps, s)
+        L.tfd_attn_rope_scores_paged(
+            ptr(self.qkv), ptr(w["gamma_q"]), ptr(w["gamma_k"]), ptr(self.cos), ptr(self.sin),
+            self.cap, ptr(self.pos), ptr(self.pos), ptr(self.page_table), self.max_pages,
+            ptr(kp), ptr(vp), self.max_pages, self.HQ, self.HKV, D, self.scale, self.eps,
+            ptr(self.scores), self.cap, ptr(self.smax), ptr(self.snew), self.nsplit,
+            ptr(self.err), s)
+        L.tfd_attn_pv_combine_paged(
+            ptr(self.qkv), ptr(self.pos), ptr(self.page_table), self.max_pages, ptr(vp),
+            self.max_pages, self.HQ, self.HKV, D, ptr(self.scores), self.cap, ptr(self.smax),
+            ptr(self.snew), ptr(self.psum), ptr(self.pout), self.nsplit, ptr(self.counters),
+            ptr(self.attn), ptr(self.err), s)
+        L.tfd_gemv_bf16(ptr(self.attn), None, ptr(w["w_o"]), ptr(self.hid), ptr(self.h1),
+                        self.HQ * D, H, _lib.PRO_PLAIN, _lib.EPI_RESID, self.eps, s)
+        L.tfd_gemv_bf16(ptr(self.h1), ptr(w["gamma_post"]), ptr(w["w_gu"]), None, ptr(self.hmid),
+                        H, 2 * I, _lib.PRO_NORM, _lib.EPI_SWIGLU, self.eps, s)
+        L.tfd_gemv_bf16(ptr(self.hmid), None, ptr(w["w_down"]), ptr(self.h1), ptr(self.hid),
+                        I, H, _lib.PRO_PLAIN, _lib.EPI_RESID, self.eps, s)
+
+    def _step(self, record: list | None = None):
+        """One decode step: every layer, then head + pick + next embedding."""
+        s = self._stream()
+        if record is not None:
+            record.append(self.hid.clone())
+        for i in range(self.L):
+            self._layer(i, s)
+            if record is not None:
+                record.append(self.hid.clone())
+        self._lib.tfd_lm_head_argmax_bf16(ptr(self.hid), ptr(self.gamma_final), ptr(self.w_head),
+                                          ptr(self.logits), ptr(self.bv), ptr(self.bi), self.H,
+                                          self.V, self.nb, self.eps, s)
+        self._lib.tfd_argmax_finalize(ptr(self.bv), ptr(self.bi), self.nb, ptr(self.inp),
+                                      ptr(self.plen), ptr(self.ids), ptr(self.pos),
+                                      ptr(self.sam), self.nsteps, ptr(self.w_embed),
+                                      ptr(self.hid), self.H, self.V, ptr(self.err), s)
+
+    def _embed_current(self):
+        self._lib.tfd_embed_bf16(ptr(self.w_embed), ptr(self.ids), ptr(self.hid), self.H, self.V,
+                                 ptr(self.err), self._stream())
+
+    def _capture(self):
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self._load_prompt([0])
+            for _ in range(3):
+                self._step()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+        torch.cuda.synchronize(self.device)
+        self._reset()
+
+    def replay(self):
+        """One decode step (graph replay, or direct launches without a graph)."""
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._step()
+
+    # ------------------------------------------------------------- generation
+    def _reset(self):
+        self.pos.zero_()
+        self.sam.zero_()
+        self.err.zero_()
+
+    def _load_prompt(self, prompt_ids: list[int]):
+        pl = len(prompt_ids)
+        self._reset()
+        self.inp.zero_()
+        self.inp[:pl] = torch.tensor(prompt_ids, dtype=torch.int32).to(self.device)
+        self.plen.fill_(pl)
+        self.ids.fill_(int(prompt_ids[0]))
+        self._embed_current()
+
+    def check_errors(self):
+        """Raise if a kernel flagged an out-of-range index since the last reset."""
+        e = int(self.err.item())
+        if e:
+            names = [n for bit, n in ((1, "token id"), (2, "position"), (4, "page-table entry"),
+                                      (8, "step")) if e & bit]
+            raise RuntimeError(f"decode kernels flagged an out-of-range {', '.join(names)}")
+
+    def generate(self, prompt_ids: list[int], max_new: int,
+                 record_logits: bool = False) -> Generated:
+        """Walk *prompt_ids*, then continue for *max_new* greedy tokens
+        (engine.py:239-271); the timing covers the continuation only."""
+        pl = len(prompt_ids)
+        if pl < 1:
+            raise ValueError("decode needs a prompt of at least one token")
+        if pl + max_new > self.nsteps:
+            raise ValueError(f"prompt {pl} + {max_new} new exceeds this engine's "
+                             f"{self.nsteps} steps")
+        if any(not 0 <= int(t) < self.V for t in prompt_ids):
+            raise ValueError(f"prompt ids must lie in [0, {self.V})")
+        self._load_prompt(prompt_ids)
+        hist = (torch.empty(max_new, self.V, device=self.device, dtype=torch.float32)
+                if record_logits else None)
+        torch.cuda.synchronize(self.device)
+        t0 = perf_counter()
+        for _ in range(pl - 1):
+            self.replay()
+        torch.cuda.synchronize(self.device)
+        t1 = perf_counter()
+        for k in range(max_new):
+            self.replay()
+            if hist is not None:
+                hist[k].copy_(self.logits)
+        torch.cuda.synchronize(self.device)
+        t2 = perf_counter()
+        self.check_errors()
+        out = self.sam[pl - 1: pl - 1 + max_new].tolist()
+        return Generated(out, t2 - t1, t1 - t0, pl, None if hist is None else hist.cpu())
+
+    def logits_for(self, prompt_ids: list[int]) -> torch.Tensor:
+        """The logits after consuming every token of *prompt_ids* (f32 copy)."""
+        self._load_prompt(prompt_ids)
+        for _ in range(len(prompt_ids)):
+            self.replay()
+        torch.cuda.synchronize(self.device)
+        self.check_errors()
+        return self.logits.clone()
+
+    def trace(self, prompt_ids: list[int]) -> list[torch.Tensor]:
+        """Hidden state entering the stack and leaving each layer, at the last
+        prompt position (engine.py:273-287)."""
+        self._load_prompt(prompt_ids)
+        for _ in range(len(prompt_ids) - 1):
+            self.replay()
+        rec: list[torch.Tensor] = []
+        self._step(record=rec)
+        torch.cuda.synchronize(self.device)
+        return rec
+
+    # ------------------------------------------------------------ accounting
+    def weight_bytes_per_step(self) -> int:
+        return self.cfg.weight_bytes_per_step()
+
+    def kv_bytes_at(self, pos: int) -> int:
+        """KV bytes a step at position *pos* touches: reads of pos prior
+        positions plus the write of its own, every layer."""
+        return self.cfg.kv_bytes_per_position() * (pos + 1)
