@@ -1,0 +1,203 @@
+"""Decode throughput of the Qwen3-1.7B-architecture model at batch 1.
+
+    python bench.py [--gpus 1] [--steps 2048] [--warmup 64]
+
+A step is one decode token: one replay of the captured step (28 layers, the
+head, the greedy pick).  The workload is BASELINE's config 2: bf16 weights drawn
+N(0, 0.02) from seed 0 (every parameter, norm scales included), tied
+embeddings, a 32-token uniform-random prompt (seed 0), a 16-token-page KV cache,
+and `--steps` greedy new tokens (2048 by default) timed after the prompt walk.
+Weights are resident in HBM before the timed region starts.
+
+Prints one JSON line: the metric, the whole-step HBM roofline fraction from
+algorithmic bytes (weights once + the KV each step touches), the dominant
+kernel's roofline (the gate/up projection, timed on its own over all 28 layers'
+weights with HIP events on its stream), and the CPU oracle timed on the host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK = 8.0e12          # MI355X HBM3E, bytes/s
+REFERENCE_TOKS = 612.5     # the reference's published rate for this metric (H200)
+METRIC = "decode tok/s bs=1 Qwen3-1.7B-arch bf16; achieved HBM TB/s vs 8 TB/s peak"
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def time_gate_up(eng, rounds: int) -> float:
+    """Average duration (s) of the gate/up GEMV launch, rotating over every
+    layer's weights (1.4 GB, past the 256 MB last-level cache), HIP events on
+    the launch stream."""
+    import torch
+
+    from tilefoundry_amd import _lib
+    from tilefoundry_amd._lib import ptr
+
+    stream = torch.cuda.current_stream(eng.device)
+    s = stream.cuda_stream
+    L = eng._lib
+
+    def launch(i):
+        w = eng.layers[i]
+        L.tfd_gemv_bf16(ptr(eng.h1_rows[i]), ptr(w["gamma_post"]), ptr(w["w_gu"]), None,
+                        ptr(eng.hmid_rows[i]),
+                        eng.H, 2 * eng.I, _lib.PRO_NORM, _lib.EPI_SWIGLU, eng.eps, s)
+
+    for i in range(eng.L):
+        launch(i)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(rounds):
+        for i in range(eng.L):
+            launch(i)
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / 1e3 / (rounds * eng.L)
+
+
+def cpu_baseline(weights, prompt, budget_s: float) -> dict:
+    """The CPU oracle (a restatement of the authored HIR run the way the
+    reference evaluator runs it) on this host's cores: decode steps over the
+    same weights and prompt until *budget_s* of work is done."""
+    import torch
+
+    from oracle import qwen3_hir as O
+
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    orc = O.Qwen3Oracle(O.C2, weights)
+    caches = orc.init_caches()
+    ids = torch.tensor(prompt, dtype=torch.int64)
+    O.generation_rope(O.C2)
+    steps, t0 = 0, time.perf_counter()
+    with torch.no_grad():
+        while steps < len(prompt):
+            args = orc.prepare_inputs_for_generation(ids, steps, caches)
+            _, fresh = orc.forward(*args)
+            caches = orc.append_cache(caches, fresh)
+            steps += 1
+            if time.perf_counter() - t0 >= budget_s:
+                break
+    dt = time.perf_counter() - t0
+    return {"value": round(steps / dt, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} decode steps (positions 0..{steps - 1} of the 32-token prompt, "
+                      f"same weights) of the oracle in torch on {threads} threads of "
+                      f"'{cpu_model()}', {dt:.1f} s"}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2048)
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--cpu-budget", type=float, default=20.0,
+                    help="seconds of CPU-oracle work for the cpu_baseline leg (0 skips it)")
+    ap.add_argument("--kernel-rounds", type=int, default=20)
+    ap.add_argument("--mode", default="persistent", choices=("persistent", "graph"),
+                    help="persistent: one cooperative launch per run of steps; graph: a "
+                         "captured graph of per-phase launches replayed per token")
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every box here "
+              "has one MI355X); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from tilefoundry_amd.qwen3 import QWEN3_1_7B, synthetic_weights
+    from tilefoundry_amd.qwen3.engine import Engine
+
+    cfg = QWEN3_1_7B
+    t0 = time.perf_counter()
+    weights = synthetic_weights(cfg, seed=0)
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, cfg.vocab_size, (32,), generator=g).tolist()
+    max_new = max(args.steps, 2048)
+    eng = Engine(cfg, weights, device="cuda:0", max_new=max_new, prompt_room=len(prompt),
+                 mode=args.mode)
+    print(f"[bench] weights + engine + capture {time.perf_counter() - t0:.1f}s", file=sys.stderr,
+          flush=True)
+
+    # untimed warmup: a short generation from the same prompt
+    if args.warmup:
+        eng.generate(prompt, min(args.warmup, max_new))
+    # the timed region: walk the prompt (untimed), then exactly --steps replays
+    eng._load_prompt(prompt)
+    eng.run_steps(len(prompt) - 1)
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    eng.run_steps(args.steps)
+    torch.cuda.synchronize()
+    seconds = time.perf_counter() - start
+    eng.check_errors()
+    tokens = eng.sam[len(prompt) - 1: len(prompt) - 1 + args.steps].tolist()
+
+    # algorithmic bytes: weights once per step + K/V of every position read and the new one written
+    pl = len(prompt)
+    w_bytes = cfg.weight_bytes_per_step()
+    kv_bytes = sum(eng.kv_bytes_at(p) for p in range(pl - 1, pl - 1 + args.steps))
+    step_bytes = w_bytes + kv_bytes / args.steps
+    tok_s = args.steps / seconds
+    step_bw = step_bytes * tok_s
+
+    gu_s = time_gate_up(eng, args.kernel_rounds)
+    gu_bytes = 2 * cfg.intermediate_size * cfg.hidden_size * 2 + 2 * cfg.hidden_size * 2 \
+        + cfg.intermediate_size * 2
+    gu_bw = gu_bytes / gu_s
+
+    line = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * seconds / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(tok_s / REFERENCE_TOKS, 3),
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) weights seed 0, random 32-token prompt)",
+        "config": {"workload": "C2: Qwen3-1.7B-arch bf16 decode, batch 1, 32-token prompt, "
+                               f"{args.steps} greedy new tokens, 16-token KV pages",
+                   "mode": args.mode,
+                   "batch": 1, "prompt": pl, "new_tokens": args.steps,
+                   "layers": cfg.num_hidden_layers, "hidden": cfg.hidden_size,
+                   "vocab": cfg.vocab_size},
+        "step_roofline": {"bound": "hbm", "bytes_per_step": int(step_bytes),
+                          "achieved": round(step_bw / 1e9, 1), "peak": HBM_PEAK / 1e9,
+                          "unit": "GB/s", "frac": round(step_bw / HBM_PEAK, 4),
+                          "roofline_tok_s": round(HBM_PEAK / step_bytes, 1)},
+        "roofline": {"bound": "hbm", "kernel": "k_gemv<4,4,norm,swiglu> (gate/up, 12288x2048)",
+                     "achieved": round(gu_bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": round(gu_bw / HBM_PEAK, 4), "traffic": None,
+                     "bytes_per_launch": gu_bytes, "avg_us": round(gu_s * 1e6, 3)},
+        "first_tokens": tokens[:8],
+    }
+    if args.cpu_budget > 0:
+        line["cpu_baseline"] = cpu_baseline(weights, prompt, args.cpu_budget)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

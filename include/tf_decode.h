@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TFD_ABI_VERSION 1
+#define TFD_ABI_VERSION 3
 
 /* gemv prologues / epilogues */
 #define TFD_PRO_PLAIN 0  /* x used as given */
@@ -121,6 +121,86 @@ int tfd_attn_pv_combine_paged(const void* qkv, const int32_t* cache_len,
                               const float* score_new, float* part_sum, float* part_out,
                               int nsplit, int32_t* counters, void* attn_out, int32_t* err,
                               void* stream);
+
+/* ---- persistent decode step ------------------------------------------------
+ * One cooperative launch runs `steps` whole decode steps (every layer, the head,
+ * the greedy pick, the next embedding) with grid barriers between dependent
+ * phases, instead of ~6 launches per layer.  It computes exactly what the
+ * per-kernel entries above compute, phase for phase (the same device code runs
+ * on the same data partition), so the two paths give identical bits.
+ * Replaces the captured step of fast/engine.py:189-217 (graph.replay per token). */
+typedef struct TfdLayer {
+  const void* w_qkv;      /* [HQ*D + 2*HKV*D][H] bf16: q rows, k rows, v rows */
+  const void* w_o;        /* [H][HQ*D] */
+  const void* w_gu;       /* [2*I][H], gate_i at row 2i and up_i at row 2i+1 */
+  const void* w_down;     /* [H][I] */
+  const void* gamma_in;   /* [H] */
+  const void* gamma_post; /* [H] */
+  const void* gamma_q;    /* [D] */
+  const void* gamma_k;    /* [D] */
+  void* k_pool;           /* [num_pages][HKV][16][D] */
+  void* v_pool;
+} TfdLayer;
+
+typedef struct TfdDecodeArgs {
+  const TfdLayer* layers; /* device array of n_layers entries */
+  int n_layers, hidden, heads, kv_heads, head_dim, intermediate, vocab;
+  float eps, scale;       /* rms eps; the bf16 value of head_dim^-0.5 */
+  const void* w_embed;    /* [V][H] */
+  const void* w_head;     /* [V][H] (the embedding table when tied) */
+  const void* gamma_final;
+  const void* cos_table;  /* [rope_rows][D] bf16 */
+  const void* sin_table;
+  int rope_rows;
+  const int32_t* page_table;
+  int max_pages, num_pages;
+  /* Activations, one row per layer so every address is written once per step:
+   * hid [n_layers + 1][H] (row 0 is the step's input embedding row, row l + 1 the
+   * output of layer l), h1 [n_layers][H], qkv [n_layers][HQ*D + 2*HKV*D],
+   * attn [n_layers][HQ*D], hmid [n_layers][I]; all bf16. */
+  void* hid;
+  void* h1;
+  void* qkv;
+  void* attn;
+  void* hmid;
+  float* scores;          /* [HQ][score_stride] */
+  int score_stride;
+  float* split_max;       /* [nsplit][HQ] */
+  float* score_new;       /* [HQ] */
+  float* part_sum;        /* [nsplit][HQ] */
+  float* part_out;        /* [nsplit][HQ][D] */
+  int nsplit;
+  int32_t* counters;      /* [HKV], zero */
+  float* logits;          /* [V] */
+  float* block_val;       /* [>= grid blocks] */
+  int32_t* block_idx;
+  int64_t* ids;
+  int32_t* pos;
+  const int32_t* inp;     /* [nsteps] prompt ids */
+  const int32_t* prompt_len;
+  int32_t* sam;           /* [nsteps] picks */
+  int nsteps;
+  uint32_t* barrier;      /* TFD_BARRIER_WORDS x uint32, zeroed before every launch */
+  int32_t* err;
+  /* Optional phase timeline (may be null): for the first timeline_steps steps of
+   * a launch, block 0 records the 100 MHz device wall clock before and after
+   * every grid barrier, TFD_TIMELINE_STAMPS(n_layers) stamps per step. */
+  uint64_t* timeline;
+  int timeline_steps;
+} TfdDecodeArgs;
+
+/* stamps per step: per layer 6 barriers x (arrive, leave), then head and pick */
+#define TFD_TIMELINE_STAMPS(n_layers) (12 * (n_layers) + 4)
+
+#define TFD_ERR_BARRIER 16 /* a grid barrier waited past its bound; the launch gave up */
+#define TFD_BARRIER_WORDS 1280
+
+/* Run `steps` decode steps.  nblocks <= 0 picks one block per compute unit.
+ * Returns -3 if the shape has no persistent instance (hidden must equal
+ * heads * head_dim) or the grid cannot be co-resident. */
+int tfd_decode_persistent(const TfdDecodeArgs* args, int steps, int nblocks, void* stream);
+/* The grid tfd_decode_persistent(args, ., 0, .) uses (block_val must hold this many). */
+int tfd_decode_persistent_grid(void);
 
 #ifdef __cplusplus
 }

@@ -6,6 +6,8 @@ configs here are config 1's shape at bf16 and the Qwen3-1.7B layer shape at two
 layers; the full-depth model is checked against committed golden fixtures in
 test_gpu_golden.py.
 """
+import math
+
 import pytest
 import torch
 
@@ -29,12 +31,57 @@ def _prompt(n, vocab, seed=0):
     return torch.randint(0, vocab, (n,), generator=g).tolist()
 
 
-def _check_run(eng_run, orc_run, steps):
-    assert eng_run.tokens[:steps] == orc_run.tokens[:steps], (
-        eng_run.tokens[:steps], orc_run.tokens[:steps], orc_run.margins[:steps])
+def _ulp_at(v: float) -> float:
+    return 2.0 ** (math.floor(math.log2(abs(v))) - 7) if v else 2.0 ** -133
+
+
+def _first_divergence(a, b):
+    for k, (x, y) in enumerate(zip(a, b)):
+        if x != y:
+            return k
+    return None
+
+
+def _check_run(eng_run, orc_run, steps, strict=True):
+    """Free-running greedy parity.  strict: all *steps* tokens identical.
+    Otherwise the first divergence must sit where the oracle's own bf16 logits
+    put the engine's pick within one ulp of its pick (a tie at the reference's
+    output precision, decided by f32 summation order)."""
+    k = _first_divergence(eng_run.tokens[:steps], orc_run.tokens[:steps])
+    upto = steps if k is None else k + 1
+    for j in range(upto):
+        r = report(eng_run.logits[j], orc_run.logits[j])
+        assert r["max_rel"] <= 2e-2, (j, r)
+    if k is None:
+        return None
+    ol = orc_run.logits[k]
+    mine, theirs = eng_run.tokens[k], orc_run.tokens[k]
+    gap = float(ol[theirs] - ol[mine])
+    detail = (f"diverged at step {k}: engine {mine} (oracle logit {float(ol[mine])}, engine "
+              f"{float(eng_run.logits[k][mine])}) vs oracle {theirs} (oracle logit "
+              f"{float(ol[theirs])}, engine {float(eng_run.logits[k][theirs])}); "
+              f"oracle margin {orc_run.margins[k]}")
+    assert not strict, detail
+    assert gap <= _ulp_at(float(ol[theirs])), detail
+    return k
+
+
+def _teacher_forced(eng, prompt, orc_run, steps):
+    """Feed the oracle's own continuation as the prompt: the engine's pick at
+    every position must equal the oracle's unless the oracle's top-2 are within
+    one bf16 ulp (then the engine's pick must be one of those)."""
+    seq = list(prompt) + orc_run.tokens[:steps - 1]
+    eng.logits_for(seq)
+    picks = eng.sam[len(prompt) - 1: len(prompt) - 1 + steps].tolist()
+    near_ties = 0
     for k in range(steps):
-        r = report(eng_run.logits[k], orc_run.logits[k])
-        assert r["max_rel"] <= 2e-2, (k, r)
+        if picks[k] == orc_run.tokens[k]:
+            continue
+        ol = orc_run.logits[k]
+        top = float(ol.max())
+        assert float(ol[picks[k]]) >= top - _ulp_at(top), (k, picks[k], orc_run.tokens[k])
+        near_ties += 1
+    return near_ties
 
 
 SMALL = TINY.with_(dtype=torch.bfloat16)
@@ -48,6 +95,7 @@ def test_small_bf16_greedy_64(gpu_device, norms):
     eng = Engine(SMALL, w, device=gpu_device, max_new=64, prompt_room=16)
     run = eng.generate(prompt, 64, record_logits=True)
     _check_run(run, orc, 64)
+    assert _teacher_forced(eng, prompt, orc, 64) == 0
 
 
 def test_qwen3_layer_shape_two_layers_greedy_64(gpu_device):
@@ -57,7 +105,10 @@ def test_qwen3_layer_shape_two_layers_greedy_64(gpu_device):
     orc = O.decode(O.Qwen3Oracle(_dims(cfg), w), prompt, 64)
     eng = Engine(cfg, w, device=gpu_device, max_new=64, prompt_room=8)
     run = eng.generate(prompt, 64, record_logits=True)
-    _check_run(run, orc, 64)
+    k = _check_run(run, orc, 64, strict=False)
+    ties = _teacher_forced(eng, prompt, orc, 64)
+    print(f"free-running identical for {64 if k is None else k} steps; teacher-forced "
+          f"near-tie picks: {ties}; oracle margins min {min(orc.margins):.4g}")
 
 
 def test_paging_and_graph_do_not_change_results(gpu_device):
@@ -95,3 +146,22 @@ def test_capacity_and_prompt_checks(gpu_device):
         eng.generate([], 4)
     with pytest.raises(ValueError):
         eng.generate([SMALL.vocab_size], 4)        # id out of range
+
+
+@pytest.mark.parametrize("shape", ["small", "qwen3_2layer"])
+def test_persistent_kernel_equals_per_phase_launches(gpu_device, shape):
+    """The persistent kernel runs the same phase code on the same partition as
+    the per-phase launches: tokens and logits must be bit-identical, and one
+    launch of n steps must equal n launches of one step."""
+    cfg = SMALL if shape == "small" else QWEN3_1_7B.with_(num_hidden_layers=2)
+    w = synthetic_weights(cfg, seed=6, norms="ones")
+    prompt = _prompt(12, cfg.vocab_size, seed=9)
+    ref = Engine(cfg, w, device=gpu_device, max_new=48, prompt_room=12, mode="graph")
+    per = Engine(cfg, w, device=gpu_device, max_new=48, prompt_room=12, mode="persistent")
+    a = ref.generate(prompt, 48, record_logits=True)
+    b = per.generate(prompt, 48, record_logits=True)
+    assert a.tokens == b.tokens
+    assert torch.equal(a.logits, b.logits)
+    c = per.generate(prompt, 48)                    # two launches: prompt walk, continuation
+    assert c.tokens == a.tokens
+    assert torch.equal(per.logits, ref.logits)

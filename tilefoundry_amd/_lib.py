@@ -13,12 +13,13 @@ from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 1
+ABI_VERSION = 3
 
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU = 0, 1, 2
-ERR_TOKEN_RANGE, ERR_POS_RANGE, ERR_PAGE_RANGE, ERR_STEP_RANGE = 1, 2, 4, 8
+ERR_TOKEN_RANGE, ERR_POS_RANGE, ERR_PAGE_RANGE, ERR_STEP_RANGE, ERR_BARRIER = 1, 2, 4, 8, 16
 PAGE_SIZE = 16
+BARRIER_WORDS = 1280
 ATTN_SPLIT = 64
 
 P = c_void_p
@@ -37,8 +38,49 @@ SIGNATURES: dict[str, list] = {
     "tfd_attn_rope_scores_paged": [P, P, P, P, P, I, P, P, P, I, P, P, I, I, I, I, F, F, P, I,
                                    P, P, I, P, P],
     "tfd_attn_pv_combine_paged": [P, P, P, I, P, I, I, I, I, P, I, P, P, P, P, I, P, P, P, P],
+    "tfd_decode_persistent": [P, I, I, P],
+    "tfd_decode_persistent_grid": [],
 }
 RESTYPES = {"tfd_last_error": ctypes.c_char_p}
+UNCHECKED = {"tfd_abi_version", "tfd_decode_persistent_grid"}
+
+
+class TfdLayer(ctypes.Structure):
+    """``TfdLayer`` of include/tf_decode.h (device pointers of one layer)."""
+
+    _fields_ = [(n, c_void_p) for n in ("w_qkv", "w_o", "w_gu", "w_down", "gamma_in",
+                                        "gamma_post", "gamma_q", "gamma_k", "k_pool", "v_pool")]
+
+
+class TfdDecodeArgs(ctypes.Structure):
+    """``TfdDecodeArgs`` of include/tf_decode.h, field for field."""
+
+    _fields_ = [
+        ("layers", c_void_p),
+        *[(n, c_int) for n in ("n_layers", "hidden", "heads", "kv_heads", "head_dim",
+                                "intermediate", "vocab")],
+        ("eps", c_float), ("scale", c_float),
+        *[(n, c_void_p) for n in ("w_embed", "w_head", "gamma_final", "cos_table",
+                                   "sin_table")],
+        ("rope_rows", c_int),
+        ("page_table", c_void_p),
+        ("max_pages", c_int), ("num_pages", c_int),
+        *[(n, c_void_p) for n in ("hid", "h1", "qkv", "attn", "hmid")],
+        ("scores", c_void_p), ("score_stride", c_int),
+        *[(n, c_void_p) for n in ("split_max", "score_new", "part_sum", "part_out")],
+        ("nsplit", c_int),
+        ("counters", c_void_p),
+        *[(n, c_void_p) for n in ("logits", "block_val", "block_idx", "ids", "pos", "inp",
+                                   "prompt_len", "sam")],
+        ("nsteps", c_int),
+        ("barrier", c_void_p), ("err", c_void_p),
+        ("timeline", c_void_p), ("timeline_steps", c_int),
+    ]
+
+
+def timeline_stamps(n_layers: int) -> int:
+    """Stamps per step of the persistent kernel's timeline (TFD_TIMELINE_STAMPS)."""
+    return 12 * n_layers + 4
 
 
 class TFDError(RuntimeError):
@@ -64,7 +106,7 @@ class _Checked:
 
     def __getattr__(self, name):
         fn = getattr(self._dll, name)
-        if name in RESTYPES or name == "tfd_abi_version":
+        if name in RESTYPES or name in UNCHECKED:
             return fn
 
         def call(*args):

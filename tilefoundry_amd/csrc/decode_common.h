@@ -73,6 +73,53 @@ __device__ __forceinline__ u32x4 load16_stream(const bf16* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// ---------------------------------------------------------------------------
+// Device-coherent access.  Data one block writes and another block of the same
+// launch reads (activations, attention partials, the KV cache, the step
+// counters) goes through these.  Device-scope loads miss the per-CU L1 and the
+// per-XCD L2 for those lines and device-scope stores write through, so crossing
+// a grid barrier needs no L2 writeback/invalidate -- only each wave's wait for
+// its own stores (stores_done).  Bases must be wave-uniform (a kernel argument).
+// ---------------------------------------------------------------------------
+constexpr int kCoherent = 16;  // buffer cache-policy bits: device scope (sc1)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, -1, 0x00020000);
+}
+__device__ __forceinline__ u32x4 coh_ld16(const void* base, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), byte_off, 0, kCoherent);
+}
+__device__ __forceinline__ void coh_st16(void* base, uint32_t byte_off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, rsrc(base), byte_off, 0, kCoherent);
+}
+__device__ __forceinline__ bf16 coh_ld_bf16(const bf16* base, uint32_t idx) {
+  return __builtin_amdgcn_raw_buffer_load_b16(rsrc(base), idx * 2u, 0, kCoherent);
+}
+__device__ __forceinline__ void coh_st_bf16(bf16* base, uint32_t idx, bf16 v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, rsrc(base), idx * 2u, 0, kCoherent);
+}
+__device__ __forceinline__ float coh_ldf(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_stf(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int coh_ldi(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_sti(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coh_sti64(int64_t* p, int64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// This wave's memory operations have completed (stores are visible device-wide).
+__device__ __forceinline__ void stores_done() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 __device__ __forceinline__ float dot8(const u32x4 w, const u32x4 x, float acc) {
   acc = fmaf(bf_lo(w.x), bf_lo(x.x), acc);
   acc = fmaf(bf_hi(w.x), bf_hi(x.x), acc);
@@ -90,24 +137,39 @@ __device__ __forceinline__ float dot8(const u32x4 w, const u32x4 x, float acc) {
 // l, l+64, l+128, ... of a length-K bf16 vector (K % 8 == 0); kCmax bounds the
 // chunks per lane (K <= kCmax * 512).
 // ---------------------------------------------------------------------------
+// Loads are unconditional from clamped in-bounds addresses and masked
+// afterwards: a load under a divergent branch makes the wait-count pass fall
+// back to waiting for every outstanding load at the join.
 template <int kCmax>
 __device__ __forceinline__ void load_x(const bf16* __restrict__ x, int nch, int lane,
                                        u32x4 (&xr)[kCmax]) {
 #pragma unroll
   for (int i = 0; i < kCmax; ++i) {
     const int c = i * kWave + lane;
-    xr[i] = c < nch ? load16(x + (int64_t)c * 8) : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 v = load16(x + (int64_t)(c < nch ? c : nch - 1) * 8);
+    xr[i] = c < nch ? v : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// The same, for an activation another block produced (device-coherent loads).
+template <int kCmax>
+__device__ __forceinline__ void load_x_coh(const bf16* __restrict__ x, int nch, int lane,
+                                           u32x4 (&xr)[kCmax]) {
+#pragma unroll
+  for (int i = 0; i < kCmax; ++i) {
+    const int c = i * kWave + lane;
+    const u32x4 v = coh_ld16(x, (uint32_t)(c < nch ? c : nch - 1) * 16u);
+    xr[i] = c < nch ? v : u32x4{0u, 0u, 0u, 0u};
   }
 }
 
 // The Qwen3 RMSNorm (model.py:134-137): xn = bf16(bf16(x * rsqrt(mean(x^2)+eps)) * gamma),
-// computed by one wave over the whole vector, result left in the wave's chunks.
+// computed by one wave over the whole vector.  Split in two so a caller can
+// issue the x / gamma loads, then its weight loads, and only then wait for x:
+// memory counters retire in order, so x must be requested first.
 template <int kCmax>
-__device__ __forceinline__ void rms_norm_x(const bf16* __restrict__ x,
-                                           const bf16* __restrict__ gamma, int K, float eps,
-                                           int lane, u32x4 (&xr)[kCmax]) {
-  const int nch = K / 8;
-  load_x<kCmax>(x, nch, lane, xr);
+__device__ __forceinline__ void rms_norm_apply(u32x4 (&xr)[kCmax], const u32x4 (&gr)[kCmax], int K,
+                                               float eps) {
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < kCmax; ++i) {
@@ -123,40 +185,57 @@ __device__ __forceinline__ void rms_norm_x(const bf16* __restrict__ x,
   const float r = 1.0f / sqrtf(ss / (float)K + eps);
 #pragma unroll
   for (int i = 0; i < kCmax; ++i) {
-    const int c = i * kWave + lane;
-    if (c < nch) {
-      const u32x4 g = load16(gamma + (int64_t)c * 8);
-      const uint32_t w[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-      const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
-      uint32_t o[4];
+    const uint32_t w[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+    const uint32_t gw[4] = {gr[i].x, gr[i].y, gr[i].z, gr[i].w};
+    uint32_t o[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float lo = rbf(rbf(bf_lo(w[e]) * r) * bf_lo(gw[e]));
-        const float hi = rbf(rbf(bf_hi(w[e]) * r) * bf_hi(gw[e]));
-        o[e] = pack2(lo, hi);
-      }
-      xr[i] = u32x4{o[0], o[1], o[2], o[3]};
+    for (int e = 0; e < 4; ++e) {
+      const float lo = rbf(rbf(bf_lo(w[e]) * r) * bf_lo(gw[e]));
+      const float hi = rbf(rbf(bf_hi(w[e]) * r) * bf_hi(gw[e]));
+      o[e] = pack2(lo, hi);
     }
+    xr[i] = u32x4{o[0], o[1], o[2], o[3]};   // chunks past K stay zero (0 * r * 0)
   }
 }
 
-// Dot products of kR consecutive rows of W (row-major [N][K] bf16) with the
-// wave's x chunks.  All kR*kCmax loads are issued before the FMAs consume them.
+template <int kCmax>
+__device__ __forceinline__ void rms_norm_x(const bf16* __restrict__ x,
+                                           const bf16* __restrict__ gamma, int K, float eps,
+                                           int lane, u32x4 (&xr)[kCmax]) {
+  const int nch = K / 8;
+  u32x4 gr[kCmax];
+  load_x<kCmax>(x, nch, lane, xr);
+  load_x<kCmax>(gamma, nch, lane, gr);
+  rms_norm_apply<kCmax>(xr, gr, K, eps);
+}
+
+// Issue the loads of kR consecutive rows of W (row-major [N][K] bf16): lane l
+// gets chunks l, l+64, ... of each row.  Weights do not depend on the
+// activation, so callers issue these before anything that waits on memory.
 template <int kCmax, int kR>
-__device__ __forceinline__ void dot_rows(const bf16* __restrict__ W, int K, int nch, int64_t row0,
-                                         int nvalid, const u32x4 (&xr)[kCmax], int lane,
-                                         float (&acc)[kR]) {
-  u32x4 w[kR][kCmax];
+__device__ __forceinline__ void load_rows(const bf16* __restrict__ W, int K, int nch, int64_t row0,
+                                          int nvalid, int lane, u32x4 (&w)[kR][kCmax]) {
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
-    const bf16* rowp = W + (row0 + r) * (int64_t)K;
+    // rows past the end re-read the last valid row; their sums are never stored
+    const bf16* rowp = W + (row0 + (r < nvalid ? r : nvalid - 1)) * (int64_t)K;
 #pragma unroll
     for (int i = 0; i < kCmax; ++i) {
       const int c = i * kWave + lane;
-      w[r][i] = (r < nvalid && c < nch) ? load16_stream(rowp + (int64_t)c * 8)
-                                        : u32x4{0u, 0u, 0u, 0u};
+      // chunks past K re-read a valid chunk; x is zero there, so they add 0
+      w[r][i] = load16_stream(rowp + (int64_t)(c < nch ? c : nch - 1) * 8);
     }
   }
+  // keep every weight load ahead of the arithmetic that follows: the scheduler
+  // otherwise interleaves them with it and fewer bytes are in flight
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Row dot products of loaded weights with the wave's x chunks (all lanes get
+// every row's sum).
+template <int kCmax, int kR>
+__device__ __forceinline__ void dot_loaded(const u32x4 (&w)[kR][kCmax], const u32x4 (&xr)[kCmax],
+                                           float (&acc)[kR]) {
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
     float a = 0.f;
@@ -164,6 +243,15 @@ __device__ __forceinline__ void dot_rows(const bf16* __restrict__ W, int K, int 
     for (int i = 0; i < kCmax; ++i) a = dot8(w[r][i], xr[i], a);
     acc[r] = wave_sum(a);
   }
+}
+
+template <int kCmax, int kR>
+__device__ __forceinline__ void dot_rows(const bf16* __restrict__ W, int K, int nch, int64_t row0,
+                                         int nvalid, const u32x4 (&xr)[kCmax], int lane,
+                                         float (&acc)[kR]) {
+  u32x4 w[kR][kCmax];
+  load_rows<kCmax, kR>(W, K, nch, row0, nvalid, lane, w);
+  dot_loaded<kCmax, kR>(w, xr, acc);
 }
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
@@ -175,6 +263,7 @@ enum DeviceError : int {
   kErrPosRange = 2,        // a position past the rope table or the page table
   kErrPageRange = 4,       // a page-table entry outside the pool
   kErrStepRange = 8,       // a step past the sample buffer
+  kErrBarrier = 16,        // a grid barrier waited past its bound
 };
 
 __device__ __forceinline__ void raise_error(int* err, int code) {

@@ -19,7 +19,8 @@
 // Weights are row-major [out][in] bf16, so a row is one contiguous dot product
 // and the tied head reads the embedding table in place.
 
-#include "decode_common.h"
+#include "decode_phases.h"
+#include "tf_decode.h"
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -29,10 +30,7 @@ using namespace tfd;
 
 namespace {
 
-constexpr float kNegInf = -__builtin_huge_valf();
-
-enum Prologue { kPlain = 0, kNorm = 1 };
-enum Epilogue { kStore = 0, kResid = 1, kSwiglu = 2 };
+constexpr float kNegInfHost = -__builtin_huge_valf();
 
 // ---------------------------------------------------------------------------
 // Standalone RMSNorm (input_rms_norm / final_rms_norm, model.py:125-137, 289-298)
@@ -70,10 +68,9 @@ __global__ __launch_bounds__(kBlock) void k_embed(const bf16* __restrict__ table
     *reinterpret_cast<u32x4*>(out + (int64_t)c * 8) = load16(row + (int64_t)c * 8);
 }
 
+
 // ---------------------------------------------------------------------------
-// Row-dot GEMV with fused prologue / epilogue.  One wave owns kR consecutive
-// output rows; a block is 4 waves.  Every wave normalises x itself (a few KB
-// from L2) so no block waits on another.
+// one kernel per phase (virtual block = blockIdx)
 // ---------------------------------------------------------------------------
 template <int kCmax, int kR, int kPro, int kEpi>
 __global__ __launch_bounds__(kBlock) void k_gemv(const bf16* __restrict__ x,
@@ -81,53 +78,7 @@ __global__ __launch_bounds__(kBlock) void k_gemv(const bf16* __restrict__ x,
                                                  const bf16* __restrict__ W,
                                                  const bf16* __restrict__ resid,
                                                  bf16* __restrict__ out, int K, int N, float eps) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int64_t row0 = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * kR;
-  if (row0 >= N) return;
-  const int nch = K / 8;
-  u32x4 xr[kCmax];
-  if (kPro == kNorm)
-    rms_norm_x<kCmax>(x, gamma, K, eps, lane, xr);
-  else
-    load_x<kCmax>(x, nch, lane, xr);
-  const int nvalid = (int)((N - row0) < kR ? (N - row0) : kR);
-  float acc[kR];
-  dot_rows<kCmax, kR>(W, K, nch, row0, nvalid, xr, lane, acc);
-
-  if (kEpi == kSwiglu) {
-    // rows come as (gate_n, up_n) pairs: mlp(), model.py:230-233
-#pragma unroll
-    for (int p = 0; p < kR / 2; ++p) {
-      if (lane == p && 2 * p + 1 < nvalid) {
-        const float g = rbf(acc[2 * p]);
-        const float u = rbf(acc[2 * p + 1]);
-        const float a = rbf(silu_f(g));
-        out[row0 / 2 + p] = f2bf(a * u);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int r = 0; r < kR; ++r) {
-      if (lane == r && r < nvalid) {
-        const float y = rbf(acc[r]);
-        if (kEpi == kResid)
-          out[row0 + r] = f2bf(bf2f(resid[row0 + r]) + y);
-        else
-          out[row0 + r] = f2bf(y);
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// lm_head (model.py:300-305) with the final norm folded in and a per-block
-// greedy pick: logits are rounded to bf16 (the HIR declares them bf16) and the
-// block keeps the largest, lowest index on ties (torch.argmax's rule,
-// generation.py:24-26).
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
-  return v > bv || (v == bv && i < bi);
+  gemv_phase<kCmax, kR, kPro, kEpi>(blockIdx.x, x, gamma, W, resid, out, K, N, eps);
 }
 
 template <int kCmax, int kR>
@@ -135,32 +86,201 @@ __global__ __launch_bounds__(kBlock) void k_lm_head_argmax(
     const bf16* __restrict__ x, const bf16* __restrict__ gamma, const bf16* __restrict__ W,
     float* __restrict__ logits, float* __restrict__ bv, int* __restrict__ bi, int K, int V,
     float eps) {
+  lm_head_phase<kCmax, kR>(blockIdx.x, gridDim.x, x, gamma, W, logits, bv, bi, K, V, eps);
+}
+
+__global__ __launch_bounds__(1024) void k_argmax_finalize(
+    const float* __restrict__ bv, const int* __restrict__ bi, int nb,
+    const int* __restrict__ inp, const int* __restrict__ plen, int64_t* __restrict__ ids,
+    int* __restrict__ pos, int* __restrict__ sam, int nsteps, const bf16* __restrict__ table,
+    bf16* __restrict__ hid, int hidden, int vocab, int* err) {
+  finalize_phase(bv, bi, nb, inp, plen, ids, pos, sam, nsteps, table, hid, hidden, vocab, err);
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(kBlock) void k_attn_rope_scores(
+    const bf16* __restrict__ qkv, const bf16* __restrict__ gq, const bf16* __restrict__ gk,
+    const bf16* __restrict__ cos_t, const bf16* __restrict__ sin_t, int rope_rows,
+    const int* __restrict__ rope_pos, const int* __restrict__ cache_len,
+    const int* __restrict__ page_table, int max_pages, bf16* __restrict__ kpool,
+    bf16* __restrict__ vpool, int num_pages, int kv_heads, float scale, float eps,
+    float* __restrict__ S, int s_stride, float* __restrict__ smax, float* __restrict__ snew,
+    int* err) {
+  attn_scores_phase<D, G>(blockIdx.x, blockIdx.y, qkv, gq, gk, cos_t, sin_t, rope_rows,
+                          coh_ldi(rope_pos), coh_ldi(cache_len), page_table, max_pages, kpool,
+                          vpool, num_pages, kv_heads, scale, eps, S, s_stride, smax, snew, err);
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(kBlock) void k_attn_pv_combine(
+    const bf16* __restrict__ qkv, const int* __restrict__ cache_len,
+    const int* __restrict__ page_table, int max_pages, const bf16* __restrict__ vpool,
+    int num_pages, int kv_heads, const float* __restrict__ S, int s_stride,
+    const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
+    float* part_out, int* counters, bf16* __restrict__ attn_out, int* err) {
+  attn_pv_phase<D, G>(blockIdx.x, blockIdx.y, gridDim.x, qkv, coh_ldi(cache_len), page_table,
+                      max_pages, vpool, num_pages, kv_heads, S, s_stride, smax, snew, part_sum,
+                      part_out, counters, attn_out, err);
+}
+
+// ---------------------------------------------------------------------------
+// Grid barrier for the persistent kernel (every block co-resident: the launch
+// is cooperative).  Counters are monotonic within a launch (barrier k completes
+// when the count reaches (k+1) x participants) and zeroed by the caller before
+// each launch, so nothing is ever reset under a racing increment.  Arrivals
+// are counted per XCD first (the hardware XCC id), one counter per XCD on its
+// own cache line, and only each XCD's last arrival touches the global counter:
+// same-address atomics serialise, so this turns 256 serial increments into 8
+// parallel groups of 32 plus 8.  Data crosses the barrier device-coherently
+// (decode_phases.h), so the barrier itself is just: every wave's stores done,
+// count in, wait.  The wait is bounded: past the bound the error bit is raised
+// and every later wait falls through, so a protocol fault ends the launch.
+//
+// Layout of the barrier buffer (uint32): [0] global count; [64 * (1 + x)] XCD
+// x's count (x < 16); [1088 + x] blocks on XCD x; [1152] the setup count.
+// ---------------------------------------------------------------------------
+constexpr unsigned kSpinBound = 1u << 20;
+
+__device__ __forceinline__ unsigned xcc_id() {
+  return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((16 - 1) << 11)) & 0xfu;
+}
+__device__ __forceinline__ unsigned coh_ldu(unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned coh_addu(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void wait_count(unsigned* p, unsigned target, int* err) {
+  if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrBarrier) return;
+  unsigned spins = 0;
+  while (coh_ldu(p) < target) {
+    if (++spins > kSpinBound) {
+      atomicOr(err, kErrBarrier);
+      return;
+    }
+    if ((spins & 1023u) == 0 &&
+        (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrBarrier))
+      return;
+  }
+}
+
+struct GridBarrier {
+  unsigned* bar;
+  int* err;
+  unsigned xcc, per_xcc, n_xcc, k;
+
+  // One-time count of blocks per XCD (a flat barrier on its own counter).
+  __device__ __forceinline__ void setup(unsigned* b, int* e) {
+    __shared__ unsigned s_x, s_nx, s_nxcc;
+    bar = b;
+    err = e;
+    k = 0;
+    tl = nullptr;
+    if (threadIdx.x == 0) {
+      const unsigned x = xcc_id();
+      coh_addu(bar + 1088 + x, 1u);
+      stores_done();
+      coh_addu(bar + 1152, 1u);
+      wait_count(bar + 1152, gridDim.x, err);
+      unsigned n = 0;
+      for (int i = 0; i < 16; ++i) n += coh_ldu(bar + 1088 + i) ? 1u : 0u;
+      s_x = x;
+      s_nx = coh_ldu(bar + 1088 + x);
+      s_nxcc = n;
+    }
+    __syncthreads();
+    xcc = s_x;
+    per_xcc = s_nx;
+    n_xcc = s_nxcc;
+  }
+
+  uint64_t* tl;   // timeline slot of the current step (block 0 only), or null
+
+  __device__ __forceinline__ void stamp() {
+    if (tl && blockIdx.x == 0 && threadIdx.x == 0) *tl++ = wall_clock64();
+  }
+
+  // A barrier is arrive() then wait().  Memory counters retire in issue order
+  // and count loads with stores, so waiting for this block's stores must come
+  // before the next phase's weight loads are issued: callers put those loads
+  // between arrive() and wait(), where they stream while the barrier resolves.
+  __device__ __forceinline__ void arrive() {
+    stamp();
+    stores_done();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const unsigned prev = coh_addu(bar + 64 * (1 + xcc), 1u);
+      if (prev == (k + 1) * per_xcc - 1) coh_addu(bar, 1u);
+    }
+  }
+
+  __device__ __forceinline__ void wait() {
+    if (threadIdx.x == 0) wait_count(bar, (k + 1) * n_xcc, err);
+    ++k;
+    __syncthreads();
+    stamp();
+  }
+
+  __device__ __forceinline__ void sync() {
+    arrive();
+    wait();
+  }
+};
+
+// ---------------------------------------------------------------------------
+// lm_head for the persistent kernel: the same per-row arithmetic as
+// lm_head_phase, with the block's row groups double-buffered in registers so
+// the next group's loads are in flight while the current one is reduced.
+// ---------------------------------------------------------------------------
+template <int kCmax, int kR>
+__device__ __forceinline__ void lm_head_rows(int64_t row0, int V, int K, int nch, int lane,
+                                             const u32x4 (&xr)[kCmax],
+                                             const u32x4 (&w)[kR][kCmax], float* logits,
+                                             float& best, int& besti) {
+  if (row0 >= V) return;
+  const int nvalid = (int)((V - row0) < kR ? (V - row0) : kR);
+  float acc[kR];
+  dot_loaded<kCmax, kR>(w, xr, acc);
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    if (r < nvalid) {
+      const float y = rbf(acc[r]);
+      if (lane == r) logits[row0 + r] = y;
+      if (better(y, (int)(row0 + r), best, besti)) {
+        best = y;
+        besti = (int)(row0 + r);
+      }
+    }
+  }
+}
+
+template <int kCmax, int kR>
+__device__ __forceinline__ void lm_head_pipelined(const bf16* __restrict__ x,
+                                                  const bf16* __restrict__ gamma,
+                                                  const bf16* __restrict__ W, float* logits,
+                                                  float* bv, int* bi, int K, int V, float eps) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nch = K / 8;
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock * kR;
+  int64_t r0 = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * kR;
+  u32x4 wa[kR][kCmax], wb[kR][kCmax];
+  gemv_issue<kCmax, kR>(blockIdx.x, W, K, V, wa);
   u32x4 xr[kCmax];
   rms_norm_x<kCmax>(x, gamma, K, eps, lane, xr);
   float best = kNegInf;
   int besti = 0x7fffffff;
-  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock * kR;
-  for (int64_t row0 = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * kR; row0 < V;
-       row0 += stride) {
-    const int nvalid = (int)((V - row0) < kR ? (V - row0) : kR);
-    float acc[kR];
-    dot_rows<kCmax, kR>(W, K, nch, row0, nvalid, xr, lane, acc);
-#pragma unroll
-    for (int r = 0; r < kR; ++r) {
-      if (r < nvalid) {
-        const float y = rbf(acc[r]);
-        if (lane == r) logits[row0 + r] = y;
-        if (better(y, (int)(row0 + r), best, besti)) {
-          best = y;
-          besti = (int)(row0 + r);
-        }
-      }
-    }
+  while (r0 < V) {
+    const int64_t r1 = r0 + stride;
+    gemv_issue<kCmax, kR>((int)(r1 / (kWavesPerBlock * kR)), W, K, V, wb);
+    lm_head_rows<kCmax, kR>(r0, V, K, nch, lane, xr, wa, logits, best, besti);
+    if (r1 >= V) break;
+    const int64_t r2 = r1 + stride;
+    gemv_issue<kCmax, kR>((int)(r2 / (kWavesPerBlock * kR)), W, K, V, wa);
+    lm_head_rows<kCmax, kR>(r1, V, K, nch, lane, xr, wb, logits, best, besti);
+    r0 = r2;
   }
-  // every lane of a wave holds the same (best, besti); reduce across waves
   __shared__ float sv[kWavesPerBlock];
   __shared__ int si[kWavesPerBlock];
   if (lane == 0) {
@@ -176,366 +296,126 @@ __global__ __launch_bounds__(kBlock) void k_lm_head_argmax(
         b = sv[w];
         i = si[w];
       }
-    bv[blockIdx.x] = b;
-    bi[blockIdx.x] = i;
+    coh_stf(&bv[blockIdx.x], b);
+    coh_sti(&bi[blockIdx.x], i);
+  }
+  __syncthreads();
+}
+
+// One GEMV phase of the persistent kernel.  The weights of the block's first
+// virtual block are already in flight (issued before the barrier that
+// precedes this phase); any further virtual blocks issue and finish in turn.
+template <int kCmax, int kR, int kPro, int kEpi>
+__device__ __forceinline__ void gemv_persistent(const bf16* x, const bf16* gamma, const bf16* W,
+                                                const bf16* resid, bf16* out, int K, int N,
+                                                float eps, u32x4 (&w)[kR][kCmax]) {
+  const int rows_per_vb = kWavesPerBlock * kR;
+  for (int vb = blockIdx.x; vb * rows_per_vb < N; vb += gridDim.x) {
+    if (vb != (int)blockIdx.x) gemv_issue<kCmax, kR>(vb, W, K, N, w);
+    u32x4 xr[kCmax], gr[kCmax];
+    gemv_load_x<kCmax, kPro>(x, gamma, K, xr, gr);
+    gemv_finish<kCmax, kR, kPro, kEpi>(vb, x, gamma, resid, out, K, N, eps, xr, gr, w);
   }
 }
 
 // ---------------------------------------------------------------------------
-// The step's last node (fast/kernels.py:591-637 does the same job): global
-// argmax over the block picks, record it at Sam[pos], feed the next prompt token
-// while the prompt lasts and the pick after, advance pos, and stage the next
-// token's embedding row as the next step's hidden state.
+// The persistent decode kernel: `steps` whole decode steps in one launch.
+// Row tiles are sized so each GEMV phase is one round of loads per wave on a
+// 256-block grid at the Qwen3-1.7B shape (qkv 4096 = 1024 waves x 4 rows,
+// o 2048 x 2, gate/up 12288 x 12, down 2048 x 2); other shapes loop.  The next
+// GEMV's weights are issued before every grid barrier, so HBM streams while
+// the barrier resolves, and the o-projection's weights ride through both
+// attention phases.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(1024) void k_argmax_finalize(
-    const float* __restrict__ bv, const int* __restrict__ bi, int nb,
-    const int* __restrict__ inp, const int* __restrict__ plen, int64_t* __restrict__ ids,
-    int* __restrict__ pos, int* __restrict__ sam, int nsteps, const bf16* __restrict__ table,
-    bf16* __restrict__ hid, int hidden, int vocab, int* err) {
-  const int tid = threadIdx.x;
-  float b = kNegInf;
-  int i = 0x7fffffff;
-  for (int k = tid; k < nb; k += blockDim.x)
-    if (better(bv[k], bi[k], b, i)) {
-      b = bv[k];
-      i = bi[k];
-    }
-  // wave reduction of (value, index)
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const float ob = __shfl_xor(b, m, kWave);
-    const int oi = __shfl_xor(i, m, kWave);
-    if (better(ob, oi, b, i)) {
-      b = ob;
-      i = oi;
-    }
-  }
-  __shared__ float sv[16];
-  __shared__ int si[16];
-  __shared__ int next_s;
-  const int lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-  if (lane == 0) {
-    sv[wave] = b;
-    si[wave] = i;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float bb = sv[0];
-    int ii = si[0];
-    for (int w = 1; w < nw; ++w)
-      if (better(sv[w], si[w], bb, ii)) {
-        bb = sv[w];
-        ii = si[w];
-      }
-    if (ii < 0 || ii >= vocab) ii = 0;  // all-NaN row: no pick exists
-    const int p = pos[0];
-    int next = ii;
-    if (p < 0 || p >= nsteps) {
-      raise_error(err, kErrStepRange);
-    } else {
-      sam[p] = ii;
-      if (p + 1 < plen[0] && p + 1 < nsteps) next = inp[p + 1];
-    }
-    if (next < 0 || next >= vocab) {
-      raise_error(err, kErrTokenRange);
-      next = 0;
-    }
-    ids[0] = next;
-    pos[0] = p + 1;
-    next_s = next;
-  }
-  __syncthreads();
-  const bf16* row = table + (int64_t)next_s * hidden;
-  for (int c = tid; c < hidden / 8; c += blockDim.x)
-    *reinterpret_cast<u32x4*>(hid + (int64_t)c * 8) = load16(row + (int64_t)c * 8);
-}
+template <int kCH, int kCI, int D, int G>
+__global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, int steps) {
+  constexpr int kRqkv = 4, kRo = 2, kRgu = 12, kRdown = 2, kRhead = 4;
+  const int nb = gridDim.x;
+  const int H = a.hidden, I = a.intermediate, V = a.vocab;
+  const int QD = a.heads * D;
+  const int qkv_n = QD + 2 * a.kv_heads * D;
+  const int nvb_attn = a.nsplit * a.kv_heads;
+  const float eps = a.eps;
+  // activation rows: one per layer (hid has n_layers + 1), so each address is
+  // written once per step and can be read through the caches
+  bf16* const hid = (bf16*)a.hid;
+  bf16* const h1 = (bf16*)a.h1;
+  bf16* const qkv = (bf16*)a.qkv;
+  bf16* const attn = (bf16*)a.attn;
+  bf16* const hmid = (bf16*)a.hmid;
+  const int vb0 = blockIdx.x;
+  GridBarrier gb;
+  gb.setup(a.barrier, a.err);
+  int P = coh_ldi(a.pos);   // position of step 0; finalize advances it by one per step
 
-// ---------------------------------------------------------------------------
-// Attention, part 1 (self_attention, model.py:172-198).
-// Grid (nsplit, kv_heads).  Each block rebuilds its kv head's group of query
-// vectors and the new key from the bf16 QKV projection: per-head RMS, RoPE at
-// rope_pos, q_s = bf16(q_rope * scale).  Split 0 writes this token's key and
-// value into the paged cache at position cache_len and scores the new key;
-// every block scores its own kSplit positions of the prior context:
-//   s_j = bf16( sum_d bf16(q_s[d] * K[j][d]) )
-// and records the split's max per query head.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ int64_t page_offset(const int* page_table, int j, int kv_heads,
-                                               int h, int D, int num_pages, bool* ok) {
-  const int page = page_table[j / kPage];
-  if (page < 0 || page >= num_pages) {
-    *ok = false;
-    return 0;
-  }
-  return (((int64_t)page * kv_heads + h) * kPage + (j % kPage)) * D;
-}
-
-template <int D, int G>
-__global__ __launch_bounds__(kBlock) void k_attn_rope_scores(
-    const bf16* __restrict__ qkv, const bf16* __restrict__ gq, const bf16* __restrict__ gk,
-    const bf16* __restrict__ cos_t, const bf16* __restrict__ sin_t, int rope_rows,
-    const int* __restrict__ rope_pos, const int* __restrict__ cache_len,
-    const int* __restrict__ page_table, int max_pages, bf16* __restrict__ kpool,
-    bf16* __restrict__ vpool, int num_pages, int kv_heads, float scale, float eps,
-    float* __restrict__ S, int s_stride, float* __restrict__ smax, float* __restrict__ snew,
-    int* err) {
-  constexpr int kHalf = D / 2;
-  constexpr int kLpp = D / 8;             // lanes per position (one 16-byte chunk each)
-  constexpr int kPpw = kWave / kLpp;      // positions per wave per pass
-  static_assert(kHalf <= kWave, "one wave holds a head as (d, d + D/2) lane pairs");
-  const int split = blockIdx.x, h = blockIdx.y;
-  const int heads = kv_heads * G;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int P = cache_len[0];
-  const int rp = rope_pos[0];
-  const int j0 = split * kSplit;
-  if (split != 0 && j0 >= P) {
-    if (tid < G) smax[split * heads + h * G + tid] = kNegInf;
-    return;
-  }
-  if (P < 0 || P >= max_pages * kPage || rp < 0 || rp >= rope_rows) {
-    if (tid == 0) raise_error(err, kErrPosRange);
-    if (tid < G) {
-      smax[split * heads + h * G + tid] = kNegInf;
-      if (split == 0) snew[h * G + tid] = 0.f;
+  u32x4 wq[kRqkv][kCH], wo[kRo][kCH], wg[kRgu][kCH], wd[kRdown][kCI];
+  gemv_issue<kCH, kRqkv>(vb0, (const bf16*)a.layers[0].w_qkv, H, qkv_n, wq);
+  for (int t = 0; t < steps; ++t, ++P) {
+    gb.tl = (a.timeline && t < a.timeline_steps)
+                ? a.timeline + (int64_t)t * (12 * a.n_layers + 4) : nullptr;
+    for (int l = 0; l < a.n_layers; ++l) {
+      const TfdLayer w = a.layers[l];
+      bf16* const x_in = hid + (int64_t)l * H;
+      bf16* const x_out = hid + (int64_t)(l + 1) * H;
+      bf16* const h1_l = h1 + (int64_t)l * H;
+      bf16* const qkv_l = qkv + (int64_t)l * qkv_n;
+      bf16* const attn_l = attn + (int64_t)l * QD;
+      bf16* const hmid_l = hmid + (int64_t)l * I;
+      gemv_persistent<kCH, kRqkv, kNorm, kStore>(x_in, (const bf16*)w.gamma_in,
+                                                 (const bf16*)w.w_qkv, nullptr, qkv_l, H, qkv_n,
+                                                 eps, wq);
+      gb.arrive();
+      gemv_issue<kCH, kRo>(vb0, (const bf16*)w.w_o, QD, H, wo);
+      gb.wait();
+      for (int vb = blockIdx.x; vb < nvb_attn; vb += nb)
+        attn_scores_phase<D, G>(vb % a.nsplit, vb / a.nsplit, qkv_l, (const bf16*)w.gamma_q,
+                                (const bf16*)w.gamma_k, (const bf16*)a.cos_table,
+                                (const bf16*)a.sin_table, a.rope_rows, P, P, a.page_table,
+                                a.max_pages, (bf16*)w.k_pool, (bf16*)w.v_pool, a.num_pages,
+                                a.kv_heads, a.scale, eps, a.scores, a.score_stride, a.split_max,
+                                a.score_new, a.err);
+      gb.sync();
+      for (int vb = blockIdx.x; vb < nvb_attn; vb += nb)
+        attn_pv_phase<D, G>(vb % a.nsplit, vb / a.nsplit, a.nsplit, qkv_l, P, a.page_table,
+                            a.max_pages, (const bf16*)w.v_pool, a.num_pages, a.kv_heads,
+                            a.scores, a.score_stride, a.split_max, a.score_new, a.part_sum,
+                            a.part_out, a.counters, attn_l, a.err);
+      gb.sync();
+      gemv_persistent<kCH, kRo, kPlain, kResid>(attn_l, nullptr, (const bf16*)w.w_o, x_in, h1_l,
+                                                QD, H, eps, wo);
+      gb.arrive();
+      gemv_issue<kCH, kRgu>(vb0, (const bf16*)w.w_gu, H, 2 * I, wg);
+      gb.wait();
+      gemv_persistent<kCH, kRgu, kNorm, kSwiglu>(h1_l, (const bf16*)w.gamma_post,
+                                                 (const bf16*)w.w_gu, nullptr, hmid_l, H, 2 * I,
+                                                 eps, wg);
+      gb.arrive();
+      gemv_issue<kCI, kRdown>(vb0, (const bf16*)w.w_down, I, H, wd);
+      gb.wait();
+      gemv_persistent<kCI, kRdown, kPlain, kResid>(hmid_l, nullptr, (const bf16*)w.w_down, h1_l,
+                                                   x_out, I, H, eps, wd);
+      gb.arrive();
+      // the next layer's qkv weights -- or, after the last layer, layer 0's for
+      // the next step (issued unconditionally: a conditional issue would keep
+      // the tile live through the whole step)
+      gemv_issue<kCH, kRqkv>(vb0, (const bf16*)a.layers[(l + 1) % a.n_layers].w_qkv, H, qkv_n,
+                             wq);
+      gb.wait();
     }
-    return;
+    lm_head_pipelined<kCH, kRhead>(hid + (int64_t)a.n_layers * H, (const bf16*)a.gamma_final,
+                                   (const bf16*)a.w_head, a.logits, a.block_val, a.block_idx, H,
+                                   V, eps);
+    gb.sync();
+    if (blockIdx.x == 0)
+      finalize_phase(a.block_val, a.block_idx, nb, a.inp, a.prompt_len, a.ids, a.pos, a.sam,
+                     a.nsteps, (const bf16*)a.w_embed, hid, H, V, a.err);
+    gb.sync();
+    // the next step rewrites every activation row: drop this step's copies from
+    // this CU's L1 and this XCD's L2 before reading any of them again
+    if (threadIdx.x == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __syncthreads();
+    if (__hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrBarrier) break;
   }
-
-  __shared__ float qs[G][D];
-  __shared__ float kn[D];
-  __shared__ float wmax[kWavesPerBlock][G];
-
-  // ---- q group and the new key: RMS over D, bf16, * gamma, RoPE, (q) * scale
-  for (int v = wave; v < G + 1; v += kWavesPerBlock) {
-    const bool isq = v < G;
-    const bf16* src = isq ? qkv + (int64_t)(h * G + v) * D : qkv + (int64_t)heads * D + h * D;
-    const bf16* gam = isq ? gq : gk;
-    const bool act = lane < kHalf;
-    const float x0 = act ? bf2f(src[lane]) : 0.f;
-    const float x1 = act ? bf2f(src[lane + kHalf]) : 0.f;
-    float ss = x0 * x0;
-    ss += x1 * x1;
-    ss = wave_sum(ss);
-    const float r = 1.0f / sqrtf(ss / (float)D + eps);
-    if (act) {
-      const float n0 = rbf(rbf(x0 * r) * bf2f(gam[lane]));
-      const float n1 = rbf(rbf(x1 * r) * bf2f(gam[lane + kHalf]));
-      const float c0 = bf2f(cos_t[(int64_t)rp * D + lane]);
-      const float s0 = bf2f(sin_t[(int64_t)rp * D + lane]);
-      const float c1 = bf2f(cos_t[(int64_t)rp * D + lane + kHalf]);
-      const float s1 = bf2f(sin_t[(int64_t)rp * D + lane + kHalf]);
-      // rope.py:154-162: x*cos + rotate_half(x)*sin, rotate_half = (-x2, x1)
-      const float o0 = rbf(n0 * c0 + (-n1) * s0);
-      const float o1 = rbf(n1 * c1 + n0 * s1);
-      if (isq) {
-        qs[v][lane] = rbf(o0 * scale);
-        qs[v][lane + kHalf] = rbf(o1 * scale);
-      } else {
-        kn[lane] = o0;
-        kn[lane + kHalf] = o1;
-      }
-    }
-  }
-  __syncthreads();
-
-  if (split == 0) {
-    // this token's entry goes to the cache at P (fast/kernels.py:385-409)
-    bool ok = true;
-    const int64_t off = page_offset(page_table, P, kv_heads, h, D, num_pages, &ok);
-    if (!ok) {
-      if (tid == 0) raise_error(err, kErrPageRange);
-    } else {
-      const bf16* vsrc = qkv + (int64_t)heads * D + (int64_t)kv_heads * D + h * D;
-      for (int d = tid; d < D; d += kBlock) {
-        kpool[off + d] = f2bf(kn[d]);
-        vpool[off + d] = vsrc[d];
-      }
-    }
-    // score of the new key (score_new, model.py:198)
-    if (wave < G) {
-      float a = 0.f;
-      if (lane < kHalf) {
-        a = rbf(qs[wave][lane] * kn[lane]);
-        a += rbf(qs[wave][lane + kHalf] * kn[lane + kHalf]);
-      }
-      a = wave_sum(a);
-      if (lane == 0) snew[h * G + wave] = rbf(a);
-    }
-  }
-
-  // ---- scores over this split of the prior context
-  const int jend = (j0 + kSplit < P) ? j0 + kSplit : P;
-  const int sub = lane / kLpp, ch = lane % kLpp;
-  float qv[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qv[g][e] = qs[g][ch * 8 + e];
-  float mymax[G];
-#pragma unroll
-  for (int g = 0; g < G; ++g) mymax[g] = kNegInf;
-  bool page_ok = true;
-  for (int jb = j0 + wave * kPpw; jb < jend; jb += kWavesPerBlock * kPpw) {
-    const int j = jb + sub;
-    const bool valid = j < jend;
-    u32x4 kv = u32x4{0u, 0u, 0u, 0u};
-    if (valid) {
-      bool ok = true;
-      const int64_t off = page_offset(page_table, j, kv_heads, h, D, num_pages, &ok);
-      if (ok)
-        kv = load16(kpool + off + ch * 8);
-      else
-        page_ok = false;
-    }
-    const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float a = 0.f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        a += rbf(qv[g][2 * e] * bf_lo(kw[e]));
-        a += rbf(qv[g][2 * e + 1] * bf_hi(kw[e]));
-      }
-      a = group_sum<kLpp>(a);
-      const float sc = rbf(a);
-      if (valid) {
-        if (ch == 0) S[(int64_t)(h * G + g) * s_stride + j] = sc;
-        mymax[g] = fmaxf(mymax[g], sc);
-      }
-    }
-  }
-  if (!page_ok) raise_error(err, kErrPageRange);
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float m = wave_max(mymax[g]);
-    if (lane == 0) wmax[wave][g] = m;
-  }
-  __syncthreads();
-  if (tid < G) {
-    float m = wmax[0][tid];
-    for (int w = 1; w < kWavesPerBlock; ++w) m = fmaxf(m, wmax[w][tid]);
-    smax[split * heads + h * G + tid] = m;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Attention, part 2 (model.py:200-212).  Grid (nsplit, kv_heads).
-// With the joint peak M = max(split maxima, score_new):
-//   p_j = bf16(exp(bf16(s_j - M)))
-//   per split: sum_j p_j and sum_j bf16(p_j * V[j][d]) in f32
-// The last block of a kv head to finish merges every split (in split order):
-//   total    = bf16(bf16(sum p) + p_new)
-//   weighted = bf16(bf16(sum pV) + bf16(p_new * v_new))
-//   attn     = bf16(weighted / total)
-// ---------------------------------------------------------------------------
-template <int D, int G>
-__global__ __launch_bounds__(kBlock) void k_attn_pv_combine(
-    const bf16* __restrict__ qkv, const int* __restrict__ cache_len,
-    const int* __restrict__ page_table, int max_pages, const bf16* __restrict__ vpool,
-    int num_pages, int kv_heads, const float* __restrict__ S, int s_stride,
-    const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
-    float* part_out, int* counters, bf16* __restrict__ attn_out, int* err) {
-  constexpr int kLpp = D / 8;
-  constexpr int kGroups = kBlock / kLpp;   // position groups in the P.V pass
-  static_assert(kSplit == kWave, "one wave sums one head's split of p");
-  const int split = blockIdx.x, h = blockIdx.y;
-  const int heads = kv_heads * G;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  int P = cache_len[0];
-  if (P < 0 || P >= max_pages * kPage) P = 0;  // part 1 already raised the flag
-  const int nact = (P + kSplit - 1) / kSplit;
-  const int participants = nact > 0 ? nact : 1;
-  if (split >= participants) return;
-
-  __shared__ float M[G];
-  __shared__ float p[G][kSplit];
-  __shared__ float red[kGroups][G * D];
-  __shared__ int is_last;
-
-  if (tid < G) {
-    float m = snew[h * G + tid];
-    for (int s = 0; s < nact; ++s) m = fmaxf(m, smax[s * heads + h * G + tid]);
-    M[tid] = m;
-  }
-  __syncthreads();
-  const int j0 = split * kSplit;
-  const int jend = (j0 + kSplit < P) ? j0 + kSplit : P;
-  for (int idx = tid; idx < G * kSplit; idx += kBlock) {
-    const int g = idx / kSplit, jj = idx % kSplit, j = j0 + jj;
-    p[g][jj] = (j < jend) ? rbf(expf(rbf(S[(int64_t)(h * G + g) * s_stride + j] - M[g]))) : 0.f;
-  }
-  __syncthreads();
-  if (wave < G) {
-    const float s = wave_sum(p[wave][lane]);
-    if (lane == 0) part_sum[split * heads + h * G + wave] = s;
-  }
-  {
-    const int ch = tid % kLpp, jo = tid / kLpp;
-    float acc[G][8];
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-    bool page_ok = true;
-    for (int jj = jo; jj < kSplit; jj += kGroups) {
-      const int j = j0 + jj;
-      if (j < jend) {
-        bool ok = true;
-        const int64_t off = page_offset(page_table, j, kv_heads, h, D, num_pages, &ok);
-        if (!ok) {
-          page_ok = false;
-          continue;
-        }
-        const u32x4 vv = load16(vpool + off + ch * 8);
-        const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          const float pj = p[g][jj];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            acc[g][2 * e] += rbf(pj * bf_lo(vw[e]));
-            acc[g][2 * e + 1] += rbf(pj * bf_hi(vw[e]));
-          }
-        }
-      }
-    }
-    if (!page_ok) raise_error(err, kErrPageRange);
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) red[jo][g * D + ch * 8 + e] = acc[g][e];
-  }
-  __syncthreads();
-  for (int o = tid; o < G * D; o += kBlock) {
-    float s = 0.f;
-    for (int q = 0; q < kGroups; ++q) s += red[q][o];
-    part_out[((int64_t)split * heads + h * G) * D + o] = s;
-  }
-  // ---- last block of this kv head merges the splits
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int ticket = atomicAdd(&counters[h], 1);
-    is_last = (ticket == participants - 1);
-  }
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  const bf16* vnew = qkv + (int64_t)heads * D + (int64_t)kv_heads * D + h * D;
-  for (int o = tid; o < G * D; o += kBlock) {
-    const int g = o / D, d = o % D;
-    float sp = 0.f, sv = 0.f;
-    for (int s = 0; s < nact; ++s) {
-      sp += part_sum[s * heads + h * G + g];
-      sv += part_out[((int64_t)s * heads + h * G) * D + o];
-    }
-    const float pn = rbf(expf(rbf(snew[h * G + g] - M[g])));
-    const float total = rbf(rbf(sp) + pn);
-    const float weighted = rbf(rbf(sv) + rbf(pn * bf2f(vnew[d])));
-    attn_out[(int64_t)(h * G + g) * D + d] = f2bf(weighted / total);
-  }
-  if (tid == 0) atomicExch(&counters[h], 0);
 }
 
 // ---------------------------------------------------------------------------
@@ -594,7 +474,6 @@ void launch_gemv(const bf16* x, const bf16* gamma, const bf16* W, const bf16* re
 
 }  // namespace
 
-#include "../../include/tf_decode.h"
 
 extern "C" {
 
@@ -701,8 +580,6 @@ int tfd_argmax_finalize(const float* block_val, const int32_t* block_idx, int nb
   if (D == 128 && G == 2) { constexpr int kD = 128, kG = 2; CALL; }        \
   else if (D == 64 && G == 2) { constexpr int kD = 64, kG = 2; CALL; }     \
   else if (D == 128 && G == 1) { constexpr int kD = 128, kG = 1; CALL; }   \
-  else if (D == 128 && G == 4) { constexpr int kD = 128, kG = 4; CALL; }   \
-  else if (D == 64 && G == 4) { constexpr int kD = 64, kG = 4; CALL; }     \
   else return fail(kUnsupported, "attention: head_dim=%d group=%d not built", D, G);
 
 int tfd_attn_rope_scores_paged(const void* qkv, const void* gamma_q, const void* gamma_k,
@@ -761,6 +638,62 @@ int tfd_attn_pv_combine_paged(const void* qkv, const int32_t* cache_len,
                                      score_stride, split_max, score_new, part_sum, part_out,
                                      counters, (bf16*)attn_out, err));
   return launched("attn_pv_combine");
+}
+
+int tfd_decode_persistent_grid(void) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  return cus;
+}
+
+int tfd_decode_persistent(const TfdDecodeArgs* args, int steps, int nblocks, void* stream) {
+  if (!args) return fail(kBadArg, "decode_persistent: null args");
+  const TfdDecodeArgs& a = *args;
+  if (!a.layers || !a.w_embed || !a.w_head || !a.gamma_final || !a.cos_table || !a.sin_table ||
+      !a.page_table || !a.hid || !a.h1 || !a.qkv || !a.attn || !a.hmid || !a.scores ||
+      !a.split_max || !a.score_new || !a.part_sum || !a.part_out || !a.counters || !a.logits ||
+      !a.block_val || !a.block_idx || !a.ids || !a.pos || !a.inp || !a.prompt_len || !a.sam ||
+      !a.barrier || !a.err)
+    return fail(kBadArg, "decode_persistent: null pointer in args");
+  if (steps < 0) return fail(kBadArg, "decode_persistent: steps=%d", steps);
+  if (steps == 0) return 0;
+  if (a.n_layers <= 0 || a.kv_heads <= 0 || a.heads % a.kv_heads || a.hidden % 8 ||
+      a.intermediate % 8 || a.vocab <= 0 || a.nsteps <= 0)
+    return fail(kBadShape, "decode_persistent: bad model shape");
+  if (a.heads * a.head_dim != a.hidden)
+    return fail(kUnsupported, "decode_persistent: needs hidden == heads * head_dim (%d vs %d)",
+                a.hidden, a.heads * a.head_dim);
+  if ((int64_t)a.nsplit * kSplit < (int64_t)a.max_pages * kPage ||
+      a.score_stride < a.nsplit * kSplit || a.num_pages <= 0)
+    return fail(kBadShape, "decode_persistent: nsplit=%d does not cover max_pages=%d", a.nsplit,
+                a.max_pages);
+  const int grid = nblocks > 0 ? nblocks : tfd_decode_persistent_grid();
+  if (grid <= 0) return fail(kUnsupported, "decode_persistent: no device");
+  const int G = a.heads / a.kv_heads;
+  const int ch = cmax_for(a.hidden), ci = cmax_for(a.intermediate);
+  const void* fn = nullptr;
+  if (ch == 4 && ci == 12 && a.head_dim == 128 && G == 2)
+    fn = reinterpret_cast<const void*>(&k_decode_persistent<4, 12, 128, 2>);
+  else if (ch == 1 && ci == 2 && a.head_dim == 64 && G == 2)
+    fn = reinterpret_cast<const void*>(&k_decode_persistent<1, 2, 64, 2>);
+  else
+    return fail(kUnsupported, "decode_persistent: no instance for hidden=%d inter=%d D=%d G=%d",
+                a.hidden, a.intermediate, a.head_dim, G);
+  int per_cu = 0, cus = tfd_decode_persistent_grid();
+  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kBlock, 0);
+  if (e != hipSuccess) return fail((int)e, "decode_persistent: occupancy query failed");
+  if (grid > per_cu * cus)
+    return fail(kUnsupported, "decode_persistent: %d blocks cannot be co-resident (%d x %d)",
+                grid, per_cu, cus);
+  TfdDecodeArgs karg = a;
+  int ksteps = steps;
+  void* kargs[] = {&karg, &ksteps};
+  e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kBlock), kargs, 0, (hipStream_t)stream);
+  if (e != hipSuccess) return fail((int)e, "decode_persistent: launch failed: %s",
+                                   hipGetErrorString(e));
+  return launched("decode_persistent");
 }
 
 }  // extern "C"

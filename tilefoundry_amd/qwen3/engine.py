@@ -20,6 +20,7 @@ What differs, MI355X-first:
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from time import perf_counter
 
@@ -61,7 +62,11 @@ class Engine:
     def __init__(self, cfg: Qwen3Config, weights: dict[str, torch.Tensor], *,
                  device: str = "cuda:0", max_new: int = 2048, prompt_room: int = 512,
                  page_seed: int | None = 0, graph: bool = True,
-                 lm_head_blocks: int = 2048):
+                 lm_head_blocks: int = 2048, mode: str | None = None):
+        """*mode*: ``"persistent"`` runs whole steps in one cooperative launch
+        (``tfd_decode_persistent``); ``"graph"`` replays a captured graph of the
+        per-phase launches; ``"direct"`` issues those launches each step.  The
+        default is ``"graph"`` (``"direct"`` when *graph* is False)."""
         if cfg.dtype != torch.bfloat16:
             raise ValueError(f"the HIP engine runs bf16 weights; config has {cfg.dtype}")
         validate(cfg, weights)
@@ -82,11 +87,16 @@ class Engine:
             raise ValueError(f"capacity {self.cap} exceeds the rope table "
                              f"({cfg.max_position_embeddings} positions)")
         self.nb = lm_head_blocks
+        self.mode = mode or ("graph" if graph else "direct")
+        if self.mode not in ("persistent", "graph", "direct"):
+            raise ValueError(f"mode {self.mode!r}")
         self._lib = lib()
         self._pack(weights, page_seed)
         self._buffers()
         self.graph = None
-        if graph:
+        if self.mode == "persistent":
+            self._persistent_args()
+        elif self.mode == "graph":
             self._capture()
 
     # ---------------------------------------------------------------- weights
@@ -118,11 +128,14 @@ class Engine:
         def z(*shape, dtype=bf):
             return torch.zeros(*shape, device=dev, dtype=dtype)
 
-        self.hid = z(self.H)
-        self.h1 = z(self.H)
-        self.qkv = z(self.cfg.qkv_size)
-        self.attn = z(self.HQ * self.D)
-        self.hmid = z(self.I)
+        # one activation row per layer: every address is written once per step
+        # (the persistent kernel reads them through the caches)
+        self.hid_rows = z(self.L + 1, self.H)     # row 0: the step's input embedding
+        self.hid = self.hid_rows[0]
+        self.h1_rows = z(self.L, self.H)
+        self.qkv_rows = z(self.L, self.cfg.qkv_size)
+        self.attn_rows = z(self.L, self.HQ * self.D)
+        self.hmid_rows = z(self.L, self.I)
         self.kpool = z(self.L, self.max_pages, self.HKV, _lib.PAGE_SIZE, self.D)
         self.vpool = z(self.L, self.max_pages, self.HKV, _lib.PAGE_SIZE, self.D)
         self.scores = z(self.HQ, self.cap, dtype=f32)
@@ -132,8 +145,10 @@ class Engine:
         self.pout = z(self.nsplit, self.HQ, self.D, dtype=f32)
         self.counters = z(self.HKV, dtype=i32)
         self.logits = z(self.V, dtype=f32)
-        self.bv = z(self.nb, dtype=f32)
-        self.bi = z(self.nb, dtype=i32)
+        self.grid = int(self._lib.tfd_decode_persistent_grid())
+        self.bv = z(max(self.nb, self.grid), dtype=f32)
+        self.bi = z(max(self.nb, self.grid), dtype=i32)
+        self.barrier = z(_lib.BARRIER_WORDS, dtype=i32)
         self.pos = z(1, dtype=i32)
         self.ids = z(1, dtype=torch.int64)
         self.inp = z(self.nsteps, dtype=i32)
@@ -150,24 +165,26 @@ class Engine:
         L, w = self._lib, self.layers[i]
         H, I, D = self.H, self.I, self.D
         kp, vp = self.kpool[i], self.vpool[i]
-        L.tfd_gemv_bf16(ptr(self.hid), ptr(w["gamma_in"]), ptr(w["w_qkv"]), None, ptr(self.qkv),
+        x_in, x_out = self.hid_rows[i], self.hid_rows[i + 1]
+        h1, qkv, attn, hmid = self.h1_rows[i], self.qkv_rows[i], self.attn_rows[i], self.hmid_rows[i]
+        L.tfd_gemv_bf16(ptr(x_in), ptr(w["gamma_in"]), ptr(w["w_qkv"]), None, ptr(qkv),
                         H, self.cfg.qkv_size, _lib.PRO_NORM, _lib.EPI_STORE, self.eps, s)
         L.tfd_attn_rope_scores_paged(
-            ptr(self.qkv), ptr(w["gamma_q"]), ptr(w["gamma_k"]), ptr(self.cos), ptr(self.sin),
+            ptr(qkv), ptr(w["gamma_q"]), ptr(w["gamma_k"]), ptr(self.cos), ptr(self.sin),
             self.cap, ptr(self.pos), ptr(self.pos), ptr(self.page_table), self.max_pages,
             ptr(kp), ptr(vp), self.max_pages, self.HQ, self.HKV, D, self.scale, self.eps,
             ptr(self.scores), self.cap, ptr(self.smax), ptr(self.snew), self.nsplit,
             ptr(self.err), s)
         L.tfd_attn_pv_combine_paged(
-            ptr(self.qkv), ptr(self.pos), ptr(self.page_table), self.max_pages, ptr(vp),
+            ptr(qkv), ptr(self.pos), ptr(self.page_table), self.max_pages, ptr(vp),
             self.max_pages, self.HQ, self.HKV, D, ptr(self.scores), self.cap, ptr(self.smax),
             ptr(self.snew), ptr(self.psum), ptr(self.pout), self.nsplit, ptr(self.counters),
-            ptr(self.attn), ptr(self.err), s)
-        L.tfd_gemv_bf16(ptr(self.attn), None, ptr(w["w_o"]), ptr(self.hid), ptr(self.h1),
+            ptr(attn), ptr(self.err), s)
+        L.tfd_gemv_bf16(ptr(attn), None, ptr(w["w_o"]), ptr(x_in), ptr(h1),
                         self.HQ * D, H, _lib.PRO_PLAIN, _lib.EPI_RESID, self.eps, s)
-        L.tfd_gemv_bf16(ptr(self.h1), ptr(w["gamma_post"]), ptr(w["w_gu"]), None, ptr(self.hmid),
+        L.tfd_gemv_bf16(ptr(h1), ptr(w["gamma_post"]), ptr(w["w_gu"]), None, ptr(hmid),
                         H, 2 * I, _lib.PRO_NORM, _lib.EPI_SWIGLU, self.eps, s)
-        L.tfd_gemv_bf16(ptr(self.hmid), None, ptr(w["w_down"]), ptr(self.h1), ptr(self.hid),
+        L.tfd_gemv_bf16(ptr(hmid), None, ptr(w["w_down"]), ptr(h1), ptr(x_out),
                         I, H, _lib.PRO_PLAIN, _lib.EPI_RESID, self.eps, s)
 
     def _step(self, record: list | None = None):
@@ -178,8 +195,9 @@ class Engine:
         for i in range(self.L):
             self._layer(i, s)
             if record is not None:
-                record.append(self.hid.clone())
-        self._lib.tfd_lm_head_argmax_bf16(ptr(self.hid), ptr(self.gamma_final), ptr(self.w_head),
+                record.append(self.hid_rows[i + 1].clone())
+        self._lib.tfd_lm_head_argmax_bf16(ptr(self.hid_rows[self.L]), ptr(self.gamma_final),
+                                          ptr(self.w_head),
                                           ptr(self.logits), ptr(self.bv), ptr(self.bi), self.H,
                                           self.V, self.nb, self.eps, s)
         self._lib.tfd_argmax_finalize(ptr(self.bv), ptr(self.bi), self.nb, ptr(self.inp),
@@ -206,9 +224,76 @@ class Engine:
         torch.cuda.synchronize(self.device)
         self._reset()
 
+    def _persistent_args(self):
+        """The layer table (device) and the argument block of the persistent kernel."""
+        layers = (_lib.TfdLayer * self.L)()
+        for i, w in enumerate(self.layers):
+            layers[i] = _lib.TfdLayer(
+                ptr(w["w_qkv"]), ptr(w["w_o"]), ptr(w["w_gu"]), ptr(w["w_down"]),
+                ptr(w["gamma_in"]), ptr(w["gamma_post"]), ptr(w["gamma_q"]), ptr(w["gamma_k"]),
+                ptr(self.kpool[i]), ptr(self.vpool[i]))
+        raw = torch.frombuffer(bytearray(bytes(layers)), dtype=torch.uint8)
+        self.layer_table = raw.to(self.device)
+        c = self.cfg
+        self.args = _lib.TfdDecodeArgs(
+            layers=ptr(self.layer_table), n_layers=self.L, hidden=self.H, heads=self.HQ,
+            kv_heads=self.HKV, head_dim=self.D, intermediate=self.I, vocab=self.V,
+            eps=self.eps, scale=self.scale, w_embed=ptr(self.w_embed), w_head=ptr(self.w_head),
+            gamma_final=ptr(self.gamma_final), cos_table=ptr(self.cos), sin_table=ptr(self.sin),
+            rope_rows=self.cap, page_table=ptr(self.page_table), max_pages=self.max_pages,
+            num_pages=self.max_pages, hid=ptr(self.hid_rows), h1=ptr(self.h1_rows),
+            qkv=ptr(self.qkv_rows), attn=ptr(self.attn_rows), hmid=ptr(self.hmid_rows),
+            scores=ptr(self.scores),
+            score_stride=self.cap, split_max=ptr(self.smax), score_new=ptr(self.snew),
+            part_sum=ptr(self.psum), part_out=ptr(self.pout), nsplit=self.nsplit,
+            counters=ptr(self.counters), logits=ptr(self.logits), block_val=ptr(self.bv),
+            block_idx=ptr(self.bi), ids=ptr(self.ids), pos=ptr(self.pos), inp=ptr(self.inp),
+            prompt_len=ptr(self.plen), sam=ptr(self.sam), nsteps=self.nsteps,
+            barrier=ptr(self.barrier), err=ptr(self.err))
+        del c
+
+    def phase_timeline(self, prompt_ids: list[int], steps: int) -> torch.Tensor:
+        """Per-phase device time (us) of the persistent kernel for *steps* steps
+        after walking *prompt_ids*: ``[steps, 6 * layers + 2]`` -- for each layer
+        qkv, attention scores, attention P.V, o, gate/up, down (each measured on
+        block 0 from leaving one grid barrier to leaving the next), then the
+        head and the pick."""
+        if self.mode != "persistent":
+            raise ValueError("the phase timeline belongs to the persistent kernel")
+        n = _lib.timeline_stamps(self.L)
+        buf = torch.zeros(steps * n, device=self.device, dtype=torch.int64)
+        self._load_prompt(prompt_ids)
+        self.run_steps(len(prompt_ids) - 1)
+        self.args.timeline, self.args.timeline_steps = ptr(buf), steps
+        try:
+            self.run_steps(steps)
+            torch.cuda.synchronize(self.device)
+        finally:
+            self.args.timeline, self.args.timeline_steps = None, 0
+        stamps = buf.view(steps, n).double().cpu() * 0.01      # 100 MHz clock -> us
+        leave = stamps[:, 1::2]                                 # barrier exits
+        first = stamps[:, :1]                                   # arrival at the first barrier
+        # phase k runs from leaving barrier k-1 to leaving barrier k
+        prev = torch.cat([first, leave[:, :-1]], dim=1)
+        return leave - prev
+
+    def run_steps(self, n: int):
+        """*n* decode steps: one persistent launch, or n replays / direct steps."""
+        if n <= 0:
+            return
+        if self.mode == "persistent":
+            self.barrier.zero_()
+            self._lib.tfd_decode_persistent(ctypes.byref(self.args), n, 0, self._stream())
+        else:
+            for _ in range(n):
+                self.replay()
+
     def replay(self):
-        """One decode step (graph replay, or direct launches without a graph)."""
-        if self.graph is not None:
+        """One decode step."""
+        if self.mode == "persistent":
+            self.barrier.zero_()
+            self._lib.tfd_decode_persistent(ctypes.byref(self.args), 1, 0, self._stream())
+        elif self.graph is not None:
             self.graph.replay()
         else:
             self._step()
@@ -232,6 +317,10 @@ class Engine:
         """Raise if a kernel flagged an out-of-range index since the last reset."""
         e = int(self.err.item())
         if e:
+            if e & _lib.ERR_BARRIER:
+                self.barrier.zero_()
+                raise RuntimeError("the persistent decode kernel gave up at a grid barrier "
+                                   "(bounded wait exceeded); its results are void")
             names = [n for bit, n in ((1, "token id"), (2, "position"), (4, "page-table entry"),
                                       (8, "step")) if e & bit]
             raise RuntimeError(f"decode kernels flagged an out-of-range {', '.join(names)}")
@@ -253,13 +342,14 @@ class Engine:
                 if record_logits else None)
         torch.cuda.synchronize(self.device)
         t0 = perf_counter()
-        for _ in range(pl - 1):
-            self.replay()
+        self.run_steps(pl - 1)
         torch.cuda.synchronize(self.device)
         t1 = perf_counter()
-        for k in range(max_new):
-            self.replay()
-            if hist is not None:
+        if hist is None:
+            self.run_steps(max_new)
+        else:
+            for k in range(max_new):
+                self.replay()
                 hist[k].copy_(self.logits)
         torch.cuda.synchronize(self.device)
         t2 = perf_counter()
@@ -270,8 +360,7 @@ class Engine:
     def logits_for(self, prompt_ids: list[int]) -> torch.Tensor:
         """The logits after consuming every token of *prompt_ids* (f32 copy)."""
         self._load_prompt(prompt_ids)
-        for _ in range(len(prompt_ids)):
-            self.replay()
+        self.run_steps(len(prompt_ids))
         torch.cuda.synchronize(self.device)
         self.check_errors()
         return self.logits.clone()
@@ -280,8 +369,7 @@ class Engine:
         """Hidden state entering the stack and leaving each layer, at the last
         prompt position (engine.py:273-287)."""
         self._load_prompt(prompt_ids)
-        for _ in range(len(prompt_ids) - 1):
-            self.replay()
+        self.run_steps(len(prompt_ids) - 1)
         rec: list[torch.Tensor] = []
         self._step(record=rec)
         torch.cuda.synchronize(self.device)
