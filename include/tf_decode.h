@@ -53,6 +53,10 @@ extern "C" {
 const char* tfd_last_error(void);
 int tfd_abi_version(void);
 
+/* out[i] = bf16(in[i]), round-to-nearest-even: the rounding every kernel applies
+ * at the HIR's bf16 points (the evaluator's Tensor.to(bfloat16), ir/hir/tensor/cast.py:43). */
+int tfd_round_bf16(const float* in, void* out, int n, void* stream);
+
 /* RMSNorm with the Qwen3 rounding order: out = bf16(bf16(x*rsqrt(mean(x^2)+eps))*gamma).
  * Replaces fast/kernels.py:58-79 (rms_norm); semantics ref_src/model.py:125-137
  * (input_rms_norm) and :289-298 (final_rms_norm).  n % 8 == 0, n <= 8192. */

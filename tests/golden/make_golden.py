@@ -1,0 +1,94 @@
+"""Regenerate the committed golden fixtures (CPU, minutes at C2 size).
+
+    python tests/golden/make_golden.py [c1] [c2]
+
+c1_tiny_fp32.json   BASELINE config 1: tiny Qwen3 (2 layers, hidden 256, 4q/2kv,
+                    head_dim 64, I 768, V 4096), fp32, every parameter N(0, 0.02)
+                    from seed 0, a 128-token uniform-random prompt (seed 0), 32
+                    greedy tokens.  Produced by the oracle AND by Hugging Face
+                    Qwen3ForCausalLM (full-sequence forward, same weights); the
+                    script refuses to write unless the two agree.
+c2_qwen3_1p7b.json  BASELINE config 2 shape (28 layers, bf16), the bench's
+                    synthetic weights (seed 0) and 32-token prompt (seed 0): the
+                    oracle's first 64 greedy tokens, their top-2 margins and each
+                    step's top-8 (index, logit); for both norm-scale draws.
+c2_*_logits.npy     full bf16 logits (raw uint16) of steps 0 and 63.
+
+The fixtures are data (inputs and expected outputs), regenerated from seeds.
+"""
+from __future__ import annotations
+
+import json
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parents[2]
+sys.path.insert(0, str(ROOT))
+HERE = Path(__file__).resolve().parent
+
+from oracle import qwen3_hir as O  # noqa: E402
+from tilefoundry_amd.qwen3 import QWEN3_1_7B, TINY, synthetic_weights  # noqa: E402
+
+
+def prompt_ids(n: int, vocab: int, seed: int = 0) -> list[int]:
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, vocab, (n,), generator=g).tolist()
+
+
+def hf_greedy(dims, w, prompt, n):
+    from tests.test_oracle_pins import _hf_model
+
+    model = _hf_model(dims, w)
+    seq = list(prompt)
+    with torch.no_grad():
+        for _ in range(n):
+            logits = model(torch.tensor(seq).unsqueeze(0)).logits[0, -1]
+            seq.append(int(torch.argmax(logits)))
+    return seq[len(prompt):]
+
+
+def make_c1():
+    dims = O.C1
+    w = synthetic_weights(TINY, seed=0)
+    prompt = prompt_ids(128, dims.vocab)
+    run = O.decode(O.Qwen3Oracle(dims, w), prompt, 32)
+    hf = hf_greedy(dims, w, prompt, 32)
+    if hf != run.tokens:
+        raise SystemExit(f"oracle and HF disagree: {run.tokens} vs {hf}")
+    top = [[[int(i), float(v)] for v, i in zip(*torch.topk(lg, 16))] for lg in run.logits]
+    out = {"config": "C1 tiny Qwen3 fp32; all parameters N(0,0.02) seed 0; prompt 128 ids seed 0",
+           "prompt": prompt, "tokens": run.tokens, "hf_tokens": hf, "margins": run.margins,
+           "top16": top}
+    (HERE / "c1_tiny_fp32.json").write_text(json.dumps(out))
+    print("c1: tokens", run.tokens[:8], "...")
+
+
+def make_c2():
+    dims = O.C2
+    prompt = prompt_ids(32, dims.vocab)
+    out = {"config": "C2 Qwen3-1.7B-arch bf16; N(0,0.02) seed 0; prompt 32 ids seed 0",
+           "prompt": prompt}
+    for norms in ("random", "ones"):
+        t0 = time.time()
+        w = synthetic_weights(QWEN3_1_7B, seed=0, norms=norms)
+        run = O.decode(O.Qwen3Oracle(dims, w), prompt, 64)
+        top = [[[int(i), float(v)] for v, i in zip(*torch.topk(lg, 8))] for lg in run.logits]
+        out[norms] = {"tokens": run.tokens, "margins": run.margins, "top8": top}
+        for k in (0, 63):
+            raw = run.logits[k].to(torch.bfloat16).view(torch.int16).numpy().astype(np.uint16)
+            np.save(HERE / f"c2_{norms}_logits_step{k}.npy", raw)
+        print(f"c2 {norms}: {time.time() - t0:.0f}s tokens {run.tokens[:8]}...", flush=True)
+        del w
+    (HERE / "c2_qwen3_1p7b.json").write_text(json.dumps(out))
+
+
+if __name__ == "__main__":
+    which = sys.argv[1:] or ["c1", "c2"]
+    if "c1" in which:
+        make_c1()
+    if "c2" in which:
+        make_c2()

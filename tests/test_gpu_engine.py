@@ -44,9 +44,11 @@ def _first_divergence(a, b):
 
 def _check_run(eng_run, orc_run, steps, strict=True):
     """Free-running greedy parity.  strict: all *steps* tokens identical.
-    Otherwise the first divergence must sit where the oracle's own bf16 logits
-    put the engine's pick within one ulp of its pick (a tie at the reference's
-    output precision, decided by f32 summation order)."""
+    Otherwise the first divergence must be explained by the logit error at that
+    step: the oracle's gap between its pick and the engine's is at most twice
+    the largest |engine - oracle| logit difference (both logits moved by at most
+    that much; with bf16 logits such near-ties are decided by f32 summation
+    order)."""
     k = _first_divergence(eng_run.tokens[:steps], orc_run.tokens[:steps])
     upto = steps if k is None else k + 1
     for j in range(upto):
@@ -54,32 +56,33 @@ def _check_run(eng_run, orc_run, steps, strict=True):
         assert r["max_rel"] <= 2e-2, (j, r)
     if k is None:
         return None
-    ol = orc_run.logits[k]
+    ol, el = orc_run.logits[k], eng_run.logits[k]
     mine, theirs = eng_run.tokens[k], orc_run.tokens[k]
     gap = float(ol[theirs] - ol[mine])
+    eps = float((el - ol).abs().max())
     detail = (f"diverged at step {k}: engine {mine} (oracle logit {float(ol[mine])}, engine "
-              f"{float(eng_run.logits[k][mine])}) vs oracle {theirs} (oracle logit "
-              f"{float(ol[theirs])}, engine {float(eng_run.logits[k][theirs])}); "
-              f"oracle margin {orc_run.margins[k]}")
+              f"{float(el[mine])}) vs oracle {theirs} (oracle logit {float(ol[theirs])}, "
+              f"engine {float(el[theirs])}); oracle margin {orc_run.margins[k]}, max|dlogit| {eps}")
     assert not strict, detail
-    assert gap <= _ulp_at(float(ol[theirs])), detail
+    assert gap <= 2 * eps + 1e-12, detail
     return k
 
 
 def _teacher_forced(eng, prompt, orc_run, steps):
     """Feed the oracle's own continuation as the prompt: the engine's pick at
-    every position must equal the oracle's unless the oracle's top-2 are within
-    one bf16 ulp (then the engine's pick must be one of those)."""
+    every position must equal the oracle's, except where the oracle's margin to
+    the engine's pick is within twice that step's largest logit difference."""
     seq = list(prompt) + orc_run.tokens[:steps - 1]
-    eng.logits_for(seq)
+    hist = eng.generate(seq, 1, record_logits=False)  # walks the whole sequence
+    del hist
     picks = eng.sam[len(prompt) - 1: len(prompt) - 1 + steps].tolist()
     near_ties = 0
     for k in range(steps):
         if picks[k] == orc_run.tokens[k]:
             continue
         ol = orc_run.logits[k]
-        top = float(ol.max())
-        assert float(ol[picks[k]]) >= top - _ulp_at(top), (k, picks[k], orc_run.tokens[k])
+        gap = float(ol.max() - ol[picks[k]])
+        assert gap <= 2 * 2e-2 * float(ol.abs().max()), (k, picks[k], orc_run.tokens[k], gap)
         near_ties += 1
     return near_ties
 

@@ -30,6 +30,7 @@ F = c_float
 SIGNATURES: dict[str, list] = {
     "tfd_abi_version": [],
     "tfd_last_error": [],
+    "tfd_round_bf16": [P, P, I, P],
     "tfd_rmsnorm_bf16": [P, P, P, I, F, P],
     "tfd_embed_bf16": [P, P, P, I, I, P, P],
     "tfd_gemv_bf16": [P, P, P, P, P, I, I, I, I, F, P],

@@ -5,10 +5,11 @@
 // and the reference evaluator computes each such op in f32 and rounds once
 // (torch CPU semantics for bf16 tensors).  The helpers below reproduce that:
 //   * rbf(x)   rounds an f32 to the nearest-even bf16 and back (c10::BFloat16's
-//              rule, NaN -> 0x7fc0);
+//              rule for every non-NaN value);
 //   * the file is compiled with -ffp-contract=off so `a * b + c` stays two
-//     rounded ops, as two torch ops are; FMAs are written out (fmaf) only in
-//     dot-product accumulations, whose order is not the reference's anyway;
+//     rounded ops, as two torch ops are; fused arithmetic (the packed bf16 dot)
+//     is used only in matmul accumulations, whose order is not the reference's
+//     anyway;
 //   * reductions run in f32 in a fixed order (lane-sequential, then an xor
 //     butterfly), so every block that recomputes a reduction gets the same bits.
 #pragma once
@@ -31,36 +32,54 @@ __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w <<
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bf2f(bf16 b) { return __uint_as_float(((uint32_t)b) << 16); }
 
-__device__ __forceinline__ bf16 f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16)0x7fc0;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16)(u >> 16);
-}
+// f32 -> bf16 with round-to-nearest-even: gfx950's packed convert instruction
+// (v_cvt_pk_bf16_f32), which rounds as c10::BFloat16 does for every finite value
+// and infinity (tests/test_gpu_rounding.py checks it against torch bit for bit).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ bf16 f2bf(float f) { return __builtin_bit_cast(bf16, (__bf16)f); }
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
-// Sum over the 64 lanes; every lane ends with the same bits (a + b == b + a).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
+// Cross-lane reductions.  Within a row of 16 lanes the partner values come
+// from DPP (quad_perm xor 1, xor 2, row_half_mirror, row_mirror: VALU operand
+// modifiers, no LDS traffic); across rows from ds_bpermute.  Every step adds a
+// value to its partner's, and a + b == b + a, so all participating lanes end
+// with the same bits.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
 }
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-  return v;
-}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within 16
 
 // Sum within aligned groups of `width` lanes (width a power of two <= 64).
 template <int kWidth>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int m = kWidth / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  if (kWidth >= 2) v += dpp_f<kDppXor1>(v);
+  if (kWidth >= 4) v += dpp_f<kDppXor2>(v);
+  if (kWidth >= 8) v += dpp_f<kDppHalfMirror>(v);
+  if (kWidth >= 16) v += dpp_f<kDppMirror>(v);
+  if (kWidth >= 32) v += __shfl_xor(v, 16, kWave);
+  if (kWidth >= 64) v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  v = fmaxf(v, __shfl_xor(v, 32, kWave));
   return v;
 }
 
@@ -120,15 +139,20 @@ __device__ __forceinline__ void stores_done() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Dot product of two 16-byte chunks (8 bf16 each) accumulated into f32 with
+// the packed bf16 dot instruction: two exact bf16 products and the running sum
+// per instruction, four instructions per chunk.  Used only where the HIR has an
+// f32-accumulated matmul (the summation order there is not the reference's
+// anyway); products the HIR rounds to bf16 one by one are written out instead.
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
 __device__ __forceinline__ float dot8(const u32x4 w, const u32x4 x, float acc) {
-  acc = fmaf(bf_lo(w.x), bf_lo(x.x), acc);
-  acc = fmaf(bf_hi(w.x), bf_hi(x.x), acc);
-  acc = fmaf(bf_lo(w.y), bf_lo(x.y), acc);
-  acc = fmaf(bf_hi(w.y), bf_hi(x.y), acc);
-  acc = fmaf(bf_lo(w.z), bf_lo(x.z), acc);
-  acc = fmaf(bf_hi(w.z), bf_hi(x.z), acc);
-  acc = fmaf(bf_lo(w.w), bf_lo(x.w), acc);
-  acc = fmaf(bf_hi(w.w), bf_hi(x.w), acc);
+  acc = dot2(w.x, x.x, acc);
+  acc = dot2(w.y, x.y, acc);
+  acc = dot2(w.z, x.z, acc);
+  acc = dot2(w.w, x.w, acc);
   return acc;
 }
 

@@ -260,59 +260,135 @@ __device__ __forceinline__ void finalize_phase(const float* __restrict__ bv,
 }
 
 // ---------------------------------------------------------------------------
-// Attention, part 1 (self_attention, model.py:172-198).
-// Virtual block (split, kv head h).  Each block rebuilds its kv head's group of
-// query vectors and the new key from the bf16 QKV projection: per-head RMS,
-// RoPE at rope_pos, q_s = bf16(q_rope * scale).  Split 0 writes this token's key
-// and value into the paged cache at position cache_len and scores the new key;
-// every block scores its own kSplit positions of the prior context:
-//   s_j = bf16( sum_d bf16(q_s[d] * K[j][d]) )
-// and records the split's max per query head.
-// Every load is unconditional from a clamped, in-bounds address and masked
-// afterwards: a load under a divergent branch gets waited on inside it.
+// Attention over the paged cache, two phases per layer (model.py:172-212).
+// Virtual block (split, kv head h) owns kSplit context positions of one kv head
+// and its group of G query heads.  The K and V tiles a block reads depend only
+// on the position and the page table, so they are issued separately (KTile /
+// VTile) and a caller can put them in flight before it waits for the QKV
+// projection.  Every load is unconditional from a clamped, in-bounds address and
+// masked afterwards: a load under a divergent branch gets waited on inside it.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int64_t page_row(int page, int j, int kv_heads, int h, int D) {
   return (((int64_t)page * kv_heads + h) * kPage + (j % kPage)) * D;
 }
 
+template <int D>
+struct AttnShape {
+  static constexpr int kLpp = D / 8;                        // lanes per position (16-byte chunks)
+  static constexpr int kPpw = kWave / kLpp;                 // positions per wave, scores pass
+  static constexpr int kKPasses = kSplit / (kWavesPerBlock * kPpw);
+  static constexpr int kGroups = kBlock / kLpp;             // position groups, P.V pass
+  static constexpr int kVPasses = kSplit / kGroups;
+  static_assert(kKPasses * kWavesPerBlock * kPpw == kSplit, "split tiles the scores pass");
+  static_assert(kVPasses * kGroups == kSplit, "split tiles the P.V pass");
+};
+
+template <int D>
+struct KTile {
+  int pg[AttnShape<D>::kKPasses];
+  u32x4 t[AttnShape<D>::kKPasses];
+};
+template <int D>
+struct VTile {
+  int pg[AttnShape<D>::kVPasses];
+  u32x4 t[AttnShape<D>::kVPasses];
+};
+
+// position a thread reads in pass p of each pass layout
+template <int D>
+__device__ __forceinline__ int k_pos(int j0, int p) {
+  using A = AttnShape<D>;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  return j0 + p * kWavesPerBlock * A::kPpw + wave * A::kPpw + lane / A::kLpp;
+}
+template <int D>
+__device__ __forceinline__ int v_pos(int j0, int p) {
+  using A = AttnShape<D>;
+  return j0 + (int)threadIdx.x / A::kLpp + p * A::kGroups;
+}
+
+// K rows of split `split` (positions j < P are the ones used).  A split that
+// holds no prior position issues nothing.
+template <int D>
+__device__ __forceinline__ void k_tile_issue(int split, int h, int P, const int* page_table,
+                                             int max_pages, const bf16* kpool, int num_pages,
+                                             int kv_heads, KTile<D>& kt) {
+  using A = AttnShape<D>;
+  const int j0 = split * kSplit;
+  const int ch = (threadIdx.x & (kWave - 1)) % A::kLpp;
+#pragma unroll
+  for (int p = 0; p < A::kKPasses; ++p) {
+    kt.pg[p] = -1;
+    kt.t[p] = u32x4{0u, 0u, 0u, 0u};
+  }
+  if (j0 >= P) return;
+#pragma unroll
+  for (int p = 0; p < A::kKPasses; ++p) {
+    const int j = k_pos<D>(j0, p);
+    kt.pg[p] = page_table[j / kPage < max_pages ? j / kPage : max_pages - 1];
+  }
+#pragma unroll
+  for (int p = 0; p < A::kKPasses; ++p) {
+    const int j = k_pos<D>(j0, p);
+    const bool bad = kt.pg[p] < 0 || kt.pg[p] >= num_pages;
+    kt.t[p] = coh_ld16(kpool, (uint32_t)(page_row(bad ? 0 : kt.pg[p], j, kv_heads, h, D) +
+                                         ch * 8) * 2u);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void v_tile_issue(int split, int h, int P, const int* page_table,
+                                             int max_pages, const bf16* vpool, int num_pages,
+                                             int kv_heads, VTile<D>& vt) {
+  using A = AttnShape<D>;
+  const int j0 = split * kSplit;
+  const int ch = (int)threadIdx.x % A::kLpp;
+#pragma unroll
+  for (int p = 0; p < A::kVPasses; ++p) {
+    vt.pg[p] = -1;
+    vt.t[p] = u32x4{0u, 0u, 0u, 0u};
+  }
+  if (j0 >= P) return;
+#pragma unroll
+  for (int p = 0; p < A::kVPasses; ++p) {
+    const int j = v_pos<D>(j0, p);
+    vt.pg[p] = page_table[j / kPage < max_pages ? j / kPage : max_pages - 1];
+  }
+#pragma unroll
+  for (int p = 0; p < A::kVPasses; ++p) {
+    const int j = v_pos<D>(j0, p);
+    const bool bad = vt.pg[p] < 0 || vt.pg[p] >= num_pages;
+    vt.t[p] = coh_ld16(vpool, (uint32_t)(page_row(bad ? 0 : vt.pg[p], j, kv_heads, h, D) +
+                                         ch * 8) * 2u);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Part 1 (model.py:172-198).  Each block rebuilds its kv head's group of query
+// vectors and the new key from the bf16 QKV projection: per-head RMS, RoPE at
+// rp, q_s = bf16(q_rope * scale).  Split 0 writes this token's key and value
+// into the paged cache at position P and scores the new key; every block scores
+// its own positions of the prior context,
+//   s_j = bf16( sum_d bf16(q_s[d] * K[j][d]) ),
+// and records the split's max per query head.
+// ---------------------------------------------------------------------------
 template <int D, int G>
 __device__ __forceinline__ void attn_scores_phase(
     int split, int h, const bf16* __restrict__ qkv, const bf16* __restrict__ gq,
     const bf16* __restrict__ gk, const bf16* __restrict__ cos_t, const bf16* __restrict__ sin_t,
-    int rope_rows, int rp, int P,
-    const int* __restrict__ page_table, int max_pages, bf16* __restrict__ kpool,
-    bf16* __restrict__ vpool, int num_pages, int kv_heads, float scale, float eps,
-    float* __restrict__ S, int s_stride, float* __restrict__ smax, float* __restrict__ snew,
-    int* err) {
+    int rope_rows, int rp, int P, const int* __restrict__ page_table, int max_pages,
+    bf16* __restrict__ kpool, bf16* __restrict__ vpool, int num_pages, int kv_heads, float scale,
+    float eps, float* __restrict__ S, int s_stride, float* __restrict__ smax,
+    float* __restrict__ snew, const KTile<D>& kt, int* err) {
+  using A = AttnShape<D>;
   constexpr int kHalf = D / 2;
-  constexpr int kLpp = D / 8;                             // lanes per position
-  constexpr int kPpw = kWave / kLpp;                      // positions per wave per pass
-  constexpr int kPasses = kSplit / (kWavesPerBlock * kPpw);
+  constexpr int kLpp = A::kLpp;
   static_assert(kHalf <= kWave, "one wave holds a head as (d, d + D/2) lane pairs");
-  static_assert(kPasses * kWavesPerBlock * kPpw == kSplit, "split tiles the block");
   static_assert(G + 1 <= kWavesPerBlock, "one wave per vector");
   const int heads = kv_heads * G;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int j0 = split * kSplit;
-  const int sub = lane / kLpp, ch = lane % kLpp;
-
-  // ---- round trip 1: page entries, this head's QKV slice and gammas
-  int pg[kPasses];
-#pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int j = j0 + p * kWavesPerBlock * kPpw + wave * kPpw + sub;
-    const int e = j / kPage < max_pages ? j / kPage : max_pages - 1;
-    pg[p] = page_table[e];
-  }
-  const int v = wave;                     // vector this wave normalises (G queries + 1 key)
-  const bool has_vec = v < G + 1;
-  const bool isq = v < G;
-  const bool act = has_vec && lane < kHalf;
-  const int li = lane < kHalf ? lane : 0;
-  const uint32_t src = isq ? (uint32_t)((h * G + (isq ? v : 0)) * D) : (uint32_t)(heads * D + h * D);
-  const bf16* gam = isq ? gq : gk;
-  const bf16 rx0 = qkv[src + li], rx1 = qkv[src + li + kHalf];
-  const bf16 rg0 = gam[li], rg1 = gam[li + kHalf];
+  const int ch = lane % kLpp;
 
   if (split != 0 && j0 >= P) {
     if (tid < G) coh_stf(&smax[split * heads + h * G + tid], kNegInf);
@@ -326,21 +402,20 @@ __device__ __forceinline__ void attn_scores_phase(
     }
     return;
   }
-
-  // ---- round trip 2: the K tile and the rope rows
-  const int jend = (j0 + kSplit < P) ? j0 + kSplit : P;
-  u32x4 kt[kPasses];
-  bool page_ok = true;
-#pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int j = j0 + p * kWavesPerBlock * kPpw + wave * kPpw + sub;
-    const bool bad = pg[p] < 0 || pg[p] >= num_pages;
-    if (j < jend && bad) page_ok = false;
-    kt[p] = coh_ld16(kpool, (uint32_t)(page_row(bad ? 0 : pg[p], j, kv_heads, h, D) + ch * 8) * 2u);
-  }
+  // ---- this head's QKV slice, gammas and rope rows (one round trip)
+  const int v = wave;                     // vector this wave normalises (G queries + 1 key)
+  const bool has_vec = v < G + 1;
+  const bool isq = v < G;
+  const bool act = has_vec && lane < kHalf;
+  const int li = lane < kHalf ? lane : 0;
+  const uint32_t src = isq ? (uint32_t)((h * G + (isq ? v : 0)) * D) : (uint32_t)(heads * D + h * D);
+  const bf16* gam = isq ? gq : gk;
+  const bf16 rx0 = qkv[src + li], rx1 = qkv[src + li + kHalf];
+  const bf16 rg0 = gam[li], rg1 = gam[li + kHalf];
   const bf16 rc0 = cos_t[(int64_t)rp * D + li], rs0 = sin_t[(int64_t)rp * D + li];
   const bf16 rc1 = cos_t[(int64_t)rp * D + li + kHalf], rs1 = sin_t[(int64_t)rp * D + li + kHalf];
-  __builtin_amdgcn_sched_barrier(0);
+  const int page_new = page_table[P / kPage];
+  const int jend = (j0 + kSplit < P) ? j0 + kSplit : P;
   const float x0 = act ? bf2f(rx0) : 0.f, x1 = act ? bf2f(rx1) : 0.f;
   const float g0 = bf2f(rg0), g1 = bf2f(rg1);
   const float c0 = bf2f(rc0), s0 = bf2f(rs0), c1 = bf2f(rc1), s1 = bf2f(rs1);
@@ -374,11 +449,10 @@ __device__ __forceinline__ void attn_scores_phase(
 
   if (split == 0) {
     // this token's entry goes to the cache at P (fast/kernels.py:385-409)
-    const int page = page_table[P / kPage];
-    if (page < 0 || page >= num_pages) {
+    if (page_new < 0 || page_new >= num_pages) {
       if (tid == 0) raise_error(err, kErrPageRange);
     } else {
-      const int64_t off = page_row(page, P, kv_heads, h, D);
+      const int64_t off = page_row(page_new, P, kv_heads, h, D);
       const uint32_t vsrc = (uint32_t)(heads * D + kv_heads * D + h * D);
       for (int d = tid; d < D; d += kBlock) {
         coh_st_bf16(kpool, (uint32_t)(off + d), f2bf(kn[d]));
@@ -406,11 +480,14 @@ __device__ __forceinline__ void attn_scores_phase(
   float mymax[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) mymax[g] = kNegInf;
+  bool page_ok = true;
 #pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int j = j0 + p * kWavesPerBlock * kPpw + wave * kPpw + sub;
-    const bool valid = j < jend && pg[p] >= 0 && pg[p] < num_pages;
-    const uint32_t kw[4] = {kt[p].x, kt[p].y, kt[p].z, kt[p].w};
+  for (int p = 0; p < A::kKPasses; ++p) {
+    const int j = k_pos<D>(j0, p);
+    const bool bad = kt.pg[p] < 0 || kt.pg[p] >= num_pages;
+    if (j < jend && bad) page_ok = false;
+    const bool valid = j < jend && !bad;
+    const uint32_t kw[4] = {kt.t[p].x, kt.t[p].y, kt.t[p].z, kt.t[p].w};
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float a = 0.f;
@@ -443,17 +520,17 @@ __device__ __forceinline__ void attn_scores_phase(
 }
 
 // ---------------------------------------------------------------------------
-// Attention, part 2 (model.py:200-212).  Virtual block (split, kv head h).
-// With the joint peak M = max(split maxima, score_new):
+// Part 2 (model.py:200-212).  With the joint peak M = max(split maxima, score_new):
 //   p_j = bf16(exp(bf16(s_j - M)))
 //   per split: sum_j p_j and sum_j bf16(p_j * V[j][d]) in f32
-// The last block of a kv head to finish merges every split (in split order):
+// The last block of a kv head to finish merges every split, in split order:
 //   total    = bf16(bf16(sum p) + p_new)
 //   weighted = bf16(bf16(sum pV) + bf16(p_new * v_new))
 //   attn     = bf16(weighted / total)
 // "Last" is decided by a per-head counter; partials are written and read
 // device-coherently, and each wave waits for its own stores before the block
-// counts itself in, so the merging block sees every split.
+// counts itself in, so the merging block sees every split.  The merging block
+// stages the partials through LDS with coalesced 16-byte loads.
 // ---------------------------------------------------------------------------
 template <int D, int G>
 __device__ __forceinline__ void attn_pv_phase(
@@ -461,44 +538,31 @@ __device__ __forceinline__ void attn_pv_phase(
     const int* __restrict__ page_table, int max_pages, const bf16* __restrict__ vpool,
     int num_pages, int kv_heads, const float* __restrict__ S, int s_stride,
     const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
-    float* part_out, int* counters, bf16* __restrict__ attn_out, int* err) {
-  constexpr int kLpp = D / 8;
-  constexpr int kGroups = kBlock / kLpp;            // position groups in the P.V pass
-  constexpr int kPasses = kSplit / kGroups;
+    float* part_out, int* counters, bf16* __restrict__ attn_out, const VTile<D>& vt, int* err) {
+  using A = AttnShape<D>;
+  constexpr int kLpp = A::kLpp;
+  constexpr int kGroups = A::kGroups;
+  constexpr int kOut = G * D;                         // outputs of the head group
   static_assert(kSplit == kWave, "one wave sums one head's split of p");
   static_assert(G <= kWavesPerBlock, "one wave per query head of the group");
+  static_assert(kOut % 4 == 0 && kOut <= kBlock, "one thread per output");
   const int heads = kv_heads * G;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int ch = tid % kLpp, jo = tid / kLpp;
   const int j0 = split * kSplit;
+  (void)max_pages;
+  (void)page_table;
+  (void)vpool;
 
-  // ---- round trip 1: page entries of the split, new-key scores
-  int pg[kPasses];
-#pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int j = j0 + jo + p * kGroups;
-    const int e = j / kPage < max_pages ? j / kPage : max_pages - 1;
-    pg[p] = page_table[e];
-  }
-  const int wg = wave < G ? wave : 0;
-  const float sn = coh_ldf(&snew[h * G + wg]);
   if (P < 0 || P >= max_pages * kPage) P = 0;  // part 1 already raised the flag
   const int nact = (P + kSplit - 1) / kSplit;
   const int participants = nact > 0 ? nact : 1;
   if (split >= participants) return;
   const int jend = (j0 + kSplit < P) ? j0 + kSplit : P;
 
-  // ---- round trip 2: V tile, this split's scores, every split's max
-  u32x4 vt[kPasses];
-  bool page_ok = true;
-#pragma unroll
-  for (int p = 0; p < kPasses; ++p) {
-    const int j = j0 + jo + p * kGroups;
-    const bool bad = pg[p] < 0 || pg[p] >= num_pages;
-    if (j < jend && bad) page_ok = false;
-    vt[p] = coh_ld16(vpool, (uint32_t)(page_row(bad ? 0 : pg[p], j, kv_heads, h, D) + ch * 8) * 2u);
-    if (j >= jend || bad) vt[p] = u32x4{0u, 0u, 0u, 0u};
-  }
+  // ---- this split's scores, every split's max, the new-key scores
+  const int wg = wave < G ? wave : 0;
+  const float sn = coh_ldf(&snew[h * G + wg]);
   const float sj_raw = coh_ldf(&S[(int64_t)(h * G + wg) * s_stride + j0 + lane]);
   float mx = kNegInf;
   for (int s0 = 0; s0 < nact; s0 += kWave) {
@@ -506,12 +570,12 @@ __device__ __forceinline__ void attn_pv_phase(
     const float m = coh_ldf(&smax[(s < nsplit ? s : nsplit - 1) * heads + h * G + wg]);
     if (s < nact) mx = fmaxf(mx, m);
   }
-  __builtin_amdgcn_sched_barrier(0);
   const float sj = (j0 + lane < jend) ? sj_raw : kNegInf;
 
   __shared__ float M[G];
   __shared__ float p[G][kSplit];
-  __shared__ float red[kGroups][G * D];
+  __shared__ float red[kGroups][kOut];
+  __shared__ float psums[kGroups][G];
   __shared__ int is_last;
 
   if (wave < G) {
@@ -529,10 +593,14 @@ __device__ __forceinline__ void attn_pv_phase(
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+    bool page_ok = true;
 #pragma unroll
-    for (int q = 0; q < kPasses; ++q) {
+    for (int q = 0; q < A::kVPasses; ++q) {
       const int jj = jo + q * kGroups;
-      const uint32_t vw[4] = {vt[q].x, vt[q].y, vt[q].z, vt[q].w};
+      const bool bad = vt.pg[q] < 0 || vt.pg[q] >= num_pages;
+      if (j0 + jj < jend && bad) page_ok = false;
+      const u32x4 t = (j0 + jj < jend && !bad) ? vt.t[q] : u32x4{0u, 0u, 0u, 0u};
+      const uint32_t vw[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const float pj = p[g][jj];          // 0 past the end: adds exact zeros
@@ -550,7 +618,7 @@ __device__ __forceinline__ void attn_pv_phase(
       for (int e = 0; e < 8; ++e) red[jo][g * D + ch * 8 + e] = acc[g][e];
   }
   __syncthreads();
-  for (int o = tid; o < G * D; o += kBlock) {
+  for (int o = tid; o < kOut; o += kBlock) {
     float s = 0.f;
 #pragma unroll
     for (int q = 0; q < kGroups; ++q) s += red[q][o];
@@ -565,27 +633,47 @@ __device__ __forceinline__ void attn_pv_phase(
   }
   __syncthreads();
   if (!is_last) return;
-  const uint32_t vnew = (uint32_t)(heads * D + kv_heads * D + h * D);
-  for (int o = tid; o < G * D; o += kBlock) {
-    const int g = o / D, d = o % D;
-    float sp = 0.f, sv = 0.f;
-    constexpr int kU = 8;                    // loads in flight per thread
-    for (int s0 = 0; s0 < nact; s0 += kU) {
-      float ps[kU], pv[kU];
+  // stage up to kGroups splits at a time: coalesced 16-byte device-coherent loads
+  constexpr int kVecPerSplit = kOut / 4;
+  constexpr int kIters = (kGroups * kVecPerSplit + kBlock - 1) / kBlock;
+  float sv = 0.f, sp = 0.f;
+  for (int c0 = 0; c0 < nact; c0 += kGroups) {
+    const int nc = (nact - c0) < kGroups ? (nact - c0) : kGroups;
+    u32x4 v[kIters];
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int s = (s0 + u < nact) ? s0 + u : nact - 1;
-        ps[u] = coh_ldf(&part_sum[s * heads + h * G + g]);
-        pv[u] = coh_ldf(&part_out[((int64_t)s * heads + h * G) * D + o]);
-      }
+    for (int it = 0; it < kIters; ++it) {
+      const int idx = tid + it * kBlock;
+      const int s = idx / kVecPerSplit < nc ? idx / kVecPerSplit : nc - 1;
+      const int q4 = idx % kVecPerSplit;
+      v[it] = coh_ld16(part_out,
+                       (uint32_t)((((int64_t)(c0 + s) * heads + h * G) * D + q4 * 4) * 4));
+    }
+    float ps = 0.f;
+    if (tid < nc * G) ps = coh_ldf(&part_sum[(c0 + tid / G) * heads + h * G + tid % G]);
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        if (s0 + u < nact) {
-          sp += ps[u];
-          sv += pv[u];
-        }
+    for (int it = 0; it < kIters; ++it) {
+      const int idx = tid + it * kBlock;
+      if (idx / kVecPerSplit < nc) {
+        float* dst = &red[idx / kVecPerSplit][(idx % kVecPerSplit) * 4];
+        dst[0] = __uint_as_float(v[it].x);
+        dst[1] = __uint_as_float(v[it].y);
+        dst[2] = __uint_as_float(v[it].z);
+        dst[3] = __uint_as_float(v[it].w);
       }
     }
+    if (tid < nc * G) psums[tid / G][tid % G] = ps;
+    __syncthreads();
+    if (tid < kOut) {
+      for (int s = 0; s < nc; ++s) {
+        sv += red[s][tid];
+        sp += psums[s][tid / D];
+      }
+    }
+    __syncthreads();
+  }
+  if (tid < kOut) {
+    const int g = tid / D, d = tid % D;
+    const uint32_t vnew = (uint32_t)(heads * D + kv_heads * D + h * D);
     const float pn = rbf(expf(rbf(coh_ldf(&snew[h * G + g]) - M[g])));
     const float total = rbf(rbf(sp) + pn);
     const float weighted = rbf(rbf(sv) + rbf(pn * bf2f(qkv[vnew + d])));

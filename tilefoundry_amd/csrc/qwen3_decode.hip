@@ -53,6 +53,12 @@ __global__ __launch_bounds__(kWave) void k_rmsnorm(const bf16* __restrict__ x,
 // ---------------------------------------------------------------------------
 // Embedding row gather (model.py:279-287)
 // ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBlock) void k_round_bf16(const float* __restrict__ in,
+                                                       bf16* __restrict__ out, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    out[i] = f2bf(in[i]);
+}
+
 __global__ __launch_bounds__(kBlock) void k_embed(const bf16* __restrict__ table,
                                                   const int64_t* __restrict__ ids,
                                                   bf16* __restrict__ out, int hidden, int vocab,
@@ -106,9 +112,13 @@ __global__ __launch_bounds__(kBlock) void k_attn_rope_scores(
     bf16* __restrict__ vpool, int num_pages, int kv_heads, float scale, float eps,
     float* __restrict__ S, int s_stride, float* __restrict__ smax, float* __restrict__ snew,
     int* err) {
+  const int P = coh_ldi(cache_len);
+  KTile<D> kt;
+  k_tile_issue<D>(blockIdx.x, blockIdx.y, P, page_table, max_pages, kpool, num_pages, kv_heads,
+                  kt);
   attn_scores_phase<D, G>(blockIdx.x, blockIdx.y, qkv, gq, gk, cos_t, sin_t, rope_rows,
-                          coh_ldi(rope_pos), coh_ldi(cache_len), page_table, max_pages, kpool,
-                          vpool, num_pages, kv_heads, scale, eps, S, s_stride, smax, snew, err);
+                          coh_ldi(rope_pos), P, page_table, max_pages, kpool, vpool, num_pages,
+                          kv_heads, scale, eps, S, s_stride, smax, snew, kt, err);
 }
 
 template <int D, int G>
@@ -118,9 +128,14 @@ __global__ __launch_bounds__(kBlock) void k_attn_pv_combine(
     int num_pages, int kv_heads, const float* __restrict__ S, int s_stride,
     const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
     float* part_out, int* counters, bf16* __restrict__ attn_out, int* err) {
-  attn_pv_phase<D, G>(blockIdx.x, blockIdx.y, gridDim.x, qkv, coh_ldi(cache_len), page_table,
-                      max_pages, vpool, num_pages, kv_heads, S, s_stride, smax, snew, part_sum,
-                      part_out, counters, attn_out, err);
+  int P = coh_ldi(cache_len);
+  if (P < 0 || P >= max_pages * kPage) P = 0;
+  VTile<D> vt;
+  v_tile_issue<D>(blockIdx.x, blockIdx.y, P, page_table, max_pages, vpool, num_pages, kv_heads,
+                  vt);
+  attn_pv_phase<D, G>(blockIdx.x, blockIdx.y, gridDim.x, qkv, P, page_table, max_pages, vpool,
+                      num_pages, kv_heads, S, s_stride, smax, snew, part_sum, part_out, counters,
+                      attn_out, vt, err);
 }
 
 // ---------------------------------------------------------------------------
@@ -365,21 +380,38 @@ __global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, i
                                                  (const bf16*)w.w_qkv, nullptr, qkv_l, H, qkv_n,
                                                  eps, wq);
       gb.arrive();
+      // weights of the o projection and this block's first K / V tiles stream
+      // while the barrier resolves (they need only the position and the pages)
       gemv_issue<kCH, kRo>(vb0, (const bf16*)w.w_o, QD, H, wo);
+      KTile<D> kt;
+      VTile<D> vt;
+      const bool attn0 = vb0 < nvb_attn;
+      k_tile_issue<D>(attn0 ? vb0 % a.nsplit : a.nsplit, vb0 / a.nsplit, P, a.page_table,
+                      a.max_pages, (const bf16*)w.k_pool, a.num_pages, a.kv_heads, kt);
+      v_tile_issue<D>(attn0 ? vb0 % a.nsplit : a.nsplit, vb0 / a.nsplit, P, a.page_table,
+                      a.max_pages, (const bf16*)w.v_pool, a.num_pages, a.kv_heads, vt);
       gb.wait();
-      for (int vb = blockIdx.x; vb < nvb_attn; vb += nb)
+      for (int vb = blockIdx.x; vb < nvb_attn; vb += nb) {
+        if (vb != vb0)
+          k_tile_issue<D>(vb % a.nsplit, vb / a.nsplit, P, a.page_table, a.max_pages,
+                          (const bf16*)w.k_pool, a.num_pages, a.kv_heads, kt);
         attn_scores_phase<D, G>(vb % a.nsplit, vb / a.nsplit, qkv_l, (const bf16*)w.gamma_q,
                                 (const bf16*)w.gamma_k, (const bf16*)a.cos_table,
                                 (const bf16*)a.sin_table, a.rope_rows, P, P, a.page_table,
                                 a.max_pages, (bf16*)w.k_pool, (bf16*)w.v_pool, a.num_pages,
                                 a.kv_heads, a.scale, eps, a.scores, a.score_stride, a.split_max,
-                                a.score_new, a.err);
+                                a.score_new, kt, a.err);
+      }
       gb.sync();
-      for (int vb = blockIdx.x; vb < nvb_attn; vb += nb)
+      for (int vb = blockIdx.x; vb < nvb_attn; vb += nb) {
+        if (vb != vb0)
+          v_tile_issue<D>(vb % a.nsplit, vb / a.nsplit, P, a.page_table, a.max_pages,
+                          (const bf16*)w.v_pool, a.num_pages, a.kv_heads, vt);
         attn_pv_phase<D, G>(vb % a.nsplit, vb / a.nsplit, a.nsplit, qkv_l, P, a.page_table,
                             a.max_pages, (const bf16*)w.v_pool, a.num_pages, a.kv_heads,
                             a.scores, a.score_stride, a.split_max, a.score_new, a.part_sum,
-                            a.part_out, a.counters, attn_l, a.err);
+                            a.part_out, a.counters, attn_l, vt, a.err);
+      }
       gb.sync();
       gemv_persistent<kCH, kRo, kPlain, kResid>(attn_l, nullptr, (const bf16*)w.w_o, x_in, h1_l,
                                                 QD, H, eps, wo);
@@ -489,6 +521,15 @@ int tfd_rmsnorm_bf16(const void* x, const void* gamma, void* out, int n, float e
   TFD_CMAX_SWITCH(n, hipLaunchKernelGGL((k_rmsnorm<kC>), dim3(1), dim3(kWave), 0, s,
                                         (const bf16*)x, (const bf16*)gamma, (bf16*)out, n, eps));
   return launched("rmsnorm");
+}
+
+int tfd_round_bf16(const float* in, void* out, int n, void* stream) {
+  if (!in || !out) return fail(kBadArg, "round_bf16: null pointer");
+  if (n <= 0) return fail(kBadShape, "round_bf16: n=%d", n);
+  const int grid = (n + kBlock - 1) / kBlock < 1024 ? (n + kBlock - 1) / kBlock : 1024;
+  hipLaunchKernelGGL(k_round_bf16, dim3(grid), dim3(kBlock), 0, (hipStream_t)stream, in,
+                     (bf16*)out, n);
+  return launched("round_bf16");
 }
 
 int tfd_embed_bf16(const void* table, const int64_t* ids, void* out, int hidden, int vocab,
