@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TFD_ABI_VERSION 3
+#define TFD_ABI_VERSION 4
 
 /* gemv prologues / epilogues */
 #define TFD_PRO_PLAIN 0  /* x used as given */
@@ -128,10 +128,11 @@ int tfd_attn_pv_combine_paged(const void* qkv, const int32_t* cache_len,
 
 /* ---- persistent decode step ------------------------------------------------
  * One cooperative launch runs `steps` whole decode steps (every layer, the head,
- * the greedy pick, the next embedding) with grid barriers between dependent
- * phases, instead of ~6 launches per layer.  It computes exactly what the
- * per-kernel entries above compute, phase for phase (the same device code runs
- * on the same data partition), so the two paths give identical bits.
+ * the greedy pick, the next embedding), instead of ~6 launches per layer.  No
+ * grid barrier: every block polls for the data it needs (flag-in-data words),
+ * so a phase starts in each block as soon as its inputs exist.  It computes
+ * exactly what the per-kernel entries above compute, with the same arithmetic
+ * in the same order, so the two paths give identical bits.
  * Replaces the captured step of fast/engine.py:189-217 (graph.replay per token). */
 typedef struct TfdLayer {
   const void* w_qkv;      /* [HQ*D + 2*HKV*D][H] bf16: q rows, k rows, v rows */
@@ -158,52 +159,53 @@ typedef struct TfdDecodeArgs {
   int rope_rows;
   const int32_t* page_table;
   int max_pages, num_pages;
-  /* Activations, one row per layer so every address is written once per step:
-   * hid [n_layers + 1][H] (row 0 is the step's input embedding row, row l + 1 the
-   * output of layer l), h1 [n_layers][H], qkv [n_layers][HQ*D + 2*HKV*D],
-   * attn [n_layers][HQ*D], hmid [n_layers][I]; all bf16. */
-  void* hid;
-  void* h1;
-  void* qkv;
-  void* attn;
-  void* hmid;
-  float* scores;          /* [HQ][score_stride] */
+  /* Blocks exchange data through flag-in-data words: 8 bytes, a 32-bit payload
+   * (a bf16 pair or an f32) and the 32-bit tag of the step and layer that wrote
+   * it.  Zero these buffers once when they are allocated; tags then continue
+   * across launches from `epoch`, which the caller advances by
+   * TFD_TAGS_PER_STEP(n_layers) for every step run (and, before it would pass
+   * 2^32, zeroes the buffers again and restarts at 0). */
+  uint32_t* x_hid;        /* [H/2] words: the hidden state entering a layer or the head */
+  uint32_t* x_h1;         /* [H/2]: after attention and its residual */
+  uint32_t* x_qkv;        /* [(HQ*D + 2*HKV*D)/2] */
+  uint32_t* x_attn;       /* [HQ*D/2] */
+  uint32_t* x_mid;        /* [I/2] */
+  uint32_t* x_smax;       /* [nsplit][HQ] */
+  uint32_t* x_psum;       /* [nsplit][HQ] */
+  uint32_t* x_pout;       /* [nsplit][HQ][D] */
+  uint32_t* x_best;       /* [2 x grid blocks] */
+  uint32_t epoch;
+  float* scores;          /* [HQ][score_stride] workspace */
   int score_stride;
-  float* split_max;       /* [nsplit][HQ] */
-  float* score_new;       /* [HQ] */
-  float* part_sum;        /* [nsplit][HQ] */
-  float* part_out;        /* [nsplit][HQ][D] */
-  int nsplit;
-  int32_t* counters;      /* [HKV], zero */
-  float* logits;          /* [V] */
-  float* block_val;       /* [>= grid blocks] */
-  int32_t* block_idx;
-  int64_t* ids;
-  int32_t* pos;
+  float* score_new;       /* [HQ] workspace */
+  int nsplit;             /* >= ceil(max position + 1, 64) */
+  float* logits;          /* [V], the last step's */
+  int64_t* ids;           /* the token entering the next step */
+  int32_t* pos;           /* its position */
   const int32_t* inp;     /* [nsteps] prompt ids */
   const int32_t* prompt_len;
   int32_t* sam;           /* [nsteps] picks */
   int nsteps;
-  uint32_t* barrier;      /* TFD_BARRIER_WORDS x uint32, zeroed before every launch */
   int32_t* err;
   /* Optional phase timeline (may be null): for the first timeline_steps steps of
-   * a launch, block 0 records the 100 MHz device wall clock before and after
-   * every grid barrier, TFD_TIMELINE_STAMPS(n_layers) stamps per step. */
+   * a launch, block 0 records the 100 MHz device wall clock when each phase's
+   * input is ready and when its output is out, TFD_TIMELINE_STAMPS(n_layers)
+   * stamps per step. */
   uint64_t* timeline;
   int timeline_steps;
 } TfdDecodeArgs;
 
-/* stamps per step: per layer 6 barriers x (arrive, leave), then head and pick */
-#define TFD_TIMELINE_STAMPS(n_layers) (12 * (n_layers) + 4)
+/* per layer 7 phases (qkv, scores, P.V, merge, o, gate/up, down), then head and pick */
+#define TFD_TIMELINE_STAMPS(n_layers) (14 * (n_layers) + 4)
+#define TFD_TAGS_PER_STEP(n_layers) ((n_layers) + 1)
 
-#define TFD_ERR_BARRIER 16 /* a grid barrier waited past its bound; the launch gave up */
-#define TFD_BARRIER_WORDS 1280
+#define TFD_ERR_SYNC 16 /* a wait for another block's data passed its bound; the launch gave up */
 
-/* Run `steps` decode steps.  nblocks <= 0 picks one block per compute unit.
- * Returns -3 if the shape has no persistent instance (hidden must equal
- * heads * head_dim) or the grid cannot be co-resident. */
+/* Run `steps` decode steps in one launch.  nblocks <= 0 picks one block per
+ * compute unit.  Returns -3 if the shape has no persistent instance (hidden
+ * must equal heads * head_dim) or the grid cannot be co-resident. */
 int tfd_decode_persistent(const TfdDecodeArgs* args, int steps, int nblocks, void* stream);
-/* The grid tfd_decode_persistent(args, ., 0, .) uses (block_val must hold this many). */
+/* The grid tfd_decode_persistent(args, ., 0, .) uses (x_best must hold 2x this many words). */
 int tfd_decode_persistent_grid(void);
 
 #ifdef __cplusplus

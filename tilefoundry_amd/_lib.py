@@ -13,13 +13,12 @@ from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU = 0, 1, 2
-ERR_TOKEN_RANGE, ERR_POS_RANGE, ERR_PAGE_RANGE, ERR_STEP_RANGE, ERR_BARRIER = 1, 2, 4, 8, 16
+ERR_TOKEN_RANGE, ERR_POS_RANGE, ERR_PAGE_RANGE, ERR_STEP_RANGE, ERR_SYNC = 1, 2, 4, 8, 16
 PAGE_SIZE = 16
-BARRIER_WORDS = 1280
 ATTN_SPLIT = 64
 
 P = c_void_p
@@ -66,22 +65,27 @@ class TfdDecodeArgs(ctypes.Structure):
         ("rope_rows", c_int),
         ("page_table", c_void_p),
         ("max_pages", c_int), ("num_pages", c_int),
-        *[(n, c_void_p) for n in ("hid", "h1", "qkv", "attn", "hmid")],
+        *[(n, c_void_p) for n in ("x_hid", "x_h1", "x_qkv", "x_attn", "x_mid", "x_smax",
+                                   "x_psum", "x_pout", "x_best")],
+        ("epoch", ctypes.c_uint32),
         ("scores", c_void_p), ("score_stride", c_int),
-        *[(n, c_void_p) for n in ("split_max", "score_new", "part_sum", "part_out")],
+        ("score_new", c_void_p),
         ("nsplit", c_int),
-        ("counters", c_void_p),
-        *[(n, c_void_p) for n in ("logits", "block_val", "block_idx", "ids", "pos", "inp",
-                                   "prompt_len", "sam")],
+        *[(n, c_void_p) for n in ("logits", "ids", "pos", "inp", "prompt_len", "sam")],
         ("nsteps", c_int),
-        ("barrier", c_void_p), ("err", c_void_p),
+        ("err", c_void_p),
         ("timeline", c_void_p), ("timeline_steps", c_int),
     ]
 
 
 def timeline_stamps(n_layers: int) -> int:
     """Stamps per step of the persistent kernel's timeline (TFD_TIMELINE_STAMPS)."""
-    return 12 * n_layers + 4
+    return 14 * n_layers + 4
+
+
+def tags_per_step(n_layers: int) -> int:
+    """Flag-in-data tags one persistent step uses (TFD_TAGS_PER_STEP)."""
+    return n_layers + 1
 
 
 class TFDError(RuntimeError):

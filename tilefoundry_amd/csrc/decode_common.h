@@ -287,11 +287,84 @@ enum DeviceError : int {
   kErrPosRange = 2,        // a position past the rope table or the page table
   kErrPageRange = 4,       // a page-table entry outside the pool
   kErrStepRange = 8,       // a step past the sample buffer
-  kErrBarrier = 16,        // a grid barrier waited past its bound
+  kErrSync = 16,           // a wait for another block's data passed its bound
 };
 
 __device__ __forceinline__ void raise_error(int* err, int code) {
   if (err) atomicOr(err, code);
+}
+
+// ---------------------------------------------------------------------------
+// Flag-in-data words for the persistent kernel.  A word is 8 bytes: a 32-bit
+// payload and the 32-bit tag of the (step, layer) that wrote it, written by one
+// 8-byte device-coherent store (two words by one 16-byte store, each 8-byte half
+// carrying its own tag), so a reader sees the old word or the new one, never a
+// mix.  A reader polls until the tag it expects is there: the data is its own
+// ready signal, so no barrier, counter or store-completion wait sits between a
+// producer and its consumers.  Tags grow over a run and a buffer is rewritten
+// only after every reader of its previous contents is done (each rewrite
+// depends, through the step's data flow, on outputs that every reader produced
+// after reading), so equality is the test.  A wait is bounded: past the bound
+// it raises kErrSync, and once the flag is up every other wait gives up too.
+// ---------------------------------------------------------------------------
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+constexpr uint32_t kPollBound = 1u << 21;
+
+__device__ __forceinline__ void ll_put(uint32_t* base, uint32_t word, uint32_t payload,
+                                       uint32_t tag) {
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2{payload, tag}, rsrc(base), word * 8u, 0, kCoherent);
+}
+// words `word` and `word + 1` (word even) in one store
+__device__ __forceinline__ void ll_put2(uint32_t* base, uint32_t word, uint32_t p0, uint32_t p1,
+                                        uint32_t tag) {
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{p0, tag, p1, tag}, rsrc(base), word * 8u, 0,
+                                         kCoherent);
+}
+
+__device__ __forceinline__ bool ll_give_up(uint32_t& spins, int* err) {
+  if ((++spins & 255u) != 0) return false;
+  if (spins > kPollBound) {
+    raise_error(err, kErrSync);
+    return true;
+  }
+  return (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSync) != 0;
+}
+
+// The payloads of words `word`, `word + 1` (word even) once both carry `tag`.
+__device__ __forceinline__ u32x2 ll_get2(const uint32_t* base, uint32_t word, uint32_t tag,
+                                         int* err) {
+  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), word * 8u, 0, kCoherent);
+  uint32_t spins = 0;
+  while (v.y != tag || v.w != tag) {
+    if (ll_give_up(spins, err)) break;
+    // the compiler must issue the load again: without a clobber it may reuse the first result
+    __asm__ volatile("" ::: "memory");
+    v = __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), word * 8u, 0, kCoherent);
+  }
+  return u32x2{v.x, v.z};
+}
+
+__device__ __forceinline__ uint32_t ll_get(const uint32_t* base, uint32_t word, uint32_t tag,
+                                           int* err) {
+  u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rsrc(base), word * 8u, 0, kCoherent);
+  uint32_t spins = 0;
+  while (v.y != tag) {
+    if (ll_give_up(spins, err)) break;
+    __asm__ volatile("" ::: "memory");
+    v = __builtin_amdgcn_raw_buffer_load_b64(rsrc(base), word * 8u, 0, kCoherent);
+  }
+  return v.x;
+}
+
+// Stage a flag-in-data bf16 vector of n values (n % 4 == 0) into LDS as plain
+// bf16 pairs; the caller synchronises the block before reading it.
+__device__ __forceinline__ void ll_stage(const uint32_t* ll, int n, uint32_t tag,
+                                         uint32_t* __restrict__ lds, int* err) {
+  for (int i = threadIdx.x; i < n / 4; i += kBlock) {
+    const u32x2 p = ll_get2(ll, 2u * i, tag, err);
+    lds[2 * i] = p.x;
+    lds[2 * i + 1] = p.y;
+  }
 }
 
 }  // namespace tfd

@@ -123,6 +123,93 @@ __device__ __forceinline__ void gemv_phase(int vb, const bf16* __restrict__ x,
 }
 
 // ---------------------------------------------------------------------------
+// The persistent kernel's GEMV: x is a bf16 vector in LDS (staged from
+// flag-in-data words, or the embedding row), the residual too, and the output
+// goes out as flag-in-data bf16 pairs.  Same arithmetic as gemv_finish.
+// ---------------------------------------------------------------------------
+template <int kCmax>
+__device__ __forceinline__ void x_from_lds(const uint32_t* xs, int nch, int lane,
+                                           u32x4 (&xr)[kCmax]) {
+#pragma unroll
+  for (int i = 0; i < kCmax; ++i) {
+    const int c = i * kWave + lane;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(xs + 4 * (c < nch ? c : nch - 1));
+    xr[i] = c < nch ? v : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+__device__ __forceinline__ uint32_t bf_pair(bf16 lo, bf16 hi) {
+  return (uint32_t)lo | ((uint32_t)hi << 16);
+}
+
+template <int kCmax, int kR, int kPro, int kEpi>
+__device__ __forceinline__ void gemv_finish_ll(int vb, const uint32_t* xs,
+                                               const u32x4 (&gr)[kCmax],
+                                               const uint32_t* resid_s, uint32_t* out,
+                                               uint32_t tag, int K, int N, float eps,
+                                               const u32x4 (&w)[kR][kCmax]) {
+  static_assert(kR % 2 == 0, "outputs leave in pairs");
+  static_assert(kEpi != kSwiglu || kR % 4 == 0, "swiglu outputs leave in pairs");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t row0 = ((int64_t)vb * kWavesPerBlock + wave) * kR;
+  if (row0 >= N) return;
+  const int nvalid = (int)((N - row0) < kR ? (N - row0) : kR);
+  u32x4 xr[kCmax];
+  x_from_lds<kCmax>(xs, K / 8, lane, xr);
+  if (kPro == kNorm) rms_norm_apply<kCmax>(xr, gr, K, eps);
+  float acc[kR];
+  dot_loaded<kCmax, kR>(w, xr, acc);
+  if (kEpi == kSwiglu) {
+    // rows come as (gate_n, up_n) pairs: mlp(), model.py:230-233
+#pragma unroll
+    for (int q = 0; q < kR / 4; ++q) {
+      if (lane == q && 4 * q + 3 < nvalid) {
+        bf16 o[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float g = rbf(acc[4 * q + 2 * e]);
+          const float u = rbf(acc[4 * q + 2 * e + 1]);
+          o[e] = f2bf(rbf(silu_f(g)) * u);
+        }
+        ll_put(out, (uint32_t)(row0 / 4 + q), bf_pair(o[0], o[1]), tag);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < kR / 2; ++q) {
+      if (lane == q && 2 * q + 1 < nvalid) {
+        const float y0 = rbf(acc[2 * q]), y1 = rbf(acc[2 * q + 1]);
+        uint32_t pr;
+        if (kEpi == kResid) {
+          const uint32_t r = resid_s[(row0 + 2 * q) / 2];
+          pr = bf_pair(f2bf(bf_lo(r) + y0), f2bf(bf_hi(r) + y1));
+        } else {
+          pr = bf_pair(f2bf(y0), f2bf(y1));
+        }
+        ll_put(out, (uint32_t)((row0 + 2 * q) / 2), pr, tag);
+      }
+    }
+  }
+}
+
+// One GEMV phase of the persistent kernel.  The weights of the block's first
+// virtual block and the norm scales (gr, this lane's chunks) are already in
+// flight, issued before the wait for x; further virtual blocks issue and
+// finish in turn.
+template <int kCmax, int kR, int kPro, int kEpi>
+__device__ __forceinline__ void gemv_ll(const uint32_t* xs, const u32x4 (&gr)[kCmax],
+                                        const bf16* W, const uint32_t* resid_s, uint32_t* out,
+                                        uint32_t tag, int K, int N, float eps,
+                                        u32x4 (&w)[kR][kCmax]) {
+  const int rows_per_vb = kWavesPerBlock * kR;
+  for (int vb = blockIdx.x; vb * rows_per_vb < N; vb += gridDim.x) {
+    if (vb != (int)blockIdx.x) gemv_issue<kCmax, kR>(vb, W, K, N, w);
+    gemv_finish_ll<kCmax, kR, kPro, kEpi>(vb, xs, gr, resid_s, out, tag, K, N, eps, w);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // lm_head (model.py:300-305) with the final norm folded in and a per-block
 // greedy pick: logits are rounded to bf16 (the HIR declares them bf16) and the
 // block keeps the largest, lowest index on ties (torch.argmax's rule,
@@ -260,6 +347,76 @@ __device__ __forceinline__ void finalize_phase(const float* __restrict__ bv,
 }
 
 // ---------------------------------------------------------------------------
+// The step's last node in the persistent kernel: every block reduces all block
+// picks (flag-in-data (value, index) pairs) the way finalize_phase does and
+// derives the next token itself; block 0 also records the pick and publishes
+// the token and position for the host.  Returns the next token.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int finalize_ll(const uint32_t* best, int nb, uint32_t tag, int p,
+                                           const int* __restrict__ inp,
+                                           const int* __restrict__ plen, int nsteps, int vocab,
+                                           int64_t* ids, int* pos, int* sam, int* err) {
+  const int tid = threadIdx.x;
+  float b = kNegInf;
+  int i = 0x7fffffff;
+  for (int k = tid; k < nb; k += kBlock) {
+    const u32x2 v = ll_get2(best, 2u * k, tag, err);
+    const float bv = __uint_as_float(v.x);
+    const int bi = (int)v.y;
+    if (better(bv, bi, b, i)) {
+      b = bv;
+      i = bi;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ob = __shfl_xor(b, m, kWave);
+    const int oi = __shfl_xor(i, m, kWave);
+    if (better(ob, oi, b, i)) {
+      b = ob;
+      i = oi;
+    }
+  }
+  __shared__ float sv[kWavesPerBlock];
+  __shared__ int si[kWavesPerBlock];
+  __shared__ int next_s;
+  const int lane = tid & 63, wave = tid >> 6;
+  if (lane == 0) {
+    sv[wave] = b;
+    si[wave] = i;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float bb = sv[0];
+    int ii = si[0];
+    for (int w = 1; w < kWavesPerBlock; ++w)
+      if (better(sv[w], si[w], bb, ii)) {
+        bb = sv[w];
+        ii = si[w];
+      }
+    if (ii < 0 || ii >= vocab) ii = 0;  // all-NaN row: no pick exists
+    int next = ii;
+    if (p < 0 || p >= nsteps) {
+      if (blockIdx.x == 0) raise_error(err, kErrStepRange);
+    } else {
+      if (blockIdx.x == 0) sam[p] = ii;
+      if (p + 1 < plen[0] && p + 1 < nsteps) next = inp[p + 1];
+    }
+    if (next < 0 || next >= vocab) {
+      if (blockIdx.x == 0) raise_error(err, kErrTokenRange);
+      next = 0;
+    }
+    if (blockIdx.x == 0) {
+      coh_sti64(ids, next);
+      coh_sti(pos, p + 1);
+    }
+    next_s = next;
+  }
+  __syncthreads();
+  return next_s;
+}
+
+// ---------------------------------------------------------------------------
 // Attention over the paged cache, two phases per layer (model.py:172-212).
 // Virtual block (split, kv head h) owns kSplit context positions of one kv head
 // and its group of G query heads.  The K and V tiles a block reads depend only
@@ -364,22 +521,97 @@ __device__ __forceinline__ void v_tile_issue(int split, int h, int P, const int*
 }
 
 // ---------------------------------------------------------------------------
+// Where the attention phases exchange data.  Per-phase launches (kLL = false)
+// use plain device-coherent buffers and the kernel boundary as the barrier.
+// The persistent kernel (kLL = true) uses flag-in-data words tagged with the
+// (step, layer): the QKV projection, split maxima, numerator sums and P.V
+// partials are polled for, and the merged output is published the same way.
+// ---------------------------------------------------------------------------
+struct AttnLL {
+  const uint32_t* qkv;  // the layer's QKV projection, bf16 pairs
+  uint32_t* smax;       // [split][heads] split maxima (f32)
+  uint32_t* psum;       // [split][heads] numerator sums (f32)
+  uint32_t* pout;       // [split][heads][D] P.V partials (f32)
+  uint32_t* attn;       // [heads * D] merged output, bf16 pairs
+  uint32_t tag;
+};
+
+// The head slice one kv head's blocks work on, staged in LDS as bf16 pairs:
+// the G query vectors, then the key, then the value (D values each).
+template <int D, int G>
+__device__ __forceinline__ int head_src(int idx, int h, int heads, int kv_heads) {
+  if (idx < G * D) return h * G * D + idx;
+  if (idx < (G + 1) * D) return heads * D + h * D + (idx - G * D);
+  return heads * D + kv_heads * D + h * D + (idx - (G + 1) * D);
+}
+
+template <int D, int G>
+__device__ __forceinline__ void stage_head(int h, int heads, int kv_heads,
+                                           const bf16* __restrict__ qkv, uint32_t* hs) {
+  for (int i = threadIdx.x; i < (G + 2) * D / 2; i += kBlock) {
+    const int src = head_src<D, G>(2 * i, h, heads, kv_heads);
+    hs[i] = (uint32_t)qkv[src] | ((uint32_t)qkv[src + 1] << 16);
+  }
+}
+
+template <int D, int G>
+__device__ __forceinline__ void stage_head_ll(int h, int heads, int kv_heads, const AttnLL& ll,
+                                              uint32_t* hs, int* err) {
+  // pairs of words: every run (q group, k, v) starts at an even word
+  for (int i = threadIdx.x; i < (G + 2) * D / 4; i += kBlock) {
+    const int src = head_src<D, G>(4 * i, h, heads, kv_heads);
+    const u32x2 v = ll_get2(ll.qkv, (uint32_t)src / 2u, ll.tag, err);
+    hs[2 * i] = v.x;
+    hs[2 * i + 1] = v.y;
+  }
+}
+
+__device__ __forceinline__ float hs_at(const uint32_t* hs, int idx) {
+  const uint32_t w = hs[idx >> 1];
+  return (idx & 1) ? bf_hi(w) : bf_lo(w);
+}
+
+// Per-lane operands of the q/k norm and RoPE -- this wave's gamma pair and the
+// rope-table pair at rp -- and the page of the new position.  They depend only
+// on the layer and the position, so a caller can load them before the QKV
+// projection exists.  Indices are clamped; part 1 raises the range errors.
+struct QKPre {
+  bf16 g0, g1, c0, s0, c1, s1;
+  int page_new;
+};
+
+template <int D, int G>
+__device__ __forceinline__ QKPre qk_prefetch(int rp, int P, const bf16* __restrict__ gq,
+                                             const bf16* __restrict__ gk,
+                                             const bf16* __restrict__ cos_t,
+                                             const bf16* __restrict__ sin_t, int rope_rows,
+                                             const int* __restrict__ page_table, int max_pages) {
+  constexpr int kHalf = D / 2;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int li = lane < kHalf ? lane : 0;
+  const int64_t r = (int64_t)((rp >= 0 && rp < rope_rows) ? rp : 0) * D;
+  const int pg = (P >= 0 && P < max_pages * kPage) ? P / kPage : 0;
+  const bf16* gam = wave < G ? gq : gk;
+  return QKPre{gam[li],           gam[li + kHalf],           cos_t[r + li], sin_t[r + li],
+               cos_t[r + li + kHalf], sin_t[r + li + kHalf], page_table[pg]};
+}
+
+// ---------------------------------------------------------------------------
 // Part 1 (model.py:172-198).  Each block rebuilds its kv head's group of query
-// vectors and the new key from the bf16 QKV projection: per-head RMS, RoPE at
+// vectors and the new key from the staged head slice: per-head RMS, RoPE at
 // rp, q_s = bf16(q_rope * scale).  Split 0 writes this token's key and value
-// into the paged cache at position P and scores the new key; every block scores
-// its own positions of the prior context,
+// into the paged cache at position P; every block scores the new key (the same
+// bits in every block) and its own positions of the prior context,
 //   s_j = bf16( sum_d bf16(q_s[d] * K[j][d]) ),
 // and records the split's max per query head.
 // ---------------------------------------------------------------------------
-template <int D, int G>
+template <int D, int G, bool kLL>
 __device__ __forceinline__ void attn_scores_phase(
-    int split, int h, const bf16* __restrict__ qkv, const bf16* __restrict__ gq,
-    const bf16* __restrict__ gk, const bf16* __restrict__ cos_t, const bf16* __restrict__ sin_t,
-    int rope_rows, int rp, int P, const int* __restrict__ page_table, int max_pages,
-    bf16* __restrict__ kpool, bf16* __restrict__ vpool, int num_pages, int kv_heads, float scale,
-    float eps, float* __restrict__ S, int s_stride, float* __restrict__ smax,
-    float* __restrict__ snew, const KTile<D>& kt, int* err) {
+    int split, int h, const uint32_t* hs, const QKPre& pre, int rope_rows, int rp, int P,
+    int max_pages, bf16* __restrict__ kpool, bf16* __restrict__ vpool, int num_pages,
+    int kv_heads, float scale, float eps, float* __restrict__ S, int s_stride,
+    float* __restrict__ smax, float* __restrict__ snew, const AttnLL& ll, const KTile<D>& kt,
+    int* err) {
   using A = AttnShape<D>;
   constexpr int kHalf = D / 2;
   constexpr int kLpp = A::kLpp;
@@ -390,35 +622,40 @@ __device__ __forceinline__ void attn_scores_phase(
   const int j0 = split * kSplit;
   const int ch = lane % kLpp;
 
+  auto put_max = [&](int g, float m) {
+    if (kLL)
+      ll_put(ll.smax, (uint32_t)(split * heads + h * G + g), __float_as_uint(m), ll.tag);
+    else
+      coh_stf(&smax[split * heads + h * G + g], m);
+  };
   if (split != 0 && j0 >= P) {
-    if (tid < G) coh_stf(&smax[split * heads + h * G + tid], kNegInf);
+    if (tid < G) put_max(tid, kNegInf);
     return;
   }
   if (P < 0 || P >= max_pages * kPage || rp < 0 || rp >= rope_rows) {
     if (tid == 0) raise_error(err, kErrPosRange);
     if (tid < G) {
-      coh_stf(&smax[split * heads + h * G + tid], kNegInf);
-      if (split == 0) coh_stf(&snew[h * G + tid], 0.f);
+      put_max(tid, kNegInf);
+      if (kLL)
+        snew[tid] = 0.f;
+      else
+        coh_stf(&snew[h * G + tid], 0.f);
     }
     return;
   }
-  // ---- this head's QKV slice, gammas and rope rows (one round trip)
+  // ---- the head slice is in LDS; gammas and rope rows came with `pre`
   const int v = wave;                     // vector this wave normalises (G queries + 1 key)
   const bool has_vec = v < G + 1;
   const bool isq = v < G;
   const bool act = has_vec && lane < kHalf;
   const int li = lane < kHalf ? lane : 0;
-  const uint32_t src = isq ? (uint32_t)((h * G + (isq ? v : 0)) * D) : (uint32_t)(heads * D + h * D);
-  const bf16* gam = isq ? gq : gk;
-  const bf16 rx0 = qkv[src + li], rx1 = qkv[src + li + kHalf];
-  const bf16 rg0 = gam[li], rg1 = gam[li + kHalf];
-  const bf16 rc0 = cos_t[(int64_t)rp * D + li], rs0 = sin_t[(int64_t)rp * D + li];
-  const bf16 rc1 = cos_t[(int64_t)rp * D + li + kHalf], rs1 = sin_t[(int64_t)rp * D + li + kHalf];
-  const int page_new = page_table[P / kPage];
+  const int vbase = (v < G + 1 ? v : 0) * D;
+  const int page_new = pre.page_new;
   const int jend = (j0 + kSplit < P) ? j0 + kSplit : P;
-  const float x0 = act ? bf2f(rx0) : 0.f, x1 = act ? bf2f(rx1) : 0.f;
-  const float g0 = bf2f(rg0), g1 = bf2f(rg1);
-  const float c0 = bf2f(rc0), s0 = bf2f(rs0), c1 = bf2f(rc1), s1 = bf2f(rs1);
+  const float x0 = act ? hs_at(hs, vbase + li) : 0.f;
+  const float x1 = act ? hs_at(hs, vbase + li + kHalf) : 0.f;
+  const float g0 = bf2f(pre.g0), g1 = bf2f(pre.g1);
+  const float c0 = bf2f(pre.c0), s0 = bf2f(pre.s0), c1 = bf2f(pre.c1), s1 = bf2f(pre.s1);
 
   __shared__ float qs[G][D];
   __shared__ float kn[D];
@@ -453,21 +690,29 @@ __device__ __forceinline__ void attn_scores_phase(
       if (tid == 0) raise_error(err, kErrPageRange);
     } else {
       const int64_t off = page_row(page_new, P, kv_heads, h, D);
-      const uint32_t vsrc = (uint32_t)(heads * D + kv_heads * D + h * D);
       for (int d = tid; d < D; d += kBlock) {
         coh_st_bf16(kpool, (uint32_t)(off + d), f2bf(kn[d]));
-        coh_st_bf16(vpool, (uint32_t)(off + d), qkv[vsrc + d]);
+        const uint32_t w = hs[((G + 1) * D + d) >> 1];
+        coh_st_bf16(vpool, (uint32_t)(off + d), (bf16)((d & 1) ? (w >> 16) : (w & 0xffffu)));
       }
+      // (later steps read these rows; in the persistent kernel the wait for
+      // this block's next poll retires them before it publishes anything else)
     }
-    // score of the new key (score_new, model.py:198)
-    if (wave < G) {
-      float a = 0.f;
-      if (lane < kHalf) {
-        a = rbf(qs[wave][lane] * kn[lane]);
-        a += rbf(qs[wave][lane + kHalf] * kn[lane + kHalf]);
-      }
-      a = wave_sum(a);
-      if (lane == 0) coh_stf(&snew[h * G + wave], rbf(a));
+  }
+  // score of the new key (score_new, model.py:198): per-phase launches keep
+  // split 0's; the persistent kernel keeps every block's own copy in LDS
+  if (wave < G) {
+    float a = 0.f;
+    if (lane < kHalf) {
+      a = rbf(qs[wave][lane] * kn[lane]);
+      a += rbf(qs[wave][lane + kHalf] * kn[lane + kHalf]);
+    }
+    a = wave_sum(a);
+    if (lane == 0) {
+      if (kLL)
+        snew[wave] = rbf(a);
+      else if (split == 0)
+        coh_stf(&snew[h * G + wave], rbf(a));
     }
   }
 
@@ -499,7 +744,12 @@ __device__ __forceinline__ void attn_scores_phase(
       a = group_sum<kLpp>(a);
       const float sc = rbf(a);
       if (valid) {
-        if (ch == 0) coh_stf(&S[(int64_t)(h * G + g) * s_stride + j], sc);
+        if (ch == 0) {
+          if (kLL)
+            S[g * kSplit + (j - j0)] = sc;
+          else
+            coh_stf(&S[(int64_t)(h * G + g) * s_stride + j], sc);
+        }
         mymax[g] = fmaxf(mymax[g], sc);
       }
     }
@@ -514,31 +764,45 @@ __device__ __forceinline__ void attn_scores_phase(
   if (tid < G) {
     float m = wmax[0][tid];
     for (int w = 1; w < kWavesPerBlock; ++w) m = fmaxf(m, wmax[w][tid]);
-    coh_stf(&smax[split * heads + h * G + tid], m);
+    put_max(tid, m);
   }
   __syncthreads();
+}
+
+__device__ __forceinline__ float sn_of(const float* snew, int i) { return coh_ldf(&snew[i]); }
+
+// The last step of the softmax for one output (model.py:206-212): with the
+// joint peak M, the split sums in split order sp and sv, and the new key's
+// score and value,
+//   total    = bf16(bf16(sp) + p_new),  p_new = bf16(exp(bf16(s_new - M)))
+//   weighted = bf16(bf16(sv) + bf16(p_new * v_new))
+//   out      = bf16(weighted / total)
+__device__ __forceinline__ bf16 attn_merge_one(float sp, float sv, float sn, float M,
+                                               float vnew) {
+  const float pn = rbf(expf(rbf(sn - M)));
+  const float total = rbf(rbf(sp) + pn);
+  const float weighted = rbf(rbf(sv) + rbf(pn * vnew));
+  return f2bf(weighted / total);
 }
 
 // ---------------------------------------------------------------------------
 // Part 2 (model.py:200-212).  With the joint peak M = max(split maxima, score_new):
 //   p_j = bf16(exp(bf16(s_j - M)))
 //   per split: sum_j p_j and sum_j bf16(p_j * V[j][d]) in f32
-// The last block of a kv head to finish merges every split, in split order:
-//   total    = bf16(bf16(sum p) + p_new)
-//   weighted = bf16(bf16(sum pV) + bf16(p_new * v_new))
-//   attn     = bf16(weighted / total)
-// "Last" is decided by a per-head counter; partials are written and read
-// device-coherently, and each wave waits for its own stores before the block
-// counts itself in, so the merging block sees every split.  The merging block
-// stages the partials through LDS with coalesced 16-byte loads.
+// Per-phase launches merge in the last block of a kv head to finish (a per-head
+// counter decides; partials go through device-coherent stores, and each wave
+// waits for its own before the block counts itself in), staging the partials
+// through LDS with coalesced loads and summing in split order.  The persistent
+// kernel publishes the partials as flag-in-data words and merges in part 3.
 // ---------------------------------------------------------------------------
-template <int D, int G>
+template <int D, int G, bool kLL>
 __device__ __forceinline__ void attn_pv_phase(
     int split, int h, int nsplit, const bf16* __restrict__ qkv, int P,
     const int* __restrict__ page_table, int max_pages, const bf16* __restrict__ vpool,
     int num_pages, int kv_heads, const float* __restrict__ S, int s_stride,
     const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
-    float* part_out, int* counters, bf16* __restrict__ attn_out, const VTile<D>& vt, int* err) {
+    float* part_out, int* counters, bf16* __restrict__ attn_out, const AttnLL& ll,
+    const VTile<D>& vt, int* err) {
   using A = AttnShape<D>;
   constexpr int kLpp = A::kLpp;
   constexpr int kGroups = A::kGroups;
@@ -562,12 +826,21 @@ __device__ __forceinline__ void attn_pv_phase(
 
   // ---- this split's scores, every split's max, the new-key scores
   const int wg = wave < G ? wave : 0;
-  const float sn = coh_ldf(&snew[h * G + wg]);
-  const float sj_raw = coh_ldf(&S[(int64_t)(h * G + wg) * s_stride + j0 + lane]);
+  // the persistent kernel passes this block's own scores and new-key scores (LDS)
+  const float sn = kLL ? snew[wg] : coh_ldf(&snew[h * G + wg]);
+  const float sj_raw =
+      kLL ? S[wg * kSplit + lane] : coh_ldf(&S[(int64_t)(h * G + wg) * s_stride + j0 + lane]);
   float mx = kNegInf;
   for (int s0 = 0; s0 < nact; s0 += kWave) {
     const int s = s0 + lane;
-    const float m = coh_ldf(&smax[(s < nsplit ? s : nsplit - 1) * heads + h * G + wg]);
+    float m;
+    if (kLL) {
+      // lanes past the active splits re-read split 0's word (always written)
+      m = __uint_as_float(
+          ll_get(ll.smax, (uint32_t)((s < nact ? s : 0) * heads + h * G + wg), ll.tag, err));
+    } else {
+      m = coh_ldf(&smax[(s < nsplit ? s : nsplit - 1) * heads + h * G + wg]);
+    }
     if (s < nact) mx = fmaxf(mx, m);
   }
   const float sj = (j0 + lane < jend) ? sj_raw : kNegInf;
@@ -584,7 +857,12 @@ __device__ __forceinline__ void attn_pv_phase(
     const float pj = (j0 + lane < jend) ? rbf(expf(rbf(sj - m))) : 0.f;
     p[wave][lane] = pj;
     const float s = wave_sum(pj);
-    if (lane == 0) coh_stf(&part_sum[split * heads + h * G + wave], s);
+    if (lane == 0) {
+      if (kLL)
+        ll_put(ll.psum, (uint32_t)(split * heads + h * G + wave), __float_as_uint(s), ll.tag);
+      else
+        coh_stf(&part_sum[split * heads + h * G + wave], s);
+    }
   }
   __syncthreads();
   {
@@ -618,6 +896,20 @@ __device__ __forceinline__ void attn_pv_phase(
       for (int e = 0; e < 8; ++e) red[jo][g * D + ch * 8 + e] = acc[g][e];
   }
   __syncthreads();
+  if (kLL) {
+    for (int o = 2 * tid; o < kOut; o += 2 * kBlock) {
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int q = 0; q < kGroups; ++q) {
+        s0 += red[q][o];
+        s1 += red[q][o + 1];
+      }
+      ll_put2(ll.pout, (uint32_t)(((int64_t)split * heads + h * G) * D + o), __float_as_uint(s0),
+              __float_as_uint(s1), ll.tag);
+    }
+    __syncthreads();
+    return;
+  }
   for (int o = tid; o < kOut; o += kBlock) {
     float s = 0.f;
 #pragma unroll
@@ -674,13 +966,74 @@ __device__ __forceinline__ void attn_pv_phase(
   if (tid < kOut) {
     const int g = tid / D, d = tid % D;
     const uint32_t vnew = (uint32_t)(heads * D + kv_heads * D + h * D);
-    const float pn = rbf(expf(rbf(coh_ldf(&snew[h * G + g]) - M[g])));
-    const float total = rbf(rbf(sp) + pn);
-    const float weighted = rbf(rbf(sv) + rbf(pn * bf2f(qkv[vnew + d])));
-    coh_st_bf16(attn_out, (uint32_t)((h * G + g) * D + d), f2bf(weighted / total));
+    coh_st_bf16(attn_out, (uint32_t)((h * G + g) * D + d),
+                attn_merge_one(sp, sv, sn_of(snew, h * G + g), M[g], bf2f(qkv[vnew + d])));
   }
   if (tid == 0) atomicExch(&counters[h], 0);
   __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Part 3, persistent kernel only: every active split of a kv head merges its
+// own slice of the head group's G * D outputs (pairs of values), reading every
+// split's partials for that slice and the numerator sums, in split order --
+// the same arithmetic as the last-block merge above.
+// ---------------------------------------------------------------------------
+template <int D, int G>
+__device__ __forceinline__ void attn_merge_ll(int split, int h, int P, int max_pages,
+                                              int kv_heads, const float* snew, const AttnLL& ll,
+                                              int* err) {
+  constexpr int kPairs = G * D / 2;
+  constexpr int kChunk = 16;                          // splits staged at a time
+  const int heads = kv_heads * G;
+  const int tid = threadIdx.x;
+  if (P < 0 || P >= max_pages * kPage) P = 0;
+  const int nact = (P + kSplit - 1) / kSplit;
+  const int participants = nact > 0 ? nact : 1;
+  if (split >= participants) return;
+  const int q0 = split * kPairs / participants, q1 = (split + 1) * kPairs / participants;
+  const int nq = q1 - q0;
+
+  __shared__ float sm[kChunk][G], ps[kChunk][G];
+  __shared__ u32x2 po[kChunk][kPairs];
+  float sv0 = 0.f, sv1 = 0.f, sp = 0.f, mx = kNegInf;
+  const int o = 2 * (q0 + (tid < nq ? tid : 0));
+  const int g = o / D, d = o % D;
+  // the new key's values d, d + 1 (one word of the QKV projection)
+  const uint32_t vw = ll_get(ll.qkv, (uint32_t)(heads * D + kv_heads * D + h * D + d) / 2u,
+                             ll.tag, err);
+  for (int c0 = 0; c0 < participants; c0 += kChunk) {
+    const int nc = (participants - c0) < kChunk ? (participants - c0) : kChunk;
+    for (int i = tid; i < nc * G; i += kBlock) {
+      const uint32_t w = (uint32_t)((c0 + i / G) * heads + h * G + i % G);
+      ps[i / G][i % G] = __uint_as_float(ll_get(ll.psum, w, ll.tag, err));
+      // split maxima exist only for splits holding a prior position
+      sm[i / G][i % G] =
+          (c0 + i / G < nact) ? __uint_as_float(ll_get(ll.smax, w, ll.tag, err)) : kNegInf;
+    }
+    for (int i = tid; i < nc * nq; i += kBlock) {
+      const int s = i / nq, q = i % nq;
+      po[s][q] = ll_get2(ll.pout, (uint32_t)(((int64_t)(c0 + s) * heads + h * G) * D + 2 * (q0 + q)),
+                         ll.tag, err);
+    }
+    __syncthreads();
+    if (tid < nq) {
+      for (int s = 0; s < nc; ++s) {
+        sv0 += __uint_as_float(po[s][tid].x);
+        sv1 += __uint_as_float(po[s][tid].y);
+        sp += ps[s][g];
+        mx = fmaxf(mx, sm[s][g]);
+      }
+    }
+    __syncthreads();
+  }
+  if (tid < nq) {
+    const float sn = snew[g];
+    const float M = fmaxf(mx, sn);
+    const bf16 r0 = attn_merge_one(sp, sv0, sn, M, bf_lo(vw));
+    const bf16 r1 = attn_merge_one(sp, sv1, sn, M, bf_hi(vw));
+    ll_put(ll.attn, (uint32_t)((h * G * D + o) / 2), (uint32_t)r0 | ((uint32_t)r1 << 16), ll.tag);
+  }
 }
 
 }  // namespace tfd

@@ -116,9 +116,15 @@ __global__ __launch_bounds__(kBlock) void k_attn_rope_scores(
   KTile<D> kt;
   k_tile_issue<D>(blockIdx.x, blockIdx.y, P, page_table, max_pages, kpool, num_pages, kv_heads,
                   kt);
-  attn_scores_phase<D, G>(blockIdx.x, blockIdx.y, qkv, gq, gk, cos_t, sin_t, rope_rows,
-                          coh_ldi(rope_pos), P, page_table, max_pages, kpool, vpool, num_pages,
-                          kv_heads, scale, eps, S, s_stride, smax, snew, kt, err);
+  const int rp = coh_ldi(rope_pos);
+  const QKPre pre = qk_prefetch<D, G>(rp, P, gq, gk, cos_t, sin_t, rope_rows, page_table,
+                                      max_pages);
+  __shared__ __attribute__((aligned(16))) uint32_t hs[(G + 2) * D / 2];
+  stage_head<D, G>(blockIdx.y, kv_heads * G, kv_heads, qkv, hs);
+  __syncthreads();
+  attn_scores_phase<D, G, false>(blockIdx.x, blockIdx.y, hs, pre, rope_rows, rp, P, max_pages,
+                                 kpool, vpool, num_pages, kv_heads, scale, eps, S, s_stride, smax,
+                                 snew, AttnLL{}, kt, err);
 }
 
 template <int D, int G>
@@ -133,115 +139,10 @@ __global__ __launch_bounds__(kBlock) void k_attn_pv_combine(
   VTile<D> vt;
   v_tile_issue<D>(blockIdx.x, blockIdx.y, P, page_table, max_pages, vpool, num_pages, kv_heads,
                   vt);
-  attn_pv_phase<D, G>(blockIdx.x, blockIdx.y, gridDim.x, qkv, P, page_table, max_pages, vpool,
-                      num_pages, kv_heads, S, s_stride, smax, snew, part_sum, part_out, counters,
-                      attn_out, vt, err);
+  attn_pv_phase<D, G, false>(blockIdx.x, blockIdx.y, gridDim.x, qkv, P, page_table, max_pages,
+                             vpool, num_pages, kv_heads, S, s_stride, smax, snew, part_sum,
+                             part_out, counters, attn_out, AttnLL{}, vt, err);
 }
-
-// ---------------------------------------------------------------------------
-// Grid barrier for the persistent kernel (every block co-resident: the launch
-// is cooperative).  Counters are monotonic within a launch (barrier k completes
-// when the count reaches (k+1) x participants) and zeroed by the caller before
-// each launch, so nothing is ever reset under a racing increment.  Arrivals
-// are counted per XCD first (the hardware XCC id), one counter per XCD on its
-// own cache line, and only each XCD's last arrival touches the global counter:
-// same-address atomics serialise, so this turns 256 serial increments into 8
-// parallel groups of 32 plus 8.  Data crosses the barrier device-coherently
-// (decode_phases.h), so the barrier itself is just: every wave's stores done,
-// count in, wait.  The wait is bounded: past the bound the error bit is raised
-// and every later wait falls through, so a protocol fault ends the launch.
-//
-// Layout of the barrier buffer (uint32): [0] global count; [64 * (1 + x)] XCD
-// x's count (x < 16); [1088 + x] blocks on XCD x; [1152] the setup count.
-// ---------------------------------------------------------------------------
-constexpr unsigned kSpinBound = 1u << 20;
-
-__device__ __forceinline__ unsigned xcc_id() {
-  return __builtin_amdgcn_s_getreg((20) | (0 << 6) | ((16 - 1) << 11)) & 0xfu;
-}
-__device__ __forceinline__ unsigned coh_ldu(unsigned* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned coh_addu(unsigned* p, unsigned v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ void wait_count(unsigned* p, unsigned target, int* err) {
-  if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrBarrier) return;
-  unsigned spins = 0;
-  while (coh_ldu(p) < target) {
-    if (++spins > kSpinBound) {
-      atomicOr(err, kErrBarrier);
-      return;
-    }
-    if ((spins & 1023u) == 0 &&
-        (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrBarrier))
-      return;
-  }
-}
-
-struct GridBarrier {
-  unsigned* bar;
-  int* err;
-  unsigned xcc, per_xcc, n_xcc, k;
-
-  // One-time count of blocks per XCD (a flat barrier on its own counter).
-  __device__ __forceinline__ void setup(unsigned* b, int* e) {
-    __shared__ unsigned s_x, s_nx, s_nxcc;
-    bar = b;
-    err = e;
-    k = 0;
-    tl = nullptr;
-    if (threadIdx.x == 0) {
-      const unsigned x = xcc_id();
-      coh_addu(bar + 1088 + x, 1u);
-      stores_done();
-      coh_addu(bar + 1152, 1u);
-      wait_count(bar + 1152, gridDim.x, err);
-      unsigned n = 0;
-      for (int i = 0; i < 16; ++i) n += coh_ldu(bar + 1088 + i) ? 1u : 0u;
-      s_x = x;
-      s_nx = coh_ldu(bar + 1088 + x);
-      s_nxcc = n;
-    }
-    __syncthreads();
-    xcc = s_x;
-    per_xcc = s_nx;
-    n_xcc = s_nxcc;
-  }
-
-  uint64_t* tl;   // timeline slot of the current step (block 0 only), or null
-
-  __device__ __forceinline__ void stamp() {
-    if (tl && blockIdx.x == 0 && threadIdx.x == 0) *tl++ = wall_clock64();
-  }
-
-  // A barrier is arrive() then wait().  Memory counters retire in issue order
-  // and count loads with stores, so waiting for this block's stores must come
-  // before the next phase's weight loads are issued: callers put those loads
-  // between arrive() and wait(), where they stream while the barrier resolves.
-  __device__ __forceinline__ void arrive() {
-    stamp();
-    stores_done();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const unsigned prev = coh_addu(bar + 64 * (1 + xcc), 1u);
-      if (prev == (k + 1) * per_xcc - 1) coh_addu(bar, 1u);
-    }
-  }
-
-  __device__ __forceinline__ void wait() {
-    if (threadIdx.x == 0) wait_count(bar, (k + 1) * n_xcc, err);
-    ++k;
-    __syncthreads();
-    stamp();
-  }
-
-  __device__ __forceinline__ void sync() {
-    arrive();
-    wait();
-  }
-};
 
 // ---------------------------------------------------------------------------
 // lm_head for the persistent kernel: the same per-row arithmetic as
@@ -249,7 +150,7 @@ struct GridBarrier {
 // the next group's loads are in flight while the current one is reduced.
 // ---------------------------------------------------------------------------
 template <int kCmax, int kR>
-__device__ __forceinline__ void lm_head_rows(int64_t row0, int V, int K, int nch, int lane,
+__device__ __forceinline__ void lm_head_rows(int64_t row0, int V, int lane,
                                              const u32x4 (&xr)[kCmax],
                                              const u32x4 (&w)[kR][kCmax], float* logits,
                                              float& best, int& besti) {
@@ -270,30 +171,27 @@ __device__ __forceinline__ void lm_head_rows(int64_t row0, int V, int K, int nch
   }
 }
 
+// xr: the normalised final hidden state.  Publishes the block's pick as a
+// flag-in-data (value, index) pair.
 template <int kCmax, int kR>
-__device__ __forceinline__ void lm_head_pipelined(const bf16* __restrict__ x,
-                                                  const bf16* __restrict__ gamma,
-                                                  const bf16* __restrict__ W, float* logits,
-                                                  float* bv, int* bi, int K, int V, float eps) {
+__device__ __forceinline__ void lm_head_ll(const u32x4 (&xr)[kCmax], const bf16* __restrict__ W,
+                                           float* logits, uint32_t* best_ll, uint32_t tag, int K,
+                                           int V, u32x4 (&wa)[kR][kCmax]) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nch = K / 8;
   const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock * kR;
   int64_t r0 = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * kR;
-  u32x4 wa[kR][kCmax], wb[kR][kCmax];
-  gemv_issue<kCmax, kR>(blockIdx.x, W, K, V, wa);
-  u32x4 xr[kCmax];
-  rms_norm_x<kCmax>(x, gamma, K, eps, lane, xr);
+  u32x4 wb[kR][kCmax];
   float best = kNegInf;
   int besti = 0x7fffffff;
   while (r0 < V) {
     const int64_t r1 = r0 + stride;
     gemv_issue<kCmax, kR>((int)(r1 / (kWavesPerBlock * kR)), W, K, V, wb);
-    lm_head_rows<kCmax, kR>(r0, V, K, nch, lane, xr, wa, logits, best, besti);
+    lm_head_rows<kCmax, kR>(r0, V, lane, xr, wa, logits, best, besti);
     if (r1 >= V) break;
     const int64_t r2 = r1 + stride;
     gemv_issue<kCmax, kR>((int)(r2 / (kWavesPerBlock * kR)), W, K, V, wa);
-    lm_head_rows<kCmax, kR>(r1, V, K, nch, lane, xr, wb, logits, best, besti);
+    lm_head_rows<kCmax, kR>(r1, V, lane, xr, wb, logits, best, besti);
     r0 = r2;
   }
   __shared__ float sv[kWavesPerBlock];
@@ -311,142 +209,201 @@ __device__ __forceinline__ void lm_head_pipelined(const bf16* __restrict__ x,
         b = sv[w];
         i = si[w];
       }
-    coh_stf(&bv[blockIdx.x], b);
-    coh_sti(&bi[blockIdx.x], i);
+    ll_put2(best_ll, 2u * blockIdx.x, __float_as_uint(b), (uint32_t)i, tag);
   }
   __syncthreads();
 }
 
-// One GEMV phase of the persistent kernel.  The weights of the block's first
-// virtual block are already in flight (issued before the barrier that
-// precedes this phase); any further virtual blocks issue and finish in turn.
-template <int kCmax, int kR, int kPro, int kEpi>
-__device__ __forceinline__ void gemv_persistent(const bf16* x, const bf16* gamma, const bf16* W,
-                                                const bf16* resid, bf16* out, int K, int N,
-                                                float eps, u32x4 (&w)[kR][kCmax]) {
-  const int rows_per_vb = kWavesPerBlock * kR;
-  for (int vb = blockIdx.x; vb * rows_per_vb < N; vb += gridDim.x) {
-    if (vb != (int)blockIdx.x) gemv_issue<kCmax, kR>(vb, W, K, N, w);
-    u32x4 xr[kCmax], gr[kCmax];
-    gemv_load_x<kCmax, kPro>(x, gamma, K, xr, gr);
-    gemv_finish<kCmax, kR, kPro, kEpi>(vb, x, gamma, resid, out, K, N, eps, xr, gr, w);
-  }
+__device__ __forceinline__ void stamp(uint64_t*& tl) {
+  if (tl && blockIdx.x == 0 && threadIdx.x == 0) *tl++ = wall_clock64();
 }
 
 // ---------------------------------------------------------------------------
-// The persistent decode kernel: `steps` whole decode steps in one launch.
-// Row tiles are sized so each GEMV phase is one round of loads per wave on a
-// 256-block grid at the Qwen3-1.7B shape (qkv 4096 = 1024 waves x 4 rows,
-// o 2048 x 2, gate/up 12288 x 12, down 2048 x 2); other shapes loop.  The next
-// GEMV's weights are issued before every grid barrier, so HBM streams while
-// the barrier resolves, and the o-projection's weights ride through both
-// attention phases.
+// The persistent decode kernel: `steps` whole decode steps in one launch, with
+// no grid barrier.  Blocks hand data to each other as flag-in-data words tagged
+// with the (step, layer), and each block polls for exactly what it needs:
+//   qkv    x = the hidden state (the embedding row at layer 0, which every block
+//          reads from the table itself) -> QKV
+//   attn   head slices of QKV -> scores, split maxima -> P.V partials ->
+//          merged output (part 1, 2, 3; each block runs all its part-1 work
+//          before it waits in part 2, and all its part-2 work before part 3,
+//          so no wait can depend on work queued behind it)
+//   o      x = attention output, residual = the hidden state kept in LDS -> h1
+//   gu     x = h1 (kept in LDS for the down residual) -> SwiGLU output
+//   down   x = SwiGLU output -> the next hidden state
+//   head   x = the last hidden state -> logits and one (value, index) per block;
+//          every block reduces all of them and knows the next token.
+// The next phase's weights are issued before the wait for its input, so HBM
+// streams while the data arrives.  Row tiles are sized so each GEMV phase is one
+// round of loads per wave on a 256-block grid at the Qwen3-1.7B shape (qkv
+// 4096 = 1024 waves x 4 rows, o 2048 x 2, gate/up 12288 x 12, down 2048 x 2);
+// other shapes loop.
 // ---------------------------------------------------------------------------
 template <int kCH, int kCI, int D, int G>
 __global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, int steps) {
   constexpr int kRqkv = 4, kRo = 2, kRgu = 12, kRdown = 2, kRhead = 4;
+  constexpr int kXs = (kCH > kCI ? kCH : kCI) * kWave * 4;   // words: the longest x
+  __shared__ __attribute__((aligned(16))) uint32_t xs[kXs];
+  __shared__ __attribute__((aligned(16))) uint32_t hid_s[kCH * kWave * 4];
+  __shared__ __attribute__((aligned(16))) uint32_t h1_s[kCH * kWave * 4];
+  __shared__ __attribute__((aligned(16))) uint32_t hs[(G + 2) * D / 2];
+  // each attention work item's scores and new-key scores stay in LDS from part
+  // 1 to parts 2 and 3 (a block runs at most kMaxItems items per layer)
+  constexpr int kMaxItems = 4;
+  __shared__ float s_sc[kMaxItems][G * kSplit];
+  __shared__ float s_new[kMaxItems][G];
   const int nb = gridDim.x;
   const int H = a.hidden, I = a.intermediate, V = a.vocab;
   const int QD = a.heads * D;
   const int qkv_n = QD + 2 * a.kv_heads * D;
-  const int nvb_attn = a.nsplit * a.kv_heads;
   const float eps = a.eps;
-  // activation rows: one per layer (hid has n_layers + 1), so each address is
-  // written once per step and can be read through the caches
-  bf16* const hid = (bf16*)a.hid;
-  bf16* const h1 = (bf16*)a.h1;
-  bf16* const qkv = (bf16*)a.qkv;
-  bf16* const attn = (bf16*)a.attn;
-  bf16* const hmid = (bf16*)a.hmid;
   const int vb0 = blockIdx.x;
-  GridBarrier gb;
-  gb.setup(a.barrier, a.err);
-  int P = coh_ldi(a.pos);   // position of step 0; finalize advances it by one per step
+  int* const err = a.err;
+  int P = coh_ldi(a.pos);   // position of this step; advances by one per step
+  int tok = (int)__hip_atomic_load(a.ids, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
+  const int lane = threadIdx.x & (kWave - 1);
   u32x4 wq[kRqkv][kCH], wo[kRo][kCH], wg[kRgu][kCH], wd[kRdown][kCI];
+  u32x4 gq_in[kCH], gq_post[kCH], none[kCI];
+#pragma unroll
+  for (int i = 0; i < kCI; ++i) none[i] = u32x4{0u, 0u, 0u, 0u};
   gemv_issue<kCH, kRqkv>(vb0, (const bf16*)a.layers[0].w_qkv, H, qkv_n, wq);
+  load_x<kCH>((const bf16*)a.layers[0].gamma_in, H / 8, lane, gq_in);
   for (int t = 0; t < steps; ++t, ++P) {
-    gb.tl = (a.timeline && t < a.timeline_steps)
-                ? a.timeline + (int64_t)t * (12 * a.n_layers + 4) : nullptr;
+    uint64_t* tl = (a.timeline && t < a.timeline_steps)
+                       ? a.timeline + (int64_t)t * (14 * a.n_layers + 4) : nullptr;
+    const uint32_t tag0 = a.epoch + (uint32_t)t * (uint32_t)(a.n_layers + 1);
+    // this step's input: the embedding row of the current token
+    {
+      const int id = (tok >= 0 && tok < V) ? tok : 0;
+      const uint32_t* row = reinterpret_cast<const uint32_t*>((const bf16*)a.w_embed +
+                                                              (int64_t)id * H);
+      for (int i = threadIdx.x; i < H / 8; i += kBlock)
+        *reinterpret_cast<u32x4*>(hid_s + 4 * i) = *reinterpret_cast<const u32x4*>(row + 4 * i);
+    }
+    // attention shape at this position
+    const int nact = (P + kSplit - 1) / kSplit;
+    const int parts = nact > 0 ? nact : 1;
+    const int nvb = parts * a.kv_heads;
     for (int l = 0; l < a.n_layers; ++l) {
       const TfdLayer w = a.layers[l];
-      bf16* const x_in = hid + (int64_t)l * H;
-      bf16* const x_out = hid + (int64_t)(l + 1) * H;
-      bf16* const h1_l = h1 + (int64_t)l * H;
-      bf16* const qkv_l = qkv + (int64_t)l * qkv_n;
-      bf16* const attn_l = attn + (int64_t)l * QD;
-      bf16* const hmid_l = hmid + (int64_t)l * I;
-      gemv_persistent<kCH, kRqkv, kNorm, kStore>(x_in, (const bf16*)w.gamma_in,
-                                                 (const bf16*)w.w_qkv, nullptr, qkv_l, H, qkv_n,
-                                                 eps, wq);
-      gb.arrive();
-      // weights of the o projection and this block's first K / V tiles stream
-      // while the barrier resolves (they need only the position and the pages)
+      const uint32_t tag = tag0 + (uint32_t)l + 1u;
+      // ---- qkv
+      if (l > 0) ll_stage(a.x_hid, H, tag - 1u, hid_s, err);
+      __syncthreads();
+      stamp(tl);
+      gemv_ll<kCH, kRqkv, kNorm, kStore>(hid_s, gq_in, (const bf16*)w.w_qkv, nullptr, a.x_qkv,
+                                         tag, H, qkv_n, eps, wq);
+      stamp(tl);
+      // the o projection's weights and this block's first K / V tiles stream
+      // while the QKV projection arrives
       gemv_issue<kCH, kRo>(vb0, (const bf16*)w.w_o, QD, H, wo);
       KTile<D> kt;
       VTile<D> vt;
-      const bool attn0 = vb0 < nvb_attn;
-      k_tile_issue<D>(attn0 ? vb0 % a.nsplit : a.nsplit, vb0 / a.nsplit, P, a.page_table,
-                      a.max_pages, (const bf16*)w.k_pool, a.num_pages, a.kv_heads, kt);
-      v_tile_issue<D>(attn0 ? vb0 % a.nsplit : a.nsplit, vb0 / a.nsplit, P, a.page_table,
-                      a.max_pages, (const bf16*)w.v_pool, a.num_pages, a.kv_heads, vt);
-      gb.wait();
-      for (int vb = blockIdx.x; vb < nvb_attn; vb += nb) {
+      const int s0 = vb0 < nvb ? vb0 % parts : parts, h0 = vb0 / parts;
+      k_tile_issue<D>(s0, h0, P, a.page_table, a.max_pages, (const bf16*)w.k_pool, a.num_pages,
+                      a.kv_heads, kt);
+      v_tile_issue<D>(s0, h0, P, a.page_table, a.max_pages, (const bf16*)w.v_pool, a.num_pages,
+                      a.kv_heads, vt);
+      const QKPre pre = qk_prefetch<D, G>(P, P, (const bf16*)w.gamma_q, (const bf16*)w.gamma_k,
+                                          (const bf16*)a.cos_table, (const bf16*)a.sin_table,
+                                          a.rope_rows, a.page_table, a.max_pages);
+      const AttnLL ll{a.x_qkv, a.x_smax, a.x_psum, a.x_pout, a.x_attn, tag};
+      // ---- attention part 1: scores
+      for (int vb = vb0; vb < nvb; vb += nb) {
+        const int split = vb % parts, h = vb / parts;
         if (vb != vb0)
-          k_tile_issue<D>(vb % a.nsplit, vb / a.nsplit, P, a.page_table, a.max_pages,
-                          (const bf16*)w.k_pool, a.num_pages, a.kv_heads, kt);
-        attn_scores_phase<D, G>(vb % a.nsplit, vb / a.nsplit, qkv_l, (const bf16*)w.gamma_q,
-                                (const bf16*)w.gamma_k, (const bf16*)a.cos_table,
-                                (const bf16*)a.sin_table, a.rope_rows, P, P, a.page_table,
-                                a.max_pages, (bf16*)w.k_pool, (bf16*)w.v_pool, a.num_pages,
-                                a.kv_heads, a.scale, eps, a.scores, a.score_stride, a.split_max,
-                                a.score_new, kt, a.err);
+          k_tile_issue<D>(split, h, P, a.page_table, a.max_pages, (const bf16*)w.k_pool,
+                          a.num_pages, a.kv_heads, kt);
+        stage_head_ll<D, G>(h, a.heads, a.kv_heads, ll, hs, err);
+        __syncthreads();
+        if (vb == vb0) stamp(tl);
+        const int lv = (vb - vb0) / nb;
+        attn_scores_phase<D, G, true>(split, h, hs, pre, a.rope_rows, P, P, a.max_pages,
+                                      (bf16*)w.k_pool, (bf16*)w.v_pool, a.num_pages, a.kv_heads,
+                                      a.scale, eps, s_sc[lv], 0, nullptr, s_new[lv], ll, kt,
+                                      err);
+        if (vb == vb0) stamp(tl);
       }
-      gb.sync();
-      for (int vb = blockIdx.x; vb < nvb_attn; vb += nb) {
+      // ---- part 2: P.V partials
+      for (int vb = vb0; vb < nvb; vb += nb) {
+        const int split = vb % parts, h = vb / parts;
         if (vb != vb0)
-          v_tile_issue<D>(vb % a.nsplit, vb / a.nsplit, P, a.page_table, a.max_pages,
-                          (const bf16*)w.v_pool, a.num_pages, a.kv_heads, vt);
-        attn_pv_phase<D, G>(vb % a.nsplit, vb / a.nsplit, a.nsplit, qkv_l, P, a.page_table,
-                            a.max_pages, (const bf16*)w.v_pool, a.num_pages, a.kv_heads,
-                            a.scores, a.score_stride, a.split_max, a.score_new, a.part_sum,
-                            a.part_out, a.counters, attn_l, vt, a.err);
+          v_tile_issue<D>(split, h, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
+                          a.num_pages, a.kv_heads, vt);
+        if (vb == vb0) stamp(tl);
+        const int lv = (vb - vb0) / nb;
+        attn_pv_phase<D, G, true>(split, h, a.nsplit, nullptr, P, a.page_table, a.max_pages,
+                                  (const bf16*)w.v_pool, a.num_pages, a.kv_heads, s_sc[lv], 0,
+                                  nullptr, s_new[lv], nullptr, nullptr, nullptr, nullptr, ll, vt,
+                                  err);
+        if (vb == vb0) stamp(tl);
       }
-      gb.sync();
-      gemv_persistent<kCH, kRo, kPlain, kResid>(attn_l, nullptr, (const bf16*)w.w_o, x_in, h1_l,
-                                                QD, H, eps, wo);
-      gb.arrive();
+      // ---- part 3: merge
+      for (int vb = vb0; vb < nvb; vb += nb) {
+        if (vb == vb0) stamp(tl);
+        attn_merge_ll<D, G>(vb % parts, vb / parts, P, a.max_pages, a.kv_heads,
+                            s_new[(vb - vb0) / nb], ll, err);
+        __syncthreads();
+        if (vb == vb0) stamp(tl);
+      }
+      if (vb0 >= nvb) {
+        stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl);
+      }
+      // ---- o projection + residual
+      ll_stage(a.x_attn, QD, tag, xs, err);
+      __syncthreads();
+      stamp(tl);
+      gemv_ll<kCH, kRo, kPlain, kResid>(xs, (const u32x4(&)[kCH])none, (const bf16*)w.w_o, hid_s,
+                                        a.x_h1, tag, QD, H, eps, wo);
+      stamp(tl);
       gemv_issue<kCH, kRgu>(vb0, (const bf16*)w.w_gu, H, 2 * I, wg);
-      gb.wait();
-      gemv_persistent<kCH, kRgu, kNorm, kSwiglu>(h1_l, (const bf16*)w.gamma_post,
-                                                 (const bf16*)w.w_gu, nullptr, hmid_l, H, 2 * I,
-                                                 eps, wg);
-      gb.arrive();
+      load_x<kCH>((const bf16*)w.gamma_post, H / 8, lane, gq_post);
+      // ---- gate/up + SwiGLU
+      ll_stage(a.x_h1, H, tag, h1_s, err);
+      __syncthreads();
+      stamp(tl);
+      gemv_ll<kCH, kRgu, kNorm, kSwiglu>(h1_s, gq_post, (const bf16*)w.w_gu, nullptr, a.x_mid,
+                                         tag, H, 2 * I, eps, wg);
+      stamp(tl);
       gemv_issue<kCI, kRdown>(vb0, (const bf16*)w.w_down, I, H, wd);
-      gb.wait();
-      gemv_persistent<kCI, kRdown, kPlain, kResid>(hmid_l, nullptr, (const bf16*)w.w_down, h1_l,
-                                                   x_out, I, H, eps, wd);
-      gb.arrive();
+      // ---- down + residual
+      ll_stage(a.x_mid, I, tag, xs, err);
+      __syncthreads();
+      stamp(tl);
+      gemv_ll<kCI, kRdown, kPlain, kResid>(xs, none, (const bf16*)w.w_down, h1_s, a.x_hid, tag,
+                                           I, H, eps, wd);
+      stamp(tl);
       // the next layer's qkv weights -- or, after the last layer, layer 0's for
       // the next step (issued unconditionally: a conditional issue would keep
-      // the tile live through the whole step)
+      // the tile live through the whole step); the head streams its own
       gemv_issue<kCH, kRqkv>(vb0, (const bf16*)a.layers[(l + 1) % a.n_layers].w_qkv, H, qkv_n,
                              wq);
-      gb.wait();
+      load_x<kCH>((const bf16*)a.layers[(l + 1) % a.n_layers].gamma_in, H / 8, lane, gq_in);
+      __syncthreads();
     }
-    lm_head_pipelined<kCH, kRhead>(hid + (int64_t)a.n_layers * H, (const bf16*)a.gamma_final,
-                                   (const bf16*)a.w_head, a.logits, a.block_val, a.block_idx, H,
-                                   V, eps);
-    gb.sync();
-    if (blockIdx.x == 0)
-      finalize_phase(a.block_val, a.block_idx, nb, a.inp, a.prompt_len, a.ids, a.pos, a.sam,
-                     a.nsteps, (const bf16*)a.w_embed, hid, H, V, a.err);
-    gb.sync();
-    // the next step rewrites every activation row: drop this step's copies from
-    // this CU's L1 and this XCD's L2 before reading any of them again
-    if (threadIdx.x == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    __syncthreads();
-    if (__hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrBarrier) break;
+    // ---- head: final norm, logits, block pick
+    {
+      const uint32_t tag_head = tag0 + (uint32_t)a.n_layers;
+      u32x4 wa[kRhead][kCH], gr[kCH];
+      gemv_issue<kCH, kRhead>(vb0, (const bf16*)a.w_head, H, V, wa);
+      load_x<kCH>((const bf16*)a.gamma_final, H / 8, lane, gr);
+      ll_stage(a.x_hid, H, tag_head, hid_s, err);
+      __syncthreads();
+      stamp(tl);
+      u32x4 xr[kCH];
+      x_from_lds<kCH>(hid_s, H / 8, lane, xr);
+      rms_norm_apply<kCH>(xr, gr, H, eps);
+      lm_head_ll<kCH, kRhead>(xr, (const bf16*)a.w_head, a.logits, a.x_best, tag_head + 1u, H, V,
+                              wa);
+      stamp(tl);
+    }
+    // ---- the pick and the next token (every block)
+    stamp(tl);
+    tok = finalize_ll(a.x_best, nb, tag0 + (uint32_t)a.n_layers + 1u, P, a.inp, a.prompt_len,
+                      a.nsteps, V, a.ids, a.pos, a.sam, err);
+    stamp(tl);
+    if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSync) break;
   }
 }
 
@@ -693,16 +650,18 @@ int tfd_decode_persistent(const TfdDecodeArgs* args, int steps, int nblocks, voi
   if (!args) return fail(kBadArg, "decode_persistent: null args");
   const TfdDecodeArgs& a = *args;
   if (!a.layers || !a.w_embed || !a.w_head || !a.gamma_final || !a.cos_table || !a.sin_table ||
-      !a.page_table || !a.hid || !a.h1 || !a.qkv || !a.attn || !a.hmid || !a.scores ||
-      !a.split_max || !a.score_new || !a.part_sum || !a.part_out || !a.counters || !a.logits ||
-      !a.block_val || !a.block_idx || !a.ids || !a.pos || !a.inp || !a.prompt_len || !a.sam ||
-      !a.barrier || !a.err)
+      !a.page_table || !a.x_hid || !a.x_h1 || !a.x_qkv || !a.x_attn || !a.x_mid || !a.x_smax ||
+      !a.x_psum || !a.x_pout || !a.x_best || !a.scores || !a.score_new || !a.logits || !a.ids ||
+      !a.pos || !a.inp || !a.prompt_len || !a.sam || !a.err)
     return fail(kBadArg, "decode_persistent: null pointer in args");
   if (steps < 0) return fail(kBadArg, "decode_persistent: steps=%d", steps);
   if (steps == 0) return 0;
   if (a.n_layers <= 0 || a.kv_heads <= 0 || a.heads % a.kv_heads || a.hidden % 8 ||
       a.intermediate % 8 || a.vocab <= 0 || a.nsteps <= 0)
     return fail(kBadShape, "decode_persistent: bad model shape");
+  if ((uint64_t)a.epoch + (uint64_t)steps * (uint64_t)(a.n_layers + 1) >= 0xffffffffull)
+    return fail(kBadArg, "decode_persistent: epoch %u + %d steps passes 2^32: zero the exchange "
+                "buffers and restart the epoch at 0", a.epoch, steps);
   if (a.heads * a.head_dim != a.hidden)
     return fail(kUnsupported, "decode_persistent: needs hidden == heads * head_dim (%d vs %d)",
                 a.hidden, a.heads * a.head_dim);
@@ -712,6 +671,9 @@ int tfd_decode_persistent(const TfdDecodeArgs* args, int steps, int nblocks, voi
                 a.max_pages);
   const int grid = nblocks > 0 ? nblocks : tfd_decode_persistent_grid();
   if (grid <= 0) return fail(kUnsupported, "decode_persistent: no device");
+  if ((int64_t)a.nsplit * a.kv_heads > 4LL * grid)
+    return fail(kUnsupported, "decode_persistent: %d attention items exceed 4 per block of %d",
+                a.nsplit * a.kv_heads, grid);
   const int G = a.heads / a.kv_heads;
   const int ch = cmax_for(a.hidden), ci = cmax_for(a.intermediate);
   const void* fn = nullptr;

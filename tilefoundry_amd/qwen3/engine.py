@@ -148,7 +148,6 @@ class Engine:
         self.grid = int(self._lib.tfd_decode_persistent_grid())
         self.bv = z(max(self.nb, self.grid), dtype=f32)
         self.bi = z(max(self.nb, self.grid), dtype=i32)
-        self.barrier = z(_lib.BARRIER_WORDS, dtype=i32)
         self.pos = z(1, dtype=i32)
         self.ids = z(1, dtype=torch.int64)
         self.inp = z(self.nsteps, dtype=i32)
@@ -225,7 +224,8 @@ class Engine:
         self._reset()
 
     def _persistent_args(self):
-        """The layer table (device) and the argument block of the persistent kernel."""
+        """The layer table (device), the flag-in-data exchange buffers and the
+        argument block of the persistent kernel."""
         layers = (_lib.TfdLayer * self.L)()
         for i, w in enumerate(self.layers):
             layers[i] = _lib.TfdLayer(
@@ -234,36 +234,50 @@ class Engine:
                 ptr(self.kpool[i]), ptr(self.vpool[i]))
         raw = torch.frombuffer(bytearray(bytes(layers)), dtype=torch.uint8)
         self.layer_table = raw.to(self.device)
-        c = self.cfg
+        # exchange buffers: one 8-byte word per bf16 pair or f32 (payload, tag)
+        words = {"x_hid": self.H // 2, "x_h1": self.H // 2, "x_qkv": self.cfg.qkv_size // 2,
+                 "x_attn": self.HQ * self.D // 2, "x_mid": self.I // 2,
+                 "x_smax": self.nsplit * self.HQ, "x_psum": self.nsplit * self.HQ,
+                 "x_pout": self.nsplit * self.HQ * self.D, "x_best": 2 * self.grid}
+        self.xbuf = {k: torch.zeros(2 * n, device=self.device, dtype=torch.int32)
+                     for k, n in words.items()}
+        self.epoch = 0
         self.args = _lib.TfdDecodeArgs(
             layers=ptr(self.layer_table), n_layers=self.L, hidden=self.H, heads=self.HQ,
             kv_heads=self.HKV, head_dim=self.D, intermediate=self.I, vocab=self.V,
             eps=self.eps, scale=self.scale, w_embed=ptr(self.w_embed), w_head=ptr(self.w_head),
             gamma_final=ptr(self.gamma_final), cos_table=ptr(self.cos), sin_table=ptr(self.sin),
             rope_rows=self.cap, page_table=ptr(self.page_table), max_pages=self.max_pages,
-            num_pages=self.max_pages, hid=ptr(self.hid_rows), h1=ptr(self.h1_rows),
-            qkv=ptr(self.qkv_rows), attn=ptr(self.attn_rows), hmid=ptr(self.hmid_rows),
-            scores=ptr(self.scores),
-            score_stride=self.cap, split_max=ptr(self.smax), score_new=ptr(self.snew),
-            part_sum=ptr(self.psum), part_out=ptr(self.pout), nsplit=self.nsplit,
-            counters=ptr(self.counters), logits=ptr(self.logits), block_val=ptr(self.bv),
-            block_idx=ptr(self.bi), ids=ptr(self.ids), pos=ptr(self.pos), inp=ptr(self.inp),
-            prompt_len=ptr(self.plen), sam=ptr(self.sam), nsteps=self.nsteps,
-            barrier=ptr(self.barrier), err=ptr(self.err))
-        del c
+            num_pages=self.max_pages, **{k: ptr(t) for k, t in self.xbuf.items()}, epoch=0,
+            scores=ptr(self.scores), score_stride=self.cap, score_new=ptr(self.snew),
+            nsplit=self.nsplit, logits=ptr(self.logits), ids=ptr(self.ids), pos=ptr(self.pos),
+            inp=ptr(self.inp), prompt_len=ptr(self.plen), sam=ptr(self.sam), nsteps=self.nsteps,
+            err=ptr(self.err))
+
+    def _launch_persistent(self, n: int):
+        """One launch of *n* steps; advances the exchange-buffer epoch past them."""
+        tags = n * _lib.tags_per_step(self.L)
+        if self.epoch + tags >= 0xFFFFFFFF:
+            for t in self.xbuf.values():
+                t.zero_()
+            self.epoch = 0
+        self.args.epoch = self.epoch
+        self._lib.tfd_decode_persistent(ctypes.byref(self.args), n, 0, self._stream())
+        self.epoch += tags
 
     def phase_timeline(self, prompt_ids: list[int], steps: int) -> torch.Tensor:
-        """Per-phase device time (us) of the persistent kernel for *steps* steps
-        after walking *prompt_ids*: ``[steps, 6 * layers + 2]`` -- for each layer
-        qkv, attention scores, attention P.V, o, gate/up, down (each measured on
-        block 0 from leaving one grid barrier to leaving the next), then the
-        head and the pick."""
+        """Block 0's view of *steps* persistent steps after walking *prompt_ids*:
+        ``[steps, 7 * layers + 2, 2]`` microseconds -- per layer the qkv, attention
+        scores, P.V and merge, o, gate/up and down phases, then the head and the
+        pick; for each, the wait for its input (from the previous phase's end) and
+        its own run time."""
         if self.mode != "persistent":
             raise ValueError("the phase timeline belongs to the persistent kernel")
         n = _lib.timeline_stamps(self.L)
         buf = torch.zeros(steps * n, device=self.device, dtype=torch.int64)
         self._load_prompt(prompt_ids)
         self.run_steps(len(prompt_ids) - 1)
+        torch.cuda.synchronize(self.device)
         self.args.timeline, self.args.timeline_steps = ptr(buf), steps
         try:
             self.run_steps(steps)
@@ -271,19 +285,16 @@ class Engine:
         finally:
             self.args.timeline, self.args.timeline_steps = None, 0
         stamps = buf.view(steps, n).double().cpu() * 0.01      # 100 MHz clock -> us
-        leave = stamps[:, 1::2]                                 # barrier exits
-        first = stamps[:, :1]                                   # arrival at the first barrier
-        # phase k runs from leaving barrier k-1 to leaving barrier k
-        prev = torch.cat([first, leave[:, :-1]], dim=1)
-        return leave - prev
+        ready, done = stamps[:, 0::2], stamps[:, 1::2]
+        prev = torch.cat([ready[:, :1], done[:, :-1]], dim=1)
+        return torch.stack([ready - prev, done - ready], dim=-1)
 
     def run_steps(self, n: int):
         """*n* decode steps: one persistent launch, or n replays / direct steps."""
         if n <= 0:
             return
         if self.mode == "persistent":
-            self.barrier.zero_()
-            self._lib.tfd_decode_persistent(ctypes.byref(self.args), n, 0, self._stream())
+            self._launch_persistent(n)
         else:
             for _ in range(n):
                 self.replay()
@@ -291,8 +302,7 @@ class Engine:
     def replay(self):
         """One decode step."""
         if self.mode == "persistent":
-            self.barrier.zero_()
-            self._lib.tfd_decode_persistent(ctypes.byref(self.args), 1, 0, self._stream())
+            self._launch_persistent(1)
         elif self.graph is not None:
             self.graph.replay()
         else:
@@ -317,10 +327,9 @@ class Engine:
         """Raise if a kernel flagged an out-of-range index since the last reset."""
         e = int(self.err.item())
         if e:
-            if e & _lib.ERR_BARRIER:
-                self.barrier.zero_()
-                raise RuntimeError("the persistent decode kernel gave up at a grid barrier "
-                                   "(bounded wait exceeded); its results are void")
+            if e & _lib.ERR_SYNC:
+                raise RuntimeError("the persistent decode kernel gave up waiting for another "
+                                   "block's data (bounded wait exceeded); its results are void")
             names = [n for bit, n in ((1, "token id"), (2, "position"), (4, "page-table entry"),
                                       (8, "step")) if e & bit]
             raise RuntimeError(f"decode kernels flagged an out-of-range {', '.join(names)}")
