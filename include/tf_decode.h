@@ -188,9 +188,9 @@ typedef struct TfdDecodeArgs {
   int nsteps;
   int32_t* err;
   /* Optional phase timeline (may be null): for the first timeline_steps steps of
-   * a launch, block 0 records the 100 MHz device wall clock when each phase's
-   * input is ready and when its output is out, TFD_TIMELINE_STAMPS(n_layers)
-   * stamps per step. */
+   * a launch, every block records the 100 MHz device wall clock when each
+   * phase's input is ready and when its output is out: [step][block][stamp],
+   * TFD_TIMELINE_STAMPS(n_layers) stamps per step and block. */
   uint64_t* timeline;
   int timeline_steps;
 } TfdDecodeArgs;

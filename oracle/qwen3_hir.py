@@ -28,10 +28,46 @@ layouts (``ref_src/hf_alias.py:25-43``): top-level ``w_embed (V,H)``,
 """
 from __future__ import annotations
 
+from contextlib import contextmanager
 from dataclasses import dataclass
 from functools import lru_cache
 
 import torch
+
+
+class _Sums:
+    """How the oracle evaluates the HIR's f32-accumulated reductions (matmul and
+    ``reduce_sum``).  The default is torch's own kernels, as the evaluator runs
+    them.  ``exact_sums()`` switches to sums taken in f64 and rounded once to
+    the declared dtype: the same HIR semantics with a different (correctly
+    rounded) summation, used to measure how far any f32 summation order moves
+    the results -- the noise floor a correct implementation must stay within."""
+
+    exact = False
+
+    def matmul(self, a, b):
+        if self.exact:
+            return torch.matmul(a.double(), b.double()).to(a.dtype)
+        return torch.matmul(a, b)
+
+    def sum(self, x, dim, keepdim=False):
+        if self.exact:
+            return x.double().sum(dim=dim, keepdim=keepdim).to(x.dtype)
+        return x.sum(dim=dim, keepdim=keepdim)
+
+
+_ops = _Sums()
+
+
+@contextmanager
+def exact_sums():
+    """Evaluate every matmul and attention sum exactly (f64) inside the block."""
+    prev = _ops.exact
+    _ops.exact = True
+    try:
+        yield
+    finally:
+        _ops.exact = prev
 
 
 @dataclass(frozen=True)
@@ -121,9 +157,9 @@ def self_attention(dims: Qwen3Dims, hidden, gamma_in, w_q, w_k, w_v, gamma_q, ga
     hq, hkv, d, g = dims.heads, dims.kv_heads, dims.head_dim, dims.group
     ctx = k_cache.shape[1]
     hidden_norm = input_rms_norm(dims, hidden, gamma_in)
-    q = torch.matmul(hidden_norm, w_q).reshape(1, 1, hq, d)
-    k = torch.matmul(hidden_norm, w_k).reshape(1, 1, hkv, d)
-    v = torch.matmul(hidden_norm, w_v).reshape(1, 1, hkv, d)
+    q = _ops.matmul(hidden_norm, w_q).reshape(1, 1, hq, d)
+    k = _ops.matmul(hidden_norm, w_k).reshape(1, 1, hkv, d)
+    v = _ops.matmul(hidden_norm, w_v).reshape(1, 1, hkv, d)
     q_n = _head_rms(q, gamma_q, dims.eps, dt)
     q_rope = _rope(q_n, cos_cache, sin_cache, pos_ids, dt)
     k_n = _head_rms(k, gamma_k, dims.eps, dt)
@@ -136,8 +172,8 @@ def self_attention(dims: Qwen3Dims, hidden, gamma_in, w_q, w_k, w_v, gamma_q, ga
     v_new = torch.repeat_interleave(v, g, dim=2)
 
     q_e = q_s.reshape(1, 1, hq, 1, d)
-    score_ctx = (q_e * k_ctx).sum(dim=-1, keepdim=True)            # (1,1,hq,ctx,1)
-    score_new = (q_s * k_new).sum(dim=-1, keepdim=True)            # (1,1,hq,1)
+    score_ctx = _ops.sum(q_e * k_ctx, dim=-1, keepdim=True)            # (1,1,hq,ctx,1)
+    score_new = _ops.sum(q_s * k_new, dim=-1, keepdim=True)            # (1,1,hq,1)
     if ctx == 0:
         # reduce.py:124-133: an empty max is the dtype's least representable value
         ctx_max = torch.full((1, 1, hq, 1), float("-inf"), dtype=dt)
@@ -147,20 +183,20 @@ def self_attention(dims: Qwen3Dims, hidden, gamma_in, w_q, w_k, w_v, gamma_q, ga
     peak_e = peak.reshape(1, 1, hq, 1, 1)
     p_ctx = torch.exp(score_ctx - peak_e)
     p_new = torch.exp(score_new - peak)
-    total = p_ctx.sum(dim=-2) + p_new
-    weighted = (p_ctx * v_ctx).sum(dim=-2) + p_new * v_new
+    total = _ops.sum(p_ctx, dim=-2) + p_new
+    weighted = _ops.sum(p_ctx * v_ctx, dim=-2) + p_new * v_new
     attn = weighted / total
-    out = torch.matmul(attn.reshape(1, 1, hq * d), w_o)
+    out = _ops.matmul(attn.reshape(1, 1, hq * d), w_o)
     return out, k_rope, v
 
 
 def mlp(dims: Qwen3Dims, hidden, gamma_post, w_gate, w_up, w_down):
     """``mlp`` (``model.py:218-234``): fused post-attention norm + dense SwiGLU."""
     hidden_norm = input_rms_norm(dims, hidden, gamma_post)
-    gate = torch.matmul(hidden_norm, w_gate)
-    up = torch.matmul(hidden_norm, w_up)
+    gate = _ops.matmul(hidden_norm, w_gate)
+    up = _ops.matmul(hidden_norm, w_up)
     act = torch.nn.functional.silu(gate)
-    return torch.matmul(act * up, w_down)
+    return _ops.matmul(act * up, w_down)
 
 
 def decoder_layer(dims: Qwen3Dims, hidden, gamma_in, w_q, w_k, w_v, gamma_q, gamma_k,
@@ -187,7 +223,7 @@ def final_rms_norm(dims: Qwen3Dims, hidden, gamma_final):
 
 def lm_head(dims: Qwen3Dims, hidden, w_head):
     """``lm_head`` (``model.py:300-305``): logits in the model dtype."""
-    return torch.matmul(hidden.reshape(1, dims.hidden), w_head)
+    return _ops.matmul(hidden.reshape(1, dims.hidden), w_head)
 
 
 _LAYER_WEIGHTS = ("gamma_in", "w_q", "w_k", "w_v", "gamma_q", "gamma_k", "w_o",

@@ -13,6 +13,13 @@ c2_qwen3_1p7b.json  BASELINE config 2 shape (28 layers, bf16), the bench's
                     oracle's first 64 greedy tokens, their top-2 margins and each
                     step's top-8 (index, logit); for both norm-scale draws.
 c2_*_logits.npy     full bf16 logits (raw uint16) of steps 0 and 63.
+c2_*_exact_step*.npy  (target c2x) the same two steps teacher-forced on the
+                    recorded tokens, with every matmul and attention sum taken
+                    exactly (oracle.exact_sums: the HIR's rounding points, f64
+                    sums).  c2_order_noise.json records how far the oracle's own
+                    f32 sums sit from these: the noise floor of f32 summation
+                    order at this depth, which bounds what any correct
+                    implementation can be asked to match.
 
 The fixtures are data (inputs and expected outputs), regenerated from seeds.
 """
@@ -86,9 +93,52 @@ def make_c2():
     (HERE / "c2_qwen3_1p7b.json").write_text(json.dumps(out))
 
 
+def forced_logits(oracle, seq, at):
+    """Logits after consuming seq[:k + 1] for each k in *at* (one pass over seq)."""
+    input_ids = torch.tensor(seq, dtype=torch.int64)
+    caches = oracle.init_caches()
+    out = {}
+    with torch.no_grad():
+        for step in range(max(at) + 1):
+            args = oracle.prepare_inputs_for_generation(input_ids, step, caches)
+            logits, fresh = oracle.forward(*args)
+            caches = oracle.append_cache(caches, fresh)
+            if step in at:
+                out[step] = logits.float().reshape(-1).clone()
+    return out
+
+
+def make_c2x():
+    fx = json.loads((HERE / "c2_qwen3_1p7b.json").read_text())
+    prompt = fx["prompt"]
+    pl = len(prompt)
+    noise = {}
+    for norms in ("random", "ones"):
+        t0 = time.time()
+        w = synthetic_weights(QWEN3_1_7B, seed=0, norms=norms)
+        seq = prompt + fx[norms]["tokens"][:63]
+        with O.exact_sums():
+            ex = forced_logits(O.Qwen3Oracle(O.C2, w), seq, {pl - 1, pl - 1 + 63})
+        noise[norms] = {}
+        for k in (0, 63):
+            lg = ex[pl - 1 + k]
+            raw = lg.to(torch.bfloat16).view(torch.int16).numpy().astype(np.uint16)
+            np.save(HERE / f"c2_{norms}_exact_step{k}.npy", raw)
+            ref = np.load(HERE / f"c2_{norms}_logits_step{k}.npy").astype(np.int16)
+            orc = torch.from_numpy(ref).view(torch.bfloat16).float()
+            d = (orc - lg).abs()
+            noise[norms][f"step{k}"] = {"max_abs": float(d.max()), "mean_abs": float(d.mean()),
+                                       "max_logit": float(orc.abs().max())}
+        print(f"c2x {norms}: {time.time() - t0:.0f}s {noise[norms]}", flush=True)
+        del w
+    (HERE / "c2_order_noise.json").write_text(json.dumps(noise, indent=1))
+
+
 if __name__ == "__main__":
-    which = sys.argv[1:] or ["c1", "c2"]
+    which = sys.argv[1:] or ["c1", "c2", "c2x"]
     if "c1" in which:
         make_c1()
     if "c2" in which:
         make_c2()
+    if "c2x" in which:
+        make_c2x()

@@ -357,13 +357,35 @@ __device__ __forceinline__ uint32_t ll_get(const uint32_t* base, uint32_t word, 
 }
 
 // Stage a flag-in-data bf16 vector of n values (n % 4 == 0) into LDS as plain
-// bf16 pairs; the caller synchronises the block before reading it.
+// bf16 pairs; the caller synchronises the block before reading it.  Each
+// thread issues all its loads of a batch before checking any, so a long vector
+// costs one round trip rather than one per load.
 __device__ __forceinline__ void ll_stage(const uint32_t* ll, int n, uint32_t tag,
                                          uint32_t* __restrict__ lds, int* err) {
-  for (int i = threadIdx.x; i < n / 4; i += kBlock) {
-    const u32x2 p = ll_get2(ll, 2u * i, tag, err);
-    lds[2 * i] = p.x;
-    lds[2 * i + 1] = p.y;
+  constexpr int kBatch = 8;
+  const int npairs = n / 4;
+  for (int i0 = threadIdx.x; i0 < npairs; i0 += kBlock * kBatch) {
+    u32x4 v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int i = i0 + k * kBlock;
+      v[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(ll), (uint32_t)(i < npairs ? i : 0) * 16u,
+                                                   0, kCoherent);
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int i = i0 + k * kBlock;
+      if (i < npairs) {
+        uint32_t spins = 0;
+        while (v[k].y != tag || v[k].w != tag) {
+          if (ll_give_up(spins, err)) break;
+          __asm__ volatile("" ::: "memory");
+          v[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(ll), (uint32_t)i * 16u, 0, kCoherent);
+        }
+        lds[2 * i] = v[k].x;
+        lds[2 * i + 1] = v[k].z;
+      }
+    }
   }
 }
 

@@ -47,6 +47,78 @@ __device__ __forceinline__ void gemv_issue(int vb, const bf16* __restrict__ W, i
   load_rows<kCmax, kR>(W, K, K / 8, row0, nvalid, lane, w);
 }
 
+// Rows [kLo, kHi) of gemv_issue's tile only, so a caller can spread one
+// tile's loads over several points of its schedule.
+template <int kCmax, int kR, int kLo, int kHi>
+__device__ __forceinline__ void gemv_issue_part(int vb, const bf16* __restrict__ W, int K, int N,
+                                                u32x4 (&w)[kR][kCmax]) {
+  static_assert(0 <= kLo && kLo < kHi && kHi <= kR, "row range");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t row0 = ((int64_t)vb * kWavesPerBlock + wave) * kR;
+  const int nch = K / 8;
+  const int nvalid = row0 >= N ? 0 : (int)((N - row0) < kR ? (N - row0) : kR);
+#pragma unroll
+  for (int r = kLo; r < kHi; ++r) {
+    if (nvalid == 0) {
+#pragma unroll
+      for (int i = 0; i < kCmax; ++i) w[r][i] = u32x4{0u, 0u, 0u, 0u};
+    } else {
+      const bf16* rowp = W + (row0 + (r < nvalid ? r : nvalid - 1)) * (int64_t)K;
+#pragma unroll
+      for (int i = 0; i < kCmax; ++i) {
+        const int c = i * kWave + lane;
+        w[r][i] = load16_stream(rowp + (int64_t)(c < nch ? c : nch - 1) * 8);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Rows [kLo, kHi) of gemv_issue's tile straight into LDS (no registers):
+// row r, chunk i of this wave lands at lds[((wave * kRl + r - kLo0) * kCmax + i) * 256
+// + 4 * lane] (u32 words), kRl rows per wave, kLo0 the first LDS-held row.
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+typedef __attribute__((address_space(1))) void* global_void_ptr;
+
+template <int kCmax, int kR, int kRl, int kLo, int kHi>
+__device__ __forceinline__ void gemv_issue_lds(int vb, const bf16* __restrict__ W, int K, int N,
+                                               uint32_t* lds) {
+  static_assert(0 <= kLo && kLo < kHi && kHi <= kRl && kRl <= kR, "row range");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t row0 = ((int64_t)vb * kWavesPerBlock + wave) * kR;
+  const int nch = K / 8;
+  // rows past the end re-read the last valid row (never stored); a tile
+  // wholly past the end reads row 0 (never used)
+  const int nvalid = row0 >= N ? 1 : (int)((N - row0) < kR ? (N - row0) : kR);
+  const int64_t base = row0 >= N ? 0 : row0;
+#pragma unroll
+  for (int r = kLo; r < kHi; ++r) {
+    const bf16* rowp = W + (base + (r < nvalid ? r : nvalid - 1)) * (int64_t)K;
+#pragma unroll
+    for (int i = 0; i < kCmax; ++i) {
+      const int c = i * kWave + lane;
+      __builtin_amdgcn_global_load_lds(
+          (global_void_ptr)(rowp + (int64_t)(c < nch ? c : nch - 1) * 8),
+          (lds_void_ptr)(lds + ((wave * kRl + r) * kCmax + i) * 256), 16, 0, 0);
+    }
+  }
+}
+
+// Copy the LDS-held rows [0, kRl) of this wave's tile into registers.
+template <int kCmax, int kR, int kRl>
+__device__ __forceinline__ void gemv_tile_from_lds(const uint32_t* lds, u32x4 (&w)[kR][kCmax]) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int r = 0; r < kRl; ++r)
+#pragma unroll
+    for (int i = 0; i < kCmax; ++i)
+      w[r][i] = *reinterpret_cast<const u32x4*>(lds + ((wave * kRl + r) * kCmax + i) * 256 +
+                                                4 * lane);
+}
+
 template <int kCmax, int kR, int kPro, int kEpi>
 __device__ __forceinline__ void gemv_finish(int vb, const bf16* __restrict__ x,
                                             const bf16* __restrict__ gamma,
@@ -795,14 +867,21 @@ __device__ __forceinline__ bf16 attn_merge_one(float sp, float sv, float sn, flo
 // through LDS with coalesced loads and summing in split order.  The persistent
 // kernel publishes the partials as flag-in-data words and merges in part 3.
 // ---------------------------------------------------------------------------
-template <int D, int G, bool kLL>
+struct NoHook {
+  __device__ void operator()() const {}
+};
+
+// `polled` runs once this block's waits of the phase are over (the persistent
+// kernel issues weight loads there: memory counters retire in order, so loads
+// issued before a wait would hold it up)
+template <int D, int G, bool kLL, class Hook = NoHook>
 __device__ __forceinline__ void attn_pv_phase(
     int split, int h, int nsplit, const bf16* __restrict__ qkv, int P,
     const int* __restrict__ page_table, int max_pages, const bf16* __restrict__ vpool,
     int num_pages, int kv_heads, const float* __restrict__ S, int s_stride,
     const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
     float* part_out, int* counters, bf16* __restrict__ attn_out, const AttnLL& ll,
-    const VTile<D>& vt, int* err) {
+    const VTile<D>& vt, int* err, const Hook& polled = Hook()) {
   using A = AttnShape<D>;
   constexpr int kLpp = A::kLpp;
   constexpr int kGroups = A::kGroups;
@@ -843,6 +922,7 @@ __device__ __forceinline__ void attn_pv_phase(
     }
     if (s < nact) mx = fmaxf(mx, m);
   }
+  polled();
   const float sj = (j0 + lane < jend) ? sj_raw : kNegInf;
 
   __shared__ float M[G];
@@ -979,10 +1059,10 @@ __device__ __forceinline__ void attn_pv_phase(
 // split's partials for that slice and the numerator sums, in split order --
 // the same arithmetic as the last-block merge above.
 // ---------------------------------------------------------------------------
-template <int D, int G>
+template <int D, int G, class Hook = NoHook>
 __device__ __forceinline__ void attn_merge_ll(int split, int h, int P, int max_pages,
                                               int kv_heads, const float* snew, const AttnLL& ll,
-                                              int* err) {
+                                              int* err, const Hook& polled = Hook()) {
   constexpr int kPairs = G * D / 2;
   constexpr int kChunk = 16;                          // splits staged at a time
   const int heads = kv_heads * G;
@@ -1017,6 +1097,7 @@ __device__ __forceinline__ void attn_merge_ll(int split, int h, int P, int max_p
                          ll.tag, err);
     }
     __syncthreads();
+    if (c0 == 0) polled();
     if (tid < nq) {
       for (int s = 0; s < nc; ++s) {
         sv0 += __uint_as_float(po[s][tid].x);

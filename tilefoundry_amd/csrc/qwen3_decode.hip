@@ -215,7 +215,7 @@ __device__ __forceinline__ void lm_head_ll(const u32x4 (&xr)[kCmax], const bf16*
 }
 
 __device__ __forceinline__ void stamp(uint64_t*& tl) {
-  if (tl && blockIdx.x == 0 && threadIdx.x == 0) *tl++ = wall_clock64();
+  if (tl && threadIdx.x == 0) *tl++ = wall_clock64();
 }
 
 // ---------------------------------------------------------------------------
@@ -264,14 +264,13 @@ __global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, i
 
   const int lane = threadIdx.x & (kWave - 1);
   u32x4 wq[kRqkv][kCH], wo[kRo][kCH], wg[kRgu][kCH], wd[kRdown][kCI];
-  u32x4 gq_in[kCH], gq_post[kCH], none[kCI];
-#pragma unroll
-  for (int i = 0; i < kCI; ++i) none[i] = u32x4{0u, 0u, 0u, 0u};
+  u32x4 gq_in[kCH], gq_post[kCH];   // norm scales, prefetched with the weights
   gemv_issue<kCH, kRqkv>(vb0, (const bf16*)a.layers[0].w_qkv, H, qkv_n, wq);
   load_x<kCH>((const bf16*)a.layers[0].gamma_in, H / 8, lane, gq_in);
   for (int t = 0; t < steps; ++t, ++P) {
     uint64_t* tl = (a.timeline && t < a.timeline_steps)
-                       ? a.timeline + (int64_t)t * (14 * a.n_layers + 4) : nullptr;
+                       ? a.timeline + ((int64_t)t * nb + blockIdx.x) * (14 * a.n_layers + 4)
+                       : nullptr;
     const uint32_t tag0 = a.epoch + (uint32_t)t * (uint32_t)(a.n_layers + 1);
     // this step's input: the embedding row of the current token
     {
@@ -281,8 +280,10 @@ __global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, i
       for (int i = threadIdx.x; i < H / 8; i += kBlock)
         *reinterpret_cast<u32x4*>(hid_s + 4 * i) = *reinterpret_cast<const u32x4*>(row + 4 * i);
     }
-    // attention shape at this position
-    const int nact = (P + kSplit - 1) / kSplit;
+    // attention shape at this position (an out-of-range position has raised
+    // its error in part 1; the shape then stays that of position 0)
+    const int Pc = (P >= 0 && P < a.max_pages * kPage) ? P : 0;
+    const int nact = (Pc + kSplit - 1) / kSplit;
     const int parts = nact > 0 ? nact : 1;
     const int nvb = parts * a.kv_heads;
     for (int l = 0; l < a.n_layers; ++l) {
@@ -354,8 +355,9 @@ __global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, i
       ll_stage(a.x_attn, QD, tag, xs, err);
       __syncthreads();
       stamp(tl);
-      gemv_ll<kCH, kRo, kPlain, kResid>(xs, (const u32x4(&)[kCH])none, (const bf16*)w.w_o, hid_s,
-                                        a.x_h1, tag, QD, H, eps, wo);
+      // (a plain prologue takes no norm scales: any array of the right shape will do)
+      gemv_ll<kCH, kRo, kPlain, kResid>(xs, gq_post, (const bf16*)w.w_o, hid_s, a.x_h1, tag, QD,
+                                        H, eps, wo);
       stamp(tl);
       gemv_issue<kCH, kRgu>(vb0, (const bf16*)w.w_gu, H, 2 * I, wg);
       load_x<kCH>((const bf16*)w.gamma_post, H / 8, lane, gq_post);
@@ -371,7 +373,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, i
       ll_stage(a.x_mid, I, tag, xs, err);
       __syncthreads();
       stamp(tl);
-      gemv_ll<kCI, kRdown, kPlain, kResid>(xs, none, (const bf16*)w.w_down, h1_s, a.x_hid, tag,
+      gemv_ll<kCI, kRdown, kPlain, kResid>(xs, wd[0], (const bf16*)w.w_down, h1_s, a.x_hid, tag,
                                            I, H, eps, wd);
       stamp(tl);
       // the next layer's qkv weights -- or, after the last layer, layer 0's for

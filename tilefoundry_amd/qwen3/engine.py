@@ -266,15 +266,15 @@ class Engine:
         self.epoch += tags
 
     def phase_timeline(self, prompt_ids: list[int], steps: int) -> torch.Tensor:
-        """Block 0's view of *steps* persistent steps after walking *prompt_ids*:
-        ``[steps, 7 * layers + 2, 2]`` microseconds -- per layer the qkv, attention
-        scores, P.V and merge, o, gate/up and down phases, then the head and the
-        pick; for each, the wait for its input (from the previous phase's end) and
-        its own run time."""
+        """Device clock stamps of *steps* persistent steps after walking
+        *prompt_ids*: ``[steps, blocks, 7 * layers + 2, 2]`` microseconds since
+        block 0 began the first step -- per layer the qkv, attention scores, P.V
+        and merge, o, gate/up and down phases, then the head and the pick; for
+        each, when the block had its input and when its output was out."""
         if self.mode != "persistent":
             raise ValueError("the phase timeline belongs to the persistent kernel")
         n = _lib.timeline_stamps(self.L)
-        buf = torch.zeros(steps * n, device=self.device, dtype=torch.int64)
+        buf = torch.zeros(steps * self.grid * n, device=self.device, dtype=torch.int64)
         self._load_prompt(prompt_ids)
         self.run_steps(len(prompt_ids) - 1)
         torch.cuda.synchronize(self.device)
@@ -284,10 +284,9 @@ class Engine:
             torch.cuda.synchronize(self.device)
         finally:
             self.args.timeline, self.args.timeline_steps = None, 0
-        stamps = buf.view(steps, n).double().cpu() * 0.01      # 100 MHz clock -> us
-        ready, done = stamps[:, 0::2], stamps[:, 1::2]
-        prev = torch.cat([ready[:, :1], done[:, :-1]], dim=1)
-        return torch.stack([ready - prev, done - ready], dim=-1)
+        st = buf.view(steps, self.grid, n).double().cpu()
+        st = (st - st[0, 0, 0]) * 0.01                          # 100 MHz clock -> us
+        return st.view(steps, self.grid, n // 2, 2)
 
     def run_steps(self, n: int):
         """*n* decode steps: one persistent launch, or n replays / direct steps."""
