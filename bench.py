@@ -1,18 +1,26 @@
 """Decode throughput of the Qwen3-1.7B-architecture model at batch 1.
 
-    python bench.py [--gpus 1] [--steps 2048] [--warmup 64]
+    python bench.py [--gpus 1] [--steps 2048] [--warmup 64] [--mode persistent|graph]
 
-A step is one decode token: one replay of the captured step (28 layers, the
-head, the greedy pick).  The workload is BASELINE's config 2: bf16 weights drawn
-N(0, 0.02) from seed 0 (every parameter, norm scales included), tied
-embeddings, a 32-token uniform-random prompt (seed 0), a 16-token-page KV cache,
-and `--steps` greedy new tokens (2048 by default) timed after the prompt walk.
-Weights are resident in HBM before the timed region starts.
+A step is one decode token: every layer, the head, the greedy pick.  The
+workload is BASELINE's config 2: bf16 weights drawn N(0, 0.02) from seed 0
+(every parameter, norm scales included), tied embeddings, a 32-token
+uniform-random prompt (seed 0), a 16-token-page KV cache, and `--steps` greedy
+new tokens (2048 by default) timed after the prompt walk.  Weights are resident
+in HBM before the timed region starts.
 
-Prints one JSON line: the metric, the whole-step HBM roofline fraction from
-algorithmic bytes (weights once + the KV each step touches), the dominant
-kernel's roofline (the gate/up projection, timed on its own over all 28 layers'
-weights with HIP events on its stream), and the CPU oracle timed on the host.
+Modes: "persistent" (default) runs all the steps in one launch of the
+persistent decode kernel; "graph" replays a captured graph of per-phase
+launches once per token.
+
+Prints one JSON line: the metric; the whole-step HBM roofline fraction from
+algorithmic bytes (weights once + the KV each step touches); the dominant
+kernel's roofline -- in persistent mode the persistent kernel itself: the
+algorithmic bytes of its launches over their mean duration, HIP events on the
+launch stream around every launch this run makes (the ones rocprofv3 sees for
+the same command); in graph mode the gate/up GEMV -- with the HBM traffic that
+rocprofv3's counters measured for it when a profile is committed; and the CPU
+oracle timed on the host.
 """
 from __future__ import annotations
 
@@ -73,6 +81,75 @@ def time_gate_up(eng, rounds: int) -> float:
     return start.elapsed_time(end) / 1e3 / (rounds * eng.L)
 
 
+class LaunchClock:
+    """HIP events on the launch stream around every persistent launch of *eng*,
+    with the algorithmic bytes of each (weights once per step + the KV every
+    step reads and writes at its position)."""
+
+    def __init__(self, eng):
+        import torch
+
+        self.eng, self.torch = eng, torch
+        self.records = []          # (start event, end event, bytes)
+        self.pos = 0
+        launch, load = eng._launch_persistent, eng._load_prompt
+
+        def timed_launch(n):
+            w = eng.weight_bytes_per_step()
+            nbytes = sum(w + eng.kv_bytes_at(p) for p in range(self.pos, self.pos + n))
+            stream = torch.cuda.current_stream(eng.device)
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            launch(n)
+            b.record(stream)
+            self.records.append((a, b, nbytes))
+            self.pos += n
+
+        def timed_load(prompt_ids):
+            self.pos = 0
+            load(prompt_ids)
+
+        eng._launch_persistent = timed_launch
+        eng._load_prompt = timed_load
+
+    def summary(self):
+        self.torch.cuda.synchronize(self.eng.device)
+        secs = [a.elapsed_time(b) / 1e3 for a, b, _ in self.records]
+        nbytes = [n for _, _, n in self.records]
+        k = len(secs)
+        return k, sum(nbytes) / k, sum(secs) / k
+
+
+def traffic_ratio(kernel: str):
+    """HBM bytes moved per algorithmic byte for *kernel*, from the committed
+    rocprofv3 counter summary (profiles/hbm_traffic.json: FETCH_SIZE and
+    WRITE_SIZE of one profiled launch, scaled by what the same counters read for
+    a plain copy of known size), or None when no profile is committed."""
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    if not path.exists():
+        return None
+    try:
+        entry = json.loads(path.read_text()).get(kernel)
+        return float(entry["hbm_bytes"]) / float(entry["algorithmic_bytes"])
+    except (ValueError, KeyError, TypeError, ZeroDivisionError, AttributeError):
+        return None
+
+
+def copy_probe(nbytes: int = 1 << 30) -> int:
+    """A plain device copy of *nbytes* (three launches): the calibration kernel
+    for the FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": nbytes, "launches": 3}), flush=True)
+    return 0
+
+
 def cpu_baseline(weights, prompt, budget_s: float) -> dict:
     """The CPU oracle (a restatement of the authored HIR run the way the
     reference evaluator runs it) on this host's cores: decode steps over the
@@ -112,10 +189,14 @@ def main(argv=None) -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0,
                     help="seconds of CPU-oracle work for the cpu_baseline leg (0 skips it)")
     ap.add_argument("--kernel-rounds", type=int, default=20)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a 1 GiB device copy (counter calibration) and exit")
     ap.add_argument("--mode", default="persistent", choices=("persistent", "graph"),
                     help="persistent: one cooperative launch per run of steps; graph: a "
                          "captured graph of per-phase launches replayed per token")
     args = ap.parse_args(argv)
+    if args.copy_probe:
+        return copy_probe()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box here "
               "has one MI355X); run with --gpus 1", file=sys.stderr)
@@ -134,6 +215,7 @@ def main(argv=None) -> int:
     max_new = max(args.steps, 2048)
     eng = Engine(cfg, weights, device="cuda:0", max_new=max_new, prompt_room=len(prompt),
                  mode=args.mode)
+    clock = LaunchClock(eng) if args.mode == "persistent" else None
     print(f"[bench] weights + engine + capture {time.perf_counter() - t0:.1f}s", file=sys.stderr,
           flush=True)
 
@@ -159,10 +241,26 @@ def main(argv=None) -> int:
     tok_s = args.steps / seconds
     step_bw = step_bytes * tok_s
 
-    gu_s = time_gate_up(eng, args.kernel_rounds)
-    gu_bytes = 2 * cfg.intermediate_size * cfg.hidden_size * 2 + 2 * cfg.hidden_size * 2 \
-        + cfg.intermediate_size * 2
-    gu_bw = gu_bytes / gu_s
+    if clock is not None:
+        launches, bytes_per_launch, launch_s = clock.summary()
+        kernel = "k_decode_persistent<4,12,128,2>"
+        ratio = traffic_ratio(kernel)
+        bw = bytes_per_launch / launch_s
+        roofline = {"bound": "hbm", "kernel": f"{kernel} (whole decode steps per launch)",
+                    "achieved": round(bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                    "frac": round(bw / HBM_PEAK, 4),
+                    "traffic": None if ratio is None else round(ratio * bytes_per_launch),
+                    "bytes_per_launch": int(bytes_per_launch),
+                    "avg_launch_ms": round(launch_s * 1e3, 3), "launches": launches}
+    else:
+        gu_s = time_gate_up(eng, args.kernel_rounds)
+        gu_bytes = 2 * cfg.intermediate_size * cfg.hidden_size * 2 + 2 * cfg.hidden_size * 2 \
+            + cfg.intermediate_size * 2
+        gu_bw = gu_bytes / gu_s
+        roofline = {"bound": "hbm", "kernel": "k_gemv<4,4,norm,swiglu> (gate/up, 12288x2048)",
+                    "achieved": round(gu_bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                    "frac": round(gu_bw / HBM_PEAK, 4), "traffic": None,
+                    "bytes_per_launch": gu_bytes, "avg_us": round(gu_s * 1e6, 3)}
 
     line = {
         "metric": METRIC,
@@ -187,10 +285,7 @@ def main(argv=None) -> int:
                           "achieved": round(step_bw / 1e9, 1), "peak": HBM_PEAK / 1e9,
                           "unit": "GB/s", "frac": round(step_bw / HBM_PEAK, 4),
                           "roofline_tok_s": round(HBM_PEAK / step_bytes, 1)},
-        "roofline": {"bound": "hbm", "kernel": "k_gemv<4,4,norm,swiglu> (gate/up, 12288x2048)",
-                     "achieved": round(gu_bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                     "frac": round(gu_bw / HBM_PEAK, 4), "traffic": None,
-                     "bytes_per_launch": gu_bytes, "avg_us": round(gu_s * 1e6, 3)},
+        "roofline": roofline,
         "first_tokens": tokens[:8],
     }
     if args.cpu_budget > 0:

@@ -10,6 +10,15 @@ of about one bf16 ulp, and even with unit norm scales ("ones") three of the 64
 steps are exact bf16 ties; there f32 summation order decides the pick, so a
 step may differ only where the recorded margin is within the measured logit
 error.
+
+Logits at steps 0 and 63 are held against the exact-sum evaluation of the same
+HIR (c2_*_exact_step*.npy: every matmul and attention sum in f64, rounded where
+the HIR rounds).  The oracle's own f32 sums sit `noise` away from it
+(c2_order_noise.json); at 28 layers with unit norm scales that is 2.5% of the
+largest logit, above the 2e-2 bar, because every layer's bf16 roundings
+amplify one-ulp flips.  So the bound is max(2e-2 * max|logit|, 2 * noise): the
+engine must be as close to the exact result as the torch evaluator is, within a
+factor of two, and never worse than the bar where the noise is below it.
 """
 import json
 from pathlib import Path
@@ -33,6 +42,11 @@ def _golden_logits(norms, k):
     return torch.from_numpy(raw.astype(np.int16)).view(torch.bfloat16).float()
 
 
+def _bf16_npy(name):
+    raw = np.load(GOLDEN / name)
+    return torch.from_numpy(raw.astype(np.int16)).view(torch.bfloat16).float()
+
+
 def _top8_error(logits, top8):
     return max(abs(float(logits[i]) - v) for i, v in top8)
 
@@ -51,11 +65,15 @@ def test_c2_full_depth_against_golden(gpu_device, norms):
         # full logits of steps 0 and 63 (teacher-forced on the golden tokens)
         for k in (0, STEPS - 1):
             ref = _golden_logits(norms, k)
+            exact = _bf16_npy(f"c2_{norms}_exact_step{k}.npy")
+            noise = float((ref - exact).abs().max())
             got = eng.logits_for(prompt + gold["tokens"][:k]).float().cpu()
-            err = float((got - ref).abs().max())
-            bound = TOL * float(ref.abs().max())
-            print(f"  step {k}: max|dlogit| {err:.4g} (bound {bound:.4g})", flush=True)
-            assert err <= bound, (mode, k, err, bound)
+            err_exact = float((got - exact).abs().max())
+            err_oracle = float((got - ref).abs().max())
+            bound = max(TOL * float(exact.abs().max()), 2 * noise)
+            print(f"  step {k}: max|engine-exact| {err_exact:.4g}, max|oracle-exact| {noise:.4g}, "
+                  f"max|engine-oracle| {err_oracle:.4g}; bound {bound:.4g}", flush=True)
+            assert err_exact <= bound, (mode, k, err_exact, bound)
 
         # teacher-forced: every step's pick, and its top-8 logits
         seq = prompt + gold["tokens"][:STEPS - 1]

@@ -40,3 +40,26 @@ def test_c2_fixture_is_self_consistent():
             best = max(v for _, v in top)
             first = min(i for i, v in top if v == best)
             assert tok == first
+
+
+def test_c2_order_noise_fixture():
+    """The exact-sum fixtures agree with the oracle's own logits to within the
+    recorded noise, and the noise is what summation order alone can produce:
+    small against the logits, nonzero, and the same picks."""
+    import numpy as np
+
+    noise = json.loads((GOLDEN / "c2_order_noise.json").read_text())
+    fx = json.loads((GOLDEN / "c2_qwen3_1p7b.json").read_text())
+    for norms in ("random", "ones"):
+        for k in (0, 63):
+            def load(name):
+                raw = np.load(GOLDEN / name).astype(np.int16)
+                return torch.from_numpy(raw).view(torch.bfloat16).float()
+            orc = load(f"c2_{norms}_logits_step{k}.npy")
+            ex = load(f"c2_{norms}_exact_step{k}.npy")
+            d = float((orc - ex).abs().max())
+            assert d == noise[norms][f"step{k}"]["max_abs"]
+            assert 0 < d <= 0.05 * float(orc.abs().max())
+            # the exact evaluation picks the same token unless the step is a near-tie
+            assert int(torch.argmax(ex)) == fx[norms]["tokens"][k] or \
+                fx[norms]["margins"][k] <= 2 * d

@@ -23,6 +23,7 @@
 #include "tf_decode.h"
 
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -695,7 +696,18 @@ int tfd_decode_persistent(const TfdDecodeArgs* args, int steps, int nblocks, voi
   TfdDecodeArgs karg = a;
   int ksteps = steps;
   void* kargs[] = {&karg, &ksteps};
-  e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kBlock), kargs, 0, (hipStream_t)stream);
+  // The grid fits the device at once (checked above), which is all the kernel
+  // needs; the cooperative launch makes the runtime guarantee it.
+  // TFD_PLAIN_LAUNCH=1 uses an ordinary launch instead, for profilers that do
+  // not handle cooperative launches.
+  static const bool plain = [] {
+    const char* v = getenv("TFD_PLAIN_LAUNCH");
+    return v && v[0] == '1';
+  }();
+  if (plain)
+    e = hipLaunchKernel(fn, dim3(grid), dim3(kBlock), kargs, 0, (hipStream_t)stream);
+  else
+    e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kBlock), kargs, 0, (hipStream_t)stream);
   if (e != hipSuccess) return fail((int)e, "decode_persistent: launch failed: %s",
                                    hipGetErrorString(e));
   return launched("decode_persistent");
