@@ -59,6 +59,24 @@ constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within 8
 constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within 16
 
+// Across the two 16-lane rows of each 32-lane half, and across the two halves:
+// gfx950's lane-swap instructions (v_permlane16_swap / v_permlane32_swap) hand
+// every lane both values of its pair in registers, no LDS round trip.  With
+// both operands the same vector, result [0] holds the pair's lower member and
+// [1] the upper one in every lane.
+__device__ __forceinline__ void pair16(float v, float& lo, float& hi) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void pair32(float v, float& lo, float& hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+
 // Sum within aligned groups of `width` lanes (width a power of two <= 64).
 template <int kWidth>
 __device__ __forceinline__ float group_sum(float v) {
@@ -67,7 +85,11 @@ __device__ __forceinline__ float group_sum(float v) {
   if (kWidth >= 8) v += dpp_f<kDppHalfMirror>(v);
   if (kWidth >= 16) v += dpp_f<kDppMirror>(v);
   if (kWidth >= 32) v += __shfl_xor(v, 16, kWave);
-  if (kWidth >= 64) v += __shfl_xor(v, 32, kWave);
+  if (kWidth >= 64) {
+    float lo, hi;
+    pair32(v, lo, hi);
+    v = lo + hi;
+  }
   return v;
 }
 
@@ -79,8 +101,9 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
   v = fmaxf(v, dpp_f<kDppMirror>(v));
   v = fmaxf(v, __shfl_xor(v, 16, kWave));
-  v = fmaxf(v, __shfl_xor(v, 32, kWave));
-  return v;
+  float lo, hi;
+  pair32(v, lo, hi);
+  return fmaxf(lo, hi);
 }
 
 __device__ __forceinline__ u32x4 load16(const bf16* p) {
