@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TFD_ABI_VERSION 4
+#define TFD_ABI_VERSION 5
 
 /* gemv prologues / epilogues */
 #define TFD_PRO_PLAIN 0  /* x used as given */
@@ -37,6 +37,7 @@ extern "C" {
 #define TFD_EPI_STORE 0  /* out[n] = bf16(W[n].x) */
 #define TFD_EPI_RESID 1  /* out[n] = bf16(resid[n] + bf16(W[n].x)) */
 #define TFD_EPI_SWIGLU 2 /* rows are (gate_i, up_i) pairs: out[i] = bf16(bf16(silu(g)) * u) */
+#define TFD_EPI_LOGITS 3 /* skinny GEMM only: out (f32) = bf16-valued W[n].x (the HIR's bf16 logits) */
 
 /* device error bits */
 #define TFD_ERR_TOKEN_RANGE 1
@@ -125,6 +126,62 @@ int tfd_attn_pv_combine_paged(const void* qkv, const int32_t* cache_len,
                               const float* score_new, float* part_sum, float* part_out,
                               int nsplit, int32_t* counters, void* attn_out, int32_t* err,
                               void* stream);
+
+/* ---- batched decode (up to 32 sequences per step) -------
+ * Activations are row-major [rows][n] with leading dimensions; each sequence has
+ * its own position (pos[b]) and page-table row (page_table + b * max_pages). */
+
+/* Row-wise Qwen3 RMSNorm of `rows` vectors of n values (input_rms_norm per
+ * sequence, ref_src/model.py:125-137).  n % 8 == 0, n <= 8192. */
+int tfd_rmsnorm_rows_bf16(const void* x, int ldx, const void* gamma, void* out, int ldo,
+                          int rows, int n, float eps, void* stream);
+
+/* Skinny GEMM on the matrix cores: Y[m][n] = sum_k X[m][k] W[n][k] for m < M <= 32
+ * (the q/k/v, o, gate/up, down and head projections of a batch, ref_src/model.py:160-171,
+ * 213-215, 230-234, 300-305, at M = batch; SURVEY's gemm_bf16_skinny entry, which
+ * replaces fast/kernels.py:123-145 / 260-321 at batch > 1).  f32 accumulation,
+ * one rounding per output; epilogue TFD_EPI_STORE / RESID (resid [M][ldr]) / SWIGLU
+ * (out [M][N/2]) / LOGITS (out f32).  K % 32 == 0. */
+int tfd_gemm_skinny_bf16(const void* x, int ldx, const void* w, int M, int K, int N,
+                         int epilogue, const void* resid, int ldr, void* out, int ldo,
+                         void* stream);
+
+/* tfd_attn_rope_scores_paged for `batch` sequences at once (grid nsplit x kv_heads x
+ * batch): sequence b reads QKV row b (stride ldq) at its own position pos[b] and
+ * page-table row b; its workspaces are the single-sequence ones at b * (their size).
+ * Replaces fast/kernels.py:385-501 at batch > 1 (flash-decode over the paged cache). */
+int tfd_attn_rope_scores_paged_batched(
+    const void* qkv, int ldq, const void* gamma_q, const void* gamma_k, const void* cos_table,
+    const void* sin_table, int rope_rows, const int32_t* pos, const int32_t* page_table,
+    int max_pages, void* k_pool, void* v_pool, int num_pages, int batch, int heads, int kv_heads,
+    int head_dim, float scale, float eps, float* scores, int score_stride, float* split_max,
+    float* score_new, int nsplit, int32_t* err, void* stream);
+
+/* tfd_attn_pv_combine_paged for `batch` sequences (counters: batch x kv_heads, zero;
+ * output row b at attn_out + b * lda). */
+int tfd_attn_pv_combine_paged_batched(
+    const void* qkv, int ldq, const int32_t* pos, const int32_t* page_table, int max_pages,
+    const void* v_pool, int num_pages, int batch, int heads, int kv_heads, int head_dim,
+    const float* scores, int score_stride, const float* split_max, const float* score_new,
+    float* part_sum, float* part_out, int nsplit, int32_t* counters, void* attn_out, int lda,
+    int32_t* err, void* stream);
+
+/* Greedy pick per row: the first maximal logit (ref_src/generation.py:24-26). */
+int tfd_argmax_rows(const float* logits, int ldl, int rows, int vocab, int32_t* pick,
+                    void* stream);
+
+/* The step's last node per sequence (the batch form of tfd_argmax_finalize,
+ * fast/kernels.py:591-637): record pick[b] at sam[b][pos[b]], feed the next prompt
+ * token while sequence b's prompt lasts and the pick after, advance pos[b], stage the
+ * next token's embedding row in hid row b. */
+int tfd_finalize_rows(const int32_t* pick, int rows, const int32_t* inp, int ld_inp,
+                      const int32_t* prompt_len, int64_t* ids, int32_t* pos, int32_t* sam,
+                      int ld_sam, int nsteps, const void* table, void* hid, int ldh, int hidden,
+                      int vocab, int32_t* err, void* stream);
+
+/* Embedding rows of ids[0..rows) (Qwen3_1_7B.embed per sequence, ref_src/model.py:279-287). */
+int tfd_embed_rows_bf16(const void* table, const int64_t* ids, void* out, int ldo, int rows,
+                        int hidden, int vocab, int32_t* err, void* stream);
 
 /* ---- persistent decode step ------------------------------------------------
  * One cooperative launch runs `steps` whole decode steps (every layer, the head,

@@ -20,6 +20,7 @@
 // and the tied head reads the embedding table in place.
 
 #include "decode_phases.h"
+#include "host_common.h"
 #include "tf_decode.h"
 
 #include <stdarg.h>
@@ -28,6 +29,7 @@
 #include <string.h>
 
 using namespace tfd;
+using namespace tfd_host;
 
 namespace {
 
@@ -413,9 +415,22 @@ __global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, i
 // ---------------------------------------------------------------------------
 // host side: argument checks, error text, launches
 // ---------------------------------------------------------------------------
+template <int kC, int kR, int kPro, int kEpi>
+void launch_gemv(const bf16* x, const bf16* gamma, const bf16* W, const bf16* resid, bf16* out,
+                 int K, int N, float eps, hipStream_t s) {
+  const int rows_per_block = kWavesPerBlock * kR;
+  const int grid = (N + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL((k_gemv<kC, kR, kPro, kEpi>), dim3(grid), dim3(kBlock), 0, s, x, gamma, W,
+                     resid, out, K, N, eps);
+}
+
+}  // namespace
+
+
+namespace tfd_host {
+
 thread_local char g_err[512] = "";
 
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -430,9 +445,6 @@ int launched(const char* what) {
   return 0;
 }
 
-// error codes returned by the entries (negative; positive values are hipError_t)
-enum : int { kBadArg = -1, kBadShape = -2, kUnsupported = -3 };
-
 int cmax_for(int K) {
   const int per_lane = (K / 8 + kWave - 1) / kWave;
   if (per_lane <= 1) return 1;
@@ -444,32 +456,11 @@ int cmax_for(int K) {
   return 0;
 }
 
-#define TFD_CMAX_SWITCH(K, CALL)                                          \
-  switch (cmax_for(K)) {                                                  \
-    case 1: { constexpr int kC = 1; CALL; break; }                        \
-    case 2: { constexpr int kC = 2; CALL; break; }                        \
-    case 4: { constexpr int kC = 4; CALL; break; }                        \
-    case 8: { constexpr int kC = 8; CALL; break; }                        \
-    case 12: { constexpr int kC = 12; CALL; break; }                      \
-    case 16: { constexpr int kC = 16; CALL; break; }                      \
-    default: return fail(kUnsupported, "K=%d exceeds 8192", K);           \
-  }
-
-template <int kC, int kR, int kPro, int kEpi>
-void launch_gemv(const bf16* x, const bf16* gamma, const bf16* W, const bf16* resid, bf16* out,
-                 int K, int N, float eps, hipStream_t s) {
-  const int rows_per_block = kWavesPerBlock * kR;
-  const int grid = (N + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL((k_gemv<kC, kR, kPro, kEpi>), dim3(grid), dim3(kBlock), 0, s, x, gamma, W,
-                     resid, out, K, N, eps);
-}
-
-}  // namespace
-
+}  // namespace tfd_host
 
 extern "C" {
 
-const char* tfd_last_error(void) { return g_err; }
+const char* tfd_last_error(void) { return tfd_host::g_err; }
 
 int tfd_abi_version(void) { return TFD_ABI_VERSION; }
 

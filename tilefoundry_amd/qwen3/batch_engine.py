@@ -1,0 +1,288 @@
+"""Batched decode: up to 32 sequences advance one token per step.
+
+The batch-1 engine's structure (``engine.py``; the reference's
+``examples/qwen3_1_7b-tilelang/fast/engine.py:69-301``) with a batch axis:
+
+* each sequence has its own position, prompt, picks and page-table row over one
+  shared page pool per layer (``[B * pages][HKV][16][D]`` bf16, a seeded
+  permutation so every sequence's pages are scattered through the pool);
+* the projections are skinny GEMMs on the matrix cores
+  (``tfd_gemm_skinny_bf16``: M = batch rows, 16x16x32 bf16 MFMA), the norms run
+  row by row, and attention runs per (split, kv head, sequence);
+* the whole step -- every layer, the head, the per-sequence pick and the next
+  embeddings -- is recorded once into a HIP graph and replayed; the last kernel
+  feeds each sequence its next prompt token while its prompt lasts and its pick
+  after, so prompts of different lengths walk and continue without host round trips.
+"""
+from __future__ import annotations
+
+from time import perf_counter
+
+import torch
+
+from .. import _lib
+from .._lib import lib, ptr
+from .config import Qwen3Config
+from .engine import bf16_scale
+from .weights import head_rows, pack_layer, validate
+
+MAX_BATCH = 32
+
+
+def _round_up(n: int, m: int) -> int:
+    return (n + m - 1) // m * m
+
+
+class BatchGenerated:
+    """Per-sequence continuations of one batched run and its timing."""
+
+    def __init__(self, tokens, seconds, prefill_seconds, steps, logits=None):
+        self.tokens: list[list[int]] = tokens
+        self.seconds = seconds
+        self.prefill_seconds = prefill_seconds
+        self.steps = steps                    # timed steps (each advances every sequence)
+        self.logits = logits                  # [steps, B, V] f32 when recorded
+
+    @property
+    def tokens_per_second(self) -> float:
+        n = sum(len(t) for t in self.tokens)
+        return n / self.seconds if self.seconds > 0 else float("inf")
+
+
+class BatchEngine:
+    """A loaded Qwen3 dense decoder stepping `batch` sequences together."""
+
+    def __init__(self, cfg: Qwen3Config, weights: dict[str, torch.Tensor], *, batch: int,
+                 device: str = "cuda:0", max_new: int = 256, prompt_room: int = 4096,
+                 page_seed: int | None = 0, graph: bool = True):
+        if cfg.dtype != torch.bfloat16:
+            raise ValueError(f"the HIP engine runs bf16 weights; config has {cfg.dtype}")
+        if not 1 <= batch <= MAX_BATCH:
+            raise ValueError(f"batch must lie in [1, {MAX_BATCH}], got {batch}")
+        validate(cfg, weights)
+        self.cfg, self.B = cfg, batch
+        self.device = torch.device(device)
+        self.L = cfg.num_hidden_layers
+        self.H, self.V = cfg.hidden_size, cfg.vocab_size
+        self.HQ, self.HKV, self.D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        self.I = cfg.intermediate_size
+        self.QD = self.HQ * self.D
+        self.qkv_n = cfg.qkv_size
+        self.eps = float(cfg.rms_norm_eps)
+        self.scale = bf16_scale(self.D)
+        self.nsteps = max_new + prompt_room
+        self.cap = _round_up(self.nsteps, _lib.ATTN_SPLIT)
+        self.max_pages = self.cap // _lib.PAGE_SIZE
+        self.nsplit = self.cap // _lib.ATTN_SPLIT
+        if self.cap > cfg.max_position_embeddings:
+            raise ValueError(f"capacity {self.cap} exceeds the rope table "
+                             f"({cfg.max_position_embeddings} positions)")
+        self._lib = lib()
+        self._pack(weights, page_seed)
+        self._buffers()
+        self.graph = None
+        if graph:
+            self._capture()
+
+    # ---------------------------------------------------------------- setup
+    def _pack(self, weights, page_seed):
+        dev = self.device
+        self.layers = [pack_layer(weights, i, dev) for i in range(self.L)]
+        self.w_embed, self.w_head = head_rows(weights, dev)
+        self.gamma_final = weights["gamma_final"].to(dev).contiguous()
+        d = self.D
+        inv = 1.0 / (self.cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+        ph = torch.outer(torch.arange(self.cap, dtype=torch.float32), inv)
+        ph = torch.cat((ph, ph), dim=-1)
+        self.cos = ph.cos().to(torch.bfloat16).to(dev).contiguous()
+        self.sin = ph.sin().to(torch.bfloat16).to(dev).contiguous()
+        self.num_pages = self.B * self.max_pages
+        if page_seed is None:
+            table = torch.arange(self.num_pages, dtype=torch.int32)
+        else:
+            g = torch.Generator().manual_seed(page_seed)
+            table = torch.randperm(self.num_pages, generator=g).to(torch.int32)
+        self.page_table = table.view(self.B, self.max_pages).to(dev).contiguous()
+
+    def _buffers(self):
+        dev, bf, f32, i32 = self.device, torch.bfloat16, torch.float32, torch.int32
+        B = self.B
+
+        def z(*shape, dtype=bf):
+            return torch.zeros(*shape, device=dev, dtype=dtype)
+
+        self.hid_rows = z(self.L + 1, B, self.H)      # [0]: the step's input embeddings
+        self.hid = self.hid_rows[0]
+        self.xn = z(B, self.H)
+        self.qkv = z(B, self.qkv_n)
+        self.attn = z(B, self.QD)
+        self.h1 = z(B, self.H)
+        self.hmid = z(B, self.I)
+        self.kpool = z(self.L, self.num_pages, self.HKV, _lib.PAGE_SIZE, self.D)
+        self.vpool = z(self.L, self.num_pages, self.HKV, _lib.PAGE_SIZE, self.D)
+        self.scores = z(B, self.HQ, self.cap, dtype=f32)
+        self.smax = z(B, self.nsplit, self.HQ, dtype=f32)
+        self.snew = z(B, self.HQ, dtype=f32)
+        self.psum = z(B, self.nsplit, self.HQ, dtype=f32)
+        self.pout = z(B, self.nsplit, self.HQ, self.D, dtype=f32)
+        self.counters = z(B, self.HKV, dtype=i32)
+        self.logits = z(B, self.V, dtype=f32)
+        self.pick = z(B, dtype=i32)
+        self.pos = z(B, dtype=i32)
+        self.ids = z(B, dtype=torch.int64)
+        self.inp = z(B, self.nsteps, dtype=i32)
+        self.sam = z(B, self.nsteps, dtype=i32)
+        self.plen = z(B, dtype=i32)
+        self.err = z(1, dtype=i32)
+
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    # ---------------------------------------------------------------- the step
+    def _layer(self, i: int, s: int):
+        """One decoder layer (model.py:236-266) for every sequence."""
+        L, w = self._lib, self.layers[i]
+        B, H, I, D = self.B, self.H, self.I, self.D
+        x_in, x_out = self.hid_rows[i], self.hid_rows[i + 1]
+        L.tfd_rmsnorm_rows_bf16(ptr(x_in), H, ptr(w["gamma_in"]), ptr(self.xn), H, B, H,
+                                self.eps, s)
+        L.tfd_gemm_skinny_bf16(ptr(self.xn), H, ptr(w["w_qkv"]), B, H, self.qkv_n,
+                               _lib.EPI_STORE, None, 0, ptr(self.qkv), self.qkv_n, s)
+        L.tfd_attn_rope_scores_paged_batched(
+            ptr(self.qkv), self.qkv_n, ptr(w["gamma_q"]), ptr(w["gamma_k"]), ptr(self.cos),
+            ptr(self.sin), self.cap, ptr(self.pos), ptr(self.page_table), self.max_pages,
+            ptr(self.kpool[i]), ptr(self.vpool[i]), self.num_pages, B, self.HQ, self.HKV, D,
+            self.scale, self.eps, ptr(self.scores), self.cap, ptr(self.smax), ptr(self.snew),
+            self.nsplit, ptr(self.err), s)
+        L.tfd_attn_pv_combine_paged_batched(
+            ptr(self.qkv), self.qkv_n, ptr(self.pos), ptr(self.page_table), self.max_pages,
+            ptr(self.vpool[i]), self.num_pages, B, self.HQ, self.HKV, D, ptr(self.scores),
+            self.cap, ptr(self.smax), ptr(self.snew), ptr(self.psum), ptr(self.pout),
+            self.nsplit, ptr(self.counters), ptr(self.attn), self.QD, ptr(self.err), s)
+        L.tfd_gemm_skinny_bf16(ptr(self.attn), self.QD, ptr(w["w_o"]), B, self.QD, H,
+                               _lib.EPI_RESID, ptr(x_in), H, ptr(self.h1), H, s)
+        L.tfd_rmsnorm_rows_bf16(ptr(self.h1), H, ptr(w["gamma_post"]), ptr(self.xn), H, B, H,
+                                self.eps, s)
+        L.tfd_gemm_skinny_bf16(ptr(self.xn), H, ptr(w["w_gu"]), B, H, 2 * I, _lib.EPI_SWIGLU,
+                               None, 0, ptr(self.hmid), I, s)
+        L.tfd_gemm_skinny_bf16(ptr(self.hmid), I, ptr(w["w_down"]), B, I, H, _lib.EPI_RESID,
+                               ptr(self.h1), H, ptr(x_out), H, s)
+
+    def _step(self):
+        s = self._stream()
+        for i in range(self.L):
+            self._layer(i, s)
+        L, B, H = self._lib, self.B, self.H
+        L.tfd_rmsnorm_rows_bf16(ptr(self.hid_rows[self.L]), H, ptr(self.gamma_final),
+                                ptr(self.xn), H, B, H, self.eps, s)
+        L.tfd_gemm_skinny_bf16(ptr(self.xn), H, ptr(self.w_head), B, H, self.V,
+                               _lib.EPI_LOGITS, None, 0, ptr(self.logits), self.V, s)
+        L.tfd_argmax_rows(ptr(self.logits), self.V, B, self.V, ptr(self.pick), s)
+        L.tfd_finalize_rows(ptr(self.pick), B, ptr(self.inp), self.nsteps, ptr(self.plen),
+                            ptr(self.ids), ptr(self.pos), ptr(self.sam), self.nsteps,
+                            self.nsteps, ptr(self.w_embed), ptr(self.hid), H, H, self.V,
+                            ptr(self.err), s)
+
+    def _capture(self):
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self._load_prompts([[0]] * self.B)
+            for _ in range(3):
+                self._step()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._step()
+        torch.cuda.synchronize(self.device)
+        self._reset()
+
+    def replay(self):
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._step()
+
+    def run_steps(self, n: int):
+        for _ in range(n):
+            self.replay()
+
+    # ------------------------------------------------------------- generation
+    def _reset(self):
+        self.pos.zero_()
+        self.sam.zero_()
+        self.err.zero_()
+
+    def _load_prompts(self, prompts: list[list[int]]):
+        self._reset()
+        self.inp.zero_()
+        lens = []
+        for b, p in enumerate(prompts):
+            self.inp[b, :len(p)] = torch.tensor(p, dtype=torch.int32).to(self.device)
+            lens.append(len(p))
+        self.plen.copy_(torch.tensor(lens, dtype=torch.int32))
+        self.ids.copy_(torch.tensor([p[0] for p in prompts], dtype=torch.int64))
+        self._lib.tfd_embed_rows_bf16(ptr(self.w_embed), ptr(self.ids), ptr(self.hid), self.H,
+                                      self.B, self.H, self.V, ptr(self.err), self._stream())
+
+    def check_errors(self):
+        e = int(self.err.item())
+        if e:
+            names = [n for bit, n in ((1, "token id"), (2, "position"), (4, "page-table entry"),
+                                      (8, "step")) if e & bit]
+            raise RuntimeError(f"decode kernels flagged an out-of-range {', '.join(names)}")
+
+    def generate(self, prompts: list[list[int]], max_new: int,
+                 record_logits: bool = False) -> BatchGenerated:
+        """Walk every prompt, then continue for *max_new* greedy tokens per
+        sequence.  Sequence b's continuation starts after its own prompt; all
+        sequences step together, so the step count is max(prompt) - 1 + max_new,
+        and the timing covers the steps after the longest prompt."""
+        if len(prompts) != self.B:
+            raise ValueError(f"engine holds {self.B} sequences, got {len(prompts)} prompts")
+        if any(len(p) < 1 for p in prompts):
+            raise ValueError("every sequence needs a prompt of at least one token")
+        longest = max(len(p) for p in prompts)
+        if longest + max_new > self.nsteps:
+            raise ValueError(f"prompt {longest} + {max_new} new exceeds this engine's "
+                             f"{self.nsteps} steps")
+        if any(not 0 <= int(t) < self.V for p in prompts for t in p):
+            raise ValueError(f"prompt ids must lie in [0, {self.V})")
+        self._load_prompts(prompts)
+        steps = longest - 1 + max_new
+        warm = longest - 1
+        hist = (torch.empty(steps, self.B, self.V, device=self.device, dtype=torch.float32)
+                if record_logits else None)
+        torch.cuda.synchronize(self.device)
+        t0 = perf_counter()
+        for k in range(warm):
+            self.replay()
+            if hist is not None:
+                hist[k].copy_(self.logits)
+        torch.cuda.synchronize(self.device)
+        t1 = perf_counter()
+        for k in range(warm, steps):
+            self.replay()
+            if hist is not None:
+                hist[k].copy_(self.logits)
+        torch.cuda.synchronize(self.device)
+        t2 = perf_counter()
+        self.check_errors()
+        sam = self.sam.cpu()
+        tokens = [sam[b, len(p) - 1: len(p) - 1 + max_new].tolist()
+                  for b, p in enumerate(prompts)]
+        logits = None
+        if hist is not None:
+            h = hist.cpu()
+            # logits at each sequence's own picks: step len(p) - 1 + j
+            logits = [h[len(p) - 1: len(p) - 1 + max_new, b] for b, p in enumerate(prompts)]
+        return BatchGenerated(tokens, t2 - t1, t1 - t0, max_new, logits)
+
+    # ------------------------------------------------------------ accounting
+    def weight_bytes_per_step(self) -> int:
+        return self.cfg.weight_bytes_per_step()
+
+    def kv_bytes_at(self, positions) -> int:
+        """KV bytes one step touches with sequences at *positions*."""
+        return sum(self.cfg.kv_bytes_per_position() * (p + 1) for p in positions)
