@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TFD_ABI_VERSION 5
+#define TFD_ABI_VERSION 7
 
 /* gemv prologues / epilogues */
 #define TFD_PRO_PLAIN 0  /* x used as given */
@@ -127,7 +127,7 @@ int tfd_attn_pv_combine_paged(const void* qkv, const int32_t* cache_len,
                               int nsplit, int32_t* counters, void* attn_out, int32_t* err,
                               void* stream);
 
-/* ---- batched decode (up to 32 sequences per step) -------
+/* ---- batched decode (workload C3: up to 32 sequences per step) -------
  * Activations are row-major [rows][n] with leading dimensions; each sequence has
  * its own position (pos[b]) and page-table row (page_table + b * max_pages). */
 
@@ -136,15 +136,29 @@ int tfd_attn_pv_combine_paged(const void* qkv, const int32_t* cache_len,
 int tfd_rmsnorm_rows_bf16(const void* x, int ldx, const void* gamma, void* out, int ldo,
                           int rows, int n, float eps, void* stream);
 
-/* Skinny GEMM on the matrix cores: Y[m][n] = sum_k X[m][k] W[n][k] for m < M <= 32
- * (the q/k/v, o, gate/up, down and head projections of a batch, ref_src/model.py:160-171,
- * 213-215, 230-234, 300-305, at M = batch; SURVEY's gemm_bf16_skinny entry, which
- * replaces fast/kernels.py:123-145 / 260-321 at batch > 1).  f32 accumulation,
- * one rounding per output; epilogue TFD_EPI_STORE / RESID (resid [M][ldr]) / SWIGLU
- * (out [M][N/2]) / LOGITS (out f32).  K % 32 == 0. */
+/* Weights [N][K] (row stride ldw) re-laid for tfd_gemm_skinny_bf16: 16-row x 32-k
+ * blocks of 1 KiB in the matrix cores' operand order, rows padded with zeros to a
+ * multiple of 16; `packed` holds ceil(N/16) * 16 * K bf16.  K % 256 == 0.  Done once
+ * when a batched engine loads its weights.  The reference's kernels take weights as
+ * ref_src/hf_alias.py:20-43 binds them ([in][out]); this layout is internal to the
+ * batched path and has no counterpart there. */
+int tfd_pack_skinny_bf16(const void* w, int ldw, int N, int K, void* packed, void* stream);
+
+/* Skinny GEMM on the matrix cores: Y[m][n] = sum_k X[m][k] W[n][k] for m < M <= 32,
+ * W packed by tfd_pack_skinny_bf16 (the q/k/v, o, gate/up, down and head projections of a batch, ref_src/model.py:160-171,
+ * 213-215, 230-234, 300-305, at M = batch; it replaces fast/kernels.py:123-145 / 260-321
+ * at batch > 1).  f32 accumulation, one rounding per output; epilogue TFD_EPI_STORE /
+ * RESID (resid [M][ldr]) / SWIGLU (out [M][N/2]) / LOGITS (out f32).
+ * K % 256 == 0.  `work` (work_floats f32 values; NULL with 0 allowed when K <= 2048)
+ * lets the library split K into slices: it begins with TFD_SKINNY_COUNTERS int32 tile
+ * counters, zero before the first call (every call leaves them at zero), followed by
+ * f32 partials of slices * ceil(N/16) * 512 floats; the last wave to finish a tile
+ * adds its slices in slice order.  A smaller buffer means fewer slices; K > 2048 needs
+ * at least K/2048 of them.  Calls sharing one buffer must be stream-ordered. */
+#define TFD_SKINNY_COUNTERS 16384
 int tfd_gemm_skinny_bf16(const void* x, int ldx, const void* w, int M, int K, int N,
                          int epilogue, const void* resid, int ldr, void* out, int ldo,
-                         void* stream);
+                         float* work, int64_t work_floats, void* stream);
 
 /* tfd_attn_rope_scores_paged for `batch` sequences at once (grid nsplit x kv_heads x
  * batch): sequence b reads QKV row b (stride ldq) at its own position pos[b] and
@@ -155,16 +169,18 @@ int tfd_attn_rope_scores_paged_batched(
     const void* sin_table, int rope_rows, const int32_t* pos, const int32_t* page_table,
     int max_pages, void* k_pool, void* v_pool, int num_pages, int batch, int heads, int kv_heads,
     int head_dim, float scale, float eps, float* scores, int score_stride, float* split_max,
-    float* score_new, int nsplit, int32_t* err, void* stream);
+    float* score_new, int nsplit, int split_tiles, int32_t* err, void* stream);
 
 /* tfd_attn_pv_combine_paged for `batch` sequences (counters: batch x kv_heads, zero;
- * output row b at attn_out + b * lda). */
+ * output row b at attn_out + b * lda).  A split covers split_tiles x 64 positions in
+ * both entries (long contexts: fewer, longer splits; one tile's loads are in flight
+ * while the previous one is reduced); nsplit x split_tiles x 64 >= max_pages x 16. */
 int tfd_attn_pv_combine_paged_batched(
     const void* qkv, int ldq, const int32_t* pos, const int32_t* page_table, int max_pages,
     const void* v_pool, int num_pages, int batch, int heads, int kv_heads, int head_dim,
     const float* scores, int score_stride, const float* split_max, const float* score_new,
-    float* part_sum, float* part_out, int nsplit, int32_t* counters, void* attn_out, int lda,
-    int32_t* err, void* stream);
+    float* part_sum, float* part_out, int nsplit, int split_tiles, int32_t* counters,
+    void* attn_out, int lda, int32_t* err, void* stream);
 
 /* Greedy pick per row: the first maximal logit (ref_src/generation.py:24-26). */
 int tfd_argmax_rows(const float* logits, int ldl, int rows, int vocab, int32_t* pick,

@@ -91,10 +91,10 @@ class Qwen3Dims:
         return self.heads // self.kv_heads
 
 
-#: BASELINE config 1: tiny Qwen3-style decoder, fp32.
+#: Workload C1: tiny Qwen3-style decoder, fp32.
 C1 = Qwen3Dims(hidden=256, heads=4, kv_heads=2, head_dim=64, intermediate=768,
                vocab=4096, layers=2, dtype=torch.float32)
-#: BASELINE config 2: the Qwen3-1.7B architecture, bf16.
+#: Workload C2: the Qwen3-1.7B architecture, bf16.
 C2 = Qwen3Dims(hidden=2048, heads=16, kv_heads=8, head_dim=128, intermediate=6144,
                vocab=151936, layers=28, dtype=torch.bfloat16)
 

@@ -2,13 +2,13 @@
 
     python tests/golden/make_golden.py [c1] [c2]
 
-c1_tiny_fp32.json   BASELINE config 1: tiny Qwen3 (2 layers, hidden 256, 4q/2kv,
+c1_tiny_fp32.json   workload C1: tiny Qwen3 (2 layers, hidden 256, 4q/2kv,
                     head_dim 64, I 768, V 4096), fp32, every parameter N(0, 0.02)
                     from seed 0, a 128-token uniform-random prompt (seed 0), 32
                     greedy tokens.  Produced by the oracle AND by Hugging Face
                     Qwen3ForCausalLM (full-sequence forward, same weights); the
                     script refuses to write unless the two agree.
-c2_qwen3_1p7b.json  BASELINE config 2 shape (28 layers, bf16), the bench's
+c2_qwen3_1p7b.json  workload C2 shape (28 layers, bf16), the bench's
                     synthetic weights (seed 0) and 32-token prompt (seed 0): the
                     oracle's first 64 greedy tokens, their top-2 margins and each
                     step's top-8 (index, logit); for both norm-scale draws.

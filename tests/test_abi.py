@@ -27,6 +27,17 @@ def test_header_declares_entries():
     assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
 
 
+def test_header_constants_match_binding():
+    """Every plain #define of the header has the value the binding uses."""
+    defines = dict(re.findall(r"^#define TFD_(\w+) (\d+)", HEADER.read_text(), re.M))
+    names = {"ABI_VERSION", "PRO_PLAIN", "PRO_NORM", "EPI_STORE", "EPI_RESID", "EPI_SWIGLU",
+             "EPI_LOGITS", "ERR_TOKEN_RANGE", "ERR_POS_RANGE", "ERR_PAGE_RANGE",
+             "ERR_STEP_RANGE", "ERR_SYNC", "PAGE_SIZE", "ATTN_SPLIT", "SKINNY_COUNTERS"}
+    assert names <= set(defines), names - set(defines)
+    for name in names:
+        assert getattr(_lib, name) == int(defines[name]), name
+
+
 @pytest.mark.skipif(not Path(LIB).exists(), reason="library not built")
 def test_library_exports_every_declared_entry():
     dll = ctypes.CDLL(str(LIB))

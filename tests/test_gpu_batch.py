@@ -1,4 +1,4 @@
-"""Batched decode (BASELINE config 3 path) on the GPU.
+"""Batched decode (workload C3) on the GPU.
 
 * The skinny GEMM against an f64 matmul of the same bf16 operands: every output
   is one f32 sum rounded once, so it lies within one bf16 ulp of the exact value
@@ -23,9 +23,17 @@ from tilefoundry_amd.qwen3.batch_engine import BatchEngine
 pytestmark = pytest.mark.gpu
 
 
-def _gemm(x, w, epi, resid=None):
+def _packed(w):
+    N, K = w.shape
+    out = torch.full((-(-N // 16) * 16, K), float("nan"), device=w.device, dtype=w.dtype)
+    lib().tfd_pack_skinny_bf16(ptr(w), K, N, K, ptr(out), torch.cuda.current_stream().cuda_stream)
+    return out
+
+
+def _gemm(x, w, epi, resid=None, work=None):
     M, K = x.shape
     N = w.shape[0]
+    w = _packed(w)
     if epi == _lib.EPI_SWIGLU:
         out = torch.zeros(M, N // 2, device=x.device, dtype=torch.bfloat16)
     elif epi == _lib.EPI_LOGITS:
@@ -34,20 +42,34 @@ def _gemm(x, w, epi, resid=None):
         out = torch.zeros(M, N, device=x.device, dtype=torch.bfloat16)
     lib().tfd_gemm_skinny_bf16(ptr(x), K, ptr(w), M, K, N, epi,
                                None if resid is None else ptr(resid), N, ptr(out),
-                               out.shape[1], torch.cuda.current_stream().cuda_stream)
+                               out.shape[1], None if work is None else ptr(work),
+                               0 if work is None else work.numel(),
+                               torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     return out.cpu()
 
 
+@pytest.mark.parametrize("split", [False, True], ids=["one-slice", "split-k"])
 @pytest.mark.parametrize("M", [1, 5, 16, 17, 32])
-@pytest.mark.parametrize("K,N", [(2048, 48), (6144, 40), (64, 16), (2048, 2050)])
-def test_skinny_gemm_within_one_ulp_of_exact(gpu_device, M, K, N):
+@pytest.mark.parametrize("K,N", [(2048, 48), (6144, 40), (256, 16), (2048, 2050), (2048, 4200)])
+def test_skinny_gemm_within_one_ulp_of_exact(gpu_device, M, K, N, split):
+    """With a work buffer the library splits K into slices (8 for most shapes
+    here, 4 at N = 4200) whose partial tiles the last-arriving wave adds in
+    slice order; without one, K up to 2048 runs in one slice and a deeper K is
+    refused (it does not fit the LDS stage)."""
     g = torch.Generator().manual_seed(M * 7919 + K + N)
+    tiles = (N + 15) // 16
+    work = (torch.zeros(_lib.SKINNY_COUNTERS + 16 * tiles * 512, device=gpu_device,
+                        dtype=torch.float32) if split else None)
     x = (torch.randn(M, K, generator=g) * 0.5).to(torch.bfloat16)
     w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    if work is None and K > 2048:
+        with pytest.raises(_lib.TFDError):
+            _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_STORE)
+        return
     exact = x.double() @ w.double().t()                          # [M][N]
     want = exact.to(torch.bfloat16).float()
-    got = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_STORE).float()
+    got = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_STORE, work=work).float()
     # one rounding of an f32 sum: within an ulp of the exact value plus the f32
     # accumulation bound K * 2^-24 * sum |x||w| (which matters only under cancellation)
     acc_bound = K * 2.0 ** -24 * (x.double().abs() @ w.double().abs().t())
@@ -55,20 +77,55 @@ def test_skinny_gemm_within_one_ulp_of_exact(gpu_device, M, K, N):
     bad = (got.double() - exact).abs() > bound
     assert not bad.any(), (int(bad.sum()), got[bad][:4], exact[bad][:4])
     # logits: the same rounding, returned as f32
-    lg = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_LOGITS)
+    lg = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_LOGITS, work=work)
     assert torch.equal(lg, got)
     # residual: bf16(resid + bf16(y))
     r = (torch.randn(M, N, generator=g)).to(torch.bfloat16)
-    res = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_RESID, r.to(gpu_device)).float()
+    res = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_RESID, r.to(gpu_device),
+                work=work).float()
     assert torch.equal(res, (r.float() + got).to(torch.bfloat16).float())
     # swiglu over (gate, up) row pairs, from the kernel's own rounded pair
     if N % 2 == 0:
-        sw = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_SWIGLU).float()
+        sw = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_SWIGLU, work=work).float()
         gate, up = got[:, 0::2], got[:, 1::2]
         act = torch.nn.functional.silu(gate.to(torch.bfloat16)).float()
         want_sw = (act * up).to(torch.bfloat16).float()
         # silu's own f32 evaluation may differ from torch's by an ulp before rounding
         assert ((sw - want_sw).abs() <= ulp_bf16(want_sw)).all()
+    if work is not None:
+        # every call leaves the tile counters at zero for the next one
+        assert not work[:tiles].any()
+
+
+def test_pack_skinny_layout(gpu_device):
+    """The packed layout, element by element: block (tile t, step s) is 1 KiB and
+    lane l's 8 values are W[16t + l % 16][32s + 8(l // 16) + j]; padding rows are 0."""
+    N, K = 40, 512
+    w = torch.arange(N * K, dtype=torch.float32).remainder(251).to(torch.bfloat16)
+    w = w.view(N, K).to(gpu_device)
+    got = _packed(w).cpu().view(-1, 64, 8)                         # [block][lane][j]
+    tiles, steps = -(-N // 16), K // 32
+    wp = torch.cat([w.cpu(), torch.zeros(tiles * 16 - N, K, dtype=w.dtype)])
+    want = wp.view(tiles, 16, steps, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1, 64, 8)
+    assert torch.equal(got, want)
+
+
+def test_skinny_gemm_shapes_share_one_work_buffer(gpu_device):
+    """GEMMs of different tile counts and slice counts in a row on one work
+    buffer (the layer's q/k/v, o, gate/up and down) give the bits each gives on
+    a fresh buffer: the counters sit at a fixed place and are left at zero."""
+    g = torch.Generator().manual_seed(99)
+    M = 32
+    shapes = [(2048, 4096, _lib.EPI_STORE), (2048, 2048, _lib.EPI_STORE),
+              (2048, 12288, _lib.EPI_SWIGLU), (6144, 2048, _lib.EPI_STORE)] * 2
+    big = torch.zeros(1 << 21, device=gpu_device, dtype=torch.float32)
+    for K, N, epi in shapes:
+        x = (torch.randn(M, K, generator=g) * 0.5).to(torch.bfloat16).to(gpu_device)
+        w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu_device)
+        shared = _gemm(x, w, epi, work=big)
+        fresh = _gemm(x, w, epi, work=torch.zeros_like(big))
+        assert torch.equal(shared, fresh), (K, N)
+    assert not big[:_lib.SKINNY_COUNTERS].any()
 
 
 def _oracle_runs(cfg, w, prompts, max_new):
@@ -95,6 +152,21 @@ def test_batch_engine_qwen3_layer_shape(gpu_device):
         seq = type("Run", (), {"tokens": run.tokens[b], "logits": run.logits[b]})
         k = _check_run(seq, orc, 16, strict=False)
         print(f"sequence {b}: identical for {16 if k is None else k} of 16 steps")
+
+
+@pytest.mark.parametrize("split_tiles", [1, 3])
+def test_batch_engine_long_splits(gpu_device, split_tiles):
+    """Splits of several 64-position tiles (the long-context partition) against
+    the oracle, with contexts past several splits."""
+    cfg = QWEN3_1_7B.with_(num_hidden_layers=2)
+    w = synthetic_weights(cfg, seed=1, norms="ones")
+    prompts = [_prompt(n, cfg.vocab_size, seed=20 + n) for n in (230, 150, 400)]
+    eng = BatchEngine(cfg, w, batch=3, device=gpu_device, max_new=8, prompt_room=400,
+                      split_tiles=split_tiles)
+    run = eng.generate(prompts, 8, record_logits=True)
+    for b, orc in enumerate(_oracle_runs(cfg, w, prompts, 8)):
+        seq = type("Run", (), {"tokens": run.tokens[b], "logits": run.logits[b]})
+        _check_run(seq, orc, 8, strict=False)
 
 
 def test_batch_engine_paging_and_graph_change_no_bit(gpu_device):

@@ -1,6 +1,6 @@
 """The captured decode engine against the oracle's greedy loop.
 
-greedy tokens identical for the first 64 steps;
+Parity bar of the decode path: greedy tokens identical for the first 64 steps;
 logits within max |delta| <= 2e-2 of the oracle's max |logit| (bf16).  The small
 configs here are config 1's shape at bf16 and the Qwen3-1.7B layer shape at two
 layers; the full-depth model is checked against committed golden fixtures in

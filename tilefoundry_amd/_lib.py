@@ -7,23 +7,25 @@ returns non-zero raises ``TFDError`` carrying the library's own message.
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_float, c_int, c_void_p
+from ctypes import c_float, c_int, c_int64, c_void_p
 from functools import lru_cache
 from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 5
+ABI_VERSION = 7
 
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS = 0, 1, 2, 3
 ERR_TOKEN_RANGE, ERR_POS_RANGE, ERR_PAGE_RANGE, ERR_STEP_RANGE, ERR_SYNC = 1, 2, 4, 8, 16
 PAGE_SIZE = 16
+SKINNY_COUNTERS = 16384     # tile counters at the start of a skinny-GEMM work buffer
 ATTN_SPLIT = 64
 
 P = c_void_p
 I = c_int
 F = c_float
+L = c_int64
 
 #: argtypes of every entry, in header order (restype is int unless named here)
 SIGNATURES: dict[str, list] = {
@@ -39,11 +41,12 @@ SIGNATURES: dict[str, list] = {
                                    P, P, I, P, P],
     "tfd_attn_pv_combine_paged": [P, P, P, I, P, I, I, I, I, P, I, P, P, P, P, I, P, P, P, P],
     "tfd_rmsnorm_rows_bf16": [P, I, P, P, I, I, I, F, P],
-    "tfd_gemm_skinny_bf16": [P, I, P, I, I, I, I, P, I, P, I, P],
+    "tfd_pack_skinny_bf16": [P, I, I, I, P, P],
+    "tfd_gemm_skinny_bf16": [P, I, P, I, I, I, I, P, I, P, I, P, L, P],
     "tfd_attn_rope_scores_paged_batched": [P, I, P, P, P, P, I, P, P, I, P, P, I, I, I, I, I, F,
-                                           F, P, I, P, P, I, P, P],
+                                           F, P, I, P, P, I, I, P, P],
     "tfd_attn_pv_combine_paged_batched": [P, I, P, P, I, P, I, I, I, I, I, P, I, P, P, P, P, I,
-                                          P, P, I, P, P],
+                                          I, P, P, I, P, P],
     "tfd_argmax_rows": [P, I, I, I, P, P],
     "tfd_finalize_rows": [P, I, P, I, P, P, P, P, I, I, P, P, I, I, I, P, P],
     "tfd_embed_rows_bf16": [P, P, P, I, I, I, I, P, P],

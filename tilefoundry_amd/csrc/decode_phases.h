@@ -536,14 +536,13 @@ __device__ __forceinline__ int v_pos(int j0, int p) {
   return j0 + (int)threadIdx.x / A::kLpp + p * A::kGroups;
 }
 
-// K rows of split `split` (positions j < P are the ones used).  A split that
-// holds no prior position issues nothing.
+// K rows of the 64 positions from j0 (positions j < P are the ones used).  A
+// tile that holds no prior position issues nothing.
 template <int D>
-__device__ __forceinline__ void k_tile_issue(int split, int h, int P, const int* page_table,
-                                             int max_pages, const bf16* kpool, int num_pages,
-                                             int kv_heads, KTile<D>& kt) {
+__device__ __forceinline__ void k_tile_issue_at(int j0, int h, int P, const int* page_table,
+                                                int max_pages, const bf16* kpool, int num_pages,
+                                                int kv_heads, KTile<D>& kt) {
   using A = AttnShape<D>;
-  const int j0 = split * kSplit;
   const int ch = (threadIdx.x & (kWave - 1)) % A::kLpp;
 #pragma unroll
   for (int p = 0; p < A::kKPasses; ++p) {
@@ -566,11 +565,10 @@ __device__ __forceinline__ void k_tile_issue(int split, int h, int P, const int*
 }
 
 template <int D>
-__device__ __forceinline__ void v_tile_issue(int split, int h, int P, const int* page_table,
-                                             int max_pages, const bf16* vpool, int num_pages,
-                                             int kv_heads, VTile<D>& vt) {
+__device__ __forceinline__ void v_tile_issue_at(int j0, int h, int P, const int* page_table,
+                                                int max_pages, const bf16* vpool, int num_pages,
+                                                int kv_heads, VTile<D>& vt) {
   using A = AttnShape<D>;
-  const int j0 = split * kSplit;
   const int ch = (int)threadIdx.x % A::kLpp;
 #pragma unroll
   for (int p = 0; p < A::kVPasses; ++p) {
@@ -590,6 +588,20 @@ __device__ __forceinline__ void v_tile_issue(int split, int h, int P, const int*
     vt.t[p] = coh_ld16(vpool, (uint32_t)(page_row(bad ? 0 : vt.pg[p], j, kv_heads, h, D) +
                                          ch * 8) * 2u);
   }
+}
+
+// The first tile of split `split` of a one-tile-per-split partition.
+template <int D>
+__device__ __forceinline__ void k_tile_issue(int split, int h, int P, const int* page_table,
+                                             int max_pages, const bf16* kpool, int num_pages,
+                                             int kv_heads, KTile<D>& kt) {
+  k_tile_issue_at<D>(split * kSplit, h, P, page_table, max_pages, kpool, num_pages, kv_heads, kt);
+}
+template <int D>
+__device__ __forceinline__ void v_tile_issue(int split, int h, int P, const int* page_table,
+                                             int max_pages, const bf16* vpool, int num_pages,
+                                             int kv_heads, VTile<D>& vt) {
+  v_tile_issue_at<D>(split * kSplit, h, P, page_table, max_pages, vpool, num_pages, kv_heads, vt);
 }
 
 // ---------------------------------------------------------------------------
@@ -680,10 +692,10 @@ __device__ __forceinline__ QKPre qk_prefetch(int rp, int P, const bf16* __restri
 template <int D, int G, bool kLL>
 __device__ __forceinline__ void attn_scores_phase(
     int split, int h, const uint32_t* hs, const QKPre& pre, int rope_rows, int rp, int P,
-    int max_pages, bf16* __restrict__ kpool, bf16* __restrict__ vpool, int num_pages,
+    const int* __restrict__ page_table, int max_pages, bf16* __restrict__ kpool, bf16* __restrict__ vpool, int num_pages,
     int kv_heads, float scale, float eps, float* __restrict__ S, int s_stride,
     float* __restrict__ smax, float* __restrict__ snew, const AttnLL& ll, const KTile<D>& kt,
-    int* err) {
+    int* err, int chunks = 1) {
   using A = AttnShape<D>;
   constexpr int kHalf = D / 2;
   constexpr int kLpp = A::kLpp;
@@ -691,14 +703,17 @@ __device__ __forceinline__ void attn_scores_phase(
   static_assert(G + 1 <= kWavesPerBlock, "one wave per vector");
   const int heads = kv_heads * G;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int j0 = split * kSplit;
+  // a split is `chunks` tiles of 64 positions (the persistent kernel uses one)
+  const int j0 = split * chunks * kSplit;
   const int ch = lane % kLpp;
 
+  // per-phase launches hand scores, maxima and new-key scores to the next
+  // kernel, so plain (cached, write-back) stores are enough there
   auto put_max = [&](int g, float m) {
     if (kLL)
       ll_put(ll.smax, (uint32_t)(split * heads + h * G + g), __float_as_uint(m), ll.tag);
     else
-      coh_stf(&smax[split * heads + h * G + g], m);
+      smax[split * heads + h * G + g] = m;
   };
   if (split != 0 && j0 >= P) {
     if (tid < G) put_max(tid, kNegInf);
@@ -711,7 +726,7 @@ __device__ __forceinline__ void attn_scores_phase(
       if (kLL)
         snew[tid] = 0.f;
       else
-        coh_stf(&snew[h * G + tid], 0.f);
+        snew[h * G + tid] = 0.f;
     }
     return;
   }
@@ -723,7 +738,7 @@ __device__ __forceinline__ void attn_scores_phase(
   const int li = lane < kHalf ? lane : 0;
   const int vbase = (v < G + 1 ? v : 0) * D;
   const int page_new = pre.page_new;
-  const int jend = (j0 + kSplit < P) ? j0 + kSplit : P;
+  const int jend = (j0 + chunks * kSplit < P) ? j0 + chunks * kSplit : P;
   const float x0 = act ? hs_at(hs, vbase + li) : 0.f;
   const float x1 = act ? hs_at(hs, vbase + li + kHalf) : 0.f;
   const float g0 = bf2f(pre.g0), g1 = bf2f(pre.g1);
@@ -784,7 +799,7 @@ __device__ __forceinline__ void attn_scores_phase(
       if (kLL)
         snew[wave] = rbf(a);
       else if (split == 0)
-        coh_stf(&snew[h * G + wave], rbf(a));
+        snew[h * G + wave] = rbf(a);
     }
   }
 
@@ -798,33 +813,44 @@ __device__ __forceinline__ void attn_scores_phase(
 #pragma unroll
   for (int g = 0; g < G; ++g) mymax[g] = kNegInf;
   bool page_ok = true;
+  KTile<D> cur = kt;
+  for (int c = 0; c < chunks; ++c) {
+    const int jc = j0 + c * kSplit;
+    if (jc >= jend) break;
+    // the next tile's loads go out before this one is reduced
+    KTile<D> nxt;
+    if (c + 1 < chunks)
+      k_tile_issue_at<D>(jc + kSplit, h, P, page_table, max_pages, kpool, num_pages,
+                         kv_heads, nxt);
 #pragma unroll
-  for (int p = 0; p < A::kKPasses; ++p) {
-    const int j = k_pos<D>(j0, p);
-    const bool bad = kt.pg[p] < 0 || kt.pg[p] >= num_pages;
-    if (j < jend && bad) page_ok = false;
-    const bool valid = j < jend && !bad;
-    const uint32_t kw[4] = {kt.t[p].x, kt.t[p].y, kt.t[p].z, kt.t[p].w};
+    for (int p = 0; p < A::kKPasses; ++p) {
+      const int j = k_pos<D>(jc, p);
+      const bool bad = cur.pg[p] < 0 || cur.pg[p] >= num_pages;
+      if (j < jend && bad) page_ok = false;
+      const bool valid = j < jend && !bad;
+      const uint32_t kw[4] = {cur.t[p].x, cur.t[p].y, cur.t[p].z, cur.t[p].w};
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float a = 0.f;
+      for (int g = 0; g < G; ++g) {
+        float a = 0.f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        a += rbf(qv[g][2 * e] * bf_lo(kw[e]));
-        a += rbf(qv[g][2 * e + 1] * bf_hi(kw[e]));
-      }
-      a = group_sum<kLpp>(a);
-      const float sc = rbf(a);
-      if (valid) {
-        if (ch == 0) {
-          if (kLL)
-            S[g * kSplit + (j - j0)] = sc;
-          else
-            coh_stf(&S[(int64_t)(h * G + g) * s_stride + j], sc);
+        for (int e = 0; e < 4; ++e) {
+          a += rbf(qv[g][2 * e] * bf_lo(kw[e]));
+          a += rbf(qv[g][2 * e + 1] * bf_hi(kw[e]));
         }
-        mymax[g] = fmaxf(mymax[g], sc);
+        a = group_sum<kLpp>(a);
+        const float sc = rbf(a);
+        if (valid) {
+          if (ch == 0) {
+            if (kLL)
+              S[g * kSplit + (j - j0)] = sc;
+            else
+              S[(int64_t)(h * G + g) * s_stride + j] = sc;
+          }
+          mymax[g] = fmaxf(mymax[g], sc);
+        }
       }
     }
+    if (c + 1 < chunks) cur = nxt;
   }
   if (!page_ok) raise_error(err, kErrPageRange);
 #pragma unroll
@@ -881,34 +907,33 @@ __device__ __forceinline__ void attn_pv_phase(
     int num_pages, int kv_heads, const float* __restrict__ S, int s_stride,
     const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
     float* part_out, int* counters, bf16* __restrict__ attn_out, const AttnLL& ll,
-    const VTile<D>& vt, int* err, const Hook& polled = Hook()) {
+    const VTile<D>& vt, int* err, int chunks = 1, const Hook& polled = Hook()) {
   using A = AttnShape<D>;
   constexpr int kLpp = A::kLpp;
   constexpr int kGroups = A::kGroups;
   constexpr int kOut = G * D;                         // outputs of the head group
-  static_assert(kSplit == kWave, "one wave sums one head's split of p");
+  static_assert(kSplit == kWave, "one wave sums one head's tile of p");
   static_assert(G <= kWavesPerBlock, "one wave per query head of the group");
   static_assert(kOut % 4 == 0 && kOut <= kBlock, "one thread per output");
   const int heads = kv_heads * G;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int ch = tid % kLpp, jo = tid / kLpp;
-  const int j0 = split * kSplit;
-  (void)max_pages;
-  (void)page_table;
-  (void)vpool;
+  // a split is `chunks` tiles of 64 positions (the persistent kernel uses one)
+  const int slen = chunks * kSplit;
+  const int j0 = split * slen;
 
   if (P < 0 || P >= max_pages * kPage) P = 0;  // part 1 already raised the flag
-  const int nact = (P + kSplit - 1) / kSplit;
+  const int nact = (P + slen - 1) / slen;
   const int participants = nact > 0 ? nact : 1;
   if (split >= participants) return;
-  const int jend = (j0 + kSplit < P) ? j0 + kSplit : P;
+  const int jend = (j0 + slen < P) ? j0 + slen : P;
 
-  // ---- this split's scores, every split's max, the new-key scores
+  // ---- the first tile's scores, every split's max, the new-key scores
   const int wg = wave < G ? wave : 0;
   // the persistent kernel passes this block's own scores and new-key scores (LDS)
-  const float sn = kLL ? snew[wg] : coh_ldf(&snew[h * G + wg]);
-  const float sj_raw =
-      kLL ? S[wg * kSplit + lane] : coh_ldf(&S[(int64_t)(h * G + wg) * s_stride + j0 + lane]);
+  const float sn = kLL ? snew[wg] : snew[h * G + wg];
+  const float sj_first =
+      kLL ? S[wg * kSplit + lane] : S[(int64_t)(h * G + wg) * s_stride + j0 + lane];
   float mx = kNegInf;
   for (int s0 = 0; s0 < nact; s0 += kWave) {
     const int s = s0 + lane;
@@ -918,12 +943,11 @@ __device__ __forceinline__ void attn_pv_phase(
       m = __uint_as_float(
           ll_get(ll.smax, (uint32_t)((s < nact ? s : 0) * heads + h * G + wg), ll.tag, err));
     } else {
-      m = coh_ldf(&smax[(s < nsplit ? s : nsplit - 1) * heads + h * G + wg]);
+      m = smax[(s < nsplit ? s : nsplit - 1) * heads + h * G + wg];
     }
     if (s < nact) mx = fmaxf(mx, m);
   }
   polled();
-  const float sj = (j0 + lane < jend) ? sj_raw : kNegInf;
 
   __shared__ float M[G];
   __shared__ float p[G][kSplit];
@@ -931,33 +955,41 @@ __device__ __forceinline__ void attn_pv_phase(
   __shared__ float psums[kGroups][G];
   __shared__ int is_last;
 
+  float mw = 0.f;                                     // wave g's joint peak
   if (wave < G) {
-    const float m = fmaxf(wave_max(mx), sn);
-    if (lane == 0) M[wave] = m;
-    const float pj = (j0 + lane < jend) ? rbf(expf(rbf(sj - m))) : 0.f;
-    p[wave][lane] = pj;
-    const float s = wave_sum(pj);
-    if (lane == 0) {
-      if (kLL)
-        ll_put(ll.psum, (uint32_t)(split * heads + h * G + wave), __float_as_uint(s), ll.tag);
-      else
-        coh_stf(&part_sum[split * heads + h * G + wave], s);
-    }
+    mw = fmaxf(wave_max(mx), sn);
+    if (lane == 0) M[wave] = mw;
   }
-  __syncthreads();
-  {
-    float acc[G][8];
+  float psum = 0.f;                                   // wave g: sum of p, tile by tile
+  float acc[G][8];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+  for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-    bool page_ok = true;
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  bool page_ok = true;
+  VTile<D> cur = vt;
+  for (int c = 0; c < chunks; ++c) {
+    const int jc = j0 + c * kSplit;
+    if (jc >= jend) break;
+    // the next tile's loads go out before this one is reduced
+    VTile<D> nxt;
+    if (c + 1 < chunks)
+      v_tile_issue_at<D>(jc + kSplit, h, P, page_table, max_pages, vpool, num_pages, kv_heads,
+                         nxt);
+    if (wave < G) {
+      const float sj_raw =
+          c == 0 ? sj_first : S[(int64_t)(h * G + wg) * s_stride + jc + lane];
+      const float pj = (jc + lane < jend) ? rbf(expf(rbf(sj_raw - mw))) : 0.f;
+      p[wave][lane] = pj;
+      psum += wave_sum(pj);
+    }
+    __syncthreads();
 #pragma unroll
     for (int q = 0; q < A::kVPasses; ++q) {
       const int jj = jo + q * kGroups;
-      const bool bad = vt.pg[q] < 0 || vt.pg[q] >= num_pages;
-      if (j0 + jj < jend && bad) page_ok = false;
-      const u32x4 t = (j0 + jj < jend && !bad) ? vt.t[q] : u32x4{0u, 0u, 0u, 0u};
+      const bool bad = cur.pg[q] < 0 || cur.pg[q] >= num_pages;
+      if (jc + jj < jend && bad) page_ok = false;
+      const u32x4 t = (jc + jj < jend && !bad) ? cur.t[q] : u32x4{0u, 0u, 0u, 0u};
       const uint32_t vw[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -969,12 +1001,20 @@ __device__ __forceinline__ void attn_pv_phase(
         }
       }
     }
-    if (!page_ok) raise_error(err, kErrPageRange);
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) red[jo][g * D + ch * 8 + e] = acc[g][e];
+    __syncthreads();                        // p is rewritten by the next tile
+    if (c + 1 < chunks) cur = nxt;
   }
+  if (!page_ok) raise_error(err, kErrPageRange);
+  if (wave < G && lane == 0) {
+    if (kLL)
+      ll_put(ll.psum, (uint32_t)(split * heads + h * G + wave), __float_as_uint(psum), ll.tag);
+    else
+      coh_stf(&part_sum[split * heads + h * G + wave], psum);
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[jo][g * D + ch * 8 + e] = acc[g][e];
   __syncthreads();
   if (kLL) {
     for (int o = 2 * tid; o < kOut; o += 2 * kBlock) {

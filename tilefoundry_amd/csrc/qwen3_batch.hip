@@ -8,7 +8,7 @@
 // rows a projection is a real contraction (2 flops per weight byte per row), so
 // the VALU dot path would be compute-bound before HBM is.
 //
-// Kernels of one layer (Qwen3-1.7B at batch 32):
+// Kernels of one layer (workload C3: Qwen3-1.7B at batch 32):
 //   rmsnorm_rows                 x -> bf16 normalised rows
 //   gemm_skinny<STORE>           xn @ [q|k|v]^T            -> qkv   [B][HQ*D+2*HKV*D]
 //   attn_rope_scores_batched     per (split, kv head, sequence), as the batch-1 phase
@@ -17,6 +17,8 @@
 //   rmsnorm_rows, gemm_skinny<SWIGLU>, gemm_skinny<RESID> (down)
 // and per step: rmsnorm_rows (final), gemm_skinny<LOGITS> (bf16-valued f32
 // logits), argmax_rows, finalize_rows (pick, next token, position, embedding).
+
+#include <type_traits>
 
 #include "decode_phases.h"
 #include "host_common.h"
@@ -31,7 +33,6 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxRows = 32;      // one skinny GEMM covers two 16-row MFMA tiles
-constexpr int kSkSteps = 4;       // 32-wide k steps in flight per wave
 
 // ---------------------------------------------------------------------------
 // Row-wise RMSNorm (model.py:125-137 on each sequence's hidden state): one
@@ -56,93 +57,220 @@ __global__ __launch_bounds__(kWave) void k_rmsnorm_rows(const bf16* __restrict__
 }
 
 // ---------------------------------------------------------------------------
-// Skinny GEMM: Y[m][n] = sum_k X[m][k] W[n][k] for m < M <= 32.
-// A block owns one 16-column tile of Y (16 weight rows) for all rows; its four
-// waves split K in quarters, each accumulating two 16x16 MFMA tiles (rows 0-15
-// and 16-31) over 32-wide k steps, kSkSteps steps of loads in flight.  Operand
-// layout of v_mfma_f32_16x16x32_bf16: lane l holds A[l % 16][8 (l / 16) .. +7],
-// B[8 (l / 16) .. +7][l % 16], and gets D[4 (l / 16) .. +3][l % 16] -- so a lane
-// loads 16 contiguous bytes of one weight row and of one activation row.  The
-// quarters are summed in wave order through LDS; wave 0 applies the epilogue.
+// Skinny GEMM: Y[m][n] = sum_k X[m][k] W[n][k] for m < M <= 32, W packed in
+// MFMA order (k_pack_skinny).
+//
+// At 32 rows the weights are the only large operand (X is at most 32 x 6144
+// bf16), so the kernel keeps X stationary: a block stages its K slice of X
+// ([rows][Ks], rows = 16 or 32) in LDS once, and its eight waves then stream
+// 16-row tiles of W past it -- every weight byte is read once from HBM and X is
+// read from L2 once per block, not once per tile.  A wave owns whole tiles (all
+// Ks of them), so no cross-wave reduction is needed; with kDepth 32-wide k
+// steps (1 KiB per wave each) of weights in flight it crosses tile boundaries
+// without draining.  Blocks are persistent over a contiguous range of tiles.
+//
+// MFMA operand layout of v_mfma_f32_16x16x32_bf16: lane l holds
+// A[l % 16][8 (l / 16) .. +7], B[8 (l / 16) .. +7][l % 16] and gets
+// D[4 (l / 16) .. +3][l % 16]; A is X (rows) from LDS, B is W^T (16 bytes of one
+// weight row per lane).
+//
+// K is split into `slices` (grid.y) when there are too few tiles to fill the
+// chip (o and down: 128 tiles).  Each slice's wave stores its f32 tile in
+// fragment order (1 KiB per 16-row half, coalesced), bumps the tile's counter,
+// and the wave that arrives last adds the slices in slice order -- so the sum
+// does not depend on which slice finishes first -- applies the epilogue and
+// puts the counter back to zero for the next call.
 // ---------------------------------------------------------------------------
 enum SkinnyEpi { kSkStore = 0, kSkResid = 1, kSkSwiglu = 2, kSkLogits = 3 };
 
+// Two shapes: Ks <= 1024 (66 KiB of LDS, two blocks of four waves per compute
+// unit, eight steps in flight per wave) and Ks <= 2048 (the head: one block of
+// eight waves per compute unit, sixteen steps in flight per wave when Ks is a
+// multiple of 512).
+constexpr int kGxPad = 8;      // bf16 of padding per LDS row: rows start 16 bytes apart mod 256
+
+template <int kKsMax>
+constexpr int gx_lds_bytes() {
+  return 32 * (kKsMax + kGxPad) * 2;
+}
+
 template <int kEpi>
-__global__ __launch_bounds__(kBlock) void k_gemm_skinny(const bf16* __restrict__ X, int ldx,
-                                                        const bf16* __restrict__ W, int M, int K,
-                                                        int N, const bf16* __restrict__ resid,
-                                                        int ldr, void* __restrict__ out,
-                                                        int ldo) {
-  __shared__ f32x4 red[kWavesPerBlock][2][kWave];
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int n0 = blockIdx.x * 16;
+__device__ __forceinline__ void skinny_store(const f32x4 (&c)[2], int halves, int tile, int lane,
+                                             int M, int N, const bf16* __restrict__ resid,
+                                             int ldr, void* __restrict__ out, int ldo) {
   const int r = lane & 15, kq = lane >> 4;
-  const int nsteps = K / 32;
-  const int per = (nsteps + kWavesPerBlock - 1) / kWavesPerBlock;
-  const int s0 = wave * per;
-  const int s1 = (s0 + per < nsteps) ? s0 + per : nsteps;
-  // rows past M / N read row M-1 / N-1 (in bounds); their results are not stored
-  const bf16* wrow = W + (int64_t)((n0 + r < N) ? n0 + r : N - 1) * K + 8 * kq;
-  const bf16* xa = X + (int64_t)((r < M) ? r : M - 1) * ldx + 8 * kq;
-  const bf16* xb = X + (int64_t)((16 + r < M) ? 16 + r : M - 1) * ldx + 8 * kq;
-  f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
-  for (int s = s0; s < s1; s += kSkSteps) {
-    u32x4 b[kSkSteps], a0[kSkSteps], a1[kSkSteps];
-#pragma unroll
-    for (int u = 0; u < kSkSteps; ++u) {
-      const int k = ((s + u < s1) ? s + u : s1 - 1) * 32;
-      b[u] = load16_stream(wrow + k);
-      a0[u] = load16(xa + k);
-      a1[u] = load16(xb + k);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < kSkSteps; ++u) {
-      if (s + u < s1) {
-        const bf16x8_t bw = __builtin_bit_cast(bf16x8_t, b[u]);
-        c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a0[u]), bw, c0,
-                                                     0, 0, 0);
-        c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a1[u]), bw, c1,
-                                                     0, 0, 0);
-      }
-    }
-  }
-  red[wave][0][lane] = c0;
-  red[wave][1][lane] = c1;
-  __syncthreads();
-  if (wave != 0) return;
-  f32x4 t[2] = {red[0][0][lane], red[0][1][lane]};
-#pragma unroll
-  for (int w = 1; w < kWavesPerBlock; ++w) {
-    const f32x4 u0 = red[w][0][lane], u1 = red[w][1][lane];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      t[0][e] += u0[e];
-      t[1][e] += u1[e];
-    }
-  }
-  const int n = n0 + r;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  const int n = tile * 16 + r;
+  for (int h = 0; h < halves; ++h) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int m = 16 * h + 4 * kq + e;
-      const float y = rbf(t[h][e]);
+      const float y = rbf(c[h][e]);
       if (kEpi == kSkSwiglu) {
-        // gate at even columns, up at the odd column next to it (the next lane)
+        // (gate, up) pairs sit in adjacent columns: lanes r and r ^ 1
         const float u = __shfl_xor(y, 1, kWave);
         if ((r & 1) == 0 && m < M && n + 1 < N)
           ((bf16*)out)[(int64_t)m * ldo + n / 2] = f2bf(rbf(silu_f(y)) * u);
       } else if (m < M && n < N) {
-        if (kEpi == kSkStore) {
+        if (kEpi == kSkStore)
           ((bf16*)out)[(int64_t)m * ldo + n] = f2bf(y);
-        } else if (kEpi == kSkResid) {
+        else if (kEpi == kSkResid)
           ((bf16*)out)[(int64_t)m * ldo + n] = f2bf(bf2f(resid[(int64_t)m * ldr + n]) + y);
-        } else {
+        else
           ((float*)out)[(int64_t)m * ldo + n] = y;
-        }
       }
     }
+  }
+}
+
+// Weights in MFMA order: for 16-row tile t and 32-wide k step s, a 1 KiB block
+// at (t * K/32 + s) KiB whose 16 bytes at l * 16 are
+// W[16 t + l % 16][32 s + 8 (l / 16) .. +7] -- the B operand of lane l -- so
+// the GEMM's weight loads are whole contiguous KiBs.  Rows past N are zero.
+__global__ __launch_bounds__(kBlock) void k_pack_skinny(const bf16* __restrict__ W, int ldw,
+                                                        int N, int K, bf16* __restrict__ out,
+                                                        int64_t chunks) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= chunks) return;
+  const int l = (int)(i & 63);
+  const int64_t blk = i >> 6;
+  const int ks = K / 32;
+  const int64_t t = blk / ks;
+  const int st = (int)(blk % ks);
+  const int64_t row = t * 16 + (l & 15);
+  const u32x4 v = row < N ? load16(W + row * ldw + st * 32 + 8 * (l >> 4)) : u32x4{0u, 0u, 0u, 0u};
+  *reinterpret_cast<u32x4*>(out + i * 8) = v;
+}
+
+template <int kEpi, int kKsMax, int kWaves, int kDepth>
+__global__ __launch_bounds__(kWaves * kWave) void k_gemm_skinny(
+    const bf16* __restrict__ X, int ldx, const bf16* __restrict__ W, int M, int K, int N, int Ks,
+    const bf16* __restrict__ resid, int ldr, void* __restrict__ out, int ldo,
+    float* __restrict__ part, int* __restrict__ counters) {
+  constexpr int kThreads = kWaves * kWave;
+  __shared__ __align__(16) bf16 xs[32 * (kKsMax + kGxPad)];
+  const int lane = threadIdx.x & (kWave - 1);
+  // wave-uniform (scalar) so the tile and step loops branch on scalars
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int r = lane & 15, kq = lane >> 4;
+  const int halves = M > 16 ? 2 : 1;
+  const int slices = gridDim.y, slice = blockIdx.y;
+  const int kbase = slice * Ks;
+  const int ntiles = (N + 15) / 16;
+  const int t0 = (int)((int64_t)blockIdx.x * ntiles / gridDim.x);
+  const int t1 = (int)((int64_t)(blockIdx.x + 1) * ntiles / gridDim.x);
+  const int steps = Ks / 32;                 // a multiple of kDepth
+  const int first = t0 + wave;
+  const int ntw = first < t1 ? (t1 - first + kWaves - 1) / kWaves : 0;
+  const int stride = Ks + kGxPad;
+
+  // Load cursor over this wave's (tile, step) sequence in the packed weights:
+  // one step of one tile is 1 KiB, lane l's 16 bytes at l * 16 (a wave's load is
+  // contiguous).  A wave without tiles reads its block's first tile.
+  int lt = first < t1 ? first : (t0 < ntiles ? t0 : ntiles - 1), lk = 0;
+  const int ksteps = K / 32;
+  const bf16* wbase = W + (int64_t)(kbase / 32) * 512 + lane * 8;
+  auto load_next = [&]() {
+    const u32x4 v = load16_stream(wbase + ((int64_t)lt * ksteps + lk) * 512);
+    const bool wrap = lk + 1 == steps;
+    lk = wrap ? 0 : lk + 1;
+    lt = wrap ? lt + kWaves : lt;
+    return v;
+  };
+  u32x4 b[kDepth];
+#pragma unroll
+  for (int u = 0; u < kDepth; ++u) b[u] = load_next();   // in flight while X is staged
+  // X slice -> LDS, all 32 rows (rows past M are zero)
+  {
+    const int cpr = Ks / 8;                    // 16-byte chunks per row
+    const int nchunks = 32 * cpr;
+    constexpr int kB = 8;
+    for (int c0 = threadIdx.x; c0 < nchunks; c0 += kB * kThreads) {
+      u32x4 v[kB];
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int c = c0 + j * kThreads;
+        const int row = c / cpr, col = c % cpr;
+        v[j] = (c < nchunks && row < M) ? load16(X + (int64_t)row * ldx + kbase + col * 8)
+                                        : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        const int c = c0 + j * kThreads;
+        if (c < nchunks)
+          *reinterpret_cast<u32x4*>(&xs[(c / cpr) * stride + (c % cpr) * 8]) = v[j];
+      }
+    }
+  }
+  __syncthreads();
+
+  const bf16* xa = xs + r * stride + 8 * kq;
+  f32x4 c[2];
+  // kDepth steps from LDS x the weights in flight; with kRefill each slot is
+  // reloaded with the step kDepth ahead right behind its use (the wave's last
+  // chunk has nothing ahead, so it loads nothing)
+  auto chunk = [&](int k0, auto refill) {
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) {
+      const bf16* xk = xa + (k0 + u) * 32;
+      const bf16x8_t bw = __builtin_bit_cast(bf16x8_t, b[u]);
+      c[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_t*>(xk), bw,
+                                                     c[0], 0, 0, 0);
+      c[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          *reinterpret_cast<const bf16x8_t*>(xk + 16 * stride), bw, c[1], 0, 0, 0);
+      if (decltype(refill)::value) b[u] = load_next();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int t = 0; t < ntw; ++t) {
+    const int tile = first + t * kWaves;
+    c[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    c[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int kend = (t + 1 == ntw) ? steps - kDepth : steps;
+    for (int k0 = 0; k0 < kend; k0 += kDepth) chunk(k0, std::true_type{});
+    if (t + 1 == ntw) chunk(steps - kDepth, std::false_type{});
+    bool mine = true;
+    if (slices > 1) {
+      // this slice's tile in fragment order: [slice][tile][half][lane] x 16 bytes
+      const uint32_t own = ((uint32_t)(slice * ntiles + tile) * 2u) * 1024u + lane * 16u;
+      for (int h = 0; h < halves; ++h)
+        coh_st16(part, own + h * 1024u, __builtin_bit_cast(u32x4, c[h]));
+      stores_done();
+      int ticket = 0;
+      if (lane == 0) ticket = atomicAdd(&counters[tile], 1);
+      ticket = __shfl(ticket, 0, kWave);
+      mine = ticket == slices - 1;
+      if (mine) {
+        // the last arrival adds the slices in slice order (four at a time in
+        // flight) and re-arms the counter
+        f32x4 sum[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        for (int s0 = 0; s0 < slices; s0 += 4) {
+          u32x4 v[4][2];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int sl = s0 + j < slices ? s0 + j : slices - 1;
+            const uint32_t off = ((uint32_t)(sl * ntiles + tile) * 2u) * 1024u + lane * 16u;
+            v[j][0] = coh_ld16(part, off);
+            v[j][1] = coh_ld16(part, off + 1024u);   // written only when halves == 2
+          }
+          // every load is consumed (a select, not a branch), so none is left
+          // in flight into registers the next tile reuses
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bool valid = s0 + j < slices;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const f32x4 x = __builtin_bit_cast(f32x4, v[j][h]);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) sum[h][e] += valid ? x[e] : 0.f;
+            }
+          }
+        }
+        c[0] = sum[0];
+        c[1] = sum[1];
+        if (lane == 0) coh_sti(&counters[tile], 0);
+      }
+    }
+    if (mine) skinny_store<kEpi>(c, halves, tile, lane, M, N, resid, ldr, out, ldo);
   }
 }
 
@@ -158,21 +286,22 @@ __global__ __launch_bounds__(kBlock) void k_attn_scores_b(
     int rope_rows, const int* __restrict__ pos, const int* __restrict__ page_table, int max_pages,
     bf16* __restrict__ kpool, bf16* __restrict__ vpool, int num_pages, int kv_heads, float scale,
     float eps, float* __restrict__ S, int s_stride, float* __restrict__ smax,
-    float* __restrict__ snew, int* err) {
+    float* __restrict__ snew, int chunks, int* err) {
   const int b = blockIdx.z, heads = kv_heads * G, nsplit = gridDim.x;
   const int P = coh_ldi(pos + b);
   const int* pt = page_table + (int64_t)b * max_pages;
   KTile<D> kt;
-  k_tile_issue<D>(blockIdx.x, blockIdx.y, P, pt, max_pages, kpool, num_pages, kv_heads, kt);
+  k_tile_issue_at<D>(blockIdx.x * chunks * kSplit, blockIdx.y, P, pt, max_pages, kpool,
+                     num_pages, kv_heads, kt);
   const QKPre pre = qk_prefetch<D, G>(P, P, gq, gk, cos_t, sin_t, rope_rows, pt, max_pages);
   __shared__ __attribute__((aligned(16))) uint32_t hs[(G + 2) * D / 2];
   stage_head<D, G>(blockIdx.y, heads, kv_heads, qkv + (int64_t)b * ldq, hs);
   __syncthreads();
-  attn_scores_phase<D, G, false>(blockIdx.x, blockIdx.y, hs, pre, rope_rows, P, P, max_pages,
-                                 kpool, vpool, num_pages, kv_heads, scale, eps,
+  attn_scores_phase<D, G, false>(blockIdx.x, blockIdx.y, hs, pre, rope_rows, P, P, pt,
+                                 max_pages, kpool, vpool, num_pages, kv_heads, scale, eps,
                                  S + (int64_t)b * heads * s_stride, s_stride,
                                  smax + (int64_t)b * nsplit * heads, snew + (int64_t)b * heads,
-                                 AttnLL{}, kt, err);
+                                 AttnLL{}, kt, err, chunks);
 }
 
 template <int D, int G>
@@ -181,13 +310,14 @@ __global__ __launch_bounds__(kBlock) void k_attn_pv_b(
     const int* __restrict__ page_table, int max_pages, const bf16* __restrict__ vpool,
     int num_pages, int kv_heads, const float* __restrict__ S, int s_stride,
     const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
-    float* part_out, int* counters, bf16* __restrict__ attn_out, int lda, int* err) {
+    float* part_out, int* counters, bf16* __restrict__ attn_out, int lda, int chunks, int* err) {
   const int b = blockIdx.z, heads = kv_heads * G, nsplit = gridDim.x;
   int P = coh_ldi(pos + b);
   if (P < 0 || P >= max_pages * kPage) P = 0;
   const int* pt = page_table + (int64_t)b * max_pages;
   VTile<D> vt;
-  v_tile_issue<D>(blockIdx.x, blockIdx.y, P, pt, max_pages, vpool, num_pages, kv_heads, vt);
+  v_tile_issue_at<D>(blockIdx.x * chunks * kSplit, blockIdx.y, P, pt, max_pages, vpool,
+                     num_pages, kv_heads, vt);
   attn_pv_phase<D, G, false>(blockIdx.x, blockIdx.y, nsplit, qkv + (int64_t)b * ldq, P, pt,
                              max_pages, vpool, num_pages, kv_heads,
                              S + (int64_t)b * heads * s_stride, s_stride,
@@ -195,7 +325,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_pv_b(
                              part_sum + (int64_t)b * nsplit * heads,
                              part_out + (int64_t)b * nsplit * heads * D,
                              counters + (int64_t)b * kv_heads, attn_out + (int64_t)b * lda,
-                             AttnLL{}, vt, err);
+                             AttnLL{}, vt, err, chunks);
 }
 
 // ---------------------------------------------------------------------------
@@ -312,42 +442,126 @@ int tfd_rmsnorm_rows_bf16(const void* x, int ldx, const void* gamma, void* out, 
   return launched("rmsnorm_rows");
 }
 
+}  // extern "C"
+
+namespace {
+
+// Launch shape of one skinny GEMM.  K is split into a power-of-two number of
+// slices until there are at least four tile-slices per compute unit (each slice
+// a multiple of 256 deep and at most 2048, the LDS stage); blocks are
+// persistent over tiles, one or two per compute unit.
+struct SkinnyPlan {
+  int slices, Ks, blocks_per_slice;
+  bool wide;                // Ks > 1024: the 2048-deep LDS stage
+  int64_t work_floats;      // counters + partials
+};
+
+int compute_units() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// The work buffer starts with kSkCounters tile counters (zero before first use;
+// every call leaves the ones it used at zero) at a fixed place, so GEMMs of
+// different shapes can share one buffer; the f32 partials follow.
+constexpr int kSkCounters = TFD_SKINNY_COUNTERS;
+
+int64_t skinny_work(int ntiles, int slices) {
+  return slices == 1 ? 0 : (int64_t)kSkCounters + (int64_t)slices * ntiles * 512;
+}
+
+SkinnyPlan skinny_plan(int K, int N, int64_t work_floats) {
+  const int ntiles = (N + 15) / 16;
+  const int cus = compute_units();
+  int s = 1;
+  while (K / s > 2048 && K % (512 * s) == 0) s *= 2;
+  while ((int64_t)ntiles * s < 4 * cus && K % (512 * s) == 0) s *= 2;
+  while (s > 1 && (skinny_work(ntiles, s) > work_floats || ntiles > kSkCounters)) s /= 2;
+  SkinnyPlan p;
+  p.slices = s;
+  p.Ks = K / s;
+  p.wide = p.Ks > 1024;
+  const int per_cu = p.wide ? 1 : 2;
+  const int waves = p.wide ? 8 : 4;
+  int64_t bps = ((int64_t)ntiles + waves - 1) / waves;
+  const int64_t cap = ((int64_t)per_cu * cus + s - 1) / s;
+  if (bps > cap) bps = cap;
+  p.blocks_per_slice = (int)(bps < 1 ? 1 : bps);
+  p.work_floats = skinny_work(ntiles, s);
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tfd_pack_skinny_bf16(const void* w, int ldw, int N, int K, void* packed, void* stream) {
+  if (!w || !packed) return fail(kBadArg, "pack_skinny: null pointer");
+  if (N <= 0 || K <= 0 || K % 256 || ldw < K || ldw % 8)
+    return fail(kBadShape, "pack_skinny: N=%d K=%d (multiple of 256) ldw=%d", N, K, ldw);
+  const int64_t chunks = (int64_t)(N + 15) / 16 * (K / 32) * 64;
+  hipLaunchKernelGGL(k_pack_skinny, dim3((unsigned)((chunks + kBlock - 1) / kBlock)),
+                     dim3(kBlock), 0, (hipStream_t)stream, (const bf16*)w, ldw, N, K,
+                     (bf16*)packed, chunks);
+  return launched("pack_skinny");
+}
+
 int tfd_gemm_skinny_bf16(const void* x, int ldx, const void* w, int M, int K, int N,
                          int epilogue, const void* resid, int ldr, void* out, int ldo,
-                         void* stream) {
+                         float* work, int64_t work_floats, void* stream) {
   if (!x || !w || !out) return fail(kBadArg, "gemm_skinny: null pointer");
-  if (M <= 0 || M > kMaxRows || K <= 0 || K % 32 || N <= 0 || ldx < K || ldx % 8)
-    return fail(kBadShape, "gemm_skinny: M=%d (1..32) K=%d (multiple of 32) N=%d ldx=%d", M, K,
-                N, ldx);
+  if (M <= 0 || M > kMaxRows || K <= 0 || K % 256 || N <= 0 || ldx < K || ldx % 8)
+    return fail(kBadShape, "gemm_skinny: M=%d (1..32) K=%d (multiple of 256) N=%d ldx=%d", M,
+                K, N, ldx);
   if (epilogue == TFD_EPI_RESID && (!resid || ldr < N))
     return fail(kBadArg, "gemm_skinny: residual epilogue needs resid with ldr >= N");
   if (epilogue == TFD_EPI_SWIGLU ? (N % 2 || ldo < N / 2) : ldo < N)
     return fail(kBadShape, "gemm_skinny: ldo=%d too small for N=%d", ldo, N);
-  const dim3 grid((N + 15) / 16);
+  if (work_floats < 0 || (work_floats > 0 && !work))
+    return fail(kBadArg, "gemm_skinny: work=%p with %lld floats", (void*)work,
+                (long long)work_floats);
+  const SkinnyPlan plan = skinny_plan(K, N, work ? work_floats : 0);
+  if (plan.Ks > 2048 || plan.Ks % 256)
+    return fail(kBadShape, "gemm_skinny: K=%d needs slices of at most 2048 (multiples of 256); "
+                "a work buffer of %lld floats allows %d", K, (long long)plan.work_floats,
+                plan.slices);
+  if ((int64_t)plan.slices * ((N + 15) / 16) * 2048 >= ((int64_t)1 << 31))
+    return fail(kBadShape, "gemm_skinny: N=%d with %d K slices", N, plan.slices);
+  int* counters = plan.slices > 1 ? (int*)work : nullptr;
+  float* part = plan.slices > 1 ? work + kSkCounters : nullptr;
+  const dim3 grid(plan.blocks_per_slice, plan.slices);
   auto s = (hipStream_t)stream;
   auto xb = (const bf16*)x;
   auto wb = (const bf16*)w;
   auto rb = (const bf16*)resid;
+#define TFD_SKINNY_LAUNCH(EPI)                                                                \
+  if (plan.wide && plan.Ks % 512 == 0)                                                        \
+    hipLaunchKernelGGL((k_gemm_skinny<EPI, 2048, 8, 16>), grid, dim3(8 * kWave), 0, s, xb,    \
+                       ldx, wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);         \
+  else if (plan.wide)                                                                         \
+    hipLaunchKernelGGL((k_gemm_skinny<EPI, 2048, 8, 8>), grid, dim3(8 * kWave), 0, s, xb,     \
+                       ldx, wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);         \
+  else                                                                                        \
+    hipLaunchKernelGGL((k_gemm_skinny<EPI, 1024, 4, 8>), grid, dim3(4 * kWave), 0, s, xb,     \
+                       ldx, wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);
   switch (epilogue) {
-    case TFD_EPI_STORE:
-      hipLaunchKernelGGL(k_gemm_skinny<kSkStore>, grid, dim3(kBlock), 0, s, xb, ldx, wb, M, K, N,
-                         rb, ldr, out, ldo);
-      break;
-    case TFD_EPI_RESID:
-      hipLaunchKernelGGL(k_gemm_skinny<kSkResid>, grid, dim3(kBlock), 0, s, xb, ldx, wb, M, K, N,
-                         rb, ldr, out, ldo);
-      break;
-    case TFD_EPI_SWIGLU:
-      hipLaunchKernelGGL(k_gemm_skinny<kSkSwiglu>, grid, dim3(kBlock), 0, s, xb, ldx, wb, M, K,
-                         N, rb, ldr, out, ldo);
-      break;
-    case TFD_EPI_LOGITS:
-      hipLaunchKernelGGL(k_gemm_skinny<kSkLogits>, grid, dim3(kBlock), 0, s, xb, ldx, wb, M, K,
-                         N, rb, ldr, out, ldo);
-      break;
+    case TFD_EPI_STORE: TFD_SKINNY_LAUNCH(kSkStore); break;
+    case TFD_EPI_RESID: TFD_SKINNY_LAUNCH(kSkResid); break;
+    case TFD_EPI_SWIGLU: TFD_SKINNY_LAUNCH(kSkSwiglu); break;
+    case TFD_EPI_LOGITS: TFD_SKINNY_LAUNCH(kSkLogits); break;
     default:
       return fail(kBadArg, "gemm_skinny: epilogue %d", epilogue);
   }
+#undef TFD_SKINNY_LAUNCH
   return launched("gemm_skinny");
 }
 
@@ -356,15 +570,16 @@ int tfd_attn_rope_scores_paged_batched(
     const void* sin_table, int rope_rows, const int32_t* pos, const int32_t* page_table,
     int max_pages, void* k_pool, void* v_pool, int num_pages, int batch, int heads, int kv_heads,
     int head_dim, float scale, float eps, float* scores, int score_stride, float* split_max,
-    float* score_new, int nsplit, int32_t* err, void* stream) {
+    float* score_new, int nsplit, int split_tiles, int32_t* err, void* stream) {
   if (!qkv || !gamma_q || !gamma_k || !cos_table || !sin_table || !pos || !page_table ||
       !k_pool || !v_pool || !scores || !split_max || !score_new)
     return fail(kBadArg, "attn_rope_scores_batched: null pointer");
   if (batch <= 0 || batch > 65535 || kv_heads <= 0 || heads % kv_heads || nsplit <= 0 ||
-      max_pages <= 0 || num_pages <= 0)
-    return fail(kBadShape, "attn_rope_scores_batched: batch=%d heads=%d kv_heads=%d nsplit=%d",
-                batch, heads, kv_heads, nsplit);
-  if ((int64_t)nsplit * kSplit < (int64_t)max_pages * kPage || score_stride < nsplit * kSplit ||
+      max_pages <= 0 || num_pages <= 0 || split_tiles <= 0)
+    return fail(kBadShape, "attn_rope_scores_batched: batch=%d heads=%d kv_heads=%d nsplit=%d "
+                "split_tiles=%d", batch, heads, kv_heads, nsplit, split_tiles);
+  const int64_t slen = (int64_t)split_tiles * kSplit;
+  if (nsplit * slen < (int64_t)max_pages * kPage || score_stride < nsplit * slen ||
       ldq < (heads + 2 * kv_heads) * head_dim)
     return fail(kBadShape, "attn_rope_scores_batched: nsplit=%d / score_stride=%d / ldq=%d do "
                 "not cover the cache", nsplit, score_stride, ldq);
@@ -376,7 +591,8 @@ int tfd_attn_rope_scores_paged_batched(
                          ldq, (const bf16*)gamma_q, (const bf16*)gamma_k,
                          (const bf16*)cos_table, (const bf16*)sin_table, rope_rows, pos,
                          page_table, max_pages, (bf16*)k_pool, (bf16*)v_pool, num_pages,
-                         kv_heads, scale, eps, scores, score_stride, split_max, score_new, err));
+                         kv_heads, scale, eps, scores, score_stride, split_max, score_new,
+                         split_tiles, err));
   return launched("attn_rope_scores_batched");
 }
 
@@ -384,16 +600,17 @@ int tfd_attn_pv_combine_paged_batched(
     const void* qkv, int ldq, const int32_t* pos, const int32_t* page_table, int max_pages,
     const void* v_pool, int num_pages, int batch, int heads, int kv_heads, int head_dim,
     const float* scores, int score_stride, const float* split_max, const float* score_new,
-    float* part_sum, float* part_out, int nsplit, int32_t* counters, void* attn_out, int lda,
-    int32_t* err, void* stream) {
+    float* part_sum, float* part_out, int nsplit, int split_tiles, int32_t* counters,
+    void* attn_out, int lda, int32_t* err, void* stream) {
   if (!qkv || !pos || !page_table || !v_pool || !scores || !split_max || !score_new ||
       !part_sum || !part_out || !counters || !attn_out)
     return fail(kBadArg, "attn_pv_combine_batched: null pointer");
   if (batch <= 0 || batch > 65535 || kv_heads <= 0 || heads % kv_heads || nsplit <= 0 ||
-      max_pages <= 0 || num_pages <= 0 || lda < heads * head_dim)
+      max_pages <= 0 || num_pages <= 0 || lda < heads * head_dim || split_tiles <= 0)
     return fail(kBadShape, "attn_pv_combine_batched: batch=%d heads=%d kv_heads=%d nsplit=%d "
-                "lda=%d", batch, heads, kv_heads, nsplit, lda);
-  if ((int64_t)nsplit * kSplit < (int64_t)max_pages * kPage || score_stride < nsplit * kSplit)
+                "lda=%d split_tiles=%d", batch, heads, kv_heads, nsplit, lda, split_tiles);
+  const int64_t slen = (int64_t)split_tiles * kSplit;
+  if (nsplit * slen < (int64_t)max_pages * kPage || score_stride < nsplit * slen)
     return fail(kBadShape, "attn_pv_combine_batched: nsplit=%d does not cover the cache", nsplit);
   const int G = heads / kv_heads;
   const dim3 grid(nsplit, kv_heads, batch);
@@ -402,7 +619,7 @@ int tfd_attn_pv_combine_paged_batched(
       hipLaunchKernelGGL((k_attn_pv_b<kD, kG>), grid, dim3(kBlock), 0, s, (const bf16*)qkv, ldq,
                          pos, page_table, max_pages, (const bf16*)v_pool, num_pages, kv_heads,
                          scores, score_stride, split_max, score_new, part_sum, part_out,
-                         counters, (bf16*)attn_out, lda, err));
+                         counters, (bf16*)attn_out, lda, split_tiles, err));
   return launched("attn_pv_combine_batched");
 }
 

@@ -125,9 +125,9 @@ __global__ __launch_bounds__(kBlock) void k_attn_rope_scores(
   __shared__ __attribute__((aligned(16))) uint32_t hs[(G + 2) * D / 2];
   stage_head<D, G>(blockIdx.y, kv_heads * G, kv_heads, qkv, hs);
   __syncthreads();
-  attn_scores_phase<D, G, false>(blockIdx.x, blockIdx.y, hs, pre, rope_rows, rp, P, max_pages,
-                                 kpool, vpool, num_pages, kv_heads, scale, eps, S, s_stride, smax,
-                                 snew, AttnLL{}, kt, err);
+  attn_scores_phase<D, G, false>(blockIdx.x, blockIdx.y, hs, pre, rope_rows, rp, P, page_table,
+                                 max_pages, kpool, vpool, num_pages, kv_heads, scale, eps, S,
+                                 s_stride, smax, snew, AttnLL{}, kt, err);
 }
 
 template <int D, int G>
@@ -323,10 +323,10 @@ __global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, i
         __syncthreads();
         if (vb == vb0) stamp(tl);
         const int lv = (vb - vb0) / nb;
-        attn_scores_phase<D, G, true>(split, h, hs, pre, a.rope_rows, P, P, a.max_pages,
-                                      (bf16*)w.k_pool, (bf16*)w.v_pool, a.num_pages, a.kv_heads,
-                                      a.scale, eps, s_sc[lv], 0, nullptr, s_new[lv], ll, kt,
-                                      err);
+        attn_scores_phase<D, G, true>(split, h, hs, pre, a.rope_rows, P, P, a.page_table,
+                                      a.max_pages, (bf16*)w.k_pool, (bf16*)w.v_pool,
+                                      a.num_pages, a.kv_heads, a.scale, eps, s_sc[lv], 0,
+                                      nullptr, s_new[lv], ll, kt, err);
         if (vb == vb0) stamp(tl);
       }
       // ---- part 2: P.V partials

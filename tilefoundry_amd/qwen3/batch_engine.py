@@ -1,4 +1,4 @@
-"""Batched decode: up to 32 sequences advance one token per step.
+"""Batched decode: up to 32 sequences advance one token per step (workload C3).
 
 The batch-1 engine's structure (``engine.py``; the reference's
 ``examples/qwen3_1_7b-tilelang/fast/engine.py:69-301``) with a batch axis:
@@ -54,7 +54,9 @@ class BatchEngine:
 
     def __init__(self, cfg: Qwen3Config, weights: dict[str, torch.Tensor], *, batch: int,
                  device: str = "cuda:0", max_new: int = 256, prompt_room: int = 4096,
-                 page_seed: int | None = 0, graph: bool = True):
+                 page_seed: int | None = 0, graph: bool = True, split_tiles: int | None = None):
+        """*split_tiles*: 64-position tiles per attention split (default: about 16
+        splits per sequence and kv head at full capacity)."""
         if cfg.dtype != torch.bfloat16:
             raise ValueError(f"the HIP engine runs bf16 weights; config has {cfg.dtype}")
         if not 1 <= batch <= MAX_BATCH:
@@ -73,7 +75,12 @@ class BatchEngine:
         self.nsteps = max_new + prompt_room
         self.cap = _round_up(self.nsteps, _lib.ATTN_SPLIT)
         self.max_pages = self.cap // _lib.PAGE_SIZE
-        self.nsplit = self.cap // _lib.ATTN_SPLIT
+        tiles = self.cap // _lib.ATTN_SPLIT
+        self.split_tiles = split_tiles or max(1, round(tiles / 16))
+        if self.split_tiles < 1:
+            raise ValueError(f"split_tiles must be positive, got {split_tiles}")
+        self.nsplit = -(-tiles // self.split_tiles)
+        self.score_stride = self.nsplit * self.split_tiles * _lib.ATTN_SPLIT
         if self.cap > cfg.max_position_embeddings:
             raise ValueError(f"capacity {self.cap} exceeds the rope table "
                              f"({cfg.max_position_embeddings} positions)")
@@ -87,8 +94,14 @@ class BatchEngine:
     # ---------------------------------------------------------------- setup
     def _pack(self, weights, page_seed):
         dev = self.device
-        self.layers = [pack_layer(weights, i, dev) for i in range(self.L)]
-        self.w_embed, self.w_head = head_rows(weights, dev)
+        self.layers = []
+        for i in range(self.L):
+            layer = pack_layer(weights, i, dev)
+            for n in ("w_qkv", "w_o", "w_gu", "w_down"):
+                layer[n] = self._mfma_order(layer[n])
+            self.layers.append(layer)
+        self.w_embed, head = head_rows(weights, dev)
+        self.w_head = self._mfma_order(head)
         self.gamma_final = weights["gamma_final"].to(dev).contiguous()
         d = self.D
         inv = 1.0 / (self.cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
@@ -103,6 +116,15 @@ class BatchEngine:
             g = torch.Generator().manual_seed(page_seed)
             table = torch.randperm(self.num_pages, generator=g).to(torch.int32)
         self.page_table = table.view(self.B, self.max_pages).to(dev).contiguous()
+
+    def _mfma_order(self, w: torch.Tensor) -> torch.Tensor:
+        """[N][K] row-major weights -> the skinny GEMM's 1 KiB operand blocks."""
+        N, K = w.shape
+        out = torch.empty(-(-N // 16) * 16, K, device=w.device, dtype=w.dtype)
+        self._lib.tfd_pack_skinny_bf16(ptr(w), K, N, K, ptr(out),
+                                       torch.cuda.current_stream(w.device).cuda_stream)
+        torch.cuda.synchronize(w.device)
+        return out
 
     def _buffers(self):
         dev, bf, f32, i32 = self.device, torch.bfloat16, torch.float32, torch.int32
@@ -120,7 +142,7 @@ class BatchEngine:
         self.hmid = z(B, self.I)
         self.kpool = z(self.L, self.num_pages, self.HKV, _lib.PAGE_SIZE, self.D)
         self.vpool = z(self.L, self.num_pages, self.HKV, _lib.PAGE_SIZE, self.D)
-        self.scores = z(B, self.HQ, self.cap, dtype=f32)
+        self.scores = z(B, self.HQ, self.score_stride, dtype=f32)
         self.smax = z(B, self.nsplit, self.HQ, dtype=f32)
         self.snew = z(B, self.HQ, dtype=f32)
         self.psum = z(B, self.nsplit, self.HQ, dtype=f32)
@@ -134,11 +156,21 @@ class BatchEngine:
         self.sam = z(B, self.nsteps, dtype=i32)
         self.plen = z(B, dtype=i32)
         self.err = z(1, dtype=i32)
+        # skinny-GEMM work: tile counters (kept at zero by the library) and the
+        # f32 partial tiles of GEMMs that split K; 8 MiB covers every projection
+        self.work = z(1 << 21, dtype=f32)
 
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
 
     # ---------------------------------------------------------------- the step
+    def _gemm(self, x, ldx, w, K, N, epi, resid, out, ldo, s):
+        """out = epi(x @ w^T) for the batch's rows (model.py:160-171 and friends)."""
+        self._lib.tfd_gemm_skinny_bf16(ptr(x), ldx, ptr(w), self.B, K, N, epi,
+                                       None if resid is None else ptr(resid),
+                                       0 if resid is None else resid.shape[-1], ptr(out), ldo,
+                                       ptr(self.work), self.work.numel(), s)
+
     def _layer(self, i: int, s: int):
         """One decoder layer (model.py:236-266) for every sequence."""
         L, w = self._lib, self.layers[i]
@@ -146,27 +178,26 @@ class BatchEngine:
         x_in, x_out = self.hid_rows[i], self.hid_rows[i + 1]
         L.tfd_rmsnorm_rows_bf16(ptr(x_in), H, ptr(w["gamma_in"]), ptr(self.xn), H, B, H,
                                 self.eps, s)
-        L.tfd_gemm_skinny_bf16(ptr(self.xn), H, ptr(w["w_qkv"]), B, H, self.qkv_n,
-                               _lib.EPI_STORE, None, 0, ptr(self.qkv), self.qkv_n, s)
+        self._gemm(self.xn, H, w["w_qkv"], H, self.qkv_n, _lib.EPI_STORE, None, self.qkv,
+                   self.qkv_n, s)
         L.tfd_attn_rope_scores_paged_batched(
             ptr(self.qkv), self.qkv_n, ptr(w["gamma_q"]), ptr(w["gamma_k"]), ptr(self.cos),
             ptr(self.sin), self.cap, ptr(self.pos), ptr(self.page_table), self.max_pages,
             ptr(self.kpool[i]), ptr(self.vpool[i]), self.num_pages, B, self.HQ, self.HKV, D,
-            self.scale, self.eps, ptr(self.scores), self.cap, ptr(self.smax), ptr(self.snew),
-            self.nsplit, ptr(self.err), s)
+            self.scale, self.eps, ptr(self.scores), self.score_stride, ptr(self.smax),
+            ptr(self.snew), self.nsplit, self.split_tiles, ptr(self.err), s)
         L.tfd_attn_pv_combine_paged_batched(
             ptr(self.qkv), self.qkv_n, ptr(self.pos), ptr(self.page_table), self.max_pages,
             ptr(self.vpool[i]), self.num_pages, B, self.HQ, self.HKV, D, ptr(self.scores),
-            self.cap, ptr(self.smax), ptr(self.snew), ptr(self.psum), ptr(self.pout),
-            self.nsplit, ptr(self.counters), ptr(self.attn), self.QD, ptr(self.err), s)
-        L.tfd_gemm_skinny_bf16(ptr(self.attn), self.QD, ptr(w["w_o"]), B, self.QD, H,
-                               _lib.EPI_RESID, ptr(x_in), H, ptr(self.h1), H, s)
+            self.score_stride, ptr(self.smax), ptr(self.snew), ptr(self.psum), ptr(self.pout),
+            self.nsplit, self.split_tiles, ptr(self.counters), ptr(self.attn), self.QD,
+            ptr(self.err), s)
+        self._gemm(self.attn, self.QD, w["w_o"], self.QD, H, _lib.EPI_RESID, x_in, self.h1, H,
+                   s)
         L.tfd_rmsnorm_rows_bf16(ptr(self.h1), H, ptr(w["gamma_post"]), ptr(self.xn), H, B, H,
                                 self.eps, s)
-        L.tfd_gemm_skinny_bf16(ptr(self.xn), H, ptr(w["w_gu"]), B, H, 2 * I, _lib.EPI_SWIGLU,
-                               None, 0, ptr(self.hmid), I, s)
-        L.tfd_gemm_skinny_bf16(ptr(self.hmid), I, ptr(w["w_down"]), B, I, H, _lib.EPI_RESID,
-                               ptr(self.h1), H, ptr(x_out), H, s)
+        self._gemm(self.xn, H, w["w_gu"], H, 2 * I, _lib.EPI_SWIGLU, None, self.hmid, I, s)
+        self._gemm(self.hmid, I, w["w_down"], I, H, _lib.EPI_RESID, self.h1, x_out, H, s)
 
     def _step(self):
         s = self._stream()
@@ -175,8 +206,8 @@ class BatchEngine:
         L, B, H = self._lib, self.B, self.H
         L.tfd_rmsnorm_rows_bf16(ptr(self.hid_rows[self.L]), H, ptr(self.gamma_final),
                                 ptr(self.xn), H, B, H, self.eps, s)
-        L.tfd_gemm_skinny_bf16(ptr(self.xn), H, ptr(self.w_head), B, H, self.V,
-                               _lib.EPI_LOGITS, None, 0, ptr(self.logits), self.V, s)
+        self._gemm(self.xn, H, self.w_head, H, self.V, _lib.EPI_LOGITS, None, self.logits,
+                   self.V, s)
         L.tfd_argmax_rows(ptr(self.logits), self.V, B, self.V, ptr(self.pick), s)
         L.tfd_finalize_rows(ptr(self.pick), B, ptr(self.inp), self.nsteps, ptr(self.plen),
                             ptr(self.ids), ptr(self.pos), ptr(self.sam), self.nsteps,

@@ -3,7 +3,7 @@
 The reference builds its model from the checkpoint's own ``config.json`` through
 Hugging Face's ``Qwen3Config`` (``examples/qwen3_1_7b-tilelang/ref_src/model.py:67-73``;
 "a published dimension is published, never derived").  ``from_json`` does the
-same from the dict, and the presets restate BASELINE's configs 1 and 2.
+same from the dict, and the presets restate the benchmark's configs C1 and C2.
 """
 from __future__ import annotations
 
@@ -92,11 +92,11 @@ class Qwen3Config:
         return replace(self, **kw)
 
 
-#: BASELINE config 1 -- tiny Qwen3-style decoder (fp32, CPU plumbing).
+#: Workload C1 -- tiny Qwen3-style decoder (fp32, CPU plumbing).
 TINY = Qwen3Config(hidden_size=256, num_attention_heads=4, num_key_value_heads=2, head_dim=64,
                    intermediate_size=768, vocab_size=4096, num_hidden_layers=2,
                    dtype=torch.float32)
-#: BASELINE config 2 -- the Qwen3-1.7B architecture (ref_src/config.json), bf16.
+#: Workload C2 -- the Qwen3-1.7B architecture (ref_src/config.json), bf16.
 QWEN3_1_7B = Qwen3Config(hidden_size=2048, num_attention_heads=16, num_key_value_heads=8,
                          head_dim=128, intermediate_size=6144, vocab_size=151936,
                          num_hidden_layers=28)
