@@ -244,8 +244,7 @@ def bench_c3(args) -> int:
             ptr(eng.qkv), eng.qkv_n, ptr(eng.pos), ptr(eng.page_table), eng.max_pages,
             ptr(eng.vpool[0]), eng.num_pages, batch, eng.HQ, eng.HKV, eng.D, ptr(eng.scores),
             eng.score_stride, ptr(eng.smax), ptr(eng.snew), ptr(eng.psum), ptr(eng.pout),
-            eng.nsplit, eng.split_tiles, ptr(eng.counters), ptr(eng.attn), eng.QD,
-            ptr(eng.err), s)
+            eng.nsplit, eng.split_tiles, ptr(eng.counters), ptr(eng.attn), ptr(eng.err), s)
 
     def time_it(fn):
         fn()

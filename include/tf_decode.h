@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TFD_ABI_VERSION 7
+#define TFD_ABI_VERSION 8
 
 /* gemv prologues / epilogues */
 #define TFD_PRO_PLAIN 0  /* x used as given */
@@ -128,13 +128,19 @@ int tfd_attn_pv_combine_paged(const void* qkv, const int32_t* cache_len,
                               void* stream);
 
 /* ---- batched decode (workload C3: up to 32 sequences per step) -------
- * Activations are row-major [rows][n] with leading dimensions; each sequence has
- * its own position (pos[b]) and page-table row (page_table + b * max_pages). */
+ * Row activations are row-major [rows][n] with leading dimensions; each sequence
+ * has its own position (pos[b]) and page-table row (page_table + b * max_pages).
+ * Activations that feed a skinny GEMM (normalised rows, attention output, SwiGLU
+ * output) are kept in OPERAND ORDER instead: 32 rows x K bf16 where, for 32-wide k
+ * step s and 16-row half h, the 1 KiB block at (2s + h) KiB holds at byte l * 16
+ * X[16h + l % 16][32s + 8(l / 16) .. +7] (rows past the batch are never written).
+ * This layout is internal to the batched path. */
 
 /* Row-wise Qwen3 RMSNorm of `rows` vectors of n values (input_rms_norm per
- * sequence, ref_src/model.py:125-137).  n % 8 == 0, n <= 8192. */
+ * sequence, ref_src/model.py:125-137).  n % 8 == 0, n <= 8192.  packed != 0: `out`
+ * is in operand order (rows <= 32, n % 32 == 0; ldo unused). */
 int tfd_rmsnorm_rows_bf16(const void* x, int ldx, const void* gamma, void* out, int ldo,
-                          int rows, int n, float eps, void* stream);
+                          int rows, int n, float eps, int packed, void* stream);
 
 /* Weights [N][K] (row stride ldw) re-laid for tfd_gemm_skinny_bf16: 16-row x 32-k
  * blocks of 1 KiB in the matrix cores' operand order, rows padded with zeros to a
@@ -145,20 +151,23 @@ int tfd_rmsnorm_rows_bf16(const void* x, int ldx, const void* gamma, void* out, 
 int tfd_pack_skinny_bf16(const void* w, int ldw, int N, int K, void* packed, void* stream);
 
 /* Skinny GEMM on the matrix cores: Y[m][n] = sum_k X[m][k] W[n][k] for m < M <= 32,
- * W packed by tfd_pack_skinny_bf16 (the q/k/v, o, gate/up, down and head projections of a batch, ref_src/model.py:160-171,
- * 213-215, 230-234, 300-305, at M = batch; it replaces fast/kernels.py:123-145 / 260-321
- * at batch > 1).  f32 accumulation, one rounding per output; epilogue TFD_EPI_STORE /
- * RESID (resid [M][ldr]) / SWIGLU (out [M][N/2]) / LOGITS (out f32).
- * K % 256 == 0.  `work` (work_floats f32 values; NULL with 0 allowed when K <= 2048)
- * lets the library split K into slices: it begins with TFD_SKINNY_COUNTERS int32 tile
- * counters, zero before the first call (every call leaves them at zero), followed by
- * f32 partials of slices * ceil(N/16) * 512 floats; the last wave to finish a tile
- * adds its slices in slice order.  A smaller buffer means fewer slices; K > 2048 needs
- * at least K/2048 of them.  Calls sharing one buffer must be stream-ordered. */
+ * X in operand order (32 x K), W packed by tfd_pack_skinny_bf16 -- the q/k/v, o,
+ * gate/up, down and head projections of a batch (ref_src/model.py:160-171, 213-215,
+ * 230-234, 300-305 at M = batch; it replaces fast/kernels.py:123-145 / 260-321 at
+ * batch > 1).  f32 accumulation, one rounding per output; epilogue TFD_EPI_STORE (out
+ * [M][ldo]) / RESID (resid [M][ldr], out [M][ldo]) / SWIGLU (out [M][N/2] in operand
+ * order, N/2 % 32 == 0; it feeds the down projection) / LOGITS (out f32 [M][ldo]).
+ * K % 256 == 0.  Few-tile shapes (N/16 under four per compute unit, or K > 2048) split
+ * K across the waves of a block and need no work buffer.  The others may split K
+ * across blocks when `work` (work_floats f32 values, NULL with 0 allowed) permits: it
+ * begins with TFD_SKINNY_COUNTERS int32 tile counters, zero before the first call
+ * (every call leaves them at zero), followed by f32 partials of slices * ceil(N/16) *
+ * 512 floats; the last wave to finish a tile adds its slices in slice order.  Calls
+ * sharing one buffer must be stream-ordered. */
 #define TFD_SKINNY_COUNTERS 16384
-int tfd_gemm_skinny_bf16(const void* x, int ldx, const void* w, int M, int K, int N,
-                         int epilogue, const void* resid, int ldr, void* out, int ldo,
-                         float* work, int64_t work_floats, void* stream);
+int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int epilogue,
+                         const void* resid, int ldr, void* out, int ldo, float* work,
+                         int64_t work_floats, void* stream);
 
 /* tfd_attn_rope_scores_paged for `batch` sequences at once (grid nsplit x kv_heads x
  * batch): sequence b reads QKV row b (stride ldq) at its own position pos[b] and
@@ -171,8 +180,9 @@ int tfd_attn_rope_scores_paged_batched(
     int head_dim, float scale, float eps, float* scores, int score_stride, float* split_max,
     float* score_new, int nsplit, int split_tiles, int32_t* err, void* stream);
 
-/* tfd_attn_pv_combine_paged for `batch` sequences (counters: batch x kv_heads, zero;
- * output row b at attn_out + b * lda).  A split covers split_tiles x 64 positions in
+/* tfd_attn_pv_combine_paged for `batch` <= 32 sequences (counters: batch x kv_heads,
+ * zero; the output rows go to attn_out in operand order, 32 x heads * head_dim, for
+ * the o projection).  A split covers split_tiles x 64 positions in
  * both entries (long contexts: fewer, longer splits; one tile's loads are in flight
  * while the previous one is reduced); nsplit x split_tiles x 64 >= max_pages x 16. */
 int tfd_attn_pv_combine_paged_batched(
@@ -180,7 +190,7 @@ int tfd_attn_pv_combine_paged_batched(
     const void* v_pool, int num_pages, int batch, int heads, int kv_heads, int head_dim,
     const float* scores, int score_stride, const float* split_max, const float* score_new,
     float* part_sum, float* part_out, int nsplit, int split_tiles, int32_t* counters,
-    void* attn_out, int lda, int32_t* err, void* stream);
+    void* attn_out, int32_t* err, void* stream);
 
 /* Greedy pick per row: the first maximal logit (ref_src/generation.py:24-26). */
 int tfd_argmax_rows(const float* logits, int ldl, int rows, int vocab, int32_t* pick,

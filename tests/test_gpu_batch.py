@@ -30,28 +30,45 @@ def _packed(w):
     return out
 
 
+def operand_order(x):
+    """[M][K] rows (M <= 32) -> the batched path's operand-order layout (flat, 32 x K;
+    rows past M hold NaN: they may only reach output rows that are not stored)."""
+    M, K = x.shape
+    full = torch.full((32, K), float("nan"), dtype=x.dtype, device=x.device)
+    full[:M] = x
+    return full.view(2, 16, K // 32, 4, 8).permute(2, 0, 3, 1, 4).reshape(-1).contiguous()
+
+
+def from_operand_order(flat, M, K):
+    """Inverse of operand_order (the first M rows)."""
+    return flat.view(K // 32, 2, 4, 16, 8).permute(1, 3, 0, 2, 4).reshape(32, K)[:M]
+
+
 def _gemm(x, w, epi, resid=None, work=None):
     M, K = x.shape
     N = w.shape[0]
     w = _packed(w)
     if epi == _lib.EPI_SWIGLU:
-        out = torch.zeros(M, N // 2, device=x.device, dtype=torch.bfloat16)
+        out = torch.full((32 * (N // 2),), float("nan"), device=x.device, dtype=torch.bfloat16)
     elif epi == _lib.EPI_LOGITS:
         out = torch.zeros(M, N, device=x.device, dtype=torch.float32)
     else:
         out = torch.zeros(M, N, device=x.device, dtype=torch.bfloat16)
-    lib().tfd_gemm_skinny_bf16(ptr(x), K, ptr(w), M, K, N, epi,
+    lib().tfd_gemm_skinny_bf16(ptr(operand_order(x)), ptr(w), M, K, N, epi,
                                None if resid is None else ptr(resid), N, ptr(out),
-                               out.shape[1], None if work is None else ptr(work),
+                               N, None if work is None else ptr(work),
                                0 if work is None else work.numel(),
                                torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
+    if epi == _lib.EPI_SWIGLU:
+        return from_operand_order(out, M, N // 2).cpu()
     return out.cpu()
 
 
 @pytest.mark.parametrize("split", [False, True], ids=["one-slice", "split-k"])
 @pytest.mark.parametrize("M", [1, 5, 16, 17, 32])
-@pytest.mark.parametrize("K,N", [(2048, 48), (6144, 40), (256, 16), (2048, 2050), (2048, 4200)])
+@pytest.mark.parametrize("K,N", [(2048, 64), (6144, 40), (256, 16), (768, 128), (2048, 2050),
+                                 (2048, 4200), (2048, 16448)])
 def test_skinny_gemm_within_one_ulp_of_exact(gpu_device, M, K, N, split):
     """With a work buffer the library splits K into slices (8 for most shapes
     here, 4 at N = 4200) whose partial tiles the last-arriving wave adds in
@@ -63,10 +80,6 @@ def test_skinny_gemm_within_one_ulp_of_exact(gpu_device, M, K, N, split):
                         dtype=torch.float32) if split else None)
     x = (torch.randn(M, K, generator=g) * 0.5).to(torch.bfloat16)
     w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
-    if work is None and K > 2048:
-        with pytest.raises(_lib.TFDError):
-            _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_STORE)
-        return
     exact = x.double() @ w.double().t()                          # [M][N]
     want = exact.to(torch.bfloat16).float()
     got = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_STORE, work=work).float()
@@ -85,7 +98,7 @@ def test_skinny_gemm_within_one_ulp_of_exact(gpu_device, M, K, N, split):
                 work=work).float()
     assert torch.equal(res, (r.float() + got).to(torch.bfloat16).float())
     # swiglu over (gate, up) row pairs, from the kernel's own rounded pair
-    if N % 2 == 0:
+    if N % 64 == 0:
         sw = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_SWIGLU, work=work).float()
         gate, up = got[:, 0::2], got[:, 1::2]
         act = torch.nn.functional.silu(gate.to(torch.bfloat16)).float()
@@ -108,6 +121,22 @@ def test_pack_skinny_layout(gpu_device):
     wp = torch.cat([w.cpu(), torch.zeros(tiles * 16 - N, K, dtype=w.dtype)])
     want = wp.view(tiles, 16, steps, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1, 64, 8)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("rows", [1, 7, 32])
+def test_rmsnorm_rows_operand_order(gpu_device, rows):
+    """The operand-order output of the row norm holds the row-major output's bits."""
+    g = torch.Generator().manual_seed(rows)
+    H = 2048
+    x = torch.randn(rows, H, generator=g).to(torch.bfloat16).to(gpu_device)
+    gamma = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(gpu_device)
+    flat = torch.zeros(rows, H, dtype=torch.bfloat16, device=gpu_device)
+    packed = torch.full((32 * H,), float("nan"), dtype=torch.bfloat16, device=gpu_device)
+    s = torch.cuda.current_stream().cuda_stream
+    lib().tfd_rmsnorm_rows_bf16(ptr(x), H, ptr(gamma), ptr(flat), H, rows, H, 1e-6, 0, s)
+    lib().tfd_rmsnorm_rows_bf16(ptr(x), H, ptr(gamma), ptr(packed), 0, rows, H, 1e-6, 1, s)
+    torch.cuda.synchronize()
+    assert torch.equal(from_operand_order(packed, rows, H), flat)
 
 
 def test_skinny_gemm_shapes_share_one_work_buffer(gpu_device):

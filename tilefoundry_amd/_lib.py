@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS = 0, 1, 2, 3
@@ -40,13 +40,13 @@ SIGNATURES: dict[str, list] = {
     "tfd_attn_rope_scores_paged": [P, P, P, P, P, I, P, P, P, I, P, P, I, I, I, I, F, F, P, I,
                                    P, P, I, P, P],
     "tfd_attn_pv_combine_paged": [P, P, P, I, P, I, I, I, I, P, I, P, P, P, P, I, P, P, P, P],
-    "tfd_rmsnorm_rows_bf16": [P, I, P, P, I, I, I, F, P],
+    "tfd_rmsnorm_rows_bf16": [P, I, P, P, I, I, I, F, I, P],
     "tfd_pack_skinny_bf16": [P, I, I, I, P, P],
-    "tfd_gemm_skinny_bf16": [P, I, P, I, I, I, I, P, I, P, I, P, L, P],
+    "tfd_gemm_skinny_bf16": [P, P, I, I, I, I, P, I, P, I, P, L, P],
     "tfd_attn_rope_scores_paged_batched": [P, I, P, P, P, P, I, P, P, I, P, P, I, I, I, I, I, F,
                                            F, P, I, P, P, I, I, P, P],
     "tfd_attn_pv_combine_paged_batched": [P, I, P, P, I, P, I, I, I, I, I, P, I, P, P, P, P, I,
-                                          I, P, P, I, P, P],
+                                          I, P, P, P, P],
     "tfd_argmax_rows": [P, I, I, I, P, P],
     "tfd_finalize_rows": [P, I, P, I, P, P, P, P, I, I, P, P, I, I, I, P, P],
     "tfd_embed_rows_bf16": [P, P, P, I, I, I, I, P, P],

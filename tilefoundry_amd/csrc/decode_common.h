@@ -44,6 +44,16 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// acc + bf16(p0) + bf16(p1): the two products are rounded to bf16 by one
+// conversion and added to the f32 accumulator by one dot instruction against
+// (1, 1) -- the HIR's "round each product, sum in f32" at two VALU operations
+// per pair instead of six (the sum's association differs, as any f32 order may).
+__device__ __forceinline__ float add_rounded2(float acc, float p0, float p1) {
+  const bf16x2_t r = {(__bf16)p0, (__bf16)p1};
+  const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(r, one, acc, false);
+}
+
 // Cross-lane reductions.  Within a row of 16 lanes the partner values come
 // from DPP (quad_perm xor 1, xor 2, row_half_mirror, row_mirror: VALU operand
 // modifiers, no LDS traffic); across rows from ds_bpermute.  Every step adds a

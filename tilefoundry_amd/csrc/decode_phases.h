@@ -538,12 +538,22 @@ __device__ __forceinline__ int v_pos(int j0, int p) {
 
 // K rows of the 64 positions from j0 (positions j < P are the ones used).  A
 // tile that holds no prior position issues nothing.
+// A wave's positions in one pass lie in one page (kPpw and 64 / kLpp divide
+// the page), so the page-table entry is wave-uniform: a scalar load, which does
+// not queue behind the tile loads already in flight the way a vector load would.
+__device__ __forceinline__ int wave_page(const int* page_table, int max_pages, int first_pos) {
+  const int pi = __builtin_amdgcn_readfirstlane(first_pos / kPage);
+  return page_table[pi < max_pages ? pi : max_pages - 1];
+}
+
 template <int D>
 __device__ __forceinline__ void k_tile_issue_at(int j0, int h, int P, const int* page_table,
                                                 int max_pages, const bf16* kpool, int num_pages,
                                                 int kv_heads, KTile<D>& kt) {
   using A = AttnShape<D>;
+  static_assert(kPage % A::kPpw == 0, "a wave's pass stays in one page");
   const int ch = (threadIdx.x & (kWave - 1)) % A::kLpp;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
 #pragma unroll
   for (int p = 0; p < A::kKPasses; ++p) {
     kt.pg[p] = -1;
@@ -551,10 +561,8 @@ __device__ __forceinline__ void k_tile_issue_at(int j0, int h, int P, const int*
   }
   if (j0 >= P) return;
 #pragma unroll
-  for (int p = 0; p < A::kKPasses; ++p) {
-    const int j = k_pos<D>(j0, p);
-    kt.pg[p] = page_table[j / kPage < max_pages ? j / kPage : max_pages - 1];
-  }
+  for (int p = 0; p < A::kKPasses; ++p)
+    kt.pg[p] = wave_page(page_table, max_pages, j0 + (p * kWavesPerBlock + wave) * A::kPpw);
 #pragma unroll
   for (int p = 0; p < A::kKPasses; ++p) {
     const int j = k_pos<D>(j0, p);
@@ -569,7 +577,9 @@ __device__ __forceinline__ void v_tile_issue_at(int j0, int h, int P, const int*
                                                 int max_pages, const bf16* vpool, int num_pages,
                                                 int kv_heads, VTile<D>& vt) {
   using A = AttnShape<D>;
+  static_assert(kPage % (kWave / A::kLpp) == 0, "a wave's pass stays in one page");
   const int ch = (int)threadIdx.x % A::kLpp;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
 #pragma unroll
   for (int p = 0; p < A::kVPasses; ++p) {
     vt.pg[p] = -1;
@@ -577,10 +587,8 @@ __device__ __forceinline__ void v_tile_issue_at(int j0, int h, int P, const int*
   }
   if (j0 >= P) return;
 #pragma unroll
-  for (int p = 0; p < A::kVPasses; ++p) {
-    const int j = v_pos<D>(j0, p);
-    vt.pg[p] = page_table[j / kPage < max_pages ? j / kPage : max_pages - 1];
-  }
+  for (int p = 0; p < A::kVPasses; ++p)
+    vt.pg[p] = wave_page(page_table, max_pages, j0 + p * A::kGroups + wave * (kWave / A::kLpp));
 #pragma unroll
   for (int p = 0; p < A::kVPasses; ++p) {
     const int j = v_pos<D>(j0, p);
@@ -833,10 +841,8 @@ __device__ __forceinline__ void attn_scores_phase(
       for (int g = 0; g < G; ++g) {
         float a = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          a += rbf(qv[g][2 * e] * bf_lo(kw[e]));
-          a += rbf(qv[g][2 * e + 1] * bf_hi(kw[e]));
-        }
+        for (int e = 0; e < 4; ++e)
+          a = add_rounded2(a, qv[g][2 * e] * bf_lo(kw[e]), qv[g][2 * e + 1] * bf_hi(kw[e]));
         a = group_sum<kLpp>(a);
         const float sc = rbf(a);
         if (valid) {
@@ -896,18 +902,23 @@ __device__ __forceinline__ bf16 attn_merge_one(float sp, float sv, float sn, flo
 struct NoHook {
   __device__ void operator()() const {}
 };
+// Where output value k of the attention row goes (element index from attn_out).
+struct RowOut {
+  __device__ uint32_t operator()(int k) const { return (uint32_t)k; }
+};
 
 // `polled` runs once this block's waits of the phase are over (the persistent
 // kernel issues weight loads there: memory counters retire in order, so loads
 // issued before a wait would hold it up)
-template <int D, int G, bool kLL, class Hook = NoHook>
+template <int D, int G, bool kLL, class Hook = NoHook, class OutMap = RowOut>
 __device__ __forceinline__ void attn_pv_phase(
     int split, int h, int nsplit, const bf16* __restrict__ qkv, int P,
     const int* __restrict__ page_table, int max_pages, const bf16* __restrict__ vpool,
     int num_pages, int kv_heads, const float* __restrict__ S, int s_stride,
     const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
     float* part_out, int* counters, bf16* __restrict__ attn_out, const AttnLL& ll,
-    const VTile<D>& vt, int* err, int chunks = 1, const Hook& polled = Hook()) {
+    const VTile<D>& vt, int* err, int chunks = 1, const Hook& polled = Hook(),
+    const OutMap& omap = OutMap()) {
   using A = AttnShape<D>;
   constexpr int kLpp = A::kLpp;
   constexpr int kGroups = A::kGroups;
@@ -984,20 +995,34 @@ __device__ __forceinline__ void attn_pv_phase(
       psum += wave_sum(pj);
     }
     __syncthreads();
+    // passes q and q + 1 hold the same dims of two positions: their rounded
+    // products go to each accumulator as one pair
+    static_assert(A::kVPasses % 2 == 0, "passes pair up");
 #pragma unroll
-    for (int q = 0; q < A::kVPasses; ++q) {
-      const int jj = jo + q * kGroups;
-      const bool bad = cur.pg[q] < 0 || cur.pg[q] >= num_pages;
-      if (jc + jj < jend && bad) page_ok = false;
-      const u32x4 t = (jc + jj < jend && !bad) ? cur.t[q] : u32x4{0u, 0u, 0u, 0u};
-      const uint32_t vw[4] = {t.x, t.y, t.z, t.w};
+    for (int q = 0; q < A::kVPasses; q += 2) {
+      uint32_t vw[2][4];
+      float pj[2][G];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int jj = jo + (q + u) * kGroups;
+        const bool bad = cur.pg[q + u] < 0 || cur.pg[q + u] >= num_pages;
+        if (jc + jj < jend && bad) page_ok = false;
+        const u32x4 t = (jc + jj < jend && !bad) ? cur.t[q + u] : u32x4{0u, 0u, 0u, 0u};
+        vw[u][0] = t.x;
+        vw[u][1] = t.y;
+        vw[u][2] = t.z;
+        vw[u][3] = t.w;
+#pragma unroll
+        for (int g = 0; g < G; ++g) pj[u][g] = p[g][jj];   // 0 past the end: exact zeros
+      }
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float pj = p[g][jj];          // 0 past the end: adds exact zeros
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          acc[g][2 * e] += rbf(pj * bf_lo(vw[e]));
-          acc[g][2 * e + 1] += rbf(pj * bf_hi(vw[e]));
+          acc[g][2 * e] = add_rounded2(acc[g][2 * e], pj[0][g] * bf_lo(vw[0][e]),
+                                       pj[1][g] * bf_lo(vw[1][e]));
+          acc[g][2 * e + 1] = add_rounded2(acc[g][2 * e + 1], pj[0][g] * bf_hi(vw[0][e]),
+                                           pj[1][g] * bf_hi(vw[1][e]));
         }
       }
     }
@@ -1086,7 +1111,7 @@ __device__ __forceinline__ void attn_pv_phase(
   if (tid < kOut) {
     const int g = tid / D, d = tid % D;
     const uint32_t vnew = (uint32_t)(heads * D + kv_heads * D + h * D);
-    coh_st_bf16(attn_out, (uint32_t)((h * G + g) * D + d),
+    coh_st_bf16(attn_out, omap((h * G + g) * D + d),
                 attn_merge_one(sp, sv, sn_of(snew, h * G + g), M[g], bf2f(qkv[vnew + d])));
   }
   if (tid == 0) atomicExch(&counters[h], 0);

@@ -34,6 +34,18 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxRows = 32;      // one skinny GEMM covers two 16-row MFMA tiles
 
+// Activations that feed a skinny GEMM (the normalised rows, the attention
+// output, the SwiGLU output) are stored in the matrix cores' A-operand order,
+// 32 rows x K: for 32-wide k step s and 16-row half h, a 1 KiB block at
+// (2 s + h) KiB whose 16 bytes at l * 16 hold X[16 h + l % 16][32 s + 8 (l / 16)
+// .. +7].  A wave then loads one step's operand as one contiguous KiB.  Rows
+// past the batch are never written; they only feed output rows that are not
+// stored.
+__device__ __forceinline__ int64_t xp_off(int m, int k) {
+  return ((int64_t)((k >> 5) * 2 + (m >> 4)) * 64 + (m & 15) + 16 * ((k >> 3) & 3)) * 8 +
+         (k & 7);
+}
+
 // ---------------------------------------------------------------------------
 // Row-wise RMSNorm (model.py:125-137 on each sequence's hidden state): one
 // wave per row, the batch-1 arithmetic.
@@ -42,17 +54,20 @@ template <int kCmax>
 __global__ __launch_bounds__(kWave) void k_rmsnorm_rows(const bf16* __restrict__ x, int ldx,
                                                         const bf16* __restrict__ gamma,
                                                         bf16* __restrict__ out, int ldo, int n,
-                                                        float eps) {
+                                                        float eps, int packed) {
   const int lane = threadIdx.x;
-  const bf16* xr_p = x + (int64_t)blockIdx.x * ldx;
-  bf16* o = out + (int64_t)blockIdx.x * ldo;
+  const int m = blockIdx.x;
+  const bf16* xr_p = x + (int64_t)m * ldx;
   u32x4 xr[kCmax];
   rms_norm_x<kCmax>(xr_p, gamma, n, eps, lane, xr);
   const int nch = n / 8;
 #pragma unroll
   for (int i = 0; i < kCmax; ++i) {
     const int c = i * kWave + lane;
-    if (c < nch) *reinterpret_cast<u32x4*>(o + (int64_t)c * 8) = xr[i];
+    if (c < nch) {
+      bf16* o = packed ? out + xp_off(m, c * 8) : out + (int64_t)m * ldo + (int64_t)c * 8;
+      *reinterpret_cast<u32x4*>(o) = xr[i];
+    }
   }
 }
 
@@ -87,12 +102,7 @@ enum SkinnyEpi { kSkStore = 0, kSkResid = 1, kSkSwiglu = 2, kSkLogits = 3 };
 // unit, eight steps in flight per wave) and Ks <= 2048 (the head: one block of
 // eight waves per compute unit, sixteen steps in flight per wave when Ks is a
 // multiple of 512).
-constexpr int kGxPad = 8;      // bf16 of padding per LDS row: rows start 16 bytes apart mod 256
 
-template <int kKsMax>
-constexpr int gx_lds_bytes() {
-  return 32 * (kKsMax + kGxPad) * 2;
-}
 
 template <int kEpi>
 __device__ __forceinline__ void skinny_store(const f32x4 (&c)[2], int halves, int tile, int lane,
@@ -106,10 +116,11 @@ __device__ __forceinline__ void skinny_store(const f32x4 (&c)[2], int halves, in
       const int m = 16 * h + 4 * kq + e;
       const float y = rbf(c[h][e]);
       if (kEpi == kSkSwiglu) {
-        // (gate, up) pairs sit in adjacent columns: lanes r and r ^ 1
+        // (gate, up) pairs sit in adjacent columns: lanes r and r ^ 1; the
+        // product feeds the down projection, so it is stored in operand order
         const float u = __shfl_xor(y, 1, kWave);
         if ((r & 1) == 0 && m < M && n + 1 < N)
-          ((bf16*)out)[(int64_t)m * ldo + n / 2] = f2bf(rbf(silu_f(y)) * u);
+          ((bf16*)out)[xp_off(m, n / 2)] = f2bf(rbf(silu_f(y)) * u);
       } else if (m < M && n < N) {
         if (kEpi == kSkStore)
           ((bf16*)out)[(int64_t)m * ldo + n] = f2bf(y);
@@ -143,11 +154,11 @@ __global__ __launch_bounds__(kBlock) void k_pack_skinny(const bf16* __restrict__
 
 template <int kEpi, int kKsMax, int kWaves, int kDepth>
 __global__ __launch_bounds__(kWaves * kWave) void k_gemm_skinny(
-    const bf16* __restrict__ X, int ldx, const bf16* __restrict__ W, int M, int K, int N, int Ks,
+    const bf16* __restrict__ X, const bf16* __restrict__ W, int M, int K, int N, int Ks,
     const bf16* __restrict__ resid, int ldr, void* __restrict__ out, int ldo,
     float* __restrict__ part, int* __restrict__ counters) {
   constexpr int kThreads = kWaves * kWave;
-  __shared__ __align__(16) bf16 xs[32 * (kKsMax + kGxPad)];
+  __shared__ __align__(16) bf16 xs[32 * kKsMax];
   const int lane = threadIdx.x & (kWave - 1);
   // wave-uniform (scalar) so the tile and step loops branch on scalars
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -161,7 +172,6 @@ __global__ __launch_bounds__(kWaves * kWave) void k_gemm_skinny(
   const int steps = Ks / 32;                 // a multiple of kDepth
   const int first = t0 + wave;
   const int ntw = first < t1 ? (t1 - first + kWaves - 1) / kWaves : 0;
-  const int stride = Ks + kGxPad;
 
   // Load cursor over this wave's (tile, step) sequence in the packed weights:
   // one step of one tile is 1 KiB, lane l's 16 bytes at l * 16 (a wave's load is
@@ -179,31 +189,28 @@ __global__ __launch_bounds__(kWaves * kWave) void k_gemm_skinny(
   u32x4 b[kDepth];
 #pragma unroll
   for (int u = 0; u < kDepth; ++u) b[u] = load_next();   // in flight while X is staged
-  // X slice -> LDS, all 32 rows (rows past M are zero)
+  // the X slice (operand-order blocks of steps kbase/32 ..) -> LDS, a plain copy
   {
-    const int cpr = Ks / 8;                    // 16-byte chunks per row
-    const int nchunks = 32 * cpr;
+    const bf16* xsrc = X + (int64_t)(kbase / 32) * 1024;
+    const int nchunks = Ks * 4;                // 16-byte chunks: 32 rows x Ks / 8
     constexpr int kB = 8;
     for (int c0 = threadIdx.x; c0 < nchunks; c0 += kB * kThreads) {
       u32x4 v[kB];
 #pragma unroll
       for (int j = 0; j < kB; ++j) {
         const int c = c0 + j * kThreads;
-        const int row = c / cpr, col = c % cpr;
-        v[j] = (c < nchunks && row < M) ? load16(X + (int64_t)row * ldx + kbase + col * 8)
-                                        : u32x4{0u, 0u, 0u, 0u};
+        v[j] = load16(xsrc + (int64_t)(c < nchunks ? c : 0) * 8);
       }
 #pragma unroll
       for (int j = 0; j < kB; ++j) {
         const int c = c0 + j * kThreads;
-        if (c < nchunks)
-          *reinterpret_cast<u32x4*>(&xs[(c / cpr) * stride + (c % cpr) * 8]) = v[j];
+        if (c < nchunks) *reinterpret_cast<u32x4*>(&xs[c * 8]) = v[j];
       }
     }
   }
   __syncthreads();
 
-  const bf16* xa = xs + r * stride + 8 * kq;
+  const bf16* xa = xs + lane * 8;
   f32x4 c[2];
   // kDepth steps from LDS x the weights in flight; with kRefill each slot is
   // reloaded with the step kDepth ahead right behind its use (the wave's last
@@ -211,12 +218,12 @@ __global__ __launch_bounds__(kWaves * kWave) void k_gemm_skinny(
   auto chunk = [&](int k0, auto refill) {
 #pragma unroll
     for (int u = 0; u < kDepth; ++u) {
-      const bf16* xk = xa + (k0 + u) * 32;
+      const bf16* xk = xa + (k0 + u) * 1024;
       const bf16x8_t bw = __builtin_bit_cast(bf16x8_t, b[u]);
       c[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8_t*>(xk), bw,
                                                      c[0], 0, 0, 0);
       c[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          *reinterpret_cast<const bf16x8_t*>(xk + 16 * stride), bw, c[1], 0, 0, 0);
+          *reinterpret_cast<const bf16x8_t*>(xk + 512), bw, c[1], 0, 0, 0);
       if (decltype(refill)::value) b[u] = load_next();
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -275,6 +282,95 @@ __global__ __launch_bounds__(kWaves * kWave) void k_gemm_skinny(
 }
 
 // ---------------------------------------------------------------------------
+// Skinny GEMM for few tiles (the q/k/v, o, gate/up and down projections at
+// N / 16 <= a few per compute unit): one block per kT consecutive 16-column
+// tiles, its kKW waves splitting K evenly.  Wave w streams the packed weights
+// of its K range for its tiles and reads the matching operand-order X blocks
+// straight into registers (no other wave needs them, so nothing is staged),
+// kDepth steps in flight; the waves' sums meet in LDS and are added in wave
+// order.  No partial ever leaves the block, so the launch is one round trip
+// of loads plus a barrier -- what the narrow projections need, whose weights
+// alone do not keep the chip busy for long.
+// ---------------------------------------------------------------------------
+template <int kEpi, int kT, int kKW, int kDepth>
+__global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
+    const bf16* __restrict__ X, const bf16* __restrict__ W, int M, int K, int N,
+    const bf16* __restrict__ resid, int ldr, void* __restrict__ out, int ldo) {
+  __shared__ f32x4 red[kKW][kT][2][kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int ntiles = (N + 15) / 16;
+  const int tile0 = blockIdx.x * kT;
+  const int ksteps = K / 32;
+  const int steps = ksteps / kKW;            // per wave, a multiple of kDepth
+  const int s0 = wave * steps;
+  // X in operand order: step k's two 16-row halves are consecutive KiBs
+  const bf16* xa = X + (int64_t)s0 * 1024 + lane * 8;
+  const bf16* wt[kT];
+#pragma unroll
+  for (int t = 0; t < kT; ++t) {
+    const int tt = tile0 + t < ntiles ? tile0 + t : ntiles - 1;
+    wt[t] = W + ((int64_t)tt * ksteps + s0) * 512 + lane * 8;
+  }
+  u32x4 b[kDepth][kT], a0[kDepth], a1[kDepth];
+  auto issue = [&](int u, int k) {
+#pragma unroll
+    for (int t = 0; t < kT; ++t) b[u][t] = load16_stream(wt[t] + (int64_t)k * 512);
+    a0[u] = load16(xa + (int64_t)k * 1024);
+    a1[u] = load16(xa + (int64_t)k * 1024 + 512);
+  };
+#pragma unroll
+  for (int u = 0; u < kDepth; ++u) {
+    issue(u, u);
+    __builtin_amdgcn_sched_barrier(0);        // issue in step order
+  }
+  f32x4 c[kT][2];
+#pragma unroll
+  for (int t = 0; t < kT; ++t) c[t][0] = c[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // each slot is refilled with the step kDepth ahead right behind its use; the
+  // last chunk has nothing ahead (a separate copy, so no branch sits between a
+  // load and its use)
+  auto chunk = [&](int k0, auto refill) {
+#pragma unroll
+    for (int u = 0; u < kDepth; ++u) {
+      const bf16x8_t x0 = __builtin_bit_cast(bf16x8_t, a0[u]);
+      const bf16x8_t x1 = __builtin_bit_cast(bf16x8_t, a1[u]);
+#pragma unroll
+      for (int t = 0; t < kT; ++t) {
+        const bf16x8_t bw = __builtin_bit_cast(bf16x8_t, b[u][t]);
+        c[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, bw, c[t][0], 0, 0, 0);
+        c[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, bw, c[t][1], 0, 0, 0);
+      }
+      if (decltype(refill)::value) issue(u, k0 + kDepth + u);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int k0 = 0; k0 + kDepth < steps; k0 += kDepth) chunk(k0, std::true_type{});
+  chunk(steps - kDepth, std::false_type{});
+#pragma unroll
+  for (int t = 0; t < kT; ++t) {
+    red[wave][t][0][lane] = c[t][0];
+    red[wave][t][1][lane] = c[t][1];
+  }
+  __syncthreads();
+  if (wave >= kT) return;
+  // wave t adds the K ranges of tile t in wave order and applies the epilogue
+  const int t = wave;
+  if (tile0 + t >= ntiles) return;
+  f32x4 sum[2] = {red[0][t][0][lane], red[0][t][1][lane]};
+#pragma unroll
+  for (int w = 1; w < kKW; ++w) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const f32x4 v = red[w][t][h][lane];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum[h][e] += v[e];
+    }
+  }
+  skinny_store<kEpi>(sum, M > 16 ? 2 : 1, tile0 + t, lane, M, N, resid, ldr, out, ldo);
+}
+
+// ---------------------------------------------------------------------------
 // Attention for a batch: grid (nsplit, kv heads, sequences); sequence b has its
 // own position, page-table row, QKV row and workspaces.  The phase bodies are
 // the batch-1 ones.
@@ -304,13 +400,19 @@ __global__ __launch_bounds__(kBlock) void k_attn_scores_b(
                                  AttnLL{}, kt, err, chunks);
 }
 
+// Attention output of sequence b in operand order (it feeds the o projection).
+struct PackedOut {
+  int b;
+  __device__ uint32_t operator()(int k) const { return (uint32_t)xp_off(b, k); }
+};
+
 template <int D, int G>
 __global__ __launch_bounds__(kBlock) void k_attn_pv_b(
     const bf16* __restrict__ qkv, int ldq, const int* __restrict__ pos,
     const int* __restrict__ page_table, int max_pages, const bf16* __restrict__ vpool,
     int num_pages, int kv_heads, const float* __restrict__ S, int s_stride,
     const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
-    float* part_out, int* counters, bf16* __restrict__ attn_out, int lda, int chunks, int* err) {
+    float* part_out, int* counters, bf16* __restrict__ attn_out, int chunks, int* err) {
   const int b = blockIdx.z, heads = kv_heads * G, nsplit = gridDim.x;
   int P = coh_ldi(pos + b);
   if (P < 0 || P >= max_pages * kPage) P = 0;
@@ -318,14 +420,13 @@ __global__ __launch_bounds__(kBlock) void k_attn_pv_b(
   VTile<D> vt;
   v_tile_issue_at<D>(blockIdx.x * chunks * kSplit, blockIdx.y, P, pt, max_pages, vpool,
                      num_pages, kv_heads, vt);
-  attn_pv_phase<D, G, false>(blockIdx.x, blockIdx.y, nsplit, qkv + (int64_t)b * ldq, P, pt,
-                             max_pages, vpool, num_pages, kv_heads,
-                             S + (int64_t)b * heads * s_stride, s_stride,
-                             smax + (int64_t)b * nsplit * heads, snew + (int64_t)b * heads,
-                             part_sum + (int64_t)b * nsplit * heads,
-                             part_out + (int64_t)b * nsplit * heads * D,
-                             counters + (int64_t)b * kv_heads, attn_out + (int64_t)b * lda,
-                             AttnLL{}, vt, err, chunks);
+  attn_pv_phase<D, G, false, NoHook, PackedOut>(
+      blockIdx.x, blockIdx.y, nsplit, qkv + (int64_t)b * ldq, P, pt, max_pages, vpool,
+      num_pages, kv_heads, S + (int64_t)b * heads * s_stride, s_stride,
+      smax + (int64_t)b * nsplit * heads, snew + (int64_t)b * heads,
+      part_sum + (int64_t)b * nsplit * heads, part_out + (int64_t)b * nsplit * heads * D,
+      counters + (int64_t)b * kv_heads, attn_out, AttnLL{}, vt, err, chunks, NoHook{},
+      PackedOut{b});
 }
 
 // ---------------------------------------------------------------------------
@@ -431,14 +532,16 @@ __global__ __launch_bounds__(kBlock) void k_embed_rows(const bf16* __restrict__ 
 extern "C" {
 
 int tfd_rmsnorm_rows_bf16(const void* x, int ldx, const void* gamma, void* out, int ldo,
-                          int rows, int n, float eps, void* stream) {
+                          int rows, int n, float eps, int packed, void* stream) {
   if (!x || !gamma || !out) return fail(kBadArg, "rmsnorm_rows: null pointer");
-  if (rows <= 0 || n <= 0 || n % 8 || ldx < n || ldo < n || ldx % 8 || ldo % 8)
-    return fail(kBadShape, "rmsnorm_rows: rows=%d n=%d ldx=%d ldo=%d", rows, n, ldx, ldo);
+  if (rows <= 0 || n <= 0 || n % 8 || ldx < n || ldx % 8 ||
+      (packed ? (rows > kMaxRows || n % 32) : (ldo < n || ldo % 8)))
+    return fail(kBadShape, "rmsnorm_rows: rows=%d n=%d ldx=%d ldo=%d packed=%d", rows, n, ldx,
+                ldo, packed);
   auto s = (hipStream_t)stream;
   TFD_CMAX_SWITCH(n, hipLaunchKernelGGL((k_rmsnorm_rows<kC>), dim3(rows), dim3(kWave), 0, s,
                                         (const bf16*)x, ldx, (const bf16*)gamma, (bf16*)out, ldo,
-                                        n, eps));
+                                        n, eps, packed));
   return launched("rmsnorm_rows");
 }
 
@@ -500,6 +603,17 @@ SkinnyPlan skinny_plan(int K, int N, int64_t work_floats) {
   return p;
 }
 
+// Which kernel: tiles per block of the K-split kernel, or 0 for the
+// X-stationary one.  The K-split kernel takes the projections with few tiles
+// (it needs no partials outside the block) and any K deeper than the LDS stage;
+// the X-stationary kernel takes the head, whose many tiles fill the chip and
+// whose X is worth keeping in LDS across them.
+int ksplit_tiles(int K, int N) {
+  const int ntiles = (N + 15) / 16;
+  if (K > 2048 || ntiles < 4 * compute_units()) return ntiles >= 512 ? 2 : 1;
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -515,20 +629,49 @@ int tfd_pack_skinny_bf16(const void* w, int ldw, int N, int K, void* packed, voi
   return launched("pack_skinny");
 }
 
-int tfd_gemm_skinny_bf16(const void* x, int ldx, const void* w, int M, int K, int N,
-                         int epilogue, const void* resid, int ldr, void* out, int ldo,
-                         float* work, int64_t work_floats, void* stream) {
+int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int epilogue,
+                         const void* resid, int ldr, void* out, int ldo, float* work,
+                         int64_t work_floats, void* stream) {
   if (!x || !w || !out) return fail(kBadArg, "gemm_skinny: null pointer");
-  if (M <= 0 || M > kMaxRows || K <= 0 || K % 256 || N <= 0 || ldx < K || ldx % 8)
-    return fail(kBadShape, "gemm_skinny: M=%d (1..32) K=%d (multiple of 256) N=%d ldx=%d", M,
-                K, N, ldx);
+  if (M <= 0 || M > kMaxRows || K <= 0 || K % 256 || N <= 0)
+    return fail(kBadShape, "gemm_skinny: M=%d (1..32) K=%d (multiple of 256) N=%d", M, K, N);
   if (epilogue == TFD_EPI_RESID && (!resid || ldr < N))
     return fail(kBadArg, "gemm_skinny: residual epilogue needs resid with ldr >= N");
-  if (epilogue == TFD_EPI_SWIGLU ? (N % 2 || ldo < N / 2) : ldo < N)
-    return fail(kBadShape, "gemm_skinny: ldo=%d too small for N=%d", ldo, N);
+  if (epilogue == TFD_EPI_SWIGLU ? (N % 2 || (N / 2) % 32) : ldo < N)
+    return fail(kBadShape, "gemm_skinny: ldo=%d N=%d (SwiGLU: N/2 a multiple of 32)", ldo, N);
   if (work_floats < 0 || (work_floats > 0 && !work))
     return fail(kBadArg, "gemm_skinny: work=%p with %lld floats", (void*)work,
                 (long long)work_floats);
+  auto s = (hipStream_t)stream;
+  auto xb = (const bf16*)x;
+  auto wb = (const bf16*)w;
+  auto rb = (const bf16*)resid;
+  const int ntiles = (N + 15) / 16;
+  const int kt = ksplit_tiles(K, N);
+  if (kt > 0) {
+    const int steps = K / 32 / 8;
+    const dim3 grid((ntiles + kt - 1) / kt);
+#define TFD_KSPLIT(EPI, KT, D)                                                                  \
+  hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D>), grid, dim3(8 * kWave), 0, s, xb, wb, M, \
+                     K, N, rb, ldr, out, ldo)
+#define TFD_KSPLIT_EPI(EPI)                              \
+  if (kt == 2 && steps % 8 == 0) TFD_KSPLIT(EPI, 2, 8);  \
+  else if (steps % 8 == 0) TFD_KSPLIT(EPI, 1, 8);        \
+  else if (steps % 4 == 0) TFD_KSPLIT(EPI, 1, 4);        \
+  else if (steps % 2 == 0) TFD_KSPLIT(EPI, 1, 2);        \
+  else TFD_KSPLIT(EPI, 1, 1);
+    switch (epilogue) {
+      case TFD_EPI_STORE: TFD_KSPLIT_EPI(kSkStore); break;
+      case TFD_EPI_RESID: TFD_KSPLIT_EPI(kSkResid); break;
+      case TFD_EPI_SWIGLU: TFD_KSPLIT_EPI(kSkSwiglu); break;
+      case TFD_EPI_LOGITS: TFD_KSPLIT_EPI(kSkLogits); break;
+      default:
+        return fail(kBadArg, "gemm_skinny: epilogue %d", epilogue);
+    }
+#undef TFD_KSPLIT_EPI
+#undef TFD_KSPLIT
+    return launched("gemm_skinny");
+  }
   const SkinnyPlan plan = skinny_plan(K, N, work ? work_floats : 0);
   if (plan.Ks > 2048 || plan.Ks % 256)
     return fail(kBadShape, "gemm_skinny: K=%d needs slices of at most 2048 (multiples of 256); "
@@ -539,20 +682,16 @@ int tfd_gemm_skinny_bf16(const void* x, int ldx, const void* w, int M, int K, in
   int* counters = plan.slices > 1 ? (int*)work : nullptr;
   float* part = plan.slices > 1 ? work + kSkCounters : nullptr;
   const dim3 grid(plan.blocks_per_slice, plan.slices);
-  auto s = (hipStream_t)stream;
-  auto xb = (const bf16*)x;
-  auto wb = (const bf16*)w;
-  auto rb = (const bf16*)resid;
 #define TFD_SKINNY_LAUNCH(EPI)                                                                \
   if (plan.wide && plan.Ks % 512 == 0)                                                        \
     hipLaunchKernelGGL((k_gemm_skinny<EPI, 2048, 8, 16>), grid, dim3(8 * kWave), 0, s, xb,    \
-                       ldx, wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);         \
+                       wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);              \
   else if (plan.wide)                                                                         \
     hipLaunchKernelGGL((k_gemm_skinny<EPI, 2048, 8, 8>), grid, dim3(8 * kWave), 0, s, xb,     \
-                       ldx, wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);         \
+                       wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);              \
   else                                                                                        \
     hipLaunchKernelGGL((k_gemm_skinny<EPI, 1024, 4, 8>), grid, dim3(4 * kWave), 0, s, xb,     \
-                       ldx, wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);
+                       wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);
   switch (epilogue) {
     case TFD_EPI_STORE: TFD_SKINNY_LAUNCH(kSkStore); break;
     case TFD_EPI_RESID: TFD_SKINNY_LAUNCH(kSkResid); break;
@@ -601,14 +740,14 @@ int tfd_attn_pv_combine_paged_batched(
     const void* v_pool, int num_pages, int batch, int heads, int kv_heads, int head_dim,
     const float* scores, int score_stride, const float* split_max, const float* score_new,
     float* part_sum, float* part_out, int nsplit, int split_tiles, int32_t* counters,
-    void* attn_out, int lda, int32_t* err, void* stream) {
+    void* attn_out, int32_t* err, void* stream) {
   if (!qkv || !pos || !page_table || !v_pool || !scores || !split_max || !score_new ||
       !part_sum || !part_out || !counters || !attn_out)
     return fail(kBadArg, "attn_pv_combine_batched: null pointer");
-  if (batch <= 0 || batch > 65535 || kv_heads <= 0 || heads % kv_heads || nsplit <= 0 ||
-      max_pages <= 0 || num_pages <= 0 || lda < heads * head_dim || split_tiles <= 0)
-    return fail(kBadShape, "attn_pv_combine_batched: batch=%d heads=%d kv_heads=%d nsplit=%d "
-                "lda=%d split_tiles=%d", batch, heads, kv_heads, nsplit, lda, split_tiles);
+  if (batch <= 0 || batch > kMaxRows || kv_heads <= 0 || heads % kv_heads || nsplit <= 0 ||
+      max_pages <= 0 || num_pages <= 0 || (heads * head_dim) % 32 || split_tiles <= 0)
+    return fail(kBadShape, "attn_pv_combine_batched: batch=%d (1..32) heads=%d kv_heads=%d "
+                "nsplit=%d split_tiles=%d", batch, heads, kv_heads, nsplit, split_tiles);
   const int64_t slen = (int64_t)split_tiles * kSplit;
   if (nsplit * slen < (int64_t)max_pages * kPage || score_stride < nsplit * slen)
     return fail(kBadShape, "attn_pv_combine_batched: nsplit=%d does not cover the cache", nsplit);
@@ -619,7 +758,7 @@ int tfd_attn_pv_combine_paged_batched(
       hipLaunchKernelGGL((k_attn_pv_b<kD, kG>), grid, dim3(kBlock), 0, s, (const bf16*)qkv, ldq,
                          pos, page_table, max_pages, (const bf16*)v_pool, num_pages, kv_heads,
                          scores, score_stride, split_max, score_new, part_sum, part_out,
-                         counters, (bf16*)attn_out, lda, split_tiles, err));
+                         counters, (bf16*)attn_out, split_tiles, err));
   return launched("attn_pv_combine_batched");
 }
 

@@ -135,11 +135,12 @@ class BatchEngine:
 
         self.hid_rows = z(self.L + 1, B, self.H)      # [0]: the step's input embeddings
         self.hid = self.hid_rows[0]
-        self.xn = z(B, self.H)
+        # GEMM inputs in operand order (32 rows x K, see tfd_rmsnorm_rows_bf16)
+        self.xn = z(32 * self.H)
         self.qkv = z(B, self.qkv_n)
-        self.attn = z(B, self.QD)
+        self.attn = z(32 * self.QD)
         self.h1 = z(B, self.H)
-        self.hmid = z(B, self.I)
+        self.hmid = z(32 * self.I)
         self.kpool = z(self.L, self.num_pages, self.HKV, _lib.PAGE_SIZE, self.D)
         self.vpool = z(self.L, self.num_pages, self.HKV, _lib.PAGE_SIZE, self.D)
         self.scores = z(B, self.HQ, self.score_stride, dtype=f32)
@@ -164,9 +165,9 @@ class BatchEngine:
         return torch.cuda.current_stream(self.device).cuda_stream
 
     # ---------------------------------------------------------------- the step
-    def _gemm(self, x, ldx, w, K, N, epi, resid, out, ldo, s):
+    def _gemm(self, x, w, K, N, epi, resid, out, ldo, s):
         """out = epi(x @ w^T) for the batch's rows (model.py:160-171 and friends)."""
-        self._lib.tfd_gemm_skinny_bf16(ptr(x), ldx, ptr(w), self.B, K, N, epi,
+        self._lib.tfd_gemm_skinny_bf16(ptr(x), ptr(w), self.B, K, N, epi,
                                        None if resid is None else ptr(resid),
                                        0 if resid is None else resid.shape[-1], ptr(out), ldo,
                                        ptr(self.work), self.work.numel(), s)
@@ -176,9 +177,9 @@ class BatchEngine:
         L, w = self._lib, self.layers[i]
         B, H, I, D = self.B, self.H, self.I, self.D
         x_in, x_out = self.hid_rows[i], self.hid_rows[i + 1]
-        L.tfd_rmsnorm_rows_bf16(ptr(x_in), H, ptr(w["gamma_in"]), ptr(self.xn), H, B, H,
-                                self.eps, s)
-        self._gemm(self.xn, H, w["w_qkv"], H, self.qkv_n, _lib.EPI_STORE, None, self.qkv,
+        L.tfd_rmsnorm_rows_bf16(ptr(x_in), H, ptr(w["gamma_in"]), ptr(self.xn), 0, B, H,
+                                self.eps, 1, s)
+        self._gemm(self.xn, w["w_qkv"], H, self.qkv_n, _lib.EPI_STORE, None, self.qkv,
                    self.qkv_n, s)
         L.tfd_attn_rope_scores_paged_batched(
             ptr(self.qkv), self.qkv_n, ptr(w["gamma_q"]), ptr(w["gamma_k"]), ptr(self.cos),
@@ -190,14 +191,14 @@ class BatchEngine:
             ptr(self.qkv), self.qkv_n, ptr(self.pos), ptr(self.page_table), self.max_pages,
             ptr(self.vpool[i]), self.num_pages, B, self.HQ, self.HKV, D, ptr(self.scores),
             self.score_stride, ptr(self.smax), ptr(self.snew), ptr(self.psum), ptr(self.pout),
-            self.nsplit, self.split_tiles, ptr(self.counters), ptr(self.attn), self.QD,
+            self.nsplit, self.split_tiles, ptr(self.counters), ptr(self.attn),
             ptr(self.err), s)
-        self._gemm(self.attn, self.QD, w["w_o"], self.QD, H, _lib.EPI_RESID, x_in, self.h1, H,
+        self._gemm(self.attn, w["w_o"], self.QD, H, _lib.EPI_RESID, x_in, self.h1, H,
                    s)
-        L.tfd_rmsnorm_rows_bf16(ptr(self.h1), H, ptr(w["gamma_post"]), ptr(self.xn), H, B, H,
-                                self.eps, s)
-        self._gemm(self.xn, H, w["w_gu"], H, 2 * I, _lib.EPI_SWIGLU, None, self.hmid, I, s)
-        self._gemm(self.hmid, I, w["w_down"], I, H, _lib.EPI_RESID, self.h1, x_out, H, s)
+        L.tfd_rmsnorm_rows_bf16(ptr(self.h1), H, ptr(w["gamma_post"]), ptr(self.xn), 0, B, H,
+                                self.eps, 1, s)
+        self._gemm(self.xn, w["w_gu"], H, 2 * I, _lib.EPI_SWIGLU, None, self.hmid, 0, s)
+        self._gemm(self.hmid, w["w_down"], I, H, _lib.EPI_RESID, self.h1, x_out, H, s)
 
     def _step(self):
         s = self._stream()
@@ -205,8 +206,8 @@ class BatchEngine:
             self._layer(i, s)
         L, B, H = self._lib, self.B, self.H
         L.tfd_rmsnorm_rows_bf16(ptr(self.hid_rows[self.L]), H, ptr(self.gamma_final),
-                                ptr(self.xn), H, B, H, self.eps, s)
-        self._gemm(self.xn, H, self.w_head, H, self.V, _lib.EPI_LOGITS, None, self.logits,
+                                ptr(self.xn), 0, B, H, self.eps, 1, s)
+        self._gemm(self.xn, self.w_head, H, self.V, _lib.EPI_LOGITS, None, self.logits,
                    self.V, s)
         L.tfd_argmax_rows(ptr(self.logits), self.V, B, self.V, ptr(self.pick), s)
         L.tfd_finalize_rows(ptr(self.pick), B, ptr(self.inp), self.nsteps, ptr(self.plen),
