@@ -12,6 +12,8 @@
 // tables and the page table are read-only for a launch and use plain loads.
 #pragma once
 
+#include <type_traits>
+
 #include "decode_common.h"
 
 namespace tfd {
@@ -503,19 +505,26 @@ __device__ __forceinline__ int64_t page_row(int page, int j, int kv_heads, int h
 
 template <int D>
 struct AttnShape {
-  static constexpr int kLpp = D / 8;                        // lanes per position (16-byte chunks)
-  static constexpr int kPpw = kWave / kLpp;                 // positions per wave, scores pass
-  static constexpr int kKPasses = kSplit / (kWavesPerBlock * kPpw);
-  static constexpr int kGroups = kBlock / kLpp;             // position groups, P.V pass
+  // P.V pass: kLpp lanes per position (16-byte chunks of V), kGroups positions
+  static constexpr int kLpp = D / 8;
+  static constexpr int kGroups = kBlock / kLpp;
   static constexpr int kVPasses = kSplit / kGroups;
-  static_assert(kKPasses * kWavesPerBlock * kPpw == kSplit, "split tiles the scores pass");
   static_assert(kVPasses * kGroups == kSplit, "split tiles the P.V pass");
+  // scores pass: kKLanes lanes per position, kKDims dims each, read as
+  // kKChunks loads of which load i of the position's lanes covers 128
+  // contiguous bytes (whole cache lines); kKPasses passes of the block per tile
+  static constexpr int kKLanes = 8;
+  static constexpr int kKDims = D / kKLanes;
+  static constexpr int kKChunks = kKDims / 8;
+  static constexpr int kKPpw = kWave / kKLanes;             // positions per wave and pass
+  static constexpr int kKPasses = kSplit / (kWavesPerBlock * kKPpw);
+  static_assert(kKPasses * kWavesPerBlock * kKPpw == kSplit, "passes cover a tile");
 };
 
 template <int D>
 struct KTile {
-  int pg[AttnShape<D>::kKPasses];
-  u32x4 t[AttnShape<D>::kKPasses];
+  int pg[AttnShape<D>::kKPasses];          // the wave's page in each pass
+  u32x4 t[AttnShape<D>::kKPasses][AttnShape<D>::kKChunks];
 };
 template <int D>
 struct VTile {
@@ -523,12 +532,12 @@ struct VTile {
   u32x4 t[AttnShape<D>::kVPasses];
 };
 
-// position a thread reads in pass p of each pass layout
+// position a thread reads in each pass layout
 template <int D>
 __device__ __forceinline__ int k_pos(int j0, int p) {
   using A = AttnShape<D>;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  return j0 + p * kWavesPerBlock * A::kPpw + wave * A::kPpw + lane / A::kLpp;
+  return j0 + (p * kWavesPerBlock + wave) * A::kKPpw + lane / A::kKLanes;
 }
 template <int D>
 __device__ __forceinline__ int v_pos(int j0, int p) {
@@ -536,14 +545,40 @@ __device__ __forceinline__ int v_pos(int j0, int p) {
   return j0 + (int)threadIdx.x / A::kLpp + p * A::kGroups;
 }
 
-// K rows of the 64 positions from j0 (positions j < P are the ones used).  A
-// tile that holds no prior position issues nothing.
-// A wave's positions in one pass lie in one page (kPpw and 64 / kLpp divide
-// the page), so the page-table entry is wave-uniform: a scalar load, which does
-// not queue behind the tile loads already in flight the way a vector load would.
+// A wave's positions in one pass lie in one page (16 positions per wave in
+// the scores pass; 64 / kLpp divides the page in the P.V pass), so the
+// page-table entry is wave-uniform: a scalar load, which does not queue behind
+// the tile loads already in flight the way a vector load would.
 __device__ __forceinline__ int wave_page(const int* page_table, int max_pages, int first_pos) {
   const int pi = __builtin_amdgcn_readfirstlane(first_pos / kPage);
   return page_table[pi < max_pages ? pi : max_pages - 1];
+}
+
+// K rows of the 64 positions from j0 (positions j < P are the ones used): in
+// pass p, lane l of wave w reads position j0 + 8 (4 p + w) + l / 8, chunks
+// (l % 8) and (l % 8) + 8 (16 dims each), so a load instruction covers whole
+// 128-byte lines.  A tile that holds no prior position issues nothing.
+// (the loads only: the caller knows the tile holds a position below P)
+template <int D>
+__device__ __forceinline__ void k_tile_load_at(int j0, int h, const int* page_table,
+                                               int max_pages, const bf16* kpool, int num_pages,
+                                               int kv_heads, KTile<D>& kt) {
+  using A = AttnShape<D>;
+  static_assert(kPage % A::kKPpw == 0, "a wave's positions of a pass stay in one page");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+#pragma unroll
+  for (int p = 0; p < A::kKPasses; ++p)
+    kt.pg[p] = wave_page(page_table, max_pages, j0 + (p * kWavesPerBlock + wave) * A::kKPpw);
+#pragma unroll
+  for (int p = 0; p < A::kKPasses; ++p) {
+    const bool bad = kt.pg[p] < 0 || kt.pg[p] >= num_pages;
+    const int j = j0 + (p * kWavesPerBlock + wave) * A::kKPpw + lane / A::kKLanes;
+    const int64_t row = page_row(bad ? 0 : kt.pg[p], j, kv_heads, h, D) + (lane % A::kKLanes) * 8;
+#pragma unroll
+    for (int i = 0; i < A::kKChunks; ++i)
+      kt.t[p][i] = coh_ld16(kpool, (uint32_t)(row + 64 * i) * 2u);
+  }
 }
 
 template <int D>
@@ -551,41 +586,23 @@ __device__ __forceinline__ void k_tile_issue_at(int j0, int h, int P, const int*
                                                 int max_pages, const bf16* kpool, int num_pages,
                                                 int kv_heads, KTile<D>& kt) {
   using A = AttnShape<D>;
-  static_assert(kPage % A::kPpw == 0, "a wave's pass stays in one page");
-  const int ch = (threadIdx.x & (kWave - 1)) % A::kLpp;
-  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
 #pragma unroll
   for (int p = 0; p < A::kKPasses; ++p) {
     kt.pg[p] = -1;
-    kt.t[p] = u32x4{0u, 0u, 0u, 0u};
-  }
-  if (j0 >= P) return;
 #pragma unroll
-  for (int p = 0; p < A::kKPasses; ++p)
-    kt.pg[p] = wave_page(page_table, max_pages, j0 + (p * kWavesPerBlock + wave) * A::kPpw);
-#pragma unroll
-  for (int p = 0; p < A::kKPasses; ++p) {
-    const int j = k_pos<D>(j0, p);
-    const bool bad = kt.pg[p] < 0 || kt.pg[p] >= num_pages;
-    kt.t[p] = coh_ld16(kpool, (uint32_t)(page_row(bad ? 0 : kt.pg[p], j, kv_heads, h, D) +
-                                         ch * 8) * 2u);
+    for (int i = 0; i < A::kKChunks; ++i) kt.t[p][i] = u32x4{0u, 0u, 0u, 0u};
   }
+  if (j0 < P) k_tile_load_at<D>(j0, h, page_table, max_pages, kpool, num_pages, kv_heads, kt);
 }
 
 template <int D>
-__device__ __forceinline__ void v_tile_issue_at(int j0, int h, int P, const int* page_table,
-                                                int max_pages, const bf16* vpool, int num_pages,
-                                                int kv_heads, VTile<D>& vt) {
+__device__ __forceinline__ void v_tile_load_at(int j0, int h, const int* page_table,
+                                               int max_pages, const bf16* vpool, int num_pages,
+                                               int kv_heads, VTile<D>& vt) {
   using A = AttnShape<D>;
   static_assert(kPage % (kWave / A::kLpp) == 0, "a wave's pass stays in one page");
   const int ch = (int)threadIdx.x % A::kLpp;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
-#pragma unroll
-  for (int p = 0; p < A::kVPasses; ++p) {
-    vt.pg[p] = -1;
-    vt.t[p] = u32x4{0u, 0u, 0u, 0u};
-  }
-  if (j0 >= P) return;
 #pragma unroll
   for (int p = 0; p < A::kVPasses; ++p)
     vt.pg[p] = wave_page(page_table, max_pages, j0 + p * A::kGroups + wave * (kWave / A::kLpp));
@@ -596,6 +613,19 @@ __device__ __forceinline__ void v_tile_issue_at(int j0, int h, int P, const int*
     vt.t[p] = coh_ld16(vpool, (uint32_t)(page_row(bad ? 0 : vt.pg[p], j, kv_heads, h, D) +
                                          ch * 8) * 2u);
   }
+}
+
+template <int D>
+__device__ __forceinline__ void v_tile_issue_at(int j0, int h, int P, const int* page_table,
+                                                int max_pages, const bf16* vpool, int num_pages,
+                                                int kv_heads, VTile<D>& vt) {
+  using A = AttnShape<D>;
+#pragma unroll
+  for (int p = 0; p < A::kVPasses; ++p) {
+    vt.pg[p] = -1;
+    vt.t[p] = u32x4{0u, 0u, 0u, 0u};
+  }
+  if (j0 < P) v_tile_load_at<D>(j0, h, page_table, max_pages, vpool, num_pages, kv_heads, vt);
 }
 
 // The first tile of split `split` of a one-tile-per-split partition.
@@ -706,14 +736,12 @@ __device__ __forceinline__ void attn_scores_phase(
     int* err, int chunks = 1) {
   using A = AttnShape<D>;
   constexpr int kHalf = D / 2;
-  constexpr int kLpp = A::kLpp;
   static_assert(kHalf <= kWave, "one wave holds a head as (d, d + D/2) lane pairs");
   static_assert(G + 1 <= kWavesPerBlock, "one wave per vector");
   const int heads = kv_heads * G;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   // a split is `chunks` tiles of 64 positions (the persistent kernel uses one)
   const int j0 = split * chunks * kSplit;
-  const int ch = lane % kLpp;
 
   // per-phase launches hand scores, maxima and new-key scores to the next
   // kernel, so plain (cached, write-back) stores are enough there
@@ -811,42 +839,51 @@ __device__ __forceinline__ void attn_scores_phase(
     }
   }
 
-  // ---- scores over this split of the prior context
-  float qv[G][8];
+  // ---- scores over this split of the prior context: kKLanes lanes per
+  // position; lane part p holds dims 8 (8 i + p) .. +7 of chunk i
+  constexpr int kKL = A::kKLanes;
+  const int part = lane % kKL;
+  float qv[G][A::kKChunks][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qv[g][e] = qs[g][ch * 8 + e];
+    for (int i = 0; i < A::kKChunks; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[g][i][e] = qs[g][8 * (kKL * i + part) + e];
   float mymax[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) mymax[g] = kNegInf;
   bool page_ok = true;
-  KTile<D> cur = kt;
-  for (int c = 0; c < chunks; ++c) {
+  // tile c is reduced from `cur` while tile c + 1 loads into `nxt`; the two
+  // buffers alternate (no copy between them), and every tile but the last
+  // issues the next one's loads unconditionally, so the wait for `cur` never
+  // has to cover a path without them (which would make it wait for `nxt`)
+  const int ntl = (jend - j0 + kSplit - 1) / kSplit;    // tiles with a position < jend
+  auto tile = [&](int c, const KTile<D>& cur, KTile<D>& nxt, auto issue) {
     const int jc = j0 + c * kSplit;
-    if (jc >= jend) break;
-    // the next tile's loads go out before this one is reduced
-    KTile<D> nxt;
-    if (c + 1 < chunks)
-      k_tile_issue_at<D>(jc + kSplit, h, P, page_table, max_pages, kpool, num_pages,
-                         kv_heads, nxt);
+    if (decltype(issue)::value)
+      k_tile_load_at<D>(jc + kSplit, h, page_table, max_pages, kpool, num_pages, kv_heads, nxt);
 #pragma unroll
     for (int p = 0; p < A::kKPasses; ++p) {
       const int j = k_pos<D>(jc, p);
       const bool bad = cur.pg[p] < 0 || cur.pg[p] >= num_pages;
       if (j < jend && bad) page_ok = false;
       const bool valid = j < jend && !bad;
-      const uint32_t kw[4] = {cur.t[p].x, cur.t[p].y, cur.t[p].z, cur.t[p].w};
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float a = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          a = add_rounded2(a, qv[g][2 * e] * bf_lo(kw[e]), qv[g][2 * e + 1] * bf_hi(kw[e]));
-        a = group_sum<kLpp>(a);
+        for (int i = 0; i < A::kKChunks; ++i) {
+          const uint32_t kw[4] = {cur.t[p][i].x, cur.t[p][i].y, cur.t[p][i].z, cur.t[p][i].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            a = add_rounded2(a, qv[g][i][2 * e] * bf_lo(kw[e]),
+                             qv[g][i][2 * e + 1] * bf_hi(kw[e]));
+        }
+        a = group_sum<kKL>(a);
         const float sc = rbf(a);
         if (valid) {
-          if (ch == 0) {
+          if (part == 0) {
             if (kLL)
               S[g * kSplit + (j - j0)] = sc;
             else
@@ -856,7 +893,18 @@ __device__ __forceinline__ void attn_scores_phase(
         }
       }
     }
-    if (c + 1 < chunks) cur = nxt;
+  };
+  KTile<D> ka = kt, kb;
+  int c = 0;
+  for (; c + 2 < ntl; c += 2) {
+    tile(c, ka, kb, std::true_type{});
+    tile(c + 1, kb, ka, std::true_type{});
+  }
+  if (c + 1 < ntl) {
+    tile(c, ka, kb, std::true_type{});
+    tile(c + 1, kb, ka, std::false_type{});
+  } else if (c < ntl) {
+    tile(c, ka, kb, std::false_type{});
   }
   if (!page_ok) raise_error(err, kErrPageRange);
 #pragma unroll
@@ -978,19 +1026,27 @@ __device__ __forceinline__ void attn_pv_phase(
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   bool page_ok = true;
-  VTile<D> cur = vt;
-  for (int c = 0; c < chunks; ++c) {
+  // have the first scores here, on every path, so no wait for them is left
+  // pending into the tile loop (where it would also wait for the V rows the
+  // loop prefetches)
+  asm volatile("" ::"v"(sj_first));
+  // tile c is reduced from `cur` (scores sj) while tile c + 1's scores, then
+  // its V rows, load into `nxt` / sj_next -- the scores first: memory counters
+  // retire in order, so waiting for them does not wait for the V rows.  The
+  // buffers alternate (no copy between them), and every tile but the last
+  // issues the next one's loads unconditionally.
+  const int ntl = (jend - j0 + kSplit - 1) / kSplit;    // tiles with a position < jend
+  auto tile = [&](int c, const VTile<D>& cur, float sj, VTile<D>& nxt, float& sj_next,
+                  auto issue) {
     const int jc = j0 + c * kSplit;
-    if (jc >= jend) break;
-    // the next tile's loads go out before this one is reduced
-    VTile<D> nxt;
-    if (c + 1 < chunks)
-      v_tile_issue_at<D>(jc + kSplit, h, P, page_table, max_pages, vpool, num_pages, kv_heads,
-                         nxt);
+    if (decltype(issue)::value) {
+      // lanes past jend read a score of this row (in bounds, unused)
+      const int jn = jc + kSplit + lane;
+      sj_next = S[(int64_t)(h * G + wg) * s_stride + (jn < jend ? jn : jend - 1)];
+      v_tile_load_at<D>(jc + kSplit, h, page_table, max_pages, vpool, num_pages, kv_heads, nxt);
+    }
     if (wave < G) {
-      const float sj_raw =
-          c == 0 ? sj_first : S[(int64_t)(h * G + wg) * s_stride + jc + lane];
-      const float pj = (jc + lane < jend) ? rbf(expf(rbf(sj_raw - mw))) : 0.f;
+      const float pj = (jc + lane < jend) ? rbf(expf(rbf(sj - mw))) : 0.f;
       p[wave][lane] = pj;
       psum += wave_sum(pj);
     }
@@ -1027,7 +1083,19 @@ __device__ __forceinline__ void attn_pv_phase(
       }
     }
     __syncthreads();                        // p is rewritten by the next tile
-    if (c + 1 < chunks) cur = nxt;
+  };
+  VTile<D> va = vt, vb;
+  float sa = sj_first, sb = 0.f;
+  int c = 0;
+  for (; c + 2 < ntl; c += 2) {
+    tile(c, va, sa, vb, sb, std::true_type{});
+    tile(c + 1, vb, sb, va, sa, std::true_type{});
+  }
+  if (c + 1 < ntl) {
+    tile(c, va, sa, vb, sb, std::true_type{});
+    tile(c + 1, vb, sb, va, sa, std::false_type{});
+  } else if (c < ntl) {
+    tile(c, va, sa, vb, sb, std::false_type{});
   }
   if (!page_ok) raise_error(err, kErrPageRange);
   if (wave < G && lane == 0) {
