@@ -558,8 +558,21 @@ __device__ __forceinline__ int wave_page(const int* page_table, int max_pages, i
 // pass p, lane l of wave w reads position j0 + 8 (4 p + w) + l / 8, chunks
 // (l % 8) and (l % 8) + 8 (16 dims each), so a load instruction covers whole
 // 128-byte lines.  A tile that holds no prior position issues nothing.
+// K/V rows are read once per step.  Launches of one phase see the rows earlier
+// launches wrote without device-scope loads (kCoh = false: streaming loads);
+// the persistent kernel reads rows written earlier in the same launch, so its
+// loads are device-coherent.
+#ifndef TFD_KV_STREAM_POLICY
+#define TFD_KV_STREAM_POLICY 2
+#endif
+template <bool kCoh>
+__device__ __forceinline__ u32x4 kv_ld16(const void* base, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), byte_off, 0,
+                                               kCoh ? kCoherent : TFD_KV_STREAM_POLICY);
+}
+
 // (the loads only: the caller knows the tile holds a position below P)
-template <int D>
+template <int D, bool kCoh>
 __device__ __forceinline__ void k_tile_load_at(int j0, int h, const int* page_table,
                                                int max_pages, const bf16* kpool, int num_pages,
                                                int kv_heads, KTile<D>& kt) {
@@ -577,11 +590,11 @@ __device__ __forceinline__ void k_tile_load_at(int j0, int h, const int* page_ta
     const int64_t row = page_row(bad ? 0 : kt.pg[p], j, kv_heads, h, D) + (lane % A::kKLanes) * 8;
 #pragma unroll
     for (int i = 0; i < A::kKChunks; ++i)
-      kt.t[p][i] = coh_ld16(kpool, (uint32_t)(row + 64 * i) * 2u);
+      kt.t[p][i] = kv_ld16<kCoh>(kpool, (uint32_t)(row + 64 * i) * 2u);
   }
 }
 
-template <int D>
+template <int D, bool kCoh>
 __device__ __forceinline__ void k_tile_issue_at(int j0, int h, int P, const int* page_table,
                                                 int max_pages, const bf16* kpool, int num_pages,
                                                 int kv_heads, KTile<D>& kt) {
@@ -592,10 +605,11 @@ __device__ __forceinline__ void k_tile_issue_at(int j0, int h, int P, const int*
 #pragma unroll
     for (int i = 0; i < A::kKChunks; ++i) kt.t[p][i] = u32x4{0u, 0u, 0u, 0u};
   }
-  if (j0 < P) k_tile_load_at<D>(j0, h, page_table, max_pages, kpool, num_pages, kv_heads, kt);
+  if (j0 < P)
+    k_tile_load_at<D, kCoh>(j0, h, page_table, max_pages, kpool, num_pages, kv_heads, kt);
 }
 
-template <int D>
+template <int D, bool kCoh>
 __device__ __forceinline__ void v_tile_load_at(int j0, int h, const int* page_table,
                                                int max_pages, const bf16* vpool, int num_pages,
                                                int kv_heads, VTile<D>& vt) {
@@ -610,12 +624,12 @@ __device__ __forceinline__ void v_tile_load_at(int j0, int h, const int* page_ta
   for (int p = 0; p < A::kVPasses; ++p) {
     const int j = v_pos<D>(j0, p);
     const bool bad = vt.pg[p] < 0 || vt.pg[p] >= num_pages;
-    vt.t[p] = coh_ld16(vpool, (uint32_t)(page_row(bad ? 0 : vt.pg[p], j, kv_heads, h, D) +
+    vt.t[p] = kv_ld16<kCoh>(vpool, (uint32_t)(page_row(bad ? 0 : vt.pg[p], j, kv_heads, h, D) +
                                          ch * 8) * 2u);
   }
 }
 
-template <int D>
+template <int D, bool kCoh>
 __device__ __forceinline__ void v_tile_issue_at(int j0, int h, int P, const int* page_table,
                                                 int max_pages, const bf16* vpool, int num_pages,
                                                 int kv_heads, VTile<D>& vt) {
@@ -625,21 +639,24 @@ __device__ __forceinline__ void v_tile_issue_at(int j0, int h, int P, const int*
     vt.pg[p] = -1;
     vt.t[p] = u32x4{0u, 0u, 0u, 0u};
   }
-  if (j0 < P) v_tile_load_at<D>(j0, h, page_table, max_pages, vpool, num_pages, kv_heads, vt);
+  if (j0 < P)
+    v_tile_load_at<D, kCoh>(j0, h, page_table, max_pages, vpool, num_pages, kv_heads, vt);
 }
 
 // The first tile of split `split` of a one-tile-per-split partition.
-template <int D>
+template <int D, bool kCoh>
 __device__ __forceinline__ void k_tile_issue(int split, int h, int P, const int* page_table,
                                              int max_pages, const bf16* kpool, int num_pages,
                                              int kv_heads, KTile<D>& kt) {
-  k_tile_issue_at<D>(split * kSplit, h, P, page_table, max_pages, kpool, num_pages, kv_heads, kt);
+  k_tile_issue_at<D, kCoh>(split * kSplit, h, P, page_table, max_pages, kpool, num_pages,
+                           kv_heads, kt);
 }
-template <int D>
+template <int D, bool kCoh>
 __device__ __forceinline__ void v_tile_issue(int split, int h, int P, const int* page_table,
                                              int max_pages, const bf16* vpool, int num_pages,
                                              int kv_heads, VTile<D>& vt) {
-  v_tile_issue_at<D>(split * kSplit, h, P, page_table, max_pages, vpool, num_pages, kv_heads, vt);
+  v_tile_issue_at<D, kCoh>(split * kSplit, h, P, page_table, max_pages, vpool, num_pages,
+                           kv_heads, vt);
 }
 
 // ---------------------------------------------------------------------------
@@ -862,7 +879,8 @@ __device__ __forceinline__ void attn_scores_phase(
   auto tile = [&](int c, const KTile<D>& cur, KTile<D>& nxt, auto issue) {
     const int jc = j0 + c * kSplit;
     if (decltype(issue)::value)
-      k_tile_load_at<D>(jc + kSplit, h, page_table, max_pages, kpool, num_pages, kv_heads, nxt);
+      k_tile_load_at<D, kLL>(jc + kSplit, h, page_table, max_pages, kpool, num_pages, kv_heads,
+                             nxt);
 #pragma unroll
     for (int p = 0; p < A::kKPasses; ++p) {
       const int j = k_pos<D>(jc, p);
@@ -1043,7 +1061,8 @@ __device__ __forceinline__ void attn_pv_phase(
       // lanes past jend read a score of this row (in bounds, unused)
       const int jn = jc + kSplit + lane;
       sj_next = S[(int64_t)(h * G + wg) * s_stride + (jn < jend ? jn : jend - 1)];
-      v_tile_load_at<D>(jc + kSplit, h, page_table, max_pages, vpool, num_pages, kv_heads, nxt);
+      v_tile_load_at<D, kLL>(jc + kSplit, h, page_table, max_pages, vpool, num_pages, kv_heads,
+                             nxt);
     }
     if (wave < G) {
       const float pj = (jc + lane < jend) ? rbf(expf(rbf(sj - mw))) : 0.f;

@@ -387,7 +387,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_scores_b(
   const int P = coh_ldi(pos + b);
   const int* pt = page_table + (int64_t)b * max_pages;
   KTile<D> kt;
-  k_tile_issue_at<D>(blockIdx.x * chunks * kSplit, blockIdx.y, P, pt, max_pages, kpool,
+  k_tile_issue_at<D, false>(blockIdx.x * chunks * kSplit, blockIdx.y, P, pt, max_pages, kpool,
                      num_pages, kv_heads, kt);
   const QKPre pre = qk_prefetch<D, G>(P, P, gq, gk, cos_t, sin_t, rope_rows, pt, max_pages);
   __shared__ __attribute__((aligned(16))) uint32_t hs[(G + 2) * D / 2];
@@ -418,7 +418,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_pv_b(
   if (P < 0 || P >= max_pages * kPage) P = 0;
   const int* pt = page_table + (int64_t)b * max_pages;
   VTile<D> vt;
-  v_tile_issue_at<D>(blockIdx.x * chunks * kSplit, blockIdx.y, P, pt, max_pages, vpool,
+  v_tile_issue_at<D, false>(blockIdx.x * chunks * kSplit, blockIdx.y, P, pt, max_pages, vpool,
                      num_pages, kv_heads, vt);
   attn_pv_phase<D, G, false, NoHook, PackedOut>(
       blockIdx.x, blockIdx.y, nsplit, qkv + (int64_t)b * ldq, P, pt, max_pages, vpool,

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_rope_scores(
     int* err) {
   const int P = coh_ldi(cache_len);
   KTile<D> kt;
-  k_tile_issue<D>(blockIdx.x, blockIdx.y, P, page_table, max_pages, kpool, num_pages, kv_heads,
+  k_tile_issue<D, false>(blockIdx.x, blockIdx.y, P, page_table, max_pages, kpool, num_pages, kv_heads,
                   kt);
   const int rp = coh_ldi(rope_pos);
   const QKPre pre = qk_prefetch<D, G>(rp, P, gq, gk, cos_t, sin_t, rope_rows, page_table,
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_pv_combine(
   int P = coh_ldi(cache_len);
   if (P < 0 || P >= max_pages * kPage) P = 0;
   VTile<D> vt;
-  v_tile_issue<D>(blockIdx.x, blockIdx.y, P, page_table, max_pages, vpool, num_pages, kv_heads,
+  v_tile_issue<D, false>(blockIdx.x, blockIdx.y, P, page_table, max_pages, vpool, num_pages, kv_heads,
                   vt);
   attn_pv_phase<D, G, false>(blockIdx.x, blockIdx.y, gridDim.x, qkv, P, page_table, max_pages,
                              vpool, num_pages, kv_heads, S, s_stride, smax, snew, part_sum,
@@ -305,9 +305,9 @@ __global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, i
       KTile<D> kt;
       VTile<D> vt;
       const int s0 = vb0 < nvb ? vb0 % parts : parts, h0 = vb0 / parts;
-      k_tile_issue<D>(s0, h0, P, a.page_table, a.max_pages, (const bf16*)w.k_pool, a.num_pages,
+      k_tile_issue<D, true>(s0, h0, P, a.page_table, a.max_pages, (const bf16*)w.k_pool, a.num_pages,
                       a.kv_heads, kt);
-      v_tile_issue<D>(s0, h0, P, a.page_table, a.max_pages, (const bf16*)w.v_pool, a.num_pages,
+      v_tile_issue<D, true>(s0, h0, P, a.page_table, a.max_pages, (const bf16*)w.v_pool, a.num_pages,
                       a.kv_heads, vt);
       const QKPre pre = qk_prefetch<D, G>(P, P, (const bf16*)w.gamma_q, (const bf16*)w.gamma_k,
                                           (const bf16*)a.cos_table, (const bf16*)a.sin_table,
@@ -317,7 +317,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, i
       for (int vb = vb0; vb < nvb; vb += nb) {
         const int split = vb % parts, h = vb / parts;
         if (vb != vb0)
-          k_tile_issue<D>(split, h, P, a.page_table, a.max_pages, (const bf16*)w.k_pool,
+          k_tile_issue<D, true>(split, h, P, a.page_table, a.max_pages, (const bf16*)w.k_pool,
                           a.num_pages, a.kv_heads, kt);
         stage_head_ll<D, G>(h, a.heads, a.kv_heads, ll, hs, err);
         __syncthreads();
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_persistent(TfdDecodeArgs a, i
       for (int vb = vb0; vb < nvb; vb += nb) {
         const int split = vb % parts, h = vb / parts;
         if (vb != vb0)
-          v_tile_issue<D>(split, h, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
+          v_tile_issue<D, true>(split, h, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
                           a.num_pages, a.kv_heads, vt);
         if (vb == vb0) stamp(tl);
         const int lv = (vb - vb0) / nb;
