@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TFD_ABI_VERSION 8
+#define TFD_ABI_VERSION 9
 
 /* gemv prologues / epilogues */
 #define TFD_PRO_PLAIN 0  /* x used as given */
@@ -192,9 +192,12 @@ int tfd_attn_pv_combine_paged_batched(
     float* part_sum, float* part_out, int nsplit, int split_tiles, int32_t* counters,
     void* attn_out, int32_t* err, void* stream);
 
-/* Greedy pick per row: the first maximal logit (ref_src/generation.py:24-26). */
+/* Greedy pick per row: the first maximal logit (ref_src/generation.py:24-26).  With
+ * `work` (rows * TFD_ARGMAX_WORK int32) the rows are scanned by 64 blocks each and the
+ * chunk winners reduced by a second launch; NULL scans each row with one block. */
+#define TFD_ARGMAX_WORK 128
 int tfd_argmax_rows(const float* logits, int ldl, int rows, int vocab, int32_t* pick,
-                    void* stream);
+                    int32_t* work, void* stream);
 
 /* The step's last node per sequence (the batch form of tfd_argmax_finalize,
  * fast/kernels.py:591-637): record pick[b] at sam[b][pos[b]], feed the next prompt

@@ -139,6 +139,31 @@ def test_rmsnorm_rows_operand_order(gpu_device, rows):
     assert torch.equal(from_operand_order(packed, rows, H), flat)
 
 
+@pytest.mark.parametrize("two_stage", [False, True], ids=["one-block", "chunked"])
+def test_argmax_rows_first_maximum(gpu_device, two_stage):
+    """The first maximal logit of each row, as torch.argmax picks it, with ties
+    placed across chunk boundaries, a row of equal values, a NaN-only row (pick
+    0) and NaNs beside the maximum."""
+    g = torch.Generator().manual_seed(3)
+    rows, V = 7, 151936
+    x = torch.randn(rows, V, generator=g).to(torch.bfloat16).float()
+    x[1, [5, 2374, 2375, 100000]] = 9.0            # ties: the first wins
+    x[2] = 0.5                                     # all equal: index 0
+    x[3] = float("nan")                            # no pick: 0
+    x[4, 77] = float("nan")
+    x[4, 150000] = 7.0
+    x[5, V - 1] = 50.0                             # the last column
+    want = torch.nan_to_num(x, nan=-float("inf")).argmax(dim=1).to(torch.int32)
+    want[3] = 0
+    xd = x.to(gpu_device)
+    pick = torch.zeros(rows, dtype=torch.int32, device=gpu_device)
+    work = torch.zeros(rows * _lib.ARGMAX_WORK, dtype=torch.int32, device=gpu_device)
+    lib().tfd_argmax_rows(ptr(xd), V, rows, V, ptr(pick), ptr(work) if two_stage else None,
+                          torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(pick.cpu(), want), (pick.cpu(), want)
+
+
 def test_skinny_gemm_shapes_share_one_work_buffer(gpu_device):
     """GEMMs of different tile counts and slice counts in a row on one work
     buffer (the layer's q/k/v, o, gate/up and down) give the bits each gives on

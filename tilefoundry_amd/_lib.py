@@ -13,13 +13,14 @@ from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS = 0, 1, 2, 3
 ERR_TOKEN_RANGE, ERR_POS_RANGE, ERR_PAGE_RANGE, ERR_STEP_RANGE, ERR_SYNC = 1, 2, 4, 8, 16
 PAGE_SIZE = 16
 SKINNY_COUNTERS = 16384     # tile counters at the start of a skinny-GEMM work buffer
+ARGMAX_WORK = 128           # int32 per row of tfd_argmax_rows' two-stage work buffer
 ATTN_SPLIT = 64
 
 P = c_void_p
@@ -47,7 +48,7 @@ SIGNATURES: dict[str, list] = {
                                            F, P, I, P, P, I, I, P, P],
     "tfd_attn_pv_combine_paged_batched": [P, I, P, P, I, P, I, I, I, I, I, P, I, P, P, P, P, I,
                                           I, P, P, P, P],
-    "tfd_argmax_rows": [P, I, I, I, P, P],
+    "tfd_argmax_rows": [P, I, I, I, P, P, P],
     "tfd_finalize_rows": [P, I, P, I, P, P, P, P, I, I, P, P, I, I, I, P, P],
     "tfd_embed_rows_bf16": [P, P, P, I, I, I, I, P, P],
     "tfd_decode_persistent": [P, I, I, P],

@@ -474,6 +474,74 @@ __global__ __launch_bounds__(1024) void k_argmax_rows(const float* __restrict__ 
   }
 }
 
+// The same pick in two stages for long rows: kArgChunks blocks per row each
+// find their chunk's first maximum, then one wave per row picks the first
+// maximum among the chunk winners (ties go to the lower index: the chunks are
+// in index order and `better` prefers the lower index).
+constexpr int kArgChunks = 64;
+
+__global__ __launch_bounds__(kBlock) void k_argmax_chunks(const float* __restrict__ logits,
+                                                          int ldl, int V,
+                                                          int* __restrict__ part) {
+  const int row = blockIdx.y, chunk = blockIdx.x;
+  const int per = (V + kArgChunks - 1) / kArgChunks;
+  const int k0 = chunk * per;
+  const int k1 = (k0 + per < V) ? k0 + per : V;
+  const float* r = logits + (int64_t)row * ldl;
+  float b = kNegInf;
+  int i = 0x7fffffff;
+  for (int k = k0 + (int)threadIdx.x; k < k1; k += kBlock) {
+    const float v = r[k];
+    if (better(v, k, b, i)) {
+      b = v;
+      i = k;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ob = __shfl_xor(b, m, kWave);
+    const int oi = __shfl_xor(i, m, kWave);
+    if (better(ob, oi, b, i)) {
+      b = ob;
+      i = oi;
+    }
+  }
+  __shared__ float sv[kWavesPerBlock];
+  __shared__ int si[kWavesPerBlock];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = b;
+    si[wave] = i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kWavesPerBlock; ++w)
+      if (better(sv[w], si[w], b, i)) {
+        b = sv[w];
+        i = si[w];
+      }
+    part[((int64_t)row * kArgChunks + chunk) * 2] = __float_as_int(b);
+    part[((int64_t)row * kArgChunks + chunk) * 2 + 1] = i;
+  }
+}
+
+__global__ __launch_bounds__(kWave) void k_argmax_pick(const int* __restrict__ part, int V,
+                                                       int* __restrict__ pick) {
+  const int row = blockIdx.x, lane = threadIdx.x;
+  float b = __int_as_float(part[((int64_t)row * kArgChunks + lane) * 2]);
+  int i = part[((int64_t)row * kArgChunks + lane) * 2 + 1];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ob = __shfl_xor(b, m, kWave);
+    const int oi = __shfl_xor(i, m, kWave);
+    if (better(ob, oi, b, i)) {
+      b = ob;
+      i = oi;
+    }
+  }
+  if (lane == 0) pick[row] = (i >= 0 && i < V) ? i : 0;   // an all-NaN row has no pick
+}
+
 __global__ __launch_bounds__(kBlock) void k_finalize_rows(
     const int* __restrict__ pick, const int* __restrict__ inp, int ld_inp,
     const int* __restrict__ plen, int64_t* __restrict__ ids, int* __restrict__ pos,
@@ -763,12 +831,18 @@ int tfd_attn_pv_combine_paged_batched(
 }
 
 int tfd_argmax_rows(const float* logits, int ldl, int rows, int vocab, int32_t* pick,
-                    void* stream) {
+                    int32_t* work, void* stream) {
   if (!logits || !pick) return fail(kBadArg, "argmax_rows: null pointer");
-  if (rows <= 0 || vocab <= 0 || ldl < vocab)
+  if (rows <= 0 || rows > 65535 || vocab <= 0 || ldl < vocab)
     return fail(kBadShape, "argmax_rows: rows=%d vocab=%d ldl=%d", rows, vocab, ldl);
-  hipLaunchKernelGGL(k_argmax_rows, dim3(rows), dim3(1024), 0, (hipStream_t)stream, logits, ldl,
-                     vocab, pick);
+  auto s = (hipStream_t)stream;
+  if (!work) {
+    hipLaunchKernelGGL(k_argmax_rows, dim3(rows), dim3(1024), 0, s, logits, ldl, vocab, pick);
+  } else {
+    hipLaunchKernelGGL(k_argmax_chunks, dim3(kArgChunks, rows), dim3(kBlock), 0, s, logits, ldl,
+                       vocab, work);
+    hipLaunchKernelGGL(k_argmax_pick, dim3(rows), dim3(kWave), 0, s, work, vocab, pick);
+  }
   return launched("argmax_rows");
 }
 

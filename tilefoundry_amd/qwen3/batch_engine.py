@@ -151,6 +151,7 @@ class BatchEngine:
         self.counters = z(B, self.HKV, dtype=i32)
         self.logits = z(B, self.V, dtype=f32)
         self.pick = z(B, dtype=i32)
+        self.argmax_work = z(B * _lib.ARGMAX_WORK, dtype=i32)
         self.pos = z(B, dtype=i32)
         self.ids = z(B, dtype=torch.int64)
         self.inp = z(B, self.nsteps, dtype=i32)
@@ -209,7 +210,8 @@ class BatchEngine:
                                 ptr(self.xn), 0, B, H, self.eps, 1, s)
         self._gemm(self.xn, self.w_head, H, self.V, _lib.EPI_LOGITS, None, self.logits,
                    self.V, s)
-        L.tfd_argmax_rows(ptr(self.logits), self.V, B, self.V, ptr(self.pick), s)
+        L.tfd_argmax_rows(ptr(self.logits), self.V, B, self.V, ptr(self.pick),
+                          ptr(self.argmax_work), s)
         L.tfd_finalize_rows(ptr(self.pick), B, ptr(self.inp), self.nsteps, ptr(self.plen),
                             ptr(self.ids), ptr(self.pos), ptr(self.sam), self.nsteps,
                             self.nsteps, ptr(self.w_embed), ptr(self.hid), H, H, self.V,
