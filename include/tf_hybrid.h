@@ -1,0 +1,142 @@
+/* Decode-step pieces of the hybrid models on gfx950 (workloads C4 and C5).
+ *
+ * C4 is Qwen3.5-35B-A3B-style (gated DeltaNet + GQA layers, softmax-top-8 MoE);
+ * its arithmetic follows the reference example's plain-torch twin
+ * (examples/qwen3_5_35b_a3b-tilelang/kernels/torch_ref.py:22-40: f32 activations
+ * and state, matmuls at the weights' bf16 with one rounding of the f32 sum).
+ * C5 is Granite-4.0-H-style (Mamba2 + GQA layers, top-10-then-softmax MoE) with
+ * fp8-e4m3fn weights and per-output-channel f32 scales; its arithmetic follows
+ * the authored HIR (examples/granite_4_0_h_small-cuda/model.py: bf16 ops rounded
+ * as written, f32 where it casts to f32).
+ *
+ * Every entry returns 0 or an error (tfd_last_error() holds the text), takes
+ * device pointers and a hipStream_t, allocates nothing and does not synchronise.
+ * Batch rows are sequences, one token each.  The projections around these
+ * entries are tfd_gemm_skinny_bf16 / tfd_gemm_skinny_fp8 (tf_decode.h); GEMM
+ * inputs are in the skinny GEMMs' operand order (tf_decode.h). */
+#ifndef TF_HYBRID_H
+#define TF_HYBRID_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* fp8-e4m3fn weights with one f32 scale per output row (workload C5's
+ * "fp8 per-channel" projections; SURVEY entry gemv_fp8_perchannel).  The
+ * reference has no fp8 GEMV: its Granite projections are bf16 nn.Linear
+ * (examples/granite_4_0_h_small-cuda/model.py:140-152 in_projection, :266-270
+ * out_proj, :294-330 attention q/k/v/o, :459-471 shared MLP), so this build
+ * defines W[n][k] = f32(e4m3fn(code[n][k])) * scale[n].
+ * tfd_pack_skinny_fp8 lays codes [N][K] (row stride ldw bytes) out in 512-byte
+ * blocks of 16 rows x 32 k, the fp8 counterpart of tfd_pack_skinny_bf16; `packed`
+ * holds ceil(N/16) * 16 * K bytes.  K % 256 == 0. */
+int tfd_pack_skinny_fp8(const void* w, int ldw, int N, int K, void* packed, void* stream);
+
+/* Y[m][n] = scale[n] * sum_k X[m][k] e4m3(W[n][k]) for m < M <= 32 (f32 sums,
+ * one bf16 rounding per output), X in operand order, W packed by
+ * tfd_pack_skinny_fp8, scale f32 [N]; the epilogues of tfd_gemm_skinny_bf16.
+ * K splits across the waves of one block (no work buffer). */
+int tfd_gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M, int K, int N,
+                        int epilogue, const void* resid, int ldr, void* out, int ldo,
+                        void* stream);
+
+#define TFD_ROUTE_SOFTMAX_TOPK 0 /* C4: softmax over all experts, top k, renormalise */
+#define TFD_ROUTE_TOPK_SOFTMAX 1 /* C5: top k logits, softmax over them, bf16 weights */
+
+/* The routers after their projection: logits f32 [rows][ldl] (experts <= 256)
+ * -> weights f32 [rows][k] (C5: bf16 values) and expert ids int32 [rows][k],
+ * largest first with ties to the lower id (torch.topk's order).
+ * Replaces Qwen3_5Router.routing's softmax/topk/renormalise
+ * (tests/models/qwen3_5_35b_a3b/model.py:355-366; torch_ref.py:417-430; SURVEY
+ * entry moe_router_softmax_topk) and GraniteRouter.routing's topk/softmax
+ * (examples/granite_4_0_h_small-cuda/model.py:376-390; moe_router_topk_softmax).
+ * The reference returns int64 ids; these are int32. */
+int tfd_route_topk(const float* logits, int ldl, int rows, int experts, int k, int mode,
+                   float* weights, int32_t* idx, void* stream);
+
+#define TFD_POLICY_F32 0  /* C4 (torch_ref policy) */
+#define TFD_POLICY_BF16 1 /* C5 (HIR policy) */
+
+/* Routed experts + shared expert of the MoE block for a batch, given the
+ * routing (replaces Qwen3_5MoE.routed_experts/shared_expert/experts,
+ * tests/models/qwen3_5_35b_a3b/model.py:383-456 / torch_ref.py:451-530, and
+ * GraniteMoE.routed_experts/shared_mlp/experts, granite model.py:406-471; SURVEY
+ * entries moe_experts_gateup / moe_experts_down).  Weights keep the reference's
+ * (out, in) rows: w_gate/w_up [E][I][H], w_down [E][H][I]; the shared expert's
+ * gate rows then up rows in w_shared_in [2 IS][H] and w_shared_out [H][IS].  With
+ * fp8 != 0 every weight is e4m3fn bytes with an f32 scale per row (s_*).  C4's
+ * shared expert has a sigmoid gate row w_shared_scale [H] (bf16, NULL for C5).
+ * x [rows][H] bf16 (the post-norm tokens); out f32 [rows][H] (C5: bf16 values).
+ * Work: hidden bf16 [rows][k + 1][hidden_ld] and shared_scale f32 [rows].
+ * H <= 4096 and I, IS <= 2048, multiples of 64. */
+typedef struct {
+  const void* x;
+  const float* weights;
+  const int32_t* idx;
+  const void *w_gate, *w_up, *w_down;
+  const float *s_gate, *s_up, *s_down;
+  const void *w_shared_in, *w_shared_out;
+  const float *s_shared_in, *s_shared_out;
+  const void* w_shared_scale;
+  void* hidden;
+  float* shared_scale;
+  float* out;
+  int rows, k, experts, hidden_size, inter, shared_inter, hidden_ld;
+  int fp8, policy;
+  int32_t* err;
+} TfdMoeArgs;
+int tfd_moe_experts(const TfdMoeArgs* args, void* stream);
+
+/* Gated DeltaNet at one token per sequence, everything between the in- and
+ * out-projections of Qwen3_5LinearAttention.linear_attention: conv_step,
+ * l2_normalise, beta/g, delta_step and the gated RMS norm
+ * (tests/models/qwen3_5_35b_a3b/model.py:124-232; torch_ref.py:188-312; SURVEY
+ * entry gdn_conv_delta).  proj f32 [rows][proj_ld] holds this token's
+ * projections (bf16 values): the conv channels q|k|v (2 hk dk + hv dv), then z
+ * (hv dv), b (hv), a (hv).  conv_in/conv_out f32 [rows][CONV][3] (distinct
+ * buffers: the window after this token goes to conv_out); state f32
+ * [rows][hv][dk][dv] is updated in place.  out: the gated read-out in operand
+ * order (32 x hv dv) for the out-projection.  dk = dv = 128, conv kernel 4. */
+typedef struct {
+  const float* proj;
+  int proj_ld;
+  const float* conv_in;
+  float* conv_out;
+  float* state;
+  const void *conv_w, *a_log, *dt_bias, *gamma;
+  void* out;
+  int rows, key_heads, value_heads, head_k_dim, head_v_dim, conv_kernel;
+  float l2_eps, rms_eps;
+} TfdGdnArgs;
+int tfd_gdn_step(const TfdGdnArgs* args, void* stream);
+
+/* Mamba2 at one token per sequence, everything between in_proj and out_proj of
+ * GraniteMamba.mamba_mixer: conv_step, ssm_step and gated_out's RMSNormGated
+ * (examples/granite_4_0_h_small-cuda/model.py:154-270; SURVEY entries
+ * mamba_conv / mamba_ssm / rmsnorm_gated).  proj bf16 [rows][proj_ld]: gate
+ * (EXP), the conv channels x|B|C (EXP + 2 ns), dt (heads); conv_in/conv_out bf16
+ * [rows][CONV][3] (distinct); state f32 [rows][heads][64][128] in place.  Work:
+ * gated f32 [rows][EXP], ssq f32 [rows][heads].  out: the normed gated output in
+ * operand order (32 x EXP) for out_proj.  head_dim 64, state 128, 1 group. */
+typedef struct {
+  const void* proj;
+  int proj_ld;
+  const void* conv_in;
+  void* conv_out;
+  float* state;
+  const void *conv_w, *conv_b, *a_log, *dt_bias, *d_skip, *gamma;
+  float* gated;
+  float* ssq;
+  void* out;
+  int rows, heads, head_dim, state_dim, groups, conv_kernel;
+  float eps;
+} TfdMambaArgs;
+int tfd_mamba_step(const TfdMambaArgs* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

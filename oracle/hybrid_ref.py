@@ -1,0 +1,234 @@
+"""The hybrid models' per-token mixers, routers and experts (CPU torch).
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+Two arithmetic policies, each the one the reference states for its model:
+
+* **C4, Qwen3.5-35B-A3B** -- the example's plain-torch twin
+  ``examples/qwen3_5_35b_a3b-tilelang/kernels/torch_ref.py`` (its "dtype policy",
+  ``:22-40``): activations and state f32; a matmul runs at the weights' dtype, so
+  the activation is cast to bf16, the product summed in f32 and rounded to bf16
+  once, and handed on as f32 (``_mm``/``_wm`` ``:134-143``); everything else in
+  f32.  The GDN recurrent state is f32 (the benchmark's "fp32 recurrent state").
+* **C5, Granite-4.0-H** -- the authored HIR
+  ``examples/granite_4_0_h_small-cuda/model.py``: bf16 activations, every binary
+  op rounded to bf16 (binary ops never promote, ``ir/hir/math/binary.py:130-139``),
+  the explicit f32 casts where the HIR writes them, f32 SSM state.  Weights are
+  fp8-e4m3fn with one f32 scale per output channel (the benchmark's C5; the
+  reference has no fp8 GEMV, so the build defines ``W = f32(e4m3) * scale[out]``
+  with f32 accumulation -- parity there is against that definition).
+
+Every function cites the reference function it restates.  Matmul sums run in f64
+(``exact=True``) or f32; the kernels' f32 sums differ only in order.
+"""
+from __future__ import annotations
+
+import torch
+
+F32, BF16 = torch.float32, torch.bfloat16
+
+
+def bf(x: torch.Tensor) -> torch.Tensor:
+    """Round to bf16 and hand back as f32."""
+    return x.to(BF16).float()
+
+
+def mm_rows(w: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """sum_k w[n][k] x[..., k] in f64, as f32 (w [N][K] (out, in), x [..., K])."""
+    return (x.double() @ w.double().t()).float()
+
+
+# ---------------------------------------------------------------------------
+# fp8-e4m3fn weights with per-output-channel scales (a23)
+# ---------------------------------------------------------------------------
+def fp8_dequant(codes: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """``W = f32(e4m3fn(code)) * scale[out]``: codes uint8 [N][K], scale f32 [N].
+    Every e4m3fn value is exact in f32 (``torch.float8_e4m3fn -> float32``)."""
+    return codes.view(torch.float8_e4m3fn).float() * scale.float()[:, None]
+
+
+def gemv_fp8(codes: torch.Tensor, scale: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """bf16 activations x [B][K] against fp8 rows: y[b][n] = scale[n] *
+    sum_k e4m3(w[n][k]) * x[b][k], f32 (the build's definition; see the header)."""
+    raw = codes.view(torch.float8_e4m3fn).double()
+    return ((x.double() @ raw.t()) * scale.double()[None, :]).float()
+
+
+# ---------------------------------------------------------------------------
+# Routers (a17, a21)
+# ---------------------------------------------------------------------------
+def topk_ordered(v: torch.Tensor, k: int):
+    """``torch.topk(v, k)`` with its tie order fixed: largest first, equal values
+    by ascending index.  torch.topk leaves the order of equal values unspecified
+    (its CPU and GPU kernels differ), and bf16-valued router logits tie often
+    (256 experts, 8 mantissa bits); the build's routers use this order."""
+    vals, idx = torch.sort(v, dim=-1, descending=True, stable=True)
+    return vals[..., :k], idx[..., :k]
+
+
+def route_softmax_topk(logits: torch.Tensor, k: int):
+    """Qwen3.5 router after its projection (torch_ref.py:417-430, HF
+    ``Qwen3_5MoeTopKRouter``): softmax over every expert in f32, the top k
+    (largest first, ties to the lower index), renormalised by their sum.
+    -> (weights f32 [B][k], indices i64 [B][k])."""
+    probs = torch.softmax(logits.float(), dim=-1)
+    vals, idx = topk_ordered(probs, k)
+    return vals / vals.sum(dim=-1, keepdim=True), idx
+
+
+def route_topk_softmax(logits: torch.Tensor, k: int):
+    """Granite router after its projection (model.py:376-390, HF
+    ``GraniteMoeHybridTopKRouter``): the top k logits (f32, ties to the lower
+    index), then a softmax over those k alone, cast to the activation dtype.
+    -> (weights as bf16 values in f32 [B][k], indices i64 [B][k])."""
+    vals, idx = topk_ordered(logits.float(), k)
+    return bf(torch.softmax(vals, dim=-1)), idx
+
+
+# ---------------------------------------------------------------------------
+# Experts (a18, a22)
+# ---------------------------------------------------------------------------
+def moe_c4(x, weights, idx, w_gate, w_up, w_down, ws_gate, ws_up, ws_down, ws_scale):
+    """Qwen3.5 routed + shared experts, torch_ref policy (torch_ref.py:451-530).
+
+    x [B][H] (bf16 values), weights f32 [B][k], idx [B][k];
+    w_gate/w_up [E][I][H], w_down [E][H][I] (out, in); shared ws_gate/ws_up
+    [IS][H], ws_down [H][IS], ws_scale [1][H] (the (out, in) transposes of the
+    reference's (in, out) shared weights).  -> f32 [B][H]."""
+    B = x.shape[0]
+    out = torch.zeros(B, w_down.shape[1])
+    for b in range(B):
+        xb = bf(x[b])
+        routed = torch.zeros(w_down.shape[1])
+        for s in range(idx.shape[1]):
+            e = int(idx[b, s])
+            g = bf(mm_rows(w_gate[e].float(), xb))
+            u = bf(mm_rows(w_up[e].float(), xb))
+            h = torch.nn.functional.silu(g) * u                  # f32
+            d = bf(mm_rows(w_down[e].float(), bf(h)))            # _wm casts h to bf16
+            routed = routed + d * weights[b, s].float()
+        g = bf(mm_rows(ws_gate.float(), xb))
+        u = bf(mm_rows(ws_up.float(), xb))
+        dense = bf(mm_rows(ws_down.float(), bf(torch.nn.functional.silu(g) * u)))
+        scale = torch.sigmoid(bf(mm_rows(ws_scale.float(), xb)))
+        out[b] = routed + dense * scale
+    return out
+
+
+def moe_c5(x, weights, idx, g_codes, g_scale, u_codes, u_scale, d_codes, d_scale,
+           si_codes, si_scale, so_codes, so_scale):
+    """Granite routed experts + shared MLP, HIR policy with fp8 weights
+    (model.py:406-471).  x [B][H] (bf16 values), weights [B][k] (bf16 values);
+    expert codes [E][I][H] / [E][H][I] with scales [E][I] / [E][H]; shared
+    w_shared_in [2 IS][H] and w_shared_out [H][IS] as codes + per-row scales.
+    -> bf16 values [B][H]."""
+    B, H = x.shape
+    out = torch.zeros(B, H)
+    for b in range(B):
+        xb = bf(x[b])
+        weighted = []
+        for s in range(idx.shape[1]):
+            e = int(idx[b, s])
+            g = bf(gemv_fp8(g_codes[e], g_scale[e], xb[None])[0])
+            u = bf(gemv_fp8(u_codes[e], u_scale[e], xb[None])[0])
+            inner = bf(bf(torch.nn.functional.silu(g)) * u)
+            d = bf(gemv_fp8(d_codes[e], d_scale[e], inner[None])[0])
+            weighted.append(bf(d * weights[b, s].float()))
+        # tf.reduce(kind="sum") over the slots in bf16: one f32 sum, rounded once
+        routed = bf(torch.stack(weighted).double().sum(dim=0).float())
+        both = bf(gemv_fp8(si_codes, si_scale, xb[None])[0])
+        IS = si_codes.shape[0] // 2
+        inner = bf(bf(torch.nn.functional.silu(both[:IS])) * both[IS:])
+        shared = bf(gemv_fp8(so_codes, so_scale, inner[None])[0])
+        out[b] = bf(routed + shared)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Gated DeltaNet decode step (a15), torch_ref policy
+# ---------------------------------------------------------------------------
+def gdn_step(proj, conv_state, state, conv_w, a_log, dt_bias, gamma_gdn, *, hk, hv, dk, dv,
+             l2_eps=1e-6, rms_eps=1e-6):
+    """Everything of ``linear_attention`` between the in-projection and the
+    out-projection (torch_ref.py:188-312; model.py:124-232), for a batch.
+
+    proj  [B][2*KEY + VAL + 2*HV]: this token's projections, f32 of bf16 values,
+          in the order [q | k | v] (the conv channels), z, b, a
+    conv_state [B][CONV][KERNEL-1] f32, state [B][HV][DK][DV] f32,
+    conv_w [CONV][KERNEL], a_log/dt_bias [HV], gamma_gdn [DV].
+    -> (gated f32 [B][VAL] (before the out-projection's bf16 cast),
+        new conv_state, new state)."""
+    B = proj.shape[0]
+    key, val = hk * dk, hv * dv
+    conv = 2 * key + val
+    entry = proj[:, :conv]
+    z = proj[:, conv:conv + val]
+    b_raw = proj[:, conv + val:conv + val + hv]
+    a_raw = proj[:, conv + val + hv:conv + val + 2 * hv]
+    window = torch.cat((conv_state.float(), entry[:, :, None].float()), dim=2)
+    mixed = torch.nn.functional.silu((window * conv_w.float()[None]).sum(dim=-1))
+    q = mixed[:, :key].reshape(B, hk, dk).repeat_interleave(hv // hk, dim=1)
+    k = mixed[:, key:2 * key].reshape(B, hk, dk).repeat_interleave(hv // hk, dim=1)
+    v = mixed[:, 2 * key:].reshape(B, hv, dv)
+    q = q * torch.rsqrt(q.pow(2).sum(-1, keepdim=True) + l2_eps)       # l2_normalise :206-216
+    k = k * torch.rsqrt(k.pow(2).sum(-1, keepdim=True) + l2_eps)
+    beta = torch.sigmoid(b_raw)
+    g = -torch.exp(a_log.float()) * torch.nn.functional.softplus(a_raw + dt_bias.float())
+    # delta_step :218-241
+    decayed = state.double() * torch.exp(g.double())[:, :, None, None]
+    recalled = (decayed * k.double()[:, :, :, None]).sum(dim=2)
+    delta = (v.double() - recalled) * beta.double()[:, :, None]
+    updated = decayed + k.double()[:, :, :, None] * delta[:, :, None, :]
+    read = (updated * (q.double() * dk ** -0.5)[:, :, :, None]).sum(dim=2)
+    read = read.float()
+    # gated norm: _rms_norm(read, gamma_gdn) * silu(z), per value head
+    normed = read * torch.rsqrt(read.pow(2).mean(-1, keepdim=True) + rms_eps) * gamma_gdn.float()
+    gated = normed * torch.nn.functional.silu(z.reshape(B, hv, dv))
+    new_conv = window[:, :, 1:].contiguous()
+    return gated.reshape(B, val), new_conv, updated.float()
+
+
+# ---------------------------------------------------------------------------
+# Mamba2 decode step (a19), HIR policy
+# ---------------------------------------------------------------------------
+def mamba_step(proj, conv_state, ssm_state, conv_w, conv_b, a_log, dt_bias, d_skip, gamma_ssm,
+               *, nh, pd, ns, ng, eps=1e-5):
+    """``mamba_mixer`` between ``in_projection`` and ``out_proj``
+    (model.py:154-270): conv_step (:154-168), ssm_step (:170-221) and the
+    RMSNormGated of gated_out (:223-238), for a batch.
+
+    proj [B][EXP + CONV + NH] bf16 values: gate | x B C | dt_raw;
+    conv_state [B][CONV][KRN-1] bf16 values; ssm_state [B][NH][PD][NS] f32;
+    conv_w [CONV][KRN], conv_b [CONV], a_log/dt_bias/d_skip [NH], gamma_ssm [EXP].
+    -> (normed bf16 values [B][EXP] (out_proj's input), new conv_state, new state)."""
+    B = proj.shape[0]
+    exp_ = nh * pd
+    conv = exp_ + 2 * ng * ns
+    gate = proj[:, :exp_]
+    entry = proj[:, exp_:exp_ + conv]
+    dt_raw = proj[:, exp_ + conv:exp_ + conv + nh]
+    # conv_step: bf16 window * kernel (rounded), sum (f32, rounded once), + bias, silu
+    window = torch.cat((conv_state.float(), entry[:, :, None].float()), dim=2)
+    weighted = bf(window * conv_w.float()[None])
+    summed = bf(weighted.double().sum(dim=-1).float())
+    mixed = bf(torch.nn.functional.silu(bf(summed + conv_b.float()[None])))
+    x = mixed[:, :exp_].reshape(B, nh, pd)
+    bvec = mixed[:, exp_:exp_ + ng * ns].reshape(B, ng, ns)
+    cvec = mixed[:, exp_ + ng * ns:].reshape(B, ng, ns)
+    # ssm_step
+    dt = bf(torch.nn.functional.softplus(bf(dt_raw + dt_bias.float()[None])))
+    a = -torch.exp(a_log.float())
+    decay = torch.exp(dt * a[None])                                          # f32
+    hpg = nh // ng
+    b_e = bvec.repeat_interleave(hpg, dim=1)[:, :, None, :]                  # [B][NH][1][NS]
+    c_e = cvec.repeat_interleave(hpg, dim=1)[:, :, None, :]
+    d_b = bf(dt[:, :, None, None] * b_e)
+    d_bx = bf(d_b * x[:, :, :, None])
+    updated = ssm_state.float() * decay[:, :, None, None] + d_bx
+    read = (bf(updated).double() * c_e.double()).sum(dim=-1).float()
+    y = bf(bf(read) + bf(x * d_skip.float()[None, :, None]))
+    # gated_out's RMSNormGated: gate multiplies before the norm, f32, then bf16
+    gated = y.reshape(B, exp_) * torch.nn.functional.silu(gate)
+    normed = gated * torch.rsqrt(gated.pow(2).mean(-1, keepdim=True) + eps) * gamma_ssm.float()
+    new_conv = window[:, :, 1:].contiguous()
+    return bf(normed), new_conv, updated

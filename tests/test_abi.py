@@ -1,5 +1,5 @@
-"""The C ABI: the built library exports every entry include/tf_decode.h declares,
-the ctypes binding covers them, and the ctypes structs have the C layout.
+"""The C ABI: the built library exports every entry include/*.h declares, the
+ctypes binding covers them, and the ctypes structs have the C layout.
 No GPU work is done here (only tfd_abi_version is called)."""
 import ctypes
 import re
@@ -14,25 +14,33 @@ from tilefoundry_amd.build import LIB
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "tf_decode.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def declared_functions() -> list[str]:
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(tfd_\w+)\s*\(", text, re.M)))
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names |= set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(tfd_\w+)\s*\(", text, re.M))
+    return sorted(names)
 
 
 def test_header_declares_entries():
     names = declared_functions()
     assert "tfd_gemv_bf16" in names and "tfd_decode_persistent" in names
+    assert "tfd_gdn_step" in names and "tfd_gemm_skinny_fp8" in names
     assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
 
 
 def test_header_constants_match_binding():
     """Every plain #define of the header has the value the binding uses."""
-    defines = dict(re.findall(r"^#define TFD_(\w+) (\d+)", HEADER.read_text(), re.M))
+    defines = {}
+    for header in HEADERS:
+        defines.update(re.findall(r"^#define TFD_(\w+) (\d+)", header.read_text(), re.M))
     names = {"ABI_VERSION", "PRO_PLAIN", "PRO_NORM", "EPI_STORE", "EPI_RESID", "EPI_SWIGLU",
              "EPI_LOGITS", "ERR_TOKEN_RANGE", "ERR_POS_RANGE", "ERR_PAGE_RANGE",
-             "ERR_STEP_RANGE", "ERR_SYNC", "PAGE_SIZE", "ATTN_SPLIT", "SKINNY_COUNTERS"}
+             "ERR_STEP_RANGE", "ERR_SYNC", "PAGE_SIZE", "ATTN_SPLIT", "SKINNY_COUNTERS",
+             "ROUTE_SOFTMAX_TOPK", "ROUTE_TOPK_SOFTMAX", "POLICY_F32", "POLICY_BF16"}
     assert names <= set(defines), names - set(defines)
     for name in names:
         assert getattr(_lib, name) == int(defines[name]), name
@@ -47,15 +55,19 @@ def test_library_exports_every_declared_entry():
     assert dll.tfd_abi_version() == _lib.ABI_VERSION
 
 
+STRUCTS = {"TfdDecodeArgs": _lib.TfdDecodeArgs, "TfdLayer": _lib.TfdLayer,
+           "TfdMoeArgs": _lib.TfdMoeArgs, "TfdGdnArgs": _lib.TfdGdnArgs,
+           "TfdMambaArgs": _lib.TfdMambaArgs}
+
+
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="no C compiler")
 def test_ctypes_structs_match_c_layout(tmp_path):
-    fields = [f for f, _ in _lib.TfdDecodeArgs._fields_]
-    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"',
-             'int main(void) {',
-             '  printf("TfdLayer %zu\\n", sizeof(TfdLayer));',
-             '  printf("TfdDecodeArgs %zu\\n", sizeof(TfdDecodeArgs));']
-    for f in fields:
-        lines.append(f'  printf("{f} %zu\\n", offsetof(TfdDecodeArgs, {f}));')
+    lines = ['#include <stdio.h>', '#include <stddef.h>',
+             *[f'#include "{h}"' for h in HEADERS], 'int main(void) {']
+    for name, cls in STRUCTS.items():
+        lines.append(f'  printf("{name} %zu\\n", sizeof({name}));')
+        for f, _ in cls._fields_:
+            lines.append(f'  printf("{name}.{f} %zu\\n", offsetof({name}, {f}));')
     lines.append("  return 0; }")
     src = tmp_path / "probe.c"
     src.write_text("\n".join(lines))
@@ -63,7 +75,7 @@ def test_ctypes_structs_match_c_layout(tmp_path):
     subprocess.run(["gcc", str(src), "-o", str(exe)], check=True)
     out = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True,
                                                         text=True, check=True).stdout.splitlines())
-    assert int(out["TfdLayer"]) == ctypes.sizeof(_lib.TfdLayer)
-    assert int(out["TfdDecodeArgs"]) == ctypes.sizeof(_lib.TfdDecodeArgs)
-    for f in fields:
-        assert int(out[f]) == getattr(_lib.TfdDecodeArgs, f).offset, f
+    for name, cls in STRUCTS.items():
+        assert int(out[name]) == ctypes.sizeof(cls), name
+        for f, _ in cls._fields_:
+            assert int(out[f"{name}.{f}"]) == getattr(cls, f).offset, f"{name}.{f}"

@@ -54,7 +54,8 @@ def _gemm(x, w, epi, resid=None, work=None):
         out = torch.zeros(M, N, device=x.device, dtype=torch.float32)
     else:
         out = torch.zeros(M, N, device=x.device, dtype=torch.bfloat16)
-    lib().tfd_gemm_skinny_bf16(ptr(operand_order(x)), ptr(w), M, K, N, epi,
+    xo = operand_order(x)                       # held: see the fp8 twin in test_gpu_hybrid
+    lib().tfd_gemm_skinny_bf16(ptr(xo), ptr(w), M, K, N, epi,
                                None if resid is None else ptr(resid), N, ptr(out),
                                N, None if work is None else ptr(work),
                                0 if work is None else work.numel(),

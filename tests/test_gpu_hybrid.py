@@ -1,0 +1,373 @@
+"""The hybrid models' kernels (workloads C4 and C5) against the oracle, on the GPU.
+
+* fp8 skinny GEMM: every output within one bf16 ulp of the exact
+  scale[n] * sum_k x e4m3(w) plus the f32 accumulation bound, every epilogue.
+* Routers: the oracle's expert ids exactly; weights to f32 rounding (C4) or
+  within one bf16 ulp (C5: bf16 weights); ties go to the lower id.
+* MoE experts (C4 bf16 / C5 fp8), GDN and Mamba2 steps at the models' real
+  widths: against the oracle to the bf16 bar (the kernels' f32 sums run in
+  another order than the oracle's f64 ones, so a rounding may land one bf16 ulp
+  away and carry on), conv windows bit-exact, recurrent state to f32 rounding,
+  over two chained steps.
+"""
+import ctypes
+
+import pytest
+import torch
+
+from oracle import hybrid_ref as H
+from tests._parity import assert_close_bf16, report, ulp_bf16
+from tests.test_gpu_batch import from_operand_order, operand_order
+from tilefoundry_amd import _lib
+from tilefoundry_amd._lib import lib, ptr
+
+pytestmark = pytest.mark.gpu
+
+BF = torch.bfloat16
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _fp8_codes(shape, gen, std=0.6):
+    return (torch.randn(shape, generator=gen) * std).to(torch.float8_e4m3fn).view(torch.uint8)
+
+
+# ---------------------------------------------------------------------------
+# fp8 skinny GEMM (per-output-channel scales)
+# ---------------------------------------------------------------------------
+def _packed_fp8(codes):
+    N, K = codes.shape
+    out = torch.full((-(-N // 16) * 16 * K,), 0x7F, device=codes.device, dtype=torch.uint8)
+    lib().tfd_pack_skinny_fp8(ptr(codes), K, N, K, ptr(out), _stream())
+    return out
+
+
+def _gemm_fp8(x, codes, scale, epi, resid=None):
+    M, K = x.shape
+    N = codes.shape[0]
+    dev = "cuda:0"
+    w = _packed_fp8(codes.to(dev))
+    if epi == _lib.EPI_SWIGLU:
+        out = torch.full((32 * (N // 2),), float("nan"), device=dev, dtype=BF)
+    elif epi == _lib.EPI_LOGITS:
+        out = torch.zeros(M, N, device=dev, dtype=torch.float32)
+    else:
+        out = torch.zeros(M, N, device=dev, dtype=BF)
+    # device copies held in locals: a temporary freed before the launch could
+    # hand its memory to the next copy, which the stream runs first
+    xd, sd = operand_order(x.to(dev)), scale.to(dev)
+    rd = None if resid is None else resid.to(dev)
+    lib().tfd_gemm_skinny_fp8(ptr(xd), ptr(w), ptr(sd), M, K, N, epi,
+                              None if rd is None else ptr(rd), N, ptr(out), N, _stream())
+    torch.cuda.synchronize()
+    if epi == _lib.EPI_SWIGLU:
+        return from_operand_order(out, M, N // 2).cpu()
+    return out.cpu()
+
+
+@pytest.mark.parametrize("M", [1, 8, 32])
+@pytest.mark.parametrize("K,N", [(4096, 8512), (4096, 4096), (1536, 4096), (768, 4096),
+                                 (256, 40)])
+def test_fp8_gemm_within_one_ulp_of_exact(gpu_device, M, K, N):
+    g = torch.Generator().manual_seed(M * 131 + K + N)
+    x = (torch.randn(M, K, generator=g) * 0.5).to(BF)
+    codes = _fp8_codes((N, K), g)
+    scale = torch.rand(N, generator=g) * 0.02 + 0.005
+    exact = H.gemv_fp8(codes, scale, x.float()).double()
+    got = _gemm_fp8(x, codes, scale, _lib.EPI_STORE).float()
+    raw = codes.view(torch.float8_e4m3fn).double()
+    acc_bound = K * 2.0 ** -24 * (x.double().abs() @ raw.abs().t()) * scale.double()
+    want = exact.to(BF).float()
+    bound = ulp_bf16(want).double() + acc_bound
+    bad = (got.double() - exact).abs() > bound
+    assert not bad.any(), (int(bad.sum()), got[bad][:4], exact[bad][:4])
+    assert torch.equal(_gemm_fp8(x, codes, scale, _lib.EPI_LOGITS), got)
+    r = torch.randn(M, N, generator=g).to(BF)
+    res = _gemm_fp8(x, codes, scale, _lib.EPI_RESID, r).float()
+    assert torch.equal(res, (r.float() + got).to(BF).float())
+    if N % 64 == 0:
+        sw = _gemm_fp8(x, codes, scale, _lib.EPI_SWIGLU).float()
+        act = torch.nn.functional.silu(got[:, 0::2].to(BF)).float()
+        want_sw = (act * got[:, 1::2]).to(BF).float()
+        assert ((sw - want_sw).abs() <= ulp_bf16(want_sw)).all()
+
+
+def test_fp8_pack_layout(gpu_device):
+    """Block (tile t, step s) is 512 bytes; lane l's 8 codes are
+    W[16t + l % 16][32s + 8(l // 16) + j]; padding rows are 0."""
+    N, K = 40, 512
+    codes = (torch.arange(N * K) % 251).to(torch.uint8).view(N, K)
+    got = _packed_fp8(codes.to(gpu_device)).cpu().view(-1, 64, 8)
+    tiles, steps = -(-N // 16), K // 32
+    wp = torch.cat([codes, torch.zeros(tiles * 16 - N, K, dtype=torch.uint8)])
+    want = wp.view(tiles, 16, steps, 4, 8).permute(0, 2, 3, 1, 4).reshape(-1, 64, 8)
+    assert torch.equal(got, want)
+
+
+# ---------------------------------------------------------------------------
+# Routers
+# ---------------------------------------------------------------------------
+def _route(logits, k, mode, ldl=None):
+    rows, E = logits.shape
+    ldl = ldl or E
+    buf = torch.full((rows, ldl), float("nan"), device="cuda:0")
+    buf[:, :E] = logits.to("cuda:0")
+    w = torch.zeros(rows, k, device="cuda:0")
+    idx = torch.full((rows, k), -1, dtype=torch.int32, device="cuda:0")
+    lib().tfd_route_topk(ptr(buf), ldl, rows, E, k, mode, ptr(w), ptr(idx), _stream())
+    torch.cuda.synchronize()
+    return w.cpu(), idx.cpu().long()
+
+
+@pytest.mark.parametrize("rows", [1, 16, 32])
+def test_route_softmax_topk_c4(gpu_device, rows):
+    g = torch.Generator().manual_seed(rows)
+    logits = H.bf(torch.randn(rows, 256, generator=g) * 2)
+    w, idx = _route(logits, 8, _lib.ROUTE_SOFTMAX_TOPK, ldl=260)
+    want_w, want_i = H.route_softmax_topk(logits, 8)
+    assert torch.equal(idx, want_i)
+    torch.testing.assert_close(w, want_w, atol=1e-6, rtol=1e-5)
+
+
+@pytest.mark.parametrize("rows", [1, 8, 32])
+def test_route_topk_softmax_c5(gpu_device, rows):
+    g = torch.Generator().manual_seed(100 + rows)
+    logits = H.bf(torch.randn(rows, 72, generator=g) * 2)
+    w, idx = _route(logits, 10, _lib.ROUTE_TOPK_SOFTMAX)
+    want_w, want_i = H.route_topk_softmax(logits, 10)
+    assert torch.equal(idx, want_i)
+    assert ((w - want_w).abs() <= ulp_bf16(want_w)).all(), report(w, want_w)
+    assert torch.equal(w, w.to(BF).float())
+
+
+def test_route_ties_go_to_the_lower_expert(gpu_device):
+    logits = torch.zeros(2, 64)
+    logits[0, [5, 9, 40]] = 1.0
+    logits[1, [63, 2]] = 3.0
+    for mode in (_lib.ROUTE_SOFTMAX_TOPK, _lib.ROUTE_TOPK_SOFTMAX):
+        _, idx = _route(logits, 4, mode)
+        assert idx[0].tolist() == [5, 9, 40, 0]
+        assert idx[1].tolist() == [2, 63, 0, 1]
+
+
+def test_route_rejects_bad_shapes(gpu_device):
+    with pytest.raises(_lib.TFDError):
+        _route(torch.zeros(1, 300), 8, _lib.ROUTE_SOFTMAX_TOPK)
+    with pytest.raises(_lib.TFDError):
+        _route(torch.zeros(1, 16), 17, _lib.ROUTE_SOFTMAX_TOPK)
+
+
+# ---------------------------------------------------------------------------
+# MoE experts
+# ---------------------------------------------------------------------------
+def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w_sscale=None,
+              fp8=False, policy):
+    dev = "cuda:0"
+    rows, hs = x.shape
+    k = idx.shape[1]
+    experts, inter = w_gate.shape[0], w_gate.shape[1]
+    sh = w_sout.shape[1]
+    ld = max(inter, sh)
+    keep = []
+
+    def d(t):
+        t = t.to(dev).contiguous()
+        keep.append(t)
+        return ptr(t)
+
+    hidden = torch.full((rows, k + 1, ld), float("nan"), device=dev, dtype=BF)
+    out = torch.full((rows, hs), float("nan"), device=dev)
+    sscale = torch.zeros(rows, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    a = _lib.TfdMoeArgs()
+    a.x, a.weights, a.idx = d(x.to(BF)), d(weights.float()), d(idx.to(torch.int32))
+    a.w_gate, a.w_up, a.w_down = d(w_gate), d(w_up), d(w_down)
+    a.w_shared_in, a.w_shared_out = d(w_sin), d(w_sout)
+    if fp8:
+        a.s_gate, a.s_up, a.s_down, a.s_shared_in, a.s_shared_out = [d(v) for v in s]
+    a.w_shared_scale = None if w_sscale is None else d(w_sscale)
+    a.hidden, a.shared_scale, a.out = ptr(hidden), ptr(sscale), ptr(out)
+    a.rows, a.k, a.experts, a.hidden_size = rows, k, experts, hs
+    a.inter, a.shared_inter, a.hidden_ld = inter, sh, ld
+    a.fp8, a.policy, a.err = int(fp8), policy, ptr(err)
+    lib().tfd_moe_experts(ctypes.addressof(a), _stream())
+    torch.cuda.synchronize()
+    assert err.item() == 0
+    return out.cpu()
+
+
+def _routing(rows, experts, k, gen):
+    idx = torch.stack([torch.randperm(experts, generator=gen)[:k] for _ in range(rows)])
+    w = torch.rand(rows, k, generator=gen) + 0.1
+    return w / w.sum(-1, keepdim=True), idx
+
+
+@pytest.mark.parametrize("rows", [1, 4, 16])
+def test_moe_experts_c4_bf16(gpu_device, rows):
+    """Qwen3.5 widths: H 2048, I 512, shared 512, top 8 (16 experts resident)."""
+    g = torch.Generator().manual_seed(rows)
+    hs, inter, sh, E, k = 2048, 512, 512, 16, 8
+    rnd = lambda *s, std=0.03: H.bf(torch.randn(*s, generator=g) * std)
+    x = rnd(rows, hs, std=1.0)
+    weights, idx = _routing(rows, E, k, g)
+    w_gate, w_up, w_down = rnd(E, inter, hs), rnd(E, inter, hs), rnd(E, hs, inter)
+    ws_gate, ws_up, ws_down, ws_scale = rnd(sh, hs), rnd(sh, hs), rnd(hs, sh), rnd(1, hs)
+    got = _moe_call(x, weights, idx, w_gate=w_gate.to(BF), w_up=w_up.to(BF),
+                    w_down=w_down.to(BF), w_sin=torch.cat([ws_gate, ws_up]).to(BF),
+                    w_sout=ws_down.to(BF), w_sscale=ws_scale.to(BF), policy=_lib.POLICY_F32)
+    want = H.moe_c4(x, weights, idx, w_gate, w_up, w_down, ws_gate, ws_up, ws_down, ws_scale)
+    assert_close_bf16(got, want, max_rel=1e-2, min_cos=0.99999, name="moe c4")
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_moe_experts_c5_fp8(gpu_device, rows):
+    """Granite widths: H 4096, I 768, shared 1536, top 10 (16 experts resident)."""
+    g = torch.Generator().manual_seed(50 + rows)
+    hs, inter, sh, E, k = 4096, 768, 1536, 16, 10
+    x = H.bf(torch.randn(rows, hs, generator=g))
+    weights, idx = _routing(rows, E, k, g)
+    weights = H.bf(weights)
+    sc = lambda *s: torch.rand(*s, generator=g) * 0.004 + 0.002
+    gc, uc, dc = _fp8_codes((E, inter, hs), g), _fp8_codes((E, inter, hs), g), \
+        _fp8_codes((E, hs, inter), g)
+    gs, us, ds = sc(E, inter), sc(E, inter), sc(E, hs)
+    sic, soc = _fp8_codes((2 * sh, hs), g), _fp8_codes((hs, sh), g)
+    sis, sos = sc(2 * sh), sc(hs)
+    got = _moe_call(x, weights, idx, w_gate=gc, w_up=uc, w_down=dc, w_sin=sic, w_sout=soc,
+                    s=(gs, us, ds, sis, sos), fp8=True, policy=_lib.POLICY_BF16)
+    want = H.moe_c5(x, weights, idx, gc, gs, uc, us, dc, ds, sic, sis, soc, sos)
+    assert torch.equal(got, got.to(BF).float())
+    assert_close_bf16(got, want, max_rel=2e-2, min_cos=0.9999, name="moe c5")
+
+
+# ---------------------------------------------------------------------------
+# Gated DeltaNet step (C4: 16 key heads, 32 value heads, 128-wide)
+# ---------------------------------------------------------------------------
+def _gdn_inputs(rows, g, hk=16, hv=32):
+    key, val = hk * 128, hv * 128
+    conv = 2 * key + val
+    proj = H.bf(torch.randn(rows, conv + val + 2 * hv, generator=g))
+    return dict(
+        proj=proj, conv_state=torch.randn(rows, conv, 3, generator=g),
+        state=torch.randn(rows, hv, 128, 128, generator=g) * 0.05,
+        conv_w=H.bf(torch.randn(conv, 4, generator=g) * 0.5),
+        a_log=H.bf(torch.randn(hv, generator=g) * 0.5),
+        dt_bias=H.bf(torch.randn(hv, generator=g) * 0.5),
+        gamma=H.bf(1 + 0.1 * torch.randn(128, generator=g)), hk=hk, hv=hv)
+
+
+def _gdn_gpu(inp, proj, conv_in, state):
+    dev = "cuda:0"
+    rows = proj.shape[0]
+    hk, hv = inp["hk"], inp["hv"]
+    val = hv * 128
+    proj_d = torch.zeros(rows, proj.shape[1] + 8, device=dev)
+    proj_d[:, :proj.shape[1]] = proj.to(dev)
+    cin = conv_in.to(dev).contiguous()
+    cout = torch.full_like(cin, float("nan"))
+    st = state.to(dev).contiguous()
+    params = [inp[n].to(dev).to(BF) for n in ("conv_w", "a_log", "dt_bias", "gamma")]
+    out = torch.full((32 * val,), float("nan"), device=dev, dtype=BF)
+    a = _lib.TfdGdnArgs()
+    a.proj, a.proj_ld, a.conv_in, a.conv_out, a.state = ptr(proj_d), proj_d.shape[1], ptr(cin), \
+        ptr(cout), ptr(st)
+    a.conv_w, a.a_log, a.dt_bias, a.gamma = [ptr(p) for p in params]
+    a.out = ptr(out)
+    a.rows, a.key_heads, a.value_heads, a.head_k_dim, a.head_v_dim, a.conv_kernel = \
+        rows, hk, hv, 128, 128, 4
+    a.l2_eps, a.rms_eps = 1e-6, 1e-6
+    lib().tfd_gdn_step(ctypes.addressof(a), _stream())
+    torch.cuda.synchronize()
+    return from_operand_order(out, rows, val).float().cpu(), cout.cpu(), st.cpu()
+
+
+@pytest.mark.parametrize("rows", [1, 16])
+def test_gdn_step_two_tokens(gpu_device, rows):
+    g = torch.Generator().manual_seed(7 + rows)
+    inp = _gdn_inputs(rows, g)
+    conv_state, state = inp["conv_state"], inp["state"]
+    gconv, gstate = conv_state, state
+    for step in range(2):
+        proj = inp["proj"] if step == 0 else H.bf(torch.randn(inp["proj"].shape, generator=g))
+        want, conv_state, state = H.gdn_step(
+            proj, conv_state, state, inp["conv_w"], inp["a_log"], inp["dt_bias"], inp["gamma"],
+            hk=inp["hk"], hv=inp["hv"], dk=128, dv=128)
+        got, gconv, gstate = _gdn_gpu(inp, proj, gconv, gstate)
+        assert torch.equal(gconv, conv_state), step
+        torch.testing.assert_close(gstate, state, atol=1e-5, rtol=1e-4)
+        r = assert_close_bf16(got, H.bf(want), max_rel=1e-2, min_cos=0.99999,
+                              name=f"gdn step {step}")
+        assert r["within_1ulp"] >= 0.999, r
+
+
+def test_gdn_step_rejects_bad_shapes(gpu_device):
+    a = _lib.TfdGdnArgs()
+    a.rows = 1
+    with pytest.raises(_lib.TFDError):
+        lib().tfd_gdn_step(ctypes.addressof(a), _stream())
+
+
+# ---------------------------------------------------------------------------
+# Mamba2 step (C5: 128 heads of 64, state 128, one group)
+# ---------------------------------------------------------------------------
+def _mamba_inputs(rows, g, nh=128):
+    exp_ = nh * 64
+    conv = exp_ + 256
+    return dict(
+        proj=H.bf(torch.randn(rows, exp_ + conv + nh, generator=g)),
+        conv_state=H.bf(torch.randn(rows, conv, 3, generator=g)),
+        state=torch.randn(rows, nh, 64, 128, generator=g) * 0.3,
+        conv_w=H.bf(torch.randn(conv, 4, generator=g) * 0.5),
+        conv_b=H.bf(torch.randn(conv, generator=g) * 0.1),
+        a_log=H.bf(torch.randn(nh, generator=g) * 0.5),
+        dt_bias=H.bf(torch.randn(nh, generator=g) * 0.5),
+        d_skip=H.bf(torch.randn(nh, generator=g)),
+        gamma=H.bf(1 + 0.1 * torch.randn(exp_, generator=g)), nh=nh)
+
+
+def _mamba_gpu(inp, proj, conv_in, state):
+    dev = "cuda:0"
+    rows = proj.shape[0]
+    nh = inp["nh"]
+    exp_ = nh * 64
+    proj_d = torch.zeros(rows, proj.shape[1] + 16, device=dev, dtype=BF)
+    proj_d[:, :proj.shape[1]] = proj.to(dev).to(BF)
+    cin = conv_in.to(dev).to(BF).contiguous()
+    cout = torch.full_like(cin, float("nan"))
+    st = state.to(dev).contiguous()
+    params = [inp[n].to(dev).to(BF)
+              for n in ("conv_w", "conv_b", "a_log", "dt_bias", "d_skip", "gamma")]
+    gated = torch.zeros(rows, exp_, device=dev)
+    ssq = torch.zeros(rows, nh, device=dev)
+    out = torch.full((32 * exp_,), float("nan"), device=dev, dtype=BF)
+    a = _lib.TfdMambaArgs()
+    a.proj, a.proj_ld, a.conv_in, a.conv_out, a.state = ptr(proj_d), proj_d.shape[1], ptr(cin), \
+        ptr(cout), ptr(st)
+    a.conv_w, a.conv_b, a.a_log, a.dt_bias, a.d_skip, a.gamma = [ptr(p) for p in params]
+    a.gated, a.ssq, a.out = ptr(gated), ptr(ssq), ptr(out)
+    a.rows, a.heads, a.head_dim, a.state_dim, a.groups, a.conv_kernel = rows, nh, 64, 128, 1, 4
+    a.eps = 1e-5
+    lib().tfd_mamba_step(ctypes.addressof(a), _stream())
+    torch.cuda.synchronize()
+    return from_operand_order(out, rows, exp_).float().cpu(), cout.float().cpu(), st.cpu()
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_mamba_step_two_tokens(gpu_device, rows):
+    g = torch.Generator().manual_seed(70 + rows)
+    inp = _mamba_inputs(rows, g)
+    conv_state, state = inp["conv_state"], inp["state"]
+    gconv, gstate = conv_state, state
+    for step in range(2):
+        proj = inp["proj"] if step == 0 else H.bf(torch.randn(inp["proj"].shape, generator=g))
+        want, conv_state, state = H.mamba_step(
+            proj, conv_state, state, inp["conv_w"], inp["conv_b"], inp["a_log"], inp["dt_bias"],
+            inp["d_skip"], inp["gamma"], nh=inp["nh"], pd=64, ns=128, ng=1)
+        got, gconv, gstate = _mamba_gpu(inp, proj, gconv, gstate)
+        assert torch.equal(gconv, conv_state), step
+        srep = report(gstate, state)
+        assert srep["max_rel"] < 1e-3 and srep["cos"] > 0.999999, srep
+        r = assert_close_bf16(got, want, max_rel=2e-2, min_cos=0.9999, name=f"mamba {step}")
+        assert r["within_1ulp"] >= 0.99, r

@@ -22,6 +22,8 @@ PAGE_SIZE = 16
 SKINNY_COUNTERS = 16384     # tile counters at the start of a skinny-GEMM work buffer
 ARGMAX_WORK = 128           # int32 per row of tfd_argmax_rows' two-stage work buffer
 ATTN_SPLIT = 64
+ROUTE_SOFTMAX_TOPK, ROUTE_TOPK_SOFTMAX = 0, 1
+POLICY_F32, POLICY_BF16 = 0, 1
 
 P = c_void_p
 I = c_int
@@ -53,6 +55,13 @@ SIGNATURES: dict[str, list] = {
     "tfd_embed_rows_bf16": [P, P, P, I, I, I, I, P, P],
     "tfd_decode_persistent": [P, I, I, P],
     "tfd_decode_persistent_grid": [],
+    # include/tf_hybrid.h
+    "tfd_pack_skinny_fp8": [P, I, I, I, P, P],
+    "tfd_gemm_skinny_fp8": [P, P, P, I, I, I, I, P, I, P, I, P],
+    "tfd_route_topk": [P, I, I, I, I, I, P, P, P],
+    "tfd_moe_experts": [P, P],
+    "tfd_gdn_step": [P, P],
+    "tfd_mamba_step": [P, P],
 }
 RESTYPES = {"tfd_last_error": ctypes.c_char_p}
 UNCHECKED = {"tfd_abi_version", "tfd_decode_persistent_grid"}
@@ -63,6 +72,46 @@ class TfdLayer(ctypes.Structure):
 
     _fields_ = [(n, c_void_p) for n in ("w_qkv", "w_o", "w_gu", "w_down", "gamma_in",
                                         "gamma_post", "gamma_q", "gamma_k", "k_pool", "v_pool")]
+
+
+class TfdMoeArgs(ctypes.Structure):
+    """``TfdMoeArgs`` of include/tf_hybrid.h, field for field."""
+
+    _fields_ = [
+        *[(n, c_void_p) for n in ("x", "weights", "idx", "w_gate", "w_up", "w_down", "s_gate",
+                                   "s_up", "s_down", "w_shared_in", "w_shared_out",
+                                   "s_shared_in", "s_shared_out", "w_shared_scale", "hidden",
+                                   "shared_scale", "out")],
+        *[(n, c_int) for n in ("rows", "k", "experts", "hidden_size", "inter", "shared_inter",
+                                "hidden_ld", "fp8", "policy")],
+        ("err", c_void_p),
+    ]
+
+
+class TfdGdnArgs(ctypes.Structure):
+    """``TfdGdnArgs`` of include/tf_hybrid.h, field for field."""
+
+    _fields_ = [
+        ("proj", c_void_p), ("proj_ld", c_int),
+        *[(n, c_void_p) for n in ("conv_in", "conv_out", "state", "conv_w", "a_log", "dt_bias",
+                                   "gamma", "out")],
+        *[(n, c_int) for n in ("rows", "key_heads", "value_heads", "head_k_dim", "head_v_dim",
+                                "conv_kernel")],
+        ("l2_eps", c_float), ("rms_eps", c_float),
+    ]
+
+
+class TfdMambaArgs(ctypes.Structure):
+    """``TfdMambaArgs`` of include/tf_hybrid.h, field for field."""
+
+    _fields_ = [
+        ("proj", c_void_p), ("proj_ld", c_int),
+        *[(n, c_void_p) for n in ("conv_in", "conv_out", "state", "conv_w", "conv_b", "a_log",
+                                   "dt_bias", "d_skip", "gamma", "gated", "ssq", "out")],
+        *[(n, c_int) for n in ("rows", "heads", "head_dim", "state_dim", "groups",
+                                "conv_kernel")],
+        ("eps", c_float),
+    ]
 
 
 class TfdDecodeArgs(ctypes.Structure):

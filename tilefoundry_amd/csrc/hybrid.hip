@@ -1,0 +1,667 @@
+// Decode-step pieces of the hybrid models, for gfx950: the MoE routers and
+// experts, the gated-DeltaNet recurrence (Qwen3.5, workload C4) and the Mamba2
+// recurrence (Granite-4.0-H, workload C5).
+//
+// Arithmetic policies (one per model, the one its reference states):
+//  * C4 follows the example's plain-torch twin (torch_ref.py's dtype policy):
+//    f32 activations and f32 recurrent state; a matmul's activation is cast to
+//    bf16, summed in f32 and the result rounded to bf16 once.
+//  * C5 follows the authored HIR: bf16 activations with every binary op
+//    rounded, f32 where the HIR casts to f32, f32 SSM state; weights are
+//    fp8-e4m3fn with one f32 scale per output channel.
+// Batch rows are sequences (one token each); the projections around these
+// kernels are the skinny GEMMs (tfd_gemm_skinny_bf16 / _fp8).
+
+#include "decode_phases.h"
+#include "host_common.h"
+#include "tf_hybrid.h"
+
+using namespace tfd;
+using namespace tfd_host;
+
+namespace {
+
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kMaxRowsH = 32;
+
+// the skinny GEMMs' operand order for a [rows <= 32][K] activation
+__device__ __forceinline__ int64_t xp_off_h(int m, int k) {
+  return ((int64_t)((k >> 5) * 2 + (m >> 4)) * 64 + (m & 15) + 16 * ((k >> 3) & 3)) * 8 +
+         (k & 7);
+}
+
+__device__ __forceinline__ float softplus_f(float x) {
+  // torch.nn.functional.softplus (beta 1, threshold 20)
+  return x > 20.f ? x : log1pf(expf(x));
+}
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+
+// ---------------------------------------------------------------------------
+// Routers: one wave per row of E <= 256 f32 logits.  The top k are taken by
+// value, largest first, equal values by ascending index (torch.topk leaves the
+// order of ties open; bf16-valued logits tie often).  Qwen3.5 ranks the softmax
+// probabilities: softmax is increasing, so ranking the logits ranks them too,
+// except that two logits closer than an f32 ulp of the largest one (both
+// within 2^-24 of zero beside a logit of 1, say) round to one probability, and
+// there the larger logit goes first.
+//   kMode 0 (torch_ref.py:417-430): p = softmax over all E in f32, weights =
+//            p_topk / sum p_topk (f32)
+//   kMode 1 (granite model.py:376-390): weights = bf16(softmax over the top k)
+// ---------------------------------------------------------------------------
+template <int kMode>
+__global__ __launch_bounds__(kWave) void k_route(const float* __restrict__ logits, int ldl, int E,
+                                                 int k, float* __restrict__ weights,
+                                                 int* __restrict__ idx) {
+  const int row = blockIdx.x, lane = threadIdx.x;
+  float v[4];
+  int id[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + kWave * j;
+    id[j] = e;
+    v[j] = e < E ? logits[(int64_t)row * ldl + e] : kNegInf;
+  }
+  float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+  m = wave_max(m);
+  float sum_all = 0.f;
+  if (kMode == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (id[j] < E) sum_all += expf(v[j] - m);
+    sum_all = wave_sum(sum_all);
+  }
+  bool taken[4] = {false, false, false, false};
+  float my_val = kNegInf;
+  int my_idx = 0;
+  for (int r = 0; r < k; ++r) {
+    float bv = kNegInf;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (id[j] < E && !taken[j] && better(v[j], id[j], bv, bi)) {
+        bv = v[j];
+        bi = id[j];
+      }
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) {
+      const float ob = __shfl_xor(bv, msk, kWave);
+      const int oi = __shfl_xor(bi, msk, kWave);
+      if (better(ob, oi, bv, bi)) {
+        bv = ob;
+        bi = oi;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (id[j] == bi) taken[j] = true;
+    if (lane == r) {
+      my_val = bv;
+      my_idx = bi;
+    }
+  }
+  // weights of the k picks, held by lanes 0..k-1
+  float w = 0.f;
+  if (lane < k) w = kMode == 0 ? expf(my_val - m) / sum_all : expf(my_val - m);
+  const float tot = wave_sum(lane < k ? w : 0.f);
+  if (lane < k) {
+    const float out = kMode == 0 ? w / tot : rbf(w / tot);
+    weights[(int64_t)row * k + lane] = out;
+    idx[(int64_t)row * k + lane] = my_idx;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row dot products for the experts.  A wave owns a pair of output rows; its
+// lanes split the length-K reduction into 16-byte chunks of the bf16 input
+// (held in registers) and of the weight row (bf16, or fp8 with one scale per
+// row), exact products summed in f32.
+// ---------------------------------------------------------------------------
+template <bool kFp8>
+struct RowW;
+template <>
+struct RowW<false> {
+  // 8 weights of row `row` at chunk c (bf16)
+  static __device__ __forceinline__ float dot_chunk(const void* w, int64_t row, int K, int c,
+                                                    const u32x4& x) {
+    const u32x4 wv = load16_stream((const bf16*)w + row * K + (int64_t)c * 8);
+    return dot8(wv, x, 0.f);
+  }
+};
+template <>
+struct RowW<true> {
+  static __device__ __forceinline__ float dot_chunk(const void* w, int64_t row, int K, int c,
+                                                    const u32x4& x) {
+    const u32x2 q = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x2*>((const uint8_t*)w + row * K + (int64_t)c * 8));
+    const f32x2_t v0 = __builtin_amdgcn_cvt_pk_f32_fp8(q.x, false);
+    const f32x2_t v1 = __builtin_amdgcn_cvt_pk_f32_fp8(q.x, true);
+    const f32x2_t v2 = __builtin_amdgcn_cvt_pk_f32_fp8(q.y, false);
+    const f32x2_t v3 = __builtin_amdgcn_cvt_pk_f32_fp8(q.y, true);
+    const u32x4 wv = {pack2(v0.x, v0.y), pack2(v1.x, v1.y), pack2(v2.x, v2.y),
+                      pack2(v3.x, v3.y)};
+    return dot8(wv, x, 0.f);
+  }
+};
+
+// sum over the row of w[row] . x (x as kC 16-byte chunks per lane, chunk
+// c = lane + 64 i), every lane gets the total
+template <bool kFp8, int kC>
+__device__ __forceinline__ float row_dot(const void* w, int64_t row, int K, const u32x4 (&x)[kC],
+                                         int lane) {
+  float a = 0.f;
+  const int nch = K / 8;
+#pragma unroll
+  for (int i = 0; i < kC; ++i) {
+    const int c = lane + kWave * i;
+    if (c < nch) a += RowW<kFp8>::dot_chunk(w, row, K, c, x[i]);
+  }
+  return wave_sum(a);
+}
+
+template <int kC>
+__device__ __forceinline__ void load_vec(const bf16* x, int K, int lane, u32x4 (&xr)[kC]) {
+  const int nch = K / 8;
+#pragma unroll
+  for (int i = 0; i < kC; ++i) {
+    const int c = lane + kWave * i;
+    xr[i] = c < nch ? load16(x + (int64_t)c * 8) : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+struct MoeArgs {
+  const bf16* x;            // [B][H] the normalised tokens
+  const float* weights;     // [B][k] routing weights
+  const int* idx;           // [B][k] expert ids
+  const void *w_gate, *w_up, *w_down;        // [E][I][H], [E][I][H], [E][H][I]
+  const float *s_gate, *s_up, *s_down;       // fp8 row scales [E][I], [E][I], [E][H]
+  const void *w_sin, *w_sout;                // shared: [2 IS][H] (gate rows, then up), [H][IS]
+  const float *s_sin, *s_sout;               // fp8 row scales [2 IS], [H]
+  const bf16* w_sscale;                      // C4 shared-expert gate row [H] (or null)
+  bf16* hidden;                              // [B][k + 1][IM] work
+  float* sscale;                             // [B] work: the shared expert's sigmoid gate
+  float* out;                                // [B][H]
+  int H, I, IS, IM, k, E;
+  int* err;
+};
+
+// gate/up of every (sequence, slot): slot k is the shared expert
+template <bool kFp8, bool kF32, int kC>
+__global__ __launch_bounds__(kBlock) void k_moe_gateup(MoeArgs a) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int slot = blockIdx.y, b = blockIdx.z;
+  const bool shared = slot == a.k;
+  const int rows = shared ? a.IS : a.I;
+  const int r0 = (blockIdx.x * kWavesPerBlock + wave) * 2;
+  int e = 0;
+  if (!shared) {
+    e = a.idx[(int64_t)b * a.k + slot];
+    if (e < 0 || e >= a.E) {
+      if (threadIdx.x == 0) raise_error(a.err, kErrTokenRange);
+      e = 0;
+    }
+  }
+  u32x4 xr[kC];
+  load_vec<kC>(a.x + (int64_t)b * a.H, a.H, lane, xr);
+  if (shared && a.w_sscale && blockIdx.x == 0 && wave == 0) {
+    const float d = rbf(row_dot<false, kC>(a.w_sscale, 0, a.H, xr, lane));
+    if (lane == 0) a.sscale[b] = sigmoid_f(d);
+  }
+  if (r0 >= rows) return;
+  const void* wg = shared ? a.w_sin : a.w_gate;
+  const void* wu = shared ? a.w_sin : a.w_up;
+  const int64_t gbase = shared ? 0 : (int64_t)e * a.I;
+  const int64_t ubase = shared ? a.IS : (int64_t)e * a.I;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int r = r0 + u;
+    if (r >= rows) break;
+    float g = row_dot<kFp8, kC>(wg, gbase + r, a.H, xr, lane);
+    float v = row_dot<kFp8, kC>(wu, ubase + r, a.H, xr, lane);
+    if (kFp8) {
+      g *= shared ? a.s_sin[r] : a.s_gate[gbase + r];
+      v *= shared ? a.s_sin[a.IS + r] : a.s_up[gbase + r];
+    }
+    g = rbf(g);
+    v = rbf(v);
+    const float h = kF32 ? silu_f(g) * v : rbf(silu_f(g)) * v;
+    if (lane == 0) a.hidden[((int64_t)b * (a.k + 1) + slot) * a.IM + r] = f2bf(h);
+  }
+}
+
+// down projections of every slot and their mix, two output rows per wave
+template <bool kFp8, bool kF32, int kCI, int kCS>
+__global__ __launch_bounds__(kBlock) void k_moe_down(MoeArgs a) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int b = blockIdx.y;
+  const int n0 = (blockIdx.x * kWavesPerBlock + wave) * 2;
+  if (n0 >= a.H) return;
+  float acc[2] = {0.f, 0.f};
+  for (int s = 0; s < a.k; ++s) {
+    int e = a.idx[(int64_t)b * a.k + s];
+    if (e < 0 || e >= a.E) e = 0;              // raised by the gate/up launch
+    const float wgt = a.weights[(int64_t)b * a.k + s];
+    u32x4 hr[kCI];
+    load_vec<kCI>(a.hidden + ((int64_t)b * (a.k + 1) + s) * a.IM, a.I, lane, hr);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int n = n0 + u;
+      if (n >= a.H) break;
+      float d = row_dot<kFp8, kCI>(a.w_down, (int64_t)e * a.H + n, a.I, hr, lane);
+      if (kFp8) d *= a.s_down[(int64_t)e * a.H + n];
+      d = rbf(d);
+      acc[u] += kF32 ? d * wgt : rbf(d * wgt);
+    }
+  }
+  u32x4 hs[kCS];
+  load_vec<kCS>(a.hidden + ((int64_t)b * (a.k + 1) + a.k) * a.IM, a.IS, lane, hs);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int n = n0 + u;
+    if (n >= a.H) break;
+    float d = row_dot<kFp8, kCS>(a.w_sout, n, a.IS, hs, lane);
+    if (kFp8) d *= a.s_sout[n];
+    d = rbf(d);
+    const float o = kF32 ? acc[u] + d * (a.w_sscale ? a.sscale[b] : 1.f)
+                         : rbf(rbf(acc[u]) + d);
+    if (lane == 0) a.out[(int64_t)b * a.H + n] = o;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Gated DeltaNet, one token (torch_ref.py:188-312): one block per (value head,
+// sequence).  The block convolves the channels its head reads (its key head's
+// q and k, its own v), L2-normalises q and k, updates its [DK][DV] f32 state
+// in place and writes the gated, normalised read-out in operand order for the
+// out-projection.  A thread owns one value column over half of the key rows.
+// ---------------------------------------------------------------------------
+struct GdnArgs {
+  const float* proj;        // [B][ldp]: conv channels (q | k | v), z, b, a
+  int ldp;
+  const float* conv_in;     // [B][CONV][KW-1]
+  float* conv_out;          // [B][CONV][KW-1] (a different buffer)
+  float* state;             // [B][HV][DK][DV]
+  const bf16* conv_w;       // [CONV][KW]
+  const bf16 *a_log, *dt_bias, *gamma;   // [HV], [HV], [DV]
+  bf16* out;                // operand order, 32 x HV*DV
+  int hk, hv;
+  float l2_eps, rms_eps;
+};
+
+template <int kD, int kKW>
+__device__ __forceinline__ float conv_silu_f32(const float* cin, const bf16* w, float entry,
+                                               float* cout, bool write) {
+  float acc = 0.f;
+  float win[kKW];
+#pragma unroll
+  for (int t = 0; t < kKW - 1; ++t) win[t] = cin[t];
+  win[kKW - 1] = entry;
+#pragma unroll
+  for (int t = 0; t < kKW; ++t) acc += win[t] * bf2f(w[t]);
+  if (write) {
+#pragma unroll
+    for (int t = 0; t < kKW - 1; ++t) cout[t] = win[t + 1];
+  }
+  return silu_f(acc);
+}
+
+template <int kD>
+__global__ __launch_bounds__(2 * kD) void k_gdn_step(GdnArgs a) {
+  constexpr int kKW = 4;
+  const int hv = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int vpk = a.hv / a.hk, hk = hv / vpk;
+  const int key = a.hk * kD, val = a.hv * kD, conv = 2 * key + val;
+  const float* proj = a.proj + (int64_t)b * a.ldp;
+  const float* cin = a.conv_in + (int64_t)b * conv * (kKW - 1);
+  float* cout = a.conv_out + (int64_t)b * conv * (kKW - 1);
+  __shared__ float q_s[kD], k_s[kD], v_s[kD], red[2][kD], sc[4];
+  // ---- conv + SiLU of this head's channels; q/k windows advance once per key head
+  {
+    const int d = tid % kD;
+    const int c = tid < kD ? hk * kD + d : key + hk * kD + d;
+    const float m = conv_silu_f32<kD, kKW>(cin + (int64_t)c * (kKW - 1), a.conv_w + (int64_t)c * kKW,
+                                           proj[c], cout + (int64_t)c * (kKW - 1), hv % vpk == 0);
+    (tid < kD ? q_s : k_s)[d] = m;
+    if (tid < kD) {
+      const int cv = 2 * key + hv * kD + d;
+      v_s[d] = conv_silu_f32<kD, kKW>(cin + (int64_t)cv * (kKW - 1),
+                                      a.conv_w + (int64_t)cv * kKW, proj[cv],
+                                      cout + (int64_t)cv * (kKW - 1), true);
+    }
+  }
+  __syncthreads();
+  // ---- L2 norms of q (threads < kD) and k, beta and g
+  {
+    const int d = tid % kD;
+    const float x = tid < kD ? q_s[d] : k_s[d];
+    float ss = wave_sum(x * x);
+    if ((tid & (kWave - 1)) == 0) red[0][tid / kWave] = ss;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float sq = 0.f, sk = 0.f;
+    for (int w = 0; w < kD / kWave; ++w) sq += red[0][w];
+    for (int w = kD / kWave; w < 2 * kD / kWave; ++w) sk += red[0][w];
+    sc[0] = rsqrtf(sq + a.l2_eps);
+    sc[1] = rsqrtf(sk + a.l2_eps);
+    const float braw = proj[conv + val + hv];
+    const float araw = proj[conv + val + a.hv + hv];
+    sc[2] = sigmoid_f(braw);
+    sc[3] = expf(-expf(bf2f(a.a_log[hv])) * softplus_f(araw + bf2f(a.dt_bias[hv])));
+  }
+  __syncthreads();
+  if (tid < kD) {
+    q_s[tid] *= sc[0] * rsqrtf((float)kD);          // l2-normalised q times DK^-1/2
+    k_s[tid] *= sc[1];
+  }
+  __syncthreads();
+  // ---- the delta rule: thread (dv, half) over key rows [half * kD/2, +kD/2)
+  const int dv = tid % kD, half = tid / kD;
+  constexpr int kRows = kD / 2;
+  float* st = a.state + (((int64_t)b * a.hv + hv) * kD + half * kRows) * kD + dv;
+  const float decay = sc[3], beta = sc[2];
+  float s[kRows];
+  float rec = 0.f;
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    s[r] = st[(int64_t)r * kD] * decay;
+    rec += s[r] * k_s[half * kRows + r];
+  }
+  red[half][dv] = rec;
+  __syncthreads();
+  const float delta = (v_s[dv] - (red[0][dv] + red[1][dv])) * beta;
+  float rd = 0.f;
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) {
+    const float u = s[r] + k_s[half * kRows + r] * delta;
+    st[(int64_t)r * kD] = u;
+    rd += u * q_s[half * kRows + r];
+  }
+  __syncthreads();                      // red is reused
+  red[half][dv] = rd;
+  __syncthreads();
+  // ---- gated RMS norm over the head's DV values, then out in operand order
+  if (tid < kD) {
+    const float read = red[0][tid] + red[1][tid];
+    float ss = wave_sum(read * read);
+    if ((tid & (kWave - 1)) == 0) v_s[tid / kWave] = ss;     // v_s is free now
+  }
+  __syncthreads();
+  if (tid < kD) {
+    float ms = 0.f;
+    for (int w = 0; w < kD / kWave; ++w) ms += v_s[w];
+    ms /= (float)kD;
+    const float read = red[0][tid] + red[1][tid];
+    const float z = proj[conv + hv * kD + tid];
+    const float g = read * rsqrtf(ms + a.rms_eps) * bf2f(a.gamma[tid]) * silu_f(z);
+    a.out[xp_off_h(b, hv * kD + tid)] = f2bf(g);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Mamba2, one token (granite model.py:154-238): one block per (head,
+// sequence) for the convolution and the selective-state update (bf16 ops
+// rounded as the HIR writes them), then one block per sequence for the gated
+// RMS norm over the whole inner width.
+// ---------------------------------------------------------------------------
+struct MambaArgs {
+  const bf16* proj;         // [B][ldp]: gate (EXP) | x B C (CONV) | dt (NH)
+  int ldp;
+  const bf16* conv_in;      // [B][CONV][KW-1]
+  bf16* conv_out;           // [B][CONV][KW-1] (a different buffer)
+  float* state;             // [B][NH][PD][NS]
+  const bf16 *conv_w, *conv_b;               // [CONV][KW], [CONV]
+  const bf16 *a_log, *dt_bias, *d_skip;      // [NH]
+  const bf16* gamma;        // [EXP]
+  float* gated;             // [B][EXP] work
+  float* ssq;               // [B][NH] work
+  bf16* out;                // operand order, 32 x EXP
+  int nh, ns;               // heads, state width (ngroups 1)
+  float eps;
+};
+
+__device__ __forceinline__ float conv_silu_bf16(const bf16* cin, const bf16* w, bf16 bias,
+                                                float entry, bf16* cout, bool write) {
+  constexpr int kKW = 4;
+  float win[kKW];
+#pragma unroll
+  for (int t = 0; t < kKW - 1; ++t) win[t] = bf2f(cin[t]);
+  win[kKW - 1] = entry;
+  float sum = 0.f;
+#pragma unroll
+  for (int t = 0; t < kKW; ++t) sum += rbf(win[t] * bf2f(w[t]));   // bf16 window * kernel
+  const float pre = rbf(rbf(sum) + bf2f(bias));
+  if (write) {
+#pragma unroll
+    for (int t = 0; t < kKW - 1; ++t) cout[t] = f2bf(win[t + 1]);
+  }
+  return rbf(silu_f(pre));
+}
+
+template <int kPD>
+__global__ __launch_bounds__(kBlock) void k_mamba_step(MambaArgs a) {
+  constexpr int kKW = 4, kNS = 128;
+  const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+  const int exp_ = a.nh * kPD, conv = exp_ + 2 * kNS;
+  const bf16* proj = a.proj + (int64_t)b * a.ldp;
+  const bf16* cin = a.conv_in + (int64_t)b * conv * (kKW - 1);
+  bf16* cout = a.conv_out + (int64_t)b * conv * (kKW - 1);
+  __shared__ float x_s[kPD], b_s[kNS], c_s[kNS], dtv[2];
+  for (int i = tid; i < kPD + 2 * kNS; i += kBlock) {
+    const int ch = i < kPD ? h * kPD + i : exp_ + (i - kPD);
+    const float m = conv_silu_bf16(cin + (int64_t)ch * (kKW - 1), a.conv_w + (int64_t)ch * kKW,
+                                   a.conv_b[ch], bf2f(proj[exp_ + ch]),
+                                   cout + (int64_t)ch * (kKW - 1), i < kPD || h == 0);
+    if (i < kPD)
+      x_s[i] = m;
+    else if (i < kPD + kNS)
+      b_s[i - kPD] = m;
+    else
+      c_s[i - kPD - kNS] = m;
+  }
+  if (tid == 0) {
+    const float dt = rbf(softplus_f(rbf(bf2f(proj[exp_ + conv + h]) + bf2f(a.dt_bias[h]))));
+    dtv[0] = dt;
+    dtv[1] = expf(dt * -expf(bf2f(a.a_log[h])));
+  }
+  __syncthreads();
+  // thread (p, quarter): state row p, columns [32 quarter, +32)
+  const int p = tid >> 2, q4 = tid & 3;
+  const float dt = dtv[0], decay = dtv[1];
+  const float xp = x_s[p];
+  float* st = a.state + (((int64_t)b * a.nh + h) * kPD + p) * kNS + q4 * 32;
+  float rd = 0.f;
+#pragma unroll 8
+  for (int j = 0; j < 32; ++j) {
+    const int n = q4 * 32 + j;
+    const float dbx = rbf(rbf(dt * b_s[n]) * xp);
+    const float u = st[j] * decay + dbx;
+    st[j] = u;
+    rd += rbf(u) * c_s[n];
+  }
+  rd += dpp_f<kDppXor1>(rd);
+  rd += dpp_f<kDppXor2>(rd);
+  __shared__ float ss_w[kWavesPerBlock];
+  float g2 = 0.f;
+  if (q4 == 0) {
+    const float y = rbf(rbf(rd) + rbf(xp * bf2f(a.d_skip[h])));
+    const float gt = y * silu_f(bf2f(proj[h * kPD + p]));
+    a.gated[(int64_t)b * exp_ + h * kPD + p] = gt;
+    g2 = gt * gt;
+  }
+  g2 = wave_sum(g2);
+  if ((tid & (kWave - 1)) == 0) ss_w[tid / kWave] = g2;
+  __syncthreads();
+  if (tid == 0) {
+    float t = 0.f;
+    for (int w = 0; w < kWavesPerBlock; ++w) t += ss_w[w];
+    a.ssq[(int64_t)b * a.nh + h] = t;
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_mamba_norm(MambaArgs a, int exp_) {
+  const int b = blockIdx.x;
+  __shared__ float tot;
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+    for (int h = 0; h < a.nh; ++h) t += a.ssq[(int64_t)b * a.nh + h];
+    tot = rsqrtf(t / (float)exp_ + a.eps);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < exp_; i += kBlock)
+    a.out[xp_off_h(b, i)] = f2bf(a.gated[(int64_t)b * exp_ + i] * tot * bf2f(a.gamma[i]));
+}
+
+}  // namespace
+
+template <bool kFp8, bool kF32>
+int launch_moe(const MoeArgs& a, dim3 g1, dim3 g2, hipStream_t s) {
+  switch (cmax_for(a.H)) {
+    case 1: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 1>), g1, dim3(kBlock), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 2>), g1, dim3(kBlock), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 4>), g1, dim3(kBlock), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 8>), g1, dim3(kBlock), 0, s, a); break;
+    default: return fail(kUnsupported, "moe_experts: hidden size %d", a.H);
+  }
+  hipLaunchKernelGGL((k_moe_down<kFp8, kF32, 4, 4>), g2, dim3(kBlock), 0, s, a);
+  return launched("moe_experts");
+}
+
+extern "C" {
+
+int tfd_route_topk(const float* logits, int ldl, int rows, int experts, int k, int mode,
+                   float* weights, int32_t* idx, void* stream) {
+  if (!logits || !weights || !idx) return fail(kBadArg, "route_topk: null pointer");
+  if (rows <= 0 || experts <= 0 || experts > 256 || k <= 0 || k > experts || k > kWave ||
+      ldl < experts || (mode != TFD_ROUTE_SOFTMAX_TOPK && mode != TFD_ROUTE_TOPK_SOFTMAX))
+    return fail(kBadShape, "route_topk: rows=%d experts=%d (<= 256) k=%d mode=%d", rows,
+                experts, k, mode);
+  auto s = (hipStream_t)stream;
+  if (mode == TFD_ROUTE_SOFTMAX_TOPK)
+    hipLaunchKernelGGL(k_route<0>, dim3(rows), dim3(kWave), 0, s, logits, ldl, experts, k,
+                       weights, (int*)idx);
+  else
+    hipLaunchKernelGGL(k_route<1>, dim3(rows), dim3(kWave), 0, s, logits, ldl, experts, k,
+                       weights, (int*)idx);
+  return launched("route_topk");
+}
+
+int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
+  if (!args) return fail(kBadArg, "moe_experts: null args");
+  const TfdMoeArgs& t = *args;
+  if (!t.x || !t.weights || !t.idx || !t.w_gate || !t.w_up || !t.w_down || !t.w_shared_in ||
+      !t.w_shared_out || !t.hidden || !t.out ||
+      (t.fp8 && (!t.s_gate || !t.s_up || !t.s_down || !t.s_shared_in || !t.s_shared_out)) ||
+      (t.w_shared_scale && (!t.shared_scale || t.fp8)))
+    return fail(kBadArg, "moe_experts: null pointer or a shared-expert gate with fp8 weights");
+  if (t.rows <= 0 || t.rows > 65535 || t.k <= 0 || t.k > 64 || t.experts <= 0 ||
+      t.hidden_size % 64 || t.hidden_size > 4096 || t.inter % 64 || t.inter > 2048 ||
+      t.shared_inter % 64 || t.shared_inter > 2048 || t.hidden_ld < t.inter ||
+      t.hidden_ld < t.shared_inter || t.hidden_ld % 8)
+    return fail(kBadShape, "moe_experts: rows=%d k=%d H=%d (<= 4096) I=%d IS=%d (<= 2048) "
+                "ld=%d", t.rows, t.k, t.hidden_size, t.inter, t.shared_inter, t.hidden_ld);
+  MoeArgs a;
+  a.x = (const bf16*)t.x;
+  a.weights = t.weights;
+  a.idx = (const int*)t.idx;
+  a.w_gate = t.w_gate;
+  a.w_up = t.w_up;
+  a.w_down = t.w_down;
+  a.s_gate = t.s_gate;
+  a.s_up = t.s_up;
+  a.s_down = t.s_down;
+  a.w_sin = t.w_shared_in;
+  a.w_sout = t.w_shared_out;
+  a.s_sin = t.s_shared_in;
+  a.s_sout = t.s_shared_out;
+  a.w_sscale = (const bf16*)t.w_shared_scale;
+  a.hidden = (bf16*)t.hidden;
+  a.sscale = t.shared_scale;
+  a.out = t.out;
+  a.H = t.hidden_size;
+  a.I = t.inter;
+  a.IS = t.shared_inter;
+  a.IM = t.hidden_ld;
+  a.k = t.k;
+  a.E = t.experts;
+  a.err = t.err;
+  auto s = (hipStream_t)stream;
+  const int im = t.inter > t.shared_inter ? t.inter : t.shared_inter;
+  const dim3 g1((im + 2 * kWavesPerBlock - 1) / (2 * kWavesPerBlock), t.k + 1, t.rows);
+  const dim3 g2((t.hidden_size + 2 * kWavesPerBlock - 1) / (2 * kWavesPerBlock), t.rows);
+  if (t.fp8 && t.policy == TFD_POLICY_BF16) return launch_moe<true, false>(a, g1, g2, s);
+  if (!t.fp8 && t.policy == TFD_POLICY_F32) return launch_moe<false, true>(a, g1, g2, s);
+  if (!t.fp8 && t.policy == TFD_POLICY_BF16) return launch_moe<false, false>(a, g1, g2, s);
+  return fail(kUnsupported, "moe_experts: fp8 weights with the f32 policy are not built");
+}
+
+int tfd_gdn_step(const TfdGdnArgs* args, void* stream) {
+  if (!args) return fail(kBadArg, "gdn_step: null args");
+  const TfdGdnArgs& t = *args;
+  if (!t.proj || !t.conv_in || !t.conv_out || !t.state || !t.conv_w || !t.a_log ||
+      !t.dt_bias || !t.gamma || !t.out || t.conv_in == t.conv_out)
+    return fail(kBadArg, "gdn_step: null pointer, or conv_out == conv_in");
+  if (t.rows <= 0 || t.rows > kMaxRowsH || t.head_k_dim != 128 || t.head_v_dim != 128 ||
+      t.key_heads <= 0 || t.value_heads % t.key_heads || t.conv_kernel != 4 ||
+      t.proj_ld < 2 * t.key_heads * 128 + 2 * t.value_heads * 128 + 2 * t.value_heads)
+    return fail(kBadShape, "gdn_step: rows=%d (1..32) dk=%d dv=%d (128) hk=%d hv=%d kw=%d",
+                t.rows, t.head_k_dim, t.head_v_dim, t.key_heads, t.value_heads,
+                t.conv_kernel);
+  GdnArgs a;
+  a.proj = t.proj;
+  a.ldp = t.proj_ld;
+  a.conv_in = t.conv_in;
+  a.conv_out = t.conv_out;
+  a.state = t.state;
+  a.conv_w = (const bf16*)t.conv_w;
+  a.a_log = (const bf16*)t.a_log;
+  a.dt_bias = (const bf16*)t.dt_bias;
+  a.gamma = (const bf16*)t.gamma;
+  a.out = (bf16*)t.out;
+  a.hk = t.key_heads;
+  a.hv = t.value_heads;
+  a.l2_eps = t.l2_eps;
+  a.rms_eps = t.rms_eps;
+  hipLaunchKernelGGL(k_gdn_step<128>, dim3(t.value_heads, t.rows), dim3(256), 0,
+                     (hipStream_t)stream, a);
+  return launched("gdn_step");
+}
+
+int tfd_mamba_step(const TfdMambaArgs* args, void* stream) {
+  if (!args) return fail(kBadArg, "mamba_step: null args");
+  const TfdMambaArgs& t = *args;
+  if (!t.proj || !t.conv_in || !t.conv_out || !t.state || !t.conv_w || !t.conv_b ||
+      !t.a_log || !t.dt_bias || !t.d_skip || !t.gamma || !t.gated || !t.ssq || !t.out ||
+      t.conv_in == t.conv_out)
+    return fail(kBadArg, "mamba_step: null pointer, or conv_out == conv_in");
+  if (t.rows <= 0 || t.rows > kMaxRowsH || t.head_dim != 64 || t.state_dim != 128 ||
+      t.groups != 1 || t.conv_kernel != 4 || t.heads <= 0 ||
+      t.proj_ld < 2 * t.heads * 64 + 2 * 128 + t.heads)
+    return fail(kBadShape, "mamba_step: rows=%d (1..32) heads=%d hd=%d (64) ns=%d (128) "
+                "groups=%d (1) kw=%d (4)", t.rows, t.heads, t.head_dim, t.state_dim, t.groups,
+                t.conv_kernel);
+  MambaArgs a;
+  a.proj = (const bf16*)t.proj;
+  a.ldp = t.proj_ld;
+  a.conv_in = (const bf16*)t.conv_in;
+  a.conv_out = (bf16*)t.conv_out;
+  a.state = t.state;
+  a.conv_w = (const bf16*)t.conv_w;
+  a.conv_b = (const bf16*)t.conv_b;
+  a.a_log = (const bf16*)t.a_log;
+  a.dt_bias = (const bf16*)t.dt_bias;
+  a.d_skip = (const bf16*)t.d_skip;
+  a.gamma = (const bf16*)t.gamma;
+  a.gated = t.gated;
+  a.ssq = t.ssq;
+  a.out = (bf16*)t.out;
+  a.nh = t.heads;
+  a.ns = 128;
+  a.eps = t.eps;
+  auto s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_mamba_step<64>, dim3(t.heads, t.rows), dim3(kBlock), 0, s, a);
+  hipLaunchKernelGGL(k_mamba_norm, dim3(t.rows), dim3(kBlock), 0, s, a, t.heads * 64);
+  return launched("mamba_step");
+}
+
+}  // extern "C"

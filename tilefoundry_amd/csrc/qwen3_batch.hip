@@ -292,10 +292,62 @@ __global__ __launch_bounds__(kWaves * kWave) void k_gemm_skinny(
 // of loads plus a barrier -- what the narrow projections need, whose weights
 // alone do not keep the chip busy for long.
 // ---------------------------------------------------------------------------
-template <int kEpi, int kT, int kKW, int kDepth>
+// fp8-e4m3fn weights: the same block order at one byte per value (512-byte
+// blocks, lane l's 8 bytes at l * 8); gfx950 decodes e4m3fn exactly, every
+// value is exact in bf16, so the products and the f32 sums are those of the
+// bf16 path, and the output channel's scale multiplies the sum.
+template <bool kFp8>
+struct SkW {
+  using Raw = u32x4;
+  static __device__ __forceinline__ Raw load(const void* base, int64_t block, int lane) {
+    return load16_stream((const bf16*)base + block * 512 + lane * 8);
+  }
+  static __device__ __forceinline__ bf16x8_t value(const Raw& r) {
+    return __builtin_bit_cast(bf16x8_t, r);
+  }
+};
+template <>
+struct SkW<true> {
+  using Raw = u32x2;
+  static __device__ __forceinline__ Raw load(const void* base, int64_t block, int lane) {
+    return __builtin_nontemporal_load(
+        reinterpret_cast<const u32x2*>((const uint8_t*)base + block * 512 + lane * 8));
+  }
+  static __device__ __forceinline__ bf16x8_t value(const Raw& r) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t v0 = __builtin_amdgcn_cvt_pk_f32_fp8(r.x, false);
+    const f32x2_t v1 = __builtin_amdgcn_cvt_pk_f32_fp8(r.x, true);
+    const f32x2_t v2 = __builtin_amdgcn_cvt_pk_f32_fp8(r.y, false);
+    const f32x2_t v3 = __builtin_amdgcn_cvt_pk_f32_fp8(r.y, true);
+    const bf16x8_t o = {(__bf16)v0.x, (__bf16)v0.y, (__bf16)v1.x, (__bf16)v1.y,
+                        (__bf16)v2.x, (__bf16)v2.y, (__bf16)v3.x, (__bf16)v3.y};
+    return o;
+  }
+};
+
+__global__ __launch_bounds__(kBlock) void k_pack_skinny_fp8(const uint8_t* __restrict__ W, int ldw,
+                                                            int N, int K,
+                                                            uint8_t* __restrict__ out,
+                                                            int64_t chunks) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= chunks) return;
+  const int l = (int)(i & 63);
+  const int64_t blk = i >> 6;
+  const int ks = K / 32;
+  const int64_t t = blk / ks;
+  const int st = (int)(blk % ks);
+  const int64_t row = t * 16 + (l & 15);
+  u32x2 v = {0u, 0u};
+  if (row < N) v = *reinterpret_cast<const u32x2*>(W + row * ldw + st * 32 + 8 * (l >> 4));
+  *reinterpret_cast<u32x2*>(out + i * 8) = v;
+}
+
+template <int kEpi, int kT, int kKW, int kDepth, bool kFp8 = false>
 __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
-    const bf16* __restrict__ X, const bf16* __restrict__ W, int M, int K, int N,
-    const bf16* __restrict__ resid, int ldr, void* __restrict__ out, int ldo) {
+    const bf16* __restrict__ X, const void* __restrict__ W, int M, int K, int N,
+    const bf16* __restrict__ resid, int ldr, void* __restrict__ out, int ldo,
+    const float* __restrict__ wscale) {
+  using WL = SkW<kFp8>;
   __shared__ f32x4 red[kKW][kT][2][kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -306,16 +358,17 @@ __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
   const int s0 = wave * steps;
   // X in operand order: step k's two 16-row halves are consecutive KiBs
   const bf16* xa = X + (int64_t)s0 * 1024 + lane * 8;
-  const bf16* wt[kT];
+  int64_t wt[kT];                            // block index of (tile, step s0)
 #pragma unroll
   for (int t = 0; t < kT; ++t) {
     const int tt = tile0 + t < ntiles ? tile0 + t : ntiles - 1;
-    wt[t] = W + ((int64_t)tt * ksteps + s0) * 512 + lane * 8;
+    wt[t] = (int64_t)tt * ksteps + s0;
   }
-  u32x4 b[kDepth][kT], a0[kDepth], a1[kDepth];
+  typename WL::Raw b[kDepth][kT];
+  u32x4 a0[kDepth], a1[kDepth];
   auto issue = [&](int u, int k) {
 #pragma unroll
-    for (int t = 0; t < kT; ++t) b[u][t] = load16_stream(wt[t] + (int64_t)k * 512);
+    for (int t = 0; t < kT; ++t) b[u][t] = WL::load(W, wt[t] + k, lane);
     a0[u] = load16(xa + (int64_t)k * 1024);
     a1[u] = load16(xa + (int64_t)k * 1024 + 512);
   };
@@ -337,7 +390,7 @@ __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
       const bf16x8_t x1 = __builtin_bit_cast(bf16x8_t, a1[u]);
 #pragma unroll
       for (int t = 0; t < kT; ++t) {
-        const bf16x8_t bw = __builtin_bit_cast(bf16x8_t, b[u][t]);
+        const bf16x8_t bw = WL::value(b[u][t]);
         c[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, bw, c[t][0], 0, 0, 0);
         c[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, bw, c[t][1], 0, 0, 0);
       }
@@ -366,6 +419,15 @@ __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
 #pragma unroll
       for (int e = 0; e < 4; ++e) sum[h][e] += v[e];
     }
+  }
+  if (kFp8) {
+    // every lane holds one output column: its channel's scale
+    const int n = (tile0 + t) * 16 + (lane & 15);
+    const float sc = wscale[n < N ? n : N - 1];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sum[h][e] *= sc;
   }
   skinny_store<kEpi>(sum, M > 16 ? 2 : 1, tile0 + t, lane, M, N, resid, ldr, out, ldo);
 }
@@ -697,6 +759,54 @@ int tfd_pack_skinny_bf16(const void* w, int ldw, int N, int K, void* packed, voi
   return launched("pack_skinny");
 }
 
+int tfd_pack_skinny_fp8(const void* w, int ldw, int N, int K, void* packed, void* stream) {
+  if (!w || !packed) return fail(kBadArg, "pack_skinny_fp8: null pointer");
+  if (N <= 0 || K <= 0 || K % 256 || ldw < K || ldw % 8)
+    return fail(kBadShape, "pack_skinny_fp8: N=%d K=%d (multiple of 256) ldw=%d", N, K, ldw);
+  const int64_t chunks = (int64_t)(N + 15) / 16 * (K / 32) * 64;
+  hipLaunchKernelGGL(k_pack_skinny_fp8, dim3((unsigned)((chunks + kBlock - 1) / kBlock)),
+                     dim3(kBlock), 0, (hipStream_t)stream, (const uint8_t*)w, ldw, N, K,
+                     (uint8_t*)packed, chunks);
+  return launched("pack_skinny_fp8");
+}
+
+int tfd_gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M, int K, int N,
+                        int epilogue, const void* resid, int ldr, void* out, int ldo,
+                        void* stream) {
+  if (!x || !w || !scale || !out) return fail(kBadArg, "gemm_skinny_fp8: null pointer");
+  if (M <= 0 || M > kMaxRows || K <= 0 || K % 256 || N <= 0)
+    return fail(kBadShape, "gemm_skinny_fp8: M=%d (1..32) K=%d (multiple of 256) N=%d", M, K, N);
+  if (epilogue == TFD_EPI_RESID && (!resid || ldr < N))
+    return fail(kBadArg, "gemm_skinny_fp8: residual epilogue needs resid with ldr >= N");
+  if (epilogue == TFD_EPI_SWIGLU ? (N % 2 || (N / 2) % 32) : ldo < N)
+    return fail(kBadShape, "gemm_skinny_fp8: ldo=%d N=%d", ldo, N);
+  auto s = (hipStream_t)stream;
+  auto xb = (const bf16*)x;
+  auto rb = (const bf16*)resid;
+  const int ntiles = (N + 15) / 16;
+  const int steps = K / 32 / 8;
+  const dim3 grid(ntiles);
+#define TFD_KSPLIT8(EPI, D)                                                                     \
+  hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 8, D, true>), grid, dim3(8 * kWave), 0, s, xb, w, \
+                     M, K, N, rb, ldr, out, ldo, scale)
+#define TFD_KSPLIT8_EPI(EPI)                    \
+  if (steps % 8 == 0) TFD_KSPLIT8(EPI, 8);      \
+  else if (steps % 4 == 0) TFD_KSPLIT8(EPI, 4); \
+  else if (steps % 2 == 0) TFD_KSPLIT8(EPI, 2); \
+  else TFD_KSPLIT8(EPI, 1);
+  switch (epilogue) {
+    case TFD_EPI_STORE: TFD_KSPLIT8_EPI(kSkStore); break;
+    case TFD_EPI_RESID: TFD_KSPLIT8_EPI(kSkResid); break;
+    case TFD_EPI_SWIGLU: TFD_KSPLIT8_EPI(kSkSwiglu); break;
+    case TFD_EPI_LOGITS: TFD_KSPLIT8_EPI(kSkLogits); break;
+    default:
+      return fail(kBadArg, "gemm_skinny_fp8: epilogue %d", epilogue);
+  }
+#undef TFD_KSPLIT8_EPI
+#undef TFD_KSPLIT8
+  return launched("gemm_skinny_fp8");
+}
+
 int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int epilogue,
                          const void* resid, int ldr, void* out, int ldo, float* work,
                          int64_t work_floats, void* stream) {
@@ -721,7 +831,7 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
     const dim3 grid((ntiles + kt - 1) / kt);
 #define TFD_KSPLIT(EPI, KT, D)                                                                  \
   hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D>), grid, dim3(8 * kWave), 0, s, xb, wb, M, \
-                     K, N, rb, ldr, out, ldo)
+                     K, N, rb, ldr, out, ldo, nullptr)
 #define TFD_KSPLIT_EPI(EPI)                              \
   if (kt == 2 && steps % 8 == 0) TFD_KSPLIT(EPI, 2, 8);  \
   else if (steps % 8 == 0) TFD_KSPLIT(EPI, 1, 8);        \
