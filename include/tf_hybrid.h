@@ -135,6 +135,55 @@ typedef struct {
 } TfdMambaArgs;
 int tfd_mamba_step(const TfdMambaArgs* args, void* stream);
 
+/* The full-attention layers of both hybrids at one token per sequence,
+ * between the q/k/v projections and o_proj: GQA decode over the paged bf16 KV
+ * cache of tf_decode.h ([pages][kv_heads][16][head_dim], 16 positions a page),
+ * after appending this token's key and value at pos[b].
+ *  policy TFD_POLICY_F32 (C4, Qwen3_5FullAttention.full_attention,
+ *    tests/models/qwen3_5_35b_a3b/model.py:234-346 / torch_ref.py:318-409; SURVEY
+ *    entry attn_hd256_partial_rope): qkv f32 [rows][ldq] (bf16 values) holds per
+ *    query head its query then its output gate (2 head_dim each), then the keys,
+ *    then the values; per-head RMSNorm (gamma_q, gamma_k, flat), rotate-half
+ *    RoPE on the first rot_dim dims (cos/sin bf16 [rope_rows][rot_dim]), query
+ *    times `scale`, softmax, output times sigmoid(gate); all f32; the cache keeps
+ *    bf16(k_rope).  head_dim 256, 8 query heads per kv head.
+ *  policy TFD_POLICY_BF16 (C5, GraniteAttention.attend after cache_update,
+ *    examples/granite_4_0_h_small-cuda/model.py:310-366; SURVEY entry
+ *    attn_decode_nope): qkv bf16 [rows][ldq] = queries, keys, values; no
+ *    position embedding; score = bf16(sum bf16(q k)) * scale in f32, softmax f32
+ *    rounded to bf16, attn = bf16(sum bf16(p v)).  head_dim 128, 4 query heads per
+ *    kv head.  gamma/cos/sin unused.
+ * out: o_proj's input in operand order (32 x heads * head_dim bf16).  Work:
+ * scores f32 [rows][heads][score_stride >= max_pages * 16], stats f32
+ * [rows][heads][nsplit][2], part f32 [rows][heads][nsplit][head_dim], counters
+ * int32 [rows][kv_heads] (zero; left zero).  A split covers split_len positions
+ * (a multiple of 16, <= 512); nsplit * split_len >= max_pages * 16.  A position
+ * outside the page (or rope) table raises TFD_ERR_POS_RANGE in err, a page
+ * outside the pool TFD_ERR_PAGE_RANGE. */
+typedef struct {
+  const void* qkv;
+  int ldq;
+  const void *gamma_q, *gamma_k, *cos_table, *sin_table;
+  int rope_rows, rot_dim;
+  const int32_t* pos;
+  const int32_t* page_table;
+  int max_pages;
+  void *k_pool, *v_pool;
+  int num_pages;
+  int rows, heads, kv_heads, head_dim;
+  float scale, eps;
+  float* scores;
+  int score_stride;
+  float* stats;
+  float* part;
+  int32_t* counters;
+  int nsplit, split_len;
+  void* out;
+  int policy;
+  int32_t* err;
+} TfdGqaArgs;
+int tfd_gqa_decode(const TfdGqaArgs* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -232,3 +232,84 @@ def mamba_step(proj, conv_state, ssm_state, conv_w, conv_b, a_log, dt_bias, d_sk
     normed = gated * torch.rsqrt(gated.pow(2).mean(-1, keepdim=True) + eps) * gamma_ssm.float()
     new_conv = window[:, :, 1:].contiguous()
     return bf(normed), new_conv, updated
+
+
+# ---------------------------------------------------------------------------
+# Full-attention layers of the hybrids, between the projections and o_proj
+# ---------------------------------------------------------------------------
+def _rotate_half(x):
+    """HF ``rotate_half``: ``cat(-x[..., h:], x[..., :h])`` (torch_ref.py:157-162)."""
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+def _rms_flat(x, w, eps):
+    """``tf.rms_norm`` as torch_ref.py:145-154 spells it: flat in w, f32."""
+    xf = x.float()
+    return xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps) * w.float()
+
+
+def qwen35_attend(qg, k, v, k_past, v_past, gamma_q, gamma_k, cos, sin, scale, eps=1e-6):
+    """C4 (a16): ``full_attention`` of torch_ref.py:335-409 between the q/k/v
+    projections and o_proj, for a batch of sequences each with its own past.
+
+    qg [B][HQ][2D] f32 (bf16 values; query then output gate per head, the
+    interleaving of :371-377), k/v [B][HKV][D] f32 (bf16 values); k_past[b],
+    v_past[b] [C_b][HKV][D] (bf16 values, the cache before this token);
+    gamma_q/gamma_k [D]; cos/sin [B][ROT] (the rows at each sequence's
+    position); scale a float.  Per-head RMSNorm, rotate-half RoPE on the first
+    ROT dims (_partial_rope :165-181), softmax over past + this token, output
+    gate ``attn * sigmoid(gate)``.  Sums and the softmax in f64.
+    -> (gated f32 [B][HQ*D] (o_proj's input before its bf16 cast),
+        k_rope f32 [B][HKV][D] (the cache stores it rounded to bf16))."""
+    B, HQ, D2 = qg.shape
+    D = D2 // 2
+    HKV = k.shape[1]
+    G = HQ // HKV
+    rot = cos.shape[-1]
+    out = torch.zeros(B, HQ * D)
+    k_rope = torch.zeros(B, HKV, D)
+
+    def prope(x, b):
+        r = x[:, :rot]
+        return torch.cat((r * cos[b].float() + _rotate_half(r) * sin[b].float(), x[:, rot:]), -1)
+
+    for b in range(B):
+        q = qg[b, :, :D].float()
+        gate = qg[b, :, D:].float()
+        q_s = prope(_rms_flat(q, gamma_q, eps), b) * scale
+        kr = prope(_rms_flat(k[b], gamma_k, eps), b)
+        k_all = torch.cat((k_past[b].float(), kr[None]))
+        v_all = torch.cat((v_past[b].float(), v[b][None].float()))
+        kg = k_all.repeat_interleave(G, dim=1).double()           # [C+1][HQ][D]
+        vg = v_all.repeat_interleave(G, dim=1).double()
+        scores = (q_s.double()[None] * kg).sum(-1)                 # [C+1][HQ]
+        probs = torch.softmax(scores, dim=0)
+        attn = (probs[:, :, None] * vg).sum(0).float()             # [HQ][D]
+        out[b] = (attn * torch.sigmoid(gate)).reshape(-1)
+        k_rope[b] = kr
+    return out, k_rope
+
+
+def granite_attend(q, k_new, v_new, k_past, v_past, scale):
+    """C5 (a20): ``GraniteAttention.attend`` (model.py:310-344) after
+    ``cache_update`` at cur_pos (:362-364), for a batch: no position embedding,
+    bf16 ops rounded as the HIR writes them, the softmax in f32 (here f64, then
+    cast).  q [B][HQ][D], k_new/v_new [B][HKV][D], k_past[b]/v_past[b]
+    [C_b][HKV][D], all bf16 values; scale the attention multiplier.  Masked
+    positions contribute exp(-inf) = 0, so only positions 0..cur_pos are summed.
+    -> attn bf16 values [B][HQ*D] (o_proj's input)."""
+    B, HQ, D = q.shape
+    HKV = k_new.shape[1]
+    G = HQ // HKV
+    out = torch.zeros(B, HQ * D)
+    for b in range(B):
+        k_all = torch.cat((k_past[b].float(), k_new[b][None].float()))
+        v_all = torch.cat((v_past[b].float(), v_new[b][None].float()))
+        kg = k_all.repeat_interleave(G, dim=1)                     # [C+1][HQ][D]
+        vg = v_all.repeat_interleave(G, dim=1)
+        scores = bf(bf(q[b].float()[None] * kg).double().sum(-1).float())
+        scaled = scores * scale
+        probs = bf(torch.softmax(scaled.double(), dim=0).float())
+        out[b] = bf(bf(probs[:, :, None] * vg).double().sum(0).float()).reshape(-1)
+    return out

@@ -57,7 +57,7 @@ def test_library_exports_every_declared_entry():
 
 STRUCTS = {"TfdDecodeArgs": _lib.TfdDecodeArgs, "TfdLayer": _lib.TfdLayer,
            "TfdMoeArgs": _lib.TfdMoeArgs, "TfdGdnArgs": _lib.TfdGdnArgs,
-           "TfdMambaArgs": _lib.TfdMambaArgs}
+           "TfdMambaArgs": _lib.TfdMambaArgs, "TfdGqaArgs": _lib.TfdGqaArgs}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="no C compiler")

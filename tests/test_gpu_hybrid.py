@@ -371,3 +371,151 @@ def test_mamba_step_two_tokens(gpu_device, rows):
         assert srep["max_rel"] < 1e-3 and srep["cos"] > 0.999999, srep
         r = assert_close_bf16(got, want, max_rel=2e-2, min_cos=0.9999, name=f"mamba {step}")
         assert r["within_1ulp"] >= 0.99, r
+
+
+# ---------------------------------------------------------------------------
+# Full-attention layers (C4: 256-wide heads, RoPE on 64 dims, output gate;
+# C5: 128-wide heads, no position embedding, HIR rounding)
+# ---------------------------------------------------------------------------
+def _paged_pool(pasts, hkv, d, max_pages, gen):
+    """Logical caches [C][HKV][D] -> a shuffled page pool (NaN where unused) and
+    the page table; every sequence gets max_pages distinct pages."""
+    B = len(pasts)
+    num_pages = B * max_pages + 3
+    table = torch.randperm(num_pages, generator=gen)[:B * max_pages].view(B, max_pages)
+    kpool = torch.full((num_pages, hkv, 16, d), float("nan"), dtype=BF)
+    vpool = kpool.clone()
+    for b, (kp, vp) in enumerate(pasts):
+        j = torch.arange(kp.shape[0])
+        kpool[table[b, j // 16], :, j % 16] = kp.to(BF)
+        vpool[table[b, j // 16], :, j % 16] = vp.to(BF)
+    return kpool, vpool, table.to(torch.int32)
+
+
+def _gqa_call(qkv, pos, table, kpool, vpool, *, heads, kv_heads, head_dim, scale, split_len,
+              policy, gamma_q=None, gamma_k=None, cos=None, sin=None, eps=1e-6):
+    dev = "cuda:0"
+    rows = qkv.shape[0]
+    max_pages = table.shape[1]
+    nsplit = -(-max_pages * 16 // split_len)
+    stride = max_pages * 16
+    keep = []
+
+    def d(t):
+        t = t.to(dev).contiguous()
+        keep.append(t)
+        return ptr(t)
+
+    kp, vp = kpool.to(dev), vpool.to(dev)
+    out = torch.full((32 * heads * head_dim,), float("nan"), device=dev, dtype=BF)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
+    counters = torch.zeros(rows * kv_heads, dtype=torch.int32, device=dev)
+    a = _lib.TfdGqaArgs()
+    a.qkv, a.ldq = d(qkv), qkv.shape[1]
+    if policy == _lib.POLICY_F32:
+        a.gamma_q, a.gamma_k, a.cos_table, a.sin_table = d(gamma_q.to(BF)), d(gamma_k.to(BF)), \
+            d(cos.to(BF)), d(sin.to(BF))
+        a.rope_rows, a.rot_dim = cos.shape[0], cos.shape[1]
+    a.pos, a.page_table, a.max_pages = d(pos.to(torch.int32)), d(table), max_pages
+    a.k_pool, a.v_pool, a.num_pages = ptr(kp), ptr(vp), kpool.shape[0]
+    a.rows, a.heads, a.kv_heads, a.head_dim = rows, heads, kv_heads, head_dim
+    a.scale, a.eps = scale, eps
+    a.scores = d(torch.full((rows * heads * stride,), float("nan")))
+    a.score_stride = stride
+    a.stats = d(torch.full((rows * heads * nsplit * 2,), float("nan")))
+    a.part = d(torch.full((rows * heads * nsplit * head_dim,), float("nan")))
+    a.counters = ptr(counters)
+    a.nsplit, a.split_len = nsplit, split_len
+    a.out, a.policy, a.err = ptr(out), policy, ptr(err)
+    lib().tfd_gqa_decode(ctypes.addressof(a), _stream())
+    torch.cuda.synchronize()
+    assert not counters.any()
+    return (from_operand_order(out, rows, heads * head_dim).float().cpu(), kp.cpu(), vp.cpu(),
+            int(err.item()))
+
+
+def _rope_rows(rows, rot, theta):
+    inv = 1.0 / theta ** (torch.arange(0, rot, 2, dtype=torch.float64) / rot)
+    f = torch.arange(rows, dtype=torch.float64)[:, None] * inv[None]
+    emb = torch.cat((f, f), dim=-1)
+    return H.bf(emb.cos().float()), H.bf(emb.sin().float())
+
+
+@pytest.mark.parametrize("pos,split_len", [([0], 128), ([511], 128), ([700], 512),
+                                           ([0, 15, 16, 17, 127, 128, 129, 300, 511, 512, 640,
+                                             700, 701, 750, 3, 64], 128)])
+def test_gqa_decode_c4(gpu_device, pos, split_len):
+    """Qwen3.5 full attention: 16 q / 2 kv heads of 256, RoPE on 64 dims."""
+    g = torch.Generator().manual_seed(len(pos) * 1000 + pos[0] + split_len)
+    B, HQ, HKV, D, rot = len(pos), 16, 2, 256, 64
+    max_pages = 48
+    qg = H.bf(torch.randn(B, HQ, 2 * D, generator=g))
+    k = H.bf(torch.randn(B, HKV, D, generator=g))
+    v = H.bf(torch.randn(B, HKV, D, generator=g))
+    pasts = [(H.bf(torch.randn(p, HKV, D, generator=g)), H.bf(torch.randn(p, HKV, D, generator=g)))
+             for p in pos]
+    gq = H.bf(1 + 0.2 * torch.randn(D, generator=g))
+    gk = H.bf(1 + 0.2 * torch.randn(D, generator=g))
+    cos, sin = _rope_rows(1024, rot, 1e7)
+    scale = D ** -0.5
+    ldq = HQ * 2 * D + 2 * HKV * D + 8
+    qkv = torch.zeros(B, ldq)
+    qkv[:, :HQ * 2 * D] = qg.reshape(B, -1)
+    qkv[:, HQ * 2 * D:HQ * 2 * D + HKV * D] = k.reshape(B, -1)
+    qkv[:, HQ * 2 * D + HKV * D:HQ * 2 * D + 2 * HKV * D] = v.reshape(B, -1)
+    kpool, vpool, table = _paged_pool(pasts, HKV, D, max_pages, g)
+    got, kp, vp, err = _gqa_call(qkv, torch.tensor(pos), table, kpool, vpool, heads=HQ,
+                                 kv_heads=HKV, head_dim=D, scale=scale, split_len=split_len,
+                                 policy=_lib.POLICY_F32, gamma_q=gq, gamma_k=gk, cos=cos,
+                                 sin=sin)
+    assert err == 0
+    P = torch.tensor(pos)
+    want, k_rope = H.qwen35_attend(qg, k, v, [p[0] for p in pasts], [p[1] for p in pasts], gq,
+                                   gk, cos[P], sin[P], scale)
+    r = assert_close_bf16(got, H.bf(want), max_rel=1e-2, min_cos=0.99999, name="gqa c4")
+    assert r["within_1ulp"] >= 0.999, r
+    pg = table[torch.arange(B), P // 16].long()
+    torch.testing.assert_close(kp[pg, :, P % 16].float(), H.bf(k_rope), atol=0, rtol=1e-2)
+    assert torch.equal(vp[pg, :, P % 16].float(), v)
+
+
+@pytest.mark.parametrize("pos,split_len", [([0, 1, 2, 100, 255, 256, 1000, 2000], 256),
+                                           ([1999], 16), ([37], 512)])
+def test_gqa_decode_c5(gpu_device, pos, split_len):
+    """Granite attention: 32 q / 8 kv heads of 128, no RoPE, HIR rounding."""
+    g = torch.Generator().manual_seed(len(pos) * 100 + pos[0] + split_len)
+    B, HQ, HKV, D = len(pos), 32, 8, 128
+    max_pages = 128
+    q = H.bf(torch.randn(B, HQ, D, generator=g))
+    k = H.bf(torch.randn(B, HKV, D, generator=g))
+    v = H.bf(torch.randn(B, HKV, D, generator=g))
+    pasts = [(H.bf(torch.randn(p, HKV, D, generator=g)), H.bf(torch.randn(p, HKV, D, generator=g)))
+             for p in pos]
+    scale = 0.05
+    qkv = torch.cat([q.reshape(B, -1), k.reshape(B, -1), v.reshape(B, -1)], dim=1).to(BF)
+    kpool, vpool, table = _paged_pool(pasts, HKV, D, max_pages, g)
+    got, kp, vp, err = _gqa_call(qkv, torch.tensor(pos), table, kpool, vpool, heads=HQ,
+                                 kv_heads=HKV, head_dim=D, scale=scale, split_len=split_len,
+                                 policy=_lib.POLICY_BF16)
+    assert err == 0
+    want = H.granite_attend(q, k, v, [p[0] for p in pasts], [p[1] for p in pasts], scale)
+    r = assert_close_bf16(got, want, max_rel=2e-2, min_cos=0.9999, name="gqa c5")
+    assert r["within_1ulp"] >= 0.99, r
+    P = torch.tensor(pos)
+    pg = table[torch.arange(B), P // 16].long()
+    assert torch.equal(kp[pg, :, P % 16].float(), k)
+    assert torch.equal(vp[pg, :, P % 16].float(), v)
+
+
+def test_gqa_decode_flags_a_position_past_the_table(gpu_device):
+    """A position beyond the page table raises TFD_ERR_POS_RANGE; no block reads
+    the cache for that sequence, the others are served."""
+    g = torch.Generator().manual_seed(5)
+    B, HQ, HKV, D = 2, 32, 8, 128
+    pasts = [(torch.zeros(3, HKV, D), torch.zeros(3, HKV, D))] * 2
+    kpool, vpool, table = _paged_pool(pasts, HKV, D, 4, g)
+    qkv = H.bf(torch.randn(B, (HQ + 2 * HKV) * D, generator=g)).to(BF)
+    _, _, _, err = _gqa_call(qkv, torch.tensor([3, 64]), table, kpool, vpool, heads=HQ,
+                             kv_heads=HKV, head_dim=D, scale=0.1, split_len=16,
+                             policy=_lib.POLICY_BF16)
+    assert err == _lib.ERR_POS_RANGE

@@ -256,3 +256,83 @@ def test_mamba_step_matches_hf_composition():
     rel = lambda a, w: ((a - w).abs().max() / w.abs().max()).item()
     assert rel(new_state, st) < 2e-2
     assert rel(got, want) < 3e-2
+
+
+def _rope_rows(pos, rot, theta=1e6):
+    inv = 1.0 / theta ** (torch.arange(0, rot, 2, dtype=torch.float64) / rot)
+    f = torch.tensor(pos, dtype=torch.float64)[:, None] * inv[None]
+    emb = torch.cat((f, f), dim=-1)
+    return H.bf(emb.cos().float()), H.bf(emb.sin().float())
+
+
+def test_qwen35_attend_matches_hf_attention_pieces():
+    """Per-head norm (HF's 1 + w with w = gamma - 1), partial RoPE
+    (apply_rotary_pos_emb with a 16-wide cache on 64-wide heads), eager GQA
+    attention over the past plus this token, sigmoid output gate."""
+    g = torch.Generator().manual_seed(9)
+    B, HQ, HKV, D, rot = 3, 8, 2, 64, 16
+    past = [5, 0, 17]
+    qg = H.bf(torch.randn(B, HQ, 2 * D, generator=g))
+    k = H.bf(torch.randn(B, HKV, D, generator=g))
+    v = H.bf(torch.randn(B, HKV, D, generator=g))
+    k_past = [H.bf(torch.randn(c, HKV, D, generator=g)) for c in past]
+    v_past = [H.bf(torch.randn(c, HKV, D, generator=g)) for c in past]
+    gq = H.bf(1 + 0.2 * torch.randn(D, generator=g))
+    gk = H.bf(1 + 0.2 * torch.randn(D, generator=g))
+    cos, sin = _rope_rows(past, rot)
+    scale = D ** -0.5
+    got, kr = H.qwen35_attend(qg, k, v, k_past, v_past, gq, gk, cos, sin, scale)
+    qn = hf_q.Qwen3_5MoeRMSNorm(D, eps=1e-6)
+    kn = hf_q.Qwen3_5MoeRMSNorm(D, eps=1e-6)
+    module = type("M", (), {"num_key_value_groups": HQ // HKV, "training": False})()
+    with torch.no_grad():
+        qn.weight.copy_(gq - 1)
+        kn.weight.copy_(gk - 1)
+        for b in range(B):
+            q_b = qn(qg[b, :, :D][None, None]).transpose(1, 2)            # (1, HQ, 1, D)
+            k_b = kn(k[b][None, None]).transpose(1, 2)                     # (1, HKV, 1, D)
+            q_r, k_r = hf_q.apply_rotary_pos_emb(q_b, k_b, cos[b][None, None], sin[b][None, None])
+            keys = torch.cat((k_past[b].permute(1, 0, 2)[None], k_r), dim=2)
+            vals = torch.cat((v_past[b].permute(1, 0, 2)[None], v[b][:, None][None]), dim=2)
+            o, _ = hf_q.eager_attention_forward(module, q_r, keys, vals, None, scaling=scale)
+            want = o.reshape(-1) * torch.sigmoid(qg[b, :, D:].reshape(-1))
+            torch.testing.assert_close(got[b], want, atol=2e-5, rtol=1e-4)
+            torch.testing.assert_close(kr[b], k_r[0, :, 0], atol=1e-6, rtol=1e-5)
+
+
+def test_granite_attend_matches_hf_eager_attention():
+    g = torch.Generator().manual_seed(10)
+    B, HQ, HKV, D = 2, 8, 2, 32
+    past = [9, 2]
+    q = H.bf(torch.randn(B, HQ, D, generator=g))
+    k_new = H.bf(torch.randn(B, HKV, D, generator=g))
+    v_new = H.bf(torch.randn(B, HKV, D, generator=g))
+    k_past = [H.bf(torch.randn(c, HKV, D, generator=g)) for c in past]
+    v_past = [H.bf(torch.randn(c, HKV, D, generator=g)) for c in past]
+    scale = 0.25
+    got = H.granite_attend(q, k_new, v_new, k_past, v_past, scale)
+    module = type("M", (), {"num_key_value_groups": HQ // HKV, "training": False})()
+    for b in range(B):
+        keys = torch.cat((k_past[b], k_new[b][None])).permute(1, 0, 2)[None]
+        vals = torch.cat((v_past[b], v_new[b][None])).permute(1, 0, 2)[None]
+        o, _ = hf_g.eager_attention_forward(module, q[b][:, None][None], keys, vals, None,
+                                            scaling=scale)
+        want = o.reshape(-1)
+        err = ((got[b] - want).abs().max() / want.abs().max()).item()
+        assert err < 2e-2, err
+
+
+def test_attend_with_no_past_returns_this_tokens_value():
+    """One live position: softmax is exactly 1, so attention returns v_new."""
+    g = torch.Generator().manual_seed(11)
+    q = H.bf(torch.randn(1, 4, 16, generator=g))
+    kv = H.bf(torch.randn(2, 1, 2, 16, generator=g))
+    empty = [torch.zeros(0, 2, 16)]
+    got = H.granite_attend(q, kv[0], kv[1], empty, empty, 0.3)
+    assert torch.equal(got[0], kv[1][0].repeat_interleave(2, dim=0).reshape(-1))
+    qg = H.bf(torch.randn(1, 4, 32, generator=g))
+    cos, sin = _rope_rows([0], 8)
+    got, _ = H.qwen35_attend(qg, kv[0], kv[1], empty, empty, torch.ones(16), torch.ones(16),
+                             cos, sin, 0.25)
+    want = kv[1][0].repeat_interleave(2, dim=0) * torch.sigmoid(qg[0, :, 16:])
+    assert torch.equal(got[0], want.reshape(-1))

@@ -62,6 +62,7 @@ SIGNATURES: dict[str, list] = {
     "tfd_moe_experts": [P, P],
     "tfd_gdn_step": [P, P],
     "tfd_mamba_step": [P, P],
+    "tfd_gqa_decode": [P, P],
 }
 RESTYPES = {"tfd_last_error": ctypes.c_char_p}
 UNCHECKED = {"tfd_abi_version", "tfd_decode_persistent_grid"}
@@ -111,6 +112,24 @@ class TfdMambaArgs(ctypes.Structure):
         *[(n, c_int) for n in ("rows", "heads", "head_dim", "state_dim", "groups",
                                 "conv_kernel")],
         ("eps", c_float),
+    ]
+
+
+class TfdGqaArgs(ctypes.Structure):
+    """``TfdGqaArgs`` of include/tf_hybrid.h, field for field."""
+
+    _fields_ = [
+        ("qkv", c_void_p), ("ldq", c_int),
+        *[(n, c_void_p) for n in ("gamma_q", "gamma_k", "cos_table", "sin_table")],
+        ("rope_rows", c_int), ("rot_dim", c_int),
+        ("pos", c_void_p), ("page_table", c_void_p), ("max_pages", c_int),
+        ("k_pool", c_void_p), ("v_pool", c_void_p), ("num_pages", c_int),
+        *[(n, c_int) for n in ("rows", "heads", "kv_heads", "head_dim")],
+        ("scale", c_float), ("eps", c_float),
+        ("scores", c_void_p), ("score_stride", c_int),
+        ("stats", c_void_p), ("part", c_void_p), ("counters", c_void_p),
+        ("nsplit", c_int), ("split_len", c_int),
+        ("out", c_void_p), ("policy", c_int), ("err", c_void_p),
     ]
 
 
