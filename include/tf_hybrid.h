@@ -63,14 +63,20 @@ int tfd_route_topk(const float* logits, int ldl, int rows, int experts, int k, i
  * routing (replaces Qwen3_5MoE.routed_experts/shared_expert/experts,
  * tests/models/qwen3_5_35b_a3b/model.py:383-456 / torch_ref.py:451-530, and
  * GraniteMoE.routed_experts/shared_mlp/experts, granite model.py:406-471; SURVEY
- * entries moe_experts_gateup / moe_experts_down).  Weights keep the reference's
- * (out, in) rows: w_gate/w_up [E][I][H], w_down [E][H][I]; the shared expert's
- * gate rows then up rows in w_shared_in [2 IS][H] and w_shared_out [H][IS].  With
- * fp8 != 0 every weight is e4m3fn bytes with an f32 scale per row (s_*).  C4's
- * shared expert has a sigmoid gate row w_shared_scale [H] (bf16, NULL for C5).
- * x [rows][H] bf16 (the post-norm tokens); out f32 [rows][H] (C5: bf16 values).
- * Work: hidden bf16 [rows][k + 1][hidden_ld] and shared_scale f32 [rows].
- * H <= 4096 and I, IS <= 2048, multiples of 64. */
+ * entries moe_experts_gateup / moe_experts_down).  Grouped by expert: each weight
+ * row of a picked expert is read once per call however many sequences picked it.
+ * Weights keep the reference's (out, in) rows: w_gate/w_up [E][I][H], w_down
+ * [E][H][I]; the shared expert's gate rows then up rows in w_shared_in [2 IS][H]
+ * and w_shared_out [H][IS].  With fp8 != 0 every weight is e4m3fn bytes with an
+ * f32 scale per row (s_*).  C4's shared expert has a sigmoid gate row
+ * w_shared_scale [H] (bf16, NULL for C5).  x [rows][H] bf16 (the post-norm
+ * tokens); idx holds k distinct experts per row; out f32 [rows][H] (C5: bf16
+ * values).  Work: hidden bf16 [rows][k + 1][hidden_ld], shared_scale f32 [rows],
+ * partial f32 [rows][k + 1][H], groups int32 [TFD_MOE_GROUP_WORDS(experts, rows)].
+ * experts <= 256, H <= 4096 and I, IS <= 2048, multiples of 64.  An expert id
+ * outside [0, experts) (it is served as expert 0) or an expert repeated in a row
+ * raises TFD_ERR_TOKEN_RANGE in err. */
+#define TFD_MOE_GROUP_WORDS(experts, rows) (1 + 2 * (experts) + (experts) * (rows))
 typedef struct {
   const void* x;
   const float* weights;
@@ -82,6 +88,8 @@ typedef struct {
   const void* w_shared_scale;
   void* hidden;
   float* shared_scale;
+  float* partial;
+  int32_t* groups;
   float* out;
   int rows, k, experts, hidden_size, inter, shared_inter, hidden_ld;
   int fp8, policy;

@@ -163,7 +163,7 @@ def test_route_rejects_bad_shapes(gpu_device):
 # MoE experts
 # ---------------------------------------------------------------------------
 def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w_sscale=None,
-              fp8=False, policy):
+              fp8=False, policy, expect_err=0):
     dev = "cuda:0"
     rows, hs = x.shape
     k = idx.shape[1]
@@ -178,6 +178,9 @@ def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w
         return ptr(t)
 
     hidden = torch.full((rows, k + 1, ld), float("nan"), device=dev, dtype=BF)
+    partial = torch.full((rows, k + 1, hs), float("nan"), device=dev)
+    groups = torch.full((_lib.moe_group_words(experts, rows),), -7, dtype=torch.int32,
+                        device=dev)
     out = torch.full((rows, hs), float("nan"), device=dev)
     sscale = torch.zeros(rows, device=dev)
     err = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -189,12 +192,23 @@ def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w
         a.s_gate, a.s_up, a.s_down, a.s_shared_in, a.s_shared_out = [d(v) for v in s]
     a.w_shared_scale = None if w_sscale is None else d(w_sscale)
     a.hidden, a.shared_scale, a.out = ptr(hidden), ptr(sscale), ptr(out)
+    a.partial, a.groups = ptr(partial), ptr(groups)
     a.rows, a.k, a.experts, a.hidden_size = rows, k, experts, hs
     a.inter, a.shared_inter, a.hidden_ld = inter, sh, ld
     a.fp8, a.policy, a.err = int(fp8), policy, ptr(err)
     lib().tfd_moe_experts(ctypes.addressof(a), _stream())
     torch.cuda.synchronize()
-    assert err.item() == 0
+    if expect_err:
+        assert err.item() == expect_err
+    else:
+        assert err.item() == 0
+        # the groups: every (sequence, slot) once, under the expert it picked
+        g = groups.cpu()
+        picked = g[1:1 + g[0]].tolist()
+        assert picked == sorted(set(idx.reshape(-1).tolist()))
+        for e in picked:
+            got = sorted(g[1 + 2 * experts + e * rows:][:g[1 + experts + e]].tolist())
+            assert got == [i for i, v in enumerate(idx.reshape(-1).tolist()) if v == e]
     return out.cpu()
 
 
@@ -204,14 +218,18 @@ def _routing(rows, experts, k, gen):
     return w / w.sum(-1, keepdim=True), idx
 
 
-@pytest.mark.parametrize("rows", [1, 4, 16])
-def test_moe_experts_c4_bf16(gpu_device, rows):
-    """Qwen3.5 widths: H 2048, I 512, shared 512, top 8 (16 experts resident)."""
-    g = torch.Generator().manual_seed(rows)
+@pytest.mark.parametrize("rows,same", [(1, False), (4, False), (16, False), (16, True),
+                                       (32, False)])
+def test_moe_experts_c4_bf16(gpu_device, rows, same):
+    """Qwen3.5 widths: H 2048, I 512, shared 512, top 8 (16 experts resident, so
+    sequences share experts; `same`: every sequence picks the same 8)."""
+    g = torch.Generator().manual_seed(rows + 100 * same)
     hs, inter, sh, E, k = 2048, 512, 512, 16, 8
     rnd = lambda *s, std=0.03: H.bf(torch.randn(*s, generator=g) * std)
     x = rnd(rows, hs, std=1.0)
     weights, idx = _routing(rows, E, k, g)
+    if same:
+        idx = idx[:1].repeat(rows, 1)
     w_gate, w_up, w_down = rnd(E, inter, hs), rnd(E, inter, hs), rnd(E, hs, inter)
     ws_gate, ws_up, ws_down, ws_scale = rnd(sh, hs), rnd(sh, hs), rnd(hs, sh), rnd(1, hs)
     got = _moe_call(x, weights, idx, w_gate=w_gate.to(BF), w_up=w_up.to(BF),
@@ -219,6 +237,17 @@ def test_moe_experts_c4_bf16(gpu_device, rows):
                     w_sout=ws_down.to(BF), w_sscale=ws_scale.to(BF), policy=_lib.POLICY_F32)
     want = H.moe_c4(x, weights, idx, w_gate, w_up, w_down, ws_gate, ws_up, ws_down, ws_scale)
     assert_close_bf16(got, want, max_rel=1e-2, min_cos=0.99999, name="moe c4")
+
+
+def test_moe_experts_flags_a_bad_expert_id(gpu_device):
+    g = torch.Generator().manual_seed(3)
+    rows, hs, inter, sh, E, k = 2, 256, 64, 64, 8, 2
+    rnd = lambda *s: H.bf(torch.randn(*s, generator=g) * 0.1).to(BF)
+    weights, idx = _routing(rows, E, k, g)
+    idx[1, 0] = E + 3
+    _moe_call(H.bf(torch.randn(rows, hs, generator=g)), weights, idx, w_gate=rnd(E, inter, hs),
+              w_up=rnd(E, inter, hs), w_down=rnd(E, hs, inter), w_sin=rnd(2 * sh, hs),
+              w_sout=rnd(hs, sh), policy=_lib.POLICY_BF16, expect_err=_lib.ERR_TOKEN_RANGE)
 
 
 @pytest.mark.parametrize("rows", [1, 8])

@@ -23,6 +23,12 @@ SKINNY_COUNTERS = 16384     # tile counters at the start of a skinny-GEMM work b
 ARGMAX_WORK = 128           # int32 per row of tfd_argmax_rows' two-stage work buffer
 ATTN_SPLIT = 64
 ROUTE_SOFTMAX_TOPK, ROUTE_TOPK_SOFTMAX = 0, 1
+
+
+def moe_group_words(experts: int, rows: int) -> int:
+    """int32 words of tfd_moe_experts' group work buffer (TFD_MOE_GROUP_WORDS)."""
+    return 1 + 2 * experts + experts * rows
+
 POLICY_F32, POLICY_BF16 = 0, 1
 
 P = c_void_p
@@ -82,7 +88,7 @@ class TfdMoeArgs(ctypes.Structure):
         *[(n, c_void_p) for n in ("x", "weights", "idx", "w_gate", "w_up", "w_down", "s_gate",
                                    "s_up", "s_down", "w_shared_in", "w_shared_out",
                                    "s_shared_in", "s_shared_out", "w_shared_scale", "hidden",
-                                   "shared_scale", "out")],
+                                   "shared_scale", "partial", "groups", "out")],
         *[(n, c_int) for n in ("rows", "k", "experts", "hidden_size", "inter", "shared_inter",
                                 "hidden_ld", "fp8", "policy")],
         ("err", c_void_p),

@@ -76,6 +76,26 @@ __device__ __forceinline__ int64_t cache_row(const GqaArgs& a, int b, int j, int
   return page_row(page, j, a.hkv, h, kD);
 }
 
+// The split's page ids, staged in LDS once so that no cache load waits on a
+// page-table load; a bad entry raises kErrPageRange and reads page 0 instead.
+constexpr int kMaxSplitPages = kMaxSplitLen / kPage;
+__device__ __forceinline__ void stage_pages(const GqaArgs& a, int b, int j0, int n,
+                                            int (&pg_s)[kMaxSplitPages]) {
+  const int npg = (n + kPage - 1) / kPage;
+  if ((int)threadIdx.x < npg) {
+    int page = a.table[(int64_t)b * a.max_pages + j0 / kPage + threadIdx.x];
+    if (page < 0 || page >= a.num_pages) {
+      raise_error(a.err, kErrPageRange);
+      page = 0;
+    }
+    pg_s[threadIdx.x] = page;
+  }
+}
+
+// Positions are walked kU passes at a time: every load of the batch is issued
+// before the first is used (positions past the split re-read its last row).
+constexpr int kU = 4;
+
 // ---------------------------------------------------------------------------
 // scores
 // ---------------------------------------------------------------------------
@@ -87,6 +107,7 @@ __global__ __launch_bounds__(kBlock) void k_gqa_scores(GqaArgs a) {
   const int lane = tid & (kWave - 1), wave = tid / kWave;
   __shared__ float qk_s[kG + 1][kD];    // the query heads, then this token's key
   __shared__ float sc[kG][kMaxSplitLen];
+  __shared__ int pg_s[kMaxSplitPages];
   const int P = a.pos[b];
   if (!pos_ok(a, P, kF32)) {
     if (split == 0 && kvh == 0 && tid == 0) raise_error(a.err, kErrPosRange);
@@ -122,6 +143,7 @@ __global__ __launch_bounds__(kBlock) void k_gqa_scores(GqaArgs a) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) qk_s[r][lane + kWave * i] = x[i];
   }
+  stage_pages(a, b, j0, n, pg_s);
   __syncthreads();
   if (kF32) {
     // rotate-half RoPE on the leading rot dims: x*cos + rotate_half(x)*sin
@@ -170,37 +192,41 @@ __global__ __launch_bounds__(kBlock) void k_gqa_scores(GqaArgs a) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) qr[g][e] = qk_s[g][li * 8 + e];
   float* srow = a.scores + ((int64_t)b * a.hq + kvh * kG) * a.sstride;
-  for (int jj = pg; jj < n; jj += kPpi) {
-    const int j = j0 + jj;
-    float kv[8];
-    if (j == P) {
+  for (int jb = 0; jb < n; jb += kPpi * kU) {
+    u32x4 kw[kU];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) kv[e] = qk_s[kG][li * 8 + e];
-    } else {
-      const int64_t row = cache_row<kD>(a, b, j, kvh);
-      if (row < 0) raise_error(a.err, kErrPageRange);
-      unpack8(load16(a.kpool + (row < 0 ? 0 : row) + li * 8), kv);
+    for (int u = 0; u < kU; ++u) {
+      const int jj = min(jb + u * kPpi + pg, n - 1);
+      kw[u] = load16(a.kpool + page_row(pg_s[jj / kPage], j0 + jj, a.hkv, kvh, kD) + li * 8);
     }
-    float acc[kG];
 #pragma unroll
-    for (int g = 0; g < kG; ++g) {
-      acc[g] = 0.f;
+    for (int u = 0; u < kU; ++u) {
+      const int jj = jb + u * kPpi + pg;
+      float kv[8];
+      if (j0 + jj == P) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float prod = qr[g][e] * kv[e];
-        acc[g] += kF32 ? prod : rbf(prod);
+        for (int e = 0; e < 8; ++e) kv[e] = qk_s[kG][li * 8 + e];
+      } else {
+        unpack8(kw[u], kv);
       }
-    }
-#pragma unroll
-    for (int m = kLpp / 2; m >= 1; m >>= 1)
-#pragma unroll
-      for (int g = 0; g < kG; ++g) acc[g] += __shfl_xor(acc[g], m, kWave);
-    if (li == 0) {
+      float acc[kG];
 #pragma unroll
       for (int g = 0; g < kG; ++g) {
-        const float s = kF32 ? acc[g] : rbf(acc[g]) * a.scale;
-        sc[g][jj] = s;
-        srow[(int64_t)g * a.sstride + j] = s;
+        acc[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float prod = qr[g][e] * kv[e];
+          acc[g] += kF32 ? prod : rbf(prod);
+        }
+        acc[g] = group_sum<kLpp>(acc[g]);
+      }
+      if (li == 0 && jj < n) {
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          const float sv = kF32 ? acc[g] : rbf(acc[g]) * a.scale;
+          sc[g][jj] = sv;
+          srow[(int64_t)g * a.sstride + j0 + jj] = sv;
+        }
       }
     }
   }
@@ -232,6 +258,7 @@ __global__ __launch_bounds__(kBlock) void k_gqa_pv(GqaArgs a) {
   __shared__ float Ms[kG], Ss[kG];
   __shared__ float p_s[kG][kMaxSplitLen];
   __shared__ float red[kWavesPerBlock][kG][kD];
+  __shared__ int pg_s[kMaxSplitPages];
   __shared__ int is_last;
   const int P = a.pos[b];
   if (!pos_ok(a, P, kF32)) return;      // raised by the scores launch
@@ -248,6 +275,7 @@ __global__ __launch_bounds__(kBlock) void k_gqa_pv(GqaArgs a) {
     Ms[tid] = M;
     Ss[tid] = S;
   }
+  stage_pages(a, b, j0, n, pg_s);
   __syncthreads();
   const float* srow = a.scores + ((int64_t)b * a.hq + hq0) * a.sstride;
   for (int i = tid; i < kG * n; i += kBlock) {
@@ -262,18 +290,28 @@ __global__ __launch_bounds__(kBlock) void k_gqa_pv(GqaArgs a) {
   for (int g = 0; g < kG; ++g)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
-  for (int jj = pg; jj < n; jj += kPpi) {
-    const int64_t row = cache_row<kD>(a, b, j0 + jj, kvh);
-    if (row < 0) raise_error(a.err, kErrPageRange);
-    float v[8];
-    unpack8(load16(a.vpool + (row < 0 ? 0 : row) + li * 8), v);
+  for (int jb = 0; jb < n; jb += kPpi * kU) {
+    u32x4 vw[kU];
 #pragma unroll
-    for (int g = 0; g < kG; ++g) {
-      const float p = p_s[g][jj];
+    for (int u = 0; u < kU; ++u) {
+      const int jj = min(jb + u * kPpi + pg, n - 1);
+      vw[u] = load16(a.vpool + page_row(pg_s[jj / kPage], j0 + jj, a.hkv, kvh, kD) + li * 8);
+    }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float prod = p * v[e];
-        acc[g][e] += kF32 ? prod : rbf(prod);
+    for (int u = 0; u < kU; ++u) {
+      const int jj = jb + u * kPpi + pg;
+      if (jj < n) {
+        float v[8];
+        unpack8(vw[u], v);
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          const float p = p_s[g][jj];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float prod = p * v[e];
+            acc[g][e] += kF32 ? prod : rbf(prod);
+          }
+        }
       }
     }
   }
@@ -306,17 +344,41 @@ __global__ __launch_bounds__(kBlock) void k_gqa_pv(GqaArgs a) {
   }
   __syncthreads();
   if (!is_last) return;
-  for (int o = tid; o < kG * kD; o += kBlock) {
-    const int g = o / kD, d = o % kD;
-    const float* pp = a.part + ((int64_t)b * a.hq + hq0 + g) * a.nsplit * kD + d;
-    float s = 0.f;
-    for (int sp = 0; sp < nlive; ++sp) s += coh_ldf(pp + (int64_t)sp * kD);
-    if (kF32) {
-      const float gate = ((const float*)a.qkv)[(int64_t)b * a.ldq +
-                                               (int64_t)(hq0 + g) * 2 * kD + kD + d];
-      s = s * (1.f / (1.f + expf(-gate)));
+  // four outputs per thread and pass; the splits' partials arrive in batches of
+  // kBatch independent 16-byte device-coherent loads, added in split order
+  constexpr int kBatch = 8;
+  for (int o4 = tid; o4 < kG * kD / 4; o4 += kBlock) {
+    const int g = (o4 * 4) / kD, d = (o4 * 4) % kD;
+    const uint32_t base =
+        (uint32_t)((((int64_t)b * a.hq + hq0 + g) * a.nsplit * kD + d) * sizeof(float));
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < nlive; s0 += kBatch) {
+      u32x4 v[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int sp = s0 + i < nlive ? s0 + i : nlive - 1;
+        v[i] = coh_ld16(a.part, base + (uint32_t)(sp * kD * sizeof(float)));
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        if (s0 + i < nlive) {
+          s[0] += __uint_as_float(v[i].x);
+          s[1] += __uint_as_float(v[i].y);
+          s[2] += __uint_as_float(v[i].z);
+          s[3] += __uint_as_float(v[i].w);
+        }
+      }
     }
-    a.out[xp_off_g(b, (hq0 + g) * kD + d)] = f2bf(s);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float val = s[e];
+      if (kF32) {
+        const float gate = ((const float*)a.qkv)[(int64_t)b * a.ldq +
+                                                 (int64_t)(hq0 + g) * 2 * kD + kD + d + e];
+        val = val * (1.f / (1.f + expf(-gate)));
+      }
+      a.out[xp_off_g(b, (hq0 + g) * kD + d + e)] = f2bf(val);
+    }
   }
   if (tid == 0) atomicExch(&a.counters[b * a.hkv + kvh], 0);
 }

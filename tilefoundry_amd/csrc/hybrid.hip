@@ -112,53 +112,52 @@ __global__ __launch_bounds__(kWave) void k_route(const float* __restrict__ logit
 }
 
 // ---------------------------------------------------------------------------
-// Row dot products for the experts.  A wave owns a pair of output rows; its
-// lanes split the length-K reduction into 16-byte chunks of the bf16 input
-// (held in registers) and of the weight row (bf16, or fp8 with one scale per
-// row), exact products summed in f32.
+// Experts, grouped by expert: every weight row of an expert some sequence
+// picked is read once per launch, whatever the number of sequences that picked
+// it.  A lane holds 16-byte chunks of the bf16 input (8 values) and the
+// matching 8 weights of a row (bf16, or fp8 with one scale per row); exact
+// products are summed in f32 and the wave adds its lanes.
+//   group   one block: expert -> its (sequence, slot) entries, and the list of
+//           the experts picked at all (ascending)
+//   gate/up (picked expert or the shared one) x (row tile): a wave keeps kR
+//           gate rows and kR up rows in registers and runs every entry of the
+//           expert through them -> the SwiGLU hidden vector of each entry
+//   down    the same over the down projections -> one bf16-rounded output
+//           vector per (sequence, slot)
+//   mix     per sequence, the slots in slot order, then the shared expert
 // ---------------------------------------------------------------------------
 template <bool kFp8>
-struct RowW;
+struct WChunk;
 template <>
-struct RowW<false> {
-  // 8 weights of row `row` at chunk c (bf16)
-  static __device__ __forceinline__ float dot_chunk(const void* w, int64_t row, int K, int c,
-                                                    const u32x4& x) {
-    const u32x4 wv = load16_stream((const bf16*)w + row * K + (int64_t)c * 8);
-    return dot8(wv, x, 0.f);
+struct WChunk<false> {
+  using T = u32x4;
+  static __device__ __forceinline__ T load(const void* w, int64_t row, int K, int c) {
+    return load16_stream((const bf16*)w + row * K + (int64_t)c * 8);
+  }
+  static __device__ __forceinline__ float dot(const T& w, const u32x4& x, float acc) {
+    return dot8(w, x, acc);
   }
 };
 template <>
-struct RowW<true> {
-  static __device__ __forceinline__ float dot_chunk(const void* w, int64_t row, int K, int c,
-                                                    const u32x4& x) {
-    const u32x2 q = __builtin_nontemporal_load(
+struct WChunk<true> {
+  using T = u32x2;
+  static __device__ __forceinline__ T load(const void* w, int64_t row, int K, int c) {
+    return __builtin_nontemporal_load(
         reinterpret_cast<const u32x2*>((const uint8_t*)w + row * K + (int64_t)c * 8));
+  }
+  // e4m3fn values are exact in bf16: decode, repack, bf16 dot products
+  static __device__ __forceinline__ float dot(const T& q, const u32x4& x, float acc) {
     const f32x2_t v0 = __builtin_amdgcn_cvt_pk_f32_fp8(q.x, false);
     const f32x2_t v1 = __builtin_amdgcn_cvt_pk_f32_fp8(q.x, true);
     const f32x2_t v2 = __builtin_amdgcn_cvt_pk_f32_fp8(q.y, false);
     const f32x2_t v3 = __builtin_amdgcn_cvt_pk_f32_fp8(q.y, true);
     const u32x4 wv = {pack2(v0.x, v0.y), pack2(v1.x, v1.y), pack2(v2.x, v2.y),
                       pack2(v3.x, v3.y)};
-    return dot8(wv, x, 0.f);
+    return dot8(wv, x, acc);
   }
 };
 
-// sum over the row of w[row] . x (x as kC 16-byte chunks per lane, chunk
-// c = lane + 64 i), every lane gets the total
-template <bool kFp8, int kC>
-__device__ __forceinline__ float row_dot(const void* w, int64_t row, int K, const u32x4 (&x)[kC],
-                                         int lane) {
-  float a = 0.f;
-  const int nch = K / 8;
-#pragma unroll
-  for (int i = 0; i < kC; ++i) {
-    const int c = lane + kWave * i;
-    if (c < nch) a += RowW<kFp8>::dot_chunk(w, row, K, c, x[i]);
-  }
-  return wave_sum(a);
-}
-
+// x's chunks c = lane + 64 i (zero past the end)
 template <int kC>
 __device__ __forceinline__ void load_vec(const bf16* x, int K, int lane, u32x4 (&xr)[kC]) {
   const int nch = K / 8;
@@ -167,6 +166,20 @@ __device__ __forceinline__ void load_vec(const bf16* x, int K, int lane, u32x4 (
     const int c = lane + kWave * i;
     xr[i] = c < nch ? load16(x + (int64_t)c * 8) : u32x4{0u, 0u, 0u, 0u};
   }
+}
+
+// a row of K weights against x, summed over the wave (every lane gets it)
+template <bool kFp8, int kC>
+__device__ __forceinline__ float row_dot(const void* w, int64_t row, int K, const u32x4 (&x)[kC],
+                                         int lane) {
+  float acc = 0.f;
+  const int nch = K / 8;
+#pragma unroll
+  for (int i = 0; i < kC; ++i) {
+    const int c = lane + kWave * i;
+    if (c < nch) acc = WChunk<kFp8>::dot(WChunk<kFp8>::load(w, row, K, c), x[i], acc);
+  }
+  return wave_sum(acc);
 }
 
 struct MoeArgs {
@@ -178,94 +191,212 @@ struct MoeArgs {
   const void *w_sin, *w_sout;                // shared: [2 IS][H] (gate rows, then up), [H][IS]
   const float *s_sin, *s_sout;               // fp8 row scales [2 IS], [H]
   const bf16* w_sscale;                      // C4 shared-expert gate row [H] (or null)
-  bf16* hidden;                              // [B][k + 1][IM] work
+  bf16* hidden;                              // [B][k + 1][IM] work: SwiGLU vectors
   float* sscale;                             // [B] work: the shared expert's sigmoid gate
+  float* partial;                            // [B][k + 1][H] work: down outputs per slot
+  int* groups;                               // work: n | picked[E] | count[E] | entries[E][B]
   float* out;                                // [B][H]
-  int H, I, IS, IM, k, E;
+  int B, H, I, IS, IM, k, E;
   int* err;
 };
 
-// gate/up of every (sequence, slot): slot k is the shared expert
-template <bool kFp8, bool kF32, int kC>
-__global__ __launch_bounds__(kBlock) void k_moe_gateup(MoeArgs a) {
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int slot = blockIdx.y, b = blockIdx.z;
-  const bool shared = slot == a.k;
-  const int rows = shared ? a.IS : a.I;
-  const int r0 = (blockIdx.x * kWavesPerBlock + wave) * 2;
-  int e = 0;
-  if (!shared) {
-    e = a.idx[(int64_t)b * a.k + slot];
+__device__ __forceinline__ int* grp_picked(const MoeArgs& a) { return a.groups + 1; }
+__device__ __forceinline__ int* grp_count(const MoeArgs& a) { return a.groups + 1 + a.E; }
+__device__ __forceinline__ int* grp_entries(const MoeArgs& a) { return a.groups + 1 + 2 * a.E; }
+
+__global__ __launch_bounds__(kBlock) void k_moe_group(MoeArgs a) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  __shared__ int c_s[kBlock];
+  __shared__ int wave_n[kWavesPerBlock];
+  c_s[tid] = 0;
+  __syncthreads();
+  int* entries = grp_entries(a);
+  for (int i = tid; i < a.B * a.k; i += kBlock) {
+    int e = a.idx[i];
     if (e < 0 || e >= a.E) {
-      if (threadIdx.x == 0) raise_error(a.err, kErrTokenRange);
+      raise_error(a.err, kErrTokenRange);
       e = 0;
     }
+    const int p = atomicAdd(&c_s[e], 1);
+    if (p < a.B)
+      entries[(int64_t)e * a.B + p] = i;
+    else
+      raise_error(a.err, kErrTokenRange);   // an expert picked twice by one sequence
   }
-  u32x4 xr[kC];
-  load_vec<kC>(a.x + (int64_t)b * a.H, a.H, lane, xr);
-  if (shared && a.w_sscale && blockIdx.x == 0 && wave == 0) {
-    const float d = rbf(row_dot<false, kC>(a.w_sscale, 0, a.H, xr, lane));
-    if (lane == 0) a.sscale[b] = sigmoid_f(d);
-  }
-  if (r0 >= rows) return;
-  const void* wg = shared ? a.w_sin : a.w_gate;
-  const void* wu = shared ? a.w_sin : a.w_up;
-  const int64_t gbase = shared ? 0 : (int64_t)e * a.I;
-  const int64_t ubase = shared ? a.IS : (int64_t)e * a.I;
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int r = r0 + u;
-    if (r >= rows) break;
-    float g = row_dot<kFp8, kC>(wg, gbase + r, a.H, xr, lane);
-    float v = row_dot<kFp8, kC>(wu, ubase + r, a.H, xr, lane);
-    if (kFp8) {
-      g *= shared ? a.s_sin[r] : a.s_gate[gbase + r];
-      v *= shared ? a.s_sin[a.IS + r] : a.s_up[gbase + r];
-    }
-    g = rbf(g);
-    v = rbf(v);
-    const float h = kF32 ? silu_f(g) * v : rbf(silu_f(g)) * v;
-    if (lane == 0) a.hidden[((int64_t)b * (a.k + 1) + slot) * a.IM + r] = f2bf(h);
+  __syncthreads();
+  const int e = tid;
+  const bool on = e < a.E && c_s[e] > 0;
+  const uint64_t m = __ballot(on);
+  if (lane == 0) wave_n[wave] = __popcll(m);
+  __syncthreads();
+  int off = 0;
+  for (int w = 0; w < wave; ++w) off += wave_n[w];
+  if (on) grp_picked(a)[off + __popcll(m & ((1ull << lane) - 1ull))] = e;
+  if (e < a.E) grp_count(a)[e] = c_s[e] < a.B ? c_s[e] : a.B;
+  if (tid == 0) {
+    int n = 0;
+    for (int w = 0; w < kWavesPerBlock; ++w) n += wave_n[w];
+    a.groups[0] = n;
   }
 }
 
-// down projections of every slot and their mix, two output rows per wave
-template <bool kFp8, bool kF32, int kCI, int kCS>
-__global__ __launch_bounds__(kBlock) void k_moe_down(MoeArgs a) {
+// (expert, entries) of blockIdx.y: the picked experts, then the shared one
+struct Group {
+  bool shared;
+  int e, count;
+  const int* entries;
+};
+__device__ __forceinline__ bool moe_group(const MoeArgs& a, Group& g) {
+  g.shared = blockIdx.y == gridDim.y - 1;
+  if (g.shared) {
+    g.e = 0;
+    g.count = a.B;
+    g.entries = nullptr;
+    return true;
+  }
+  if ((int)blockIdx.y >= a.groups[0]) return false;
+  g.e = grp_picked(a)[blockIdx.y];
+  g.count = grp_count(a)[g.e];
+  g.entries = grp_entries(a) + (int64_t)g.e * a.B;
+  return true;
+}
+// sequence and slot of entry t of the group (slot k: the shared expert)
+__device__ __forceinline__ void moe_entry(const MoeArgs& a, const Group& g, int t, int& b,
+                                          int& slot) {
+  if (g.shared) {
+    b = t;
+    slot = a.k;
+  } else {
+    const int i = g.entries[t];
+    b = i / a.k;
+    slot = i % a.k;
+  }
+}
+
+template <bool kFp8, bool kF32, int kC, int kR>
+__global__ __launch_bounds__(kBlock) void k_moe_gateup(MoeArgs a) {
+  using WC = WChunk<kFp8>;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  const int b = blockIdx.y;
-  const int n0 = (blockIdx.x * kWavesPerBlock + wave) * 2;
-  if (n0 >= a.H) return;
-  float acc[2] = {0.f, 0.f};
-  for (int s = 0; s < a.k; ++s) {
-    int e = a.idx[(int64_t)b * a.k + s];
-    if (e < 0 || e >= a.E) e = 0;              // raised by the gate/up launch
-    const float wgt = a.weights[(int64_t)b * a.k + s];
-    u32x4 hr[kCI];
-    load_vec<kCI>(a.hidden + ((int64_t)b * (a.k + 1) + s) * a.IM, a.I, lane, hr);
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int n = n0 + u;
-      if (n >= a.H) break;
-      float d = row_dot<kFp8, kCI>(a.w_down, (int64_t)e * a.H + n, a.I, hr, lane);
-      if (kFp8) d *= a.s_down[(int64_t)e * a.H + n];
-      d = rbf(d);
-      acc[u] += kF32 ? d * wgt : rbf(d * wgt);
+  Group g;
+  if (!moe_group(a, g)) return;
+  if (g.shared && a.w_sscale && blockIdx.x == 0 && wave == 0) {
+    for (int b = 0; b < a.B; ++b) {
+      u32x4 xr[kC];
+      load_vec<kC>(a.x + (int64_t)b * a.H, a.H, lane, xr);
+      const float d = rbf(row_dot<false, kC>(a.w_sscale, 0, a.H, xr, lane));
+      if (lane == 0) a.sscale[b] = sigmoid_f(d);
     }
   }
-  u32x4 hs[kCS];
-  load_vec<kCS>(a.hidden + ((int64_t)b * (a.k + 1) + a.k) * a.IM, a.IS, lane, hs);
+  const int nrows = g.shared ? a.IS : a.I;
+  const int r0 = (blockIdx.x * kWavesPerBlock + wave) * kR;
+  if (r0 >= nrows) return;
+  const void* wg = g.shared ? a.w_sin : a.w_gate;
+  const void* wu = g.shared ? a.w_sin : a.w_up;
+  const int64_t gb = g.shared ? 0 : (int64_t)g.e * a.I;
+  const int64_t ub = g.shared ? a.IS : (int64_t)g.e * a.I;
+  const int nch = a.H / 8;
+  typename WC::T gw[kR][kC], uw[kR][kC];
+  float gs[kR], us[kR];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int n = n0 + u;
-    if (n >= a.H) break;
-    float d = row_dot<kFp8, kCS>(a.w_sout, n, a.IS, hs, lane);
-    if (kFp8) d *= a.s_sout[n];
-    d = rbf(d);
-    const float o = kF32 ? acc[u] + d * (a.w_sscale ? a.sscale[b] : 1.f)
-                         : rbf(rbf(acc[u]) + d);
-    if (lane == 0) a.out[(int64_t)b * a.H + n] = o;
+  for (int r = 0; r < kR; ++r) {
+    const int row = r0 + r < nrows ? r0 + r : nrows - 1;
+#pragma unroll
+    for (int i = 0; i < kC; ++i) {
+      const int c = lane + kWave * i < nch ? lane + kWave * i : 0;
+      gw[r][i] = WC::load(wg, gb + row, a.H, c);
+      uw[r][i] = WC::load(wu, ub + row, a.H, c);
+    }
+    if (kFp8) {
+      gs[r] = g.shared ? a.s_sin[row] : a.s_gate[gb + row];
+      us[r] = g.shared ? a.s_sin[a.IS + row] : a.s_up[gb + row];
+    }
   }
+  for (int t = 0; t < g.count; ++t) {
+    int b, slot;
+    moe_entry(a, g, t, b, slot);
+    u32x4 xr[kC];
+    load_vec<kC>(a.x + (int64_t)b * a.H, a.H, lane, xr);
+    bf16* hrow = a.hidden + ((int64_t)b * (a.k + 1) + slot) * a.IM;
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      float gv = 0.f, uv = 0.f;
+#pragma unroll
+      for (int i = 0; i < kC; ++i) {
+        if (lane + kWave * i < nch) {
+          gv = WC::dot(gw[r][i], xr[i], gv);
+          uv = WC::dot(uw[r][i], xr[i], uv);
+        }
+      }
+      gv = wave_sum(gv);
+      uv = wave_sum(uv);
+      if (kFp8) {
+        gv *= gs[r];
+        uv *= us[r];
+      }
+      gv = rbf(gv);
+      uv = rbf(uv);
+      const float h = kF32 ? silu_f(gv) * uv : rbf(silu_f(gv)) * uv;
+      if (lane == 0 && r0 + r < nrows) hrow[r0 + r] = f2bf(h);
+    }
+  }
+}
+
+template <bool kFp8, int kC, int kR>
+__global__ __launch_bounds__(kBlock) void k_moe_down(MoeArgs a) {
+  using WC = WChunk<kFp8>;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  Group g;
+  if (!moe_group(a, g)) return;
+  const int K = g.shared ? a.IS : a.I;
+  const int nch = K / 8;
+  const int n0 = (blockIdx.x * kWavesPerBlock + wave) * kR;
+  if (n0 >= a.H) return;
+  const void* w = g.shared ? a.w_sout : a.w_down;
+  const int64_t base = g.shared ? 0 : (int64_t)g.e * a.H;
+  typename WC::T dw[kR][kC];
+  float ds[kR];
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    const int row = n0 + r < a.H ? n0 + r : a.H - 1;
+#pragma unroll
+    for (int i = 0; i < kC; ++i) {
+      const int c = lane + kWave * i < nch ? lane + kWave * i : 0;
+      dw[r][i] = WC::load(w, base + row, K, c);
+    }
+    if (kFp8) ds[r] = g.shared ? a.s_sout[row] : a.s_down[base + row];
+  }
+  for (int t = 0; t < g.count; ++t) {
+    int b, slot;
+    moe_entry(a, g, t, b, slot);
+    u32x4 hr[kC];
+    load_vec<kC>(a.hidden + ((int64_t)b * (a.k + 1) + slot) * a.IM, K, lane, hr);
+    float* prow = a.partial + ((int64_t)b * (a.k + 1) + slot) * a.H;
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < kC; ++i)
+        if (lane + kWave * i < nch) d = WC::dot(dw[r][i], hr[i], d);
+      d = wave_sum(d);
+      if (kFp8) d *= ds[r];
+      if (lane == 0 && n0 + r < a.H) prow[n0 + r] = rbf(d);
+    }
+  }
+}
+
+template <bool kF32>
+__global__ __launch_bounds__(kBlock) void k_moe_mix(MoeArgs a) {
+  const int b = blockIdx.y, n = blockIdx.x * kBlock + threadIdx.x;
+  if (n >= a.H) return;
+  const float* pb = a.partial + (int64_t)b * (a.k + 1) * a.H + n;
+  float acc = 0.f;
+  for (int s = 0; s < a.k; ++s) {
+    const float d = pb[(int64_t)s * a.H], wgt = a.weights[(int64_t)b * a.k + s];
+    acc += kF32 ? d * wgt : rbf(d * wgt);
+  }
+  const float dsh = pb[(int64_t)a.k * a.H];
+  a.out[(int64_t)b * a.H + n] =
+      kF32 ? acc + dsh * (a.w_sscale ? a.sscale[b] : 1.f) : rbf(rbf(acc) + dsh);
 }
 
 // ---------------------------------------------------------------------------
@@ -441,12 +572,16 @@ __device__ __forceinline__ float conv_silu_bf16(const bf16* cin, const bf16* w, 
 template <int kPD>
 __global__ __launch_bounds__(kBlock) void k_mamba_step(MambaArgs a) {
   constexpr int kKW = 4, kNS = 128;
+  constexpr int kLpr = kNS / 4;                   // lanes per state row (4 columns each)
+  constexpr int kRpp = kBlock / kLpr;             // rows per pass
+  constexpr int kPass = kPD / kRpp;
   const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
   const int exp_ = a.nh * kPD, conv = exp_ + 2 * kNS;
   const bf16* proj = a.proj + (int64_t)b * a.ldp;
   const bf16* cin = a.conv_in + (int64_t)b * conv * (kKW - 1);
   bf16* cout = a.conv_out + (int64_t)b * conv * (kKW - 1);
   __shared__ float x_s[kPD], b_s[kNS], c_s[kNS], dtv[2];
+  __shared__ float ss_w[kWavesPerBlock];
   for (int i = tid; i < kPD + 2 * kNS; i += kBlock) {
     const int ch = i < kPD ? h * kPD + i : exp_ + (i - kPD);
     const float m = conv_silu_bf16(cin + (int64_t)ch * (kKW - 1), a.conv_w + (int64_t)ch * kKW,
@@ -464,30 +599,42 @@ __global__ __launch_bounds__(kBlock) void k_mamba_step(MambaArgs a) {
     dtv[0] = dt;
     dtv[1] = expf(dt * -expf(bf2f(a.a_log[h])));
   }
+  // this thread's four state columns in every pass: 16-byte loads, a row's 32
+  // lanes contiguous, all passes' loads issued before the first is used
+  const int q = tid % kLpr, r0 = tid / kLpr;
+  float4* st = reinterpret_cast<float4*>(a.state + ((int64_t)b * a.nh + h) * kPD * kNS) + q;
+  float4 sv[kPass];
+#pragma unroll
+  for (int i = 0; i < kPass; ++i) sv[i] = st[(int64_t)(r0 + kRpp * i) * kLpr];
   __syncthreads();
-  // thread (p, quarter): state row p, columns [32 quarter, +32)
-  const int p = tid >> 2, q4 = tid & 3;
   const float dt = dtv[0], decay = dtv[1];
-  const float xp = x_s[p];
-  float* st = a.state + (((int64_t)b * a.nh + h) * kPD + p) * kNS + q4 * 32;
-  float rd = 0.f;
-#pragma unroll 8
-  for (int j = 0; j < 32; ++j) {
-    const int n = q4 * 32 + j;
-    const float dbx = rbf(rbf(dt * b_s[n]) * xp);
-    const float u = st[j] * decay + dbx;
-    st[j] = u;
-    rd += rbf(u) * c_s[n];
+  float dtb[4], cq[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    dtb[e] = rbf(dt * b_s[4 * q + e]);
+    cq[e] = c_s[4 * q + e];
   }
-  rd += dpp_f<kDppXor1>(rd);
-  rd += dpp_f<kDppXor2>(rd);
-  __shared__ float ss_w[kWavesPerBlock];
+  const float dsk = bf2f(a.d_skip[h]);
   float g2 = 0.f;
-  if (q4 == 0) {
-    const float y = rbf(rbf(rd) + rbf(xp * bf2f(a.d_skip[h])));
-    const float gt = y * silu_f(bf2f(proj[h * kPD + p]));
-    a.gated[(int64_t)b * exp_ + h * kPD + p] = gt;
-    g2 = gt * gt;
+#pragma unroll
+  for (int i = 0; i < kPass; ++i) {
+    const int p = r0 + kRpp * i;
+    const float xp = x_s[p];
+    float u[4] = {sv[i].x, sv[i].y, sv[i].z, sv[i].w};
+    float rd = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      u[e] = u[e] * decay + rbf(dtb[e] * xp);
+      rd += rbf(u[e]) * cq[e];
+    }
+    st[(int64_t)p * kLpr] = float4{u[0], u[1], u[2], u[3]};
+    rd = group_sum<kLpr>(rd);
+    if (q == 0) {
+      const float y = rbf(rbf(rd) + rbf(xp * dsk));
+      const float gt = y * silu_f(bf2f(proj[h * kPD + p]));
+      a.gated[(int64_t)b * exp_ + h * kPD + p] = gt;
+      g2 += gt * gt;
+    }
   }
   g2 = wave_sum(g2);
   if ((tid & (kWave - 1)) == 0) ss_w[tid / kWave] = g2;
@@ -499,31 +646,48 @@ __global__ __launch_bounds__(kBlock) void k_mamba_step(MambaArgs a) {
   }
 }
 
+// the gated RMS norm over the whole inner width; grid (chunks of 1024, rows)
 __global__ __launch_bounds__(kBlock) void k_mamba_norm(MambaArgs a, int exp_) {
-  const int b = blockIdx.x;
+  const int b = blockIdx.y, lane = threadIdx.x & (kWave - 1);
   __shared__ float tot;
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < kWave) {
     float t = 0.f;
-    for (int h = 0; h < a.nh; ++h) t += a.ssq[(int64_t)b * a.nh + h];
-    tot = rsqrtf(t / (float)exp_ + a.eps);
+    for (int h = lane; h < a.nh; h += kWave) t += a.ssq[(int64_t)b * a.nh + h];
+    t = wave_sum(t);
+    if (lane == 0) tot = rsqrtf(t / (float)exp_ + a.eps);
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < exp_; i += kBlock)
+  const int i0 = blockIdx.x * kBlock * 4;
+  for (int i = i0 + threadIdx.x; i < i0 + kBlock * 4 && i < exp_; i += kBlock)
     a.out[xp_off_h(b, i)] = f2bf(a.gated[(int64_t)b * exp_ + i] * tot * bf2f(a.gamma[i]));
 }
 
 }  // namespace
 
 template <bool kFp8, bool kF32>
-int launch_moe(const MoeArgs& a, dim3 g1, dim3 g2, hipStream_t s) {
+int launch_moe(const MoeArgs& a, hipStream_t s) {
+  constexpr int kRgu = 4, kRdn = 8;
+  // picked experts at most min(E, B k), plus the shared one
+  const int ny = (a.E < a.B * a.k ? a.E : a.B * a.k) + 1;
+  const int im = a.I > a.IS ? a.I : a.IS;
+  const dim3 g1((im + kWavesPerBlock * kRgu - 1) / (kWavesPerBlock * kRgu), ny);
+  const dim3 g2((a.H + kWavesPerBlock * kRdn - 1) / (kWavesPerBlock * kRdn), ny);
+  const dim3 g3((a.H + kBlock - 1) / kBlock, a.B);
+  hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(kBlock), 0, s, a);
   switch (cmax_for(a.H)) {
-    case 1: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 1>), g1, dim3(kBlock), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 2>), g1, dim3(kBlock), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 4>), g1, dim3(kBlock), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 8>), g1, dim3(kBlock), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 1, kRgu>), g1, dim3(kBlock), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 2, kRgu>), g1, dim3(kBlock), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 4, kRgu>), g1, dim3(kBlock), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 8, kRgu>), g1, dim3(kBlock), 0, s, a); break;
     default: return fail(kUnsupported, "moe_experts: hidden size %d", a.H);
   }
-  hipLaunchKernelGGL((k_moe_down<kFp8, kF32, 4, 4>), g2, dim3(kBlock), 0, s, a);
+  switch (cmax_for(im)) {
+    case 1: hipLaunchKernelGGL((k_moe_down<kFp8, 1, kRdn>), g2, dim3(kBlock), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_moe_down<kFp8, 2, kRdn>), g2, dim3(kBlock), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_moe_down<kFp8, 4, kRdn>), g2, dim3(kBlock), 0, s, a); break;
+    default: return fail(kUnsupported, "moe_experts: expert width %d", im);
+  }
+  hipLaunchKernelGGL((k_moe_mix<kF32>), g3, dim3(kBlock), 0, s, a);
   return launched("moe_experts");
 }
 
@@ -550,16 +714,17 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
   if (!args) return fail(kBadArg, "moe_experts: null args");
   const TfdMoeArgs& t = *args;
   if (!t.x || !t.weights || !t.idx || !t.w_gate || !t.w_up || !t.w_down || !t.w_shared_in ||
-      !t.w_shared_out || !t.hidden || !t.out ||
+      !t.w_shared_out || !t.hidden || !t.partial || !t.groups || !t.out ||
       (t.fp8 && (!t.s_gate || !t.s_up || !t.s_down || !t.s_shared_in || !t.s_shared_out)) ||
       (t.w_shared_scale && (!t.shared_scale || t.fp8)))
     return fail(kBadArg, "moe_experts: null pointer or a shared-expert gate with fp8 weights");
   if (t.rows <= 0 || t.rows > 65535 || t.k <= 0 || t.k > 64 || t.experts <= 0 ||
-      t.hidden_size % 64 || t.hidden_size > 4096 || t.inter % 64 || t.inter > 2048 ||
-      t.shared_inter % 64 || t.shared_inter > 2048 || t.hidden_ld < t.inter ||
-      t.hidden_ld < t.shared_inter || t.hidden_ld % 8)
-    return fail(kBadShape, "moe_experts: rows=%d k=%d H=%d (<= 4096) I=%d IS=%d (<= 2048) "
-                "ld=%d", t.rows, t.k, t.hidden_size, t.inter, t.shared_inter, t.hidden_ld);
+      t.experts > kBlock || t.hidden_size % 64 || t.hidden_size > 4096 || t.inter % 64 ||
+      t.inter > 2048 || t.shared_inter % 64 || t.shared_inter > 2048 ||
+      t.hidden_ld < t.inter || t.hidden_ld < t.shared_inter || t.hidden_ld % 8)
+    return fail(kBadShape, "moe_experts: rows=%d k=%d experts=%d (<= 256) H=%d (<= 4096) "
+                "I=%d IS=%d (<= 2048) ld=%d", t.rows, t.k, t.experts, t.hidden_size, t.inter,
+                t.shared_inter, t.hidden_ld);
   MoeArgs a;
   a.x = (const bf16*)t.x;
   a.weights = t.weights;
@@ -577,7 +742,10 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
   a.w_sscale = (const bf16*)t.w_shared_scale;
   a.hidden = (bf16*)t.hidden;
   a.sscale = t.shared_scale;
+  a.partial = t.partial;
+  a.groups = (int*)t.groups;
   a.out = t.out;
+  a.B = t.rows;
   a.H = t.hidden_size;
   a.I = t.inter;
   a.IS = t.shared_inter;
@@ -586,12 +754,9 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
   a.E = t.experts;
   a.err = t.err;
   auto s = (hipStream_t)stream;
-  const int im = t.inter > t.shared_inter ? t.inter : t.shared_inter;
-  const dim3 g1((im + 2 * kWavesPerBlock - 1) / (2 * kWavesPerBlock), t.k + 1, t.rows);
-  const dim3 g2((t.hidden_size + 2 * kWavesPerBlock - 1) / (2 * kWavesPerBlock), t.rows);
-  if (t.fp8 && t.policy == TFD_POLICY_BF16) return launch_moe<true, false>(a, g1, g2, s);
-  if (!t.fp8 && t.policy == TFD_POLICY_F32) return launch_moe<false, true>(a, g1, g2, s);
-  if (!t.fp8 && t.policy == TFD_POLICY_BF16) return launch_moe<false, false>(a, g1, g2, s);
+  if (t.fp8 && t.policy == TFD_POLICY_BF16) return launch_moe<true, false>(a, s);
+  if (!t.fp8 && t.policy == TFD_POLICY_F32) return launch_moe<false, true>(a, s);
+  if (!t.fp8 && t.policy == TFD_POLICY_BF16) return launch_moe<false, false>(a, s);
   return fail(kUnsupported, "moe_experts: fp8 weights with the f32 policy are not built");
 }
 
@@ -660,7 +825,8 @@ int tfd_mamba_step(const TfdMambaArgs* args, void* stream) {
   a.eps = t.eps;
   auto s = (hipStream_t)stream;
   hipLaunchKernelGGL(k_mamba_step<64>, dim3(t.heads, t.rows), dim3(kBlock), 0, s, a);
-  hipLaunchKernelGGL(k_mamba_norm, dim3(t.rows), dim3(kBlock), 0, s, a, t.heads * 64);
+  hipLaunchKernelGGL(k_mamba_norm, dim3((t.heads * 64 + 4 * kBlock - 1) / (4 * kBlock), t.rows),
+                     dim3(kBlock), 0, s, a, t.heads * 64);
   return launched("mamba_step");
 }
 
