@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TFD_ABI_VERSION 9
+#define TFD_ABI_VERSION 10
 
 /* gemv prologues / epilogues */
 #define TFD_PRO_PLAIN 0  /* x used as given */
@@ -38,6 +38,8 @@ extern "C" {
 #define TFD_EPI_RESID 1  /* out[n] = bf16(resid[n] + bf16(W[n].x)) */
 #define TFD_EPI_SWIGLU 2 /* rows are (gate_i, up_i) pairs: out[i] = bf16(bf16(silu(g)) * u) */
 #define TFD_EPI_LOGITS 3 /* skinny GEMM only: out (f32) = bf16-valued W[n].x (the HIR's bf16 logits) */
+#define TFD_EPI_RESID_F32 4 /* skinny GEMM only: out (f32) = resid (f32) + bf16-valued W[n].x; out may
+                               be resid (an f32 residual stream, torch_ref.py:533-543) */
 
 /* device error bits */
 #define TFD_ERR_TOKEN_RANGE 1

@@ -93,6 +93,7 @@ typedef struct {
   float* out;
   int rows, k, experts, hidden_size, inter, shared_inter, hidden_ld;
   int fp8, policy;
+  int accumulate; /* TFD_POLICY_F32 only: out += the block's output (C4's residual add) */
   int32_t* err;
 } TfdMoeArgs;
 int tfd_moe_experts(const TfdMoeArgs* args, void* stream);
@@ -191,6 +192,21 @@ typedef struct {
   int32_t* err;
 } TfdGqaArgs;
 int tfd_gqa_decode(const TfdGqaArgs* args, void* stream);
+
+/* C4's f32 residual stream (torch_ref.py's policy: activations f32, a matmul
+ * casts its input to bf16).  tfd_rmsnorm_f32_rows: out = bf16(x * rsqrt(mean(x^2)
+ * + eps) * gamma) per row, f32 inside and one rounding (torch_ref.py:145-154
+ * `_rms_norm` followed by `_mm`'s cast; input_layernorm, post_norm :438-448 and
+ * final_rms_norm :558-567), to row-major out_rows [rows][ldo] and/or out_packed in
+ * the skinny GEMMs' operand order (rows <= 32, n % 32 == 0); NULL skips one.
+ * tfd_add_f32_rows: acc += add (residual_add, :533-543).  tfd_bf16_to_f32_rows:
+ * dst = f32(src) (embed's `.float()` of the table row, :546-555). */
+int tfd_rmsnorm_f32_rows(const float* x, int ldx, const void* gamma, void* out_rows, int ldo,
+                         void* out_packed, int rows, int n, float eps, void* stream);
+int tfd_add_f32_rows(float* acc, int lda, const float* add, int ldb, int rows, int n,
+                     void* stream);
+int tfd_bf16_to_f32_rows(const void* src, int lds, float* dst, int ldd, int rows, int n,
+                         void* stream);
 
 #ifdef __cplusplus
 }

@@ -313,3 +313,83 @@ def granite_attend(q, k_new, v_new, k_past, v_past, scale):
         probs = bf(torch.softmax(scaled.double(), dim=0).float())
         out[b] = bf(bf(probs[:, :, None] * vg).double().sum(0).float()).reshape(-1)
     return out
+
+
+# ---------------------------------------------------------------------------
+# Whole decode steps of the C4 model (torch_ref policy)
+# ---------------------------------------------------------------------------
+def _rope_rows(theta, rot, rows):
+    inv = 1.0 / theta ** (torch.arange(0, rot, 2, dtype=torch.float64) / rot)
+    f = torch.arange(rows, dtype=torch.float64)[:, None] * inv[None]
+    emb = torch.cat((f, f), dim=-1)
+    return emb.cos().to(BF16).float(), emb.sin().to(BF16).float()
+
+
+class Qwen35Oracle:
+    """``Qwen3_5Decoder``'s decode step for a batch of sequences, composed from
+    the torch twin's functions (torch_ref.py:243-312 linear_attention, :335-409
+    full_attention, :417-530 routing / post_norm / experts, :533-575 residual_add,
+    embed, final_rms_norm, lm_head): f32 residual stream, each matmul on the bf16
+    cast of its input with one rounding of the sum.  Weights are CPU tensors in
+    (out, in) row layouts under the names ``tilefoundry_amd.hybrid.qwen3_5``
+    uses; `cfg` supplies the shape (layer i is full attention when
+    ``cfg.is_full(i)``).  Each sequence carries its conv window, recurrent state
+    and KV cache from step to step."""
+
+    def __init__(self, cfg, weights: dict, rows: int, max_pos: int = 4096):
+        self.cfg, self.w, self.B = cfg, weights, rows
+        c = cfg
+        self.conv = {i: torch.zeros(rows, c.conv_dim, c.conv_kernel - 1)
+                     for i in range(c.layers) if not c.is_full(i)}
+        self.state = {i: torch.zeros(rows, c.lin_value_heads, c.lin_key_dim, c.lin_value_dim)
+                      for i in range(c.layers) if not c.is_full(i)}
+        self.k_past = {i: [torch.zeros(0, c.kv_heads, c.head_dim)] * rows
+                       for i in range(c.layers) if c.is_full(i)}
+        self.v_past = {i: [torch.zeros(0, c.kv_heads, c.head_dim)] * rows
+                       for i in range(c.layers) if c.is_full(i)}
+        self.cos, self.sin = _rope_rows(c.rope_theta, c.rot_dim, max_pos)
+        #: per step, per sequence: the smallest gap over layers between the k-th
+        #: and (k+1)-th router logit, in bf16 ulps of the k-th (a gap of an ulp or
+        #: two may pick another expert under any other summation order)
+        self.route_gaps: list[torch.Tensor] = []
+
+    def step(self, tokens, positions) -> torch.Tensor:
+        """One token per sequence at `positions` -> bf16-valued f32 logits [B][V]."""
+        c, B = self.cfg, self.B
+        hidden = self.w["embed"][torch.tensor(tokens)].float()
+        pos = torch.tensor(positions)
+        for i in range(c.layers):
+            W = lambda n: self.w[f"layer{i}.{n}"]
+            xn = bf(_rms_flat(hidden, W("gamma_in"), c.eps))
+            proj = bf(mm_rows(W("w_in").float(), xn))
+            if c.is_full(i):
+                HQ, HKV, D = c.heads, c.kv_heads, c.head_dim
+                qg = proj[:, :HQ * 2 * D].reshape(B, HQ, 2 * D)
+                k = proj[:, HQ * 2 * D:HQ * 2 * D + HKV * D].reshape(B, HKV, D)
+                v = proj[:, HQ * 2 * D + HKV * D:HQ * 2 * D + 2 * HKV * D].reshape(B, HKV, D)
+                mixed, k_rope = qwen35_attend(qg, k, v, self.k_past[i], self.v_past[i],
+                                              W("gamma_q"), W("gamma_k"), self.cos[pos],
+                                              self.sin[pos], D ** -0.5, c.eps)
+                self.k_past[i] = [torch.cat((self.k_past[i][b], bf(k_rope[b])[None]))
+                                  for b in range(B)]
+                self.v_past[i] = [torch.cat((self.v_past[i][b], v[b][None])) for b in range(B)]
+            else:
+                mixed, self.conv[i], self.state[i] = gdn_step(
+                    proj, self.conv[i], self.state[i], W("conv_w"), W("a_log"), W("dt_bias"),
+                    W("gamma_gdn"), hk=c.lin_key_heads, hv=c.lin_value_heads, dk=c.lin_key_dim,
+                    dv=c.lin_value_dim, rms_eps=c.eps)
+            hidden = hidden + bf(mm_rows(W("w_out").float(), bf(mixed)))
+            xm = bf(_rms_flat(hidden, W("gamma_post"), c.eps))
+            rlog = bf(mm_rows(W("w_router").float(), xm))
+            srt = rlog.sort(dim=-1, descending=True).values
+            kth = srt[:, c.top_k - 1].abs().clamp(min=2.0 ** -126)
+            gap = (srt[:, c.top_k - 1] - srt[:, c.top_k]) / torch.exp2(torch.floor(torch.log2(kth)) - 7)
+            gaps = gap if i == 0 else torch.minimum(gaps, gap)
+            rw, ridx = route_softmax_topk(rlog, c.top_k)
+            IS = c.shared_inter
+            hidden = hidden + moe_c4(xm, rw, ridx, W("w_gate"), W("w_up"), W("w_down"),
+                                     W("w_shared_in")[:IS], W("w_shared_in")[IS:],
+                                     W("w_shared_out"), W("w_shared_scale")[None])
+        self.route_gaps.append(gaps)
+        hn = bf(_rms_flat(hidden, self.w["gamma_final"], c.eps))
+        return bf(mm_rows(self.w["head"].float(), hn))

@@ -50,7 +50,7 @@ def _gemm(x, w, epi, resid=None, work=None):
     w = _packed(w)
     if epi == _lib.EPI_SWIGLU:
         out = torch.full((32 * (N // 2),), float("nan"), device=x.device, dtype=torch.bfloat16)
-    elif epi == _lib.EPI_LOGITS:
+    elif epi in (_lib.EPI_LOGITS, _lib.EPI_RESID_F32):
         out = torch.zeros(M, N, device=x.device, dtype=torch.float32)
     else:
         out = torch.zeros(M, N, device=x.device, dtype=torch.bfloat16)
@@ -98,6 +98,11 @@ def test_skinny_gemm_within_one_ulp_of_exact(gpu_device, M, K, N, split):
     res = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_RESID, r.to(gpu_device),
                 work=work).float()
     assert torch.equal(res, (r.float() + got).to(torch.bfloat16).float())
+    # f32 residual stream: out = resid + bf16-valued product, in f32
+    r32 = torch.randn(M, N, generator=g)
+    res32 = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_RESID_F32, r32.to(gpu_device),
+                  work=work)
+    assert torch.equal(res32, r32 + got)
     # swiglu over (gate, up) row pairs, from the kernel's own rounded pair
     if N % 64 == 0:
         sw = _gemm(x.to(gpu_device), w.to(gpu_device), _lib.EPI_SWIGLU, work=work).float()

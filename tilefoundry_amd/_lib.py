@@ -13,10 +13,10 @@ from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 PRO_PLAIN, PRO_NORM = 0, 1
-EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS = 0, 1, 2, 3
+EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS, EPI_RESID_F32 = 0, 1, 2, 3, 4
 ERR_TOKEN_RANGE, ERR_POS_RANGE, ERR_PAGE_RANGE, ERR_STEP_RANGE, ERR_SYNC = 1, 2, 4, 8, 16
 PAGE_SIZE = 16
 SKINNY_COUNTERS = 16384     # tile counters at the start of a skinny-GEMM work buffer
@@ -69,6 +69,9 @@ SIGNATURES: dict[str, list] = {
     "tfd_gdn_step": [P, P],
     "tfd_mamba_step": [P, P],
     "tfd_gqa_decode": [P, P],
+    "tfd_rmsnorm_f32_rows": [P, I, P, P, I, P, I, I, F, P],
+    "tfd_add_f32_rows": [P, I, P, I, I, I, P],
+    "tfd_bf16_to_f32_rows": [P, I, P, I, I, I, P],
 }
 RESTYPES = {"tfd_last_error": ctypes.c_char_p}
 UNCHECKED = {"tfd_abi_version", "tfd_decode_persistent_grid"}
@@ -90,7 +93,7 @@ class TfdMoeArgs(ctypes.Structure):
                                    "s_shared_in", "s_shared_out", "w_shared_scale", "hidden",
                                    "shared_scale", "partial", "groups", "out")],
         *[(n, c_int) for n in ("rows", "k", "experts", "hidden_size", "inter", "shared_inter",
-                                "hidden_ld", "fp8", "policy")],
+                                "hidden_ld", "fp8", "policy", "accumulate")],
         ("err", c_void_p),
     ]
 

@@ -197,6 +197,7 @@ struct MoeArgs {
   int* groups;                               // work: n | picked[E] | count[E] | entries[E][B]
   float* out;                                // [B][H]
   int B, H, I, IS, IM, k, E;
+  int accumulate;                            // out += (f32 policy)
   int* err;
 };
 
@@ -395,8 +396,13 @@ __global__ __launch_bounds__(kBlock) void k_moe_mix(MoeArgs a) {
     acc += kF32 ? d * wgt : rbf(d * wgt);
   }
   const float dsh = pb[(int64_t)a.k * a.H];
-  a.out[(int64_t)b * a.H + n] =
-      kF32 ? acc + dsh * (a.w_sscale ? a.sscale[b] : 1.f) : rbf(rbf(acc) + dsh);
+  float* o = a.out + (int64_t)b * a.H + n;
+  if (kF32) {
+    const float y = acc + dsh * (a.w_sscale ? a.sscale[b] : 1.f);
+    *o = a.accumulate ? *o + y : y;
+  } else {
+    *o = rbf(rbf(acc) + dsh);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -662,6 +668,62 @@ __global__ __launch_bounds__(kBlock) void k_mamba_norm(MambaArgs a, int exp_) {
     a.out[xp_off_h(b, i)] = f2bf(a.gated[(int64_t)b * exp_ + i] * tot * bf2f(a.gamma[i]));
 }
 
+// ---------------------------------------------------------------------------
+// The f32 residual stream of C4 (torch_ref.py's policy): norms of f32 rows with
+// one bf16 rounding of the scaled value (the matmul's cast), residual adds and
+// the embedding row lifted to f32.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kBlock) void k_rmsnorm_f32_rows(const float* __restrict__ x, int ldx,
+                                                             const bf16* __restrict__ gamma,
+                                                             bf16* out_rows, int ldo,
+                                                             bf16* out_packed, int n, float eps) {
+  constexpr int kMax4 = 8;                 // n <= 8192: the row stays in registers
+  const int b = blockIdx.x, tid = threadIdx.x, n4 = n / 4;
+  __shared__ float red[kWavesPerBlock];
+  const float4* xr = reinterpret_cast<const float4*>(x + (int64_t)b * ldx);
+  float4 v[kMax4];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMax4; ++i) {
+    const int q = tid + kBlock * i;
+    v[i] = q < n4 ? xr[q] : float4{0.f, 0.f, 0.f, 0.f};
+    ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+  }
+  ss = wave_sum(ss);
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kWavesPerBlock; ++w) tot += red[w];
+  const float r = rsqrtf(tot / (float)n + eps);
+#pragma unroll
+  for (int i = 0; i < kMax4; ++i) {
+    const int q = tid + kBlock * i;
+    if (q < n4) {
+      const int c = 4 * q;
+      const uint2 g = *reinterpret_cast<const uint2*>(gamma + c);
+      const uint2 o = {pack2(v[i].x * r * bf_lo(g.x), v[i].y * r * bf_hi(g.x)),
+                       pack2(v[i].z * r * bf_lo(g.y), v[i].w * r * bf_hi(g.y))};
+      if (out_rows) *reinterpret_cast<uint2*>(out_rows + (int64_t)b * ldo + c) = o;
+      if (out_packed) *reinterpret_cast<uint2*>(out_packed + xp_off_h(b, c)) = o;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBlock) void k_add_f32_rows(float* __restrict__ acc, int lda,
+                                                         const float* __restrict__ add, int ldb,
+                                                         int n) {
+  const int b = blockIdx.y, i = blockIdx.x * kBlock + threadIdx.x;
+  if (i < n) acc[(int64_t)b * lda + i] += add[(int64_t)b * ldb + i];
+}
+
+__global__ __launch_bounds__(kBlock) void k_bf16_to_f32_rows(const bf16* __restrict__ src,
+                                                             int lds, float* __restrict__ dst,
+                                                             int ldd, int n) {
+  const int b = blockIdx.y, i = blockIdx.x * kBlock + threadIdx.x;
+  if (i < n) dst[(int64_t)b * ldd + i] = bf2f(src[(int64_t)b * lds + i]);
+}
+
 }  // namespace
 
 template <bool kFp8, bool kF32>
@@ -752,7 +814,10 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
   a.IM = t.hidden_ld;
   a.k = t.k;
   a.E = t.experts;
+  a.accumulate = t.accumulate;
   a.err = t.err;
+  if (t.accumulate && t.policy != TFD_POLICY_F32)
+    return fail(kUnsupported, "moe_experts: accumulate needs the f32 policy");
   auto s = (hipStream_t)stream;
   if (t.fp8 && t.policy == TFD_POLICY_BF16) return launch_moe<true, false>(a, s);
   if (!t.fp8 && t.policy == TFD_POLICY_F32) return launch_moe<false, true>(a, s);
@@ -830,4 +895,37 @@ int tfd_mamba_step(const TfdMambaArgs* args, void* stream) {
   return launched("mamba_step");
 }
 
+int tfd_rmsnorm_f32_rows(const float* x, int ldx, const void* gamma, void* out_rows, int ldo,
+                         void* out_packed, int rows, int n, float eps, void* stream) {
+  if (!x || !gamma || (!out_rows && !out_packed)) return fail(kBadArg, "rmsnorm_f32: null pointer");
+  if (rows <= 0 || n <= 0 || n > 8192 || n % 4 || ldx < n || ldx % 4 ||
+      (out_rows && (ldo < n || ldo % 4)) || (out_packed && (rows > kMaxRowsH || n % 32)))
+    return fail(kBadShape, "rmsnorm_f32: rows=%d n=%d (a multiple of 4, <= 8192) ldx=%d ldo=%d",
+                rows, n, ldx, ldo);
+  hipLaunchKernelGGL(k_rmsnorm_f32_rows, dim3(rows), dim3(kBlock), 0, (hipStream_t)stream, x, ldx,
+                     (const bf16*)gamma, (bf16*)out_rows, ldo, (bf16*)out_packed, n, eps);
+  return launched("rmsnorm_f32_rows");
+}
+
+int tfd_add_f32_rows(float* acc, int lda, const float* add, int ldb, int rows, int n,
+                     void* stream) {
+  if (!acc || !add) return fail(kBadArg, "add_f32: null pointer");
+  if (rows <= 0 || n <= 0 || lda < n || ldb < n)
+    return fail(kBadShape, "add_f32: rows=%d n=%d", rows, n);
+  hipLaunchKernelGGL(k_add_f32_rows, dim3((n + kBlock - 1) / kBlock, rows), dim3(kBlock), 0,
+                     (hipStream_t)stream, acc, lda, add, ldb, n);
+  return launched("add_f32_rows");
+}
+
+int tfd_bf16_to_f32_rows(const void* src, int lds, float* dst, int ldd, int rows, int n,
+                         void* stream) {
+  if (!src || !dst) return fail(kBadArg, "bf16_to_f32: null pointer");
+  if (rows <= 0 || n <= 0 || lds < n || ldd < n)
+    return fail(kBadShape, "bf16_to_f32: rows=%d n=%d", rows, n);
+  hipLaunchKernelGGL(k_bf16_to_f32_rows, dim3((n + kBlock - 1) / kBlock, rows), dim3(kBlock), 0,
+                     (hipStream_t)stream, (const bf16*)src, lds, dst, ldd, n);
+  return launched("bf16_to_f32_rows");
+}
+
 }  // extern "C"
+

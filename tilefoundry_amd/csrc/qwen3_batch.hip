@@ -96,7 +96,7 @@ __global__ __launch_bounds__(kWave) void k_rmsnorm_rows(const bf16* __restrict__
 // does not depend on which slice finishes first -- applies the epilogue and
 // puts the counter back to zero for the next call.
 // ---------------------------------------------------------------------------
-enum SkinnyEpi { kSkStore = 0, kSkResid = 1, kSkSwiglu = 2, kSkLogits = 3 };
+enum SkinnyEpi { kSkStore = 0, kSkResid = 1, kSkSwiglu = 2, kSkLogits = 3, kSkResidF32 = 4 };
 
 // Two shapes: Ks <= 1024 (66 KiB of LDS, two blocks of four waves per compute
 // unit, eight steps in flight per wave) and Ks <= 2048 (the head: one block of
@@ -126,6 +126,9 @@ __device__ __forceinline__ void skinny_store(const f32x4 (&c)[2], int halves, in
           ((bf16*)out)[(int64_t)m * ldo + n] = f2bf(y);
         else if (kEpi == kSkResid)
           ((bf16*)out)[(int64_t)m * ldo + n] = f2bf(bf2f(resid[(int64_t)m * ldr + n]) + y);
+        else if (kEpi == kSkResidF32)   // f32 residual stream: out = resid + y (in place allowed)
+          ((float*)out)[(int64_t)m * ldo + n] =
+              reinterpret_cast<const float*>(resid)[(int64_t)m * ldr + n] + y;
         else
           ((float*)out)[(int64_t)m * ldo + n] = y;
       }
@@ -776,7 +779,7 @@ int tfd_gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M,
   if (!x || !w || !scale || !out) return fail(kBadArg, "gemm_skinny_fp8: null pointer");
   if (M <= 0 || M > kMaxRows || K <= 0 || K % 256 || N <= 0)
     return fail(kBadShape, "gemm_skinny_fp8: M=%d (1..32) K=%d (multiple of 256) N=%d", M, K, N);
-  if (epilogue == TFD_EPI_RESID && (!resid || ldr < N))
+  if ((epilogue == TFD_EPI_RESID || epilogue == TFD_EPI_RESID_F32) && (!resid || ldr < N))
     return fail(kBadArg, "gemm_skinny_fp8: residual epilogue needs resid with ldr >= N");
   if (epilogue == TFD_EPI_SWIGLU ? (N % 2 || (N / 2) % 32) : ldo < N)
     return fail(kBadShape, "gemm_skinny_fp8: ldo=%d N=%d", ldo, N);
@@ -799,6 +802,7 @@ int tfd_gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M,
     case TFD_EPI_RESID: TFD_KSPLIT8_EPI(kSkResid); break;
     case TFD_EPI_SWIGLU: TFD_KSPLIT8_EPI(kSkSwiglu); break;
     case TFD_EPI_LOGITS: TFD_KSPLIT8_EPI(kSkLogits); break;
+    case TFD_EPI_RESID_F32: TFD_KSPLIT8_EPI(kSkResidF32); break;
     default:
       return fail(kBadArg, "gemm_skinny_fp8: epilogue %d", epilogue);
   }
@@ -813,7 +817,7 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
   if (!x || !w || !out) return fail(kBadArg, "gemm_skinny: null pointer");
   if (M <= 0 || M > kMaxRows || K <= 0 || K % 256 || N <= 0)
     return fail(kBadShape, "gemm_skinny: M=%d (1..32) K=%d (multiple of 256) N=%d", M, K, N);
-  if (epilogue == TFD_EPI_RESID && (!resid || ldr < N))
+  if ((epilogue == TFD_EPI_RESID || epilogue == TFD_EPI_RESID_F32) && (!resid || ldr < N))
     return fail(kBadArg, "gemm_skinny: residual epilogue needs resid with ldr >= N");
   if (epilogue == TFD_EPI_SWIGLU ? (N % 2 || (N / 2) % 32) : ldo < N)
     return fail(kBadShape, "gemm_skinny: ldo=%d N=%d (SwiGLU: N/2 a multiple of 32)", ldo, N);
@@ -843,6 +847,7 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
       case TFD_EPI_RESID: TFD_KSPLIT_EPI(kSkResid); break;
       case TFD_EPI_SWIGLU: TFD_KSPLIT_EPI(kSkSwiglu); break;
       case TFD_EPI_LOGITS: TFD_KSPLIT_EPI(kSkLogits); break;
+      case TFD_EPI_RESID_F32: TFD_KSPLIT_EPI(kSkResidF32); break;
       default:
         return fail(kBadArg, "gemm_skinny: epilogue %d", epilogue);
     }
@@ -875,6 +880,7 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
     case TFD_EPI_RESID: TFD_SKINNY_LAUNCH(kSkResid); break;
     case TFD_EPI_SWIGLU: TFD_SKINNY_LAUNCH(kSkSwiglu); break;
     case TFD_EPI_LOGITS: TFD_SKINNY_LAUNCH(kSkLogits); break;
+    case TFD_EPI_RESID_F32: TFD_SKINNY_LAUNCH(kSkResidF32); break;
     default:
       return fail(kBadArg, "gemm_skinny: epilogue %d", epilogue);
   }

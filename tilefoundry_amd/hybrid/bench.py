@@ -1,6 +1,7 @@
 """Per-kernel HBM roofline of the hybrid models' decode kernels.
 
     python -m tilefoundry_amd.hybrid.bench [--config c4|c4b16|c5|all] [--reps 20]
+    python -m tilefoundry_amd.hybrid.bench --config c4-step --rows 1|16 [--steps 256]
 
 Every kernel runs at its workload's shapes on synthetic data (seeded) with the
 launches of one measurement captured in a HIP graph and replayed; HIP events on
@@ -25,6 +26,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import time
 
 import torch
 
@@ -325,14 +327,51 @@ def run(config: str, reps: int) -> list[dict]:
     return res
 
 
+def bench_c4_step(rows: int, steps: int, prompt: int = 32) -> dict:
+    """Whole C4 decode steps (Qwen3.5-35B-A3B shape, 40 layers, 248,320-token
+    vocabulary, synthetic weights): tok/s over `steps` greedy steps after a
+    `prompt`-token random prompt per sequence (walked untimed), and the step's
+    algorithmic bytes (dense weights once, the experts the step picked once per
+    layer, GDN state read and written, KV read) against 8 TB/s."""
+    from .qwen3_5 import Qwen35Config, Qwen35Engine, synthetic_weights
+
+    cfg = Qwen35Config()
+    t0 = time.perf_counter()
+    w = synthetic_weights(cfg, seed=0, device=DEV)
+    eng = Qwen35Engine(cfg, w, rows=rows, device=DEV, max_steps=prompt + steps + 16)
+    print(f"[bench] c4 weights + engine + capture {time.perf_counter() - t0:.1f}s", flush=True)
+    g = torch.Generator().manual_seed(0)
+    prompts = [torch.randint(0, cfg.vocab, (prompt,), generator=g).tolist() for _ in range(rows)]
+    tokens, seconds, _ = eng.generate(prompts, steps)
+    touched = len(set(eng.ridx.reshape(-1).tolist()))       # the last layer's picks, last step
+    wbytes = eng.weight_bytes_per_step(touched)
+    positions = range(prompt - 1, prompt - 1 + steps)
+    sbytes = sum(eng.state_bytes_per_step([p] * rows) for p in positions) / steps
+    step_s = seconds / steps
+    out = {"config": f"c4 step b{rows}", "tok_s": round(rows * steps / seconds, 1),
+           "ms_per_step": round(step_s * 1e3, 4), "steps": steps,
+           "bytes_per_step": int(wbytes + sbytes), "experts_touched_sample": touched,
+           "GB/s": round((wbytes + sbytes) / step_s / 1e9, 1),
+           "frac": round((wbytes + sbytes) / step_s / HBM_PEAK, 4),
+           "first_tokens": tokens[0][:8]}
+    print(json.dumps(out), flush=True)
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
-    ap.add_argument("--config", default="all", choices=("c4", "c4b16", "c5", "all"))
+    ap.add_argument("--config", default="all",
+                    choices=("c4", "c4b16", "c5", "all", "c4-step"))
     ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--rows", type=int, default=1, help="c4-step: sequences per step")
+    ap.add_argument("--steps", type=int, default=256, help="c4-step: timed steps")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         raise SystemExit("hybrid kernel bench: no GPU visible")
+    if args.config == "c4-step":
+        bench_c4_step(args.rows, args.steps)
+        return 0
     for c in (("c4", "c4b16", "c5") if args.config == "all" else (args.config,)):
         run(c, args.reps)
     return 0

@@ -1,0 +1,458 @@
+"""Qwen3.5-35B-A3B-style hybrid decode on the GPU (workload C4).
+
+The decode step of ``examples/qwen3_5_35b_a3b-tilelang/runtime_model.py`` (its
+``Qwen3_5Decoder`` over ``Qwen3_5LinearAttnLayer`` / ``Qwen3_5FullAttnLayer``),
+with the arithmetic of the example's plain-torch twin
+(``kernels/torch_ref.py:22-40``): the residual stream is f32, every matmul casts
+its input to bf16 and rounds its f32 sum once.  Per layer:
+
+* input norm (f32 in, one bf16 rounding, operand order) -> in-projection
+  (skinny GEMM, f32 out) -> gated-DeltaNet step (``tfd_gdn_step``) or the
+  full-attention step (``tfd_gqa_decode``) -> out-projection, whose epilogue
+  adds it into the f32 residual stream;
+* post norm -> router projection -> softmax/top-8 (``tfd_route_topk``) -> routed
+  + shared experts (``tfd_moe_experts``, expert-grouped), whose mix adds into the
+  stream;
+
+then the final norm, the head, the greedy pick and the next token's embedding
+(``tfd_argmax_rows``, ``tfd_finalize_rows``).  Layer i is full attention when
+i % 4 == 3 (3 GDN layers, then one GQA layer).  Sequences (up to 32) step
+together, each with its own position, conv window, recurrent state and KV pages;
+a step is recorded into a HIP graph (two, alternating, because the conv windows
+ping-pong between two buffers) and replayed.
+
+Weights are synthetic (random init on the device; there is no checkpoint here)
+in the kernels' row layouts: every projection ``[out][in]`` (the reference's
+``(in, out)`` transposed), packed once for the skinny GEMM; experts
+``[E][I][H]`` / ``[E][H][I]``.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from time import perf_counter
+
+import torch
+
+from .. import _lib
+from .._lib import lib, ptr
+
+BF = torch.bfloat16
+F32 = torch.float32
+I32 = torch.int32
+
+
+@dataclass(frozen=True)
+class Qwen35Config:
+    """The published Qwen3.5-35B-A3B decoder shape."""
+
+    hidden: int = 2048
+    layers: int = 40
+    full_every: int = 4
+    lin_key_heads: int = 16
+    lin_value_heads: int = 32
+    lin_key_dim: int = 128
+    lin_value_dim: int = 128
+    conv_kernel: int = 4
+    heads: int = 16
+    kv_heads: int = 2
+    head_dim: int = 256
+    rot_dim: int = 64
+    rope_theta: float = 1.0e7
+    experts: int = 256
+    top_k: int = 8
+    moe_inter: int = 512
+    shared_inter: int = 512
+    vocab: int = 248320
+    eps: float = 1e-6
+
+    def is_full(self, i: int) -> bool:
+        return i % self.full_every == self.full_every - 1
+
+    @property
+    def key_dim(self) -> int:
+        return self.lin_key_heads * self.lin_key_dim
+
+    @property
+    def value_dim(self) -> int:
+        return self.lin_value_heads * self.lin_value_dim
+
+    @property
+    def conv_dim(self) -> int:
+        return 2 * self.key_dim + self.value_dim
+
+    @property
+    def gdn_in(self) -> int:
+        """Rows of the GDN in-projection: conv channels (q|k|v), z, b, a."""
+        return self.conv_dim + self.value_dim + 2 * self.lin_value_heads
+
+    @property
+    def attn_in(self) -> int:
+        """Rows of the attention in-projection: q then gate per head, k, v."""
+        return self.heads * 2 * self.head_dim + 2 * self.kv_heads * self.head_dim
+
+
+def rope_tables(cfg: Qwen35Config, rows: int):
+    """bf16 cos/sin [rows][rot] of rotate-half RoPE, ``cat(freqs, freqs)``
+    (torch_ref.py:157-181)."""
+    inv = 1.0 / cfg.rope_theta ** (torch.arange(0, cfg.rot_dim, 2, dtype=torch.float64) /
+                                   cfg.rot_dim)
+    f = torch.arange(rows, dtype=torch.float64)[:, None] * inv[None]
+    emb = torch.cat((f, f), dim=-1)
+    return emb.cos().to(BF), emb.sin().to(BF)
+
+
+def synthetic_weights(cfg: Qwen35Config, seed: int = 0, device: str = "cuda:0",
+                      std: float = 0.02) -> dict[str, torch.Tensor]:
+    """Random-init weights in the kernels' layouts: matrices N(0, std) (router
+    logits then come out near N(0, 1) at hidden 2048), norm scales 1 + N(0, std),
+    a_log and dt_bias N(0, 0.5).  Drawn on `device` from a seeded generator."""
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def rn(*shape, s=std):
+        return (torch.randn(*shape, generator=g, device=device) * s).to(BF)
+
+    def gamma(n):
+        return (1 + torch.randn(n, generator=g, device=device) * std).to(BF)
+
+    H, E, I, IS = cfg.hidden, cfg.experts, cfg.moe_inter, cfg.shared_inter
+    w = {"embed": rn(cfg.vocab, H), "gamma_final": gamma(H), "head": rn(cfg.vocab, H)}
+    for i in range(cfg.layers):
+        p = f"layer{i}."
+        w[p + "gamma_in"] = gamma(H)
+        if cfg.is_full(i):
+            w[p + "w_in"] = rn(cfg.attn_in, H)
+            w[p + "gamma_q"] = gamma(cfg.head_dim)
+            w[p + "gamma_k"] = gamma(cfg.head_dim)
+            w[p + "w_out"] = rn(H, cfg.heads * cfg.head_dim)
+        else:
+            w[p + "w_in"] = rn(cfg.gdn_in, H)
+            w[p + "conv_w"] = rn(cfg.conv_dim, cfg.conv_kernel, s=0.5)
+            w[p + "a_log"] = rn(cfg.lin_value_heads, s=0.5)
+            w[p + "dt_bias"] = rn(cfg.lin_value_heads, s=0.5)
+            w[p + "gamma_gdn"] = gamma(cfg.lin_value_dim)
+            w[p + "w_out"] = rn(H, cfg.value_dim)
+        w[p + "gamma_post"] = gamma(H)
+        w[p + "w_router"] = rn(E, H)
+        w[p + "w_gate"] = rn(E, I, H)
+        w[p + "w_up"] = rn(E, I, H)
+        w[p + "w_down"] = rn(E, H, I)
+        w[p + "w_shared_in"] = rn(2 * IS, H)     # gate rows, then up rows
+        w[p + "w_shared_out"] = rn(H, IS)
+        w[p + "w_shared_scale"] = rn(H)
+    return w
+
+
+class Qwen35Engine:
+    """A Qwen3.5-style hybrid decoder stepping `rows` sequences together."""
+
+    def __init__(self, cfg: Qwen35Config, weights: dict[str, torch.Tensor], *, rows: int,
+                 device: str = "cuda:0", max_steps: int = 2112, page_seed: int = 0,
+                 split_len: int = 128, graph: bool = True):
+        if not 1 <= rows <= 32:
+            raise ValueError("rows: 1..32 sequences")
+        self.cfg, self.B, self.device = cfg, rows, device
+        self._lib = lib()
+        self.nsteps = max_steps
+        self.split_len = split_len
+        self._pack(weights)
+        self._buffers(page_seed)
+        self.graphs = None
+        self._cur = 0
+        if graph:
+            self._capture()
+
+    # ----------------------------------------------------------------- set-up
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _packed(self, w: torch.Tensor) -> torch.Tensor:
+        N, K = w.shape
+        out = torch.empty(-(-N // 16) * 16 * K, dtype=BF, device=self.device)
+        self._lib.tfd_pack_skinny_bf16(ptr(w), K, N, K, ptr(out), self._stream())
+        return out
+
+    def _pack(self, w):
+        cfg = self.cfg
+        self.layers = []
+        for i in range(cfg.layers):
+            p = f"layer{i}."
+            d = {k[len(p):]: v for k, v in w.items() if k.startswith(p)}
+            d["w_in"] = self._packed(d["w_in"])
+            d["w_out"] = self._packed(d["w_out"])
+            d["w_router"] = self._packed(d["w_router"])
+            self.layers.append(d)
+        self.embed = w["embed"]
+        self.gamma_final = w["gamma_final"]
+        self.head = self._packed(w["head"])
+        torch.cuda.synchronize(self.device)
+
+    def _buffers(self, page_seed):
+        cfg, B, dev = self.cfg, self.B, self.device
+        H, V, k = cfg.hidden, cfg.vocab, cfg.top_k
+
+        def z(*shape, dtype=F32):
+            return torch.zeros(*shape, dtype=dtype, device=dev)
+
+        self.hidden = z(B, H)
+        self.emb = z(B, H, dtype=BF)
+        self.xn = z(32 * H, dtype=BF)                       # operand order
+        self.xm = z(B, H, dtype=BF)                         # MoE input rows
+        self.nproj = max(cfg.gdn_in, cfg.attn_in)
+        self.proj = z(B, self.nproj)
+        self.mix = z(32 * max(cfg.value_dim, cfg.heads * cfg.head_dim), dtype=BF)
+        self.rlog = z(B, cfg.experts)
+        self.rw = z(B, k)
+        self.ridx = z(B, k, dtype=I32)
+        ld = max(cfg.moe_inter, cfg.shared_inter)
+        self.moe_hidden = z(B, k + 1, ld, dtype=BF)
+        self.moe_sscale = z(B)
+        self.moe_partial = z(B, k + 1, H)
+        self.moe_groups = z(_lib.moe_group_words(cfg.experts, B), dtype=I32)
+        self.moe_ld = ld
+        # GDN state and conv windows (two buffers each, ping-pong by step)
+        self.state, self.conv = {}, {}
+        for i in range(cfg.layers):
+            if not cfg.is_full(i):
+                self.state[i] = z(B, cfg.lin_value_heads, cfg.lin_key_dim, cfg.lin_value_dim)
+                self.conv[i] = (z(B, cfg.conv_dim, cfg.conv_kernel - 1),
+                                z(B, cfg.conv_dim, cfg.conv_kernel - 1))
+        # paged KV of the full-attention layers
+        self.max_pages = -(-self.nsteps // 16)
+        self.num_pages = B * self.max_pages
+        gen = torch.Generator().manual_seed(page_seed)
+        self.page_table = torch.randperm(self.num_pages, generator=gen).view(
+            B, self.max_pages).to(I32).to(dev)
+        self.kpool, self.vpool = {}, {}
+        for i in range(cfg.layers):
+            if cfg.is_full(i):
+                shape = (self.num_pages, cfg.kv_heads, 16, cfg.head_dim)
+                self.kpool[i] = z(*shape, dtype=BF)
+                self.vpool[i] = z(*shape, dtype=BF)
+        self.nsplit = -(-self.max_pages * 16 // self.split_len)
+        self.stride = self.max_pages * 16
+        self.scores = z(B * cfg.heads * self.stride)
+        self.stats = z(B * cfg.heads * self.nsplit * 2)
+        self.part = z(B * cfg.heads * self.nsplit * cfg.head_dim)
+        self.counters = z(B * cfg.kv_heads, dtype=I32)
+        cos, sin = rope_tables(cfg, self.max_pages * 16)
+        self.cos, self.sin = cos.to(dev), sin.to(dev)
+        # head, pick, token feed
+        self.logits = z(B, V)
+        self.pick = z(B, dtype=I32)
+        self.argmax_work = z(B * _lib.ARGMAX_WORK, dtype=I32)
+        self.ids = z(B, dtype=torch.int64)
+        self.pos = z(B, dtype=I32)
+        self.inp = z(B, self.nsteps, dtype=I32)
+        self.plen = z(B, dtype=I32)
+        self.sam = z(B, self.nsteps, dtype=I32)
+        self.err = z(1, dtype=I32)
+        self.work = z(1 << 21)
+
+    # ------------------------------------------------------------------ step
+    def _gemm(self, x, w, K, N, out, ldo, s, resid=None):
+        """out = bf16-valued f32 of x @ w^T, or resid + that (f32, in place)."""
+        epi = _lib.EPI_LOGITS if resid is None else _lib.EPI_RESID_F32
+        self._lib.tfd_gemm_skinny_bf16(ptr(x), ptr(w), self.B, K, N, epi,
+                                       None if resid is None else ptr(resid),
+                                       0 if resid is None else ldo, ptr(out), ldo,
+                                       ptr(self.work), self.work.numel(), s)
+
+    def _gdn(self, i, w, s, cur):
+        cfg, L = self.cfg, self._lib
+        a = _lib.TfdGdnArgs()
+        cin, cout = self.conv[i][cur], self.conv[i][1 - cur]
+        a.proj, a.proj_ld, a.conv_in, a.conv_out = ptr(self.proj), self.nproj, ptr(cin), ptr(cout)
+        a.state = ptr(self.state[i])
+        a.conv_w, a.a_log, a.dt_bias = ptr(w["conv_w"]), ptr(w["a_log"]), ptr(w["dt_bias"])
+        a.gamma, a.out = ptr(w["gamma_gdn"]), ptr(self.mix)
+        a.rows, a.key_heads, a.value_heads = self.B, cfg.lin_key_heads, cfg.lin_value_heads
+        a.head_k_dim, a.head_v_dim, a.conv_kernel = cfg.lin_key_dim, cfg.lin_value_dim, \
+            cfg.conv_kernel
+        a.l2_eps, a.rms_eps = 1e-6, cfg.eps
+        L.tfd_gdn_step(ctypes_addr(a), s)
+
+    def _attn(self, i, w, s):
+        cfg = self.cfg
+        a = _lib.TfdGqaArgs()
+        a.qkv, a.ldq = ptr(self.proj), self.nproj
+        a.gamma_q, a.gamma_k = ptr(w["gamma_q"]), ptr(w["gamma_k"])
+        a.cos_table, a.sin_table = ptr(self.cos), ptr(self.sin)
+        a.rope_rows, a.rot_dim = self.cos.shape[0], cfg.rot_dim
+        a.pos, a.page_table, a.max_pages = ptr(self.pos), ptr(self.page_table), self.max_pages
+        a.k_pool, a.v_pool, a.num_pages = ptr(self.kpool[i]), ptr(self.vpool[i]), self.num_pages
+        a.rows, a.heads, a.kv_heads, a.head_dim = self.B, cfg.heads, cfg.kv_heads, cfg.head_dim
+        a.scale, a.eps = cfg.head_dim ** -0.5, cfg.eps
+        a.scores, a.score_stride, a.stats, a.part = ptr(self.scores), self.stride, \
+            ptr(self.stats), ptr(self.part)
+        a.counters, a.nsplit, a.split_len = ptr(self.counters), self.nsplit, self.split_len
+        a.out, a.policy, a.err = ptr(self.mix), _lib.POLICY_F32, ptr(self.err)
+        self._lib.tfd_gqa_decode(ctypes_addr(a), s)
+
+    def _moe(self, w, s):
+        cfg = self.cfg
+        a = _lib.TfdMoeArgs()
+        a.x, a.weights, a.idx = ptr(self.xm), ptr(self.rw), ptr(self.ridx)
+        a.w_gate, a.w_up, a.w_down = ptr(w["w_gate"]), ptr(w["w_up"]), ptr(w["w_down"])
+        a.w_shared_in, a.w_shared_out = ptr(w["w_shared_in"]), ptr(w["w_shared_out"])
+        a.w_shared_scale = ptr(w["w_shared_scale"])
+        a.hidden, a.shared_scale, a.partial = ptr(self.moe_hidden), ptr(self.moe_sscale), \
+            ptr(self.moe_partial)
+        a.groups, a.out = ptr(self.moe_groups), ptr(self.hidden)
+        a.rows, a.k, a.experts, a.hidden_size = self.B, cfg.top_k, cfg.experts, cfg.hidden
+        a.inter, a.shared_inter, a.hidden_ld = cfg.moe_inter, cfg.shared_inter, self.moe_ld
+        a.fp8, a.policy, a.err = 0, _lib.POLICY_F32, ptr(self.err)
+        a.accumulate = 1                               # residual add into the stream
+        self._lib.tfd_moe_experts(ctypes_addr(a), s)
+
+    def _layer(self, i, s, cur):
+        cfg, L, w, B, H = self.cfg, self._lib, self.layers[i], self.B, self.cfg.hidden
+        L.tfd_rmsnorm_f32_rows(ptr(self.hidden), H, ptr(w["gamma_in"]), None, 0, ptr(self.xn),
+                               B, H, cfg.eps, s)
+        # the out-projection adds itself into the residual stream
+        if cfg.is_full(i):
+            self._gemm(self.xn, w["w_in"], H, cfg.attn_in, self.proj, self.nproj, s)
+            self._attn(i, w, s)
+            self._gemm(self.mix, w["w_out"], cfg.heads * cfg.head_dim, H, self.hidden, H, s,
+                       resid=self.hidden)
+        else:
+            self._gemm(self.xn, w["w_in"], H, cfg.gdn_in, self.proj, self.nproj, s)
+            self._gdn(i, w, s, cur)
+            self._gemm(self.mix, w["w_out"], cfg.value_dim, H, self.hidden, H, s,
+                       resid=self.hidden)
+        L.tfd_rmsnorm_f32_rows(ptr(self.hidden), H, ptr(w["gamma_post"]), ptr(self.xm), H,
+                               ptr(self.xn), B, H, cfg.eps, s)
+        self._gemm(self.xn, w["w_router"], H, cfg.experts, self.rlog, cfg.experts, s)
+        L.tfd_route_topk(ptr(self.rlog), cfg.experts, B, cfg.experts, cfg.top_k,
+                         _lib.ROUTE_SOFTMAX_TOPK, ptr(self.rw), ptr(self.ridx), s)
+        self._moe(w, s)                                # accumulates into the stream
+
+    def _step(self, cur):
+        s = self._stream()
+        cfg, L, B, H, V = self.cfg, self._lib, self.B, self.cfg.hidden, self.cfg.vocab
+        L.tfd_bf16_to_f32_rows(ptr(self.emb), H, ptr(self.hidden), H, B, H, s)
+        for i in range(cfg.layers):
+            self._layer(i, s, cur)
+        L.tfd_rmsnorm_f32_rows(ptr(self.hidden), H, ptr(self.gamma_final), None, 0,
+                               ptr(self.xn), B, H, cfg.eps, s)
+        self._gemm(self.xn, self.head, H, V, self.logits, V, s)
+        L.tfd_argmax_rows(ptr(self.logits), V, B, V, ptr(self.pick), ptr(self.argmax_work), s)
+        L.tfd_finalize_rows(ptr(self.pick), B, ptr(self.inp), self.nsteps, ptr(self.plen),
+                            ptr(self.ids), ptr(self.pos), ptr(self.sam), self.nsteps,
+                            self.nsteps, ptr(self.embed), ptr(self.emb), H, H, V, ptr(self.err),
+                            s)
+
+    def _capture(self):
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self._load_prompts([[0]] * self.B)
+            for cur in (0, 1):
+                self._step(cur)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graphs = []
+        for cur in (0, 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._step(cur)
+            self.graphs.append(g)
+        torch.cuda.synchronize(self.device)
+        self._reset()
+
+    def replay(self):
+        if self.graphs is not None:
+            self.graphs[self._cur].replay()
+        else:
+            self._step(self._cur)
+        self._cur ^= 1
+
+    # ------------------------------------------------------------- generation
+    def _reset(self):
+        self.pos.zero_()
+        self.sam.zero_()
+        self.err.zero_()
+        self.counters.zero_()
+        for i in self.state:
+            self.state[i].zero_()
+            self.conv[i][0].zero_()
+            self.conv[i][1].zero_()
+        self._cur = 0
+
+    def _load_prompts(self, prompts):
+        self._reset()
+        self.inp.zero_()
+        self.plen.copy_(torch.tensor([len(p) for p in prompts], dtype=I32))
+        for b, p in enumerate(prompts):
+            self.inp[b, :len(p)] = torch.tensor(p, dtype=I32).to(self.device)
+        self.ids.copy_(torch.tensor([p[0] for p in prompts], dtype=torch.int64))
+        self._lib.tfd_embed_rows_bf16(ptr(self.embed), ptr(self.ids), ptr(self.emb),
+                                      self.cfg.hidden, self.B, self.cfg.hidden, self.cfg.vocab,
+                                      ptr(self.err), self._stream())
+
+    def check_errors(self):
+        e = int(self.err.item())
+        if e:
+            raise RuntimeError(f"hybrid decode kernels raised error bits {e:#x}")
+
+    def generate(self, prompts: list[list[int]], max_new: int, record_logits: bool = False):
+        """Walk every prompt and continue for *max_new* greedy tokens per sequence
+        (the prompt walk is untimed).  -> (tokens per sequence, seconds of the
+        timed steps, logits [steps][rows][V] when recorded)."""
+        if len(prompts) != self.B or any(len(p) < 1 for p in prompts):
+            raise ValueError(f"need {self.B} non-empty prompts")
+        longest = max(len(p) for p in prompts)
+        if longest + max_new > self.nsteps:
+            raise ValueError(f"prompt {longest} + {max_new} exceeds {self.nsteps} steps")
+        self._load_prompts(prompts)
+        steps = longest - 1 + max_new
+        hist = [] if record_logits else None
+        torch.cuda.synchronize(self.device)
+        for _ in range(longest - 1):
+            self.replay()
+            if hist is not None:
+                hist.append(self.logits.clone())
+        torch.cuda.synchronize(self.device)
+        t0 = perf_counter()
+        for _ in range(longest - 1, steps):
+            self.replay()
+            if hist is not None:
+                hist.append(self.logits.clone())
+        torch.cuda.synchronize(self.device)
+        seconds = perf_counter() - t0
+        self.check_errors()
+        sam = self.sam.cpu()
+        tokens = [sam[b, len(p) - 1: len(p) - 1 + max_new].tolist()
+                  for b, p in enumerate(prompts)]
+        return tokens, seconds, (torch.stack(hist).cpu() if hist is not None else None)
+
+    # ------------------------------------------------------------ accounting
+    def weight_bytes_per_step(self, experts_touched: float) -> float:
+        """Algorithmic weight bytes of one step: every dense weight once, the
+        experts the step's sequences picked (their union per layer) once."""
+        cfg = self.cfg
+        H = cfg.hidden
+        total = 2 * cfg.vocab * H + 2 * H                     # head, final gamma, + one embedding row
+        for i in range(cfg.layers):
+            if cfg.is_full(i):
+                total += 2 * (cfg.attn_in * H + H * cfg.heads * cfg.head_dim + 2 * cfg.head_dim)
+            else:
+                total += 2 * (cfg.gdn_in * H + H * cfg.value_dim + cfg.conv_dim * cfg.conv_kernel
+                              + 2 * cfg.lin_value_heads + cfg.lin_value_dim)
+            total += 2 * (2 * H + cfg.experts * H + 3 * cfg.shared_inter * H + H)
+            total += experts_touched * 2 * 3 * cfg.moe_inter * H
+        return total
+
+    def state_bytes_per_step(self, positions) -> float:
+        """Recurrent state read and written, conv windows, KV read and written."""
+        cfg = self.cfg
+        gdn = sum(1 for i in range(cfg.layers) if not cfg.is_full(i))
+        full = cfg.layers - gdn
+        per_row = gdn * (2 * 4 * cfg.lin_value_heads * cfg.lin_key_dim * cfg.lin_value_dim +
+                         2 * 4 * cfg.conv_dim * (cfg.conv_kernel - 1))
+        kv = sum(full * 2 * 2 * cfg.kv_heads * cfg.head_dim * (p + 1) for p in positions)
+        return self.B * per_row + kv
+
+
+def ctypes_addr(struct) -> int:
+    import ctypes
+    return ctypes.addressof(struct)
