@@ -49,6 +49,16 @@ __device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-
 //            p_topk / sum p_topk (f32)
 //   kMode 1 (granite model.py:376-390): weights = bf16(softmax over the top k)
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ int wave_min_i(int v) {
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, kDppXor1, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, kDppXor2, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, kDppHalfMirror, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_update_dpp(0, v, kDppMirror, 0xF, 0xF, false));
+  v = min(v, __shfl_xor(v, 16, kWave));
+  const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  return min((int)r[0], (int)r[1]);
+}
+
 template <int kMode>
 __global__ __launch_bounds__(kWave) void k_route(const float* __restrict__ logits, int ldl, int E,
                                                  int k, float* __restrict__ weights,
@@ -62,8 +72,7 @@ __global__ __launch_bounds__(kWave) void k_route(const float* __restrict__ logit
     id[j] = e;
     v[j] = e < E ? logits[(int64_t)row * ldl + e] : kNegInf;
   }
-  float m = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
-  m = wave_max(m);
+  const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
   float sum_all = 0.f;
   if (kMode == 0) {
 #pragma unroll
@@ -75,29 +84,25 @@ __global__ __launch_bounds__(kWave) void k_route(const float* __restrict__ logit
   float my_val = kNegInf;
   int my_idx = 0;
   for (int r = 0; r < k; ++r) {
+    // this lane's best candidate (ids grow with j, so ties keep the first)
     float bv = kNegInf;
     int bi = 0x7fffffff;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (id[j] < E && !taken[j] && better(v[j], id[j], bv, bi)) {
+      if (id[j] < E && !taken[j] && (bi == 0x7fffffff || v[j] > bv)) {
         bv = v[j];
         bi = id[j];
       }
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) {
-      const float ob = __shfl_xor(bv, msk, kWave);
-      const int oi = __shfl_xor(bi, msk, kWave);
-      if (better(ob, oi, bv, bi)) {
-        bv = ob;
-        bi = oi;
-      }
-    }
+    // the wave's largest value, then the lowest id holding it
+    const float wm = wave_max(bv);
+    int pick = wave_min_i(bi != 0x7fffffff && bv == wm ? bi : 0x7fffffff);
+    if (pick == 0x7fffffff) pick = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (id[j] == bi) taken[j] = true;
+      if (id[j] == pick) taken[j] = true;
     if (lane == r) {
-      my_val = bv;
-      my_idx = bi;
+      my_val = wm;
+      my_idx = pick;
     }
   }
   // weights of the k picks, held by lanes 0..k-1
@@ -390,10 +395,20 @@ __global__ __launch_bounds__(kBlock) void k_moe_mix(MoeArgs a) {
   const int b = blockIdx.y, n = blockIdx.x * kBlock + threadIdx.x;
   if (n >= a.H) return;
   const float* pb = a.partial + (int64_t)b * (a.k + 1) * a.H + n;
+  const float* wb = a.weights + (int64_t)b * a.k;
   float acc = 0.f;
-  for (int s = 0; s < a.k; ++s) {
-    const float d = pb[(int64_t)s * a.H], wgt = a.weights[(int64_t)b * a.k + s];
-    acc += kF32 ? d * wgt : rbf(d * wgt);
+  constexpr int kBatch = 8;           // a batch's loads are all issued before the adds
+  for (int s0 = 0; s0 < a.k; s0 += kBatch) {
+    float d[kBatch], wg[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int s = s0 + i < a.k ? s0 + i : a.k - 1;
+      d[i] = pb[(int64_t)s * a.H];
+      wg[i] = wb[s];
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (s0 + i < a.k) acc += kF32 ? d[i] * wg[i] : rbf(d[i] * wg[i]);
   }
   const float dsh = pb[(int64_t)a.k * a.H];
   float* o = a.out + (int64_t)b * a.H + n;
@@ -728,7 +743,7 @@ __global__ __launch_bounds__(kBlock) void k_bf16_to_f32_rows(const bf16* __restr
 
 template <bool kFp8, bool kF32>
 int launch_moe(const MoeArgs& a, hipStream_t s) {
-  constexpr int kRgu = 4, kRdn = 8;
+  constexpr int kRgu = 1, kRdn = 2;     // small blocks: many per compute unit, even tails
   // picked experts at most min(E, B k), plus the shared one
   const int ny = (a.E < a.B * a.k ? a.E : a.B * a.k) + 1;
   const int im = a.I > a.IS ? a.I : a.IS;

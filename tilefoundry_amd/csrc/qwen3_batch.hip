@@ -833,11 +833,20 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
   if (kt > 0) {
     const int steps = K / 32 / 8;
     const dim3 grid((ntiles + kt - 1) / kt);
+    // fewer blocks than compute units: sixteen waves split K instead of eight,
+    // so each unit that has a tile keeps twice the loads in flight
+    const bool wide = (int)grid.x < compute_units() && (K / 32) % 16 == 0;
+    const int steps16 = K / 32 / 16;
 #define TFD_KSPLIT(EPI, KT, D)                                                                  \
   hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D>), grid, dim3(8 * kWave), 0, s, xb, wb, M, \
                      K, N, rb, ldr, out, ldo, nullptr)
+#define TFD_KSPLIT16(EPI, D)                                                                    \
+  hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 16, D>), grid, dim3(16 * kWave), 0, s, xb, wb, M, \
+                     K, N, rb, ldr, out, ldo, nullptr)
 #define TFD_KSPLIT_EPI(EPI)                              \
-  if (kt == 2 && steps % 8 == 0) TFD_KSPLIT(EPI, 2, 8);  \
+  if (wide && kt == 1 && steps16 % 8 == 0) TFD_KSPLIT16(EPI, 8); \
+  else if (wide && kt == 1 && steps16 % 4 == 0) TFD_KSPLIT16(EPI, 4); \
+  else if (kt == 2 && steps % 8 == 0) TFD_KSPLIT(EPI, 2, 8);  \
   else if (steps % 8 == 0) TFD_KSPLIT(EPI, 1, 8);        \
   else if (steps % 4 == 0) TFD_KSPLIT(EPI, 1, 4);        \
   else if (steps % 2 == 0) TFD_KSPLIT(EPI, 1, 2);        \
@@ -852,6 +861,7 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
         return fail(kBadArg, "gemm_skinny: epilogue %d", epilogue);
     }
 #undef TFD_KSPLIT_EPI
+#undef TFD_KSPLIT16
 #undef TFD_KSPLIT
     return launched("gemm_skinny");
   }
