@@ -208,6 +208,13 @@ int tfd_add_f32_rows(float* acc, int lda, const float* add, int ldb, int rows, i
 int tfd_bf16_to_f32_rows(const void* src, int lds, float* dst, int ldd, int rows, int n,
                          void* stream);
 
+/* C5's scaled residual and embedding (examples/granite_4_0_h_small-cuda/
+ * model.py:502-508 residual_add, :615-624 embed): out = bf16(a + bf16(b * m)) per
+ * element, a NULL `a` giving bf16(b * m); b is bf16 [rows][ldb], or f32 holding
+ * bf16 values with b_f32 != 0 (the experts' output).  out may alias a. */
+int tfd_scaled_add_rows(const void* a, int lda, const void* b, int ldb, int b_f32, float m,
+                        void* out, int ldo, int rows, int n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

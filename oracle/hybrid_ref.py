@@ -393,3 +393,87 @@ class Qwen35Oracle:
         self.route_gaps.append(gaps)
         hn = bf(_rms_flat(hidden, self.w["gamma_final"], c.eps))
         return bf(mm_rows(self.w["head"].float(), hn))
+
+
+# ---------------------------------------------------------------------------
+# Whole decode steps of the C5 model (HIR policy, fp8 linear weights)
+# ---------------------------------------------------------------------------
+def rms_norm_hir(x, gamma, eps):
+    """``tf.rms_norm`` at bf16 (Qwen3RMSNorm order): bf16(bf16(x * rsqrt(mean(x^2)
+    + eps)) * gamma), the variance in f32."""
+    x32 = x.float()
+    var = (x32 * x32).mean(dim=-1, keepdim=True)
+    return bf(bf(x32 * torch.rsqrt(var + eps)) * gamma.float())
+
+
+def _route_gap_ulps(rlog, k):
+    srt = rlog.sort(dim=-1, descending=True).values
+    kth = srt[:, k - 1].abs().clamp(min=2.0 ** -126)
+    return (srt[:, k - 1] - srt[:, k]) / torch.exp2(torch.floor(torch.log2(kth)) - 7)
+
+
+class GraniteOracle:
+    """``Granite4_0_H_Small``'s decode step for a batch (examples/
+    granite_4_0_h_small-cuda/model.py: embed :615-624, GraniteMamba :141-270,
+    GraniteAttention :273-366, GraniteMoE :392-477, the layers' scaled residual
+    :480-523, final norm and head :626-645) at the HIR's bf16 rounding, with every
+    linear weight fp8 codes + f32 row scales (``gemv_fp8``) and the tied table
+    bf16.  The head's ``/ logits_scaling`` (a power of two) is left out, as the
+    engine leaves it out.  Weights under the names
+    ``tilefoundry_amd.hybrid.granite`` uses, on the CPU."""
+
+    def __init__(self, cfg, weights: dict, rows: int):
+        self.cfg, self.w, self.B = cfg, weights, rows
+        c = cfg
+        self.conv = {i: torch.zeros(rows, c.conv_dim, c.conv_kernel - 1)
+                     for i in range(c.layers) if not c.is_attention(i)}
+        self.state = {i: torch.zeros(rows, c.mamba_heads, c.mamba_head_dim, c.d_state)
+                      for i in range(c.layers) if not c.is_attention(i)}
+        self.k_past = {i: [torch.zeros(0, c.kv_heads, c.head_dim)] * rows
+                       for i in range(c.layers) if c.is_attention(i)}
+        self.v_past = {i: [torch.zeros(0, c.kv_heads, c.head_dim)] * rows
+                       for i in range(c.layers) if c.is_attention(i)}
+        self.route_gaps: list[torch.Tensor] = []
+
+    def step(self, tokens) -> torch.Tensor:
+        c, B = self.cfg, self.B
+        E, I, H = c.experts, c.moe_inter, c.hidden
+        hidden = bf(self.w["embed"][torch.tensor(tokens)].float() * c.embedding_multiplier)
+        gaps = None
+        for i in range(c.layers):
+            W = lambda n: self.w[f"layer{i}.{n}"]
+            lin = lambda n, x: bf(gemv_fp8(W(n), W(n + "_scale"), x))
+            xn = rms_norm_hir(hidden, W("gamma_in"), c.eps)
+            if c.is_attention(i):
+                HQ, HKV, D = c.heads, c.kv_heads, c.head_dim
+                qkv = lin("w_in", xn)
+                q = qkv[:, :HQ * D].reshape(B, HQ, D)
+                k = qkv[:, HQ * D:(HQ + HKV) * D].reshape(B, HKV, D)
+                v = qkv[:, (HQ + HKV) * D:(HQ + 2 * HKV) * D].reshape(B, HKV, D)
+                att = granite_attend(q, k, v, self.k_past[i], self.v_past[i],
+                                     c.attention_multiplier)
+                self.k_past[i] = [torch.cat((self.k_past[i][b], k[b][None])) for b in range(B)]
+                self.v_past[i] = [torch.cat((self.v_past[i][b], v[b][None])) for b in range(B)]
+                mixed = lin("w_out", att)
+            else:
+                proj = lin("w_in", xn)
+                normed, self.conv[i], self.state[i] = mamba_step(
+                    proj, self.conv[i], self.state[i], W("conv_w"), W("conv_b"), W("a_log"),
+                    W("dt_bias"), W("d_skip"), W("gamma_ssm"), nh=c.mamba_heads,
+                    pd=c.mamba_head_dim, ns=c.d_state, ng=1, eps=c.eps)
+                mixed = lin("w_out", normed)
+            hidden = bf(hidden + bf(mixed * c.residual_multiplier))
+            xm = rms_norm_hir(hidden, W("gamma_post"), c.eps)
+            rlog = lin("w_router", xm)
+            gap = _route_gap_ulps(rlog, c.top_k)
+            gaps = gap if gaps is None else torch.minimum(gaps, gap)
+            rw, ridx = route_topk_softmax(rlog, c.top_k)
+            moe = moe_c5(xm, rw, ridx, W("w_gate").view(E, I, H), W("s_gate").view(E, I),
+                         W("w_up").view(E, I, H), W("s_up").view(E, I),
+                         W("w_down").view(E, H, I), W("s_down").view(E, H),
+                         W("w_shared_in"), W("w_shared_in_scale"), W("w_shared_out"),
+                         W("w_shared_out_scale"))
+            hidden = bf(hidden + bf(moe * c.residual_multiplier))
+        self.route_gaps.append(gaps)
+        hn = rms_norm_hir(hidden, self.w["gamma_final"], c.eps)
+        return bf(mm_rows(self.w["embed"].float(), hn))

@@ -72,6 +72,7 @@ SIGNATURES: dict[str, list] = {
     "tfd_rmsnorm_f32_rows": [P, I, P, P, I, P, I, I, F, P],
     "tfd_add_f32_rows": [P, I, P, I, I, I, P],
     "tfd_bf16_to_f32_rows": [P, I, P, I, I, I, P],
+    "tfd_scaled_add_rows": [P, I, P, I, I, F, P, I, I, I, P],
 }
 RESTYPES = {"tfd_last_error": ctypes.c_char_p}
 UNCHECKED = {"tfd_abi_version", "tfd_decode_persistent_grid"}

@@ -739,6 +739,23 @@ __global__ __launch_bounds__(kBlock) void k_bf16_to_f32_rows(const bf16* __restr
   if (i < n) dst[(int64_t)b * ldd + i] = bf2f(src[(int64_t)b * lds + i]);
 }
 
+// Granite's scaled residual (model.py:502-508, 519-523): out = a + b * m with
+// bf16 ops (the product rounded, then the sum); a NULL `a` gives bf16(b * m)
+// (the embedding times embedding_multiplier, :615-624).  b is bf16, or f32
+// holding bf16 values (the experts' output).
+__global__ __launch_bounds__(kBlock) void k_scaled_add_rows(const bf16* __restrict__ a, int lda,
+                                                            const void* __restrict__ b, int ldb,
+                                                            int b_f32, float m,
+                                                            bf16* __restrict__ out, int ldo,
+                                                            int n) {
+  const int r = blockIdx.y, i = blockIdx.x * kBlock + threadIdx.x;
+  if (i >= n) return;
+  const float bv = b_f32 ? ((const float*)b)[(int64_t)r * ldb + i]
+                         : bf2f(((const bf16*)b)[(int64_t)r * ldb + i]);
+  const float p = rbf(bv * m);
+  out[(int64_t)r * ldo + i] = f2bf(a ? bf2f(a[(int64_t)r * lda + i]) + p : p);
+}
+
 }  // namespace
 
 template <bool kFp8, bool kF32>
@@ -940,6 +957,17 @@ int tfd_bf16_to_f32_rows(const void* src, int lds, float* dst, int ldd, int rows
   hipLaunchKernelGGL(k_bf16_to_f32_rows, dim3((n + kBlock - 1) / kBlock, rows), dim3(kBlock), 0,
                      (hipStream_t)stream, (const bf16*)src, lds, dst, ldd, n);
   return launched("bf16_to_f32_rows");
+}
+
+int tfd_scaled_add_rows(const void* a, int lda, const void* b, int ldb, int b_f32, float m,
+                        void* out, int ldo, int rows, int n, void* stream) {
+  if (!b || !out) return fail(kBadArg, "scaled_add: null pointer");
+  if (rows <= 0 || n <= 0 || (a && lda < n) || ldb < n || ldo < n)
+    return fail(kBadShape, "scaled_add: rows=%d n=%d", rows, n);
+  hipLaunchKernelGGL(k_scaled_add_rows, dim3((n + kBlock - 1) / kBlock, rows), dim3(kBlock), 0,
+                     (hipStream_t)stream, (const bf16*)a, lda, b, ldb, b_f32, m, (bf16*)out, ldo,
+                     n);
+  return launched("scaled_add_rows");
 }
 
 }  // extern "C"

@@ -2,6 +2,7 @@
 
     python -m tilefoundry_amd.hybrid.bench [--config c4|c4b16|c5|all] [--reps 20]
     python -m tilefoundry_amd.hybrid.bench --config c4-step --rows 1|16 [--steps 256]
+    python -m tilefoundry_amd.hybrid.bench --config c5-step --rows 8 [--steps 256]
 
 Every kernel runs at its workload's shapes on synthetic data (seeded) with the
 launches of one measurement captured in a HIP graph and replayed; HIP events on
@@ -358,19 +359,58 @@ def bench_c4_step(rows: int, steps: int, prompt: int = 32) -> dict:
     return out
 
 
+def bench_c5_step(rows: int, steps: int, ctx: int = 8192) -> dict:
+    """Whole C5 decode steps (Granite-4.0-H-style, 40 layers, fp8 weights, batch
+    `rows`) after a `ctx`-token context per sequence that is drawn at random into
+    the caches and states rather than walked (GraniteEngine.synthetic_context:
+    the work of each later step is that of a real context of that length)."""
+    from .granite import GraniteConfig, GraniteEngine, synthetic_weights
+
+    cfg = GraniteConfig()
+    t0 = time.perf_counter()
+    w = synthetic_weights(cfg, seed=0, device=DEV)
+    eng = GraniteEngine(cfg, w, rows=rows, device=DEV, max_steps=ctx + steps + 32)
+    eng.synthetic_context(ctx)
+    for _ in range(4):
+        eng.replay()
+    torch.cuda.synchronize()
+    print(f"[bench] c5 weights + engine + capture {time.perf_counter() - t0:.1f}s", flush=True)
+    t1 = time.perf_counter()
+    for _ in range(steps):
+        eng.replay()
+    torch.cuda.synchronize()
+    seconds = time.perf_counter() - t1
+    eng.check_errors()
+    touched = len(set(eng.ridx.reshape(-1).tolist()))
+    wbytes = eng.weight_bytes_per_step(touched)
+    positions = range(ctx + 4, ctx + 4 + steps)
+    sbytes = sum(eng.state_bytes_per_step([p] * rows) for p in positions) / steps
+    step_s = seconds / steps
+    out = {"config": f"c5 step b{rows} ctx{ctx}", "tok_s": round(rows * steps / seconds, 1),
+           "ms_per_step": round(step_s * 1e3, 4), "steps": steps,
+           "bytes_per_step": int(wbytes + sbytes), "experts_touched_sample": touched,
+           "GB/s": round((wbytes + sbytes) / step_s / 1e9, 1),
+           "frac": round((wbytes + sbytes) / step_s / HBM_PEAK, 4)}
+    print(json.dumps(out), flush=True)
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--config", default="all",
-                    choices=("c4", "c4b16", "c5", "all", "c4-step"))
+                    choices=("c4", "c4b16", "c5", "all", "c4-step", "c5-step"))
     ap.add_argument("--reps", type=int, default=20)
-    ap.add_argument("--rows", type=int, default=1, help="c4-step: sequences per step")
-    ap.add_argument("--steps", type=int, default=256, help="c4-step: timed steps")
+    ap.add_argument("--rows", type=int, default=1, help="c4-step / c5-step: sequences")
+    ap.add_argument("--steps", type=int, default=256, help="c4-step / c5-step: timed steps")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         raise SystemExit("hybrid kernel bench: no GPU visible")
     if args.config == "c4-step":
         bench_c4_step(args.rows, args.steps)
+        return 0
+    if args.config == "c5-step":
+        bench_c5_step(args.rows, args.steps)
         return 0
     for c in (("c4", "c4b16", "c5") if args.config == "all" else (args.config,)):
         run(c, args.reps)

@@ -1,0 +1,486 @@
+"""Granite-4.0-H-style hybrid decode on the GPU (workload C5).
+
+The decode step of ``examples/granite_4_0_h_small-cuda/model.py``
+(``Granite4_0_H_Small``: Mamba2 and GQA layers, each followed by a top-10 MoE
+with a shared MLP) at the arithmetic of the authored HIR: a bf16 residual
+stream, every bf16 op rounded as written, f32 where the HIR casts.  The linear
+weights are fp8-e4m3fn with one f32 scale per output row (the workload's
+per-channel fp8); the tied embedding / head table stays bf16.  Per layer:
+
+* input RMSNorm (operand order) -> fp8 in-projection -> Mamba2 step
+  (``tfd_mamba_step``) or GQA decode (``tfd_gqa_decode``, no RoPE) -> fp8
+  out-projection -> ``a + b * residual_multiplier`` (``tfd_scaled_add_rows``);
+* post RMSNorm -> fp8 router -> top-10 then softmax (``tfd_route_topk``) ->
+  routed experts + shared MLP (``tfd_moe_experts``, fp8, expert-grouped) -> the
+  scaled residual again;
+
+then the final norm, the head over the tied table, the greedy pick and the next
+token's embedding times ``embedding_multiplier``.  The head's division by
+``logits_scaling`` (16, a power of two: exact in bf16 and order-preserving) is
+left out of the logits buffer; the pick is the same.  Sequences (up to 32) step
+together; a step is recorded into two HIP graphs (the conv windows ping-pong).
+Weights are synthetic (random init on the device).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from time import perf_counter
+
+import torch
+
+from .. import _lib
+from .._lib import lib, ptr
+from .qwen3_5 import ctypes_addr
+
+BF = torch.bfloat16
+F32 = torch.float32
+I32 = torch.int32
+
+
+@dataclass(frozen=True)
+class GraniteConfig:
+    """Workload C5's shape; attention layers at the
+    published ``layer_types`` positions (examples/granite_4_0_h_small-cuda/
+    config.json), multipliers as published there."""
+
+    hidden: int = 4096
+    layers: int = 40
+    attention_layers: tuple = (5, 15, 25, 35)
+    mamba_heads: int = 64
+    mamba_head_dim: int = 64
+    d_state: int = 128
+    conv_kernel: int = 4
+    heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    experts: int = 72
+    top_k: int = 10
+    moe_inter: int = 768
+    shared_inter: int = 1536
+    vocab: int = 100352
+    eps: float = 1e-5
+    embedding_multiplier: float = 12.0
+    residual_multiplier: float = 0.22
+    attention_multiplier: float = 0.0078125
+    logits_scaling: float = 16.0
+
+    def is_attention(self, i: int) -> bool:
+        return i in self.attention_layers
+
+    @property
+    def d_inner(self) -> int:
+        return self.mamba_heads * self.mamba_head_dim
+
+    @property
+    def conv_dim(self) -> int:
+        return self.d_inner + 2 * self.d_state
+
+    @property
+    def mamba_in(self) -> int:
+        """Rows of in_proj: gate, conv channels (x|B|C), dt."""
+        return self.d_inner + self.conv_dim + self.mamba_heads
+
+    @property
+    def attn_in(self) -> int:
+        return (self.heads + 2 * self.kv_heads) * self.head_dim
+
+
+def _fp8(N, K, g, device, std):
+    """e4m3fn codes of N(0, 1) draws and a per-row scale near `std`."""
+    codes = torch.randn(N, K, generator=g, device=device).to(torch.float8_e4m3fn).view(torch.uint8)
+    scale = std * (0.9 + 0.2 * torch.rand(N, generator=g, device=device))
+    return codes, scale
+
+
+def synthetic_weights(cfg: GraniteConfig, seed: int = 0, device: str = "cuda:0",
+                      std: float = 0.02) -> dict[str, torch.Tensor]:
+    """Random-init weights: every linear weight fp8 codes + f32 row scales with
+    values near N(0, std); norm scales 1 + N(0, std); the bf16 table N(0, std);
+    conv, A_log, dt_bias, D small normal draws."""
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def rn(*shape, s=std):
+        return (torch.randn(*shape, generator=g, device=device) * s).to(BF)
+
+    def gamma(n):
+        return (1 + torch.randn(n, generator=g, device=device) * std).to(BF)
+
+    H, E, I, IS = cfg.hidden, cfg.experts, cfg.moe_inter, cfg.shared_inter
+    w = {"embed": rn(cfg.vocab, H), "gamma_final": gamma(H)}
+
+    def lin(name, N, K):
+        w[name], w[name + "_scale"] = _fp8(N, K, g, device, std)
+
+    for i in range(cfg.layers):
+        p = f"layer{i}."
+        w[p + "gamma_in"] = gamma(H)
+        if cfg.is_attention(i):
+            lin(p + "w_in", cfg.attn_in, H)
+            lin(p + "w_out", H, cfg.heads * cfg.head_dim)
+        else:
+            lin(p + "w_in", cfg.mamba_in, H)
+            w[p + "conv_w"] = rn(cfg.conv_dim, cfg.conv_kernel, s=0.5)
+            w[p + "conv_b"] = rn(cfg.conv_dim, s=0.1)
+            w[p + "a_log"] = rn(cfg.mamba_heads, s=0.5)
+            w[p + "dt_bias"] = rn(cfg.mamba_heads, s=0.5)
+            w[p + "d_skip"] = rn(cfg.mamba_heads, s=1.0)
+            w[p + "gamma_ssm"] = gamma(cfg.d_inner)
+            lin(p + "w_out", H, cfg.d_inner)
+        w[p + "gamma_post"] = gamma(H)
+        lin(p + "w_router", E, H)
+        w[p + "w_gate"], w[p + "s_gate"] = _fp8(E * I, H, g, device, std)
+        w[p + "w_up"], w[p + "s_up"] = _fp8(E * I, H, g, device, std)
+        w[p + "w_down"], w[p + "s_down"] = _fp8(E * H, I, g, device, std)
+        lin(p + "w_shared_in", 2 * IS, H)
+        lin(p + "w_shared_out", H, IS)
+    return w
+
+
+class GraniteEngine:
+    """A Granite-style hybrid decoder stepping `rows` sequences together."""
+
+    def __init__(self, cfg: GraniteConfig, weights: dict[str, torch.Tensor], *, rows: int,
+                 device: str = "cuda:0", max_steps: int = 1024, page_seed: int = 0,
+                 split_len: int = 256, graph: bool = True):
+        if not 1 <= rows <= 32:
+            raise ValueError("rows: 1..32 sequences")
+        self.cfg, self.B, self.device = cfg, rows, device
+        self._lib = lib()
+        self.nsteps = max_steps
+        self.split_len = split_len
+        self._pack(weights)
+        self._buffers(page_seed)
+        self.graphs = None
+        self._cur = 0
+        if graph:
+            self._capture()
+
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _packed8(self, codes: torch.Tensor) -> torch.Tensor:
+        N, K = codes.shape
+        out = torch.empty(-(-N // 16) * 16 * K, dtype=torch.uint8, device=self.device)
+        self._lib.tfd_pack_skinny_fp8(ptr(codes), K, N, K, ptr(out), self._stream())
+        return out
+
+    def _pack(self, w):
+        cfg = self.cfg
+        self.layers = []
+        for i in range(cfg.layers):
+            p = f"layer{i}."
+            d = {k[len(p):]: v for k, v in w.items() if k.startswith(p)}
+            for name in ("w_in", "w_out", "w_router"):
+                d[name] = self._packed8(d[name])
+            self.layers.append(d)
+        self.embed = w["embed"]
+        self.gamma_final = w["gamma_final"]
+        N, K = self.embed.shape
+        self.head = torch.empty(-(-N // 16) * 16 * K, dtype=BF, device=self.device)
+        self._lib.tfd_pack_skinny_bf16(ptr(self.embed), K, N, K, ptr(self.head), self._stream())
+        torch.cuda.synchronize(self.device)
+
+    def _buffers(self, page_seed):
+        cfg, B, dev = self.cfg, self.B, self.device
+        H, V, k = cfg.hidden, cfg.vocab, cfg.top_k
+
+        def z(*shape, dtype=F32):
+            return torch.zeros(*shape, dtype=dtype, device=dev)
+
+        self.hidden = z(B, H, dtype=BF)
+        self.emb = z(B, H, dtype=BF)
+        self.xn = z(32 * H, dtype=BF)
+        self.xm = z(B, H, dtype=BF)
+        self.nproj = max(cfg.mamba_in, cfg.attn_in)
+        self.nproj += (-self.nproj) % 8
+        self.proj = z(B, self.nproj, dtype=BF)
+        self.mix = z(32 * max(cfg.d_inner, cfg.heads * cfg.head_dim), dtype=BF)
+        self.tmp = z(B, H, dtype=BF)
+        self.moe_out = z(B, H)
+        self.rlog = z(B, cfg.experts)
+        self.rw = z(B, k)
+        self.ridx = z(B, k, dtype=I32)
+        ld = max(cfg.moe_inter, cfg.shared_inter)
+        self.moe_hidden = z(B, k + 1, ld, dtype=BF)
+        self.moe_sscale = z(B)
+        self.moe_partial = z(B, k + 1, H)
+        self.moe_groups = z(_lib.moe_group_words(cfg.experts, B), dtype=I32)
+        self.moe_ld = ld
+        self.state, self.conv = {}, {}
+        for i in range(cfg.layers):
+            if not cfg.is_attention(i):
+                self.state[i] = z(B, cfg.mamba_heads, cfg.mamba_head_dim, cfg.d_state)
+                self.conv[i] = (z(B, cfg.conv_dim, cfg.conv_kernel - 1, dtype=BF),
+                                z(B, cfg.conv_dim, cfg.conv_kernel - 1, dtype=BF))
+        self.gated = z(B, cfg.d_inner)
+        self.ssq = z(B, cfg.mamba_heads)
+        self.max_pages = -(-self.nsteps // 16)
+        self.num_pages = B * self.max_pages
+        gen = torch.Generator().manual_seed(page_seed)
+        self.page_table = torch.randperm(self.num_pages, generator=gen).view(
+            B, self.max_pages).to(I32).to(dev)
+        self.kpool, self.vpool = {}, {}
+        for i in range(cfg.layers):
+            if cfg.is_attention(i):
+                shape = (self.num_pages, cfg.kv_heads, 16, cfg.head_dim)
+                self.kpool[i] = z(*shape, dtype=BF)
+                self.vpool[i] = z(*shape, dtype=BF)
+        self.nsplit = -(-self.max_pages * 16 // self.split_len)
+        self.stride = self.max_pages * 16
+        self.scores = z(B * cfg.heads * self.stride)
+        self.stats = z(B * cfg.heads * self.nsplit * 2)
+        self.part = z(B * cfg.heads * self.nsplit * cfg.head_dim)
+        self.counters = z(B * cfg.kv_heads, dtype=I32)
+        self.logits = z(B, V)
+        self.pick = z(B, dtype=I32)
+        self.argmax_work = z(B * _lib.ARGMAX_WORK, dtype=I32)
+        self.ids = z(B, dtype=torch.int64)
+        self.pos = z(B, dtype=I32)
+        self.inp = z(B, self.nsteps, dtype=I32)
+        self.plen = z(B, dtype=I32)
+        self.sam = z(B, self.nsteps, dtype=I32)
+        self.err = z(1, dtype=I32)
+        self.work = z(1 << 21)
+
+    # ------------------------------------------------------------------ step
+    def _gemm8(self, x, w, scale, K, N, epi, out, ldo, s):
+        self._lib.tfd_gemm_skinny_fp8(ptr(x), ptr(w), ptr(scale), self.B, K, N, epi, None, 0,
+                                      ptr(out), ldo, s)
+
+    def _residual(self, b, b_f32, s):
+        """hidden = bf16(hidden + bf16(b * residual_multiplier))."""
+        H = self.cfg.hidden
+        self._lib.tfd_scaled_add_rows(ptr(self.hidden), H, ptr(b), H, b_f32,
+                                      self.cfg.residual_multiplier, ptr(self.hidden), H, self.B,
+                                      H, s)
+
+    def _mamba(self, i, w, s, cur):
+        cfg = self.cfg
+        a = _lib.TfdMambaArgs()
+        cin, cout = self.conv[i][cur], self.conv[i][1 - cur]
+        a.proj, a.proj_ld, a.conv_in, a.conv_out = ptr(self.proj), self.nproj, ptr(cin), ptr(cout)
+        a.state = ptr(self.state[i])
+        a.conv_w, a.conv_b = ptr(w["conv_w"]), ptr(w["conv_b"])
+        a.a_log, a.dt_bias, a.d_skip = ptr(w["a_log"]), ptr(w["dt_bias"]), ptr(w["d_skip"])
+        a.gamma, a.gated, a.ssq, a.out = ptr(w["gamma_ssm"]), ptr(self.gated), ptr(self.ssq), \
+            ptr(self.mix)
+        a.rows, a.heads, a.head_dim, a.state_dim = self.B, cfg.mamba_heads, cfg.mamba_head_dim, \
+            cfg.d_state
+        a.groups, a.conv_kernel, a.eps = 1, cfg.conv_kernel, cfg.eps
+        self._lib.tfd_mamba_step(ctypes_addr(a), s)
+
+    def _attn(self, i, s):
+        cfg = self.cfg
+        a = _lib.TfdGqaArgs()
+        a.qkv, a.ldq = ptr(self.proj), self.nproj
+        a.pos, a.page_table, a.max_pages = ptr(self.pos), ptr(self.page_table), self.max_pages
+        a.k_pool, a.v_pool, a.num_pages = ptr(self.kpool[i]), ptr(self.vpool[i]), self.num_pages
+        a.rows, a.heads, a.kv_heads, a.head_dim = self.B, cfg.heads, cfg.kv_heads, cfg.head_dim
+        a.scale, a.eps = cfg.attention_multiplier, cfg.eps
+        a.scores, a.score_stride, a.stats, a.part = ptr(self.scores), self.stride, \
+            ptr(self.stats), ptr(self.part)
+        a.counters, a.nsplit, a.split_len = ptr(self.counters), self.nsplit, self.split_len
+        a.out, a.policy, a.err = ptr(self.mix), _lib.POLICY_BF16, ptr(self.err)
+        self._lib.tfd_gqa_decode(ctypes_addr(a), s)
+
+    def _moe(self, w, s):
+        cfg = self.cfg
+        a = _lib.TfdMoeArgs()
+        a.x, a.weights, a.idx = ptr(self.xm), ptr(self.rw), ptr(self.ridx)
+        a.w_gate, a.w_up, a.w_down = ptr(w["w_gate"]), ptr(w["w_up"]), ptr(w["w_down"])
+        a.s_gate, a.s_up, a.s_down = ptr(w["s_gate"]), ptr(w["s_up"]), ptr(w["s_down"])
+        a.w_shared_in, a.w_shared_out = ptr(w["w_shared_in"]), ptr(w["w_shared_out"])
+        a.s_shared_in, a.s_shared_out = ptr(w["w_shared_in_scale"]), ptr(w["w_shared_out_scale"])
+        a.hidden, a.shared_scale, a.partial = ptr(self.moe_hidden), ptr(self.moe_sscale), \
+            ptr(self.moe_partial)
+        a.groups, a.out = ptr(self.moe_groups), ptr(self.moe_out)
+        a.rows, a.k, a.experts, a.hidden_size = self.B, cfg.top_k, cfg.experts, cfg.hidden
+        a.inter, a.shared_inter, a.hidden_ld = cfg.moe_inter, cfg.shared_inter, self.moe_ld
+        a.fp8, a.policy, a.err = 1, _lib.POLICY_BF16, ptr(self.err)
+        self._lib.tfd_moe_experts(ctypes_addr(a), s)
+
+    def _layer(self, i, s, cur):
+        cfg, L, w, B, H = self.cfg, self._lib, self.layers[i], self.B, self.cfg.hidden
+        L.tfd_rmsnorm_rows_bf16(ptr(self.hidden), H, ptr(w["gamma_in"]), ptr(self.xn), 0, B, H,
+                                cfg.eps, 1, s)
+        if cfg.is_attention(i):
+            self._gemm8(self.xn, w["w_in"], w["w_in_scale"], H, cfg.attn_in, _lib.EPI_STORE,
+                        self.proj, self.nproj, s)
+            self._attn(i, s)
+            self._gemm8(self.mix, w["w_out"], w["w_out_scale"], cfg.heads * cfg.head_dim, H,
+                        _lib.EPI_STORE, self.tmp, H, s)
+        else:
+            self._gemm8(self.xn, w["w_in"], w["w_in_scale"], H, cfg.mamba_in, _lib.EPI_STORE,
+                        self.proj, self.nproj, s)
+            self._mamba(i, w, s, cur)
+            self._gemm8(self.mix, w["w_out"], w["w_out_scale"], cfg.d_inner, H, _lib.EPI_STORE,
+                        self.tmp, H, s)
+        self._residual(self.tmp, 0, s)
+        L.tfd_rmsnorm_rows_bf16(ptr(self.hidden), H, ptr(w["gamma_post"]), ptr(self.xn), 0, B, H,
+                                cfg.eps, 1, s)
+        L.tfd_rmsnorm_rows_bf16(ptr(self.hidden), H, ptr(w["gamma_post"]), ptr(self.xm), H, B, H,
+                                cfg.eps, 0, s)
+        self._gemm8(self.xn, w["w_router"], w["w_router_scale"], H, cfg.experts,
+                    _lib.EPI_LOGITS, self.rlog, cfg.experts, s)
+        L.tfd_route_topk(ptr(self.rlog), cfg.experts, B, cfg.experts, cfg.top_k,
+                         _lib.ROUTE_TOPK_SOFTMAX, ptr(self.rw), ptr(self.ridx), s)
+        self._moe(w, s)
+        self._residual(self.moe_out, 1, s)
+
+    def _step(self, cur):
+        s = self._stream()
+        cfg, L, B, H, V = self.cfg, self._lib, self.B, self.cfg.hidden, self.cfg.vocab
+        L.tfd_scaled_add_rows(None, 0, ptr(self.emb), H, 0, cfg.embedding_multiplier,
+                              ptr(self.hidden), H, B, H, s)
+        for i in range(cfg.layers):
+            self._layer(i, s, cur)
+        L.tfd_rmsnorm_rows_bf16(ptr(self.hidden), H, ptr(self.gamma_final), ptr(self.xn), 0, B,
+                                H, cfg.eps, 1, s)
+        L.tfd_gemm_skinny_bf16(ptr(self.xn), ptr(self.head), B, H, V, _lib.EPI_LOGITS, None, 0,
+                               ptr(self.logits), V, ptr(self.work), self.work.numel(), s)
+        L.tfd_argmax_rows(ptr(self.logits), V, B, V, ptr(self.pick), ptr(self.argmax_work), s)
+        L.tfd_finalize_rows(ptr(self.pick), B, ptr(self.inp), self.nsteps, ptr(self.plen),
+                            ptr(self.ids), ptr(self.pos), ptr(self.sam), self.nsteps,
+                            self.nsteps, ptr(self.embed), ptr(self.emb), H, H, V, ptr(self.err),
+                            s)
+
+    def _capture(self):
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self._load_prompts([[0]] * self.B)
+            for cur in (0, 1):
+                self._step(cur)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graphs = []
+        for cur in (0, 1):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._step(cur)
+            self.graphs.append(g)
+        torch.cuda.synchronize(self.device)
+        self._reset()
+
+    def replay(self):
+        if self.graphs is not None:
+            self.graphs[self._cur].replay()
+        else:
+            self._step(self._cur)
+        self._cur ^= 1
+
+    # ------------------------------------------------------------- generation
+    def _reset(self):
+        self.pos.zero_()
+        self.sam.zero_()
+        self.err.zero_()
+        self.counters.zero_()
+        for i in self.state:
+            self.state[i].zero_()
+            self.conv[i][0].zero_()
+            self.conv[i][1].zero_()
+        self._cur = 0
+
+    def _load_prompts(self, prompts):
+        self._reset()
+        self.inp.zero_()
+        self.plen.copy_(torch.tensor([len(p) for p in prompts], dtype=I32))
+        for b, p in enumerate(prompts):
+            self.inp[b, :len(p)] = torch.tensor(p, dtype=I32).to(self.device)
+        self.ids.copy_(torch.tensor([p[0] for p in prompts], dtype=torch.int64))
+        self._lib.tfd_embed_rows_bf16(ptr(self.embed), ptr(self.ids), ptr(self.emb),
+                                      self.cfg.hidden, self.B, self.cfg.hidden, self.cfg.vocab,
+                                      ptr(self.err), self._stream())
+
+    def synthetic_context(self, ctx: int, seed: int = 0):
+        """Stand in for a walked `ctx`-token context without walking it: every
+        sequence's first `ctx` cache rows, conv windows and SSM states are drawn at
+        random, and decoding continues at position `ctx` from a random token.  The
+        work of every later step is that of a real `ctx`-token context."""
+        if ctx + 1 > self.nsteps:
+            raise ValueError(f"context {ctx} exceeds this engine's {self.nsteps} positions")
+        self._reset()
+        g = torch.Generator(device=self.device).manual_seed(seed)
+        for i in self.kpool:
+            self.kpool[i].copy_(torch.randn(self.kpool[i].shape, generator=g,
+                                            device=self.device).to(BF))
+            self.vpool[i].copy_(torch.randn(self.vpool[i].shape, generator=g,
+                                            device=self.device).to(BF))
+        for i in self.state:
+            self.state[i].copy_(torch.randn(self.state[i].shape, generator=g,
+                                            device=self.device) * 0.1)
+            self.conv[i][0].copy_(torch.randn(self.conv[i][0].shape, generator=g,
+                                              device=self.device).to(BF))
+        self.pos.fill_(ctx)
+        self.plen.fill_(1)
+        ids = torch.randint(0, self.cfg.vocab, (self.B,), generator=g, device=self.device)
+        self.ids.copy_(ids)
+        self._lib.tfd_embed_rows_bf16(ptr(self.embed), ptr(self.ids), ptr(self.emb),
+                                      self.cfg.hidden, self.B, self.cfg.hidden, self.cfg.vocab,
+                                      ptr(self.err), self._stream())
+
+    def check_errors(self):
+        e = int(self.err.item())
+        if e:
+            raise RuntimeError(f"hybrid decode kernels raised error bits {e:#x}")
+
+    def generate(self, prompts: list[list[int]], max_new: int, record_logits: bool = False):
+        """Walk every prompt and continue for *max_new* greedy tokens per sequence
+        (the walk untimed) -> (tokens per sequence, seconds, logits per step)."""
+        if len(prompts) != self.B or any(len(p) < 1 for p in prompts):
+            raise ValueError(f"need {self.B} non-empty prompts")
+        longest = max(len(p) for p in prompts)
+        if longest + max_new > self.nsteps:
+            raise ValueError(f"prompt {longest} + {max_new} exceeds {self.nsteps} steps")
+        self._load_prompts(prompts)
+        steps = longest - 1 + max_new
+        hist = [] if record_logits else None
+        torch.cuda.synchronize(self.device)
+        for _ in range(longest - 1):
+            self.replay()
+            if hist is not None:
+                hist.append(self.logits.clone())
+        torch.cuda.synchronize(self.device)
+        t0 = perf_counter()
+        for _ in range(longest - 1, steps):
+            self.replay()
+            if hist is not None:
+                hist.append(self.logits.clone())
+        torch.cuda.synchronize(self.device)
+        seconds = perf_counter() - t0
+        self.check_errors()
+        sam = self.sam.cpu()
+        tokens = [sam[b, len(p) - 1: len(p) - 1 + max_new].tolist()
+                  for b, p in enumerate(prompts)]
+        return tokens, seconds, (torch.stack(hist).cpu() if hist is not None else None)
+
+    # ------------------------------------------------------------ accounting
+    def weight_bytes_per_step(self, experts_touched: float) -> float:
+        """fp8 weights (1 byte each, 4 bytes per row scale) once, the experts picked
+        (their union per layer) once, the bf16 head table once."""
+        cfg, H = self.cfg, self.cfg.hidden
+
+        def lin(n, k):
+            return n * k + 4 * n
+
+        total = 2 * cfg.vocab * H + 2 * H
+        for i in range(cfg.layers):
+            if cfg.is_attention(i):
+                total += lin(cfg.attn_in, H) + lin(H, cfg.heads * cfg.head_dim)
+            else:
+                total += (lin(cfg.mamba_in, H) + lin(H, cfg.d_inner) +
+                          2 * (cfg.conv_dim * (cfg.conv_kernel + 1) + 3 * cfg.mamba_heads +
+                               cfg.d_inner))
+            total += 2 * 2 * H + lin(cfg.experts, H)
+            total += lin(2 * cfg.shared_inter, H) + lin(H, cfg.shared_inter)
+            total += experts_touched * (2 * lin(cfg.moe_inter, H) + lin(H, cfg.moe_inter))
+        return total
+
+    def state_bytes_per_step(self, positions) -> float:
+        cfg = self.cfg
+        mamba = sum(1 for i in range(cfg.layers) if not cfg.is_attention(i))
+        attn = cfg.layers - mamba
+        per_row = mamba * (2 * 4 * cfg.mamba_heads * cfg.mamba_head_dim * cfg.d_state +
+                           2 * 2 * cfg.conv_dim * (cfg.conv_kernel - 1))
+        kv = sum(attn * 2 * 2 * cfg.kv_heads * cfg.head_dim * (p + 1) for p in positions)
+        return self.B * per_row + kv
