@@ -347,10 +347,17 @@ __global__ __launch_bounds__(kBlock) void k_moe_gateup(MoeArgs a) {
   }
 }
 
-template <bool kFp8, int kC, int kR>
+// The down projections are short rows (K = the expert width): sixteen lanes
+// share a row (16-byte chunks c = l % 16 + 16 i), a wave holds four rows per
+// pass and kP passes, and a row's sum needs only the in-row DPP steps.
+constexpr int kDownLanes = 16;
+template <bool kFp8, int kC, int kP>
 __global__ __launch_bounds__(kBlock) void k_moe_down(MoeArgs a) {
   using WC = WChunk<kFp8>;
+  constexpr int kRpp = kWave / kDownLanes;        // rows per pass
+  constexpr int kR = kRpp * kP;                   // rows per wave
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int li = lane % kDownLanes, rsub = lane / kDownLanes;
   Group g;
   if (!moe_group(a, g)) return;
   const int K = g.shared ? a.IS : a.I;
@@ -359,33 +366,40 @@ __global__ __launch_bounds__(kBlock) void k_moe_down(MoeArgs a) {
   if (n0 >= a.H) return;
   const void* w = g.shared ? a.w_sout : a.w_down;
   const int64_t base = g.shared ? 0 : (int64_t)g.e * a.H;
-  typename WC::T dw[kR][kC];
-  float ds[kR];
+  typename WC::T dw[kP][kC];
+  float ds[kP];
 #pragma unroll
-  for (int r = 0; r < kR; ++r) {
-    const int row = n0 + r < a.H ? n0 + r : a.H - 1;
+  for (int p = 0; p < kP; ++p) {
+    const int n = n0 + p * kRpp + rsub;
+    const int row = n < a.H ? n : a.H - 1;
 #pragma unroll
     for (int i = 0; i < kC; ++i) {
-      const int c = lane + kWave * i < nch ? lane + kWave * i : 0;
-      dw[r][i] = WC::load(w, base + row, K, c);
+      const int c = li + kDownLanes * i < nch ? li + kDownLanes * i : 0;
+      dw[p][i] = WC::load(w, base + row, K, c);
     }
-    if (kFp8) ds[r] = g.shared ? a.s_sout[row] : a.s_down[base + row];
+    if (kFp8) ds[p] = g.shared ? a.s_sout[row] : a.s_down[base + row];
   }
   for (int t = 0; t < g.count; ++t) {
     int b, slot;
     moe_entry(a, g, t, b, slot);
+    const bf16* hv = a.hidden + ((int64_t)b * (a.k + 1) + slot) * a.IM;
     u32x4 hr[kC];
-    load_vec<kC>(a.hidden + ((int64_t)b * (a.k + 1) + slot) * a.IM, K, lane, hr);
+#pragma unroll
+    for (int i = 0; i < kC; ++i) {
+      const int c = li + kDownLanes * i;
+      hr[i] = c < nch ? load16(hv + (int64_t)c * 8) : u32x4{0u, 0u, 0u, 0u};
+    }
     float* prow = a.partial + ((int64_t)b * (a.k + 1) + slot) * a.H;
 #pragma unroll
-    for (int r = 0; r < kR; ++r) {
+    for (int p = 0; p < kP; ++p) {
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < kC; ++i)
-        if (lane + kWave * i < nch) d = WC::dot(dw[r][i], hr[i], d);
-      d = wave_sum(d);
-      if (kFp8) d *= ds[r];
-      if (lane == 0 && n0 + r < a.H) prow[n0 + r] = rbf(d);
+        if (li + kDownLanes * i < nch) d = WC::dot(dw[p][i], hr[i], d);
+      d = group_sum<kDownLanes>(d);
+      if (kFp8) d *= ds[p];
+      const int n = n0 + p * kRpp + rsub;
+      if (li == 0 && n < a.H) prow[n] = rbf(d);
     }
   }
 }
@@ -760,7 +774,9 @@ __global__ __launch_bounds__(kBlock) void k_scaled_add_rows(const bf16* __restri
 
 template <bool kFp8, bool kF32>
 int launch_moe(const MoeArgs& a, hipStream_t s) {
-  constexpr int kRgu = 1, kRdn = 2;     // small blocks: many per compute unit, even tails
+  constexpr int kRgu = 1;               // gate/up rows per wave: many small blocks, even tails
+  constexpr int kPdn = 1;               // down passes of four rows per wave
+  constexpr int kRdn = kPdn * (kWave / kDownLanes);
   // picked experts at most min(E, B k), plus the shared one
   const int ny = (a.E < a.B * a.k ? a.E : a.B * a.k) + 1;
   const int im = a.I > a.IS ? a.I : a.IS;
@@ -775,12 +791,18 @@ int launch_moe(const MoeArgs& a, hipStream_t s) {
     case 8: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 8, kRgu>), g1, dim3(kBlock), 0, s, a); break;
     default: return fail(kUnsupported, "moe_experts: hidden size %d", a.H);
   }
-  switch (cmax_for(im)) {
-    case 1: hipLaunchKernelGGL((k_moe_down<kFp8, 1, kRdn>), g2, dim3(kBlock), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((k_moe_down<kFp8, 2, kRdn>), g2, dim3(kBlock), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_moe_down<kFp8, 4, kRdn>), g2, dim3(kBlock), 0, s, a); break;
-    default: return fail(kUnsupported, "moe_experts: expert width %d", im);
-  }
+  // down: 16-byte chunks per lane of the longer expert width over 16 lanes
+  const int dc = (im / 8 + kDownLanes - 1) / kDownLanes;
+  if (dc <= 4)
+    hipLaunchKernelGGL((k_moe_down<kFp8, 4, kPdn>), g2, dim3(kBlock), 0, s, a);
+  else if (dc <= 8)
+    hipLaunchKernelGGL((k_moe_down<kFp8, 8, kPdn>), g2, dim3(kBlock), 0, s, a);
+  else if (dc <= 12)
+    hipLaunchKernelGGL((k_moe_down<kFp8, 12, kPdn>), g2, dim3(kBlock), 0, s, a);
+  else if (dc <= 16)
+    hipLaunchKernelGGL((k_moe_down<kFp8, 16, kPdn>), g2, dim3(kBlock), 0, s, a);
+  else
+    return fail(kUnsupported, "moe_experts: expert width %d", im);
   hipLaunchKernelGGL((k_moe_mix<kF32>), g3, dim3(kBlock), 0, s, a);
   return launched("moe_experts");
 }
