@@ -150,14 +150,17 @@ struct WChunk<true> {
     return __builtin_nontemporal_load(
         reinterpret_cast<const u32x2*>((const uint8_t*)w + row * K + (int64_t)c * 8));
   }
-  // e4m3fn values are exact in bf16: decode, repack, bf16 dot products
+  // e4m3fn values are exact in bf16: gfx950's scaled fp8 -> bf16 pair
+  // conversion at scale 1.0 decodes every code exactly (bytes 0-1, then 2-3
+  // with `sel`); then bf16 dot products
   static __device__ __forceinline__ float dot(const T& q, const u32x4& x, float acc) {
-    const f32x2_t v0 = __builtin_amdgcn_cvt_pk_f32_fp8(q.x, false);
-    const f32x2_t v1 = __builtin_amdgcn_cvt_pk_f32_fp8(q.x, true);
-    const f32x2_t v2 = __builtin_amdgcn_cvt_pk_f32_fp8(q.y, false);
-    const f32x2_t v3 = __builtin_amdgcn_cvt_pk_f32_fp8(q.y, true);
-    const u32x4 wv = {pack2(v0.x, v0.y), pack2(v1.x, v1.y), pack2(v2.x, v2.y),
-                      pack2(v3.x, v3.y)};
+    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+    const bf16x2_v v0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q.x, 1.0f, false);
+    const bf16x2_v v1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q.x, 1.0f, true);
+    const bf16x2_v v2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q.y, 1.0f, false);
+    const bf16x2_v v3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q.y, 1.0f, true);
+    const u32x4 wv = {__builtin_bit_cast(uint32_t, v0), __builtin_bit_cast(uint32_t, v1),
+                      __builtin_bit_cast(uint32_t, v2), __builtin_bit_cast(uint32_t, v3)};
     return dot8(wv, x, acc);
   }
 };

@@ -316,14 +316,15 @@ struct SkW<true> {
     return __builtin_nontemporal_load(
         reinterpret_cast<const u32x2*>((const uint8_t*)base + block * 512 + lane * 8));
   }
+  // gfx950's scaled fp8 -> bf16 pair conversion with scale 1.0 decodes every
+  // e4m3fn code exactly (checked over all 256 codes); `sel` picks bytes 2-3
   static __device__ __forceinline__ bf16x8_t value(const Raw& r) {
-    typedef float f32x2_t __attribute__((ext_vector_type(2)));
-    const f32x2_t v0 = __builtin_amdgcn_cvt_pk_f32_fp8(r.x, false);
-    const f32x2_t v1 = __builtin_amdgcn_cvt_pk_f32_fp8(r.x, true);
-    const f32x2_t v2 = __builtin_amdgcn_cvt_pk_f32_fp8(r.y, false);
-    const f32x2_t v3 = __builtin_amdgcn_cvt_pk_f32_fp8(r.y, true);
-    const bf16x8_t o = {(__bf16)v0.x, (__bf16)v0.y, (__bf16)v1.x, (__bf16)v1.y,
-                        (__bf16)v2.x, (__bf16)v2.y, (__bf16)v3.x, (__bf16)v3.y};
+    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+    const bf16x2_v v0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.x, 1.0f, false);
+    const bf16x2_v v1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.x, 1.0f, true);
+    const bf16x2_v v2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.y, 1.0f, false);
+    const bf16x2_v v3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.y, 1.0f, true);
+    const bf16x8_t o = {v0.x, v0.y, v1.x, v1.y, v2.x, v2.y, v3.x, v3.y};
     return o;
   }
 };
@@ -345,7 +346,7 @@ __global__ __launch_bounds__(kBlock) void k_pack_skinny_fp8(const uint8_t* __res
   *reinterpret_cast<u32x2*>(out + i * 8) = v;
 }
 
-template <int kEpi, int kT, int kKW, int kDepth, bool kFp8 = false>
+template <int kEpi, int kT, int kKW, int kDepth, bool kFp8 = false, int kH = 2>
 __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
     const bf16* __restrict__ X, const void* __restrict__ W, int M, int K, int N,
     const bf16* __restrict__ resid, int ldr, void* __restrict__ out, int ldo,
@@ -359,8 +360,12 @@ __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
   const int ksteps = K / 32;
   const int steps = ksteps / kKW;            // per wave, a multiple of kDepth
   const int s0 = wave * steps;
-  // X in operand order: step k's two 16-row halves are consecutive KiBs
-  const bf16* xa = X + (int64_t)s0 * 1024 + lane * 8;
+  // X in operand order: step k's two 16-row halves are consecutive KiBs.  A
+  // lane whose row is past M reads row M - 1's chunk instead (its outputs are
+  // never stored), so a few-row batch loads only its own rows' bytes.
+  const int xr0 = min(lane & 15, M - 1), xr1 = min(16 + (lane & 15), M - 1) - 16;
+  const bf16* xa = X + (int64_t)s0 * 1024 + (xr0 + 16 * (lane >> 4)) * 8;
+  const bf16* xb1 = X + (int64_t)s0 * 1024 + 512 + ((xr1 < 0 ? 0 : xr1) + 16 * (lane >> 4)) * 8;
   int64_t wt[kT];                            // block index of (tile, step s0)
 #pragma unroll
   for (int t = 0; t < kT; ++t) {
@@ -373,7 +378,7 @@ __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
 #pragma unroll
     for (int t = 0; t < kT; ++t) b[u][t] = WL::load(W, wt[t] + k, lane);
     a0[u] = load16(xa + (int64_t)k * 1024);
-    a1[u] = load16(xa + (int64_t)k * 1024 + 512);
+    if (kH == 2) a1[u] = load16(xb1 + (int64_t)k * 1024);        // rows 16..31
   };
 #pragma unroll
   for (int u = 0; u < kDepth; ++u) {
@@ -390,12 +395,12 @@ __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
 #pragma unroll
     for (int u = 0; u < kDepth; ++u) {
       const bf16x8_t x0 = __builtin_bit_cast(bf16x8_t, a0[u]);
-      const bf16x8_t x1 = __builtin_bit_cast(bf16x8_t, a1[u]);
+      const bf16x8_t x1 = __builtin_bit_cast(bf16x8_t, kH == 2 ? a1[u] : a0[u]);
 #pragma unroll
       for (int t = 0; t < kT; ++t) {
         const bf16x8_t bw = WL::value(b[u][t]);
         c[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, bw, c[t][0], 0, 0, 0);
-        c[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, bw, c[t][1], 0, 0, 0);
+        if (kH == 2) c[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, bw, c[t][1], 0, 0, 0);
       }
       if (decltype(refill)::value) issue(u, k0 + kDepth + u);
       __builtin_amdgcn_sched_barrier(0);
@@ -789,9 +794,13 @@ int tfd_gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M,
   const int ntiles = (N + 15) / 16;
   const int steps = K / 32 / 8;
   const dim3 grid(ntiles);
-#define TFD_KSPLIT8(EPI, D)                                                                     \
-  hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 8, D, true>), grid, dim3(8 * kWave), 0, s, xb, w, \
-                     M, K, N, rb, ldr, out, ldo, scale)
+#define TFD_KSPLIT8(EPI, D)                                                                   \
+  if (M <= 16)                                                                                \
+    hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 8, D, true, 1>), grid, dim3(8 * kWave), 0, s, xb, \
+                       w, M, K, N, rb, ldr, out, ldo, scale);                                 \
+  else                                                                                        \
+    hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 8, D, true, 2>), grid, dim3(8 * kWave), 0, s, xb, \
+                       w, M, K, N, rb, ldr, out, ldo, scale)
 #define TFD_KSPLIT8_EPI(EPI)                    \
   if (steps % 8 == 0) TFD_KSPLIT8(EPI, 8);      \
   else if (steps % 4 == 0) TFD_KSPLIT8(EPI, 4); \
@@ -838,11 +847,19 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
     const bool wide = (int)grid.x < compute_units() && (K / 32) % 16 == 0;
     const int steps16 = K / 32 / 16;
 #define TFD_KSPLIT(EPI, KT, D)                                                                  \
-  hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D>), grid, dim3(8 * kWave), 0, s, xb, wb, M, \
-                     K, N, rb, ldr, out, ldo, nullptr)
+  if (M <= 16)                                                                                  \
+    hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D, false, 1>), grid, dim3(8 * kWave), 0, s,   \
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr);                            \
+  else                                                                                          \
+    hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D, false, 2>), grid, dim3(8 * kWave), 0, s,   \
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr)
 #define TFD_KSPLIT16(EPI, D)                                                                    \
-  hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 16, D>), grid, dim3(16 * kWave), 0, s, xb, wb, M, \
-                     K, N, rb, ldr, out, ldo, nullptr)
+  if (M <= 16)                                                                                  \
+    hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 16, D, false, 1>), grid, dim3(16 * kWave), 0, s,  \
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr);                            \
+  else                                                                                          \
+    hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 16, D, false, 2>), grid, dim3(16 * kWave), 0, s,  \
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr)
 #define TFD_KSPLIT_EPI(EPI)                              \
   if (wide && kt == 1 && steps16 % 8 == 0) TFD_KSPLIT16(EPI, 8); \
   else if (wide && kt == 1 && steps16 % 4 == 0) TFD_KSPLIT16(EPI, 4); \
