@@ -77,6 +77,9 @@ int tfd_route_topk(const float* logits, int ldl, int rows, int experts, int k, i
  * outside [0, experts) (it is served as expert 0) or an expert repeated in a row
  * raises TFD_ERR_TOKEN_RANGE in err. */
 #define TFD_MOE_GROUP_WORDS(experts, rows) (1 + 2 * (experts) + (experts) * (rows))
+#define TFD_MOE_ROUTE_GIVEN 0
+#define TFD_MOE_ROUTE_SOFTMAX_TOPK 1 /* TFD_ROUTE_SOFTMAX_TOPK inside the call */
+#define TFD_MOE_ROUTE_TOPK_SOFTMAX 2 /* TFD_ROUTE_TOPK_SOFTMAX inside the call */
 typedef struct {
   const void* x;
   const float* weights;
@@ -94,6 +97,11 @@ typedef struct {
   int rows, k, experts, hidden_size, inter, shared_inter, hidden_ld;
   int fp8, policy;
   int accumulate; /* TFD_POLICY_F32 only: out += the block's output (C4's residual add) */
+  /* route TFD_MOE_ROUTE_SOFTMAX_TOPK / _TOPK_SOFTMAX: the call routes first, as
+   * tfd_route_topk would, from logits f32 [rows][ldl] into weights / idx (then
+   * outputs, k <= 64); TFD_MOE_ROUTE_GIVEN (0): weights and idx are inputs. */
+  const float* logits;
+  int ldl, route;
   int32_t* err;
 } TfdMoeArgs;
 int tfd_moe_experts(const TfdMoeArgs* args, void* stream);

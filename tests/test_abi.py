@@ -40,7 +40,8 @@ def test_header_constants_match_binding():
     names = {"ABI_VERSION", "PRO_PLAIN", "PRO_NORM", "EPI_STORE", "EPI_RESID", "EPI_SWIGLU",
              "EPI_LOGITS", "ERR_TOKEN_RANGE", "ERR_POS_RANGE", "ERR_PAGE_RANGE",
              "ERR_STEP_RANGE", "ERR_SYNC", "PAGE_SIZE", "ATTN_SPLIT", "SKINNY_COUNTERS", "EPI_RESID_F32",
-             "ROUTE_SOFTMAX_TOPK", "ROUTE_TOPK_SOFTMAX", "POLICY_F32", "POLICY_BF16"}
+             "ROUTE_SOFTMAX_TOPK", "ROUTE_TOPK_SOFTMAX", "POLICY_F32", "POLICY_BF16",
+             "MOE_ROUTE_GIVEN", "MOE_ROUTE_SOFTMAX_TOPK", "MOE_ROUTE_TOPK_SOFTMAX"}
     assert names <= set(defines), names - set(defines)
     for name in names:
         assert getattr(_lib, name) == int(defines[name]), name

@@ -163,7 +163,7 @@ def test_route_rejects_bad_shapes(gpu_device):
 # MoE experts
 # ---------------------------------------------------------------------------
 def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w_sscale=None,
-              fp8=False, policy, expect_err=0):
+              fp8=False, policy, expect_err=0, route=None):
     dev = "cuda:0"
     rows, hs = x.shape
     k = idx.shape[1]
@@ -196,8 +196,12 @@ def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w
     a.rows, a.k, a.experts, a.hidden_size = rows, k, experts, hs
     a.inter, a.shared_inter, a.hidden_ld = inter, sh, ld
     a.fp8, a.policy, a.err = int(fp8), policy, ptr(err)
+    if route is not None:
+        a.logits, a.ldl, a.route = d(route[0].float()), route[0].shape[1], route[1]
     lib().tfd_moe_experts(ctypes.addressof(a), _stream())
     torch.cuda.synchronize()
+    if route is not None:
+        idx = keep[2].cpu()                  # the call wrote the ids
     if expect_err:
         assert err.item() == expect_err
     else:
@@ -237,6 +241,29 @@ def test_moe_experts_c4_bf16(gpu_device, rows, same):
                     w_sout=ws_down.to(BF), w_sscale=ws_scale.to(BF), policy=_lib.POLICY_F32)
     want = H.moe_c4(x, weights, idx, w_gate, w_up, w_down, ws_gate, ws_up, ws_down, ws_scale)
     assert_close_bf16(got, want, max_rel=1e-2, min_cos=0.99999, name="moe c4")
+
+
+@pytest.mark.parametrize("mode", ["softmax_topk", "topk_softmax"])
+def test_moe_routes_inside_the_call(gpu_device, mode):
+    """Routing folded into the MoE call (its first launch) gives the ids and
+    weights tfd_route_topk gives, and the same output bits."""
+    g = torch.Generator().manual_seed(21)
+    rows, hs, inter, sh, E, k = 5, 512, 128, 128, 32, 6
+    rnd = lambda *s: H.bf(torch.randn(*s, generator=g) * 0.05).to(BF)
+    x = H.bf(torch.randn(rows, hs, generator=g))
+    logits = H.bf(torch.randn(rows, E, generator=g) * 2)
+    rmode, mmode, policy = ((_lib.ROUTE_SOFTMAX_TOPK, _lib.MOE_ROUTE_SOFTMAX_TOPK,
+                             _lib.POLICY_F32) if mode == "softmax_topk" else
+                            (_lib.ROUTE_TOPK_SOFTMAX, _lib.MOE_ROUTE_TOPK_SOFTMAX,
+                             _lib.POLICY_BF16))
+    w_ref, idx_ref = _route(logits, k, rmode)
+    weights = dict(w_gate=rnd(E, inter, hs), w_up=rnd(E, inter, hs), w_down=rnd(E, hs, inter),
+                   w_sin=rnd(2 * sh, hs), w_sout=rnd(hs, sh))
+    want = _moe_call(x, w_ref, idx_ref, policy=policy, **weights)
+    wbuf = torch.zeros(rows, k)
+    ibuf = torch.full((rows, k), -1, dtype=torch.int32)
+    got = _moe_call(x, wbuf, ibuf, policy=policy, route=(logits, mmode), **weights)
+    assert torch.equal(got, want)
 
 
 def test_moe_experts_flags_a_bad_expert_id(gpu_device):

@@ -30,6 +30,7 @@ def moe_group_words(experts: int, rows: int) -> int:
     return 1 + 2 * experts + experts * rows
 
 POLICY_F32, POLICY_BF16 = 0, 1
+MOE_ROUTE_GIVEN, MOE_ROUTE_SOFTMAX_TOPK, MOE_ROUTE_TOPK_SOFTMAX = 0, 1, 2
 
 P = c_void_p
 I = c_int
@@ -95,6 +96,7 @@ class TfdMoeArgs(ctypes.Structure):
                                    "shared_scale", "partial", "groups", "out")],
         *[(n, c_int) for n in ("rows", "k", "experts", "hidden_size", "inter", "shared_inter",
                                 "hidden_ld", "fp8", "policy", "accumulate")],
+        ("logits", c_void_p), ("ldl", c_int), ("route", c_int),
         ("err", c_void_p),
     ]
 

@@ -60,17 +60,16 @@ __device__ __forceinline__ int wave_min_i(int v) {
 }
 
 template <int kMode>
-__global__ __launch_bounds__(kWave) void k_route(const float* __restrict__ logits, int ldl, int E,
-                                                 int k, float* __restrict__ weights,
-                                                 int* __restrict__ idx) {
-  const int row = blockIdx.x, lane = threadIdx.x;
+__device__ __forceinline__ void route_row(const float* __restrict__ lrow, int E, int k,
+                                          float* __restrict__ wrow, int* __restrict__ irow,
+                                          int lane) {
   float v[4];
   int id[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = lane + kWave * j;
     id[j] = e;
-    v[j] = e < E ? logits[(int64_t)row * ldl + e] : kNegInf;
+    v[j] = e < E ? lrow[e] : kNegInf;
   }
   const float m = wave_max(fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
   float sum_all = 0.f;
@@ -110,10 +109,18 @@ __global__ __launch_bounds__(kWave) void k_route(const float* __restrict__ logit
   if (lane < k) w = kMode == 0 ? expf(my_val - m) / sum_all : expf(my_val - m);
   const float tot = wave_sum(lane < k ? w : 0.f);
   if (lane < k) {
-    const float out = kMode == 0 ? w / tot : rbf(w / tot);
-    weights[(int64_t)row * k + lane] = out;
-    idx[(int64_t)row * k + lane] = my_idx;
+    wrow[lane] = kMode == 0 ? w / tot : rbf(w / tot);
+    irow[lane] = my_idx;
   }
+}
+
+template <int kMode>
+__global__ __launch_bounds__(kWave) void k_route(const float* __restrict__ logits, int ldl, int E,
+                                                 int k, float* __restrict__ weights,
+                                                 int* __restrict__ idx) {
+  const int row = blockIdx.x;
+  route_row<kMode>(logits + (int64_t)row * ldl, E, k, weights + (int64_t)row * k,
+                   idx + (int64_t)row * k, threadIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -204,6 +211,8 @@ struct MoeArgs {
   float* partial;                            // [B][k + 1][H] work: down outputs per slot
   int* groups;                               // work: n | picked[E] | count[E] | entries[E][B]
   float* out;                                // [B][H]
+  const float* logits;                       // [B][ldl] router logits when route >= 0
+  int ldl, route;                            // route: -1 given weights/idx, else mode
   int B, H, I, IS, IM, k, E;
   int accumulate;                            // out += (f32 policy)
   int* err;
@@ -213,14 +222,26 @@ __device__ __forceinline__ int* grp_picked(const MoeArgs& a) { return a.groups +
 __device__ __forceinline__ int* grp_count(const MoeArgs& a) { return a.groups + 1 + a.E; }
 __device__ __forceinline__ int* grp_entries(const MoeArgs& a) { return a.groups + 1 + 2 * a.E; }
 
-__global__ __launch_bounds__(kBlock) void k_moe_group(MoeArgs a) {
+// One block: (optionally) route every row, one wave per row, then group.
+constexpr int kGroupThreads = 1024;
+constexpr int kMaxExperts = 256;
+template <int kRoute>
+__global__ __launch_bounds__(kGroupThreads) void k_moe_group(MoeArgs a) {
+  constexpr int kWaves = kGroupThreads / kWave;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  __shared__ int c_s[kBlock];
-  __shared__ int wave_n[kWavesPerBlock];
-  c_s[tid] = 0;
+  __shared__ int c_s[kMaxExperts];
+  __shared__ int wave_n[kWaves];
+  if (kRoute >= 0) {
+    // the routing outputs are this call's weights and ids
+    for (int r = wave; r < a.B; r += kWaves)
+      route_row<kRoute>(a.logits + (int64_t)r * a.ldl, a.E, a.k,
+                        const_cast<float*>(a.weights) + (int64_t)r * a.k,
+                        const_cast<int*>(a.idx) + (int64_t)r * a.k, lane);
+  }
+  if (tid < kMaxExperts) c_s[tid] = 0;
   __syncthreads();
   int* entries = grp_entries(a);
-  for (int i = tid; i < a.B * a.k; i += kBlock) {
+  for (int i = tid; i < a.B * a.k; i += kGroupThreads) {
     int e = a.idx[i];
     if (e < 0 || e >= a.E) {
       raise_error(a.err, kErrTokenRange);
@@ -244,7 +265,7 @@ __global__ __launch_bounds__(kBlock) void k_moe_group(MoeArgs a) {
   if (e < a.E) grp_count(a)[e] = c_s[e] < a.B ? c_s[e] : a.B;
   if (tid == 0) {
     int n = 0;
-    for (int w = 0; w < kWavesPerBlock; ++w) n += wave_n[w];
+    for (int w = 0; w < kWaves; ++w) n += wave_n[w];
     a.groups[0] = n;
   }
 }
@@ -786,7 +807,12 @@ int launch_moe(const MoeArgs& a, hipStream_t s) {
   const dim3 g1((im + kWavesPerBlock * kRgu - 1) / (kWavesPerBlock * kRgu), ny);
   const dim3 g2((a.H + kWavesPerBlock * kRdn - 1) / (kWavesPerBlock * kRdn), ny);
   const dim3 g3((a.H + kBlock - 1) / kBlock, a.B);
-  hipLaunchKernelGGL(k_moe_group, dim3(1), dim3(kBlock), 0, s, a);
+  if (a.route == TFD_ROUTE_SOFTMAX_TOPK)
+    hipLaunchKernelGGL((k_moe_group<0>), dim3(1), dim3(kGroupThreads), 0, s, a);
+  else if (a.route == TFD_ROUTE_TOPK_SOFTMAX)
+    hipLaunchKernelGGL((k_moe_group<1>), dim3(1), dim3(kGroupThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_moe_group<-1>), dim3(1), dim3(kGroupThreads), 0, s, a);
   switch (cmax_for(a.H)) {
     case 1: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 1, kRgu>), g1, dim3(kBlock), 0, s, a); break;
     case 2: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 2, kRgu>), g1, dim3(kBlock), 0, s, a); break;
@@ -838,7 +864,7 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
       (t.w_shared_scale && (!t.shared_scale || t.fp8)))
     return fail(kBadArg, "moe_experts: null pointer or a shared-expert gate with fp8 weights");
   if (t.rows <= 0 || t.rows > 65535 || t.k <= 0 || t.k > 64 || t.experts <= 0 ||
-      t.experts > kBlock || t.hidden_size % 64 || t.hidden_size > 4096 || t.inter % 64 ||
+      t.experts > kMaxExperts || t.hidden_size % 64 || t.hidden_size > 4096 || t.inter % 64 ||
       t.inter > 2048 || t.shared_inter % 64 || t.shared_inter > 2048 ||
       t.hidden_ld < t.inter || t.hidden_ld < t.shared_inter || t.hidden_ld % 8)
     return fail(kBadShape, "moe_experts: rows=%d k=%d experts=%d (<= 256) H=%d (<= 4096) "
@@ -872,7 +898,16 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
   a.k = t.k;
   a.E = t.experts;
   a.accumulate = t.accumulate;
+  a.logits = t.logits;
+  a.ldl = t.ldl;
+  a.route = t.route == TFD_MOE_ROUTE_SOFTMAX_TOPK   ? TFD_ROUTE_SOFTMAX_TOPK
+            : t.route == TFD_MOE_ROUTE_TOPK_SOFTMAX ? TFD_ROUTE_TOPK_SOFTMAX
+                                                    : -1;
   a.err = t.err;
+  if (t.route < TFD_MOE_ROUTE_GIVEN || t.route > TFD_MOE_ROUTE_TOPK_SOFTMAX ||
+      (t.route != TFD_MOE_ROUTE_GIVEN && (!t.logits || t.ldl < t.experts || t.k > kWave)))
+    return fail(kBadArg, "moe_experts: route %d (0..2) needs logits with ldl >= experts and "
+                "k <= 64", t.route);
   if (t.accumulate && t.policy != TFD_POLICY_F32)
     return fail(kUnsupported, "moe_experts: accumulate needs the f32 policy");
   auto s = (hipStream_t)stream;

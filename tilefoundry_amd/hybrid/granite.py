@@ -10,9 +10,9 @@ per-channel fp8); the tied embedding / head table stays bf16.  Per layer:
 * input RMSNorm (operand order) -> fp8 in-projection -> Mamba2 step
   (``tfd_mamba_step``) or GQA decode (``tfd_gqa_decode``, no RoPE) -> fp8
   out-projection -> ``a + b * residual_multiplier`` (``tfd_scaled_add_rows``);
-* post RMSNorm -> fp8 router -> top-10 then softmax (``tfd_route_topk``) ->
-  routed experts + shared MLP (``tfd_moe_experts``, fp8, expert-grouped) -> the
-  scaled residual again;
+* post RMSNorm -> fp8 router -> routed experts + shared MLP
+  (``tfd_moe_experts``: top-10-then-softmax routing in its first launch, then fp8,
+  expert-grouped) -> the scaled residual again;
 
 then the final norm, the head over the tied table, the greedy pick and the next
 token's embedding times ``embedding_multiplier``.  The head's division by
@@ -297,6 +297,7 @@ class GraniteEngine:
         a.rows, a.k, a.experts, a.hidden_size = self.B, cfg.top_k, cfg.experts, cfg.hidden
         a.inter, a.shared_inter, a.hidden_ld = cfg.moe_inter, cfg.shared_inter, self.moe_ld
         a.fp8, a.policy, a.err = 1, _lib.POLICY_BF16, ptr(self.err)
+        a.logits, a.ldl, a.route = ptr(self.rlog), cfg.experts, _lib.MOE_ROUTE_TOPK_SOFTMAX
         self._lib.tfd_moe_experts(ctypes_addr(a), s)
 
     def _layer(self, i, s, cur):
@@ -322,9 +323,7 @@ class GraniteEngine:
                                 cfg.eps, 0, s)
         self._gemm8(self.xn, w["w_router"], w["w_router_scale"], H, cfg.experts,
                     _lib.EPI_LOGITS, self.rlog, cfg.experts, s)
-        L.tfd_route_topk(ptr(self.rlog), cfg.experts, B, cfg.experts, cfg.top_k,
-                         _lib.ROUTE_TOPK_SOFTMAX, ptr(self.rw), ptr(self.ridx), s)
-        self._moe(w, s)
+        self._moe(w, s)                    # routes (top-10, softmax) inside the call
         self._residual(self.moe_out, 1, s)
 
     def _step(self, cur):

@@ -10,9 +10,9 @@ its input to bf16 and rounds its f32 sum once.  Per layer:
   (skinny GEMM, f32 out) -> gated-DeltaNet step (``tfd_gdn_step``) or the
   full-attention step (``tfd_gqa_decode``) -> out-projection, whose epilogue
   adds it into the f32 residual stream;
-* post norm -> router projection -> softmax/top-8 (``tfd_route_topk``) -> routed
-  + shared experts (``tfd_moe_experts``, expert-grouped), whose mix adds into the
-  stream;
+* post norm -> router projection -> routed + shared experts
+  (``tfd_moe_experts``: softmax/top-8 routing in its first launch, then
+  expert-grouped), whose mix adds into the stream;
 
 then the final norm, the head, the greedy pick and the next token's embedding
 (``tfd_argmax_rows``, ``tfd_finalize_rows``).  Layer i is full attention when
@@ -302,6 +302,7 @@ class Qwen35Engine:
         a.inter, a.shared_inter, a.hidden_ld = cfg.moe_inter, cfg.shared_inter, self.moe_ld
         a.fp8, a.policy, a.err = 0, _lib.POLICY_F32, ptr(self.err)
         a.accumulate = 1                               # residual add into the stream
+        a.logits, a.ldl, a.route = ptr(self.rlog), cfg.experts, _lib.MOE_ROUTE_SOFTMAX_TOPK
         self._lib.tfd_moe_experts(ctypes_addr(a), s)
 
     def _layer(self, i, s, cur):
@@ -322,9 +323,7 @@ class Qwen35Engine:
         L.tfd_rmsnorm_f32_rows(ptr(self.hidden), H, ptr(w["gamma_post"]), ptr(self.xm), H,
                                ptr(self.xn), B, H, cfg.eps, s)
         self._gemm(self.xn, w["w_router"], H, cfg.experts, self.rlog, cfg.experts, s)
-        L.tfd_route_topk(ptr(self.rlog), cfg.experts, B, cfg.experts, cfg.top_k,
-                         _lib.ROUTE_SOFTMAX_TOPK, ptr(self.rw), ptr(self.ridx), s)
-        self._moe(w, s)                                # accumulates into the stream
+        self._moe(w, s)                    # routes, then accumulates into the stream
 
     def _step(self, cur):
         s = self._stream()
