@@ -350,16 +350,17 @@ template <int kEpi, int kT, int kKW, int kDepth, bool kFp8 = false, int kH = 2>
 __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
     const bf16* __restrict__ X, const void* __restrict__ W, int M, int K, int N,
     const bf16* __restrict__ resid, int ldr, void* __restrict__ out, int ldo,
-    const float* __restrict__ wscale) {
+    const float* __restrict__ wscale, float* __restrict__ part, int* __restrict__ counters) {
   using WL = SkW<kFp8>;
   __shared__ f32x4 red[kKW][kT][2][kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int ntiles = (N + 15) / 16;
   const int tile0 = blockIdx.x * kT;
+  const int slices = gridDim.y, slice = blockIdx.y;   // K slices across blocks
   const int ksteps = K / 32;
-  const int steps = ksteps / kKW;            // per wave, a multiple of kDepth
-  const int s0 = wave * steps;
+  const int steps = ksteps / slices / kKW;   // per wave, a multiple of kDepth
+  const int s0 = slice * (ksteps / slices) + wave * steps;
   // X in operand order: step k's two 16-row halves are consecutive KiBs.  A
   // lane whose row is past M reads row M - 1's chunk instead (its outputs are
   // never stored), so a few-row batch loads only its own rows' bytes.
@@ -427,6 +428,31 @@ __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
 #pragma unroll
       for (int e = 0; e < 4; ++e) sum[h][e] += v[e];
     }
+  }
+  if (slices > 1) {
+    // this slice's tile in fragment order ([slice][tile][half][lane] x 16
+    // bytes); the last block to arrive adds the slices in slice order
+    const int tile = tile0 + t;
+    const uint32_t own = ((uint32_t)(slice * ntiles + tile) * 2u) * 1024u + lane * 16u;
+#pragma unroll
+    for (int h = 0; h < kH; ++h) coh_st16(part, own + h * 1024u, __builtin_bit_cast(u32x4, sum[h]));
+    stores_done();
+    int ticket = 0;
+    if (lane == 0) ticket = atomicAdd(&counters[tile], 1);
+    ticket = __shfl(ticket, 0, kWave);
+    if (ticket != slices - 1) return;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) sum[h] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int sl = 0; sl < slices; ++sl) {
+      const uint32_t off = ((uint32_t)(sl * ntiles + tile) * 2u) * 1024u + lane * 16u;
+#pragma unroll
+      for (int h = 0; h < kH; ++h) {
+        const f32x4 x = __builtin_bit_cast(f32x4, coh_ld16(part, off + h * 1024u));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum[h][e] += x[e];
+      }
+    }
+    if (lane == 0) coh_sti(&counters[tile], 0);
   }
   if (kFp8) {
     // every lane holds one output column: its channel's scale
@@ -797,10 +823,10 @@ int tfd_gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M,
 #define TFD_KSPLIT8(EPI, D)                                                                   \
   if (M <= 16)                                                                                \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 8, D, true, 1>), grid, dim3(8 * kWave), 0, s, xb, \
-                       w, M, K, N, rb, ldr, out, ldo, scale);                                 \
+                       w, M, K, N, rb, ldr, out, ldo, scale, nullptr, nullptr);               \
   else                                                                                        \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 8, D, true, 2>), grid, dim3(8 * kWave), 0, s, xb, \
-                       w, M, K, N, rb, ldr, out, ldo, scale)
+                       w, M, K, N, rb, ldr, out, ldo, scale, nullptr, nullptr)
 #define TFD_KSPLIT8_EPI(EPI)                    \
   if (steps % 8 == 0) TFD_KSPLIT8(EPI, 8);      \
   else if (steps % 4 == 0) TFD_KSPLIT8(EPI, 4); \
@@ -840,26 +866,39 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
   const int ntiles = (N + 15) / 16;
   const int kt = ksplit_tiles(K, N);
   if (kt > 0) {
-    const int steps = K / 32 / 8;
-    const dim3 grid((ntiles + kt - 1) / kt);
-    // fewer blocks than compute units: sixteen waves split K instead of eight,
-    // so each unit that has a tile keeps twice the loads in flight
-    const bool wide = (int)grid.x < compute_units() && (K / 32) % 16 == 0;
+    dim3 grid((ntiles + kt - 1) / kt);
+    // fewer blocks than compute units: with a work buffer, K is also split
+    // across blocks (slices, added by the last block to finish a tile);
+    // without one, sixteen waves split K instead of eight
+    int slices = 1;
+    if (kt == 1 && work) {
+      for (int sl = 4; sl >= 2; sl /= 2)
+        if ((int)grid.x * sl <= compute_units() && (K / 32) % (sl * 8) == 0 &&
+            work_floats >= kSkCounters + (int64_t)sl * ntiles * 512 && ntiles <= kSkCounters) {
+          slices = sl;
+          break;
+        }
+    }
+    grid.y = slices;
+    int* counters = slices > 1 ? (int*)work : nullptr;
+    float* part = slices > 1 ? work + kSkCounters : nullptr;
+    const int steps = K / 32 / slices / 8;
+    const bool wide = slices == 1 && (int)grid.x < compute_units() && (K / 32) % 16 == 0;
     const int steps16 = K / 32 / 16;
 #define TFD_KSPLIT(EPI, KT, D)                                                                  \
   if (M <= 16)                                                                                  \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D, false, 1>), grid, dim3(8 * kWave), 0, s,   \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr);                            \
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, part, counters);            \
   else                                                                                          \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D, false, 2>), grid, dim3(8 * kWave), 0, s,   \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr)
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, part, counters)
 #define TFD_KSPLIT16(EPI, D)                                                                    \
   if (M <= 16)                                                                                  \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 16, D, false, 1>), grid, dim3(16 * kWave), 0, s,  \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr);                            \
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, nullptr, nullptr);          \
   else                                                                                          \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 16, D, false, 2>), grid, dim3(16 * kWave), 0, s,  \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr)
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, nullptr, nullptr)
 #define TFD_KSPLIT_EPI(EPI)                              \
   if (wide && kt == 1 && steps16 % 8 == 0) TFD_KSPLIT16(EPI, 8); \
   else if (wide && kt == 1 && steps16 % 4 == 0) TFD_KSPLIT16(EPI, 4); \
