@@ -214,7 +214,7 @@ def test_batch_engine_qwen3_layer_shape(gpu_device):
         print(f"sequence {b}: identical for {16 if k is None else k} of 16 steps")
 
 
-@pytest.mark.parametrize("split_tiles", [1, 3])
+@pytest.mark.parametrize("split_tiles", [1, 2, 3, 4, 8])
 def test_batch_engine_long_splits(gpu_device, split_tiles):
     """Splits of several 64-position tiles (the long-context partition) against
     the oracle, with contexts past several splits."""
