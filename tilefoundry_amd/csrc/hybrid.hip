@@ -270,14 +270,18 @@ __global__ __launch_bounds__(kGroupThreads) void k_moe_group(MoeArgs a) {
   }
 }
 
-// (expert, entries) of blockIdx.y: the picked experts, then the shared one
+// (expert, entries) of blockIdx.y: the picked experts, then the shared one.
+// kWho selects what a launch covers: 0 both (the shared expert is the last y),
+// 1 the picked experts only, 2 the shared expert only (when its width differs
+// from the routed experts', each gets a launch sized for it).
 struct Group {
   bool shared;
   int e, count;
   const int* entries;
 };
+template <int kWho>
 __device__ __forceinline__ bool moe_group(const MoeArgs& a, Group& g) {
-  g.shared = blockIdx.y == gridDim.y - 1;
+  g.shared = kWho == 2 || (kWho == 0 && blockIdx.y == gridDim.y - 1);
   if (g.shared) {
     g.e = 0;
     g.count = a.B;
@@ -303,12 +307,12 @@ __device__ __forceinline__ void moe_entry(const MoeArgs& a, const Group& g, int 
   }
 }
 
-template <bool kFp8, bool kF32, int kC, int kR>
+template <bool kFp8, bool kF32, int kC, int kR, int kWho = 0>
 __global__ __launch_bounds__(kBlock) void k_moe_gateup(MoeArgs a) {
   using WC = WChunk<kFp8>;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   Group g;
-  if (!moe_group(a, g)) return;
+  if (!moe_group<kWho>(a, g)) return;
   if (g.shared && a.w_sscale && blockIdx.x == 0 && wave == 0) {
     for (int b = 0; b < a.B; ++b) {
       u32x4 xr[kC];
@@ -375,7 +379,7 @@ __global__ __launch_bounds__(kBlock) void k_moe_gateup(MoeArgs a) {
 // share a row (16-byte chunks c = l % 16 + 16 i), a wave holds four rows per
 // pass and kP passes, and a row's sum needs only the in-row DPP steps.
 constexpr int kDownLanes = 16;
-template <bool kFp8, int kC, int kP>
+template <bool kFp8, int kC, int kP, int kWho = 0>
 __global__ __launch_bounds__(kBlock) void k_moe_down(MoeArgs a) {
   using WC = WChunk<kFp8>;
   constexpr int kRpp = kWave / kDownLanes;        // rows per pass
@@ -383,7 +387,7 @@ __global__ __launch_bounds__(kBlock) void k_moe_down(MoeArgs a) {
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int li = lane % kDownLanes, rsub = lane / kDownLanes;
   Group g;
-  if (!moe_group(a, g)) return;
+  if (!moe_group<kWho>(a, g)) return;
   const int K = g.shared ? a.IS : a.I;
   const int nch = K / 8;
   const int n0 = (blockIdx.x * kWavesPerBlock + wave) * kR;
@@ -796,16 +800,46 @@ __global__ __launch_bounds__(kBlock) void k_scaled_add_rows(const bf16* __restri
 
 }  // namespace
 
+// gate/up + SwiGLU and the down projections for the groups kWho selects, whose
+// expert width is `width` (rows of gate/up, K of down) over `ny` groups
+template <bool kFp8, bool kF32, int kWho>
+int launch_moe_experts(const MoeArgs& a, int width, int ny, hipStream_t s) {
+  // rows per wave: gate/up kRgu, down kPdn passes of four -- many small
+  // blocks with even tails (measured at C5's fp8 shape: two gate/up rows per
+  // wave 7% slower, four 60%; two down passes no faster)
+  constexpr int kRgu = 1;
+  constexpr int kPdn = 1;
+  constexpr int kRdn = kPdn * (kWave / kDownLanes);
+  const dim3 g1((width + kWavesPerBlock * kRgu - 1) / (kWavesPerBlock * kRgu), ny);
+  const dim3 g2((a.H + kWavesPerBlock * kRdn - 1) / (kWavesPerBlock * kRdn), ny);
+  switch (cmax_for(a.H)) {
+    case 1: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 1, kRgu, kWho>), g1, dim3(kBlock), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 2, kRgu, kWho>), g1, dim3(kBlock), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 4, kRgu, kWho>), g1, dim3(kBlock), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 8, kRgu, kWho>), g1, dim3(kBlock), 0, s, a); break;
+    default: return fail(kUnsupported, "moe_experts: hidden size %d", a.H);
+  }
+  // down: chunks of 8 weights per lane over the 16 lanes of a row
+  const int dc = (width / 8 + kDownLanes - 1) / kDownLanes;
+  if (dc <= 4)
+    hipLaunchKernelGGL((k_moe_down<kFp8, 4, kPdn, kWho>), g2, dim3(kBlock), 0, s, a);
+  else if (dc <= 6)
+    hipLaunchKernelGGL((k_moe_down<kFp8, 6, kPdn, kWho>), g2, dim3(kBlock), 0, s, a);
+  else if (dc <= 8)
+    hipLaunchKernelGGL((k_moe_down<kFp8, 8, kPdn, kWho>), g2, dim3(kBlock), 0, s, a);
+  else if (dc <= 12)
+    hipLaunchKernelGGL((k_moe_down<kFp8, 12, kPdn, kWho>), g2, dim3(kBlock), 0, s, a);
+  else if (dc <= 16)
+    hipLaunchKernelGGL((k_moe_down<kFp8, 16, kPdn, kWho>), g2, dim3(kBlock), 0, s, a);
+  else
+    return fail(kUnsupported, "moe_experts: expert width %d", width);
+  return 0;
+}
+
 template <bool kFp8, bool kF32>
 int launch_moe(const MoeArgs& a, hipStream_t s) {
-  constexpr int kRgu = 1;               // gate/up rows per wave: many small blocks, even tails
-  constexpr int kPdn = 1;               // down passes of four rows per wave
-  constexpr int kRdn = kPdn * (kWave / kDownLanes);
   // picked experts at most min(E, B k), plus the shared one
-  const int ny = (a.E < a.B * a.k ? a.E : a.B * a.k) + 1;
-  const int im = a.I > a.IS ? a.I : a.IS;
-  const dim3 g1((im + kWavesPerBlock * kRgu - 1) / (kWavesPerBlock * kRgu), ny);
-  const dim3 g2((a.H + kWavesPerBlock * kRdn - 1) / (kWavesPerBlock * kRdn), ny);
+  const int np = a.E < a.B * a.k ? a.E : a.B * a.k;
   const dim3 g3((a.H + kBlock - 1) / kBlock, a.B);
   if (a.route == TFD_ROUTE_SOFTMAX_TOPK)
     hipLaunchKernelGGL((k_moe_group<0>), dim3(1), dim3(kGroupThreads), 0, s, a);
@@ -813,25 +847,14 @@ int launch_moe(const MoeArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((k_moe_group<1>), dim3(1), dim3(kGroupThreads), 0, s, a);
   else
     hipLaunchKernelGGL((k_moe_group<-1>), dim3(1), dim3(kGroupThreads), 0, s, a);
-  switch (cmax_for(a.H)) {
-    case 1: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 1, kRgu>), g1, dim3(kBlock), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 2, kRgu>), g1, dim3(kBlock), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 4, kRgu>), g1, dim3(kBlock), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 8, kRgu>), g1, dim3(kBlock), 0, s, a); break;
-    default: return fail(kUnsupported, "moe_experts: hidden size %d", a.H);
-  }
-  // down: 16-byte chunks per lane of the longer expert width over 16 lanes
-  const int dc = (im / 8 + kDownLanes - 1) / kDownLanes;
-  if (dc <= 4)
-    hipLaunchKernelGGL((k_moe_down<kFp8, 4, kPdn>), g2, dim3(kBlock), 0, s, a);
-  else if (dc <= 8)
-    hipLaunchKernelGGL((k_moe_down<kFp8, 8, kPdn>), g2, dim3(kBlock), 0, s, a);
-  else if (dc <= 12)
-    hipLaunchKernelGGL((k_moe_down<kFp8, 12, kPdn>), g2, dim3(kBlock), 0, s, a);
-  else if (dc <= 16)
-    hipLaunchKernelGGL((k_moe_down<kFp8, 16, kPdn>), g2, dim3(kBlock), 0, s, a);
-  else
-    return fail(kUnsupported, "moe_experts: expert width %d", im);
+  // one launch pair when the shared expert is as wide as the routed ones,
+  // else a pair for each width
+  int rc;
+  if (a.I == a.IS)
+    rc = launch_moe_experts<kFp8, kF32, 0>(a, a.I, np + 1, s);
+  else if ((rc = launch_moe_experts<kFp8, kF32, 1>(a, a.I, np, s)) == 0)
+    rc = launch_moe_experts<kFp8, kF32, 2>(a, a.IS, 1, s);
+  if (rc) return rc;
   hipLaunchKernelGGL((k_moe_mix<kF32>), g3, dim3(kBlock), 0, s, a);
   return launched("moe_experts");
 }
