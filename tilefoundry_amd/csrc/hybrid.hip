@@ -800,26 +800,33 @@ __global__ __launch_bounds__(kBlock) void k_scaled_add_rows(const bf16* __restri
 
 }  // namespace
 
-// gate/up + SwiGLU and the down projections for the groups kWho selects, whose
-// expert width is `width` (rows of gate/up, K of down) over `ny` groups
-template <bool kFp8, bool kF32, int kWho>
-int launch_moe_experts(const MoeArgs& a, int width, int ny, hipStream_t s) {
-  // rows per wave: gate/up kRgu, down kPdn passes of four -- many small
-  // blocks with even tails (measured at C5's fp8 shape: two gate/up rows per
-  // wave 7% slower, four 60%; two down passes no faster)
-  constexpr int kRgu = 1;
-  constexpr int kPdn = 1;
-  constexpr int kRdn = kPdn * (kWave / kDownLanes);
+// gate/up + SwiGLU for every group (the registers per lane depend only on the
+// hidden size; blocks past a narrower expert's rows leave at once)
+template <bool kFp8, bool kF32>
+int launch_moe_gateup(const MoeArgs& a, int width, int ny, hipStream_t s) {
+  constexpr int kRgu = 1;               // one row per wave: many small blocks, even tails
   const dim3 g1((width + kWavesPerBlock * kRgu - 1) / (kWavesPerBlock * kRgu), ny);
-  const dim3 g2((a.H + kWavesPerBlock * kRdn - 1) / (kWavesPerBlock * kRdn), ny);
   switch (cmax_for(a.H)) {
-    case 1: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 1, kRgu, kWho>), g1, dim3(kBlock), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 2, kRgu, kWho>), g1, dim3(kBlock), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 4, kRgu, kWho>), g1, dim3(kBlock), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 8, kRgu, kWho>), g1, dim3(kBlock), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 1, kRgu>), g1, dim3(kBlock), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 2, kRgu>), g1, dim3(kBlock), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 4, kRgu>), g1, dim3(kBlock), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((k_moe_gateup<kFp8, kF32, 8, kRgu>), g1, dim3(kBlock), 0, s, a); break;
     default: return fail(kUnsupported, "moe_experts: hidden size %d", a.H);
   }
-  // down: chunks of 8 weights per lane over the 16 lanes of a row
+  return 0;
+}
+
+// the down projections for the groups kWho selects, whose expert width (K of
+// the projection, which sets the chunks a lane holds) is `width`, over `ny`
+// groups
+template <bool kFp8, int kWho>
+int launch_moe_down(const MoeArgs& a, int width, int ny, hipStream_t s) {
+  // one pass of four rows per wave: many small blocks with even tails
+  // (measured at C5's fp8 shape: two passes no faster)
+  constexpr int kPdn = 1;
+  constexpr int kRdn = kPdn * (kWave / kDownLanes);
+  const dim3 g2((a.H + kWavesPerBlock * kRdn - 1) / (kWavesPerBlock * kRdn), ny);
+  // chunks of 8 weights per lane over the 16 lanes of a row
   const int dc = (width / 8 + kDownLanes - 1) / kDownLanes;
   if (dc <= 4)
     hipLaunchKernelGGL((k_moe_down<kFp8, 4, kPdn, kWho>), g2, dim3(kBlock), 0, s, a);
@@ -847,13 +854,15 @@ int launch_moe(const MoeArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((k_moe_group<1>), dim3(1), dim3(kGroupThreads), 0, s, a);
   else
     hipLaunchKernelGGL((k_moe_group<-1>), dim3(1), dim3(kGroupThreads), 0, s, a);
-  // one launch pair when the shared expert is as wide as the routed ones,
-  // else a pair for each width
-  int rc;
+  // gate/up in one launch; the down projections in one launch when the shared
+  // expert is as wide as the routed ones, else one for each width (a lane's
+  // chunk registers are sized by the width)
+  int rc = launch_moe_gateup<kFp8, kF32>(a, a.I > a.IS ? a.I : a.IS, np + 1, s);
+  if (rc) return rc;
   if (a.I == a.IS)
-    rc = launch_moe_experts<kFp8, kF32, 0>(a, a.I, np + 1, s);
-  else if ((rc = launch_moe_experts<kFp8, kF32, 1>(a, a.I, np, s)) == 0)
-    rc = launch_moe_experts<kFp8, kF32, 2>(a, a.IS, 1, s);
+    rc = launch_moe_down<kFp8, 0>(a, a.I, np + 1, s);
+  else if ((rc = launch_moe_down<kFp8, 1>(a, a.I, np, s)) == 0)
+    rc = launch_moe_down<kFp8, 2>(a, a.IS, 1, s);
   if (rc) return rc;
   hipLaunchKernelGGL((k_moe_mix<kF32>), g3, dim3(kBlock), 0, s, a);
   return launched("moe_experts");

@@ -61,12 +61,17 @@ def time_graph(calls, reps: int) -> float:
     torch.cuda.synchronize()
     g.replay()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    g.replay()
-    e1.record()
-    e1.synchronize()
-    return e0.elapsed_time(e1) * 1e-3 / (reps * len(calls))
+    # the median of five timed replays: one replay of a few short launches can
+    # catch an unrelated stall of the device
+    times = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e-3)
+    return sorted(times)[2] / (reps * len(calls))
 
 
 def _line(config, kernel, rows, sec, nbytes, **extra):
