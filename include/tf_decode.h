@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TFD_ABI_VERSION 10
+#define TFD_ABI_VERSION 11
 
 /* gemv prologues / epilogues */
 #define TFD_PRO_PLAIN 0  /* x used as given */
@@ -143,6 +143,11 @@ int tfd_attn_pv_combine_paged(const void* qkv, const int32_t* cache_len,
  * is in operand order (rows <= 32, n % 32 == 0; ldo unused). */
 int tfd_rmsnorm_rows_bf16(const void* x, int ldx, const void* gamma, void* out, int ldo,
                           int rows, int n, float eps, int packed, void* stream);
+/* The same norm written to both layouts in one launch: row-major out_rows
+ * [rows][ldo] and/or out_packed in the skinny GEMMs' operand order (rows <= 32,
+ * n % 32 == 0); NULL skips one. */
+int tfd_rmsnorm_rows2_bf16(const void* x, int ldx, const void* gamma, void* out_rows, int ldo,
+                           void* out_packed, int rows, int n, float eps, void* stream);
 
 /* Weights [N][K] (row stride ldw) re-laid for tfd_gemm_skinny_bf16: 16-row x 32-k
  * blocks of 1 KiB in the matrix cores' operand order, rows padded with zeros to a

@@ -41,6 +41,12 @@ int tfd_pack_skinny_fp8(const void* w, int ldw, int N, int K, void* packed, void
 int tfd_gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M, int K, int N,
                         int epilogue, const void* resid, int ldr, void* out, int ldo,
                         void* stream);
+/* The same product with C5's scaled residual add as its epilogue: out =
+ * bf16(resid + bf16(y * mult)), y the bf16 product (examples/granite_4_0_h_small-cuda/
+ * model.py:502-508 residual_add after the mixer's out_proj).  out may alias resid. */
+int tfd_gemm_skinny_fp8_resid_scaled(const void* x, const void* w, const float* scale, int M,
+                                     int K, int N, const void* resid, int ldr, float mult,
+                                     void* out, int ldo, void* stream);
 
 #define TFD_ROUTE_SOFTMAX_TOPK 0 /* C4: softmax over all experts, top k, renormalise */
 #define TFD_ROUTE_TOPK_SOFTMAX 1 /* C5: top k logits, softmax over them, bf16 weights */
@@ -103,6 +109,12 @@ typedef struct {
   const float* logits;
   int ldl, route;
   int32_t* err;
+  /* TFD_POLICY_BF16 only: with resid set, the call adds its output into the bf16
+   * residual stream resid [rows][hidden_size] as resid = bf16(resid + bf16(y *
+   * resid_mult)) (examples/granite_4_0_h_small-cuda/model.py:502-508
+   * residual_add) instead of writing out (which may then be NULL). */
+  void* resid;
+  float resid_mult;
 } TfdMoeArgs;
 int tfd_moe_experts(const TfdMoeArgs* args, void* stream);
 

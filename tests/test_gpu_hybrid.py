@@ -94,6 +94,46 @@ def test_fp8_gemm_within_one_ulp_of_exact(gpu_device, M, K, N):
         assert ((sw - want_sw).abs() <= ulp_bf16(want_sw)).all()
 
 
+@pytest.mark.parametrize("M", [1, 8, 17])
+def test_fp8_gemm_scaled_residual_epilogue(gpu_device, M):
+    """tfd_gemm_skinny_fp8_resid_scaled in place on the stream equals the plain
+    product followed by torch's bf16 residual add h + y * m (model.py:502-508)."""
+    g = torch.Generator().manual_seed(700 + M)
+    K, N = 4096, 4096
+    x = (torch.randn(M, K, generator=g) * 0.5).to(BF)
+    codes = _fp8_codes((N, K), g)
+    scale = torch.rand(N, generator=g) * 0.004 + 0.002
+    y = _gemm_fp8(x, codes, scale, _lib.EPI_STORE)
+    h = (torch.randn(M, N, generator=g)).to(BF)
+    dev = "cuda:0"
+    w = _packed_fp8(codes.to(dev))
+    xd, sd, hd = operand_order(x.to(dev)), scale.to(dev), h.to(dev)
+    lib().tfd_gemm_skinny_fp8_resid_scaled(ptr(xd), ptr(w), ptr(sd), M, K, N, ptr(hd), N, 0.22,
+                                           ptr(hd), N, _stream())
+    torch.cuda.synchronize()
+    assert torch.equal(hd.cpu(), h + y * 0.22)
+
+
+def test_rmsnorm_rows2_writes_both_layouts(gpu_device):
+    """One launch of tfd_rmsnorm_rows2_bf16 gives the bits of the row-major and the
+    operand-order calls of tfd_rmsnorm_rows_bf16."""
+    g = torch.Generator().manual_seed(9)
+    rows, n, dev = 8, 4096, "cuda:0"
+    x = torch.randn(rows, n, generator=g).to(BF).to(dev)
+    gamma = (torch.rand(n, generator=g) + 0.5).to(BF).to(dev)
+    o_rows = torch.zeros(rows, n, dtype=BF, device=dev)
+    o_pk = torch.zeros(32 * n, dtype=BF, device=dev)
+    r2 = torch.zeros_like(o_rows)
+    p2 = torch.zeros_like(o_pk)
+    L, s = lib(), _stream()
+    L.tfd_rmsnorm_rows_bf16(ptr(x), n, ptr(gamma), ptr(o_rows), n, rows, n, 1e-5, 0, s)
+    L.tfd_rmsnorm_rows_bf16(ptr(x), n, ptr(gamma), ptr(o_pk), 0, rows, n, 1e-5, 1, s)
+    L.tfd_rmsnorm_rows2_bf16(ptr(x), n, ptr(gamma), ptr(r2), n, ptr(p2), rows, n, 1e-5, s)
+    torch.cuda.synchronize()
+    assert torch.equal(r2, o_rows) and torch.equal(p2, o_pk)
+    assert o_rows.abs().sum() > 0
+
+
 def test_fp8_pack_layout(gpu_device):
     """Block (tile t, step s) is 512 bytes; lane l's 8 codes are
     W[16t + l % 16][32s + 8(l // 16) + j]; padding rows are 0."""
@@ -163,7 +203,9 @@ def test_route_rejects_bad_shapes(gpu_device):
 # MoE experts
 # ---------------------------------------------------------------------------
 def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w_sscale=None,
-              fp8=False, policy, expect_err=0, route=None):
+              fp8=False, policy, expect_err=0, route=None, resid=None):
+    """resid = (stream, multiplier): the call adds its scaled output into a copy of
+    the bf16 stream, which is returned instead of `out`."""
     dev = "cuda:0"
     rows, hs = x.shape
     k = idx.shape[1]
@@ -198,6 +240,10 @@ def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w
     a.fp8, a.policy, a.err = int(fp8), policy, ptr(err)
     if route is not None:
         a.logits, a.ldl, a.route = d(route[0].float()), route[0].shape[1], route[1]
+    stream = None
+    if resid is not None:
+        stream = resid[0].to(dev, BF).contiguous()
+        a.out, a.resid, a.resid_mult = None, ptr(stream), resid[1]
     lib().tfd_moe_experts(ctypes.addressof(a), _stream())
     torch.cuda.synchronize()
     if route is not None:
@@ -213,7 +259,7 @@ def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w
         for e in picked:
             got = sorted(g[1 + 2 * experts + e * rows:][:g[1 + experts + e]].tolist())
             assert got == [i for i, v in enumerate(idx.reshape(-1).tolist()) if v == e]
-    return out.cpu()
+    return out.cpu() if stream is None else stream.cpu()
 
 
 def _routing(rows, experts, k, gen):
@@ -296,6 +342,13 @@ def test_moe_experts_c5_fp8(gpu_device, rows):
     want = H.moe_c5(x, weights, idx, gc, gs, uc, us, dc, ds, sic, sis, soc, sos)
     assert torch.equal(got, got.to(BF).float())
     assert_close_bf16(got, want, max_rel=2e-2, min_cos=0.9999, name="moe c5")
+    # the same call adding bf16(y * m) into a bf16 stream: the residual add of
+    # model.py:502-508 in torch's bf16 arithmetic on the plain output
+    h = H.bf(torch.randn(rows, hs, generator=g)).to(BF)
+    added = _moe_call(x, weights, idx, w_gate=gc, w_up=uc, w_down=dc, w_sin=sic, w_sout=soc,
+                      s=(gs, us, ds, sis, sos), fp8=True, policy=_lib.POLICY_BF16,
+                      resid=(h, 0.22))
+    assert torch.equal(added, h + got.to(BF) * 0.22)
 
 
 # ---------------------------------------------------------------------------

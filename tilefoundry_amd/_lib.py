@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS, EPI_RESID_F32 = 0, 1, 2, 3, 4
@@ -51,6 +51,7 @@ SIGNATURES: dict[str, list] = {
                                    P, P, I, P, P],
     "tfd_attn_pv_combine_paged": [P, P, P, I, P, I, I, I, I, P, I, P, P, P, P, I, P, P, P, P],
     "tfd_rmsnorm_rows_bf16": [P, I, P, P, I, I, I, F, I, P],
+    "tfd_rmsnorm_rows2_bf16": [P, I, P, P, I, P, I, I, F, P],
     "tfd_pack_skinny_bf16": [P, I, I, I, P, P],
     "tfd_gemm_skinny_bf16": [P, P, I, I, I, I, P, I, P, I, P, L, P],
     "tfd_attn_rope_scores_paged_batched": [P, I, P, P, P, P, I, P, P, I, P, P, I, I, I, I, I, F,
@@ -65,6 +66,7 @@ SIGNATURES: dict[str, list] = {
     # include/tf_hybrid.h
     "tfd_pack_skinny_fp8": [P, I, I, I, P, P],
     "tfd_gemm_skinny_fp8": [P, P, P, I, I, I, I, P, I, P, I, P],
+    "tfd_gemm_skinny_fp8_resid_scaled": [P, P, P, I, I, I, P, I, F, P, I, P],
     "tfd_route_topk": [P, I, I, I, I, I, P, P, P],
     "tfd_moe_experts": [P, P],
     "tfd_gdn_step": [P, P],
@@ -97,7 +99,7 @@ class TfdMoeArgs(ctypes.Structure):
         *[(n, c_int) for n in ("rows", "k", "experts", "hidden_size", "inter", "shared_inter",
                                 "hidden_ld", "fp8", "policy", "accumulate")],
         ("logits", c_void_p), ("ldl", c_int), ("route", c_int),
-        ("err", c_void_p),
+        ("err", c_void_p), ("resid", c_void_p), ("resid_mult", c_float),
     ]
 
 

@@ -215,6 +215,8 @@ struct MoeArgs {
   int ldl, route;                            // route: -1 given weights/idx, else mode
   int B, H, I, IS, IM, k, E;
   int accumulate;                            // out += (f32 policy)
+  bf16* resid;                               // bf16 policy: resid = bf16(resid + bf16(y m))
+  float resid_mult;
   int* err;
 };
 
@@ -453,12 +455,16 @@ __global__ __launch_bounds__(kBlock) void k_moe_mix(MoeArgs a) {
       if (s0 + i < a.k) acc += kF32 ? d[i] * wg[i] : rbf(d[i] * wg[i]);
   }
   const float dsh = pb[(int64_t)a.k * a.H];
-  float* o = a.out + (int64_t)b * a.H + n;
+  const int64_t at = (int64_t)b * a.H + n;
   if (kF32) {
     const float y = acc + dsh * (a.w_sscale ? a.sscale[b] : 1.f);
-    *o = a.accumulate ? *o + y : y;
+    a.out[at] = a.accumulate ? a.out[at] + y : y;
   } else {
-    *o = rbf(rbf(acc) + dsh);
+    const float y = rbf(rbf(acc) + dsh);
+    if (a.resid)
+      a.resid[at] = f2bf(bf2f(a.resid[at]) + rbf(y * a.resid_mult));
+    else
+      a.out[at] = y;
   }
 }
 
@@ -891,7 +897,7 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
   if (!args) return fail(kBadArg, "moe_experts: null args");
   const TfdMoeArgs& t = *args;
   if (!t.x || !t.weights || !t.idx || !t.w_gate || !t.w_up || !t.w_down || !t.w_shared_in ||
-      !t.w_shared_out || !t.hidden || !t.partial || !t.groups || !t.out ||
+      !t.w_shared_out || !t.hidden || !t.partial || !t.groups || (!t.out && !t.resid) ||
       (t.fp8 && (!t.s_gate || !t.s_up || !t.s_down || !t.s_shared_in || !t.s_shared_out)) ||
       (t.w_shared_scale && (!t.shared_scale || t.fp8)))
     return fail(kBadArg, "moe_experts: null pointer or a shared-expert gate with fp8 weights");
@@ -930,6 +936,8 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
   a.k = t.k;
   a.E = t.experts;
   a.accumulate = t.accumulate;
+  a.resid = (bf16*)t.resid;
+  a.resid_mult = t.resid_mult;
   a.logits = t.logits;
   a.ldl = t.ldl;
   a.route = t.route == TFD_MOE_ROUTE_SOFTMAX_TOPK   ? TFD_ROUTE_SOFTMAX_TOPK
@@ -942,6 +950,8 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
                 "k <= 64", t.route);
   if (t.accumulate && t.policy != TFD_POLICY_F32)
     return fail(kUnsupported, "moe_experts: accumulate needs the f32 policy");
+  if (t.resid && t.policy != TFD_POLICY_BF16)
+    return fail(kUnsupported, "moe_experts: resid needs the bf16 policy");
   auto s = (hipStream_t)stream;
   if (t.fp8 && t.policy == TFD_POLICY_BF16) return launch_moe<true, false>(a, s);
   if (!t.fp8 && t.policy == TFD_POLICY_F32) return launch_moe<false, true>(a, s);

@@ -53,8 +53,9 @@ __device__ __forceinline__ int64_t xp_off(int m, int k) {
 template <int kCmax>
 __global__ __launch_bounds__(kWave) void k_rmsnorm_rows(const bf16* __restrict__ x, int ldx,
                                                         const bf16* __restrict__ gamma,
-                                                        bf16* __restrict__ out, int ldo, int n,
-                                                        float eps, int packed) {
+                                                        bf16* __restrict__ out_rows, int ldo,
+                                                        bf16* __restrict__ out_packed, int n,
+                                                        float eps) {
   const int lane = threadIdx.x;
   const int m = blockIdx.x;
   const bf16* xr_p = x + (int64_t)m * ldx;
@@ -65,8 +66,9 @@ __global__ __launch_bounds__(kWave) void k_rmsnorm_rows(const bf16* __restrict__
   for (int i = 0; i < kCmax; ++i) {
     const int c = i * kWave + lane;
     if (c < nch) {
-      bf16* o = packed ? out + xp_off(m, c * 8) : out + (int64_t)m * ldo + (int64_t)c * 8;
-      *reinterpret_cast<u32x4*>(o) = xr[i];
+      if (out_rows)
+        *reinterpret_cast<u32x4*>(out_rows + (int64_t)m * ldo + (int64_t)c * 8) = xr[i];
+      if (out_packed) *reinterpret_cast<u32x4*>(out_packed + xp_off(m, c * 8)) = xr[i];
     }
   }
 }
@@ -96,7 +98,10 @@ __global__ __launch_bounds__(kWave) void k_rmsnorm_rows(const bf16* __restrict__
 // does not depend on which slice finishes first -- applies the epilogue and
 // puts the counter back to zero for the next call.
 // ---------------------------------------------------------------------------
-enum SkinnyEpi { kSkStore = 0, kSkResid = 1, kSkSwiglu = 2, kSkLogits = 3, kSkResidF32 = 4 };
+// kSkResidScaled: out = bf16(resid + bf16(y * rmul)), a scaled residual add
+enum SkinnyEpi {
+  kSkStore = 0, kSkResid = 1, kSkSwiglu = 2, kSkLogits = 3, kSkResidF32 = 4, kSkResidScaled = 5
+};
 
 // Two shapes: Ks <= 1024 (66 KiB of LDS, two blocks of four waves per compute
 // unit, eight steps in flight per wave) and Ks <= 2048 (the head: one block of
@@ -107,7 +112,8 @@ enum SkinnyEpi { kSkStore = 0, kSkResid = 1, kSkSwiglu = 2, kSkLogits = 3, kSkRe
 template <int kEpi>
 __device__ __forceinline__ void skinny_store(const f32x4 (&c)[2], int halves, int tile, int lane,
                                              int M, int N, const bf16* __restrict__ resid,
-                                             int ldr, void* __restrict__ out, int ldo) {
+                                             int ldr, void* __restrict__ out, int ldo,
+                                             float rmul = 1.f) {
   const int r = lane & 15, kq = lane >> 4;
   const int n = tile * 16 + r;
   for (int h = 0; h < halves; ++h) {
@@ -129,6 +135,9 @@ __device__ __forceinline__ void skinny_store(const f32x4 (&c)[2], int halves, in
         else if (kEpi == kSkResidF32)   // f32 residual stream: out = resid + y (in place allowed)
           ((float*)out)[(int64_t)m * ldo + n] =
               reinterpret_cast<const float*>(resid)[(int64_t)m * ldr + n] + y;
+        else if (kEpi == kSkResidScaled)   // (in place allowed)
+          ((bf16*)out)[(int64_t)m * ldo + n] =
+              f2bf(bf2f(resid[(int64_t)m * ldr + n]) + rbf(y * rmul));
         else
           ((float*)out)[(int64_t)m * ldo + n] = y;
       }
@@ -350,7 +359,8 @@ template <int kEpi, int kT, int kKW, int kDepth, bool kFp8 = false, int kH = 2>
 __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
     const bf16* __restrict__ X, const void* __restrict__ W, int M, int K, int N,
     const bf16* __restrict__ resid, int ldr, void* __restrict__ out, int ldo,
-    const float* __restrict__ wscale, float* __restrict__ part, int* __restrict__ counters) {
+    const float* __restrict__ wscale, float* __restrict__ part, int* __restrict__ counters,
+    float rmul) {
   using WL = SkW<kFp8>;
   __shared__ f32x4 red[kKW][kT][2][kWave];
   const int lane = threadIdx.x & (kWave - 1);
@@ -463,7 +473,7 @@ __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
 #pragma unroll
       for (int e = 0; e < 4; ++e) sum[h][e] *= sc;
   }
-  skinny_store<kEpi>(sum, M > 16 ? 2 : 1, tile0 + t, lane, M, N, resid, ldr, out, ldo);
+  skinny_store<kEpi>(sum, M > 16 ? 2 : 1, tile0 + t, lane, M, N, resid, ldr, out, ldo, rmul);
 }
 
 // ---------------------------------------------------------------------------
@@ -703,10 +713,26 @@ int tfd_rmsnorm_rows_bf16(const void* x, int ldx, const void* gamma, void* out, 
     return fail(kBadShape, "rmsnorm_rows: rows=%d n=%d ldx=%d ldo=%d packed=%d", rows, n, ldx,
                 ldo, packed);
   auto s = (hipStream_t)stream;
+  bf16* o_rows = packed ? nullptr : (bf16*)out;
+  bf16* o_packed = packed ? (bf16*)out : nullptr;
   TFD_CMAX_SWITCH(n, hipLaunchKernelGGL((k_rmsnorm_rows<kC>), dim3(rows), dim3(kWave), 0, s,
-                                        (const bf16*)x, ldx, (const bf16*)gamma, (bf16*)out, ldo,
-                                        n, eps, packed));
+                                        (const bf16*)x, ldx, (const bf16*)gamma, o_rows, ldo,
+                                        o_packed, n, eps));
   return launched("rmsnorm_rows");
+}
+
+int tfd_rmsnorm_rows2_bf16(const void* x, int ldx, const void* gamma, void* out_rows, int ldo,
+                           void* out_packed, int rows, int n, float eps, void* stream) {
+  if (!x || !gamma || (!out_rows && !out_packed))
+    return fail(kBadArg, "rmsnorm_rows2: null pointer");
+  if (rows <= 0 || n <= 0 || n % 8 || ldx < n || ldx % 8 ||
+      (out_packed && (rows > kMaxRows || n % 32)) || (out_rows && (ldo < n || ldo % 8)))
+    return fail(kBadShape, "rmsnorm_rows2: rows=%d n=%d ldx=%d ldo=%d", rows, n, ldx, ldo);
+  auto s = (hipStream_t)stream;
+  TFD_CMAX_SWITCH(n, hipLaunchKernelGGL((k_rmsnorm_rows<kC>), dim3(rows), dim3(kWave), 0, s,
+                                        (const bf16*)x, ldx, (const bf16*)gamma, (bf16*)out_rows,
+                                        ldo, (bf16*)out_packed, n, eps));
+  return launched("rmsnorm_rows2");
 }
 
 }  // extern "C"
@@ -804,13 +830,18 @@ int tfd_pack_skinny_fp8(const void* w, int ldw, int N, int K, void* packed, void
   return launched("pack_skinny_fp8");
 }
 
-int tfd_gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M, int K, int N,
-                        int epilogue, const void* resid, int ldr, void* out, int ldo,
-                        void* stream) {
+// the scaled residual epilogue's code inside this file (not a public epilogue:
+// its multiplier comes through tfd_gemm_skinny_fp8_resid_scaled)
+constexpr int kEpiResidScaled = -1;
+
+static int gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M, int K, int N,
+                           int epilogue, const void* resid, int ldr, float rmul, void* out,
+                           int ldo, void* stream) {
   if (!x || !w || !scale || !out) return fail(kBadArg, "gemm_skinny_fp8: null pointer");
   if (M <= 0 || M > kMaxRows || K <= 0 || K % 256 || N <= 0)
     return fail(kBadShape, "gemm_skinny_fp8: M=%d (1..32) K=%d (multiple of 256) N=%d", M, K, N);
-  if ((epilogue == TFD_EPI_RESID || epilogue == TFD_EPI_RESID_F32) && (!resid || ldr < N))
+  if ((epilogue == TFD_EPI_RESID || epilogue == TFD_EPI_RESID_F32 ||
+       epilogue == kEpiResidScaled) && (!resid || ldr < N))
     return fail(kBadArg, "gemm_skinny_fp8: residual epilogue needs resid with ldr >= N");
   if (epilogue == TFD_EPI_SWIGLU ? (N % 2 || (N / 2) % 32) : ldo < N)
     return fail(kBadShape, "gemm_skinny_fp8: ldo=%d N=%d", ldo, N);
@@ -823,10 +854,10 @@ int tfd_gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M,
 #define TFD_KSPLIT8(EPI, D)                                                                   \
   if (M <= 16)                                                                                \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 8, D, true, 1>), grid, dim3(8 * kWave), 0, s, xb, \
-                       w, M, K, N, rb, ldr, out, ldo, scale, nullptr, nullptr);               \
+                       w, M, K, N, rb, ldr, out, ldo, scale, nullptr, nullptr, rmul);               \
   else                                                                                        \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 8, D, true, 2>), grid, dim3(8 * kWave), 0, s, xb, \
-                       w, M, K, N, rb, ldr, out, ldo, scale, nullptr, nullptr)
+                       w, M, K, N, rb, ldr, out, ldo, scale, nullptr, nullptr, rmul)
 #define TFD_KSPLIT8_EPI(EPI)                    \
   if (steps % 8 == 0) TFD_KSPLIT8(EPI, 8);      \
   else if (steps % 4 == 0) TFD_KSPLIT8(EPI, 4); \
@@ -838,12 +869,27 @@ int tfd_gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M,
     case TFD_EPI_SWIGLU: TFD_KSPLIT8_EPI(kSkSwiglu); break;
     case TFD_EPI_LOGITS: TFD_KSPLIT8_EPI(kSkLogits); break;
     case TFD_EPI_RESID_F32: TFD_KSPLIT8_EPI(kSkResidF32); break;
+    case kEpiResidScaled: TFD_KSPLIT8_EPI(kSkResidScaled); break;
     default:
       return fail(kBadArg, "gemm_skinny_fp8: epilogue %d", epilogue);
   }
 #undef TFD_KSPLIT8_EPI
 #undef TFD_KSPLIT8
   return launched("gemm_skinny_fp8");
+}
+
+int tfd_gemm_skinny_fp8(const void* x, const void* w, const float* scale, int M, int K, int N,
+                        int epilogue, const void* resid, int ldr, void* out, int ldo,
+                        void* stream) {
+  if (epilogue == kEpiResidScaled) return fail(kBadArg, "gemm_skinny_fp8: epilogue %d", epilogue);
+  return gemm_skinny_fp8(x, w, scale, M, K, N, epilogue, resid, ldr, 1.f, out, ldo, stream);
+}
+
+int tfd_gemm_skinny_fp8_resid_scaled(const void* x, const void* w, const float* scale, int M,
+                                     int K, int N, const void* resid, int ldr, float mult,
+                                     void* out, int ldo, void* stream) {
+  return gemm_skinny_fp8(x, w, scale, M, K, N, kEpiResidScaled, resid, ldr, mult, out, ldo,
+                         stream);
 }
 
 int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int epilogue,
@@ -888,17 +934,17 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
 #define TFD_KSPLIT(EPI, KT, D)                                                                  \
   if (M <= 16)                                                                                  \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D, false, 1>), grid, dim3(8 * kWave), 0, s,   \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, part, counters);            \
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, part, counters, 1.f);            \
   else                                                                                          \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D, false, 2>), grid, dim3(8 * kWave), 0, s,   \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, part, counters)
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, part, counters, 1.f)
 #define TFD_KSPLIT16(EPI, D)                                                                    \
   if (M <= 16)                                                                                  \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 16, D, false, 1>), grid, dim3(16 * kWave), 0, s,  \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, nullptr, nullptr);          \
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, nullptr, nullptr, 1.f);          \
   else                                                                                          \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 16, D, false, 2>), grid, dim3(16 * kWave), 0, s,  \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, nullptr, nullptr)
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, nullptr, nullptr, 1.f)
 #define TFD_KSPLIT_EPI(EPI)                              \
   if (wide && kt == 1 && steps16 % 8 == 0) TFD_KSPLIT16(EPI, 8); \
   else if (wide && kt == 1 && steps16 % 4 == 0) TFD_KSPLIT16(EPI, 4); \

@@ -9,10 +9,12 @@ per-channel fp8); the tied embedding / head table stays bf16.  Per layer:
 
 * input RMSNorm (operand order) -> fp8 in-projection -> Mamba2 step
   (``tfd_mamba_step``) or GQA decode (``tfd_gqa_decode``, no RoPE) -> fp8
-  out-projection -> ``a + b * residual_multiplier`` (``tfd_scaled_add_rows``);
-* post RMSNorm -> fp8 router -> routed experts + shared MLP
-  (``tfd_moe_experts``: top-10-then-softmax routing in its first launch, then fp8,
-  expert-grouped) -> the scaled residual again;
+  out-projection whose epilogue adds ``bf16(b * residual_multiplier)`` into the
+  stream (``tfd_gemm_skinny_fp8_resid_scaled``);
+* post RMSNorm in both layouts at once (``tfd_rmsnorm_rows2_bf16``) -> fp8 router
+  -> routed experts + shared MLP (``tfd_moe_experts``: top-10-then-softmax routing
+  in its first launch, then fp8, expert-grouped, its last launch adding the
+  scaled output into the stream);
 
 then the final norm, the head over the tied table, the greedy pick and the next
 token's embedding times ``embedding_multiplier``.  The head's division by
@@ -195,8 +197,6 @@ class GraniteEngine:
         self.nproj += (-self.nproj) % 8
         self.proj = z(B, self.nproj, dtype=BF)
         self.mix = z(32 * max(cfg.d_inner, cfg.heads * cfg.head_dim), dtype=BF)
-        self.tmp = z(B, H, dtype=BF)
-        self.moe_out = z(B, H)
         self.rlog = z(B, cfg.experts)
         self.rw = z(B, k)
         self.ridx = z(B, k, dtype=I32)
@@ -247,12 +247,14 @@ class GraniteEngine:
         self._lib.tfd_gemm_skinny_fp8(ptr(x), ptr(w), ptr(scale), self.B, K, N, epi, None, 0,
                                       ptr(out), ldo, s)
 
-    def _residual(self, b, b_f32, s):
-        """hidden = bf16(hidden + bf16(b * residual_multiplier))."""
+    def _gemm8_residual(self, x, w, scale, K, s):
+        """hidden = bf16(hidden + bf16((x @ w^T) * residual_multiplier)): the mixer's
+        out-projection and the residual add (model.py:502-508) in one launch."""
         H = self.cfg.hidden
-        self._lib.tfd_scaled_add_rows(ptr(self.hidden), H, ptr(b), H, b_f32,
-                                      self.cfg.residual_multiplier, ptr(self.hidden), H, self.B,
-                                      H, s)
+        self._lib.tfd_gemm_skinny_fp8_resid_scaled(ptr(x), ptr(w), ptr(scale), self.B, K, H,
+                                                   ptr(self.hidden), H,
+                                                   self.cfg.residual_multiplier,
+                                                   ptr(self.hidden), H, s)
 
     def _mamba(self, i, w, s, cur):
         cfg = self.cfg
@@ -293,7 +295,9 @@ class GraniteEngine:
         a.s_shared_in, a.s_shared_out = ptr(w["w_shared_in_scale"]), ptr(w["w_shared_out_scale"])
         a.hidden, a.shared_scale, a.partial = ptr(self.moe_hidden), ptr(self.moe_sscale), \
             ptr(self.moe_partial)
-        a.groups, a.out = ptr(self.moe_groups), ptr(self.moe_out)
+        # the experts' output goes straight into the residual stream, scaled
+        a.groups, a.out = ptr(self.moe_groups), None
+        a.resid, a.resid_mult = ptr(self.hidden), cfg.residual_multiplier
         a.rows, a.k, a.experts, a.hidden_size = self.B, cfg.top_k, cfg.experts, cfg.hidden
         a.inter, a.shared_inter, a.hidden_ld = cfg.moe_inter, cfg.shared_inter, self.moe_ld
         a.fp8, a.policy, a.err = 1, _lib.POLICY_BF16, ptr(self.err)
@@ -308,23 +312,19 @@ class GraniteEngine:
             self._gemm8(self.xn, w["w_in"], w["w_in_scale"], H, cfg.attn_in, _lib.EPI_STORE,
                         self.proj, self.nproj, s)
             self._attn(i, s)
-            self._gemm8(self.mix, w["w_out"], w["w_out_scale"], cfg.heads * cfg.head_dim, H,
-                        _lib.EPI_STORE, self.tmp, H, s)
+            self._gemm8_residual(self.mix, w["w_out"], w["w_out_scale"],
+                                 cfg.heads * cfg.head_dim, s)
         else:
             self._gemm8(self.xn, w["w_in"], w["w_in_scale"], H, cfg.mamba_in, _lib.EPI_STORE,
                         self.proj, self.nproj, s)
             self._mamba(i, w, s, cur)
-            self._gemm8(self.mix, w["w_out"], w["w_out_scale"], cfg.d_inner, H, _lib.EPI_STORE,
-                        self.tmp, H, s)
-        self._residual(self.tmp, 0, s)
-        L.tfd_rmsnorm_rows_bf16(ptr(self.hidden), H, ptr(w["gamma_post"]), ptr(self.xn), 0, B, H,
-                                cfg.eps, 1, s)
-        L.tfd_rmsnorm_rows_bf16(ptr(self.hidden), H, ptr(w["gamma_post"]), ptr(self.xm), H, B, H,
-                                cfg.eps, 0, s)
+            self._gemm8_residual(self.mix, w["w_out"], w["w_out_scale"], cfg.d_inner, s)
+        # post norm: row-major for the experts, operand order for the router
+        L.tfd_rmsnorm_rows2_bf16(ptr(self.hidden), H, ptr(w["gamma_post"]), ptr(self.xm), H,
+                                 ptr(self.xn), B, H, cfg.eps, s)
         self._gemm8(self.xn, w["w_router"], w["w_router_scale"], H, cfg.experts,
                     _lib.EPI_LOGITS, self.rlog, cfg.experts, s)
-        self._moe(w, s)                    # routes (top-10, softmax) inside the call
-        self._residual(self.moe_out, 1, s)
+        self._moe(w, s)                    # routes inside the call, adds into the stream
 
     def _step(self, cur):
         s = self._stream()
