@@ -24,8 +24,7 @@ extern "C" {
 #endif
 
 /* fp8-e4m3fn weights with one f32 scale per output row (workload C5's
- * "fp8 per-channel" projections; SURVEY entry gemv_fp8_perchannel).  The
- * reference has no fp8 GEMV: its Granite projections are bf16 nn.Linear
+ * "fp8 per-channel" projections).  The reference has no fp8 GEMV: its Granite projections are bf16 nn.Linear
  * (examples/granite_4_0_h_small-cuda/model.py:140-152 in_projection, :266-270
  * out_proj, :294-330 attention q/k/v/o, :459-471 shared MLP), so this build
  * defines W[n][k] = f32(e4m3fn(code[n][k])) * scale[n].
@@ -55,9 +54,9 @@ int tfd_gemm_skinny_fp8_resid_scaled(const void* x, const void* w, const float* 
  * -> weights f32 [rows][k] (C5: bf16 values) and expert ids int32 [rows][k],
  * largest first with ties to the lower id (torch.topk's order).
  * Replaces Qwen3_5Router.routing's softmax/topk/renormalise
- * (tests/models/qwen3_5_35b_a3b/model.py:355-366; torch_ref.py:417-430; SURVEY
- * entry moe_router_softmax_topk) and GraniteRouter.routing's topk/softmax
- * (examples/granite_4_0_h_small-cuda/model.py:376-390; moe_router_topk_softmax).
+ * (tests/models/qwen3_5_35b_a3b/model.py:355-366; torch_ref.py:417-430) and
+ * GraniteRouter.routing's topk/softmax
+ * (examples/granite_4_0_h_small-cuda/model.py:376-390).
  * The reference returns int64 ids; these are int32. */
 int tfd_route_topk(const float* logits, int ldl, int rows, int experts, int k, int mode,
                    float* weights, int32_t* idx, void* stream);
@@ -68,9 +67,8 @@ int tfd_route_topk(const float* logits, int ldl, int rows, int experts, int k, i
 /* Routed experts + shared expert of the MoE block for a batch, given the
  * routing (replaces Qwen3_5MoE.routed_experts/shared_expert/experts,
  * tests/models/qwen3_5_35b_a3b/model.py:383-456 / torch_ref.py:451-530, and
- * GraniteMoE.routed_experts/shared_mlp/experts, granite model.py:406-471; SURVEY
- * entries moe_experts_gateup / moe_experts_down).  Grouped by expert: each weight
- * row of a picked expert is read once per call however many sequences picked it.
+ * GraniteMoE.routed_experts/shared_mlp/experts, granite model.py:406-471).
+ * Grouped by expert: each weight row of a picked expert is read once per call however many sequences picked it.
  * Weights keep the reference's (out, in) rows: w_gate/w_up [E][I][H], w_down
  * [E][H][I]; the shared expert's gate rows then up rows in w_shared_in [2 IS][H]
  * and w_shared_out [H][IS].  With fp8 != 0 every weight is e4m3fn bytes with an
@@ -121,9 +119,8 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream);
 /* Gated DeltaNet at one token per sequence, everything between the in- and
  * out-projections of Qwen3_5LinearAttention.linear_attention: conv_step,
  * l2_normalise, beta/g, delta_step and the gated RMS norm
- * (tests/models/qwen3_5_35b_a3b/model.py:124-232; torch_ref.py:188-312; SURVEY
- * entry gdn_conv_delta).  proj f32 [rows][proj_ld] holds this token's
- * projections (bf16 values): the conv channels q|k|v (2 hk dk + hv dv), then z
+ * (tests/models/qwen3_5_35b_a3b/model.py:124-232; torch_ref.py:188-312).  proj
+ * f32 [rows][proj_ld] holds this token's projections (bf16 values): the conv channels q|k|v (2 hk dk + hv dv), then z
  * (hv dv), b (hv), a (hv).  conv_in/conv_out f32 [rows][CONV][3] (distinct
  * buffers: the window after this token goes to conv_out); state f32
  * [rows][hv][dk][dv] is updated in place.  out: the gated read-out in operand
@@ -143,8 +140,7 @@ int tfd_gdn_step(const TfdGdnArgs* args, void* stream);
 
 /* Mamba2 at one token per sequence, everything between in_proj and out_proj of
  * GraniteMamba.mamba_mixer: conv_step, ssm_step and gated_out's RMSNormGated
- * (examples/granite_4_0_h_small-cuda/model.py:154-270; SURVEY entries
- * mamba_conv / mamba_ssm / rmsnorm_gated).  proj bf16 [rows][proj_ld]: gate
+ * (examples/granite_4_0_h_small-cuda/model.py:154-270).  proj bf16 [rows][proj_ld]: gate
  * (EXP), the conv channels x|B|C (EXP + 2 ns), dt (heads); conv_in/conv_out bf16
  * [rows][CONV][3] (distinct); state f32 [rows][heads][64][128] in place.  Work:
  * gated f32 [rows][EXP], ssq f32 [rows][heads].  out: the normed gated output in
@@ -169,16 +165,16 @@ int tfd_mamba_step(const TfdMambaArgs* args, void* stream);
  * cache of tf_decode.h ([pages][kv_heads][16][head_dim], 16 positions a page),
  * after appending this token's key and value at pos[b].
  *  policy TFD_POLICY_F32 (C4, Qwen3_5FullAttention.full_attention,
- *    tests/models/qwen3_5_35b_a3b/model.py:234-346 / torch_ref.py:318-409; SURVEY
- *    entry attn_hd256_partial_rope): qkv f32 [rows][ldq] (bf16 values) holds per
+ *    tests/models/qwen3_5_35b_a3b/model.py:234-346 / torch_ref.py:318-409):
+ *    qkv f32 [rows][ldq] (bf16 values) holds per
  *    query head its query then its output gate (2 head_dim each), then the keys,
  *    then the values; per-head RMSNorm (gamma_q, gamma_k, flat), rotate-half
  *    RoPE on the first rot_dim dims (cos/sin bf16 [rope_rows][rot_dim]), query
  *    times `scale`, softmax, output times sigmoid(gate); all f32; the cache keeps
  *    bf16(k_rope).  head_dim 256, 8 query heads per kv head.
  *  policy TFD_POLICY_BF16 (C5, GraniteAttention.attend after cache_update,
- *    examples/granite_4_0_h_small-cuda/model.py:310-366; SURVEY entry
- *    attn_decode_nope): qkv bf16 [rows][ldq] = queries, keys, values; no
+ *    examples/granite_4_0_h_small-cuda/model.py:310-366):
+ *    qkv bf16 [rows][ldq] = queries, keys, values; no
  *    position embedding; score = bf16(sum bf16(q k)) * scale in f32, softmax f32
  *    rounded to bf16, attn = bf16(sum bf16(p v)).  head_dim 128, 4 query heads per
  *    kv head.  gamma/cos/sin unused.
