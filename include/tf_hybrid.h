@@ -24,8 +24,8 @@ extern "C" {
 #endif
 
 /* fp8-e4m3fn weights with one f32 scale per output row (workload C5's
- * "fp8 per-channel" projections).  The reference has no fp8 GEMV: its Granite projections are bf16 nn.Linear
- * (examples/granite_4_0_h_small-cuda/model.py:140-152 in_projection, :266-270
+ * "fp8 per-channel" projections).  The reference has no fp8 GEMV: its Granite
+ * projections are bf16 nn.Linear (examples/granite_4_0_h_small-cuda/model.py:140-152 in_projection, :266-270
  * out_proj, :294-330 attention q/k/v/o, :459-471 shared MLP), so this build
  * defines W[n][k] = f32(e4m3fn(code[n][k])) * scale[n].
  * tfd_pack_skinny_fp8 lays codes [N][K] (row stride ldw bytes) out in 512-byte
@@ -68,7 +68,8 @@ int tfd_route_topk(const float* logits, int ldl, int rows, int experts, int k, i
  * routing (replaces Qwen3_5MoE.routed_experts/shared_expert/experts,
  * tests/models/qwen3_5_35b_a3b/model.py:383-456 / torch_ref.py:451-530, and
  * GraniteMoE.routed_experts/shared_mlp/experts, granite model.py:406-471).
- * Grouped by expert: each weight row of a picked expert is read once per call however many sequences picked it.
+ * Grouped by expert: each weight row of a picked expert is read once per call
+ * however many sequences picked it.
  * Weights keep the reference's (out, in) rows: w_gate/w_up [E][I][H], w_down
  * [E][H][I]; the shared expert's gate rows then up rows in w_shared_in [2 IS][H]
  * and w_shared_out [H][IS].  With fp8 != 0 every weight is e4m3fn bytes with an
@@ -120,8 +121,8 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream);
  * out-projections of Qwen3_5LinearAttention.linear_attention: conv_step,
  * l2_normalise, beta/g, delta_step and the gated RMS norm
  * (tests/models/qwen3_5_35b_a3b/model.py:124-232; torch_ref.py:188-312).  proj
- * f32 [rows][proj_ld] holds this token's projections (bf16 values): the conv channels q|k|v (2 hk dk + hv dv), then z
- * (hv dv), b (hv), a (hv).  conv_in/conv_out f32 [rows][CONV][3] (distinct
+ * f32 [rows][proj_ld] holds this token's projections (bf16 values): the conv
+ * channels q|k|v (2 hk dk + hv dv), then z (hv dv), b (hv), a (hv).  conv_in/conv_out f32 [rows][CONV][3] (distinct
  * buffers: the window after this token goes to conv_out); state f32
  * [rows][hv][dk][dv] is updated in place.  out: the gated read-out in operand
  * order (32 x hv dv) for the out-projection.  dk = dv = 128, conv kernel 4. */
