@@ -25,8 +25,9 @@ extern "C" {
 
 /* fp8-e4m3fn weights with one f32 scale per output row (workload C5's
  * "fp8 per-channel" projections).  The reference has no fp8 GEMV: its Granite
- * projections are bf16 nn.Linear (examples/granite_4_0_h_small-cuda/model.py:140-152 in_projection, :266-270
- * out_proj, :294-330 attention q/k/v/o, :459-471 shared MLP), so this build
+ * projections are bf16 nn.Linear (examples/granite_4_0_h_small-cuda/
+ * model.py:140-152 in_projection, :266-270 out_proj, :294-330 attention
+ * q/k/v/o, :459-471 shared MLP), so this build
  * defines W[n][k] = f32(e4m3fn(code[n][k])) * scale[n].
  * tfd_pack_skinny_fp8 lays codes [N][K] (row stride ldw bytes) out in 512-byte
  * blocks of 16 rows x 32 k, the fp8 counterpart of tfd_pack_skinny_bf16; `packed`
@@ -122,7 +123,8 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream);
  * l2_normalise, beta/g, delta_step and the gated RMS norm
  * (tests/models/qwen3_5_35b_a3b/model.py:124-232; torch_ref.py:188-312).  proj
  * f32 [rows][proj_ld] holds this token's projections (bf16 values): the conv
- * channels q|k|v (2 hk dk + hv dv), then z (hv dv), b (hv), a (hv).  conv_in/conv_out f32 [rows][CONV][3] (distinct
+ * channels q|k|v (2 hk dk + hv dv), then z (hv dv), b (hv), a (hv).
+ * conv_in/conv_out f32 [rows][CONV][3] (distinct
  * buffers: the window after this token goes to conv_out); state f32
  * [rows][hv][dk][dv] is updated in place.  out: the gated read-out in operand
  * order (32 x hv dv) for the out-projection.  dk = dv = 128, conv kernel 4. */
