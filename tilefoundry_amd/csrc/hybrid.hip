@@ -272,8 +272,11 @@ __global__ __launch_bounds__(kGroupThreads) void k_moe_group(MoeArgs a) {
   }
 }
 
-// (expert, entries) of blockIdx.y: the picked experts, then the shared one.
-// kWho selects what a launch covers: 0 both (the shared expert is the last y),
+// (expert, entries) of blockIdx.y: the shared expert, then the picked ones.
+// The shared expert has an entry per sequence (its blocks loop longest), so it
+// comes first in dispatch order and overlaps the picked experts instead of
+// trailing them.  kWho selects what a launch covers: 0 both (the shared expert
+// is y = 0),
 // 1 the picked experts only, 2 the shared expert only (when its width differs
 // from the routed experts', each gets a launch sized for it).
 struct Group {
@@ -283,15 +286,16 @@ struct Group {
 };
 template <int kWho>
 __device__ __forceinline__ bool moe_group(const MoeArgs& a, Group& g) {
-  g.shared = kWho == 2 || (kWho == 0 && blockIdx.y == gridDim.y - 1);
+  g.shared = kWho == 2 || (kWho == 0 && blockIdx.y == 0);
   if (g.shared) {
     g.e = 0;
     g.count = a.B;
     g.entries = nullptr;
     return true;
   }
-  if ((int)blockIdx.y >= a.groups[0]) return false;
-  g.e = grp_picked(a)[blockIdx.y];
+  const int y = kWho == 0 ? (int)blockIdx.y - 1 : (int)blockIdx.y;
+  if (y >= a.groups[0]) return false;
+  g.e = grp_picked(a)[y];
   g.count = grp_count(a)[g.e];
   g.entries = grp_entries(a) + (int64_t)g.e * a.B;
   return true;
@@ -409,16 +413,20 @@ __global__ __launch_bounds__(kBlock) void k_moe_down(MoeArgs a) {
     }
     if (kFp8) ds[p] = g.shared ? a.s_sout[row] : a.s_down[base + row];
   }
-  for (int t = 0; t < g.count; ++t) {
+  // entry t's SwiGLU vector, and its products into its partial row
+  auto hload = [&](int t, u32x4 (&hr)[kC]) {
     int b, slot;
     moe_entry(a, g, t, b, slot);
     const bf16* hv = a.hidden + ((int64_t)b * (a.k + 1) + slot) * a.IM;
-    u32x4 hr[kC];
 #pragma unroll
     for (int i = 0; i < kC; ++i) {
       const int c = li + kDownLanes * i;
       hr[i] = c < nch ? load16(hv + (int64_t)c * 8) : u32x4{0u, 0u, 0u, 0u};
     }
+  };
+  auto products = [&](int t, const u32x4 (&hr)[kC]) {
+    int b, slot;
+    moe_entry(a, g, t, b, slot);
     float* prow = a.partial + ((int64_t)b * (a.k + 1) + slot) * a.H;
 #pragma unroll
     for (int p = 0; p < kP; ++p) {
@@ -430,6 +438,25 @@ __global__ __launch_bounds__(kBlock) void k_moe_down(MoeArgs a) {
       if (kFp8) d *= ds[p];
       const int n = n0 + p * kRpp + rsub;
       if (li == 0 && n < a.H) prow[n] = rbf(d);
+    }
+  };
+  if constexpr (kWho == 2) {
+    // the shared expert's launch: an entry per sequence, so the next entry's
+    // vector is requested before this one's products (the last request
+    // repeats the last entry, so every iteration issues the same loads)
+    u32x4 hr[kC], hn[kC];
+    hload(0, hr);
+    for (int t = 0; t < g.count; ++t) {
+      hload(t + 1 < g.count ? t + 1 : t, hn);
+      products(t, hr);
+#pragma unroll
+      for (int i = 0; i < kC; ++i) hr[i] = hn[i];
+    }
+  } else {
+    for (int t = 0; t < g.count; ++t) {
+      u32x4 hr[kC];
+      hload(t, hr);
+      products(t, hr);
     }
   }
 }
