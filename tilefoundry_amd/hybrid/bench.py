@@ -316,7 +316,7 @@ def run(config: str, reps: int) -> list[dict]:
         res.append(bench_moe(config, rows, reps, gen, hs=2048, inter=512, sh=512, experts=256,
                              k=8, fp8=False))
         res.append(bench_gqa(config, rows, reps, gen, heads=16, kv_heads=2, d=256, ctx=1024,
-                             f32=True, split_len=128))
+                             f32=True, split_len=64))
     elif config == "c5":
         rows = 8
         res.append(bench_mamba(config, rows, reps, gen))

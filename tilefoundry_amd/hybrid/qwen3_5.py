@@ -147,7 +147,7 @@ class Qwen35Engine:
 
     def __init__(self, cfg: Qwen35Config, weights: dict[str, torch.Tensor], *, rows: int,
                  device: str = "cuda:0", max_steps: int = 2112, page_seed: int = 0,
-                 split_len: int = 128, graph: bool = True):
+                 split_len: int = 64, graph: bool = True):
         if not 1 <= rows <= 32:
             raise ValueError("rows: 1..32 sequences")
         self.cfg, self.B, self.device = cfg, rows, device
