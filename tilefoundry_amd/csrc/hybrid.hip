@@ -542,6 +542,14 @@ __global__ __launch_bounds__(2 * kD) void k_gdn_step(GdnArgs a) {
   const float* cin = a.conv_in + (int64_t)b * conv * (kKW - 1);
   float* cout = a.conv_out + (int64_t)b * conv * (kKW - 1);
   __shared__ float q_s[kD], k_s[kD], v_s[kD], red[2][kD], sc[4];
+  // this thread's state column slice (thread (dv, half): key rows [half * kD/2,
+  // +kD/2)) is requested first, so it streams in while the prologue runs
+  const int dv = tid % kD, half = tid / kD;
+  constexpr int kRows = kD / 2;
+  float* st = a.state + (((int64_t)b * a.hv + hv) * kD + half * kRows) * kD + dv;
+  float s[kRows];
+#pragma unroll
+  for (int r = 0; r < kRows; ++r) s[r] = st[(int64_t)r * kD];
   // ---- conv + SiLU of this head's channels; q/k windows advance once per key head
   {
     const int d = tid % kD;
@@ -583,15 +591,11 @@ __global__ __launch_bounds__(2 * kD) void k_gdn_step(GdnArgs a) {
   }
   __syncthreads();
   // ---- the delta rule: thread (dv, half) over key rows [half * kD/2, +kD/2)
-  const int dv = tid % kD, half = tid / kD;
-  constexpr int kRows = kD / 2;
-  float* st = a.state + (((int64_t)b * a.hv + hv) * kD + half * kRows) * kD + dv;
   const float decay = sc[3], beta = sc[2];
-  float s[kRows];
   float rec = 0.f;
 #pragma unroll
   for (int r = 0; r < kRows; ++r) {
-    s[r] = st[(int64_t)r * kD] * decay;
+    s[r] *= decay;
     rec += s[r] * k_s[half * kRows + r];
   }
   red[half][dv] = rec;
