@@ -682,6 +682,14 @@ __global__ __launch_bounds__(kBlock) void k_mamba_step(MambaArgs a) {
   bf16* cout = a.conv_out + (int64_t)b * conv * (kKW - 1);
   __shared__ float x_s[kPD], b_s[kNS], c_s[kNS], dtv[2];
   __shared__ float ss_w[kWavesPerBlock];
+  // this thread's four state columns in every pass: 16-byte loads, a row's 32
+  // lanes contiguous, all passes' loads issued first (they stream in while the
+  // conv and dt prologue runs)
+  const int q = tid % kLpr, r0 = tid / kLpr;
+  float4* st = reinterpret_cast<float4*>(a.state + ((int64_t)b * a.nh + h) * kPD * kNS) + q;
+  float4 sv[kPass];
+#pragma unroll
+  for (int i = 0; i < kPass; ++i) sv[i] = st[(int64_t)(r0 + kRpp * i) * kLpr];
   for (int i = tid; i < kPD + 2 * kNS; i += kBlock) {
     const int ch = i < kPD ? h * kPD + i : exp_ + (i - kPD);
     const float m = conv_silu_bf16(cin + (int64_t)ch * (kKW - 1), a.conv_w + (int64_t)ch * kKW,
@@ -699,13 +707,6 @@ __global__ __launch_bounds__(kBlock) void k_mamba_step(MambaArgs a) {
     dtv[0] = dt;
     dtv[1] = expf(dt * -expf(bf2f(a.a_log[h])));
   }
-  // this thread's four state columns in every pass: 16-byte loads, a row's 32
-  // lanes contiguous, all passes' loads issued before the first is used
-  const int q = tid % kLpr, r0 = tid / kLpr;
-  float4* st = reinterpret_cast<float4*>(a.state + ((int64_t)b * a.nh + h) * kPD * kNS) + q;
-  float4 sv[kPass];
-#pragma unroll
-  for (int i = 0; i < kPass; ++i) sv[i] = st[(int64_t)(r0 + kRpp * i) * kLpr];
   __syncthreads();
   const float dt = dtv[0], decay = dtv[1];
   float dtb[4], cq[4];
