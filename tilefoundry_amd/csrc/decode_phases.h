@@ -49,78 +49,6 @@ __device__ __forceinline__ void gemv_issue(int vb, const bf16* __restrict__ W, i
   load_rows<kCmax, kR>(W, K, K / 8, row0, nvalid, lane, w);
 }
 
-// Rows [kLo, kHi) of gemv_issue's tile only, so a caller can spread one
-// tile's loads over several points of its schedule.
-template <int kCmax, int kR, int kLo, int kHi>
-__device__ __forceinline__ void gemv_issue_part(int vb, const bf16* __restrict__ W, int K, int N,
-                                                u32x4 (&w)[kR][kCmax]) {
-  static_assert(0 <= kLo && kLo < kHi && kHi <= kR, "row range");
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int64_t row0 = ((int64_t)vb * kWavesPerBlock + wave) * kR;
-  const int nch = K / 8;
-  const int nvalid = row0 >= N ? 0 : (int)((N - row0) < kR ? (N - row0) : kR);
-#pragma unroll
-  for (int r = kLo; r < kHi; ++r) {
-    if (nvalid == 0) {
-#pragma unroll
-      for (int i = 0; i < kCmax; ++i) w[r][i] = u32x4{0u, 0u, 0u, 0u};
-    } else {
-      const bf16* rowp = W + (row0 + (r < nvalid ? r : nvalid - 1)) * (int64_t)K;
-#pragma unroll
-      for (int i = 0; i < kCmax; ++i) {
-        const int c = i * kWave + lane;
-        w[r][i] = load16_stream(rowp + (int64_t)(c < nch ? c : nch - 1) * 8);
-      }
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// Rows [kLo, kHi) of gemv_issue's tile straight into LDS (no registers):
-// row r, chunk i of this wave lands at lds[((wave * kRl + r - kLo0) * kCmax + i) * 256
-// + 4 * lane] (u32 words), kRl rows per wave, kLo0 the first LDS-held row.
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
-typedef __attribute__((address_space(1))) void* global_void_ptr;
-
-template <int kCmax, int kR, int kRl, int kLo, int kHi>
-__device__ __forceinline__ void gemv_issue_lds(int vb, const bf16* __restrict__ W, int K, int N,
-                                               uint32_t* lds) {
-  static_assert(0 <= kLo && kLo < kHi && kHi <= kRl && kRl <= kR, "row range");
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int64_t row0 = ((int64_t)vb * kWavesPerBlock + wave) * kR;
-  const int nch = K / 8;
-  // rows past the end re-read the last valid row (never stored); a tile
-  // wholly past the end reads row 0 (never used)
-  const int nvalid = row0 >= N ? 1 : (int)((N - row0) < kR ? (N - row0) : kR);
-  const int64_t base = row0 >= N ? 0 : row0;
-#pragma unroll
-  for (int r = kLo; r < kHi; ++r) {
-    const bf16* rowp = W + (base + (r < nvalid ? r : nvalid - 1)) * (int64_t)K;
-#pragma unroll
-    for (int i = 0; i < kCmax; ++i) {
-      const int c = i * kWave + lane;
-      __builtin_amdgcn_global_load_lds(
-          (global_void_ptr)(rowp + (int64_t)(c < nch ? c : nch - 1) * 8),
-          (lds_void_ptr)(lds + ((wave * kRl + r) * kCmax + i) * 256), 16, 0, 0);
-    }
-  }
-}
-
-// Copy the LDS-held rows [0, kRl) of this wave's tile into registers.
-template <int kCmax, int kR, int kRl>
-__device__ __forceinline__ void gemv_tile_from_lds(const uint32_t* lds, u32x4 (&w)[kR][kCmax]) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-#pragma unroll
-  for (int r = 0; r < kRl; ++r)
-#pragma unroll
-    for (int i = 0; i < kCmax; ++i)
-      w[r][i] = *reinterpret_cast<const u32x4*>(lds + ((wave * kRl + r) * kCmax + i) * 256 +
-                                                4 * lane);
-}
-
 template <int kCmax, int kR, int kPro, int kEpi>
 __device__ __forceinline__ void gemv_finish(int vb, const bf16* __restrict__ x,
                                             const bf16* __restrict__ gamma,
