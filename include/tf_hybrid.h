@@ -48,6 +48,24 @@ int tfd_gemm_skinny_fp8_resid_scaled(const void* x, const void* w, const float* 
                                      int K, int N, const void* resid, int ldr, float mult,
                                      void* out, int ldo, void* stream);
 
+/* The HIR's rms_norm op on each of `rows` bf16 vectors of n values: out =
+ * bf16(f32(f32(x * rsqrt(mean(x^2) + eps)) * gamma)), one rounding (the evaluator's
+ * handler, src/tilefoundry/ir/hir/nn/rms_norm.py:103-110).  The Granite model writes
+ * its input, post-mixer and final norms this way (examples/granite_4_0_h_small-cuda/
+ * model.py:149, 291, 403, 632); the Qwen3 norm (tfd_rmsnorm_rows_bf16) rounds before
+ * gamma instead.  Written row-major to out_rows [rows][ldo] and/or in the skinny GEMMs'
+ * operand order to out_packed (rows <= 32, n % 32 == 0); NULL skips one. */
+int tfd_tf_rmsnorm_rows_bf16(const void* x, int ldx, const void* gamma, void* out_rows, int ldo,
+                             void* out_packed, int rows, int n, float eps, void* stream);
+
+/* The head over a published divisor: out (f32 [M][ldo]) = bf16(bf16(x . W[n]) / divisor),
+ * the product as tfd_gemm_skinny_bf16's TFD_EPI_LOGITS and its work buffer rules.
+ * Replaces Granite4_0_H_Small.lm_head's `logits / logits_scaling`
+ * (examples/granite_4_0_h_small-cuda/model.py:636-645). */
+int tfd_gemm_skinny_bf16_logits_div(const void* x, const void* w, int M, int K, int N,
+                                    float divisor, void* out, int ldo, float* work,
+                                    int64_t work_floats, void* stream);
+
 #define TFD_ROUTE_SOFTMAX_TOPK 0 /* C4: softmax over all experts, top k, renormalise */
 #define TFD_ROUTE_TOPK_SOFTMAX 1 /* C5: top k logits, softmax over them, bf16 weights */
 

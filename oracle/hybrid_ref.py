@@ -23,14 +23,32 @@ Every function cites the reference function it restates.  Matmul sums run in f64
 """
 from __future__ import annotations
 
+from contextlib import contextmanager
+
 import torch
 
 F32, BF16 = torch.float32, torch.bfloat16
 
+_ROUND = True
+
 
 def bf(x: torch.Tensor) -> torch.Tensor:
-    """Round to bf16 and hand back as f32."""
-    return x.to(BF16).float()
+    """Round to bf16 and hand back as f32 (inside ``unrounded()``: f32 as is)."""
+    return x.to(BF16).float() if _ROUND else x.float()
+
+
+@contextmanager
+def unrounded():
+    """Every bf16 rounding point of this module becomes the identity: the oracle
+    is then the models' f32 mathematics, the form an independent f32
+    implementation (Hugging Face's modules) is compared with to pin how the
+    whole steps compose their pieces."""
+    global _ROUND
+    old, _ROUND = _ROUND, False
+    try:
+        yield
+    finally:
+        _ROUND = old
 
 
 def mm_rows(w: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
@@ -322,7 +340,7 @@ def _rope_rows(theta, rot, rows):
     inv = 1.0 / theta ** (torch.arange(0, rot, 2, dtype=torch.float64) / rot)
     f = torch.arange(rows, dtype=torch.float64)[:, None] * inv[None]
     emb = torch.cat((f, f), dim=-1)
-    return emb.cos().to(BF16).float(), emb.sin().to(BF16).float()
+    return bf(emb.cos().float()), bf(emb.sin().float())
 
 
 class Qwen35Oracle:
@@ -398,12 +416,13 @@ class Qwen35Oracle:
 # ---------------------------------------------------------------------------
 # Whole decode steps of the C5 model (HIR policy, fp8 linear weights)
 # ---------------------------------------------------------------------------
-def rms_norm_hir(x, gamma, eps):
-    """``tf.rms_norm`` at bf16 (Qwen3RMSNorm order): bf16(bf16(x * rsqrt(mean(x^2)
-    + eps)) * gamma), the variance in f32."""
+def rms_norm_tf(x, gamma, eps):
+    """``tf.rms_norm`` as the evaluator values it (src/tilefoundry/ir/hir/nn/
+    rms_norm.py:103-110): x and gamma in f32, ``x * rsqrt(mean(x^2) + eps) * gamma``
+    in f32, rounded to bf16 once."""
     x32 = x.float()
-    var = (x32 * x32).mean(dim=-1, keepdim=True)
-    return bf(bf(x32 * torch.rsqrt(var + eps)) * gamma.float())
+    var = x32.pow(2).mean(dim=-1, keepdim=True)
+    return bf(x32 * torch.rsqrt(var + eps) * gamma.float())
 
 
 def _route_gap_ulps(rlog, k):
@@ -416,10 +435,9 @@ class GraniteOracle:
     """``Granite4_0_H_Small``'s decode step for a batch (examples/
     granite_4_0_h_small-cuda/model.py: embed :615-624, GraniteMamba :141-270,
     GraniteAttention :273-366, GraniteMoE :392-477, the layers' scaled residual
-    :480-523, final norm and head :626-645) at the HIR's bf16 rounding, with every
-    linear weight fp8 codes + f32 row scales (``gemv_fp8``) and the tied table
-    bf16.  The head's ``/ logits_scaling`` (a power of two) is left out, as the
-    engine leaves it out.  Weights under the names
+    :480-523, final norm and head :626-645, ``/ logits_scaling`` included) at the
+    HIR's bf16 rounding, with every linear weight fp8 codes + f32 row scales
+    (``gemv_fp8``) and the tied table bf16.  Weights under the names
     ``tilefoundry_amd.hybrid.granite`` uses, on the CPU."""
 
     def __init__(self, cfg, weights: dict, rows: int):
@@ -443,7 +461,7 @@ class GraniteOracle:
         for i in range(c.layers):
             W = lambda n: self.w[f"layer{i}.{n}"]
             lin = lambda n, x: bf(gemv_fp8(W(n), W(n + "_scale"), x))
-            xn = rms_norm_hir(hidden, W("gamma_in"), c.eps)
+            xn = rms_norm_tf(hidden, W("gamma_in"), c.eps)
             if c.is_attention(i):
                 HQ, HKV, D = c.heads, c.kv_heads, c.head_dim
                 qkv = lin("w_in", xn)
@@ -463,7 +481,7 @@ class GraniteOracle:
                     pd=c.mamba_head_dim, ns=c.d_state, ng=1, eps=c.eps)
                 mixed = lin("w_out", normed)
             hidden = bf(hidden + bf(mixed * c.residual_multiplier))
-            xm = rms_norm_hir(hidden, W("gamma_post"), c.eps)
+            xm = rms_norm_tf(hidden, W("gamma_post"), c.eps)
             rlog = lin("w_router", xm)
             gap = _route_gap_ulps(rlog, c.top_k)
             gaps = gap if gaps is None else torch.minimum(gaps, gap)
@@ -475,5 +493,5 @@ class GraniteOracle:
                          W("w_shared_out_scale"))
             hidden = bf(hidden + bf(moe * c.residual_multiplier))
         self.route_gaps.append(gaps)
-        hn = rms_norm_hir(hidden, self.w["gamma_final"], c.eps)
-        return bf(mm_rows(self.w["embed"].float(), hn))
+        hn = rms_norm_tf(hidden, self.w["gamma_final"], c.eps)
+        return bf(bf(mm_rows(self.w["embed"].float(), hn)) / c.logits_scaling)

@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS, EPI_RESID_F32 = 0, 1, 2, 3, 4
@@ -76,6 +76,8 @@ SIGNATURES: dict[str, list] = {
     "tfd_add_f32_rows": [P, I, P, I, I, I, P],
     "tfd_bf16_to_f32_rows": [P, I, P, I, I, I, P],
     "tfd_scaled_add_rows": [P, I, P, I, I, F, P, I, I, I, P],
+    "tfd_tf_rmsnorm_rows_bf16": [P, I, P, P, I, P, I, I, F, P],
+    "tfd_gemm_skinny_bf16_logits_div": [P, P, I, I, I, F, P, I, P, L, P],
 }
 RESTYPES = {"tfd_last_error": ctypes.c_char_p}
 UNCHECKED = {"tfd_abi_version", "tfd_decode_persistent_grid"}

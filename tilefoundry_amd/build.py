@@ -42,14 +42,35 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile every source into ``libtfdecode_gfx950.so`` (always recompiles)."""
+    """Compile every source into ``libtfdecode_gfx950.so`` (always recompiles):
+    one object per source, compiled side by side (no device code crosses a
+    source file, so no relocatable device code is needed), then one link."""
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, *[str(CSRC / s) for s in SOURCES], "-o", str(tmp)]
+    objdir = HERE / "_build"
+    objdir.mkdir(exist_ok=True)
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    jobs = []
+    for src in SOURCES:
+        obj = objdir / (Path(src).stem + ".o")
+        cmd = [hipcc(), *compile_flags, "-c", str(CSRC / src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        jobs.append((obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE,
+                                           text=True)))
+    objs, errors = [], []
+    for obj, proc in jobs:
+        _, err = proc.communicate()
+        if proc.returncode != 0:
+            errors.append(f"{obj.name}: hipcc failed ({proc.returncode}):\n{err[-4000:]}")
+        objs.append(str(obj))
+    if errors:
+        raise RuntimeError("\n".join(errors))
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
+        raise RuntimeError(f"link failed ({proc.returncode}):\n{proc.stderr[-4000:]}")
     os.replace(tmp, LIB)
     return LIB
 

@@ -224,7 +224,10 @@ __device__ __forceinline__ void load_x_coh(const bf16* __restrict__ x, int nch, 
 // computed by one wave over the whole vector.  Split in two so a caller can
 // issue the x / gamma loads, then its weight loads, and only then wait for x:
 // memory counters retire in order, so x must be requested first.
-template <int kCmax>
+// kSingle selects the HIR's own rms_norm op instead (src/tilefoundry/ir/hir/nn/
+// rms_norm.py:103-110: f32(f32(x * r) * gamma) rounded to bf16 once), the norm
+// the Granite model writes as tf.rms_norm.
+template <int kCmax, bool kSingle = false>
 __device__ __forceinline__ void rms_norm_apply(u32x4 (&xr)[kCmax], const u32x4 (&gr)[kCmax], int K,
                                                float eps) {
   float ss = 0.f;
@@ -247,15 +250,17 @@ __device__ __forceinline__ void rms_norm_apply(u32x4 (&xr)[kCmax], const u32x4 (
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float lo = rbf(rbf(bf_lo(w[e]) * r) * bf_lo(gw[e]));
-      const float hi = rbf(rbf(bf_hi(w[e]) * r) * bf_hi(gw[e]));
+      const float lo = kSingle ? (bf_lo(w[e]) * r) * bf_lo(gw[e])
+                               : rbf(rbf(bf_lo(w[e]) * r) * bf_lo(gw[e]));
+      const float hi = kSingle ? (bf_hi(w[e]) * r) * bf_hi(gw[e])
+                               : rbf(rbf(bf_hi(w[e]) * r) * bf_hi(gw[e]));
       o[e] = pack2(lo, hi);
     }
     xr[i] = u32x4{o[0], o[1], o[2], o[3]};   // chunks past K stay zero (0 * r * 0)
   }
 }
 
-template <int kCmax>
+template <int kCmax, bool kSingle = false>
 __device__ __forceinline__ void rms_norm_x(const bf16* __restrict__ x,
                                            const bf16* __restrict__ gamma, int K, float eps,
                                            int lane, u32x4 (&xr)[kCmax]) {
@@ -263,7 +268,7 @@ __device__ __forceinline__ void rms_norm_x(const bf16* __restrict__ x,
   u32x4 gr[kCmax];
   load_x<kCmax>(x, nch, lane, xr);
   load_x<kCmax>(gamma, nch, lane, gr);
-  rms_norm_apply<kCmax>(xr, gr, K, eps);
+  rms_norm_apply<kCmax, kSingle>(xr, gr, K, eps);
 }
 
 // Issue the loads of kR consecutive rows of W (row-major [N][K] bf16): lane l

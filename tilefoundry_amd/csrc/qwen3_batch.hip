@@ -48,9 +48,10 @@ __device__ __forceinline__ int64_t xp_off(int m, int k) {
 
 // ---------------------------------------------------------------------------
 // Row-wise RMSNorm (model.py:125-137 on each sequence's hidden state): one
-// wave per row, the batch-1 arithmetic.
+// wave per row, the batch-1 arithmetic.  kSingle: the HIR's rms_norm op
+// (ir/hir/nn/rms_norm.py:103-110, one rounding after gamma).
 // ---------------------------------------------------------------------------
-template <int kCmax>
+template <int kCmax, bool kSingle = false>
 __global__ __launch_bounds__(kWave) void k_rmsnorm_rows(const bf16* __restrict__ x, int ldx,
                                                         const bf16* __restrict__ gamma,
                                                         bf16* __restrict__ out_rows, int ldo,
@@ -60,7 +61,7 @@ __global__ __launch_bounds__(kWave) void k_rmsnorm_rows(const bf16* __restrict__
   const int m = blockIdx.x;
   const bf16* xr_p = x + (int64_t)m * ldx;
   u32x4 xr[kCmax];
-  rms_norm_x<kCmax>(xr_p, gamma, n, eps, lane, xr);
+  rms_norm_x<kCmax, kSingle>(xr_p, gamma, n, eps, lane, xr);
   const int nch = n / 8;
 #pragma unroll
   for (int i = 0; i < kCmax; ++i) {
@@ -98,9 +99,11 @@ __global__ __launch_bounds__(kWave) void k_rmsnorm_rows(const bf16* __restrict__
 // does not depend on which slice finishes first -- applies the epilogue and
 // puts the counter back to zero for the next call.
 // ---------------------------------------------------------------------------
-// kSkResidScaled: out = bf16(resid + bf16(y * rmul)), a scaled residual add
+// kSkResidScaled: out = bf16(resid + bf16(y * rmul)), a scaled residual add;
+// kSkLogitsDiv: out (f32) = bf16(y / rmul), logits over a published divisor
 enum SkinnyEpi {
-  kSkStore = 0, kSkResid = 1, kSkSwiglu = 2, kSkLogits = 3, kSkResidF32 = 4, kSkResidScaled = 5
+  kSkStore = 0, kSkResid = 1, kSkSwiglu = 2, kSkLogits = 3, kSkResidF32 = 4, kSkResidScaled = 5,
+  kSkLogitsDiv = 6
 };
 
 // Two shapes: Ks <= 1024 (66 KiB of LDS, two blocks of four waves per compute
@@ -138,6 +141,8 @@ __device__ __forceinline__ void skinny_store(const f32x4 (&c)[2], int halves, in
         else if (kEpi == kSkResidScaled)   // (in place allowed)
           ((bf16*)out)[(int64_t)m * ldo + n] =
               f2bf(bf2f(resid[(int64_t)m * ldr + n]) + rbf(y * rmul));
+        else if (kEpi == kSkLogitsDiv)
+          ((float*)out)[(int64_t)m * ldo + n] = rbf(y / rmul);
         else
           ((float*)out)[(int64_t)m * ldo + n] = y;
       }
@@ -168,7 +173,7 @@ template <int kEpi, int kKsMax, int kWaves, int kDepth>
 __global__ __launch_bounds__(kWaves * kWave) void k_gemm_skinny(
     const bf16* __restrict__ X, const bf16* __restrict__ W, int M, int K, int N, int Ks,
     const bf16* __restrict__ resid, int ldr, void* __restrict__ out, int ldo,
-    float* __restrict__ part, int* __restrict__ counters) {
+    float* __restrict__ part, int* __restrict__ counters, float rmul) {
   constexpr int kThreads = kWaves * kWave;
   __shared__ __align__(16) bf16 xs[32 * kKsMax];
   const int lane = threadIdx.x & (kWave - 1);
@@ -289,7 +294,7 @@ __global__ __launch_bounds__(kWaves * kWave) void k_gemm_skinny(
         if (lane == 0) coh_sti(&counters[tile], 0);
       }
     }
-    if (mine) skinny_store<kEpi>(c, halves, tile, lane, M, N, resid, ldr, out, ldo);
+    if (mine) skinny_store<kEpi>(c, halves, tile, lane, M, N, resid, ldr, out, ldo, rmul);
   }
 }
 
@@ -735,6 +740,20 @@ int tfd_rmsnorm_rows2_bf16(const void* x, int ldx, const void* gamma, void* out_
   return launched("rmsnorm_rows2");
 }
 
+int tfd_tf_rmsnorm_rows_bf16(const void* x, int ldx, const void* gamma, void* out_rows, int ldo,
+                             void* out_packed, int rows, int n, float eps, void* stream) {
+  if (!x || !gamma || (!out_rows && !out_packed))
+    return fail(kBadArg, "tf_rmsnorm_rows: null pointer");
+  if (rows <= 0 || n <= 0 || n % 8 || ldx < n || ldx % 8 ||
+      (out_packed && (rows > kMaxRows || n % 32)) || (out_rows && (ldo < n || ldo % 8)))
+    return fail(kBadShape, "tf_rmsnorm_rows: rows=%d n=%d ldx=%d ldo=%d", rows, n, ldx, ldo);
+  auto s = (hipStream_t)stream;
+  TFD_CMAX_SWITCH(n, hipLaunchKernelGGL((k_rmsnorm_rows<kC, true>), dim3(rows), dim3(kWave), 0,
+                                        s, (const bf16*)x, ldx, (const bf16*)gamma,
+                                        (bf16*)out_rows, ldo, (bf16*)out_packed, n, eps));
+  return launched("tf_rmsnorm_rows");
+}
+
 }  // extern "C"
 
 namespace {
@@ -895,9 +914,15 @@ int tfd_gemm_skinny_fp8_resid_scaled(const void* x, const void* w, const float* 
                          stream);
 }
 
-int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int epilogue,
-                         const void* resid, int ldr, void* out, int ldo, float* work,
-                         int64_t work_floats, void* stream) {
+}  // extern "C"
+
+namespace {
+
+constexpr int kEpiLogitsDiv = -2;   // internal: tfd_gemm_skinny_bf16_logits_div
+
+int gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int epilogue,
+                     const void* resid, int ldr, void* out, int ldo, float* work,
+                     int64_t work_floats, float rmul, void* stream) {
   if (!x || !w || !out) return fail(kBadArg, "gemm_skinny: null pointer");
   if (M <= 0 || M > kMaxRows || K <= 0 || K % 256 || N <= 0)
     return fail(kBadShape, "gemm_skinny: M=%d (1..32) K=%d (multiple of 256) N=%d", M, K, N);
@@ -937,17 +962,17 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
 #define TFD_KSPLIT(EPI, KT, D)                                                                  \
   if (M <= 16)                                                                                  \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D, false, 1>), grid, dim3(8 * kWave), 0, s,   \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, part, counters, 1.f);            \
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, part, counters, rmul);           \
   else                                                                                          \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, KT, 8, D, false, 2>), grid, dim3(8 * kWave), 0, s,   \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, part, counters, 1.f)
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, part, counters, rmul)
 #define TFD_KSPLIT16(EPI, D)                                                                    \
   if (M <= 16)                                                                                  \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 16, D, false, 1>), grid, dim3(16 * kWave), 0, s,  \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, nullptr, nullptr, 1.f);          \
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, nullptr, nullptr, rmul);         \
   else                                                                                          \
     hipLaunchKernelGGL((k_gemm_ksplit<EPI, 1, 16, D, false, 2>), grid, dim3(16 * kWave), 0, s,  \
-                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, nullptr, nullptr, 1.f)
+                       xb, wb, M, K, N, rb, ldr, out, ldo, nullptr, nullptr, nullptr, rmul)
 #define TFD_KSPLIT_EPI(EPI)                              \
   if (wide && kt == 1 && steps16 % 8 == 0) TFD_KSPLIT16(EPI, 8); \
   else if (wide && kt == 1 && steps16 % 4 == 0) TFD_KSPLIT16(EPI, 4); \
@@ -962,6 +987,7 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
       case TFD_EPI_SWIGLU: TFD_KSPLIT_EPI(kSkSwiglu); break;
       case TFD_EPI_LOGITS: TFD_KSPLIT_EPI(kSkLogits); break;
       case TFD_EPI_RESID_F32: TFD_KSPLIT_EPI(kSkResidF32); break;
+      case kEpiLogitsDiv: TFD_KSPLIT_EPI(kSkLogitsDiv); break;
       default:
         return fail(kBadArg, "gemm_skinny: epilogue %d", epilogue);
     }
@@ -983,24 +1009,45 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
 #define TFD_SKINNY_LAUNCH(EPI)                                                                \
   if (plan.wide && plan.Ks % 512 == 0)                                                        \
     hipLaunchKernelGGL((k_gemm_skinny<EPI, 2048, 8, 16>), grid, dim3(8 * kWave), 0, s, xb,    \
-                       wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);              \
+                       wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters, rmul);        \
   else if (plan.wide)                                                                         \
     hipLaunchKernelGGL((k_gemm_skinny<EPI, 2048, 8, 8>), grid, dim3(8 * kWave), 0, s, xb,     \
-                       wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);              \
+                       wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters, rmul);        \
   else                                                                                        \
     hipLaunchKernelGGL((k_gemm_skinny<EPI, 1024, 4, 8>), grid, dim3(4 * kWave), 0, s, xb,     \
-                       wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters);
+                       wb, M, K, N, plan.Ks, rb, ldr, out, ldo, part, counters, rmul);
   switch (epilogue) {
     case TFD_EPI_STORE: TFD_SKINNY_LAUNCH(kSkStore); break;
     case TFD_EPI_RESID: TFD_SKINNY_LAUNCH(kSkResid); break;
     case TFD_EPI_SWIGLU: TFD_SKINNY_LAUNCH(kSkSwiglu); break;
     case TFD_EPI_LOGITS: TFD_SKINNY_LAUNCH(kSkLogits); break;
     case TFD_EPI_RESID_F32: TFD_SKINNY_LAUNCH(kSkResidF32); break;
+    case kEpiLogitsDiv: TFD_SKINNY_LAUNCH(kSkLogitsDiv); break;
     default:
       return fail(kBadArg, "gemm_skinny: epilogue %d", epilogue);
   }
 #undef TFD_SKINNY_LAUNCH
   return launched("gemm_skinny");
+}
+
+}  // namespace
+
+extern "C" {
+
+int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int epilogue,
+                         const void* resid, int ldr, void* out, int ldo, float* work,
+                         int64_t work_floats, void* stream) {
+  if (epilogue == kEpiLogitsDiv) return fail(kBadArg, "gemm_skinny: epilogue %d", epilogue);
+  return gemm_skinny_bf16(x, w, M, K, N, epilogue, resid, ldr, out, ldo, work, work_floats, 1.f,
+                          stream);
+}
+
+int tfd_gemm_skinny_bf16_logits_div(const void* x, const void* w, int M, int K, int N,
+                                    float divisor, void* out, int ldo, float* work,
+                                    int64_t work_floats, void* stream) {
+  if (!(divisor > 0.f)) return fail(kBadArg, "gemm_skinny_logits_div: divisor %g", divisor);
+  return gemm_skinny_bf16(x, w, M, K, N, kEpiLogitsDiv, nullptr, 0, out, ldo, work, work_floats,
+                          divisor, stream);
 }
 
 int tfd_attn_rope_scores_paged_batched(

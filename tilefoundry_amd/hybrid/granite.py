@@ -7,19 +7,19 @@ stream, every bf16 op rounded as written, f32 where the HIR casts.  The linear
 weights are fp8-e4m3fn with one f32 scale per output row (the workload's
 per-channel fp8); the tied embedding / head table stays bf16.  Per layer:
 
-* input RMSNorm (operand order) -> fp8 in-projection -> Mamba2 step
+* input RMSNorm (the HIR's ``tf.rms_norm``: one rounding after gamma, in operand
+  order) -> fp8 in-projection -> Mamba2 step
   (``tfd_mamba_step``) or GQA decode (``tfd_gqa_decode``, no RoPE) -> fp8
   out-projection whose epilogue adds ``bf16(b * residual_multiplier)`` into the
   stream (``tfd_gemm_skinny_fp8_resid_scaled``);
-* post RMSNorm in both layouts at once (``tfd_rmsnorm_rows2_bf16``) -> fp8 router
+* post RMSNorm in both layouts at once (``tfd_tf_rmsnorm_rows_bf16``) -> fp8 router
   -> routed experts + shared MLP (``tfd_moe_experts``: top-10-then-softmax routing
   in its first launch, then fp8, expert-grouped, its last launch adding the
   scaled output into the stream);
 
-then the final norm, the head over the tied table, the greedy pick and the next
-token's embedding times ``embedding_multiplier``.  The head's division by
-``logits_scaling`` (16, a power of two: exact in bf16 and order-preserving) is
-left out of the logits buffer; the pick is the same.  Sequences (up to 32) step
+then the final norm, the head over the tied table divided by ``logits_scaling``
+(``tfd_gemm_skinny_bf16_logits_div``, model.py:636-645), the greedy pick and the
+next token's embedding times ``embedding_multiplier``.  Sequences (up to 32) step
 together; a step is recorded into two HIP graphs (the conv windows ping-pong).
 Weights are synthetic (random init on the device).
 """
@@ -306,8 +306,8 @@ class GraniteEngine:
 
     def _layer(self, i, s, cur):
         cfg, L, w, B, H = self.cfg, self._lib, self.layers[i], self.B, self.cfg.hidden
-        L.tfd_rmsnorm_rows_bf16(ptr(self.hidden), H, ptr(w["gamma_in"]), ptr(self.xn), 0, B, H,
-                                cfg.eps, 1, s)
+        L.tfd_tf_rmsnorm_rows_bf16(ptr(self.hidden), H, ptr(w["gamma_in"]), None, 0,
+                                   ptr(self.xn), B, H, cfg.eps, s)
         if cfg.is_attention(i):
             self._gemm8(self.xn, w["w_in"], w["w_in_scale"], H, cfg.attn_in, _lib.EPI_STORE,
                         self.proj, self.nproj, s)
@@ -320,8 +320,8 @@ class GraniteEngine:
             self._mamba(i, w, s, cur)
             self._gemm8_residual(self.mix, w["w_out"], w["w_out_scale"], cfg.d_inner, s)
         # post norm: row-major for the experts, operand order for the router
-        L.tfd_rmsnorm_rows2_bf16(ptr(self.hidden), H, ptr(w["gamma_post"]), ptr(self.xm), H,
-                                 ptr(self.xn), B, H, cfg.eps, s)
+        L.tfd_tf_rmsnorm_rows_bf16(ptr(self.hidden), H, ptr(w["gamma_post"]), ptr(self.xm), H,
+                                   ptr(self.xn), B, H, cfg.eps, s)
         self._gemm8(self.xn, w["w_router"], w["w_router_scale"], H, cfg.experts,
                     _lib.EPI_LOGITS, self.rlog, cfg.experts, s)
         self._moe(w, s)                    # routes inside the call, adds into the stream
@@ -333,10 +333,11 @@ class GraniteEngine:
                               ptr(self.hidden), H, B, H, s)
         for i in range(cfg.layers):
             self._layer(i, s, cur)
-        L.tfd_rmsnorm_rows_bf16(ptr(self.hidden), H, ptr(self.gamma_final), ptr(self.xn), 0, B,
-                                H, cfg.eps, 1, s)
-        L.tfd_gemm_skinny_bf16(ptr(self.xn), ptr(self.head), B, H, V, _lib.EPI_LOGITS, None, 0,
-                               ptr(self.logits), V, ptr(self.work), self.work.numel(), s)
+        L.tfd_tf_rmsnorm_rows_bf16(ptr(self.hidden), H, ptr(self.gamma_final), None, 0,
+                                   ptr(self.xn), B, H, cfg.eps, s)
+        L.tfd_gemm_skinny_bf16_logits_div(ptr(self.xn), ptr(self.head), B, H, V,
+                                          cfg.logits_scaling, ptr(self.logits), V,
+                                          ptr(self.work), self.work.numel(), s)
         L.tfd_argmax_rows(ptr(self.logits), V, B, V, ptr(self.pick), ptr(self.argmax_work), s)
         L.tfd_finalize_rows(ptr(self.pick), B, ptr(self.inp), self.nsteps, ptr(self.plen),
                             ptr(self.ids), ptr(self.pos), ptr(self.sam), self.nsteps,
