@@ -63,10 +63,12 @@ def test_c2_full_depth_against_golden(gpu_device, norms):
         print(f"[golden] norms={norms} mode={mode}", flush=True)
 
         # full logits of steps 0 and 63 (teacher-forced on the golden tokens)
+        noise_max = 0.0
         for k in (0, STEPS - 1):
             ref = _golden_logits(norms, k)
             exact = _bf16_npy(f"c2_{norms}_exact_step{k}.npy")
             noise = float((ref - exact).abs().max())
+            noise_max = max(noise_max, noise)
             got = eng.logits_for(prompt + gold["tokens"][:k]).float().cpu()
             err_exact = float((got - exact).abs().max())
             err_oracle = float((got - ref).abs().max())
@@ -75,20 +77,28 @@ def test_c2_full_depth_against_golden(gpu_device, norms):
                   f"max|engine-oracle| {err_oracle:.4g}; bound {bound:.4g}", flush=True)
             assert err_exact <= bound, (mode, k, err_exact, bound)
 
-        # teacher-forced: every step's pick, and its top-8 logits
+        # teacher-forced: every step's pick and its top-8 logits.  A pick that
+        # differs from the golden one is allowed only where the golden gap
+        # between the two is within twice this step's measured error on the
+        # top-8 logits (both logits moved by at most that much)
         seq = prompt + gold["tokens"][:STEPS - 1]
-        eng.generate(seq, 1)
-        picks = eng.sam[len(prompt) - 1: len(prompt) - 1 + STEPS].tolist()
-        ties = 0
+        picks, tf_logits = eng.walk(seq, len(prompt) - 1, STEPS)
+        ties = close = 0
         for k in range(STEPS):
             top8 = gold["top8"][k]
+            eps = _top8_error(tf_logits[k], top8)
+            # the bar, or twice the oracle's own summation-order noise where that
+            # is larger (measured at steps 0 and 63; see the module docstring)
+            assert eps <= max(TOL * abs(top8[0][1]), 2 * noise_max), (mode, k, eps)
+            close += gold["margins"][k] <= 2 * eps
             if picks[k] == gold["tokens"][k]:
                 continue
             vals = dict((i, v) for i, v in top8)
             assert picks[k] in vals, (mode, k, picks[k], top8)
             gap = vals[gold["tokens"][k]] - vals[picks[k]]
-            assert gap <= 2 * TOL * abs(top8[0][1]), (mode, k, gap)
+            assert gap <= 2 * eps + 1e-12, (mode, k, gap, eps)
             ties += 1
+        assert ties <= close, (mode, ties, close)
 
         # free-running greedy from the prompt
         run = eng.generate(prompt, STEPS, record_logits=True)
@@ -106,8 +116,10 @@ def test_c2_full_depth_against_golden(gpu_device, norms):
             eps = _top8_error(run.logits[k], top8)
             gap = vals[gold["tokens"][k]] - vals[mine]
             assert gap <= 2 * eps + 1e-12, (mode, k, gap, eps, gold["margins"][k])
+        margins = sorted(gold["margins"])
         print(f"  free-running identical for {STEPS if first is None else first} of {STEPS} "
-              f"steps; teacher-forced near-tie picks {ties}; golden min margin "
-              f"{min(gold['margins']):.4g}", flush=True)
+              f"steps; teacher-forced near-tie picks {ties} (steps with golden margin within "
+              f"twice the error: {close}); golden margins min {margins[0]:.4g}, 10th "
+              f"{margins[6]:.4g}, median {margins[32]:.4g}", flush=True)
         del eng
         torch.cuda.empty_cache()

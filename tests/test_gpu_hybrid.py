@@ -134,6 +134,54 @@ def test_rmsnorm_rows2_writes_both_layouts(gpu_device):
     assert o_rows.abs().sum() > 0
 
 
+@pytest.mark.parametrize("rows", [1, 8])
+def test_tf_rmsnorm_rows_rounds_once(gpu_device, rows):
+    """tfd_tf_rmsnorm_rows_bf16 (the HIR's rms_norm op, used by the Granite engine):
+    every output within one bf16 ulp of the evaluator's formula (f32, one rounding:
+    the oracle's rms_norm_tf) and >= 99% equal to it, in both layouts."""
+    g = torch.Generator().manual_seed(13 + rows)
+    n, dev = 4096, "cuda:0"
+    x = H.bf(torch.randn(rows, n, generator=g) * 3)
+    gamma = H.bf(1 + 0.3 * torch.randn(n, generator=g))
+    want = H.rms_norm_tf(x, gamma, 1e-5)
+    xd, gd = x.to(BF).to(dev), gamma.to(BF).to(dev)
+    o_rows = torch.zeros(rows, n, dtype=BF, device=dev)
+    o_pk = torch.zeros(32 * n, dtype=BF, device=dev)
+    rc = lib().tfd_tf_rmsnorm_rows_bf16(ptr(xd), n, ptr(gd), ptr(o_rows), n, ptr(o_pk), rows, n,
+                                        1e-5, _stream())
+    assert rc == 0
+    torch.cuda.synchronize()
+    got = o_rows.float().cpu()
+    assert torch.equal(from_operand_order(o_pk, rows, n).float().cpu(), got)
+    assert ((got - want).abs() <= ulp_bf16(want)).all()
+    assert (got == want).float().mean() >= 0.99
+
+
+@pytest.mark.parametrize("M,V", [(1, 4096), (8, 100352)])
+def test_head_logits_divided_by_logits_scaling(gpu_device, M, V):
+    """tfd_gemm_skinny_bf16_logits_div (Granite's lm_head / logits_scaling):
+    exactly the TFD_EPI_LOGITS logits rounded and divided by 16 (a power of two,
+    so exactly logits / 16)."""
+    g = torch.Generator().manual_seed(21)
+    K, dev = 4096, "cuda:0"
+    x = H.bf(torch.randn(M, K, generator=g)).to(BF).to(dev)
+    w = (torch.randn(V, K, generator=g) * 0.02).to(BF).to(dev)
+    packed = torch.empty(-(-V // 16) * 16 * K, dtype=BF, device=dev)
+    L, s = lib(), _stream()
+    L.tfd_pack_skinny_bf16(ptr(w), K, V, K, ptr(packed), s)
+    xo = operand_order(x)
+    work = torch.zeros(1 << 21, dtype=torch.float32, device=dev)
+    plain = torch.zeros(M, V, device=dev)
+    scaled = torch.zeros(M, V, device=dev)
+    assert L.tfd_gemm_skinny_bf16(ptr(xo), ptr(packed), M, K, V, _lib.EPI_LOGITS, None, 0,
+                                  ptr(plain), V, ptr(work), work.numel(), s) == 0
+    assert L.tfd_gemm_skinny_bf16_logits_div(ptr(xo), ptr(packed), M, K, V, 16.0, ptr(scaled),
+                                             V, ptr(work), work.numel(), s) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(scaled, plain / 16)
+    assert plain.abs().max() > 0
+
+
 def test_fp8_pack_layout(gpu_device):
     """Block (tile t, step s) is 512 bytes; lane l's 8 codes are
     W[16t + l % 16][32s + 8(l // 16) + j]; padding rows are 0."""
@@ -589,12 +637,15 @@ def test_gqa_decode_c4(gpu_device, pos, split_len):
 
 
 @pytest.mark.parametrize("pos,split_len", [([0, 1, 2, 100, 255, 256, 1000, 2000], 256),
-                                           ([1999], 16), ([37], 512)])
+                                           ([1999], 16), ([37], 512),
+                                           ([8191, 8192, 8000, 4095, 8191, 6000, 8190, 7777],
+                                            256)])
 def test_gqa_decode_c5(gpu_device, pos, split_len):
-    """Granite attention: 32 q / 8 kv heads of 128, no RoPE, HIR rounding."""
+    """Granite attention: 32 q / 8 kv heads of 128, no RoPE, HIR rounding; up to
+    the workload's depth (8 rows at 8,192-token contexts)."""
     g = torch.Generator().manual_seed(len(pos) * 100 + pos[0] + split_len)
     B, HQ, HKV, D = len(pos), 32, 8, 128
-    max_pages = 128
+    max_pages = max(128, -(-(max(pos) + 1) // 16))
     q = H.bf(torch.randn(B, HQ, D, generator=g))
     k = H.bf(torch.randn(B, HKV, D, generator=g))
     v = H.bf(torch.randn(B, HKV, D, generator=g))

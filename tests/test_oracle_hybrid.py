@@ -336,3 +336,18 @@ def test_attend_with_no_past_returns_this_tokens_value():
                              cos, sin, 0.25)
     want = kv[1][0].repeat_interleave(2, dim=0) * torch.sigmoid(qg[0, :, 16:])
     assert torch.equal(got[0], want.reshape(-1))
+
+
+def test_rms_norm_tf_rounds_once_like_torch_rms_norm():
+    """``tf.rms_norm`` (the evaluator's handler, ir/hir/nn/rms_norm.py:103-110)
+    is torch's own fused f32 ``rms_norm`` cast to bf16 once; the Qwen3-order
+    norm (rounded before gamma) differs from it on many elements."""
+    g = torch.Generator().manual_seed(12)
+    x = H.bf(torch.randn(6, 4096, generator=g) * 3)
+    gamma = H.bf(1 + 0.3 * torch.randn(4096, generator=g))
+    got = H.rms_norm_tf(x, gamma, 1e-5)
+    want = F.rms_norm(x, (4096,), gamma, 1e-5).to(torch.bfloat16).float()
+    assert torch.equal(got, want)
+    r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)
+    twice = H.bf(H.bf(x * r) * gamma)
+    assert (twice != want).float().mean() > 0.05

@@ -23,7 +23,7 @@ import torch
 from .. import _lib
 from .._lib import lib, ptr
 from .config import Qwen3Config
-from .engine import bf16_scale
+from .engine import bf16_scale, scatter_cache
 from .weights import head_rows, pack_layer, validate
 
 MAX_BATCH = 32
@@ -257,6 +257,33 @@ class BatchEngine:
             lens.append(len(p))
         self.plen.copy_(torch.tensor(lens, dtype=torch.int32))
         self.ids.copy_(torch.tensor([p[0] for p in prompts], dtype=torch.int64))
+        self._lib.tfd_embed_rows_bf16(ptr(self.w_embed), ptr(self.ids), ptr(self.hid), self.H,
+                                      self.B, self.H, self.V, ptr(self.err), self._stream())
+
+    def place_context(self, k_caches, v_caches, tokens: list[int]):
+        """Stand in for walked contexts without walking them: sequence b's cache
+        rows 0 .. P_b - 1 of layer i become ``k_caches[i][b]`` /
+        ``v_caches[i][b]`` ([P_b][HKV][D] bf16, through its page-table row), and
+        the next step decodes ``tokens[b]`` at position P_b (the oracle's
+        ``forward`` with the same caches, model.py:307-317)."""
+        if len(tokens) != self.B or len(k_caches) != self.L or len(v_caches) != self.L:
+            raise ValueError(f"place_context: {self.B} sequences x {self.L} layers of caches")
+        lens = [int(c.shape[0]) for c in k_caches[0]]
+        if max(lens) + 1 > self.nsteps:
+            raise ValueError(f"place_context: a position past this engine's {self.nsteps}")
+        if any(not 0 <= int(t) < self.V for t in tokens):
+            raise ValueError(f"place_context: token ids must lie in [0, {self.V})")
+        self._reset()
+        self.inp.zero_()
+        for b, (P, t) in enumerate(zip(lens, tokens)):
+            self.inp[b, P] = int(t)
+        self.plen.copy_(torch.tensor([P + 1 for P in lens], dtype=torch.int32))
+        self.pos.copy_(torch.tensor(lens, dtype=torch.int32))
+        self.ids.copy_(torch.tensor([int(t) for t in tokens], dtype=torch.int64))
+        for b in range(self.B):
+            scatter_cache(self.kpool, self.vpool, self.page_table[b],
+                          [k_caches[i][b] for i in range(self.L)],
+                          [v_caches[i][b] for i in range(self.L)])
         self._lib.tfd_embed_rows_bf16(ptr(self.w_embed), ptr(self.ids), ptr(self.hid), self.H,
                                       self.B, self.H, self.V, ptr(self.err), self._stream())
 

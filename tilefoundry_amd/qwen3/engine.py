@@ -47,6 +47,21 @@ class Generated:
         return len(self.tokens) / self.seconds if self.seconds > 0 else float("inf")
 
 
+def scatter_cache(kpool, vpool, page_table, k_caches, v_caches):
+    """Write contiguous caches into paged pools: position p of a sequence is row
+    p % 16 of page ``page_table[p // 16]`` (per layer i, pools [L][pages][HKV]
+    [16][D], caches [P][HKV][D])."""
+    for i, (kc, vc) in enumerate(zip(k_caches, v_caches)):
+        P = int(kc.shape[0])
+        if P == 0:
+            continue
+        pos = torch.arange(P, device=kpool.device)
+        pages = page_table[pos // _lib.PAGE_SIZE].long()
+        rows = pos % _lib.PAGE_SIZE
+        kpool[i][pages, :, rows] = kc.to(kpool.device, kpool.dtype)
+        vpool[i][pages, :, rows] = vc.to(vpool.device, vpool.dtype)
+
+
 def _round_up(n: int, m: int) -> int:
     return (n + m - 1) // m * m
 
@@ -364,6 +379,48 @@ class Engine:
         self.check_errors()
         out = self.sam[pl - 1: pl - 1 + max_new].tolist()
         return Generated(out, t2 - t1, t1 - t0, pl, None if hist is None else hist.cpu())
+
+    def place_context(self, k_caches, v_caches, token: int):
+        """Stand in for a walked context without walking it: layer i's cache
+        rows 0 .. P-1 become ``k_caches[i]`` / ``v_caches[i]`` ([P][HKV][D] bf16,
+        written through the page table), and the next step decodes *token* at
+        position P -- the step the oracle's ``forward`` takes with the same caches
+        (model.py:307-317).  Run it with ``run_steps(1)``; ``logits`` then hold
+        its logits."""
+        P = int(k_caches[0].shape[0])
+        if len(k_caches) != self.L or len(v_caches) != self.L:
+            raise ValueError(f"place_context: need {self.L} layers of caches")
+        if P + 1 > self.nsteps:
+            raise ValueError(f"place_context: position {P} past this engine's {self.nsteps}")
+        if not 0 <= int(token) < self.V:
+            raise ValueError(f"place_context: token {token} outside [0, {self.V})")
+        self._reset()
+        self.inp.zero_()
+        self.inp[P] = int(token)
+        self.plen.fill_(P + 1)
+        self.ids.fill_(int(token))
+        self.pos.fill_(P)
+        scatter_cache(self.kpool, self.vpool, self.page_table, k_caches, v_caches)
+        self._embed_current()
+
+    def walk(self, seq: list[int], start: int, steps: int):
+        """Teacher-forced: feed *seq* token by token, untimed, and record the
+        steps at positions start .. start + steps - 1 -> (the engine's pick at
+        each, its logits [steps][V] f32 on the host).  The pick at position p
+        predicts seq[p + 1]; *seq* needs start + steps tokens."""
+        if start < 0 or steps < 1 or start + steps > len(seq):
+            raise ValueError(f"walk: start {start} + steps {steps} past {len(seq)} tokens")
+        if len(seq) > self.nsteps:
+            raise ValueError(f"walk: {len(seq)} tokens exceed this engine's {self.nsteps} steps")
+        self._load_prompt(seq)
+        self.run_steps(start)
+        hist = torch.empty(steps, self.V, device=self.device, dtype=torch.float32)
+        for k in range(steps):
+            self.replay()
+            hist[k].copy_(self.logits)
+        torch.cuda.synchronize(self.device)
+        self.check_errors()
+        return self.sam[start:start + steps].tolist(), hist.cpu()
 
     def logits_for(self, prompt_ids: list[int]) -> torch.Tensor:
         """The logits after consuming every token of *prompt_ids* (f32 copy)."""
