@@ -5,9 +5,11 @@
 A step is one decode token: every layer, the head, the greedy pick.  The
 workload is C2: bf16 weights drawn N(0, 0.02) from seed 0
 (every parameter, norm scales included), tied embeddings, a 32-token
-uniform-random prompt (seed 0), a 16-token-page KV cache, and `--steps` greedy
-new tokens (2048 by default) timed after the prompt walk.  Weights are resident
-in HBM before the timed region starts.
+uniform-random prompt (seed 0), a 16-token-page KV cache, and 2048 greedy new
+tokens (positions 31..2078).  `--steps N` times the LAST N tokens of that run
+(N = 2048, the default, times all of them; the first 2048 - N are decoded
+untimed first), so every timed step works at the context depth the workload
+gives it.  Weights are resident in HBM before the timed region starts.
 
 Modes: "persistent" (default) runs all the steps in one launch of the
 persistent decode kernel; "graph" replays a captured graph of per-phase
@@ -82,9 +84,10 @@ def time_gate_up(eng, rounds: int) -> float:
 
 
 class LaunchClock:
-    """HIP events on the launch stream around every persistent launch of *eng*,
-    with the algorithmic bytes of each (weights once per step + the KV every
-    step reads and writes at its position)."""
+    """HIP events on the launch stream around the persistent launches of *eng*
+    made while ``armed`` (the timed region's), with the algorithmic bytes of
+    each (weights once per step + the KV every step reads and writes at its
+    position)."""
 
     def __init__(self, eng):
         import torch
@@ -92,11 +95,16 @@ class LaunchClock:
         self.eng, self.torch = eng, torch
         self.records = []          # (start event, end event, bytes)
         self.pos = 0
+        self.armed = False
         launch, load = eng._launch_persistent, eng._load_prompt
 
         def timed_launch(n):
             w = eng.weight_bytes_per_step()
             nbytes = sum(w + eng.kv_bytes_at(p) for p in range(self.pos, self.pos + n))
+            self.pos += n
+            if not self.armed:
+                launch(n)
+                return
             stream = torch.cuda.current_stream(eng.device)
             a = torch.cuda.Event(enable_timing=True)
             b = torch.cuda.Event(enable_timing=True)
@@ -104,7 +112,6 @@ class LaunchClock:
             launch(n)
             b.record(stream)
             self.records.append((a, b, nbytes))
-            self.pos += n
 
         def timed_load(prompt_ids):
             self.pos = 0
@@ -122,18 +129,20 @@ class LaunchClock:
 
 
 def traffic_ratio(kernel: str):
-    """HBM bytes moved per algorithmic byte for *kernel*, from the committed
-    rocprofv3 counter summary (profiles/hbm_traffic.json: FETCH_SIZE and
-    WRITE_SIZE of one profiled launch, scaled by what the same counters read for
-    a plain copy of known size), or None when no profile is committed."""
+    """(HBM bytes moved per algorithmic byte for *kernel*, a description of the
+    run they were counted on) from the committed rocprofv3 counter summary
+    (profiles/hbm_traffic.json: FETCH_SIZE and WRITE_SIZE of one profiled
+    launch, scaled by what the same counters read for a plain copy of known
+    size), or (None, None) when no profile is committed."""
     path = ROOT / "profiles" / "hbm_traffic.json"
     if not path.exists():
-        return None
+        return None, None
     try:
         entry = json.loads(path.read_text()).get(kernel)
-        return float(entry["hbm_bytes"]) / float(entry["algorithmic_bytes"])
+        ratio = float(entry["hbm_bytes"]) / float(entry["algorithmic_bytes"])
+        return ratio, "counted on " + entry.get("launch", "a committed counter run")
     except (ValueError, KeyError, TypeError, ZeroDivisionError, AttributeError):
-        return None
+        return None, None
 
 
 def copy_probe(nbytes: int = 1 << 30) -> int:
@@ -158,7 +167,7 @@ def cpu_baseline(weights, prompt, budget_s: float) -> dict:
 
     from oracle import qwen3_hir as O
 
-    threads = min(16, os.cpu_count() or 1)
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     orc = O.Qwen3Oracle(O.C2, weights)
     caches = orc.init_caches()
@@ -322,8 +331,9 @@ def main(argv=None) -> int:
     weights = synthetic_weights(cfg, seed=0)
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, cfg.vocab_size, (32,), generator=g).tolist()
-    max_new = max(args.steps, 2048)
-    eng = Engine(cfg, weights, device="cuda:0", max_new=max_new, prompt_room=len(prompt),
+    run_len = max(args.steps, 2048)            # new tokens of the whole run
+    skip = run_len - args.steps                 # decoded untimed before the timed ones
+    eng = Engine(cfg, weights, device="cuda:0", max_new=run_len, prompt_room=len(prompt),
                  mode=args.mode)
     clock = LaunchClock(eng) if args.mode == "persistent" else None
     print(f"[bench] weights + engine + capture {time.perf_counter() - t0:.1f}s", file=sys.stderr,
@@ -331,22 +341,28 @@ def main(argv=None) -> int:
 
     # untimed warmup: a short generation from the same prompt
     if args.warmup:
-        eng.generate(prompt, min(args.warmup, max_new))
-    # the timed region: walk the prompt (untimed), then exactly --steps replays
+        eng.generate(prompt, min(args.warmup, run_len))
+    # the timed region: walk the prompt and the first `skip` new tokens
+    # (untimed), then exactly --steps steps
+    pl = len(prompt)
     eng._load_prompt(prompt)
-    eng.run_steps(len(prompt) - 1)
+    eng.run_steps(pl - 1 + skip)
     torch.cuda.synchronize()
+    if clock is not None:
+        clock.armed = True
     start = time.perf_counter()
     eng.run_steps(args.steps)
     torch.cuda.synchronize()
     seconds = time.perf_counter() - start
+    if clock is not None:
+        clock.armed = False
     eng.check_errors()
-    tokens = eng.sam[len(prompt) - 1: len(prompt) - 1 + args.steps].tolist()
+    first_pos = pl - 1 + skip
+    tokens = eng.sam[first_pos: first_pos + args.steps].tolist()
 
     # algorithmic bytes: weights once per step + K/V of every position read and the new one written
-    pl = len(prompt)
     w_bytes = cfg.weight_bytes_per_step()
-    kv_bytes = sum(eng.kv_bytes_at(p) for p in range(pl - 1, pl - 1 + args.steps))
+    kv_bytes = sum(eng.kv_bytes_at(p) for p in range(first_pos, first_pos + args.steps))
     step_bytes = w_bytes + kv_bytes / args.steps
     tok_s = args.steps / seconds
     step_bw = step_bytes * tok_s
@@ -354,12 +370,15 @@ def main(argv=None) -> int:
     if clock is not None:
         launches, bytes_per_launch, launch_s = clock.summary()
         kernel = "k_decode_persistent<4,12,128,2>"
-        ratio = traffic_ratio(kernel)
+        ratio, counted_on = traffic_ratio(kernel)
         bw = bytes_per_launch / launch_s
         roofline = {"bound": "hbm", "kernel": f"{kernel} (whole decode steps per launch)",
                     "achieved": round(bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                     "frac": round(bw / HBM_PEAK, 4),
                     "traffic": None if ratio is None else round(ratio * bytes_per_launch),
+                    "traffic_source": None if ratio is None else
+                    f"committed counter ratio {ratio:.4f} (HBM bytes per algorithmic byte, "
+                    f"{counted_on}) times this launch's algorithmic bytes",
                     "bytes_per_launch": int(bytes_per_launch),
                     "avg_launch_ms": round(launch_s * 1e3, 3), "launches": launches}
     else:
@@ -386,9 +405,12 @@ def main(argv=None) -> int:
         "dtype": "bf16",
         "data": "synthetic (random-init N(0,0.02) weights seed 0, random 32-token prompt)",
         "config": {"workload": "C2: Qwen3-1.7B-arch bf16 decode, batch 1, 32-token prompt, "
-                               f"{args.steps} greedy new tokens, 16-token KV pages",
+                               f"{run_len} greedy new tokens, 16-token KV pages; timed: new "
+                               f"tokens {skip + 1}..{run_len} (positions {first_pos}.."
+                               f"{first_pos + args.steps - 1})",
                    "mode": args.mode,
-                   "batch": 1, "prompt": pl, "new_tokens": args.steps,
+                   "batch": 1, "prompt": pl, "new_tokens": run_len,
+                   "timed_positions": [first_pos, first_pos + args.steps - 1],
                    "layers": cfg.num_hidden_layers, "hidden": cfg.hidden_size,
                    "vocab": cfg.vocab_size},
         "step_roofline": {"bound": "hbm", "bytes_per_step": int(step_bytes),
