@@ -176,6 +176,20 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
                          const void* resid, int ldr, void* out, int ldo, float* work,
                          int64_t work_floats, void* stream);
 
+/* tfd_gemm_skinny_bf16 that allocates nothing and takes no work buffer.  It has no
+ * counterpart in the reference: it is for callers that cannot allocate (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  Its K-split
+ * work (TFD_SKINNY_COUNTERS tile counters + 2^21 f32 partials, about 8 MiB) is a
+ * device array inside the library, one per GPU, held until the process ends; the
+ * first call on a device looks it up and clears its counters on `stream`.  The same
+ * shapes and epilogues as tfd_gemm_skinny_bf16 (TFD_EPI_*), the results of that entry
+ * with a work buffer of the same size (a K split across blocks is planned within the
+ * scratch, with fewer slices where more would not fit).  Calls that overlap on one GPU
+ * share the array and race: keep them stream-ordered. */
+int tfd_gemm_skinny_bf16_noalloc(const void* x, const void* w, int M, int K, int N,
+                                 int epilogue, const void* resid, int ldr, void* out, int ldo,
+                                 void* stream);
+
 /* tfd_attn_rope_scores_paged for `batch` sequences at once (grid nsplit x kv_heads x
  * batch): sequence b reads QKV row b (stride ldq) at its own position pos[b] and
  * page-table row b; its workspaces are the single-sequence ones at b * (their size).

@@ -20,6 +20,7 @@ EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS, EPI_RESID_F32 = 0, 1, 2, 3, 4
 ERR_TOKEN_RANGE, ERR_POS_RANGE, ERR_PAGE_RANGE, ERR_STEP_RANGE, ERR_SYNC = 1, 2, 4, 8, 16
 PAGE_SIZE = 16
 SKINNY_COUNTERS = 16384     # tile counters at the start of a skinny-GEMM work buffer
+NOALLOC_SCRATCH_FLOATS = SKINNY_COUNTERS + (1 << 21)   # tfd_gemm_skinny_bf16_noalloc's scratch
 ARGMAX_WORK = 128           # int32 per row of tfd_argmax_rows' two-stage work buffer
 ATTN_SPLIT = 64
 ROUTE_SOFTMAX_TOPK, ROUTE_TOPK_SOFTMAX = 0, 1
@@ -54,6 +55,7 @@ SIGNATURES: dict[str, list] = {
     "tfd_rmsnorm_rows2_bf16": [P, I, P, P, I, P, I, I, F, P],
     "tfd_pack_skinny_bf16": [P, I, I, I, P, P],
     "tfd_gemm_skinny_bf16": [P, P, I, I, I, I, P, I, P, I, P, L, P],
+    "tfd_gemm_skinny_bf16_noalloc": [P, P, I, I, I, I, P, I, P, I, P],
     "tfd_attn_rope_scores_paged_batched": [P, I, P, P, P, P, I, P, P, I, P, P, I, I, I, I, I, F,
                                            F, P, I, P, P, I, I, P, P],
     "tfd_attn_pv_combine_paged_batched": [P, I, P, P, I, P, I, I, I, I, I, P, I, P, P, P, P, I,

@@ -18,6 +18,7 @@
 // and per step: rmsnorm_rows (final), gemm_skinny<LOGITS> (bf16-valued f32
 // logits), argmax_rows, finalize_rows (pick, next token, position, embedding).
 
+#include <mutex>
 #include <type_traits>
 
 #include "decode_phases.h"
@@ -1148,6 +1149,89 @@ int tfd_embed_rows_bf16(const void* table, const int64_t* ids, void* out, int ld
   hipLaunchKernelGGL(k_embed_rows, dim3(rows), dim3(kBlock), 0, (hipStream_t)stream,
                      (const bf16*)table, ids, (bf16*)out, ldo, hidden, vocab, err);
   return launched("embed_rows");
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// The skinny GEMM for callers that cannot allocate (code under graph capture,
+// serving loops, harnesses that forbid hipMalloc): its K-split work -- tile
+// counters and f32 partial tiles -- lives in a file-scope device array instead
+// of a caller-supplied buffer.  Each device holds its own copy of the array for
+// the life of the process; its address on the current device is looked up once
+// (hipGetSymbolAddress: the array's name is not a device address in host code)
+// and its counters are cleared once by a fill kernel on the caller's stream
+// (not a memset: such nodes misbehave under graph replay).  Every call leaves
+// the counters it used at zero, as with a caller's buffer.  Calls that overlap
+// on one device share the array and race.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kScratchPartials = (int64_t)1 << 21;            // 8 MiB of f32 tiles
+constexpr int64_t kScratchFloats = kSkCounters + kScratchPartials;
+
+__device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kScratchDevices = 64;
+float* g_scratch[kScratchDevices] = {};
+std::mutex g_scratch_lock;
+
+__global__ __launch_bounds__(kBlock) void k_zero_words(float* __restrict__ p, int n) {
+  for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) p[i] = 0.f;
+}
+
+// The current device's scratch, set up on first use; nullptr (rc set by fail())
+// when that fails.
+float* scratch_on_device(hipStream_t s, int& rc) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    rc = fail((int)e, "gemm_skinny_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kScratchDevices) {
+    rc = fail(kUnsupported, "gemm_skinny_noalloc: device %d past the %d this library tracks",
+              dev, kScratchDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      rc = fail(e != hipSuccess ? (int)e : kUnsupported,
+                "gemm_skinny_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return nullptr;
+    }
+    hipLaunchKernelGGL(k_zero_words, dim3((kSkCounters + kBlock - 1) / kBlock), dim3(kBlock), 0,
+                       s, (float*)p, (int)kSkCounters);
+    rc = launched("gemm_skinny_noalloc: counter clear");
+    if (rc) return nullptr;
+    g_scratch[dev] = (float*)p;
+  }
+  return g_scratch[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int tfd_gemm_skinny_bf16_noalloc(const void* x, const void* w, int M, int K, int N,
+                                 int epilogue, const void* resid, int ldr, void* out, int ldo,
+                                 void* stream) {
+  if (M <= 0 || M > kMaxRows || K <= 0 || K % 256 || N <= 0)
+    return fail(kBadShape, "gemm_skinny_noalloc: M=%d (1..32) K=%d (multiple of 256) N=%d", M,
+                K, N);
+  // No shape needs more than the scratch: K deeper than one LDS stage goes to the
+  // K-split kernel, which needs no partials, and a split across blocks is
+  // planned within the scratch's size (fewer slices when it would not fit), as
+  // the work-buffer entry plans within its caller's buffer.
+  if (epilogue == kEpiLogitsDiv) return fail(kBadArg, "gemm_skinny_noalloc: epilogue %d", epilogue);
+  int rc = 0;
+  float* work = scratch_on_device((hipStream_t)stream, rc);
+  if (!work) return rc;
+  return gemm_skinny_bf16(x, w, M, K, N, epilogue, resid, ldr, out, ldo, work, kScratchFloats,
+                          1.f, stream);
 }
 
 }  // extern "C"
