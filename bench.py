@@ -303,9 +303,10 @@ def main(argv=None) -> int:
     ap.add_argument("--kernel-rounds", type=int, default=20)
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration) and exit")
-    ap.add_argument("--mode", default="persistent", choices=("persistent", "graph"),
-                    help="persistent: one cooperative launch per run of steps; graph: a "
-                         "captured graph of per-phase launches replayed per token")
+    ap.add_argument("--mode", default="persistent", choices=("persistent", "xcd", "graph"),
+                    help="persistent: one cooperative launch per run of steps; xcd: the same "
+                         "with each layer split over the 8 XCDs; graph: a captured graph of "
+                         "per-phase launches replayed per token")
     ap.add_argument("--config", default="c2", choices=("c2", "c3"),
                     help="c2: the headline batch-1 workload; c3: batch 32 over 4096-token "
                          "contexts")
@@ -335,7 +336,7 @@ def main(argv=None) -> int:
     skip = run_len - args.steps                 # decoded untimed before the timed ones
     eng = Engine(cfg, weights, device="cuda:0", max_new=run_len, prompt_room=len(prompt),
                  mode=args.mode)
-    clock = LaunchClock(eng) if args.mode == "persistent" else None
+    clock = LaunchClock(eng) if args.mode in ("persistent", "xcd") else None
     print(f"[bench] weights + engine + capture {time.perf_counter() - t0:.1f}s", file=sys.stderr,
           flush=True)
 
@@ -369,7 +370,7 @@ def main(argv=None) -> int:
 
     if clock is not None:
         launches, bytes_per_launch, launch_s = clock.summary()
-        kernel = "k_decode_persistent<4,12,128,2>"
+        kernel = "k_decode_persistent<4,12,128,2>" if args.mode == "persistent" else "k_decode_xcd"
         ratio, counted_on = traffic_ratio(kernel)
         bw = bytes_per_launch / launch_s
         roofline = {"bound": "hbm", "kernel": f"{kernel} (whole decode steps per launch)",

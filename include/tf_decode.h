@@ -307,6 +307,7 @@ typedef struct TfdDecodeArgs {
 #define TFD_TAGS_PER_STEP(n_layers) ((n_layers) + 1)
 
 #define TFD_ERR_SYNC 16 /* a wait for another block's data passed its bound; the launch gave up */
+#define TFD_ERR_PLACEMENT 32 /* tfd_decode_xcd: a block ran on another XCD than block % 8 */
 
 /* Run `steps` decode steps in one launch.  nblocks <= 0 picks one block per
  * compute unit.  Returns -3 if the shape has no persistent instance (hidden
@@ -314,6 +315,31 @@ typedef struct TfdDecodeArgs {
 int tfd_decode_persistent(const TfdDecodeArgs* args, int steps, int nblocks, void* stream);
 /* The grid tfd_decode_persistent(args, ., 0, .) uses (x_best must hold 2x this many words). */
 int tfd_decode_persistent_grid(void);
+
+/* The exchange buffers of tfd_decode_xcd beyond those of TfdDecodeArgs (flag-in-data
+ * words as there; zero once, tags from args->epoch).  Per XCD x of the 8: */
+typedef struct TfdXcdArgs {
+  uint32_t* hid;   /* [8][H/2]: the hidden state entering a layer, XCD x's copy at x * H/2 */
+  uint32_t* h1;    /* [8][H/2]: after attention and its residual */
+  uint32_t* opart; /* [8][H]: XCD x's partial o-projection sums (f32) */
+  uint32_t* dpart; /* [8][H]: XCD x's partial down-projection sums (f32) */
+  uint32_t* smax;  /* [8][nsplit][HQ]: XCD x's split maxima */
+  uint32_t* psum;  /* [8][nsplit][HQ] */
+  uint32_t* pout;  /* [8][nsplit][HQ][D] */
+} TfdXcdArgs;
+
+/* tfd_decode_persistent with the layer split over the device's 8 XCDs (256 compute
+ * units: 32 per XCD) so that most hand-offs stay inside one XCD's L2: XCD x holds
+ * kv head x, its query heads, 1/8 of the SwiGLU columns and the matching K slices
+ * of o and down, whose products are summed over XCDs by an all-reduce (two per
+ * layer).  Same step as tfd_decode_persistent (examples/qwen3_1_7b-tilelang/fast/
+ * engine.py:189-217); the o and down sums add their XCD slices in a different f32
+ * order.  For the Qwen3-1.7B shape only (hidden 2048, 16 q / 8 kv heads of 128,
+ * intermediate 6144); -3 otherwise or on a device that is not 8 x 32 compute units.
+ * args->x_hid, x_h1, x_smax, x_psum and x_pout are not used (the XCD arenas replace
+ * them); nsplit <= 128.  A block that finds itself on another XCD than block % 8
+ * raises TFD_ERR_PLACEMENT | TFD_ERR_SYNC and the launch gives up. */
+int tfd_decode_xcd(const TfdDecodeArgs* args, const TfdXcdArgs* xcd, int steps, void* stream);
 
 #ifdef __cplusplus
 }

@@ -39,7 +39,7 @@ def test_header_constants_match_binding():
         defines.update(re.findall(r"^#define TFD_(\w+) (\d+)", header.read_text(), re.M))
     names = {"ABI_VERSION", "PRO_PLAIN", "PRO_NORM", "EPI_STORE", "EPI_RESID", "EPI_SWIGLU",
              "EPI_LOGITS", "ERR_TOKEN_RANGE", "ERR_POS_RANGE", "ERR_PAGE_RANGE",
-             "ERR_STEP_RANGE", "ERR_SYNC", "PAGE_SIZE", "ATTN_SPLIT", "SKINNY_COUNTERS", "EPI_RESID_F32",
+             "ERR_STEP_RANGE", "ERR_SYNC", "ERR_PLACEMENT", "PAGE_SIZE", "ATTN_SPLIT", "SKINNY_COUNTERS", "EPI_RESID_F32",
              "ROUTE_SOFTMAX_TOPK", "ROUTE_TOPK_SOFTMAX", "POLICY_F32", "POLICY_BF16",
              "MOE_ROUTE_GIVEN", "MOE_ROUTE_SOFTMAX_TOPK", "MOE_ROUTE_TOPK_SOFTMAX"}
     assert names <= set(defines), names - set(defines)
@@ -58,7 +58,8 @@ def test_library_exports_every_declared_entry():
 
 STRUCTS = {"TfdDecodeArgs": _lib.TfdDecodeArgs, "TfdLayer": _lib.TfdLayer,
            "TfdMoeArgs": _lib.TfdMoeArgs, "TfdGdnArgs": _lib.TfdGdnArgs,
-           "TfdMambaArgs": _lib.TfdMambaArgs, "TfdGqaArgs": _lib.TfdGqaArgs}
+           "TfdMambaArgs": _lib.TfdMambaArgs, "TfdGqaArgs": _lib.TfdGqaArgs,
+           "TfdXcdArgs": _lib.TfdXcdArgs}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="no C compiler")

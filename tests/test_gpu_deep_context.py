@@ -7,7 +7,7 @@ through its page table (``place_context``), and one engine step is compared
 with the oracle's forward over the same caches.
 
 * C2: the batch-1 engine at positions near the end of the 2,048-token run
-  (2,070 and 2,078), in the persistent kernel and in the per-phase graph, with
+  (2,070 and 2,078), in both persistent kernels and in the per-phase graph, with
   the Qwen3-1.7B layer shape (two layers, a 4,096-token vocabulary so the CPU
   oracle runs in seconds).
 * C3: the batched engine at batch 32 over contexts of 4,000 .. 4,095 positions
@@ -73,7 +73,7 @@ def c2_weights():
     return synthetic_weights(C2_SHAPE, seed=3, norms="ones")
 
 
-@pytest.mark.parametrize("mode", ["persistent", "graph"])
+@pytest.mark.parametrize("mode", ["persistent", "xcd", "graph"])
 @pytest.mark.parametrize("P", [2070, 2078])
 def test_c2_step_at_depth(gpu_device, c2_weights, mode, P):
     cfg, w = C2_SHAPE, c2_weights

@@ -57,7 +57,7 @@ def test_c2_full_depth_against_golden(gpu_device, norms):
     gold = fx[norms]
     prompt = fx["prompt"]
     w = synthetic_weights(QWEN3_1_7B, seed=0, norms=norms)
-    for mode in ("graph", "persistent"):
+    for mode in ("graph", "persistent", "xcd"):
         eng = Engine(QWEN3_1_7B, w, device=gpu_device, max_new=STEPS,
                      prompt_room=len(prompt) + STEPS, mode=mode)
         print(f"[golden] norms={norms} mode={mode}", flush=True)

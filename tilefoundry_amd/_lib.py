@@ -18,6 +18,7 @@ ABI_VERSION = 12
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS, EPI_RESID_F32 = 0, 1, 2, 3, 4
 ERR_TOKEN_RANGE, ERR_POS_RANGE, ERR_PAGE_RANGE, ERR_STEP_RANGE, ERR_SYNC = 1, 2, 4, 8, 16
+ERR_PLACEMENT = 32          # tfd_decode_xcd: a block ran on another XCD than block % 8
 PAGE_SIZE = 16
 SKINNY_COUNTERS = 16384     # tile counters at the start of a skinny-GEMM work buffer
 NOALLOC_SCRATCH_FLOATS = SKINNY_COUNTERS + (1 << 21)   # tfd_gemm_skinny_bf16_noalloc's scratch
@@ -65,6 +66,7 @@ SIGNATURES: dict[str, list] = {
     "tfd_embed_rows_bf16": [P, P, P, I, I, I, I, P, P],
     "tfd_decode_persistent": [P, I, I, P],
     "tfd_decode_persistent_grid": [],
+    "tfd_decode_xcd": [P, P, I, P],
     # include/tf_hybrid.h
     "tfd_pack_skinny_fp8": [P, I, I, I, P, P],
     "tfd_gemm_skinny_fp8": [P, P, P, I, I, I, I, P, I, P, I, P],
@@ -175,6 +177,15 @@ class TfdDecodeArgs(ctypes.Structure):
         ("err", c_void_p),
         ("timeline", c_void_p), ("timeline_steps", c_int),
     ]
+
+
+class TfdXcdArgs(ctypes.Structure):
+    """``TfdXcdArgs`` of include/tf_decode.h (the XCD-partitioned kernel's arenas)."""
+
+    _fields_ = [(n, c_void_p) for n in ("hid", "h1", "opart", "dpart", "smax", "psum", "pout")]
+
+
+XCDS = 8                    # XCDs of an MI355X, the unit of tfd_decode_xcd's partition
 
 
 def timeline_stamps(n_layers: int) -> int:

@@ -318,6 +318,42 @@ __device__ __forceinline__ void dot_rows(const bf16* __restrict__ W, int K, int 
 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
+// ---------------------------------------------------------------------------
+// Thread groups a phase runs on: its thread index (0 .. kBlock-1) and its
+// barrier.  BlockGrp is the whole kBlock-thread block.  SubGrp<kFirst, kWaves>
+// is kWaves waves of a larger block starting at thread kFirst, with a barrier
+// of its own (an LDS arrival counter, so the block's other waves never wait
+// in it): a block can then run two groups side by side.
+// ---------------------------------------------------------------------------
+struct BlockGrp {
+  static __device__ __forceinline__ int tid() { return (int)threadIdx.x; }
+  static __device__ __forceinline__ void sync() { __syncthreads(); }
+};
+
+template <int kFirst, int kWaves>
+struct SubGrp {
+  static_assert(kWaves * kWave == kBlock, "a group plays one kBlock-thread block");
+  static __device__ __forceinline__ int tid() { return (int)threadIdx.x - kFirst; }
+  static __device__ __forceinline__ uint32_t* counter() {
+    __shared__ uint32_t arrivals;
+    return &arrivals;
+  }
+  // one thread of the block, followed by a whole-block barrier, before any sync()
+  static __device__ __forceinline__ void init() { *counter() = 0; }
+  static __device__ __forceinline__ void sync() {
+    // this wave's LDS accesses are complete before it counts itself in
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    uint32_t old = 0;
+    if ((threadIdx.x & (kWave - 1)) == 0)
+      old = __hip_atomic_fetch_add(counter(), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    old = __shfl(old, 0, kWave);
+    const uint32_t target = (old / kWaves + 1) * kWaves;   // every wave arrives once per barrier
+    while (__hip_atomic_load(counter(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
+      __builtin_amdgcn_s_sleep(0);
+    __asm__ volatile("" ::: "memory");
+  }
+};
+
 // Error flags a kernel raises instead of touching memory it was not given.
 enum DeviceError : int {
   kErrNone = 0,
@@ -348,15 +384,25 @@ __device__ __forceinline__ void raise_error(int* err, int code) {
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kPollBound = 1u << 21;
 
+// Cache policy of an exchange whose writer and readers all run on one XCD.
+// Device scope, as kCoherent: the workgroup-scope bit alone does not make a
+// load miss the compute unit's L1 when a workgroup stays on one compute unit,
+// so a poll through it can keep reading a stale line (measured: such polls
+// never completed).  Kept as its own name so the intra-XCD exchanges are
+// marked as such.
+constexpr int kXcdLocal = kCoherent;
+
+template <int kPol = kCoherent>
 __device__ __forceinline__ void ll_put(uint32_t* base, uint32_t word, uint32_t payload,
                                        uint32_t tag) {
-  __builtin_amdgcn_raw_buffer_store_b64(u32x2{payload, tag}, rsrc(base), word * 8u, 0, kCoherent);
+  __builtin_amdgcn_raw_buffer_store_b64(u32x2{payload, tag}, rsrc(base), word * 8u, 0, kPol);
 }
 // words `word` and `word + 1` (word even) in one store
+template <int kPol = kCoherent>
 __device__ __forceinline__ void ll_put2(uint32_t* base, uint32_t word, uint32_t p0, uint32_t p1,
                                         uint32_t tag) {
   __builtin_amdgcn_raw_buffer_store_b128(u32x4{p0, tag, p1, tag}, rsrc(base), word * 8u, 0,
-                                         kCoherent);
+                                         kPol);
 }
 
 __device__ __forceinline__ bool ll_give_up(uint32_t& spins, int* err) {
@@ -369,27 +415,29 @@ __device__ __forceinline__ bool ll_give_up(uint32_t& spins, int* err) {
 }
 
 // The payloads of words `word`, `word + 1` (word even) once both carry `tag`.
+template <int kPol = kCoherent>
 __device__ __forceinline__ u32x2 ll_get2(const uint32_t* base, uint32_t word, uint32_t tag,
                                          int* err) {
-  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), word * 8u, 0, kCoherent);
+  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), word * 8u, 0, kPol);
   uint32_t spins = 0;
   while (v.y != tag || v.w != tag) {
     if (ll_give_up(spins, err)) break;
     // the compiler must issue the load again: without a clobber it may reuse the first result
     __asm__ volatile("" ::: "memory");
-    v = __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), word * 8u, 0, kCoherent);
+    v = __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), word * 8u, 0, kPol);
   }
   return u32x2{v.x, v.z};
 }
 
+template <int kPol = kCoherent>
 __device__ __forceinline__ uint32_t ll_get(const uint32_t* base, uint32_t word, uint32_t tag,
                                            int* err) {
-  u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rsrc(base), word * 8u, 0, kCoherent);
+  u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rsrc(base), word * 8u, 0, kPol);
   uint32_t spins = 0;
   while (v.y != tag) {
     if (ll_give_up(spins, err)) break;
     __asm__ volatile("" ::: "memory");
-    v = __builtin_amdgcn_raw_buffer_load_b64(rsrc(base), word * 8u, 0, kCoherent);
+    v = __builtin_amdgcn_raw_buffer_load_b64(rsrc(base), word * 8u, 0, kPol);
   }
   return v.x;
 }
@@ -398,17 +446,18 @@ __device__ __forceinline__ uint32_t ll_get(const uint32_t* base, uint32_t word, 
 // bf16 pairs; the caller synchronises the block before reading it.  Each
 // thread issues all its loads of a batch before checking any, so a long vector
 // costs one round trip rather than one per load.
+template <int kPol = kCoherent, class Grp = BlockGrp>
 __device__ __forceinline__ void ll_stage(const uint32_t* ll, int n, uint32_t tag,
                                          uint32_t* __restrict__ lds, int* err) {
   constexpr int kBatch = 8;
   const int npairs = n / 4;
-  for (int i0 = threadIdx.x; i0 < npairs; i0 += kBlock * kBatch) {
+  for (int i0 = Grp::tid(); i0 < npairs; i0 += kBlock * kBatch) {
     u32x4 v[kBatch];
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       const int i = i0 + k * kBlock;
       v[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(ll), (uint32_t)(i < npairs ? i : 0) * 16u,
-                                                   0, kCoherent);
+                                                   0, kPol);
     }
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
@@ -418,7 +467,7 @@ __device__ __forceinline__ void ll_stage(const uint32_t* ll, int n, uint32_t tag
         while (v[k].y != tag || v[k].w != tag) {
           if (ll_give_up(spins, err)) break;
           __asm__ volatile("" ::: "memory");
-          v[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(ll), (uint32_t)i * 16u, 0, kCoherent);
+          v[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(ll), (uint32_t)i * 16u, 0, kPol);
         }
         lds[2 * i] = v[k].x;
         lds[2 * i + 1] = v[k].z;

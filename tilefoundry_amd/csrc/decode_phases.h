@@ -144,7 +144,7 @@ __device__ __forceinline__ uint32_t bf_pair(bf16 lo, bf16 hi) {
   return (uint32_t)lo | ((uint32_t)hi << 16);
 }
 
-template <int kCmax, int kR, int kPro, int kEpi>
+template <int kCmax, int kR, int kPro, int kEpi, int kPol = kCoherent>
 __device__ __forceinline__ void gemv_finish_ll(int vb, const uint32_t* xs,
                                                const u32x4 (&gr)[kCmax],
                                                const uint32_t* resid_s, uint32_t* out,
@@ -174,7 +174,7 @@ __device__ __forceinline__ void gemv_finish_ll(int vb, const uint32_t* xs,
           const float u = rbf(acc[4 * q + 2 * e + 1]);
           o[e] = f2bf(rbf(silu_f(g)) * u);
         }
-        ll_put(out, (uint32_t)(row0 / 4 + q), bf_pair(o[0], o[1]), tag);
+        ll_put<kPol>(out, (uint32_t)(row0 / 4 + q), bf_pair(o[0], o[1]), tag);
       }
     }
   } else {
@@ -189,7 +189,7 @@ __device__ __forceinline__ void gemv_finish_ll(int vb, const uint32_t* xs,
         } else {
           pr = bf_pair(f2bf(y0), f2bf(y1));
         }
-        ll_put(out, (uint32_t)((row0 + 2 * q) / 2), pr, tag);
+        ll_put<kPol>(out, (uint32_t)((row0 + 2 * q) / 2), pr, tag);
       }
     }
   }
@@ -199,7 +199,7 @@ __device__ __forceinline__ void gemv_finish_ll(int vb, const uint32_t* xs,
 // virtual block and the norm scales (gr, this lane's chunks) are already in
 // flight, issued before the wait for x; further virtual blocks issue and
 // finish in turn.
-template <int kCmax, int kR, int kPro, int kEpi>
+template <int kCmax, int kR, int kPro, int kEpi, int kPol = kCoherent>
 __device__ __forceinline__ void gemv_ll(const uint32_t* xs, const u32x4 (&gr)[kCmax],
                                         const bf16* W, const uint32_t* resid_s, uint32_t* out,
                                         uint32_t tag, int K, int N, float eps,
@@ -207,7 +207,7 @@ __device__ __forceinline__ void gemv_ll(const uint32_t* xs, const u32x4 (&gr)[kC
   const int rows_per_vb = kWavesPerBlock * kR;
   for (int vb = blockIdx.x; vb * rows_per_vb < N; vb += gridDim.x) {
     if (vb != (int)blockIdx.x) gemv_issue<kCmax, kR>(vb, W, K, N, w);
-    gemv_finish_ll<kCmax, kR, kPro, kEpi>(vb, xs, gr, resid_s, out, tag, K, N, eps, w);
+    gemv_finish_ll<kCmax, kR, kPro, kEpi, kPol>(vb, xs, gr, resid_s, out, tag, K, N, eps, w);
   }
 }
 
@@ -354,11 +354,12 @@ __device__ __forceinline__ void finalize_phase(const float* __restrict__ bv,
 // derives the next token itself; block 0 also records the pick and publishes
 // the token and position for the host.  Returns the next token.
 // ---------------------------------------------------------------------------
+template <class Grp = BlockGrp>
 __device__ __forceinline__ int finalize_ll(const uint32_t* best, int nb, uint32_t tag, int p,
                                            const int* __restrict__ inp,
                                            const int* __restrict__ plen, int nsteps, int vocab,
                                            int64_t* ids, int* pos, int* sam, int* err) {
-  const int tid = threadIdx.x;
+  const int tid = Grp::tid();
   float b = kNegInf;
   int i = 0x7fffffff;
   for (int k = tid; k < nb; k += kBlock) {
@@ -387,7 +388,7 @@ __device__ __forceinline__ int finalize_ll(const uint32_t* best, int nb, uint32_
     sv[wave] = b;
     si[wave] = i;
   }
-  __syncthreads();
+  Grp::sync();
   if (tid == 0) {
     float bb = sv[0];
     int ii = si[0];
@@ -414,7 +415,7 @@ __device__ __forceinline__ int finalize_ll(const uint32_t* best, int nb, uint32_
     }
     next_s = next;
   }
-  __syncthreads();
+  Grp::sync();
   return next_s;
 }
 
@@ -461,16 +462,16 @@ struct VTile {
 };
 
 // position a thread reads in each pass layout
-template <int D>
+template <int D, class Grp = BlockGrp>
 __device__ __forceinline__ int k_pos(int j0, int p) {
   using A = AttnShape<D>;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int lane = Grp::tid() & (kWave - 1), wave = Grp::tid() / kWave;
   return j0 + (p * kWavesPerBlock + wave) * A::kKPpw + lane / A::kKLanes;
 }
-template <int D>
+template <int D, class Grp = BlockGrp>
 __device__ __forceinline__ int v_pos(int j0, int p) {
   using A = AttnShape<D>;
-  return j0 + (int)threadIdx.x / A::kLpp + p * A::kGroups;
+  return j0 + (int)Grp::tid() / A::kLpp + p * A::kGroups;
 }
 
 // A wave's positions in one pass lie in one page (16 positions per wave in
@@ -500,14 +501,14 @@ __device__ __forceinline__ u32x4 kv_ld16(const void* base, uint32_t byte_off) {
 }
 
 // (the loads only: the caller knows the tile holds a position below P)
-template <int D, bool kCoh>
+template <int D, bool kCoh, class Grp = BlockGrp>
 __device__ __forceinline__ void k_tile_load_at(int j0, int h, const int* page_table,
                                                int max_pages, const bf16* kpool, int num_pages,
                                                int kv_heads, KTile<D>& kt) {
   using A = AttnShape<D>;
   static_assert(kPage % A::kKPpw == 0, "a wave's positions of a pass stay in one page");
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+  const int lane = Grp::tid() & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane((int)Grp::tid() / kWave);
 #pragma unroll
   for (int p = 0; p < A::kKPasses; ++p)
     kt.pg[p] = wave_page(page_table, max_pages, j0 + (p * kWavesPerBlock + wave) * A::kKPpw);
@@ -522,7 +523,7 @@ __device__ __forceinline__ void k_tile_load_at(int j0, int h, const int* page_ta
   }
 }
 
-template <int D, bool kCoh>
+template <int D, bool kCoh, class Grp = BlockGrp>
 __device__ __forceinline__ void k_tile_issue_at(int j0, int h, int P, const int* page_table,
                                                 int max_pages, const bf16* kpool, int num_pages,
                                                 int kv_heads, KTile<D>& kt) {
@@ -534,30 +535,30 @@ __device__ __forceinline__ void k_tile_issue_at(int j0, int h, int P, const int*
     for (int i = 0; i < A::kKChunks; ++i) kt.t[p][i] = u32x4{0u, 0u, 0u, 0u};
   }
   if (j0 < P)
-    k_tile_load_at<D, kCoh>(j0, h, page_table, max_pages, kpool, num_pages, kv_heads, kt);
+    k_tile_load_at<D, kCoh, Grp>(j0, h, page_table, max_pages, kpool, num_pages, kv_heads, kt);
 }
 
-template <int D, bool kCoh>
+template <int D, bool kCoh, class Grp = BlockGrp>
 __device__ __forceinline__ void v_tile_load_at(int j0, int h, const int* page_table,
                                                int max_pages, const bf16* vpool, int num_pages,
                                                int kv_heads, VTile<D>& vt) {
   using A = AttnShape<D>;
   static_assert(kPage % (kWave / A::kLpp) == 0, "a wave's pass stays in one page");
-  const int ch = (int)threadIdx.x % A::kLpp;
-  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+  const int ch = (int)Grp::tid() % A::kLpp;
+  const int wave = __builtin_amdgcn_readfirstlane((int)Grp::tid() / kWave);
 #pragma unroll
   for (int p = 0; p < A::kVPasses; ++p)
     vt.pg[p] = wave_page(page_table, max_pages, j0 + p * A::kGroups + wave * (kWave / A::kLpp));
 #pragma unroll
   for (int p = 0; p < A::kVPasses; ++p) {
-    const int j = v_pos<D>(j0, p);
+    const int j = v_pos<D, Grp>(j0, p);
     const bool bad = vt.pg[p] < 0 || vt.pg[p] >= num_pages;
     vt.t[p] = kv_ld16<kCoh>(vpool, (uint32_t)(page_row(bad ? 0 : vt.pg[p], j, kv_heads, h, D) +
                                          ch * 8) * 2u);
   }
 }
 
-template <int D, bool kCoh>
+template <int D, bool kCoh, class Grp = BlockGrp>
 __device__ __forceinline__ void v_tile_issue_at(int j0, int h, int P, const int* page_table,
                                                 int max_pages, const bf16* vpool, int num_pages,
                                                 int kv_heads, VTile<D>& vt) {
@@ -568,22 +569,22 @@ __device__ __forceinline__ void v_tile_issue_at(int j0, int h, int P, const int*
     vt.t[p] = u32x4{0u, 0u, 0u, 0u};
   }
   if (j0 < P)
-    v_tile_load_at<D, kCoh>(j0, h, page_table, max_pages, vpool, num_pages, kv_heads, vt);
+    v_tile_load_at<D, kCoh, Grp>(j0, h, page_table, max_pages, vpool, num_pages, kv_heads, vt);
 }
 
 // The first tile of split `split` of a one-tile-per-split partition.
-template <int D, bool kCoh>
+template <int D, bool kCoh, class Grp = BlockGrp>
 __device__ __forceinline__ void k_tile_issue(int split, int h, int P, const int* page_table,
                                              int max_pages, const bf16* kpool, int num_pages,
                                              int kv_heads, KTile<D>& kt) {
-  k_tile_issue_at<D, kCoh>(split * kSplit, h, P, page_table, max_pages, kpool, num_pages,
+  k_tile_issue_at<D, kCoh, Grp>(split * kSplit, h, P, page_table, max_pages, kpool, num_pages,
                            kv_heads, kt);
 }
-template <int D, bool kCoh>
+template <int D, bool kCoh, class Grp = BlockGrp>
 __device__ __forceinline__ void v_tile_issue(int split, int h, int P, const int* page_table,
                                              int max_pages, const bf16* vpool, int num_pages,
                                              int kv_heads, VTile<D>& vt) {
-  v_tile_issue_at<D, kCoh>(split * kSplit, h, P, page_table, max_pages, vpool, num_pages,
+  v_tile_issue_at<D, kCoh, Grp>(split * kSplit, h, P, page_table, max_pages, vpool, num_pages,
                            kv_heads, vt);
 }
 
@@ -612,22 +613,22 @@ __device__ __forceinline__ int head_src(int idx, int h, int heads, int kv_heads)
   return heads * D + kv_heads * D + h * D + (idx - (G + 1) * D);
 }
 
-template <int D, int G>
+template <int D, int G, class Grp = BlockGrp>
 __device__ __forceinline__ void stage_head(int h, int heads, int kv_heads,
                                            const bf16* __restrict__ qkv, uint32_t* hs) {
-  for (int i = threadIdx.x; i < (G + 2) * D / 2; i += kBlock) {
+  for (int i = Grp::tid(); i < (G + 2) * D / 2; i += kBlock) {
     const int src = head_src<D, G>(2 * i, h, heads, kv_heads);
     hs[i] = (uint32_t)qkv[src] | ((uint32_t)qkv[src + 1] << 16);
   }
 }
 
-template <int D, int G>
+template <int D, int G, int kPol = kCoherent, class Grp = BlockGrp>
 __device__ __forceinline__ void stage_head_ll(int h, int heads, int kv_heads, const AttnLL& ll,
                                               uint32_t* hs, int* err) {
   // pairs of words: every run (q group, k, v) starts at an even word
-  for (int i = threadIdx.x; i < (G + 2) * D / 4; i += kBlock) {
+  for (int i = Grp::tid(); i < (G + 2) * D / 4; i += kBlock) {
     const int src = head_src<D, G>(4 * i, h, heads, kv_heads);
-    const u32x2 v = ll_get2(ll.qkv, (uint32_t)src / 2u, ll.tag, err);
+    const u32x2 v = ll_get2<kPol>(ll.qkv, (uint32_t)src / 2u, ll.tag, err);
     hs[2 * i] = v.x;
     hs[2 * i + 1] = v.y;
   }
@@ -647,14 +648,14 @@ struct QKPre {
   int page_new;
 };
 
-template <int D, int G>
+template <int D, int G, class Grp = BlockGrp>
 __device__ __forceinline__ QKPre qk_prefetch(int rp, int P, const bf16* __restrict__ gq,
                                              const bf16* __restrict__ gk,
                                              const bf16* __restrict__ cos_t,
                                              const bf16* __restrict__ sin_t, int rope_rows,
                                              const int* __restrict__ page_table, int max_pages) {
   constexpr int kHalf = D / 2;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int lane = Grp::tid() & (kWave - 1), wave = Grp::tid() / kWave;
   const int li = lane < kHalf ? lane : 0;
   const int64_t r = (int64_t)((rp >= 0 && rp < rope_rows) ? rp : 0) * D;
   const int pg = (P >= 0 && P < max_pages * kPage) ? P / kPage : 0;
@@ -672,7 +673,7 @@ __device__ __forceinline__ QKPre qk_prefetch(int rp, int P, const bf16* __restri
 //   s_j = bf16( sum_d bf16(q_s[d] * K[j][d]) ),
 // and records the split's max per query head.
 // ---------------------------------------------------------------------------
-template <int D, int G, bool kLL>
+template <int D, int G, bool kLL, int kPol = kCoherent, class Grp = BlockGrp>
 __device__ __forceinline__ void attn_scores_phase(
     int split, int h, const uint32_t* hs, const QKPre& pre, int rope_rows, int rp, int P,
     const int* __restrict__ page_table, int max_pages, bf16* __restrict__ kpool, bf16* __restrict__ vpool, int num_pages,
@@ -684,7 +685,7 @@ __device__ __forceinline__ void attn_scores_phase(
   static_assert(kHalf <= kWave, "one wave holds a head as (d, d + D/2) lane pairs");
   static_assert(G + 1 <= kWavesPerBlock, "one wave per vector");
   const int heads = kv_heads * G;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int tid = Grp::tid(), lane = tid & (kWave - 1), wave = tid / kWave;
   // a split is `chunks` tiles of 64 positions (the persistent kernel uses one)
   const int j0 = split * chunks * kSplit;
 
@@ -692,7 +693,7 @@ __device__ __forceinline__ void attn_scores_phase(
   // kernel, so plain (cached, write-back) stores are enough there
   auto put_max = [&](int g, float m) {
     if (kLL)
-      ll_put(ll.smax, (uint32_t)(split * heads + h * G + g), __float_as_uint(m), ll.tag);
+      ll_put<kPol>(ll.smax, (uint32_t)(split * heads + h * G + g), __float_as_uint(m), ll.tag);
     else
       smax[split * heads + h * G + g] = m;
   };
@@ -750,7 +751,7 @@ __device__ __forceinline__ void attn_scores_phase(
       }
     }
   }
-  __syncthreads();
+  Grp::sync();
 
   if (split == 0) {
     // this token's entry goes to the cache at P (fast/kernels.py:385-409)
@@ -807,11 +808,11 @@ __device__ __forceinline__ void attn_scores_phase(
   auto tile = [&](int c, const KTile<D>& cur, KTile<D>& nxt, auto issue) {
     const int jc = j0 + c * kSplit;
     if (decltype(issue)::value)
-      k_tile_load_at<D, kLL>(jc + kSplit, h, page_table, max_pages, kpool, num_pages, kv_heads,
+      k_tile_load_at<D, kLL, Grp>(jc + kSplit, h, page_table, max_pages, kpool, num_pages, kv_heads,
                              nxt);
 #pragma unroll
     for (int p = 0; p < A::kKPasses; ++p) {
-      const int j = k_pos<D>(jc, p);
+      const int j = k_pos<D, Grp>(jc, p);
       const bool bad = cur.pg[p] < 0 || cur.pg[p] >= num_pages;
       if (j < jend && bad) page_ok = false;
       const bool valid = j < jend && !bad;
@@ -858,13 +859,13 @@ __device__ __forceinline__ void attn_scores_phase(
     const float m = wave_max(mymax[g]);
     if (lane == 0) wmax[wave][g] = m;
   }
-  __syncthreads();
+  Grp::sync();
   if (tid < G) {
     float m = wmax[0][tid];
     for (int w = 1; w < kWavesPerBlock; ++w) m = fmaxf(m, wmax[w][tid]);
     put_max(tid, m);
   }
-  __syncthreads();
+  Grp::sync();
 }
 
 __device__ __forceinline__ float sn_of(const float* snew, int i) { return coh_ldf(&snew[i]); }
@@ -904,7 +905,8 @@ struct RowOut {
 // `polled` runs once this block's waits of the phase are over (the persistent
 // kernel issues weight loads there: memory counters retire in order, so loads
 // issued before a wait would hold it up)
-template <int D, int G, bool kLL, class Hook = NoHook, class OutMap = RowOut>
+template <int D, int G, bool kLL, class Hook = NoHook, class OutMap = RowOut,
+          int kPol = kCoherent, class Grp = BlockGrp>
 __device__ __forceinline__ void attn_pv_phase(
     int split, int h, int nsplit, const bf16* __restrict__ qkv, int P,
     const int* __restrict__ page_table, int max_pages, const bf16* __restrict__ vpool,
@@ -921,7 +923,7 @@ __device__ __forceinline__ void attn_pv_phase(
   static_assert(G <= kWavesPerBlock, "one wave per query head of the group");
   static_assert(kOut % 4 == 0 && kOut <= kBlock, "one thread per output");
   const int heads = kv_heads * G;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int tid = Grp::tid(), lane = tid & (kWave - 1), wave = tid / kWave;
   const int ch = tid % kLpp, jo = tid / kLpp;
   // a split is `chunks` tiles of 64 positions (the persistent kernel uses one)
   const int slen = chunks * kSplit;
@@ -946,7 +948,7 @@ __device__ __forceinline__ void attn_pv_phase(
     if (kLL) {
       // lanes past the active splits re-read split 0's word (always written)
       m = __uint_as_float(
-          ll_get(ll.smax, (uint32_t)((s < nact ? s : 0) * heads + h * G + wg), ll.tag, err));
+          ll_get<kPol>(ll.smax, (uint32_t)((s < nact ? s : 0) * heads + h * G + wg), ll.tag, err));
     } else {
       m = smax[(s < nsplit ? s : nsplit - 1) * heads + h * G + wg];
     }
@@ -989,7 +991,7 @@ __device__ __forceinline__ void attn_pv_phase(
       // lanes past jend read a score of this row (in bounds, unused)
       const int jn = jc + kSplit + lane;
       sj_next = S[(int64_t)(h * G + wg) * s_stride + (jn < jend ? jn : jend - 1)];
-      v_tile_load_at<D, kLL>(jc + kSplit, h, page_table, max_pages, vpool, num_pages, kv_heads,
+      v_tile_load_at<D, kLL, Grp>(jc + kSplit, h, page_table, max_pages, vpool, num_pages, kv_heads,
                              nxt);
     }
     if (wave < G) {
@@ -997,7 +999,7 @@ __device__ __forceinline__ void attn_pv_phase(
       p[wave][lane] = pj;
       psum += wave_sum(pj);
     }
-    __syncthreads();
+    Grp::sync();
     // passes q and q + 1 hold the same dims of two positions: their rounded
     // products go to each accumulator as one pair
     static_assert(A::kVPasses % 2 == 0, "passes pair up");
@@ -1029,7 +1031,7 @@ __device__ __forceinline__ void attn_pv_phase(
         }
       }
     }
-    __syncthreads();                        // p is rewritten by the next tile
+    Grp::sync();                        // p is rewritten by the next tile
   };
   VTile<D> va = vt, vb;
   float sa = sj_first, sb = 0.f;
@@ -1047,7 +1049,7 @@ __device__ __forceinline__ void attn_pv_phase(
   if (!page_ok) raise_error(err, kErrPageRange);
   if (wave < G && lane == 0) {
     if (kLL)
-      ll_put(ll.psum, (uint32_t)(split * heads + h * G + wave), __float_as_uint(psum), ll.tag);
+      ll_put<kPol>(ll.psum, (uint32_t)(split * heads + h * G + wave), __float_as_uint(psum), ll.tag);
     else
       coh_stf(&part_sum[split * heads + h * G + wave], psum);
   }
@@ -1055,7 +1057,7 @@ __device__ __forceinline__ void attn_pv_phase(
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int e = 0; e < 8; ++e) red[jo][g * D + ch * 8 + e] = acc[g][e];
-  __syncthreads();
+  Grp::sync();
   if (kLL) {
     for (int o = 2 * tid; o < kOut; o += 2 * kBlock) {
       float s0 = 0.f, s1 = 0.f;
@@ -1064,10 +1066,10 @@ __device__ __forceinline__ void attn_pv_phase(
         s0 += red[q][o];
         s1 += red[q][o + 1];
       }
-      ll_put2(ll.pout, (uint32_t)(((int64_t)split * heads + h * G) * D + o), __float_as_uint(s0),
+      ll_put2<kPol>(ll.pout, (uint32_t)(((int64_t)split * heads + h * G) * D + o), __float_as_uint(s0),
               __float_as_uint(s1), ll.tag);
     }
-    __syncthreads();
+    Grp::sync();
     return;
   }
   for (int o = tid; o < kOut; o += kBlock) {
@@ -1078,12 +1080,12 @@ __device__ __forceinline__ void attn_pv_phase(
   }
   // ---- the last block of this kv head merges the splits
   stores_done();
-  __syncthreads();
+  Grp::sync();
   if (tid == 0) {
     const int ticket = atomicAdd(&counters[h], 1);
     is_last = (ticket == participants - 1);
   }
-  __syncthreads();
+  Grp::sync();
   if (!is_last) return;
   // stage up to kGroups splits at a time: coalesced 16-byte device-coherent loads
   constexpr int kVecPerSplit = kOut / 4;
@@ -1114,14 +1116,14 @@ __device__ __forceinline__ void attn_pv_phase(
       }
     }
     if (tid < nc * G) psums[tid / G][tid % G] = ps;
-    __syncthreads();
+    Grp::sync();
     if (tid < kOut) {
       for (int s = 0; s < nc; ++s) {
         sv += red[s][tid];
         sp += psums[s][tid / D];
       }
     }
-    __syncthreads();
+    Grp::sync();
   }
   if (tid < kOut) {
     const int g = tid / D, d = tid % D;
@@ -1130,7 +1132,7 @@ __device__ __forceinline__ void attn_pv_phase(
                 attn_merge_one(sp, sv, sn_of(snew, h * G + g), M[g], bf2f(qkv[vnew + d])));
   }
   if (tid == 0) atomicExch(&counters[h], 0);
-  __syncthreads();
+  Grp::sync();
 }
 
 // ---------------------------------------------------------------------------
@@ -1139,14 +1141,14 @@ __device__ __forceinline__ void attn_pv_phase(
 // split's partials for that slice and the numerator sums, in split order --
 // the same arithmetic as the last-block merge above.
 // ---------------------------------------------------------------------------
-template <int D, int G, class Hook = NoHook>
+template <int D, int G, class Hook = NoHook, int kPol = kCoherent, class Grp = BlockGrp>
 __device__ __forceinline__ void attn_merge_ll(int split, int h, int P, int max_pages,
                                               int kv_heads, const float* snew, const AttnLL& ll,
                                               int* err, const Hook& polled = Hook()) {
   constexpr int kPairs = G * D / 2;
   constexpr int kChunk = 16;                          // splits staged at a time
   const int heads = kv_heads * G;
-  const int tid = threadIdx.x;
+  const int tid = Grp::tid();
   if (P < 0 || P >= max_pages * kPage) P = 0;
   const int nact = (P + kSplit - 1) / kSplit;
   const int participants = nact > 0 ? nact : 1;
@@ -1160,23 +1162,23 @@ __device__ __forceinline__ void attn_merge_ll(int split, int h, int P, int max_p
   const int o = 2 * (q0 + (tid < nq ? tid : 0));
   const int g = o / D, d = o % D;
   // the new key's values d, d + 1 (one word of the QKV projection)
-  const uint32_t vw = ll_get(ll.qkv, (uint32_t)(heads * D + kv_heads * D + h * D + d) / 2u,
+  const uint32_t vw = ll_get<kPol>(ll.qkv, (uint32_t)(heads * D + kv_heads * D + h * D + d) / 2u,
                              ll.tag, err);
   for (int c0 = 0; c0 < participants; c0 += kChunk) {
     const int nc = (participants - c0) < kChunk ? (participants - c0) : kChunk;
     for (int i = tid; i < nc * G; i += kBlock) {
       const uint32_t w = (uint32_t)((c0 + i / G) * heads + h * G + i % G);
-      ps[i / G][i % G] = __uint_as_float(ll_get(ll.psum, w, ll.tag, err));
+      ps[i / G][i % G] = __uint_as_float(ll_get<kPol>(ll.psum, w, ll.tag, err));
       // split maxima exist only for splits holding a prior position
       sm[i / G][i % G] =
-          (c0 + i / G < nact) ? __uint_as_float(ll_get(ll.smax, w, ll.tag, err)) : kNegInf;
+          (c0 + i / G < nact) ? __uint_as_float(ll_get<kPol>(ll.smax, w, ll.tag, err)) : kNegInf;
     }
     for (int i = tid; i < nc * nq; i += kBlock) {
       const int s = i / nq, q = i % nq;
-      po[s][q] = ll_get2(ll.pout, (uint32_t)(((int64_t)(c0 + s) * heads + h * G) * D + 2 * (q0 + q)),
+      po[s][q] = ll_get2<kPol>(ll.pout, (uint32_t)(((int64_t)(c0 + s) * heads + h * G) * D + 2 * (q0 + q)),
                          ll.tag, err);
     }
-    __syncthreads();
+    Grp::sync();
     if (c0 == 0) polled();
     if (tid < nq) {
       for (int s = 0; s < nc; ++s) {
@@ -1186,14 +1188,14 @@ __device__ __forceinline__ void attn_merge_ll(int split, int h, int P, int max_p
         mx = fmaxf(mx, sm[s][g]);
       }
     }
-    __syncthreads();
+    Grp::sync();
   }
   if (tid < nq) {
     const float sn = snew[g];
     const float M = fmaxf(mx, sn);
     const bf16 r0 = attn_merge_one(sp, sv0, sn, M, bf_lo(vw));
     const bf16 r1 = attn_merge_one(sp, sv1, sn, M, bf_hi(vw));
-    ll_put(ll.attn, (uint32_t)((h * G * D + o) / 2), (uint32_t)r0 | ((uint32_t)r1 << 16), ll.tag);
+    ll_put<kPol>(ll.attn, (uint32_t)((h * G * D + o) / 2), (uint32_t)r0 | ((uint32_t)r1 << 16), ll.tag);
   }
 }
 

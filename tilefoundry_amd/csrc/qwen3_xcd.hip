@@ -1,0 +1,448 @@
+// The batch-1 Qwen3 decode step partitioned over the 8 XCDs of an MI355X.
+//
+// The chip is 8 XCDs of 32 compute units.  A 2048-value vector handed from
+// every block to all 256 blocks costs ~1.5 us (measured: device-scope polls,
+// every load in flight); handed among the 32 blocks of one XCD it costs ~1 us
+// (fewer readers of the same lines).  The step is a chain of hand-offs, so
+// the kernel keeps most of them inside an XCD: each layer is split across XCDs
+// the way tensor parallelism splits it across GPUs, with the XCD as the unit.
+//
+// Block b runs on XCD x = b % 8 as rank r = b / 8 of that XCD's 32 blocks (the
+// dispatcher places workgroups round-robin over XCDs; every block checks this
+// against its hardware XCC id).  Per layer, XCD x owns kv head x and its query
+// heads 2x, 2x + 1 (the Qwen3-1.7B shape: 16 q heads, 8 kv heads, head_dim 128,
+// hidden 2048, intermediate 6144):
+//   qkv     the XCD's 512 q/k/v rows (16 per block, full rows of 2048)
+//   attn    kv head x over the context, 64-position splits s = r, r + 32, ...:
+//           scores, the split maxima, P.V partials and the merge all exchange
+//           inside the XCD (model.py:172-212, the two-pass softmax as authored)
+//   o       K split: the XCD's 256 attention outputs against W_o[:, 256x..+256];
+//           block r makes rows 64r..64r+63 of that partial product
+//   gate/up the XCD's 768 intermediate columns (48 gate/up rows per block)
+//   down    K split: the XCD's 768 SwiGLU values against W_down[:, 768x..+768]
+// and the o and down products are summed over XCDs by an all-reduce: block
+// (x, r) reads the 8 XCDs' partials of rows 64r..64r+63 (device scope), adds
+// them in XCD order, applies the residual (h1 = hidden + o, out = h1 + mlp, the
+// bf16 roundings of model.py:236-266), and publishes its 64 values to its XCD;
+// every block of the XCD then reads the whole vector from the L2.  Every XCD
+// sums the same partials in the same order, so all hold the same bits.
+//
+// Hand-offs per layer: 2 across XCDs (the all-reduces), 6 inside one.  The
+// weights of each phase are issued before the wait for its input, as in the
+// chip-wide persistent kernel (qwen3_decode.hip); the lm_head and the greedy
+// pick are that kernel's.
+//
+// Replaces the same steps as tfd_decode_persistent (examples/qwen3_1_7b-
+// tilelang/fast/engine.py:189-217: one captured step per token).
+
+#include "decode_phases.h"
+#include "host_common.h"
+#include "tf_decode.h"
+
+#include <stdlib.h>
+
+using namespace tfd;
+using namespace tfd_host;
+
+namespace {
+
+constexpr int kXcds = 8;
+constexpr int kRanks = 32;                 // blocks per XCD
+constexpr int kErrPlacement = 32;          // a block ran off the XCD its partition assumes
+
+// Exchange buffers are arrays of 8-byte (payload, tag) words held as uint32_t:
+// word n starts at uint32 2n.
+__device__ __forceinline__ uint32_t* word_at(uint32_t* base, int64_t n) { return base + 2 * n; }
+
+__device__ __forceinline__ int xcc_id() {
+  int x;
+  __asm__ volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x & 0xf;
+}
+
+// ---------------------------------------------------------------------------
+// K-split slabs (o, down): a wave owns 16 output rows of its block's 64; lane l
+// works on row 2p + l / 32 of pass p, with the row's 16-byte chunks c, c + 32,
+// ... where c = l % 32 (the slab is kC chunks of 8 per lane and row: 256
+// values for o, 768 for down).  Row sums are 32-lane sums.
+// ---------------------------------------------------------------------------
+template <int kC>
+__device__ __forceinline__ void slab_issue(const bf16* __restrict__ W, int ld, int row0, int col0,
+                                           u32x4 (&w)[8][kC]) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int half = lane >> 5, c = lane & 31;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int64_t row = row0 + 16 * wave + 2 * p + half;
+#pragma unroll
+    for (int j = 0; j < kC; ++j) w[p][j] = load16_stream(W + row * ld + col0 + 8 * (c + 32 * j));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Partial row sums of the slab with x (kC chunks of 8 per lane from LDS, bf16
+// pairs) -> f32 words of part (device scope; rows row0 .. row0 + 63).
+template <int kC>
+__device__ __forceinline__ void slab_finish(const uint32_t* xs, const u32x4 (&w)[8][kC],
+                                            uint32_t* part, int row0, uint32_t tag) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int half = lane >> 5, c = lane & 31;
+  u32x4 xr[kC];
+#pragma unroll
+  for (int j = 0; j < kC; ++j) xr[j] = *reinterpret_cast<const u32x4*>(xs + 4 * (c + 32 * j));
+  float mine = 0.f;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    float a = 0.f;
+#pragma unroll
+    for (int j = 0; j < kC; ++j) a = dot8(w[p][j], xr[j], a);
+    a = group_sum<32>(a);
+    // lane 2p (row of half 0) and lane 32 + 2p (half 1) keep pass p's sums
+    if ((lane & 31) == 2 * p) mine = a;
+  }
+  // lanes 0, 2, .., 14 and 32, 34, .., 46 hold rows 2p + half: one word each
+  if ((lane & 31) < 16 && (lane & 1) == 0) {
+    const int p = (lane & 31) >> 1;
+    ll_put<kCoherent>(part, (uint32_t)(row0 + 16 * wave + 2 * p + half), __float_as_uint(mine),
+                      tag);
+  }
+}
+
+// The all-reduce of rows r*64 .. r*64+63 of an H-long f32 product held as one
+// partial per XCD (part: [8][H] words): sum in XCD order, then out = bf16(res +
+// bf16(sum)) for those rows, published to this XCD's copy (bf16 pairs), and
+// the whole vector read back into `full` (LDS, H/2 words).  `res` is the
+// residual in LDS (bf16 pairs).
+__device__ __forceinline__ void allreduce_residual(const uint32_t* part, int H, int r,
+                                                   const uint32_t* res, uint32_t* mine_xcd,
+                                                   uint32_t* full, uint32_t tag, float* red,
+                                                   int* err) {
+  const int tid = threadIdx.x;
+  {
+    const int y = tid / 32, i2 = tid % 32;          // 256 threads: 8 XCDs x 32 word pairs
+    const u32x2 v = ll_get2<kCoherent>(part, (uint32_t)(y * H + 64 * r + 2 * i2), tag, err);
+    red[y * 64 + 2 * i2] = __uint_as_float(v.x);
+    red[y * 64 + 2 * i2 + 1] = __uint_as_float(v.y);
+  }
+  __syncthreads();
+  if (tid < 32) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int y = 0; y < kXcds; ++y) {
+      s0 += red[y * 64 + 2 * tid];
+      s1 += red[y * 64 + 2 * tid + 1];
+    }
+    const int w = 32 * r + tid;                      // word of rows 64r + 2 tid, +1
+    const uint32_t rw = res[w];
+    const uint32_t pr = bf_pair(f2bf(bf_lo(rw) + rbf(s0)), f2bf(bf_hi(rw) + rbf(s1)));
+    ll_put<kXcdLocal>(mine_xcd, (uint32_t)w, pr, tag);
+  }
+  ll_stage<kXcdLocal>(mine_xcd, H, tag, full, err);
+  __syncthreads();
+}
+
+__device__ __forceinline__ void stamp(uint64_t*& tl) {
+  if (tl && threadIdx.x == 0) *tl++ = wall_clock64();
+}
+
+template <int kCmax, int kR>
+__device__ __forceinline__ void lm_head_rows(int64_t row0, int V, int lane,
+                                             const u32x4 (&xr)[kCmax],
+                                             const u32x4 (&w)[kR][kCmax], float* logits,
+                                             float& best, int& besti) {
+  if (row0 >= V) return;
+  const int nvalid = (int)((V - row0) < kR ? (V - row0) : kR);
+  float acc[kR];
+  dot_loaded<kCmax, kR>(w, xr, acc);
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    if (r < nvalid) {
+      const float y = rbf(acc[r]);
+      if (lane == r) logits[row0 + r] = y;
+      if (better(y, (int)(row0 + r), best, besti)) {
+        best = y;
+        besti = (int)(row0 + r);
+      }
+    }
+  }
+}
+
+// lm_head over the whole grid with the block's row groups double-buffered in
+// registers; publishes the block's (value, index) pick as flag-in-data words.
+template <int kCmax, int kR>
+__device__ __forceinline__ void lm_head_grid(const u32x4 (&xr)[kCmax], const bf16* __restrict__ W,
+                                             float* logits, uint32_t* best_ll, uint32_t tag,
+                                             int K, int V, u32x4 (&wa)[kR][kCmax]) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock * kR;
+  int64_t r0 = ((int64_t)blockIdx.x * kWavesPerBlock + wave) * kR;
+  u32x4 wb[kR][kCmax];
+  float best = kNegInf;
+  int besti = 0x7fffffff;
+  while (r0 < V) {
+    const int64_t r1 = r0 + stride;
+    gemv_issue<kCmax, kR>((int)(r1 / (kWavesPerBlock * kR)), W, K, V, wb);
+    lm_head_rows<kCmax, kR>(r0, V, lane, xr, wa, logits, best, besti);
+    if (r1 >= V) break;
+    const int64_t r2 = r1 + stride;
+    gemv_issue<kCmax, kR>((int)(r2 / (kWavesPerBlock * kR)), W, K, V, wa);
+    lm_head_rows<kCmax, kR>(r1, V, lane, xr, wb, logits, best, besti);
+    r0 = r2;
+  }
+  __shared__ float sv[kWavesPerBlock];
+  __shared__ int si[kWavesPerBlock];
+  if (lane == 0) {
+    sv[wave] = best;
+    si[wave] = besti;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = sv[0];
+    int i = si[0];
+    for (int w = 1; w < kWavesPerBlock; ++w)
+      if (better(sv[w], si[w], b, i)) {
+        b = sv[w];
+        i = si[w];
+      }
+    ll_put2(best_ll, 2u * blockIdx.x, __float_as_uint(b), (uint32_t)i, tag);
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// The kernel (Qwen3-1.7B shape only: H 2048, 16 q / 8 kv heads of 128, I 6144;
+// the host entry checks it).  kMaxItems attention splits per block.
+// ---------------------------------------------------------------------------
+constexpr int kH = 2048, kQD = 2048, kI = 6144, kD = 128, kG = 2;
+constexpr int kMaxItems = 4;
+constexpr int kXO = kG * kD;                 // 256: an XCD's attention outputs (o's K slice)
+constexpr int kXI = kI / kXcds;              // 768: an XCD's intermediate columns (down's K slice)
+
+__global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdArgs xa, int steps) {
+  constexpr int kCH = kH / 512;              // 16-byte chunks per lane of a 2048 row
+  constexpr int kRqkv = 4, kRgu = 12, kRhead = 4;
+  __shared__ __attribute__((aligned(16))) uint32_t xs[kXI / 2];   // o / down input slice
+  __shared__ __attribute__((aligned(16))) uint32_t hid_s[kH / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t h1_s[kH / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t hs[(kG + 2) * kD / 2];
+  __shared__ float s_sc[kMaxItems][kG * kSplit];
+  __shared__ float s_new[kMaxItems][kG];
+  __shared__ float red[kXcds * 64];
+  const int x = (int)blockIdx.x % kXcds, r = (int)blockIdx.x / kXcds;
+  const int nb = gridDim.x;
+  const int V = a.vocab;
+  const float eps = a.eps;
+  int* const err = a.err;
+  if (threadIdx.x == 0 && xcc_id() != x) raise_error(err, kErrPlacement | kErrSync);
+  int P = coh_ldi(a.pos);
+  int tok = (int)__hip_atomic_load(a.ids, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int lane = threadIdx.x & (kWave - 1);
+
+  // this block's rows: qkv (16 full rows), gate/up (48), o and down (64 of the K slice)
+  const int qkv_row0 = r < 16 ? kXO * x + 16 * r
+                              : (r < 24 ? kQD + kD * x + 16 * (r - 16)
+                                        : kQD + 8 * kD + kD * x + 16 * (r - 24));
+  const int vb_qkv = qkv_row0 / (kWavesPerBlock * kRqkv);
+  const int vb_gu = kRanks * x + r;
+  const int qkv_n = kQD + 2 * 8 * kD;
+  // this XCD's exchange arenas
+  uint32_t* const hid_x = word_at(xa.hid, (int64_t)x * (kH / 2));
+  uint32_t* const h1_x = word_at(xa.h1, (int64_t)x * (kH / 2));
+  const int64_t heads_words = (int64_t)a.nsplit * (kXcds * kG);
+  uint32_t* const smax_x = word_at(xa.smax, x * heads_words);
+  uint32_t* const psum_x = word_at(xa.psum, x * heads_words);
+  uint32_t* const pout_x = word_at(xa.pout, x * heads_words * kD);
+  uint32_t* const attn_x = word_at(a.x_attn, (int64_t)x * (kXO / 2));   // the merged outputs
+  uint32_t* const mid_x = word_at(a.x_mid, (int64_t)x * (kXI / 2));     // the SwiGLU values
+  uint32_t* const opart_x = word_at(xa.opart, (int64_t)x * kH);
+  uint32_t* const dpart_x = word_at(xa.dpart, (int64_t)x * kH);
+
+  u32x4 wq[kRqkv][kCH], wg[kRgu][kCH], wo[8][1], wd[8][3];
+  u32x4 gq_in[kCH], gq_post[kCH];
+  gemv_issue<kCH, kRqkv>(vb_qkv, (const bf16*)a.layers[0].w_qkv, kH, qkv_n, wq);
+  load_x<kCH>((const bf16*)a.layers[0].gamma_in, kH / 8, lane, gq_in);
+  for (int t = 0; t < steps; ++t, ++P) {
+    uint64_t* tl = (a.timeline && t < a.timeline_steps)
+                       ? a.timeline + ((int64_t)t * nb + blockIdx.x) * (14 * a.n_layers + 4)
+                       : nullptr;
+    const uint32_t tag0 = a.epoch + (uint32_t)t * (uint32_t)(a.n_layers + 1);
+    {
+      const int id = (tok >= 0 && tok < V) ? tok : 0;
+      const uint32_t* row = reinterpret_cast<const uint32_t*>((const bf16*)a.w_embed +
+                                                              (int64_t)id * kH);
+      for (int i = threadIdx.x; i < kH / 8; i += kBlock)
+        *reinterpret_cast<u32x4*>(hid_s + 4 * i) = *reinterpret_cast<const u32x4*>(row + 4 * i);
+    }
+    const int Pc = (P >= 0 && P < a.max_pages * kPage) ? P : 0;
+    const int nact = (Pc + kSplit - 1) / kSplit;
+    const int parts = nact > 0 ? nact : 1;
+    __syncthreads();
+    for (int l = 0; l < a.n_layers; ++l) {
+      const TfdLayer w = a.layers[l];
+      const uint32_t tag = tag0 + (uint32_t)l + 1u;
+      // ---- qkv (the hidden state is in hid_s)
+      stamp(tl);
+      gemv_finish_ll<kCH, kRqkv, kNorm, kStore, kXcdLocal>(vb_qkv, hid_s, gq_in, nullptr,
+                                                           a.x_qkv, tag, kH, qkv_n, eps, wq);
+      stamp(tl);
+      // the o slab, this block's first K / V tiles and the q/k norm operands
+      // stream while the QKV projection arrives
+      slab_issue<1>((const bf16*)w.w_o, kQD, 64 * r, kXO * x, wo);
+      KTile<kD> kt;
+      VTile<kD> vt;
+      const int s0 = r < parts ? r : parts;
+      k_tile_issue<kD, true>(s0, x, P, a.page_table, a.max_pages, (const bf16*)w.k_pool,
+                             a.num_pages, 8, kt);
+      v_tile_issue<kD, true>(s0, x, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
+                             a.num_pages, 8, vt);
+      const QKPre pre = qk_prefetch<kD, kG>(P, P, (const bf16*)w.gamma_q, (const bf16*)w.gamma_k,
+                                            (const bf16*)a.cos_table, (const bf16*)a.sin_table,
+                                            a.rope_rows, a.page_table, a.max_pages);
+      const AttnLL ll{a.x_qkv, smax_x, psum_x, pout_x, a.x_attn, tag};
+      // ---- attention part 1: scores (splits r, r + 32, ... of kv head x)
+      for (int sp = r, j = 0; sp < parts && j < kMaxItems; sp += kRanks, ++j) {
+        if (j > 0)
+          k_tile_issue<kD, true>(sp, x, P, a.page_table, a.max_pages, (const bf16*)w.k_pool,
+                                 a.num_pages, 8, kt);
+        stage_head_ll<kD, kG, kXcdLocal>(x, 8 * kG, 8, ll, hs, err);
+        __syncthreads();
+        if (j == 0) stamp(tl);
+        attn_scores_phase<kD, kG, true, kXcdLocal>(sp, x, hs, pre, a.rope_rows, P, P,
+                                                   a.page_table, a.max_pages, (bf16*)w.k_pool,
+                                                   (bf16*)w.v_pool, a.num_pages, 8, a.scale, eps,
+                                                   s_sc[j], 0, nullptr, s_new[j], ll, kt, err);
+        if (j == 0) stamp(tl);
+      }
+      // ---- part 2: P.V partials
+      for (int sp = r, j = 0; sp < parts && j < kMaxItems; sp += kRanks, ++j) {
+        if (j > 0)
+          v_tile_issue<kD, true>(sp, x, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
+                                 a.num_pages, 8, vt);
+        if (j == 0) stamp(tl);
+        attn_pv_phase<kD, kG, true, NoHook, RowOut, kXcdLocal>(
+            sp, x, a.nsplit, nullptr, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
+            a.num_pages, 8, s_sc[j], 0, nullptr, s_new[j], nullptr, nullptr, nullptr, nullptr,
+            ll, vt, err);
+        if (j == 0) stamp(tl);
+      }
+      // ---- part 3: merge
+      for (int sp = r, j = 0; sp < parts && j < kMaxItems; sp += kRanks, ++j) {
+        if (j == 0) stamp(tl);
+        attn_merge_ll<kD, kG, NoHook, kXcdLocal>(sp, x, P, a.max_pages, 8, s_new[j], ll, err);
+        __syncthreads();
+        if (j == 0) stamp(tl);
+      }
+      if (r >= parts) {
+        stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl);
+      }
+      // ---- o: this XCD's 256 attention outputs against the o slab
+      ll_stage<kXcdLocal>(attn_x, kXO, tag, xs, err);
+      __syncthreads();
+      stamp(tl);
+      slab_finish<1>(xs, wo, opart_x, 64 * r, tag);
+      stamp(tl);
+      // gate/up weights stream while the o partials are summed
+      gemv_issue<kCH, kRgu>(vb_gu, (const bf16*)w.w_gu, kH, 2 * kI, wg);
+      load_x<kCH>((const bf16*)w.gamma_post, kH / 8, lane, gq_post);
+      allreduce_residual(xa.opart, kH, r, hid_s, h1_x, h1_s, tag, red, err);
+      stamp(tl);
+      // ---- gate/up + SwiGLU: this XCD's 768 columns
+      gemv_finish_ll<kCH, kRgu, kNorm, kSwiglu, kXcdLocal>(vb_gu, h1_s, gq_post, nullptr,
+                                                           a.x_mid, tag, kH, 2 * kI, eps, wg);
+      stamp(tl);
+      slab_issue<3>((const bf16*)w.w_down, kI, 64 * r, kXI * x, wd);
+      // ---- down: this XCD's 768 SwiGLU values against the down slab
+      ll_stage<kXcdLocal>(mid_x, kXI, tag, xs, err);
+      __syncthreads();
+      stamp(tl);
+      slab_finish<3>(xs, wd, dpart_x, 64 * r, tag);
+      // the next layer's qkv weights -- after the last layer, layer 0's for the
+      // next step -- stream while the down partials are summed
+      gemv_issue<kCH, kRqkv>(vb_qkv, (const bf16*)a.layers[(l + 1) % a.n_layers].w_qkv, kH,
+                             qkv_n, wq);
+      load_x<kCH>((const bf16*)a.layers[(l + 1) % a.n_layers].gamma_in, kH / 8, lane, gq_in);
+      allreduce_residual(xa.dpart, kH, r, h1_s, hid_x, hid_s, tag, red, err);
+      stamp(tl);
+    }
+    // ---- head: final norm, logits, block pick
+    {
+      const uint32_t tag_head = tag0 + (uint32_t)a.n_layers;
+      u32x4 wa[kRhead][kCH], gr[kCH];
+      gemv_issue<kCH, kRhead>((int)blockIdx.x, (const bf16*)a.w_head, kH, V, wa);
+      load_x<kCH>((const bf16*)a.gamma_final, kH / 8, lane, gr);
+      stamp(tl);
+      u32x4 xr[kCH];
+      x_from_lds<kCH>(hid_s, kH / 8, lane, xr);
+      rms_norm_apply<kCH>(xr, gr, kH, eps);
+      lm_head_grid<kCH, kRhead>(xr, (const bf16*)a.w_head, a.logits, a.x_best, tag_head + 1u, kH,
+                                V, wa);
+      stamp(tl);
+    }
+    stamp(tl);
+    tok = finalize_ll(a.x_best, nb, tag0 + (uint32_t)a.n_layers + 1u, P, a.inp, a.prompt_len,
+                      a.nsteps, V, a.ids, a.pos, a.sam, err);
+    stamp(tl);
+    if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSync) break;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int tfd_decode_xcd(const TfdDecodeArgs* args, const TfdXcdArgs* xcd, int steps, void* stream) {
+  if (!args || !xcd) return fail(kBadArg, "decode_xcd: null args");
+  const TfdDecodeArgs& a = *args;
+  const TfdXcdArgs& xa = *xcd;
+  if (!a.layers || !a.w_embed || !a.w_head || !a.gamma_final || !a.cos_table || !a.sin_table ||
+      !a.page_table || !a.x_qkv || !a.x_attn || !a.x_mid || !a.x_best || !a.logits || !a.ids ||
+      !a.pos || !a.inp || !a.prompt_len || !a.sam || !a.err || !xa.hid || !xa.h1 || !xa.opart ||
+      !xa.dpart || !xa.smax || !xa.psum || !xa.pout)
+    return fail(kBadArg, "decode_xcd: null pointer in args");
+  if (steps < 0) return fail(kBadArg, "decode_xcd: steps=%d", steps);
+  if (steps == 0) return 0;
+  if (a.n_layers <= 0 || a.hidden != kH || a.heads != 16 || a.kv_heads != 8 ||
+      a.head_dim != kD || a.intermediate != kI || a.vocab <= 0 || a.nsteps <= 0)
+    return fail(kUnsupported,
+                "decode_xcd: partitioned for hidden 2048, 16 q / 8 kv heads of 128, "
+                "intermediate 6144 (got %d, %d / %d of %d, %d)",
+                a.hidden, a.heads, a.kv_heads, a.head_dim, a.intermediate);
+  if ((uint64_t)a.epoch + (uint64_t)steps * (uint64_t)(a.n_layers + 1) >= 0xffffffffull)
+    return fail(kBadArg, "decode_xcd: epoch %u + %d steps passes 2^32: zero the exchange "
+                "buffers and restart the epoch at 0", a.epoch, steps);
+  if ((int64_t)a.nsplit * kSplit < (int64_t)a.max_pages * kPage || a.num_pages <= 0 ||
+      a.nsplit > kRanks * kMaxItems)
+    return fail(kBadShape, "decode_xcd: nsplit=%d must cover max_pages=%d and be at most %d",
+                a.nsplit, a.max_pages, kRanks * kMaxItems);
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return fail((int)e, "decode_xcd: device query failed");
+  const int grid = kXcds * kRanks;
+  if (cus != grid)
+    return fail(kUnsupported, "decode_xcd: needs %d compute units (8 XCDs of 32), device has %d",
+                grid, cus);
+  int per_cu = 0;
+  const void* fn = reinterpret_cast<const void*>(&k_decode_xcd);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kBlock, 0);
+  if (e != hipSuccess) return fail((int)e, "decode_xcd: occupancy query failed");
+  if (per_cu < 1)
+    return fail(kUnsupported, "decode_xcd: a block does not fit a compute unit");
+  TfdDecodeArgs karg = a;
+  TfdXcdArgs kx = xa;
+  int ksteps = steps;
+  void* kargs[] = {&karg, &kx, &ksteps};
+  static const bool plain = [] {
+    const char* v = getenv("TFD_PLAIN_LAUNCH");
+    return v && v[0] == '1';
+  }();
+  if (plain)
+    e = hipLaunchKernel(fn, dim3(grid), dim3(kBlock), kargs, 0, (hipStream_t)stream);
+  else
+    e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kBlock), kargs, 0, (hipStream_t)stream);
+  if (e != hipSuccess) return fail((int)e, "decode_xcd: launch failed: %s", hipGetErrorString(e));
+  return launched("decode_xcd");
+}
+
+}  // extern "C"

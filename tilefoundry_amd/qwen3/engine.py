@@ -79,7 +79,9 @@ class Engine:
                  page_seed: int | None = 0, graph: bool = True,
                  lm_head_blocks: int = 2048, mode: str | None = None):
         """*mode*: ``"persistent"`` runs whole steps in one cooperative launch
-        (``tfd_decode_persistent``); ``"graph"`` replays a captured graph of the
+        (``tfd_decode_persistent``); ``"xcd"`` does the same with each layer split
+        over the device's 8 XCDs (``tfd_decode_xcd``: the Qwen3-1.7B shape on a
+        256-CU device); ``"graph"`` replays a captured graph of the
         per-phase launches; ``"direct"`` issues those launches each step.  The
         default is ``"graph"`` (``"direct"`` when *graph* is False)."""
         if cfg.dtype != torch.bfloat16:
@@ -103,14 +105,16 @@ class Engine:
                              f"({cfg.max_position_embeddings} positions)")
         self.nb = lm_head_blocks
         self.mode = mode or ("graph" if graph else "direct")
-        if self.mode not in ("persistent", "graph", "direct"):
+        if self.mode not in ("persistent", "xcd", "graph", "direct"):
             raise ValueError(f"mode {self.mode!r}")
         self._lib = lib()
         self._pack(weights, page_seed)
         self._buffers()
         self.graph = None
-        if self.mode == "persistent":
+        if self.mode in ("persistent", "xcd"):
             self._persistent_args()
+        if self.mode == "xcd":
+            self._xcd_args()
         elif self.mode == "graph":
             self._capture()
 
@@ -269,15 +273,31 @@ class Engine:
             inp=ptr(self.inp), prompt_len=ptr(self.plen), sam=ptr(self.sam), nsteps=self.nsteps,
             err=ptr(self.err))
 
+    def _xcd_args(self):
+        """The per-XCD exchange arenas of ``tfd_decode_xcd`` (TfdXcdArgs)."""
+        X, H = _lib.XCDS, self.H
+        words = {"hid": X * H // 2, "h1": X * H // 2, "opart": X * H, "dpart": X * H,
+                 "smax": X * self.nsplit * self.HQ, "psum": X * self.nsplit * self.HQ,
+                 "pout": X * self.nsplit * self.HQ * self.D}
+        self.xcd_buf = {k: torch.zeros(2 * n, device=self.device, dtype=torch.int32)
+                        for k, n in words.items()}
+        self.xcd_args = _lib.TfdXcdArgs(**{k: ptr(t) for k, t in self.xcd_buf.items()})
+
     def _launch_persistent(self, n: int):
         """One launch of *n* steps; advances the exchange-buffer epoch past them."""
         tags = n * _lib.tags_per_step(self.L)
         if self.epoch + tags >= 0xFFFFFFFF:
             for t in self.xbuf.values():
                 t.zero_()
+            for t in getattr(self, "xcd_buf", {}).values():
+                t.zero_()
             self.epoch = 0
         self.args.epoch = self.epoch
-        self._lib.tfd_decode_persistent(ctypes.byref(self.args), n, 0, self._stream())
+        if self.mode == "xcd":
+            self._lib.tfd_decode_xcd(ctypes.byref(self.args), ctypes.byref(self.xcd_args), n,
+                                     self._stream())
+        else:
+            self._lib.tfd_decode_persistent(ctypes.byref(self.args), n, 0, self._stream())
         self.epoch += tags
 
     def phase_timeline(self, prompt_ids: list[int], steps: int) -> torch.Tensor:
@@ -286,8 +306,8 @@ class Engine:
         block 0 began the first step -- per layer the qkv, attention scores, P.V
         and merge, o, gate/up and down phases, then the head and the pick; for
         each, when the block had its input and when its output was out."""
-        if self.mode != "persistent":
-            raise ValueError("the phase timeline belongs to the persistent kernel")
+        if self.mode not in ("persistent", "xcd"):
+            raise ValueError("the phase timeline belongs to the persistent kernels")
         n = _lib.timeline_stamps(self.L)
         buf = torch.zeros(steps * self.grid * n, device=self.device, dtype=torch.int64)
         self._load_prompt(prompt_ids)
@@ -307,7 +327,7 @@ class Engine:
         """*n* decode steps: one persistent launch, or n replays / direct steps."""
         if n <= 0:
             return
-        if self.mode == "persistent":
+        if self.mode in ("persistent", "xcd"):
             self._launch_persistent(n)
         else:
             for _ in range(n):
@@ -315,7 +335,7 @@ class Engine:
 
     def replay(self):
         """One decode step."""
-        if self.mode == "persistent":
+        if self.mode in ("persistent", "xcd"):
             self._launch_persistent(1)
         elif self.graph is not None:
             self.graph.replay()
@@ -341,6 +361,10 @@ class Engine:
         """Raise if a kernel flagged an out-of-range index since the last reset."""
         e = int(self.err.item())
         if e:
+            if e & _lib.ERR_PLACEMENT:
+                raise RuntimeError("the XCD-partitioned decode kernel found a block on another "
+                                   "XCD than its partition assumes (block % 8); its results "
+                                   "are void")
             if e & _lib.ERR_SYNC:
                 raise RuntimeError("the persistent decode kernel gave up waiting for another "
                                    "block's data (bounded wait exceeded); its results are void")
