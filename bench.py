@@ -303,7 +303,7 @@ def main(argv=None) -> int:
     ap.add_argument("--kernel-rounds", type=int, default=20)
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a 1 GiB device copy (counter calibration) and exit")
-    ap.add_argument("--mode", default="persistent", choices=("persistent", "xcd", "graph"),
+    ap.add_argument("--mode", default="xcd", choices=("persistent", "xcd", "graph"),
                     help="persistent: one cooperative launch per run of steps; xcd: the same "
                          "with each layer split over the 8 XCDs; graph: a captured graph of "
                          "per-phase launches replayed per token")

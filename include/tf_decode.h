@@ -307,7 +307,7 @@ typedef struct TfdDecodeArgs {
 #define TFD_TAGS_PER_STEP(n_layers) ((n_layers) + 1)
 
 #define TFD_ERR_SYNC 16 /* a wait for another block's data passed its bound; the launch gave up */
-#define TFD_ERR_PLACEMENT 32 /* tfd_decode_xcd: a block ran on another XCD than block % 8 */
+#define TFD_ERR_PLACEMENT 32 /* tfd_decode_xcd: a block read an XCC id outside 0..7 */
 
 /* Run `steps` decode steps in one launch.  nblocks <= 0 picks one block per
  * compute unit.  Returns -3 if the shape has no persistent instance (hidden
@@ -337,8 +337,10 @@ typedef struct TfdXcdArgs {
  * order.  For the Qwen3-1.7B shape only (hidden 2048, 16 q / 8 kv heads of 128,
  * intermediate 6144); -3 otherwise or on a device that is not 8 x 32 compute units.
  * args->x_hid, x_h1, x_smax, x_psum and x_pout are not used (the XCD arenas replace
- * them); nsplit <= 128.  A block that finds itself on another XCD than block % 8
- * raises TFD_ERR_PLACEMENT | TFD_ERR_SYNC and the launch gives up. */
+ * them); nsplit <= 128.  Block b plays the XCD of its hardware XCC id as rank b / 8;
+ * an XCC id outside 0..7 raises TFD_ERR_PLACEMENT | TFD_ERR_SYNC and the launch gives
+ * up, and a placement that is not round-robin over the XCDs leaves some rank unplayed,
+ * which ends the launch with TFD_ERR_SYNC. */
 int tfd_decode_xcd(const TfdDecodeArgs* args, const TfdXcdArgs* xcd, int steps, void* stream);
 
 #ifdef __cplusplus

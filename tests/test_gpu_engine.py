@@ -213,3 +213,22 @@ def test_xcd_kernel_tracks_the_persistent_kernel(gpu_device):
     assert c.tokens == b.tokens
     one = [xcd.generate(prompt, 1)]
     assert one[0].tokens == b.tokens[:1]
+
+
+def test_xcd_kernel_is_independent_of_where_a_launch_starts(gpu_device):
+    """The dispatcher's first XCD moves with the workgroups dispatched before a
+    launch.  Single-workgroup kernels launched in between rotate it through
+    every offset; each block takes its XCD from the hardware and its rank from
+    block / 8, so every run plays the same partition and returns the same bits."""
+    cfg = QWEN3_1_7B.with_(num_hidden_layers=2)
+    w = synthetic_weights(cfg, seed=6, norms="ones")
+    prompt = _prompt(12, cfg.vocab_size, seed=9)
+    xcd = Engine(cfg, w, device=gpu_device, max_new=16, prompt_room=12, mode="xcd")
+    base = xcd.generate(prompt, 16, record_logits=True)
+    one = torch.zeros(1, device=gpu_device)
+    for shift in range(1, 8):
+        for _ in range(shift):
+            one.add_(1.0)                           # one workgroup
+        run = xcd.generate(prompt, 16, record_logits=True)
+        assert run.tokens == base.tokens, shift
+        assert torch.equal(run.logits, base.logits), shift

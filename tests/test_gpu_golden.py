@@ -106,7 +106,9 @@ def test_c2_full_depth_against_golden(gpu_device, norms):
         upto = STEPS if first is None else first + 1
         for k in range(upto):
             top8 = gold["top8"][k]
-            assert _top8_error(run.logits[k], top8) <= TOL * abs(top8[0][1]), (mode, k)
+            # the teacher-forced bound: the bar, or twice the oracle's own noise
+            err = _top8_error(run.logits[k], top8)
+            assert err <= max(TOL * abs(top8[0][1]), 2 * noise_max), (mode, k, err)
         if first is not None:
             k = first
             top8 = gold["top8"][k]

@@ -18,7 +18,7 @@ ABI_VERSION = 12
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS, EPI_RESID_F32 = 0, 1, 2, 3, 4
 ERR_TOKEN_RANGE, ERR_POS_RANGE, ERR_PAGE_RANGE, ERR_STEP_RANGE, ERR_SYNC = 1, 2, 4, 8, 16
-ERR_PLACEMENT = 32          # tfd_decode_xcd: a block ran on another XCD than block % 8
+ERR_PLACEMENT = 32          # tfd_decode_xcd: a block read an XCC id outside 0..7
 PAGE_SIZE = 16
 SKINNY_COUNTERS = 16384     # tile counters at the start of a skinny-GEMM work buffer
 NOALLOC_SCRATCH_FLOATS = SKINNY_COUNTERS + (1 << 21)   # tfd_gemm_skinny_bf16_noalloc's scratch

@@ -319,39 +319,12 @@ __device__ __forceinline__ void dot_rows(const bf16* __restrict__ W, int K, int 
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
 // ---------------------------------------------------------------------------
-// Thread groups a phase runs on: its thread index (0 .. kBlock-1) and its
-// barrier.  BlockGrp is the whole kBlock-thread block.  SubGrp<kFirst, kWaves>
-// is kWaves waves of a larger block starting at thread kFirst, with a barrier
-// of its own (an LDS arrival counter, so the block's other waves never wait
-// in it): a block can then run two groups side by side.
+// The thread group a phase runs on: its thread index (0 .. kBlock-1) and its
+// barrier.  Every caller today runs phases on the whole kBlock-thread block.
 // ---------------------------------------------------------------------------
 struct BlockGrp {
   static __device__ __forceinline__ int tid() { return (int)threadIdx.x; }
   static __device__ __forceinline__ void sync() { __syncthreads(); }
-};
-
-template <int kFirst, int kWaves>
-struct SubGrp {
-  static_assert(kWaves * kWave == kBlock, "a group plays one kBlock-thread block");
-  static __device__ __forceinline__ int tid() { return (int)threadIdx.x - kFirst; }
-  static __device__ __forceinline__ uint32_t* counter() {
-    __shared__ uint32_t arrivals;
-    return &arrivals;
-  }
-  // one thread of the block, followed by a whole-block barrier, before any sync()
-  static __device__ __forceinline__ void init() { *counter() = 0; }
-  static __device__ __forceinline__ void sync() {
-    // this wave's LDS accesses are complete before it counts itself in
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    uint32_t old = 0;
-    if ((threadIdx.x & (kWave - 1)) == 0)
-      old = __hip_atomic_fetch_add(counter(), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    old = __shfl(old, 0, kWave);
-    const uint32_t target = (old / kWaves + 1) * kWaves;   // every wave arrives once per barrier
-    while (__hip_atomic_load(counter(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
-      __builtin_amdgcn_s_sleep(0);
-    __asm__ volatile("" ::: "memory");
-  }
 };
 
 // Error flags a kernel raises instead of touching memory it was not given.
@@ -444,31 +417,40 @@ __device__ __forceinline__ uint32_t ll_get(const uint32_t* base, uint32_t word, 
 
 // Stage a flag-in-data bf16 vector of n values (n % 4 == 0) into LDS as plain
 // bf16 pairs; the caller synchronises the block before reading it.  Each
-// thread issues all its loads of a batch before checking any, so a long vector
-// costs one round trip rather than one per load.
+// thread issues all its loads of a batch, and while any of them is stale
+// issues them all again and checks them all: a batch costs one round trip per
+// poll, never one per load.
 template <int kPol = kCoherent, class Grp = BlockGrp>
 __device__ __forceinline__ void ll_stage(const uint32_t* ll, int n, uint32_t tag,
                                          uint32_t* __restrict__ lds, int* err) {
   constexpr int kBatch = 8;
   const int npairs = n / 4;
   for (int i0 = Grp::tid(); i0 < npairs; i0 += kBlock * kBatch) {
+    // loads of this batch the wave needs at all (its first lane has the most),
+    // as a wave-uniform count; lanes past the end re-read their first word
+    const int first = __builtin_amdgcn_readfirstlane(i0);
+    const int kn = (npairs - first + kBlock - 1) / kBlock;
     u32x4 v[kBatch];
+    uint32_t spins = 0;
+    for (;;) {
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int i = i0 + k * kBlock;
-      v[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(ll), (uint32_t)(i < npairs ? i : 0) * 16u,
-                                                   0, kPol);
+      for (int k = 0; k < kBatch; ++k) {
+        const int i = i0 + k * kBlock;
+        if (k < kn)
+          v[k] = __builtin_amdgcn_raw_buffer_load_b128(
+              rsrc(ll), (uint32_t)(i < npairs ? i : i0) * 16u, 0, kPol);
+      }
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k)
+        if (k < kn) ok = ok && v[k].y == tag && v[k].w == tag;
+      if (ok || ll_give_up(spins, err)) break;
+      __asm__ volatile("" ::: "memory");
     }
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       const int i = i0 + k * kBlock;
       if (i < npairs) {
-        uint32_t spins = 0;
-        while (v[k].y != tag || v[k].w != tag) {
-          if (ll_give_up(spins, err)) break;
-          __asm__ volatile("" ::: "memory");
-          v[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(ll), (uint32_t)i * 16u, 0, kPol);
-        }
         lds[2 * i] = v[k].x;
         lds[2 * i + 1] = v[k].z;
       }

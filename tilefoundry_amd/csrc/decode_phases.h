@@ -1139,14 +1139,17 @@ __device__ __forceinline__ void attn_pv_phase(
 // Part 3, persistent kernel only: every active split of a kv head merges its
 // own slice of the head group's G * D outputs (pairs of values), reading every
 // split's partials for that slice and the numerator sums, in split order --
-// the same arithmetic as the last-block merge above.
+// the same arithmetic as the last-block merge above.  Up to kChunk splits at a
+// time, every word of a chunk (partial sums, maxima, partial outputs and the
+// new key's values) polled in one round: a thread holds at most one of each.
 // ---------------------------------------------------------------------------
 template <int D, int G, class Hook = NoHook, int kPol = kCoherent, class Grp = BlockGrp>
 __device__ __forceinline__ void attn_merge_ll(int split, int h, int P, int max_pages,
                                               int kv_heads, const float* snew, const AttnLL& ll,
                                               int* err, const Hook& polled = Hook()) {
   constexpr int kPairs = G * D / 2;
-  constexpr int kChunk = 16;                          // splits staged at a time
+  constexpr int kChunk = 32;                          // splits staged at a time
+  static_assert(kChunk * G <= kBlock && kPairs + kChunk <= kBlock, "one word of a kind per thread");
   const int heads = kv_heads * G;
   const int tid = Grp::tid();
   if (P < 0 || P >= max_pages * kPage) P = 0;
@@ -1157,33 +1160,49 @@ __device__ __forceinline__ void attn_merge_ll(int split, int h, int P, int max_p
   const int nq = q1 - q0;
 
   __shared__ float sm[kChunk][G], ps[kChunk][G];
-  __shared__ u32x2 po[kChunk][kPairs];
+  // a chunk's partial outputs, split-major: nc * nq <= kPairs + kChunk - 1
+  __shared__ u32x2 po[kPairs + kChunk];
   float sv0 = 0.f, sv1 = 0.f, sp = 0.f, mx = kNegInf;
   const int o = 2 * (q0 + (tid < nq ? tid : 0));
   const int g = o / D, d = o % D;
   // the new key's values d, d + 1 (one word of the QKV projection)
-  const uint32_t vw = ll_get<kPol>(ll.qkv, (uint32_t)(heads * D + kv_heads * D + h * D + d) / 2u,
-                             ll.tag, err);
+  const uint32_t wv = (uint32_t)(heads * D + kv_heads * D + h * D + d) / 2u;
+  uint32_t vw = 0;
   for (int c0 = 0; c0 < participants; c0 += kChunk) {
     const int nc = (participants - c0) < kChunk ? (participants - c0) : kChunk;
-    for (int i = tid; i < nc * G; i += kBlock) {
-      const uint32_t w = (uint32_t)((c0 + i / G) * heads + h * G + i % G);
-      ps[i / G][i % G] = __uint_as_float(ll_get<kPol>(ll.psum, w, ll.tag, err));
-      // split maxima exist only for splits holding a prior position
-      sm[i / G][i % G] =
-          (c0 + i / G < nact) ? __uint_as_float(ll_get<kPol>(ll.smax, w, ll.tag, err)) : kNegInf;
+    const bool has_s = tid < nc * G;
+    // split maxima exist only for splits holding a prior position
+    const bool has_m = has_s && c0 + tid / G < nact;
+    const bool has_o = tid < nc * nq;
+    const bool has_v = c0 == 0 && tid < nq;
+    const int is = has_s ? tid : 0, io = has_o ? tid : 0;
+    const uint32_t ws = (uint32_t)((c0 + is / G) * heads + h * G + is % G);
+    const uint32_t wo = (uint32_t)(((int64_t)(c0 + io / nq) * heads + h * G) * D + 2 * (q0 + io % nq));
+    u32x2 a, b, v;
+    u32x4 c;
+    uint32_t spins = 0;
+    for (;;) {
+      a = __builtin_amdgcn_raw_buffer_load_b64(rsrc(ll.psum), ws * 8u, 0, kPol);
+      b = __builtin_amdgcn_raw_buffer_load_b64(rsrc(ll.smax), ws * 8u, 0, kPol);
+      c = __builtin_amdgcn_raw_buffer_load_b128(rsrc(ll.pout), wo * 8u, 0, kPol);
+      v = __builtin_amdgcn_raw_buffer_load_b64(rsrc(ll.qkv), wv * 8u, 0, kPol);
+      const bool ok = (!has_s || a.y == ll.tag) && (!has_m || b.y == ll.tag) &&
+                      (!has_o || (c.y == ll.tag && c.w == ll.tag)) && (!has_v || v.y == ll.tag);
+      if (ok || ll_give_up(spins, err)) break;
+      __asm__ volatile("" ::: "memory");
     }
-    for (int i = tid; i < nc * nq; i += kBlock) {
-      const int s = i / nq, q = i % nq;
-      po[s][q] = ll_get2<kPol>(ll.pout, (uint32_t)(((int64_t)(c0 + s) * heads + h * G) * D + 2 * (q0 + q)),
-                         ll.tag, err);
+    if (has_s) {
+      ps[is / G][is % G] = __uint_as_float(a.x);
+      sm[is / G][is % G] = has_m ? __uint_as_float(b.x) : kNegInf;
     }
+    if (has_o) po[io] = u32x2{c.x, c.z};
+    if (has_v) vw = v.x;
     Grp::sync();
     if (c0 == 0) polled();
     if (tid < nq) {
       for (int s = 0; s < nc; ++s) {
-        sv0 += __uint_as_float(po[s][tid].x);
-        sv1 += __uint_as_float(po[s][tid].y);
+        sv0 += __uint_as_float(po[s * nq + tid].x);
+        sv1 += __uint_as_float(po[s * nq + tid].y);
         sp += ps[s][g];
         mx = fmaxf(mx, sm[s][g]);
       }

@@ -7,9 +7,15 @@
 // the kernel keeps most of them inside an XCD: each layer is split across XCDs
 // the way tensor parallelism splits it across GPUs, with the XCD as the unit.
 //
-// Block b runs on XCD x = b % 8 as rank r = b / 8 of that XCD's 32 blocks (the
-// dispatcher places workgroups round-robin over XCDs; every block checks this
-// against its hardware XCC id).  Per layer, XCD x owns kv head x and its query
+// A block plays XCD x = its hardware XCC id and rank r = b / 8 among that XCD's
+// 32 blocks.  The dispatcher places workgroups round-robin over the XCDs, but
+// the XCD it starts a launch on moves from launch to launch (measured: b % 8 is
+// not the XCC id after some launches), so x comes from the hardware; under any
+// rotation the blocks of one XCD are b = c, c + 8, ..., so b / 8 is a rank.
+// Were placement ever not round-robin, some (x, r) would go unplayed, the
+// blocks waiting for its outputs would pass their poll bound, and the launch
+// would end with kErrSync: a wrong placement cannot produce results that look
+// valid.  Per layer, XCD x owns kv head x and its query
 // heads 2x, 2x + 1 (the Qwen3-1.7B shape: 16 q heads, 8 kv heads, head_dim 128,
 // hidden 2048, intermediate 6144):
 //   qkv     the XCD's 512 q/k/v rows (16 per block, full rows of 2048)
@@ -48,7 +54,7 @@ namespace {
 
 constexpr int kXcds = 8;
 constexpr int kRanks = 32;                 // blocks per XCD
-constexpr int kErrPlacement = 32;          // a block ran off the XCD its partition assumes
+constexpr int kErrPlacement = 32;          // an XCC id outside 0..7: not the 8-XCD device
 
 // Exchange buffers are arrays of 8-byte (payload, tag) words held as uint32_t:
 // word n starts at uint32 2n.
@@ -229,12 +235,13 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
   __shared__ float s_sc[kMaxItems][kG * kSplit];
   __shared__ float s_new[kMaxItems][kG];
   __shared__ float red[kXcds * 64];
-  const int x = (int)blockIdx.x % kXcds, r = (int)blockIdx.x / kXcds;
+  const int xcc = xcc_id();
+  const int x = xcc & (kXcds - 1), r = (int)blockIdx.x / kXcds;
   const int nb = gridDim.x;
   const int V = a.vocab;
   const float eps = a.eps;
   int* const err = a.err;
-  if (threadIdx.x == 0 && xcc_id() != x) raise_error(err, kErrPlacement | kErrSync);
+  if (threadIdx.x == 0 && xcc != x) raise_error(err, kErrPlacement | kErrSync);
   int P = coh_ldi(a.pos);
   int tok = (int)__hip_atomic_load(a.ids, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int lane = threadIdx.x & (kWave - 1);

@@ -362,9 +362,8 @@ class Engine:
         e = int(self.err.item())
         if e:
             if e & _lib.ERR_PLACEMENT:
-                raise RuntimeError("the XCD-partitioned decode kernel found a block on another "
-                                   "XCD than its partition assumes (block % 8); its results "
-                                   "are void")
+                raise RuntimeError("the XCD-partitioned decode kernel read an XCC id outside "
+                                   "0..7 (not an 8-XCD device); its results are void")
             if e & _lib.ERR_SYNC:
                 raise RuntimeError("the persistent decode kernel gave up waiting for another "
                                    "block's data (bounded wait exceeded); its results are void")
