@@ -59,3 +59,39 @@ def test_scatter_cache_goes_through_the_page_table():
             assert torch.equal(vpool[i, table[p // 16], :, p % 16], vs[i][p])
     written = P * hkv * d * L
     assert int((kpool != -7.0).sum()) == written and int((vpool != -7.0).sum()) == written
+
+
+@pytest.mark.parametrize("model", ["qwen3_5", "granite"])
+def test_hybrid_validate_rejects_what_the_kernels_cannot_read(model):
+    """The hybrid engines hand raw pointers to the kernels, so their weight
+    dicts are checked first: every declared name, shape and dtype."""
+    from tilefoundry_amd.hybrid import granite as G
+    from tilefoundry_amd.hybrid import qwen3_5 as Q
+
+    if model == "qwen3_5":
+        mod, cfg = Q, Q.Qwen35Config(hidden=64, layers=4, lin_key_heads=2, lin_value_heads=4,
+                                     lin_key_dim=16, lin_value_dim=16, heads=4, kv_heads=2,
+                                     head_dim=32, rot_dim=8, experts=8, top_k=2, moe_inter=32,
+                                     shared_inter=48, vocab=96)
+        victim = "layer3.w_in"                     # a full-attention layer's in-projection
+    else:
+        mod, cfg = G, G.GraniteConfig(hidden=64, layers=3, attention_layers=(1,), mamba_heads=4,
+                                      mamba_head_dim=16, d_state=16, heads=4, kv_heads=2,
+                                      head_dim=16, experts=6, top_k=2, moe_inter=32,
+                                      shared_inter=48, vocab=96)
+        victim = "layer0.s_down"                   # an expert block's row scales
+    w = mod.synthetic_weights(cfg, seed=1, device="cpu")
+    mod.validate(cfg, w)
+    assert set(mod.declared_shapes(cfg)) == set(w)
+    missing = dict(w)
+    del missing[victim]
+    with pytest.raises(KeyError, match=victim):
+        mod.validate(cfg, missing)
+    short = dict(w)
+    short[victim] = w[victim][:-1]
+    with pytest.raises(ValueError, match="shape"):
+        mod.validate(cfg, short)
+    retyped = dict(w)
+    retyped[victim] = w[victim].to(torch.float16)
+    with pytest.raises(ValueError, match="dtype"):
+        mod.validate(cfg, retyped)

@@ -138,8 +138,61 @@ def synthetic_weights(cfg: GraniteConfig, seed: int = 0, device: str = "cuda:0",
     return w
 
 
+U8 = torch.uint8
+
+
+def declared_shapes(cfg: GraniteConfig) -> dict[str, tuple[tuple[int, ...], torch.dtype]]:
+    """Every weight the engine reads: shape and dtype (fp8 linears as uint8
+    e4m3fn codes ``[N][K]`` with f32 row scales ``[N]``)."""
+    H, E, I, IS = cfg.hidden, cfg.experts, cfg.moe_inter, cfg.shared_inter
+    out = {"embed": ((cfg.vocab, H), BF), "gamma_final": ((H,), BF)}
+
+    def lin(p, name, N, K, scale=None):
+        out[p + name] = ((N, K), U8)
+        out[p + (scale or name + "_scale")] = ((N,), F32)
+
+    for i in range(cfg.layers):
+        p = f"layer{i}."
+        out[p + "gamma_in"] = ((H,), BF)
+        out[p + "gamma_post"] = ((H,), BF)
+        if cfg.is_attention(i):
+            lin(p, "w_in", cfg.attn_in, H)
+            lin(p, "w_out", H, cfg.heads * cfg.head_dim)
+        else:
+            lin(p, "w_in", cfg.mamba_in, H)
+            out[p + "conv_w"] = ((cfg.conv_dim, cfg.conv_kernel), BF)
+            out[p + "conv_b"] = ((cfg.conv_dim,), BF)
+            for n in ("a_log", "dt_bias", "d_skip"):
+                out[p + n] = ((cfg.mamba_heads,), BF)
+            out[p + "gamma_ssm"] = ((cfg.d_inner,), BF)
+            lin(p, "w_out", H, cfg.d_inner)
+        lin(p, "w_router", E, H)
+        lin(p, "w_gate", E * I, H, "s_gate")
+        lin(p, "w_up", E * I, H, "s_up")
+        lin(p, "w_down", E * H, I, "s_down")
+        lin(p, "w_shared_in", 2 * IS, H)
+        lin(p, "w_shared_out", H, IS)
+    return out
+
+
+def validate(cfg: GraniteConfig, weights: dict[str, torch.Tensor]) -> None:
+    """``KeyError`` for a missing weight, ``ValueError`` for a wrong shape or
+    dtype -- the kernels take raw pointers and trust both."""
+    for name, (shape, dt) in declared_shapes(cfg).items():
+        if name not in weights:
+            raise KeyError(f"weight {name!r} is declared but not supplied")
+        t = weights[name]
+        if tuple(t.shape) != shape:
+            raise ValueError(f"weight {name!r}: declared shape {shape}, got {tuple(t.shape)}")
+        if t.dtype != dt:
+            raise ValueError(f"weight {name!r}: declared dtype {dt}, got {t.dtype}")
+
+
 class GraniteEngine:
-    """A Granite-style hybrid decoder stepping `rows` sequences together."""
+    """A Granite-style hybrid decoder stepping `rows` sequences together.
+
+    ``weights`` is checked against ``declared_shapes(cfg)`` and copied to the
+    device (contiguous) where it is not there already."""
 
     def __init__(self, cfg: GraniteConfig, weights: dict[str, torch.Tensor], *, rows: int,
                  device: str = "cuda:0", max_steps: int = 1024, page_seed: int = 0,
@@ -168,6 +221,8 @@ class GraniteEngine:
 
     def _pack(self, w):
         cfg = self.cfg
+        validate(cfg, w)
+        w = {n: w[n].to(self.device).contiguous() for n in declared_shapes(cfg)}
         self.layers = []
         for i in range(cfg.layers):
             p = f"layer{i}."

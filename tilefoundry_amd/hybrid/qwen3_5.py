@@ -142,8 +142,44 @@ def synthetic_weights(cfg: Qwen35Config, seed: int = 0, device: str = "cuda:0",
     return w
 
 
+def declared_shapes(cfg: Qwen35Config) -> dict[str, tuple[int, ...]]:
+    """Every weight the engine reads and its shape (all bf16, row layouts)."""
+    H, E, I, IS = cfg.hidden, cfg.experts, cfg.moe_inter, cfg.shared_inter
+    out = {"embed": (cfg.vocab, H), "gamma_final": (H,), "head": (cfg.vocab, H)}
+    for i in range(cfg.layers):
+        p = f"layer{i}."
+        per = {"gamma_in": (H,), "gamma_post": (H,), "w_router": (E, H), "w_gate": (E, I, H),
+               "w_up": (E, I, H), "w_down": (E, H, I), "w_shared_in": (2 * IS, H),
+               "w_shared_out": (H, IS), "w_shared_scale": (H,)}
+        if cfg.is_full(i):
+            per.update(w_in=(cfg.attn_in, H), gamma_q=(cfg.head_dim,), gamma_k=(cfg.head_dim,),
+                       w_out=(H, cfg.heads * cfg.head_dim))
+        else:
+            per.update(w_in=(cfg.gdn_in, H), conv_w=(cfg.conv_dim, cfg.conv_kernel),
+                       a_log=(cfg.lin_value_heads,), dt_bias=(cfg.lin_value_heads,),
+                       gamma_gdn=(cfg.lin_value_dim,), w_out=(H, cfg.value_dim))
+        out.update({p + n: s for n, s in per.items()})
+    return out
+
+
+def validate(cfg: Qwen35Config, weights: dict[str, torch.Tensor]) -> None:
+    """``KeyError`` for a missing weight, ``ValueError`` for a wrong shape or
+    dtype -- the kernels take raw pointers and trust both."""
+    for name, shape in declared_shapes(cfg).items():
+        if name not in weights:
+            raise KeyError(f"weight {name!r} is declared but not supplied")
+        t = weights[name]
+        if tuple(t.shape) != shape:
+            raise ValueError(f"weight {name!r}: declared shape {shape}, got {tuple(t.shape)}")
+        if t.dtype != BF:
+            raise ValueError(f"weight {name!r}: declared dtype {BF}, got {t.dtype}")
+
+
 class Qwen35Engine:
-    """A Qwen3.5-style hybrid decoder stepping `rows` sequences together."""
+    """A Qwen3.5-style hybrid decoder stepping `rows` sequences together.
+
+    ``weights`` is checked against ``declared_shapes(cfg)`` and copied to the
+    device (contiguous) where it is not there already."""
 
     def __init__(self, cfg: Qwen35Config, weights: dict[str, torch.Tensor], *, rows: int,
                  device: str = "cuda:0", max_steps: int = 2112, page_seed: int = 0,
@@ -173,6 +209,8 @@ class Qwen35Engine:
 
     def _pack(self, w):
         cfg = self.cfg
+        validate(cfg, w)
+        w = {n: w[n].to(self.device).contiguous() for n in declared_shapes(cfg)}
         self.layers = []
         for i in range(cfg.layers):
             p = f"layer{i}."
