@@ -116,13 +116,18 @@ __device__ __forceinline__ float wave_max(float v) {
   return fmaxf(lo, hi);
 }
 
+// Every pointer these helpers take is device (global) memory.  Saying so keeps
+// the compiler from emitting FLAT loads for pointers it read from memory (the
+// per-layer weight tables): a FLAT load also counts against the LDS/scalar
+// counter, so the next LDS read or scalar load would wait for it.
+typedef const __attribute__((address_space(1))) u32x4 g_u32x4;
 __device__ __forceinline__ u32x4 load16(const bf16* p) {
-  return *reinterpret_cast<const u32x4*>(p);
+  return *(g_u32x4*)(p);
 }
 // Weights are streamed once per step: a non-temporal hint keeps them from
 // evicting the small activation vectors every block re-reads.
 __device__ __forceinline__ u32x4 load16_stream(const bf16* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return __builtin_nontemporal_load((g_u32x4*)(p));
 }
 
 // ---------------------------------------------------------------------------
