@@ -252,6 +252,100 @@ int tfd_bf16_to_f32_rows(const void* src, int lds, float* dst, int ldd, int rows
 int tfd_scaled_add_rows(const void* a, int lda, const void* b, int ldb, int b_f32, float m,
                         void* out, int ldo, int rows, int n, void* stream);
 
+/* The mixers' authored sub-functions, one launch each, for the runtime twins
+ * (tilefoundry_amd/hybrid/twin.py) -- the decode engines run the fused
+ * tfd_gdn_step / tfd_mamba_step instead, with the same arithmetic.  One token per
+ * row; no work buffers.
+ *
+ * tfd_conv_step_rows: the depthwise causal convolution closing on this token,
+ * out[c] = silu(sum_t window[c][t] * w[c][t] (+ bias[c])) over the 3-tap window
+ * [rows][channels][3] and the entry [rows][lde] (conv kernel 4).  policy
+ * TFD_POLICY_F32: f32 window / entry / out, no bias (Qwen3_5LinearAttention.
+ * conv_step, tests/models/qwen3_5_35b_a3b/model.py:124-136); TFD_POLICY_BF16: bf16
+ * window / entry / out, every product, the sum and the biased value rounded to bf16
+ * (GraniteMamba.conv_step, examples/granite_4_0_h_small-cuda/model.py:154-168). */
+typedef struct {
+  const void* window;
+  const void* entry;
+  int lde;
+  const void *conv_w, *conv_b; /* bf16 [channels][4], bf16 [channels] or NULL */
+  void* out;
+  int ldo, rows, channels, kernel, policy;
+} TfdConvStepArgs;
+int tfd_conv_step_rows(const TfdConvStepArgs* args, void* stream);
+
+/* Qwen3_5LinearAttention.l2_normalise (model.py:138-146): out = x * rsqrt(sum(x^2) +
+ * eps) for each of nvec f32 vectors of dim <= 256 (out may alias x). */
+int tfd_l2norm_f32(const float* x, float* out, int nvec, int dim, float eps, void* stream);
+
+/* Qwen3_5LinearAttention.delta_step (model.py:148-172) on an f32 state: with
+ * decay = exp(g), recalled = sum_k decay S[k][:] k[k], delta = (v - recalled) beta,
+ * S' = decay S + k delta^T, read = sum_k S'[k][:] q[k] qscale.  state_in/state_out
+ * [rows][heads][128][128] (may alias), q/k [rows][heads][128], v [rows][heads][128],
+ * g/beta [rows][heads], read [rows][heads][128], all f32. */
+typedef struct {
+  const float* state_in;
+  float* state_out;
+  const float *q, *k, *v, *g, *beta;
+  float* read;
+  float qscale;
+  int rows, heads, head_k_dim, head_v_dim;
+} TfdDeltaStepArgs;
+int tfd_delta_step_f32(const TfdDeltaStepArgs* args, void* stream);
+
+/* Qwen3_5FullAttention.partial_rope / partial_rope_kv (model.py:235-262, torch_ref
+ * f32): the first rot dims of each head as x * cos + rotate_half(x) * sin with the
+ * bf16 table rows at pos[row] ([rope_rows][rot]), the rest copied.  x / out f32
+ * [rows][ld] holding heads x head_dim values. */
+typedef struct {
+  const float* x;
+  int ldx;
+  float* out;
+  int ldo;
+  const int32_t* pos;
+  const void *cos_table, *sin_table;
+  int rope_rows, rows, heads, head_dim, rot;
+} TfdPartialRopeArgs;
+int tfd_partial_rope_f32(const TfdPartialRopeArgs* args, void* stream);
+
+/* GraniteMamba.ssm_step (examples/granite_4_0_h_small-cuda/model.py:170-221) at the
+ * HIR's bf16 rounding: dt = softplus(dt_raw + dt_bias), decay = exp(dt * -exp(a_log)),
+ * S' = S decay + bf16(bf16(dt B) x), y = bf16(C . bf16(S')) + bf16(x D).  state_in /
+ * state_out f32 [rows][heads][64][128] (may alias); x bf16 [rows][ldx] (heads x 64),
+ * b_vec / c_vec bf16 [rows][ld] (128, one group), dt_raw bf16 [rows][lddt],
+ * a_log / dt_bias / d_skip bf16 [heads]; y bf16 [rows][ldy]. */
+typedef struct {
+  const float* state_in;
+  float* state_out;
+  const void* x;
+  int ldx;
+  const void* b_vec;
+  int ldb;
+  const void* c_vec;
+  int ldc;
+  const void* dt_raw;
+  int lddt;
+  const void *a_log, *dt_bias, *d_skip;
+  void* y;
+  int ldy, rows, heads, head_dim, state_dim;
+} TfdSsmStepArgs;
+int tfd_ssm_step_bf16(const TfdSsmStepArgs* args, void* stream);
+
+/* gated_out's RMSNormGated (model.py:223-237): g = f32(y) * silu(f32(gate)), out =
+ * bf16(g * rsqrt(mean(g^2) + eps) * gamma) per row of n <= 8192 (y, gate, gamma, out
+ * bf16). */
+typedef struct {
+  const void* y;
+  int ldy;
+  const void* gate;
+  int ldg;
+  const void* gamma;
+  void* out;
+  int ldo, rows, n;
+  float eps;
+} TfdGatedNormArgs;
+int tfd_gated_rmsnorm_bf16(const TfdGatedNormArgs* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

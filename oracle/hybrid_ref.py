@@ -133,6 +133,31 @@ def moe_c4(x, weights, idx, w_gate, w_up, w_down, ws_gate, ws_up, ws_down, ws_sc
     return out
 
 
+def moe_c5_dense(x, weights, idx, w_gate, w_up, w_down, w_shared_in, w_shared_out):
+    """Granite routed experts + shared MLP at the HIR's rounding with the authored
+    bf16 weights (model.py:406-471): w_gate/w_up [E][I][H], w_down [E][H][I],
+    w_shared_in [2 IS][H], w_shared_out [H][IS].  -> bf16 values [B][H]."""
+    B, H = x.shape
+    out = torch.zeros(B, H)
+    silu = torch.nn.functional.silu
+    for b in range(B):
+        xb = bf(x[b])
+        weighted = []
+        for s in range(idx.shape[1]):
+            e = int(idx[b, s])
+            g = bf(mm_rows(w_gate[e].float(), xb))
+            u = bf(mm_rows(w_up[e].float(), xb))
+            inner = bf(bf(silu(g)) * u)
+            d = bf(mm_rows(w_down[e].float(), inner))
+            weighted.append(bf(d * weights[b, s].float()))
+        routed = bf(torch.stack(weighted).double().sum(dim=0).float())
+        both = bf(mm_rows(w_shared_in.float(), xb))
+        IS = w_shared_in.shape[0] // 2
+        inner = bf(bf(silu(both[:IS])) * both[IS:])
+        out[b] = bf(routed + bf(mm_rows(w_shared_out.float(), inner)))
+    return out
+
+
 def moe_c5(x, weights, idx, g_codes, g_scale, u_codes, u_scale, d_codes, d_scale,
            si_codes, si_scale, so_codes, so_scale):
     """Granite routed experts + shared MLP, HIR policy with fp8 weights
@@ -165,6 +190,30 @@ def moe_c5(x, weights, idx, g_codes, g_scale, u_codes, u_scale, d_codes, d_scale
 # ---------------------------------------------------------------------------
 # Gated DeltaNet decode step (a15), torch_ref policy
 # ---------------------------------------------------------------------------
+def conv_step_c4(conv_state, entry, conv_w):
+    """``Qwen3_5LinearAttention.conv_step`` (tests/models/qwen3_5_35b_a3b/model.py:124-136;
+    torch_ref f32): silu(sum(window * w)) over the window closing on `entry`.
+    conv_state [B][C][K-1], entry [B][C] (f32) -> (mixed [B][C], the window [B][C][K])."""
+    window = torch.cat((conv_state.float(), entry[:, :, None].float()), dim=2)
+    return torch.nn.functional.silu((window * conv_w.float()[None]).sum(dim=-1)), window
+
+
+def l2_normalise(x, eps=1e-6):
+    """``l2_normalise`` (model.py:138-146): x * rsqrt(sum(x^2) + eps) over the last axis."""
+    return x * torch.rsqrt(x.pow(2).sum(-1, keepdim=True) + eps)
+
+
+def delta_step(state, q, k, v, g, beta, qscale):
+    """``delta_step`` (model.py:148-172) with f64 sums: state [B][HV][DK][DV], q/k
+    [B][HV][DK], v [B][HV][DV], g/beta [B][HV] -> (read f32 [B][HV][DV], updated f32)."""
+    decayed = state.double() * torch.exp(g.double())[:, :, None, None]
+    recalled = (decayed * k.double()[:, :, :, None]).sum(dim=2)
+    delta = (v.double() - recalled) * beta.double()[:, :, None]
+    updated = decayed + k.double()[:, :, :, None] * delta[:, :, None, :]
+    read = (updated * (q.double() * qscale)[:, :, :, None]).sum(dim=2)
+    return read.float(), updated.float()
+
+
 def gdn_step(proj, conv_state, state, conv_w, a_log, dt_bias, gamma_gdn, *, hk, hv, dk, dv,
              l2_eps=1e-6, rms_eps=1e-6):
     """Everything of ``linear_attention`` between the in-projection and the
@@ -183,32 +232,62 @@ def gdn_step(proj, conv_state, state, conv_w, a_log, dt_bias, gamma_gdn, *, hk, 
     z = proj[:, conv:conv + val]
     b_raw = proj[:, conv + val:conv + val + hv]
     a_raw = proj[:, conv + val + hv:conv + val + 2 * hv]
-    window = torch.cat((conv_state.float(), entry[:, :, None].float()), dim=2)
-    mixed = torch.nn.functional.silu((window * conv_w.float()[None]).sum(dim=-1))
+    mixed, window = conv_step_c4(conv_state, entry, conv_w)
     q = mixed[:, :key].reshape(B, hk, dk).repeat_interleave(hv // hk, dim=1)
     k = mixed[:, key:2 * key].reshape(B, hk, dk).repeat_interleave(hv // hk, dim=1)
     v = mixed[:, 2 * key:].reshape(B, hv, dv)
-    q = q * torch.rsqrt(q.pow(2).sum(-1, keepdim=True) + l2_eps)       # l2_normalise :206-216
-    k = k * torch.rsqrt(k.pow(2).sum(-1, keepdim=True) + l2_eps)
+    q = l2_normalise(q, l2_eps)                                           # :206-216
+    k = l2_normalise(k, l2_eps)
     beta = torch.sigmoid(b_raw)
     g = -torch.exp(a_log.float()) * torch.nn.functional.softplus(a_raw + dt_bias.float())
-    # delta_step :218-241
-    decayed = state.double() * torch.exp(g.double())[:, :, None, None]
-    recalled = (decayed * k.double()[:, :, :, None]).sum(dim=2)
-    delta = (v.double() - recalled) * beta.double()[:, :, None]
-    updated = decayed + k.double()[:, :, :, None] * delta[:, :, None, :]
-    read = (updated * (q.double() * dk ** -0.5)[:, :, :, None]).sum(dim=2)
-    read = read.float()
+    read, updated = delta_step(state, q, k, v, g, beta, dk ** -0.5)      # :218-241
     # gated norm: _rms_norm(read, gamma_gdn) * silu(z), per value head
     normed = read * torch.rsqrt(read.pow(2).mean(-1, keepdim=True) + rms_eps) * gamma_gdn.float()
     gated = normed * torch.nn.functional.silu(z.reshape(B, hv, dv))
     new_conv = window[:, :, 1:].contiguous()
-    return gated.reshape(B, val), new_conv, updated.float()
+    return gated.reshape(B, val), new_conv, updated
 
 
 # ---------------------------------------------------------------------------
 # Mamba2 decode step (a19), HIR policy
 # ---------------------------------------------------------------------------
+def conv_step_c5(conv_state, entry, conv_w, conv_b):
+    """``GraniteMamba.conv_step`` (examples/granite_4_0_h_small-cuda/model.py:154-168) at
+    the HIR's rounding: bf16 window * kernel (each product rounded), the sum (f32,
+    rounded once), + bias (rounded), silu (rounded).  conv_state [B][C][K-1], entry
+    [B][C] (bf16 values) -> (mixed [B][C] bf16 values, the window [B][C][K])."""
+    window = torch.cat((conv_state.float(), entry[:, :, None].float()), dim=2)
+    weighted = bf(window * conv_w.float()[None])
+    summed = bf(weighted.double().sum(dim=-1).float())
+    return bf(torch.nn.functional.silu(bf(summed + conv_b.float()[None]))), window
+
+
+def ssm_step(ssm_state, x, bvec, cvec, dt_raw, a_log, dt_bias, d_skip):
+    """``GraniteMamba.ssm_step`` (model.py:170-221) at the HIR's rounding, f32 state.
+    ssm_state [B][NH][PD][NS], x [B][NH][PD], bvec/cvec [B][NG][NS], dt_raw [B][NH]
+    (bf16 values), a_log/dt_bias/d_skip [NH] -> (y bf16 values [B][NH][PD], updated)."""
+    nh, ng = x.shape[1], bvec.shape[1]
+    dt = bf(torch.nn.functional.softplus(bf(dt_raw + dt_bias.float()[None])))
+    a = -torch.exp(a_log.float())
+    decay = torch.exp(dt * a[None])                                          # f32
+    hpg = nh // ng
+    b_e = bvec.repeat_interleave(hpg, dim=1)[:, :, None, :]                  # [B][NH][1][NS]
+    c_e = cvec.repeat_interleave(hpg, dim=1)[:, :, None, :]
+    d_b = bf(dt[:, :, None, None] * b_e)
+    d_bx = bf(d_b * x[:, :, :, None])
+    updated = ssm_state.float() * decay[:, :, None, None] + d_bx
+    read = (bf(updated).double() * c_e.double()).sum(dim=-1).float()
+    y = bf(bf(read) + bf(x * d_skip.float()[None, :, None]))
+    return y, updated
+
+
+def gated_rmsnorm(y, gate, gamma, eps):
+    """gated_out's RMSNormGated (model.py:223-237): the gate multiplies before the norm,
+    f32, then one bf16 rounding.  y/gate [B][EXP] (bf16 values) -> bf16 values."""
+    gated = y * torch.nn.functional.silu(gate)
+    return bf(gated * torch.rsqrt(gated.pow(2).mean(-1, keepdim=True) + eps) * gamma.float())
+
+
 def mamba_step(proj, conv_state, ssm_state, conv_w, conv_b, a_log, dt_bias, d_skip, gamma_ssm,
                *, nh, pd, ns, ng, eps=1e-5):
     """``mamba_mixer`` between ``in_projection`` and ``out_proj``
@@ -225,31 +304,14 @@ def mamba_step(proj, conv_state, ssm_state, conv_w, conv_b, a_log, dt_bias, d_sk
     gate = proj[:, :exp_]
     entry = proj[:, exp_:exp_ + conv]
     dt_raw = proj[:, exp_ + conv:exp_ + conv + nh]
-    # conv_step: bf16 window * kernel (rounded), sum (f32, rounded once), + bias, silu
-    window = torch.cat((conv_state.float(), entry[:, :, None].float()), dim=2)
-    weighted = bf(window * conv_w.float()[None])
-    summed = bf(weighted.double().sum(dim=-1).float())
-    mixed = bf(torch.nn.functional.silu(bf(summed + conv_b.float()[None])))
+    mixed, window = conv_step_c5(conv_state, entry, conv_w, conv_b)
     x = mixed[:, :exp_].reshape(B, nh, pd)
     bvec = mixed[:, exp_:exp_ + ng * ns].reshape(B, ng, ns)
     cvec = mixed[:, exp_ + ng * ns:].reshape(B, ng, ns)
-    # ssm_step
-    dt = bf(torch.nn.functional.softplus(bf(dt_raw + dt_bias.float()[None])))
-    a = -torch.exp(a_log.float())
-    decay = torch.exp(dt * a[None])                                          # f32
-    hpg = nh // ng
-    b_e = bvec.repeat_interleave(hpg, dim=1)[:, :, None, :]                  # [B][NH][1][NS]
-    c_e = cvec.repeat_interleave(hpg, dim=1)[:, :, None, :]
-    d_b = bf(dt[:, :, None, None] * b_e)
-    d_bx = bf(d_b * x[:, :, :, None])
-    updated = ssm_state.float() * decay[:, :, None, None] + d_bx
-    read = (bf(updated).double() * c_e.double()).sum(dim=-1).float()
-    y = bf(bf(read) + bf(x * d_skip.float()[None, :, None]))
-    # gated_out's RMSNormGated: gate multiplies before the norm, f32, then bf16
-    gated = y.reshape(B, exp_) * torch.nn.functional.silu(gate)
-    normed = gated * torch.rsqrt(gated.pow(2).mean(-1, keepdim=True) + eps) * gamma_ssm.float()
+    y, updated = ssm_step(ssm_state, x, bvec, cvec, dt_raw, a_log, dt_bias, d_skip)
+    normed = gated_rmsnorm(y.reshape(B, exp_), gate, gamma_ssm, eps)
     new_conv = window[:, :, 1:].contiguous()
-    return bf(normed), new_conv, updated
+    return normed, new_conv, updated
 
 
 # ---------------------------------------------------------------------------
@@ -265,6 +327,16 @@ def _rms_flat(x, w, eps):
     """``tf.rms_norm`` as torch_ref.py:145-154 spells it: flat in w, f32."""
     xf = x.float()
     return xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps) * w.float()
+
+
+def partial_rope(x, cos, sin):
+    """``partial_rope`` / ``partial_rope_kv`` (tests/models/qwen3_5_35b_a3b/model.py:
+    235-262; torch_ref.py:165-181, f32): x [B][H][D], cos/sin [B][ROT] the rows at each
+    sequence's position; the first ROT dims rotated half, the tail passed through."""
+    rot = cos.shape[-1]
+    r = x[..., :rot].float()
+    c, s_ = cos.float()[:, None, :], sin.float()[:, None, :]
+    return torch.cat((r * c + _rotate_half(r) * s_, x[..., rot:].float()), -1)
 
 
 def qwen35_attend(qg, k, v, k_past, v_past, gamma_q, gamma_k, cos, sin, scale, eps=1e-6):

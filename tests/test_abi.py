@@ -59,7 +59,9 @@ def test_library_exports_every_declared_entry():
 STRUCTS = {"TfdDecodeArgs": _lib.TfdDecodeArgs, "TfdLayer": _lib.TfdLayer,
            "TfdMoeArgs": _lib.TfdMoeArgs, "TfdGdnArgs": _lib.TfdGdnArgs,
            "TfdMambaArgs": _lib.TfdMambaArgs, "TfdGqaArgs": _lib.TfdGqaArgs,
-           "TfdXcdArgs": _lib.TfdXcdArgs}
+           "TfdXcdArgs": _lib.TfdXcdArgs, "TfdConvStepArgs": _lib.TfdConvStepArgs,
+           "TfdDeltaStepArgs": _lib.TfdDeltaStepArgs, "TfdPartialRopeArgs": _lib.TfdPartialRopeArgs,
+           "TfdSsmStepArgs": _lib.TfdSsmStepArgs, "TfdGatedNormArgs": _lib.TfdGatedNormArgs}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="no C compiler")

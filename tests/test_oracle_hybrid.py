@@ -351,3 +351,47 @@ def test_rms_norm_tf_rounds_once_like_torch_rms_norm():
     r = torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)
     twice = H.bf(H.bf(x * r) * gamma)
     assert (twice != want).float().mean() > 0.05
+
+
+def test_partial_rope_matches_hf_apply_rotary_pos_emb():
+    """The standalone partial RoPE (the twins' partial_rope / partial_rope_kv) is
+    HF's apply_rotary_pos_emb on the first rot dims with the tail passed through."""
+    g = torch.Generator().manual_seed(21)
+    B, HQ, HKV, D, rot = 3, 8, 2, 64, 16
+    past = [4, 0, 31]
+    q = torch.randn(B, HQ, D, generator=g)
+    k = torch.randn(B, HKV, D, generator=g)
+    cos, sin = _rope_rows(past, rot)
+    for b in range(B):
+        q_r, k_r = hf_q.apply_rotary_pos_emb(q[b][None, :, None], k[b][None, :, None],
+                                             cos[b][None, None], sin[b][None, None])
+        torch.testing.assert_close(H.partial_rope(q[b:b + 1], cos[b:b + 1], sin[b:b + 1])[0],
+                                   q_r[0, :, 0], atol=1e-6, rtol=1e-6)
+        torch.testing.assert_close(H.partial_rope(k[b:b + 1], cos[b:b + 1], sin[b:b + 1])[0],
+                                   k_r[0, :, 0], atol=1e-6, rtol=1e-6)
+
+
+def test_moe_c5_dense_equals_the_fp8_form_at_power_of_two_scales():
+    """With every row scale a power of two, the dequantised bf16 weights hold the fp8
+    products exactly, so the dense restatement and the fp8 one give the same bits; a
+    dropped shared MLP or swapped gate/up fails."""
+    g = torch.Generator().manual_seed(8)
+    hs, inter, sh, e, k, B = 64, 32, 48, 12, 4, 3
+    codes = lambda *s: (torch.randn(*s, generator=g) * 0.6).to(torch.float8_e4m3fn).view(torch.uint8)
+    p2 = lambda *s: torch.exp2(torch.randint(-8, -4, s, generator=g).float())
+    g_c, g_s = codes(e, inter, hs), p2(e, inter)
+    u_c, u_s = codes(e, inter, hs), p2(e, inter)
+    d_c, d_s = codes(e, hs, inter), p2(e, hs)
+    si_c, si_s = codes(2 * sh, hs), p2(2 * sh)
+    so_c, so_s = codes(hs, sh), p2(hs)
+    deq = lambda c, s: H.bf(c.view(torch.float8_e4m3fn).float() * s[..., None])
+    x = H.bf(torch.randn(B, hs, generator=g))
+    logits = torch.randn(B, e, generator=g)
+    w, idx = H.route_topk_softmax(logits, k)
+    want = H.moe_c5(x, w, idx, g_c, g_s, u_c, u_s, d_c, d_s, si_c, si_s, so_c, so_s)
+    got = H.moe_c5_dense(x, w, idx, deq(g_c, g_s), deq(u_c, u_s), deq(d_c, d_s),
+                         deq(si_c, si_s), deq(so_c, so_s))
+    assert torch.equal(got, want)
+    swapped = H.moe_c5_dense(x, w, idx, deq(u_c, u_s), deq(g_c, g_s), deq(d_c, d_s),
+                             deq(si_c, si_s), deq(so_c, so_s))
+    assert not torch.equal(swapped, want)

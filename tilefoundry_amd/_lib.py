@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS, EPI_RESID_F32 = 0, 1, 2, 3, 4
@@ -82,6 +82,12 @@ SIGNATURES: dict[str, list] = {
     "tfd_scaled_add_rows": [P, I, P, I, I, F, P, I, I, I, P],
     "tfd_tf_rmsnorm_rows_bf16": [P, I, P, P, I, P, I, I, F, P],
     "tfd_gemm_skinny_bf16_logits_div": [P, P, I, I, I, F, P, I, P, L, P],
+    "tfd_conv_step_rows": [P, P],
+    "tfd_l2norm_f32": [P, P, I, I, F, P],
+    "tfd_delta_step_f32": [P, P],
+    "tfd_partial_rope_f32": [P, P],
+    "tfd_ssm_step_bf16": [P, P],
+    "tfd_gated_rmsnorm_bf16": [P, P],
 }
 RESTYPES = {"tfd_last_error": ctypes.c_char_p}
 UNCHECKED = {"tfd_abi_version", "tfd_decode_persistent_grid"}
@@ -151,6 +157,49 @@ class TfdGqaArgs(ctypes.Structure):
         ("nsplit", c_int), ("split_len", c_int),
         ("out", c_void_p), ("policy", c_int), ("err", c_void_p),
     ]
+
+
+class TfdConvStepArgs(ctypes.Structure):
+    """``TfdConvStepArgs`` of include/tf_hybrid.h, field for field."""
+
+    _fields_ = [("window", c_void_p), ("entry", c_void_p), ("lde", c_int),
+                ("conv_w", c_void_p), ("conv_b", c_void_p), ("out", c_void_p),
+                *[(n, c_int) for n in ("ldo", "rows", "channels", "kernel", "policy")]]
+
+
+class TfdDeltaStepArgs(ctypes.Structure):
+    """``TfdDeltaStepArgs`` of include/tf_hybrid.h, field for field."""
+
+    _fields_ = [*[(n, c_void_p) for n in ("state_in", "state_out", "q", "k", "v", "g", "beta",
+                                           "read")],
+                ("qscale", c_float),
+                *[(n, c_int) for n in ("rows", "heads", "head_k_dim", "head_v_dim")]]
+
+
+class TfdPartialRopeArgs(ctypes.Structure):
+    """``TfdPartialRopeArgs`` of include/tf_hybrid.h, field for field."""
+
+    _fields_ = [("x", c_void_p), ("ldx", c_int), ("out", c_void_p), ("ldo", c_int),
+                ("pos", c_void_p), ("cos_table", c_void_p), ("sin_table", c_void_p),
+                *[(n, c_int) for n in ("rope_rows", "rows", "heads", "head_dim", "rot")]]
+
+
+class TfdSsmStepArgs(ctypes.Structure):
+    """``TfdSsmStepArgs`` of include/tf_hybrid.h, field for field."""
+
+    _fields_ = [("state_in", c_void_p), ("state_out", c_void_p), ("x", c_void_p), ("ldx", c_int),
+                ("b_vec", c_void_p), ("ldb", c_int), ("c_vec", c_void_p), ("ldc", c_int),
+                ("dt_raw", c_void_p), ("lddt", c_int),
+                *[(n, c_void_p) for n in ("a_log", "dt_bias", "d_skip", "y")],
+                *[(n, c_int) for n in ("ldy", "rows", "heads", "head_dim", "state_dim")]]
+
+
+class TfdGatedNormArgs(ctypes.Structure):
+    """``TfdGatedNormArgs`` of include/tf_hybrid.h, field for field."""
+
+    _fields_ = [("y", c_void_p), ("ldy", c_int), ("gate", c_void_p), ("ldg", c_int),
+                ("gamma", c_void_p), ("out", c_void_p),
+                *[(n, c_int) for n in ("ldo", "rows", "n")], ("eps", c_float)]
 
 
 class TfdDecodeArgs(ctypes.Structure):
