@@ -3,6 +3,7 @@
     python -m tilefoundry_amd.hybrid.bench [--config c4|c4b16|c5|all] [--reps 20]
     python -m tilefoundry_amd.hybrid.bench --config c4-step --rows 1|16 [--steps 256]
     python -m tilefoundry_amd.hybrid.bench --config c5-step --rows 8 [--steps 256]
+    python -m tilefoundry_amd.hybrid.bench --config gemm [--reps 20]
 
 Every kernel runs at its workload's shapes on synthetic data (seeded) with the
 launches of one measurement captured in a HIP graph and replayed; HIP events on
@@ -302,7 +303,64 @@ def bench_gemm_fp8(config, rows, reps, gen, *, K, N, name):
     nbytes = N * K + N * 4 + rows * K * 2 + rows * N * 2
     flops = 2 * rows * N * K
     return _line(config, f"gemm_skinny_fp8 {name}", rows, sec, nbytes,
-                 TFLOPs=round(flops / sec / 1e12, 2))
+                 TFLOPs=round(flops / sec / 1e12, 2), mfma_frac=round(flops / sec / 2.5e15, 4))
+
+
+def bench_gemm_bf16(config, rows, reps, gen, *, K, N, name, epi):
+    """The bf16 skinny MFMA GEMM (tfd_gemm_skinny_bf16) at one projection's shape:
+    HBM bytes (weights + activations in and out) and MFMA TFLOP/s (2 M N K flops)
+    against the 2.5 PFLOP/s dense bf16 peak."""
+    copies = max(2, -(-(1 << 30) // (2 * N * K)))
+    ws = []
+    for _ in range(copies):
+        rows_w = (_rn(N, K, gen=gen) * 0.02).to(BF)
+        packed = torch.empty(-(-N // 16) * 16 * K, dtype=BF, device=DEV)
+        lib().tfd_pack_skinny_bf16(ptr(rows_w), K, N, K, ptr(packed), _stream())
+        ws.append(packed)
+        del rows_w
+    x = (_rn(32 * K, gen=gen) * 0.5).to(BF)
+    if epi == _lib.EPI_SWIGLU:
+        out, ldo = torch.empty(32 * (N // 2), dtype=BF, device=DEV), N // 2
+    elif epi == _lib.EPI_LOGITS:
+        out, ldo = torch.empty(rows, N, dtype=torch.float32, device=DEV), N
+    else:
+        out, ldo = torch.empty(rows, N, dtype=BF, device=DEV), N
+    resid = torch.zeros(rows, N, dtype=BF, device=DEV) if epi == _lib.EPI_RESID else None
+    work = torch.zeros(1 << 21, dtype=torch.float32, device=DEV)
+    L = lib()
+    calls = [lambda w=w: L.tfd_gemm_skinny_bf16(ptr(x), ptr(w), rows, K, N, epi, ptr(resid),
+                                                N if resid is not None else 0, ptr(out), ldo,
+                                                ptr(work), work.numel(), _stream())
+             for w in ws]
+    sec = time_graph(calls, reps)
+    out_bytes = rows * N * (4 if epi == _lib.EPI_LOGITS else 2) // (2 if epi == _lib.EPI_SWIGLU
+                                                                     else 1)
+    nbytes = 2 * N * K + rows * K * 2 + out_bytes
+    flops = 2 * rows * N * K
+    return _line(config, f"gemm_skinny_bf16 {name}", rows, sec, nbytes,
+                 TFLOPs=round(flops / sec / 1e12, 2), mfma_frac=round(flops / sec / 2.5e15, 4))
+
+
+def run_gemm(reps: int) -> list[dict]:
+    """Every batched projection on the MFMA path: C3 (batch 32) q/k/v, o, gate/up,
+    down and the head; C4 batch 16's GDN and attention in/out projections, router
+    and head; C5 batch 8's fp8 in_proj and out_proj."""
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    res = []
+    for name, K, N, epi in (("c3 qkv", 2048, 4096, _lib.EPI_STORE),
+                            ("c3 o", 2048, 2048, _lib.EPI_RESID),
+                            ("c3 gate/up", 2048, 12288, _lib.EPI_SWIGLU),
+                            ("c3 down", 6144, 2048, _lib.EPI_RESID),
+                            ("c3 head", 2048, 151936, _lib.EPI_LOGITS)):
+        res.append(bench_gemm_bf16("c3", 32, reps, gen, K=K, N=N, name=name, epi=epi))
+    for name, K, N in (("c4 gdn in", 2048, 12352), ("c4 gdn out", 4096, 2048),
+                       ("c4 attn in", 2048, 9216), ("c4 attn out", 4096, 2048),
+                       ("c4 router", 2048, 256), ("c4 head", 2048, 248320)):
+        res.append(bench_gemm_bf16("c4b16", 16, reps, gen, K=K, N=N, name=name,
+                                   epi=_lib.EPI_LOGITS))
+    res.append(bench_gemm_fp8("c5", 8, reps, gen, K=4096, N=8512, name="in_proj"))
+    res.append(bench_gemm_fp8("c5", 8, reps, gen, K=4096, N=4096, name="out_proj"))
+    return res
 
 
 def run(config: str, reps: int) -> list[dict]:
@@ -404,7 +462,7 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--config", default="all",
-                    choices=("c4", "c4b16", "c5", "all", "c4-step", "c5-step"))
+                    choices=("c4", "c4b16", "c5", "all", "c4-step", "c5-step", "gemm"))
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--rows", type=int, default=1, help="c4-step / c5-step: sequences")
     ap.add_argument("--steps", type=int, default=256, help="c4-step / c5-step: timed steps")
@@ -416,6 +474,9 @@ def main(argv=None) -> int:
         return 0
     if args.config == "c5-step":
         bench_c5_step(args.rows, args.steps)
+        return 0
+    if args.config == "gemm":
+        run_gemm(args.reps)
         return 0
     for c in (("c4", "c4b16", "c5") if args.config == "all" else (args.config,)):
         run(c, args.reps)
