@@ -125,7 +125,7 @@ def build(args, model: str, device: str):
                           prompt_room=max(room, prompt_len + 8), mode=mode)
 
         def run(eng, prompt):
-            r = eng.generate(prompt, args.max_new_tokens)
+            r = eng.generate(prompt, args.max_new_tokens, prefill=args.prefill)
             return r.tokens, r.seconds, r.prefill_seconds
 
         return make, run, cfg.vocab_size, mode
@@ -185,6 +185,9 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--prompt-room", type=int, default=64,
                     help="Qwen3: prompt positions the engine reserves")
     ap.add_argument("--seed", type=int, default=0, help="weights / random prompt seed")
+    ap.add_argument("--prefill", action="store_true",
+                    help="Qwen3: fill the prompt's cache in batched passes (32 positions per "
+                         "pass) instead of walking it one decode step per token")
     args = ap.parse_args(argv)
     if args.max_new_tokens < 1:
         raise SystemExit("--max-new-tokens must be at least 1")

@@ -371,10 +371,29 @@ class Engine:
                                       (8, "step")) if e & bit]
             raise RuntimeError(f"decode kernels flagged an out-of-range {', '.join(names)}")
 
+    def prefill(self, prompt_ids: list[int]):
+        """Load *prompt_ids* and fill the cache of all but its last token in
+        batched passes (``qwen3.prefill``: up to 32 positions per pass through every
+        layer), leaving the engine at the last prompt position: the next decode step
+        consumes the last prompt token and picks the first new one, exactly where
+        walking the prompt step by step would leave it."""
+        pl = len(prompt_ids)
+        self._load_prompt(prompt_ids)
+        if pl < 2:
+            return
+        if getattr(self, "_prefiller", None) is None:
+            from .prefill import Prefill
+            self._prefiller = Prefill(self)
+        self._prefiller.run(list(prompt_ids[:-1]), 0)
+        self.pos.fill_(pl - 1)
+        self.ids.fill_(int(prompt_ids[-1]))
+        self._embed_current()
+
     def generate(self, prompt_ids: list[int], max_new: int,
-                 record_logits: bool = False) -> Generated:
-        """Walk *prompt_ids*, then continue for *max_new* greedy tokens
-        (engine.py:239-271); the timing covers the continuation only."""
+                 record_logits: bool = False, prefill: bool = False) -> Generated:
+        """Walk *prompt_ids* (or, with *prefill*, fill its cache in batched
+        passes), then continue for *max_new* greedy tokens (engine.py:239-271); the
+        timing covers the continuation only."""
         pl = len(prompt_ids)
         if pl < 1:
             raise ValueError("decode needs a prompt of at least one token")
@@ -383,12 +402,15 @@ class Engine:
                              f"{self.nsteps} steps")
         if any(not 0 <= int(t) < self.V for t in prompt_ids):
             raise ValueError(f"prompt ids must lie in [0, {self.V})")
-        self._load_prompt(prompt_ids)
         hist = (torch.empty(max_new, self.V, device=self.device, dtype=torch.float32)
                 if record_logits else None)
         torch.cuda.synchronize(self.device)
         t0 = perf_counter()
-        self.run_steps(pl - 1)
+        if prefill:
+            self.prefill(prompt_ids)
+        else:
+            self._load_prompt(prompt_ids)
+            self.run_steps(pl - 1)
         torch.cuda.synchronize(self.device)
         t1 = perf_counter()
         if hist is None:
