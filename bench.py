@@ -1,6 +1,6 @@
 """Decode throughput of the Qwen3-1.7B-architecture model at batch 1 (workload C2).
 
-    python bench.py [--gpus 1] [--steps 2048] [--warmup 64] [--mode persistent|graph]
+    python bench.py [--gpus 1] [--steps 2048] [--warmup 64] [--mode xcd|persistent|graph]
 
 A step is one decode token: every layer, the head, the greedy pick.  The
 workload is C2: bf16 weights drawn N(0, 0.02) from seed 0
@@ -11,18 +11,19 @@ tokens (positions 31..2078).  `--steps N` times the LAST N tokens of that run
 untimed first), so every timed step works at the context depth the workload
 gives it.  Weights are resident in HBM before the timed region starts.
 
-Modes: "persistent" (default) runs all the steps in one launch of the
-persistent decode kernel; "graph" replays a captured graph of per-phase
+Modes: "xcd" (default) runs all the timed steps in one launch of the
+XCD-partitioned persistent decode kernel; "persistent" in one launch of the
+chip-wide persistent kernel; "graph" replays a captured graph of per-phase
 launches once per token.
 
 Prints one JSON line: the metric; the whole-step HBM roofline fraction from
 algorithmic bytes (weights once + the KV each step touches); the dominant
-kernel's roofline -- in persistent mode the persistent kernel itself: the
-algorithmic bytes of its launches over their mean duration, HIP events on the
-launch stream around every launch this run makes (the ones rocprofv3 sees for
-the same command); in graph mode the gate/up GEMV -- with the HBM traffic that
-rocprofv3's counters measured for it when a profile is committed; and the CPU
-oracle timed on the host.
+kernel's roofline -- in the persistent modes the decode kernel itself: the
+algorithmic bytes of the timed launch over its duration, HIP events on the
+launch stream around it (rocprofv3's trace of the same command lists that
+launch as its last dispatch of the kernel); in graph mode the gate/up GEMV --
+with the HBM traffic that rocprofv3's counters measured for it when a profile
+is committed; and the CPU oracle timed on the host.
 """
 from __future__ import annotations
 
@@ -128,19 +129,28 @@ class LaunchClock:
         return k, sum(nbytes) / k, sum(secs) / k
 
 
-def traffic_ratio(kernel: str):
-    """(HBM bytes moved per algorithmic byte for *kernel*, a description of the
-    run they were counted on) from the committed rocprofv3 counter summary
-    (profiles/hbm_traffic.json: FETCH_SIZE and WRITE_SIZE of one profiled
-    launch, scaled by what the same counters read for a plain copy of known
-    size), or (None, None) when no profile is committed."""
+def traffic_for(kernel: str, positions, algorithmic_bytes: float):
+    """(HBM bytes of the timed launch, where the figure comes from) from the
+    committed rocprofv3 counter summary (profiles/hbm_traffic.json: FETCH_SIZE
+    and WRITE_SIZE of one profiled launch, each scaled by what the same counter
+    reads for a plain copy of known size), or (None, None) when none is
+    committed for *kernel*.  When the committed launch covered the same
+    positions as this run's timed launch (the same command), its measured
+    bytes are the figure; otherwise its ratio of HBM bytes to algorithmic bytes
+    is applied to this launch's algorithmic bytes, and the source says so."""
     path = ROOT / "profiles" / "hbm_traffic.json"
     if not path.exists():
         return None, None
     try:
         entry = json.loads(path.read_text()).get(kernel)
-        ratio = float(entry["hbm_bytes"]) / float(entry["algorithmic_bytes"])
-        return ratio, "counted on " + entry.get("launch", "a committed counter run")
+        hbm, alg = float(entry["hbm_bytes"]), float(entry["algorithmic_bytes"])
+        counted = entry.get("launch", "a committed counter run")
+        if list(entry.get("timed_positions", [])) == list(positions):
+            return round(hbm), f"rocprofv3 FETCH_SIZE + WRITE_SIZE of this launch ({counted})"
+        ratio = hbm / alg
+        return (round(ratio * algorithmic_bytes),
+                f"committed counter ratio {ratio:.4f} (HBM bytes per algorithmic byte, counted "
+                f"on {counted}) times this launch's algorithmic bytes")
     except (ValueError, KeyError, TypeError, ZeroDivisionError, AttributeError):
         return None, None
 
@@ -371,15 +381,13 @@ def main(argv=None) -> int:
     if clock is not None:
         launches, bytes_per_launch, launch_s = clock.summary()
         kernel = "k_decode_persistent<4,12,128,2>" if args.mode == "persistent" else "k_decode_xcd"
-        ratio, counted_on = traffic_ratio(kernel)
+        traffic, traffic_source = traffic_for(
+            kernel, [first_pos, first_pos + args.steps - 1], bytes_per_launch)
         bw = bytes_per_launch / launch_s
         roofline = {"bound": "hbm", "kernel": f"{kernel} (whole decode steps per launch)",
                     "achieved": round(bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                     "frac": round(bw / HBM_PEAK, 4),
-                    "traffic": None if ratio is None else round(ratio * bytes_per_launch),
-                    "traffic_source": None if ratio is None else
-                    f"committed counter ratio {ratio:.4f} (HBM bytes per algorithmic byte, "
-                    f"{counted_on}) times this launch's algorithmic bytes",
+                    "traffic": traffic, "traffic_source": traffic_source,
                     "bytes_per_launch": int(bytes_per_launch),
                     "avg_launch_ms": round(launch_s * 1e3, 3), "launches": launches}
     else:
