@@ -346,6 +346,59 @@ typedef struct {
 } TfdGatedNormArgs;
 int tfd_gated_rmsnorm_bf16(const TfdGatedNormArgs* args, void* stream);
 
+/* Small-batch (1..4 sequences) C4 decode: a gated-DeltaNet layer in six launches
+ * (the reference's tilelang runtime runs the mixer as three kernels,
+ * examples/qwen3_5_35b_a3b-tilelang/kernels/gdn.py:1-60, and the MoE as router
+ * logits, select and two expert kernels, kernels/moe.py:203-302, 368, 527).
+ *
+ * tfd_rowgemv_bf16: out[r][n] = bf16(sum_k W[n][k] x[r][k]) (TFD_EPI_LOGITS, f32
+ * out) or out[r][n] += that (TFD_EPI_RESID_F32, in place) for r < rows <= 4, W
+ * bf16 row-major [N][K], K 2048 or 4096, a wave per few rows (no MFMA padding).
+ * The input rows x[r][0:K] are made by a prologue:
+ *   TFD_ROWX_NORM_F32   f32 rows [rows][ldx] through RMSNorm with gamma [K], one
+ *                       rounding (tfd_rmsnorm_f32_rows' arithmetic, bit for bit)
+ *   TFD_ROWX_GATED_F32  Qwen3.5's gated output norm of the f32 read-out [rows][ldx]
+ *                       per 128-value head with gate z f32 [rows][ldg] and gamma
+ *                       [128]: bf16(x rsqrt(mean_head x^2 + eps) gamma silu(z))
+ *                       (model.py:213-232; the sums of tfd_gdn_step)
+ *   TFD_ROWX_OPERAND    bf16 rows in the skinny GEMMs' operand order
+ *   TFD_ROWX_ROWS       bf16 rows [rows][ldx]
+ * x_rows (optional): the prologue's bf16 rows [rows][ldxr] are also written there. */
+#define TFD_ROWX_NORM_F32 0
+#define TFD_ROWX_GATED_F32 1
+#define TFD_ROWX_OPERAND 2
+#define TFD_ROWX_ROWS 3
+typedef struct {
+  const void* x;
+  int ldx, x_kind;
+  const void* gamma;
+  const float* gate;
+  int ldg, head_dim;
+  float eps;
+  const void* w;
+  int K, N;
+  float* out;
+  int ldo, epilogue;
+  void* x_rows;
+  int ldxr, rows;
+} TfdRowGemvArgs;
+int tfd_rowgemv_bf16(const TfdRowGemvArgs* args, void* stream);
+
+/* tfd_gdn_step over value columns: blocks (value head, 32-column group, row),
+ * 128 at batch 1.  The same inputs, state and window updates as tfd_gdn_step
+ * (args->out and args->gamma are not used); the read-out before the gated
+ * norm goes to read f32 [rows][ldr] (hv*128 values, bit-identical to the values
+ * tfd_gdn_step normalises).  The gated norm is TFD_ROWX_GATED_F32 of the
+ * out-projection. */
+int tfd_gdn_step_cols(const TfdGdnArgs* args, float* read, int ldr, void* stream);
+
+/* tfd_moe_experts for rows <= 4 in two launches: gate/up (each block routes its
+ * row itself when route is TFD_MOE_ROUTE_SOFTMAX_TOPK, and writes weights / idx
+ * as tfd_moe_experts does), then down + mix (+= into out with accumulate).  bf16
+ * weights, TFD_POLICY_F32, hidden_size 2048, inter = shared_inter = 512, k <= 8;
+ * groups and partial are not used.  Results equal tfd_moe_experts' bit for bit. */
+int tfd_moe_experts_small(const TfdMoeArgs* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -61,7 +61,8 @@ STRUCTS = {"TfdDecodeArgs": _lib.TfdDecodeArgs, "TfdLayer": _lib.TfdLayer,
            "TfdMambaArgs": _lib.TfdMambaArgs, "TfdGqaArgs": _lib.TfdGqaArgs,
            "TfdXcdArgs": _lib.TfdXcdArgs, "TfdConvStepArgs": _lib.TfdConvStepArgs,
            "TfdDeltaStepArgs": _lib.TfdDeltaStepArgs, "TfdPartialRopeArgs": _lib.TfdPartialRopeArgs,
-           "TfdSsmStepArgs": _lib.TfdSsmStepArgs, "TfdGatedNormArgs": _lib.TfdGatedNormArgs}
+           "TfdSsmStepArgs": _lib.TfdSsmStepArgs, "TfdGatedNormArgs": _lib.TfdGatedNormArgs,
+           "TfdRowGemvArgs": _lib.TfdRowGemvArgs}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="no C compiler")

@@ -16,11 +16,16 @@ from tilefoundry_amd.hybrid.qwen3_5 import Qwen35Config, Qwen35Engine, synthetic
 pytestmark = pytest.mark.gpu
 
 
+@pytest.mark.parametrize("small", [True, False], ids=["small", "mfma"])
 @pytest.mark.parametrize("rows", [1, 3])
-def test_qwen35_engine_matches_oracle_steps(gpu_device, rows):
+def test_qwen35_engine_matches_oracle_steps(gpu_device, rows, small):
+    """small: the small-batch kernels (row GEMVs, the delta rule over value
+    columns, the two-launch experts); mfma: the batched path at the same rows."""
     cfg = Qwen35Config(layers=4, experts=16, vocab=4096)
     w = synthetic_weights(cfg, seed=3, device=gpu_device)
-    eng = Qwen35Engine(cfg, w, rows=rows, device=gpu_device, max_steps=64, split_len=16)
+    eng = Qwen35Engine(cfg, w, rows=rows, device=gpu_device, max_steps=64, split_len=16,
+                       small=small)
+    assert eng.small == small
     g = torch.Generator().manual_seed(rows)
     prompts = [torch.randint(0, cfg.vocab, (3 + b,), generator=g).tolist() for b in range(rows)]
     new = 5

@@ -209,7 +209,7 @@ def test_c4_decoder_matches_the_engine(c4):
     g = torch.Generator().manual_seed(7)
     prompt = torch.randint(0, C4.vocab, (4,), generator=g).tolist()
     new = 3
-    eng = Qwen35Engine(C4, w, rows=1, device=DEV, max_steps=32, split_len=16)
+    eng = Qwen35Engine(C4, w, rows=1, device=DEV, max_steps=32, split_len=16, small=False)
     tokens, _, logits = eng.generate([prompt], new, record_logits=True)
     feed = prompt + tokens[0][:-1]
     ids = torch.tensor(feed, dtype=torch.int64)

@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS, EPI_RESID_F32 = 0, 1, 2, 3, 4
@@ -32,6 +32,8 @@ def moe_group_words(experts: int, rows: int) -> int:
     return 1 + 2 * experts + experts * rows
 
 POLICY_F32, POLICY_BF16 = 0, 1
+ROWX_NORM_F32, ROWX_GATED_F32, ROWX_OPERAND, ROWX_ROWS = 0, 1, 2, 3
+SMALL_ROWS = 4              # rows of the small-batch entries (tfd_rowgemv_bf16 and the rest)
 MOE_ROUTE_GIVEN, MOE_ROUTE_SOFTMAX_TOPK, MOE_ROUTE_TOPK_SOFTMAX = 0, 1, 2
 
 P = c_void_p
@@ -88,6 +90,9 @@ SIGNATURES: dict[str, list] = {
     "tfd_partial_rope_f32": [P, P],
     "tfd_ssm_step_bf16": [P, P],
     "tfd_gated_rmsnorm_bf16": [P, P],
+    "tfd_rowgemv_bf16": [P, P],
+    "tfd_gdn_step_cols": [P, P, I, P],
+    "tfd_moe_experts_small": [P, P],
 }
 RESTYPES = {"tfd_last_error": ctypes.c_char_p}
 UNCHECKED = {"tfd_abi_version", "tfd_decode_persistent_grid"}
@@ -200,6 +205,15 @@ class TfdGatedNormArgs(ctypes.Structure):
     _fields_ = [("y", c_void_p), ("ldy", c_int), ("gate", c_void_p), ("ldg", c_int),
                 ("gamma", c_void_p), ("out", c_void_p),
                 *[(n, c_int) for n in ("ldo", "rows", "n")], ("eps", c_float)]
+
+
+class TfdRowGemvArgs(ctypes.Structure):
+    """``TfdRowGemvArgs`` of include/tf_hybrid.h, field for field."""
+
+    _fields_ = [("x", c_void_p), ("ldx", c_int), ("x_kind", c_int), ("gamma", c_void_p),
+                ("gate", c_void_p), ("ldg", c_int), ("head_dim", c_int), ("eps", c_float),
+                ("w", c_void_p), ("K", c_int), ("N", c_int), ("out", c_void_p), ("ldo", c_int),
+                ("epilogue", c_int), ("x_rows", c_void_p), ("ldxr", c_int), ("rows", c_int)]
 
 
 class TfdDecodeArgs(ctypes.Structure):

@@ -11,19 +11,15 @@
 // tilelang/kernels/torch_ref.py:22-40; C5 at the Granite HIR's bf16 rounding,
 // examples/granite_4_0_h_small-cuda/model.py).  They are small, one-token
 // kernels: a block per row (and head), no work buffers.
-#include "decode_common.h"
+#include "hybrid_common.h"
 #include "host_common.h"
 #include "tf_hybrid.h"
 
 using namespace tfd;
 using namespace tfd_host;
+using namespace tfd_hybrid;
 
 namespace {
-
-__device__ __forceinline__ float softplus_f(float x) {
-  // torch.nn.functional.softplus (beta 1, threshold 20)
-  return x > 20.f ? x : log1pf(expf(x));
-}
 
 // ---------------------------------------------------------------------------
 // conv_step (C4: tests/models/qwen3_5_35b_a3b/model.py:124-136, torch_ref f32;

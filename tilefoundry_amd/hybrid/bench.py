@@ -391,7 +391,7 @@ def run(config: str, reps: int) -> list[dict]:
     return res
 
 
-def bench_c4_step(rows: int, steps: int, prompt: int = 32) -> dict:
+def bench_c4_step(rows: int, steps: int, prompt: int = 32, small: bool | None = None) -> dict:
     """Whole C4 decode steps (Qwen3.5-35B-A3B shape, 40 layers, 248,320-token
     vocabulary, synthetic weights): tok/s over `steps` greedy steps after a
     `prompt`-token random prompt per sequence (walked untimed), and the step's
@@ -402,7 +402,7 @@ def bench_c4_step(rows: int, steps: int, prompt: int = 32) -> dict:
     cfg = Qwen35Config()
     t0 = time.perf_counter()
     w = synthetic_weights(cfg, seed=0, device=DEV)
-    eng = Qwen35Engine(cfg, w, rows=rows, device=DEV, max_steps=prompt + steps + 16)
+    eng = Qwen35Engine(cfg, w, rows=rows, device=DEV, max_steps=prompt + steps + 16, small=small)
     print(f"[bench] c4 weights + engine + capture {time.perf_counter() - t0:.1f}s", flush=True)
     g = torch.Generator().manual_seed(0)
     prompts = [torch.randint(0, cfg.vocab, (prompt,), generator=g).tolist() for _ in range(rows)]
@@ -412,7 +412,8 @@ def bench_c4_step(rows: int, steps: int, prompt: int = 32) -> dict:
     positions = range(prompt - 1, prompt - 1 + steps)
     sbytes = sum(eng.state_bytes_per_step([p] * rows) for p in positions) / steps
     step_s = seconds / steps
-    out = {"config": f"c4 step b{rows}", "tok_s": round(rows * steps / seconds, 1),
+    out = {"config": f"c4 step b{rows}", "path": "small" if eng.small else "mfma",
+           "tok_s": round(rows * steps / seconds, 1),
            "ms_per_step": round(step_s * 1e3, 4), "steps": steps,
            "bytes_per_step": int(wbytes + sbytes), "experts_touched_sample": touched,
            "GB/s": round((wbytes + sbytes) / step_s / 1e9, 1),
@@ -466,11 +467,15 @@ def main(argv=None) -> int:
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--rows", type=int, default=1, help="c4-step / c5-step: sequences")
     ap.add_argument("--steps", type=int, default=256, help="c4-step / c5-step: timed steps")
+    ap.add_argument("--path", choices=("auto", "small", "mfma"), default="auto",
+                    help="c4-step: the small-batch kernels (rows <= 4, the default there) or "
+                         "the batched MFMA path")
     args = ap.parse_args(argv)
     if not torch.cuda.is_available():
         raise SystemExit("hybrid kernel bench: no GPU visible")
     if args.config == "c4-step":
-        bench_c4_step(args.rows, args.steps)
+        bench_c4_step(args.rows, args.steps,
+                      small=None if args.path == "auto" else args.path == "small")
         return 0
     if args.config == "c5-step":
         bench_c5_step(args.rows, args.steps)

@@ -183,11 +183,18 @@ class Qwen35Engine:
 
     def __init__(self, cfg: Qwen35Config, weights: dict[str, torch.Tensor], *, rows: int,
                  device: str = "cuda:0", max_steps: int = 2112, page_seed: int = 0,
-                 split_len: int = 64, graph: bool = True):
+                 split_len: int = 64, graph: bool = True, small: bool | None = None):
         if not 1 <= rows <= 32:
             raise ValueError("rows: 1..32 sequences")
         self.cfg, self.B, self.device = cfg, rows, device
         self._lib = lib()
+        # the small-batch path (rows <= 4): row GEMVs on row-major weights with
+        # the norms as prologues, the delta rule over value columns, the
+        # experts in two launches (tfd_rowgemv_bf16, tfd_gdn_step_cols,
+        # tfd_moe_experts_small); otherwise MFMA GEMMs over packed weights
+        self.small = rows <= _lib.SMALL_ROWS if small is None else bool(small)
+        if self.small and rows > _lib.SMALL_ROWS:
+            raise ValueError(f"small: rows <= {_lib.SMALL_ROWS}")
         self.nsteps = max_steps
         self.split_len = split_len
         self._pack(weights)
@@ -215,13 +222,14 @@ class Qwen35Engine:
         for i in range(cfg.layers):
             p = f"layer{i}."
             d = {k[len(p):]: v for k, v in w.items() if k.startswith(p)}
-            d["w_in"] = self._packed(d["w_in"])
-            d["w_out"] = self._packed(d["w_out"])
-            d["w_router"] = self._packed(d["w_router"])
+            if not self.small:
+                d["w_in"] = self._packed(d["w_in"])
+                d["w_out"] = self._packed(d["w_out"])
+                d["w_router"] = self._packed(d["w_router"])
             self.layers.append(d)
         self.embed = w["embed"]
         self.gamma_final = w["gamma_final"]
-        self.head = self._packed(w["head"])
+        self.head = w["head"] if self.small else self._packed(w["head"])
         torch.cuda.synchronize(self.device)
 
     def _buffers(self, page_seed):
@@ -238,6 +246,7 @@ class Qwen35Engine:
         self.nproj = max(cfg.gdn_in, cfg.attn_in)
         self.proj = z(B, self.nproj)
         self.mix = z(32 * max(cfg.value_dim, cfg.heads * cfg.head_dim), dtype=BF)
+        self.read = z(B, cfg.value_dim)                     # small path: GDN read-out
         self.rlog = z(B, cfg.experts)
         self.rw = z(B, k)
         self.ridx = z(B, k, dtype=I32)
@@ -296,7 +305,11 @@ class Qwen35Engine:
                                        ptr(self.work), self.work.numel(), s)
 
     def _gdn(self, i, w, s, cur):
-        cfg, L = self.cfg, self._lib
+        a = self._gdn_args(i, w, cur)          # kept alive across the call
+        self._lib.tfd_gdn_step(ctypes_addr(a), s)
+
+    def _gdn_args(self, i, w, cur):
+        cfg = self.cfg
         a = _lib.TfdGdnArgs()
         cin, cout = self.conv[i][cur], self.conv[i][1 - cur]
         a.proj, a.proj_ld, a.conv_in, a.conv_out = ptr(self.proj), self.nproj, ptr(cin), ptr(cout)
@@ -307,7 +320,7 @@ class Qwen35Engine:
         a.head_k_dim, a.head_v_dim, a.conv_kernel = cfg.lin_key_dim, cfg.lin_value_dim, \
             cfg.conv_kernel
         a.l2_eps, a.rms_eps = 1e-6, cfg.eps
-        L.tfd_gdn_step(ctypes_addr(a), s)
+        return a
 
     def _attn(self, i, w, s):
         cfg = self.cfg
@@ -327,6 +340,10 @@ class Qwen35Engine:
         self._lib.tfd_gqa_decode(ctypes_addr(a), s)
 
     def _moe(self, w, s):
+        a = self._moe_args(w)                  # kept alive across the call
+        self._lib.tfd_moe_experts(ctypes_addr(a), s)
+
+    def _moe_args(self, w):
         cfg = self.cfg
         a = _lib.TfdMoeArgs()
         a.x, a.weights, a.idx = ptr(self.xm), ptr(self.rw), ptr(self.ridx)
@@ -341,9 +358,46 @@ class Qwen35Engine:
         a.fp8, a.policy, a.err = 0, _lib.POLICY_F32, ptr(self.err)
         a.accumulate = 1                               # residual add into the stream
         a.logits, a.ldl, a.route = ptr(self.rlog), cfg.experts, _lib.MOE_ROUTE_SOFTMAX_TOPK
-        self._lib.tfd_moe_experts(ctypes_addr(a), s)
+        return a
+
+    def _rowgemv(self, x, ldx, kind, w, K, N, out, ldo, s, *, gamma=None, gate=None, ldg=0,
+                 resid=False, x_rows=None):
+        a = _lib.TfdRowGemvArgs()
+        a.x, a.ldx, a.x_kind = x, ldx, kind
+        a.gamma = None if gamma is None else ptr(gamma)
+        a.gate, a.ldg, a.head_dim, a.eps = gate, ldg, self.cfg.lin_value_dim, self.cfg.eps
+        a.w, a.K, a.N = ptr(w), K, N
+        a.out, a.ldo = ptr(out), ldo
+        a.epilogue = _lib.EPI_RESID_F32 if resid else _lib.EPI_LOGITS
+        a.x_rows, a.ldxr = (None, 0) if x_rows is None else (ptr(x_rows), x_rows.shape[-1])
+        a.rows = self.B
+        self._lib.tfd_rowgemv_bf16(ctypes_addr(a), s)
+
+    def _layer_small(self, i, s, cur):
+        cfg, w, H = self.cfg, self.layers[i], self.cfg.hidden
+        full = cfg.is_full(i)
+        self._rowgemv(ptr(self.hidden), H, _lib.ROWX_NORM_F32, w["w_in"], H,
+                      cfg.attn_in if full else cfg.gdn_in, self.proj, self.nproj, s,
+                      gamma=w["gamma_in"])
+        if full:
+            self._attn(i, w, s)
+            self._rowgemv(ptr(self.mix), 0, _lib.ROWX_OPERAND, w["w_out"],
+                          cfg.heads * cfg.head_dim, H, self.hidden, H, s, resid=True)
+        else:
+            a = self._gdn_args(i, w, cur)
+            self._lib.tfd_gdn_step_cols(ctypes_addr(a), ptr(self.read), cfg.value_dim, s)
+            self._rowgemv(ptr(self.read), cfg.value_dim, _lib.ROWX_GATED_F32, w["w_out"],
+                          cfg.value_dim, H, self.hidden, H, s, gamma=w["gamma_gdn"],
+                          gate=ptr(self.proj) + 4 * cfg.conv_dim, ldg=self.nproj, resid=True)
+        self._rowgemv(ptr(self.hidden), H, _lib.ROWX_NORM_F32, w["w_router"], H, cfg.experts,
+                      self.rlog, cfg.experts, s, gamma=w["gamma_post"], x_rows=self.xm)
+        m = self._moe_args(w)                          # routes in its first launch
+        self._lib.tfd_moe_experts_small(ctypes_addr(m), s)
 
     def _layer(self, i, s, cur):
+        if self.small:
+            self._layer_small(i, s, cur)
+            return
         cfg, L, w, B, H = self.cfg, self._lib, self.layers[i], self.B, self.cfg.hidden
         L.tfd_rmsnorm_f32_rows(ptr(self.hidden), H, ptr(w["gamma_in"]), None, 0, ptr(self.xn),
                                B, H, cfg.eps, s)
@@ -369,9 +423,13 @@ class Qwen35Engine:
         L.tfd_bf16_to_f32_rows(ptr(self.emb), H, ptr(self.hidden), H, B, H, s)
         for i in range(cfg.layers):
             self._layer(i, s, cur)
-        L.tfd_rmsnorm_f32_rows(ptr(self.hidden), H, ptr(self.gamma_final), None, 0,
-                               ptr(self.xn), B, H, cfg.eps, s)
-        self._gemm(self.xn, self.head, H, V, self.logits, V, s)
+        if self.small:
+            self._rowgemv(ptr(self.hidden), H, _lib.ROWX_NORM_F32, self.head, H, V, self.logits,
+                          V, s, gamma=self.gamma_final)
+        else:
+            L.tfd_rmsnorm_f32_rows(ptr(self.hidden), H, ptr(self.gamma_final), None, 0,
+                                   ptr(self.xn), B, H, cfg.eps, s)
+            self._gemm(self.xn, self.head, H, V, self.logits, V, s)
         L.tfd_argmax_rows(ptr(self.logits), V, B, V, ptr(self.pick), ptr(self.argmax_work), s)
         L.tfd_finalize_rows(ptr(self.pick), B, ptr(self.inp), self.nsteps, ptr(self.plen),
                             ptr(self.ids), ptr(self.pos), ptr(self.sam), self.nsteps,
