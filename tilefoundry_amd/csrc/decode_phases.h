@@ -1182,10 +1182,10 @@ __device__ __forceinline__ void attn_merge_ll(int split, int h, int P, int max_p
     u32x4 c;
     uint32_t spins = 0;
     for (;;) {
-      a = __builtin_amdgcn_raw_buffer_load_b64(rsrc(ll.psum), ws * 8u, 0, kPol);
-      b = __builtin_amdgcn_raw_buffer_load_b64(rsrc(ll.smax), ws * 8u, 0, kPol);
-      c = __builtin_amdgcn_raw_buffer_load_b128(rsrc(ll.pout), wo * 8u, 0, kPol);
-      v = __builtin_amdgcn_raw_buffer_load_b64(rsrc(ll.qkv), wv * 8u, 0, kPol);
+      a = __builtin_amdgcn_raw_buffer_load_b64(rsrc(ll.psum), ws * 8u, 0, ld_bits(kPol));
+      b = __builtin_amdgcn_raw_buffer_load_b64(rsrc(ll.smax), ws * 8u, 0, ld_bits(kPol));
+      c = __builtin_amdgcn_raw_buffer_load_b128(rsrc(ll.pout), wo * 8u, 0, ld_bits(kPol));
+      v = __builtin_amdgcn_raw_buffer_load_b64(rsrc(ll.qkv), wv * 8u, 0, ld_bits(kPol));
       const bool ok = (!has_s || a.y == ll.tag) && (!has_m || b.y == ll.tag) &&
                       (!has_o || (c.y == ll.tag && c.w == ll.tag)) && (!has_v || v.y == ll.tag);
       if (ok || ll_give_up(spins, err)) break;
