@@ -304,13 +304,10 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
     for (int l = 0; l < a.n_layers; ++l) {
       const TfdLayer w = a.layers[l];
       const uint32_t tag = tag0 + (uint32_t)l + 1u;
-      // ---- qkv (the hidden state is in hid_s)
-      stamp(tl);
-      gemv_finish_ll<kCH, kRqkv, kNorm, kStore, kXcdLocal>(vb_qkv, hid_s, gq_in, nullptr,
-                                                           a.x_qkv, tag, kH, qkv_n, eps, wq);
       stamp(tl);
       // the o slab, this block's first K / V tiles and the q/k norm operands
-      // stream while the QKV projection arrives
+      // depend on no other block: requested before the qkv arithmetic, they
+      // land while it runs and while the QKV projection arrives
       slab_issue<1>((const bf16*)w.w_o, kQD, 64 * r, kXO * x, wo);
       KTile<kD> kt;
       VTile<kD> vt;
@@ -322,6 +319,10 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
       const QKPre pre = qk_prefetch<kD, kG>(P, P, (const bf16*)w.gamma_q, (const bf16*)w.gamma_k,
                                             (const bf16*)a.cos_table, (const bf16*)a.sin_table,
                                             a.rope_rows, a.page_table, a.max_pages);
+      // ---- qkv (the hidden state is in hid_s)
+      gemv_finish_ll<kCH, kRqkv, kNorm, kStore, kXcdLocal>(vb_qkv, hid_s, gq_in, nullptr,
+                                                           a.x_qkv, tag, kH, qkv_n, eps, wq);
+      stamp(tl);
       const AttnLL ll{a.x_qkv, smax_x, psum_x, pout_x, a.x_attn, tag};
       if (r >= parts)
         rows_issue<kCH, kRgu, kEarly>(vb_gu, (const bf16*)w.w_gu, kH, 0, we);
