@@ -500,18 +500,26 @@ __device__ __forceinline__ u32x4 kv_ld16(const void* base, uint32_t byte_off) {
                                                kCoh ? kCoherent : TFD_KV_STREAM_POLICY);
 }
 
-// (the loads only: the caller knows the tile holds a position below P)
-template <int D, bool kCoh, class Grp = BlockGrp>
-__device__ __forceinline__ void k_tile_load_at(int j0, int h, const int* page_table,
-                                               int max_pages, const bf16* kpool, int num_pages,
-                                               int kv_heads, KTile<D>& kt) {
+// The pages of a K tile's passes: they depend on the positions only, so a
+// kernel that reads the same positions in every layer can look them up once.
+template <int D, class Grp = BlockGrp>
+__device__ __forceinline__ void k_tile_pages(int j0, const int* page_table, int max_pages,
+                                             KTile<D>& kt) {
   using A = AttnShape<D>;
   static_assert(kPage % A::kKPpw == 0, "a wave's positions of a pass stay in one page");
-  const int lane = Grp::tid() & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane((int)Grp::tid() / kWave);
 #pragma unroll
   for (int p = 0; p < A::kKPasses; ++p)
     kt.pg[p] = wave_page(page_table, max_pages, j0 + (p * kWavesPerBlock + wave) * A::kKPpw);
+}
+
+// The K tile's loads from the pages already in kt.pg.
+template <int D, bool kCoh, class Grp = BlockGrp>
+__device__ __forceinline__ void k_tile_load_pages(int j0, int h, const bf16* kpool, int num_pages,
+                                                  int kv_heads, KTile<D>& kt) {
+  using A = AttnShape<D>;
+  const int lane = Grp::tid() & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane((int)Grp::tid() / kWave);
 #pragma unroll
   for (int p = 0; p < A::kKPasses; ++p) {
     const bool bad = kt.pg[p] < 0 || kt.pg[p] >= num_pages;
@@ -521,6 +529,15 @@ __device__ __forceinline__ void k_tile_load_at(int j0, int h, const int* page_ta
     for (int i = 0; i < A::kKChunks; ++i)
       kt.t[p][i] = kv_ld16<kCoh>(kpool, (uint32_t)(row + 64 * i) * 2u);
   }
+}
+
+// pages and loads (the caller knows the tile holds a position below P)
+template <int D, bool kCoh, class Grp = BlockGrp>
+__device__ __forceinline__ void k_tile_load_at(int j0, int h, const int* page_table,
+                                               int max_pages, const bf16* kpool, int num_pages,
+                                               int kv_heads, KTile<D>& kt) {
+  k_tile_pages<D, Grp>(j0, page_table, max_pages, kt);
+  k_tile_load_pages<D, kCoh, Grp>(j0, h, kpool, num_pages, kv_heads, kt);
 }
 
 template <int D, bool kCoh, class Grp = BlockGrp>
@@ -538,17 +555,22 @@ __device__ __forceinline__ void k_tile_issue_at(int j0, int h, int P, const int*
     k_tile_load_at<D, kCoh, Grp>(j0, h, page_table, max_pages, kpool, num_pages, kv_heads, kt);
 }
 
-template <int D, bool kCoh, class Grp = BlockGrp>
-__device__ __forceinline__ void v_tile_load_at(int j0, int h, const int* page_table,
-                                               int max_pages, const bf16* vpool, int num_pages,
-                                               int kv_heads, VTile<D>& vt) {
+template <int D, class Grp = BlockGrp>
+__device__ __forceinline__ void v_tile_pages(int j0, const int* page_table, int max_pages,
+                                             VTile<D>& vt) {
   using A = AttnShape<D>;
   static_assert(kPage % (kWave / A::kLpp) == 0, "a wave's pass stays in one page");
-  const int ch = (int)Grp::tid() % A::kLpp;
   const int wave = __builtin_amdgcn_readfirstlane((int)Grp::tid() / kWave);
 #pragma unroll
   for (int p = 0; p < A::kVPasses; ++p)
     vt.pg[p] = wave_page(page_table, max_pages, j0 + p * A::kGroups + wave * (kWave / A::kLpp));
+}
+
+template <int D, bool kCoh, class Grp = BlockGrp>
+__device__ __forceinline__ void v_tile_load_pages(int j0, int h, const bf16* vpool, int num_pages,
+                                                  int kv_heads, VTile<D>& vt) {
+  using A = AttnShape<D>;
+  const int ch = (int)Grp::tid() % A::kLpp;
 #pragma unroll
   for (int p = 0; p < A::kVPasses; ++p) {
     const int j = v_pos<D, Grp>(j0, p);
@@ -556,6 +578,14 @@ __device__ __forceinline__ void v_tile_load_at(int j0, int h, const int* page_ta
     vt.t[p] = kv_ld16<kCoh>(vpool, (uint32_t)(page_row(bad ? 0 : vt.pg[p], j, kv_heads, h, D) +
                                          ch * 8) * 2u);
   }
+}
+
+template <int D, bool kCoh, class Grp = BlockGrp>
+__device__ __forceinline__ void v_tile_load_at(int j0, int h, const int* page_table,
+                                               int max_pages, const bf16* vpool, int num_pages,
+                                               int kv_heads, VTile<D>& vt) {
+  v_tile_pages<D, Grp>(j0, page_table, max_pages, vt);
+  v_tile_load_pages<D, kCoh, Grp>(j0, h, vpool, num_pages, kv_heads, vt);
 }
 
 template <int D, bool kCoh, class Grp = BlockGrp>
@@ -659,9 +689,27 @@ __device__ __forceinline__ QKPre qk_prefetch(int rp, int P, const bf16* __restri
   const int li = lane < kHalf ? lane : 0;
   const int64_t r = (int64_t)((rp >= 0 && rp < rope_rows) ? rp : 0) * D;
   const int pg = (P >= 0 && P < max_pages * kPage) ? P / kPage : 0;
-  const bf16* gam = wave < G ? gq : gk;
+  // through a global address-space pointer: the select below would otherwise
+  // make these FLAT loads, which also count against the LDS counter, so the
+  // next LDS read would wait for every vector load issued before them
+  typedef const __attribute__((address_space(1))) bf16 g_bf16;
+  const g_bf16* gam = (const g_bf16*)(wave < G ? gq : gk);
   return QKPre{gam[li],           gam[li + kHalf],           cos_t[r + li], sin_t[r + li],
                cos_t[r + li + kHalf], sin_t[r + li + kHalf], page_table[pg]};
+}
+
+// The layer-dependent part of QKPre (the q/k norm scales), for a kernel that
+// keeps the position-dependent part across layers.
+template <int D, int G, class Grp = BlockGrp>
+__device__ __forceinline__ void qk_gammas(const bf16* __restrict__ gq, const bf16* __restrict__ gk,
+                                          QKPre& pre) {
+  constexpr int kHalf = D / 2;
+  const int lane = Grp::tid() & (kWave - 1), wave = Grp::tid() / kWave;
+  const int li = lane < kHalf ? lane : 0;
+  typedef const __attribute__((address_space(1))) bf16 g_bf16;
+  const g_bf16* gam = (const g_bf16*)(wave < G ? gq : gk);
+  pre.g0 = gam[li];
+  pre.g1 = gam[li + kHalf];
 }
 
 // ---------------------------------------------------------------------------

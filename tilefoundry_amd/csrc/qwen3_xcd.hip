@@ -300,25 +300,40 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
     const int Pc = (P >= 0 && P < a.max_pages * kPage) ? P : 0;
     const int nact = (Pc + kSplit - 1) / kSplit;
     const int parts = nact > 0 ? nact : 1;
+    // what the first K / V tiles and the q/k operands read depends on the
+    // position only: the pages, the rope rows and the new position's page are
+    // looked up once per step, so no layer's tile addresses wait on a load
+    const int s0 = r < parts ? r : parts;
+    KTile<kD> kt0;
+    VTile<kD> vt0;
+    k_tile_pages<kD>(s0 * kSplit, a.page_table, a.max_pages, kt0);
+    v_tile_pages<kD>(s0 * kSplit, a.page_table, a.max_pages, vt0);
+    const QKPre pre0 = qk_prefetch<kD, kG>(P, P, (const bf16*)a.layers[0].gamma_q,
+                                           (const bf16*)a.layers[0].gamma_k,
+                                           (const bf16*)a.cos_table, (const bf16*)a.sin_table,
+                                           a.rope_rows, a.page_table, a.max_pages);
     __syncthreads();
     for (int l = 0; l < a.n_layers; ++l) {
       const TfdLayer w = a.layers[l];
       const uint32_t tag = tag0 + (uint32_t)l + 1u;
       stamp(tl);
-      // the o slab, this block's first K / V tiles and the q/k norm operands
+      // this block's first K / V tiles, the q/k norm scales and the o slab
       // depend on no other block: requested before the qkv arithmetic, they
-      // land while it runs and while the QKV projection arrives
-      slab_issue<1>((const bf16*)w.w_o, kQD, 64 * r, kXO * x, wo);
+      // land while it runs and while the QKV projection arrives.  The tiles
+      // load unconditionally (a tile past P reads valid rows the attention
+      // masks): loads under a branch make the wait for the qkv rows also wait
+      // for them.
       KTile<kD> kt;
       VTile<kD> vt;
-      const int s0 = r < parts ? r : parts;
-      k_tile_issue<kD, true>(s0, x, P, a.page_table, a.max_pages, (const bf16*)w.k_pool,
-                             a.num_pages, 8, kt);
-      v_tile_issue<kD, true>(s0, x, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
-                             a.num_pages, 8, vt);
-      const QKPre pre = qk_prefetch<kD, kG>(P, P, (const bf16*)w.gamma_q, (const bf16*)w.gamma_k,
-                                            (const bf16*)a.cos_table, (const bf16*)a.sin_table,
-                                            a.rope_rows, a.page_table, a.max_pages);
+#pragma unroll
+      for (int p = 0; p < AttnShape<kD>::kKPasses; ++p) kt.pg[p] = kt0.pg[p];
+#pragma unroll
+      for (int p = 0; p < AttnShape<kD>::kVPasses; ++p) vt.pg[p] = vt0.pg[p];
+      k_tile_load_pages<kD, true>(s0 * kSplit, x, (const bf16*)w.k_pool, a.num_pages, 8, kt);
+      v_tile_load_pages<kD, true>(s0 * kSplit, x, (const bf16*)w.v_pool, a.num_pages, 8, vt);
+      QKPre pre = pre0;
+      qk_gammas<kD, kG>((const bf16*)w.gamma_q, (const bf16*)w.gamma_k, pre);
+      slab_issue<1>((const bf16*)w.w_o, kQD, 64 * r, kXO * x, wo);
       // ---- qkv (the hidden state is in hid_s)
       gemv_finish_ll<kCH, kRqkv, kNorm, kStore, kXcdLocal>(vb_qkv, hid_s, gq_in, nullptr,
                                                            a.x_qkv, tag, kH, qkv_n, eps, wq);
