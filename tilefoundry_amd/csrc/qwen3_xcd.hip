@@ -285,6 +285,9 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
   u32x4 gq_in[kCH], gq_post[kCH];
   gemv_issue<kCH, kRqkv>(vb_qkv, (const bf16*)a.layers[0].w_qkv, kH, qkv_n, wq);
   load_x<kCH>((const bf16*)a.layers[0].gamma_in, kH / 8, lane, gq_in);
+  // the layer table's entry for the next layer is read a layer ahead, so no
+  // layer's first loads wait on the read of their addresses
+  TfdLayer wn = a.layers[0];
   for (int t = 0; t < steps; ++t, ++P) {
     uint64_t* tl = (a.timeline && t < a.timeline_steps)
                        ? a.timeline + ((int64_t)t * nb + blockIdx.x) * (14 * a.n_layers + 4)
@@ -314,7 +317,8 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
                                            a.rope_rows, a.page_table, a.max_pages);
     __syncthreads();
     for (int l = 0; l < a.n_layers; ++l) {
-      const TfdLayer w = a.layers[l];
+      const TfdLayer w = wn;
+      wn = a.layers[(l + 1) % a.n_layers];
       const uint32_t tag = tag0 + (uint32_t)l + 1u;
       stamp(tl);
       // this block's first K / V tiles, the q/k norm scales and the o slab
@@ -408,9 +412,9 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
       slab_finish<3>(xs, wd, dpart_x, 64 * r, tag);
       // the next layer's qkv weights -- after the last layer, layer 0's for the
       // next step -- stream while the down partials are summed
-      gemv_issue<kCH, kRqkv>(vb_qkv, (const bf16*)a.layers[(l + 1) % a.n_layers].w_qkv, kH,
+      gemv_issue<kCH, kRqkv>(vb_qkv, (const bf16*)wn.w_qkv, kH,
                              qkv_n, wq);
-      load_x<kCH>((const bf16*)a.layers[(l + 1) % a.n_layers].gamma_in, kH / 8, lane, gq_in);
+      load_x<kCH>((const bf16*)wn.gamma_in, kH / 8, lane, gq_in);
       allreduce_residual(xa.dpart, kH, r, h1_s, hid_x, hid_s, tag, red, err);
       stamp(tl);
     }
