@@ -215,6 +215,23 @@ def test_xcd_kernel_tracks_the_persistent_kernel(gpu_device):
     assert one[0].tokens == b.tokens[:1]
 
 
+def test_xcd_kernel_paging_changes_no_bit(gpu_device):
+    """The XCD kernel looks up its first K/V tiles' pages once per step: a permuted
+    page table gives the bits of the identity layout, through contexts that cross
+    16-token pages and 64-position splits, in one launch and in launches of a step."""
+    cfg = QWEN3_1_7B.with_(num_hidden_layers=2)
+    w = synthetic_weights(cfg, seed=8, norms="ones")
+    prompt = _prompt(40, cfg.vocab_size, seed=12)
+    runs = []
+    for page_seed in (None, 7, 13):
+        eng = Engine(cfg, w, device=gpu_device, max_new=96, prompt_room=40, mode="xcd",
+                     page_seed=page_seed)
+        runs.append(eng.generate(prompt, 96, record_logits=True))
+    for r in runs[1:]:
+        assert r.tokens == runs[0].tokens
+        assert torch.equal(r.logits, runs[0].logits)
+
+
 def test_xcd_kernel_is_independent_of_where_a_launch_starts(gpu_device):
     """The dispatcher's first XCD moves with the workgroups dispatched before a
     launch.  Single-workgroup kernels launched in between rotate it through
