@@ -232,9 +232,10 @@ __device__ __forceinline__ void load_x_coh(const bf16* __restrict__ x, int nch, 
 // kSingle selects the HIR's own rms_norm op instead (src/tilefoundry/ir/hir/nn/
 // rms_norm.py:103-110: f32(f32(x * r) * gamma) rounded to bf16 once), the norm
 // the Granite model writes as tf.rms_norm.
-template <int kCmax, bool kSingle = false>
-__device__ __forceinline__ void rms_norm_apply(u32x4 (&xr)[kCmax], const u32x4 (&gr)[kCmax], int K,
-                                               float eps) {
+// The scale 1 / sqrt(mean(x^2) + eps) of a vector held as below (chunks past K
+// zero): the sum of squares in lane-chunk order, then the wave sum.
+template <int kCmax>
+__device__ __forceinline__ float rms_scale(const u32x4 (&xr)[kCmax], int K, float eps) {
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < kCmax; ++i) {
@@ -247,22 +248,55 @@ __device__ __forceinline__ void rms_norm_apply(u32x4 (&xr)[kCmax], const u32x4 (
     }
   }
   ss = wave_sum(ss);
-  const float r = 1.0f / sqrtf(ss / (float)K + eps);
+  return 1.0f / sqrtf(ss / (float)K + eps);
+}
+
+// One chunk of the normalised vector, given the scale.
+template <bool kSingle = false>
+__device__ __forceinline__ u32x4 rms_norm_chunk(const u32x4 x, const u32x4 g, float r) {
+  const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+  const uint32_t gw[4] = {g.x, g.y, g.z, g.w};
+  uint32_t o[4];
 #pragma unroll
-  for (int i = 0; i < kCmax; ++i) {
-    const uint32_t w[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
-    const uint32_t gw[4] = {gr[i].x, gr[i].y, gr[i].z, gr[i].w};
-    uint32_t o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float lo = kSingle ? (bf_lo(w[e]) * r) * bf_lo(gw[e])
-                               : rbf(rbf(bf_lo(w[e]) * r) * bf_lo(gw[e]));
-      const float hi = kSingle ? (bf_hi(w[e]) * r) * bf_hi(gw[e])
-                               : rbf(rbf(bf_hi(w[e]) * r) * bf_hi(gw[e]));
-      o[e] = pack2(lo, hi);
-    }
-    xr[i] = u32x4{o[0], o[1], o[2], o[3]};   // chunks past K stay zero (0 * r * 0)
+  for (int e = 0; e < 4; ++e) {
+    const float lo = kSingle ? (bf_lo(w[e]) * r) * bf_lo(gw[e])
+                             : rbf(rbf(bf_lo(w[e]) * r) * bf_lo(gw[e]));
+    const float hi = kSingle ? (bf_hi(w[e]) * r) * bf_hi(gw[e])
+                             : rbf(rbf(bf_hi(w[e]) * r) * bf_hi(gw[e]));
+    o[e] = pack2(lo, hi);
   }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+template <int kCmax, bool kSingle = false>
+__device__ __forceinline__ void rms_norm_apply(u32x4 (&xr)[kCmax], const u32x4 (&gr)[kCmax], int K,
+                                               float eps) {
+  const float r = rms_scale<kCmax>(xr, K, eps);
+#pragma unroll
+  for (int i = 0; i < kCmax; ++i)
+    xr[i] = rms_norm_chunk<kSingle>(xr[i], gr[i], r);   // chunks past K stay zero (0 * r * 0)
+}
+
+// The same norm shared by the kWavesPerBlock waves of a block that all hold
+// the whole vector (kCmax == kWavesPerBlock): every wave computes the scale
+// (the sum's order needs the whole vector per lane), wave w normalises chunk
+// slice w into `buf` (K/2 words of LDS) and every wave reads the result back --
+// the values rms_norm_apply gives, with a quarter of its per-element work per
+// wave.  Every wave of the block must call it (it holds a block barrier).
+template <int kCmax>
+__device__ __forceinline__ void rms_norm_apply_block(u32x4 (&xr)[kCmax], const u32x4 (&gr)[kCmax],
+                                                     int K, float eps, uint32_t* buf) {
+  static_assert(kCmax == kWavesPerBlock, "one chunk slice per wave");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+  const float r = rms_scale<kCmax>(xr, K, eps);
+#pragma unroll
+  for (int i = 0; i < kCmax; ++i)
+    if (i == wave)
+      *reinterpret_cast<u32x4*>(buf + 4 * (i * kWave + lane)) = rms_norm_chunk(xr[i], gr[i], r);
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kCmax; ++i) xr[i] = *reinterpret_cast<const u32x4*>(buf + 4 * (i * kWave + lane));
 }
 
 template <int kCmax, bool kSingle = false>

@@ -144,22 +144,33 @@ __device__ __forceinline__ uint32_t bf_pair(bf16 lo, bf16 hi) {
   return (uint32_t)lo | ((uint32_t)hi << 16);
 }
 
+// nbuf: the norm is shared by the block's waves through this LDS buffer
+// (rms_norm_apply_block); then every wave of the block must call this with
+// rows of its own (the caller's partition guarantees it).
 template <int kCmax, int kR, int kPro, int kEpi, int kPol = kCoherent>
 __device__ __forceinline__ void gemv_finish_ll(int vb, const uint32_t* xs,
                                                const u32x4 (&gr)[kCmax],
                                                const uint32_t* resid_s, uint32_t* out,
                                                uint32_t tag, int K, int N, float eps,
-                                               const u32x4 (&w)[kR][kCmax]) {
+                                               const u32x4 (&w)[kR][kCmax],
+                                               uint32_t* nbuf = nullptr) {
   static_assert(kR % 2 == 0, "outputs leave in pairs");
   static_assert(kEpi != kSwiglu || kR % 4 == 0, "swiglu outputs leave in pairs");
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int64_t row0 = ((int64_t)vb * kWavesPerBlock + wave) * kR;
-  if (row0 >= N) return;
+  // a wave without rows still takes its part in a shared norm (block barrier)
+  if (row0 >= N && !(kPro == kNorm && nbuf)) return;
   const int nvalid = (int)((N - row0) < kR ? (N - row0) : kR);
   u32x4 xr[kCmax];
   x_from_lds<kCmax>(xs, K / 8, lane, xr);
-  if (kPro == kNorm) rms_norm_apply<kCmax>(xr, gr, K, eps);
+  if constexpr (kPro == kNorm && kCmax == kWavesPerBlock) {
+    if (nbuf) rms_norm_apply_block<kCmax>(xr, gr, K, eps, nbuf);
+    else rms_norm_apply<kCmax>(xr, gr, K, eps);
+  } else if (kPro == kNorm) {
+    rms_norm_apply<kCmax>(xr, gr, K, eps);
+  }
+  if (row0 >= N) return;
   float acc[kR];
   dot_loaded<kCmax, kR>(w, xr, acc);
   if (kEpi == kSwiglu) {

@@ -251,6 +251,7 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
   __shared__ float s_sc[kMaxItems][kG * kSplit];
   __shared__ float s_new[kMaxItems][kG];
   __shared__ float red[kXcds * 64];
+  __shared__ __attribute__((aligned(16))) uint32_t nrm_s[kH / 2];   // the shared input norms
   const int xcc = xcc_id();
   const int x = xcc & (kXcds - 1), r = (int)blockIdx.x / kXcds;
   const int nb = gridDim.x;
@@ -340,7 +341,8 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
       slab_issue<1>((const bf16*)w.w_o, kQD, 64 * r, kXO * x, wo);
       // ---- qkv (the hidden state is in hid_s)
       gemv_finish_ll<kCH, kRqkv, kNorm, kStore, kXcdLocal>(vb_qkv, hid_s, gq_in, nullptr,
-                                                           a.x_qkv, tag, kH, qkv_n, eps, wq);
+                                                           a.x_qkv, tag, kH, qkv_n, eps, wq,
+                                                           nrm_s);
       stamp(tl);
       const AttnLL ll{a.x_qkv, smax_x, psum_x, pout_x, a.x_attn, tag};
       if (r >= parts)
@@ -401,7 +403,8 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
 #pragma unroll
           for (int c = 0; c < kCH; ++c) wg[i][c] = i < kEarly ? we[i][c] : wl[i - kEarly][c];
         gemv_finish_ll<kCH, kRgu, kNorm, kSwiglu, kXcdLocal>(vb_gu, h1_s, gq_post, nullptr,
-                                                             a.x_mid, tag, kH, 2 * kI, eps, wg);
+                                                             a.x_mid, tag, kH, 2 * kI, eps, wg,
+                                                             nrm_s);
       }
       stamp(tl);
       slab_issue<3>((const bf16*)w.w_down, kI, 64 * r, kXI * x, wd);
