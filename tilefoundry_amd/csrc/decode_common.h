@@ -280,7 +280,7 @@ __device__ __forceinline__ void rms_norm_apply(u32x4 (&xr)[kCmax], const u32x4 (
 // The same norm shared by the kWavesPerBlock waves of a block that all hold
 // the whole vector (kCmax == kWavesPerBlock): every wave computes the scale
 // (the sum's order needs the whole vector per lane), wave w normalises chunk
-// slice w into `buf` (K/2 words of LDS) and every wave reads the result back --
+// slice w into `buf` (kCmax * 256 words of LDS) and every wave reads it back --
 // the values rms_norm_apply gives, with a quarter of its per-element work per
 // wave.  Every wave of the block must call it (it holds a block barrier).
 template <int kCmax>
