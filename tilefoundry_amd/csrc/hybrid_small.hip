@@ -570,7 +570,11 @@ int tfd_rowgemv_bf16(const TfdRowGemvArgs* args, void* stream) {
       return fail(kBadArg, "rowgemv: x_kind %d", a.x_kind);
   }
   if (a.x_rows && a.ldxr < a.K) return fail(kBadShape, "rowgemv: ldxr < K");
-  const int kG = a.K == 2048 ? 4 : 2;
+  // a short normed projection (the router: 256 rows) takes one row per wave,
+  // four times the blocks and a quarter of the loads in flight per lane; every
+  // row's sum is the same whichever wave makes it
+  const bool one_row = a.K == 2048 && a.N <= 512 && a.x_kind == TFD_ROWX_NORM_F32;
+  const int kG = a.K == 2048 ? (one_row ? 1 : 4) : 2;
   const int ngroups = (a.N + kG - 1) / kG;
   const int blocks = std::min((ngroups + kWavesPerBlock - 1) / kWavesPerBlock, 2048);
   hipStream_t s = (hipStream_t)stream;
@@ -587,7 +591,10 @@ int tfd_rowgemv_bf16(const TfdRowGemvArgs* args, void* stream) {
     else TFD_RG_E(X, 8, 2);                \
   } while (0)
   switch (a.x_kind) {
-    case TFD_ROWX_NORM_F32: TFD_RG_K(TFD_ROWX_NORM_F32); break;
+    case TFD_ROWX_NORM_F32:
+      if (one_row) TFD_RG_E(TFD_ROWX_NORM_F32, 4, 1);
+      else TFD_RG_K(TFD_ROWX_NORM_F32);
+      break;
     case TFD_ROWX_GATED_F32: TFD_RG_K(TFD_ROWX_GATED_F32); break;
     case TFD_ROWX_OPERAND: TFD_RG_K(TFD_ROWX_OPERAND); break;
     default: TFD_RG_K(TFD_ROWX_ROWS); break;
