@@ -7,9 +7,12 @@ through its page table (``place_context``), and one engine step is compared
 with the oracle's forward over the same caches.
 
 * C2: the batch-1 engine at positions near the end of the 2,048-token run
-  (2,070 and 2,078), in both persistent kernels and in the per-phase graph, with
-  the Qwen3-1.7B layer shape (two layers, a 4,096-token vocabulary so the CPU
-  oracle runs in seconds).
+  (2,070 and 2,078) and on either side of 2,048 (where the XCD kernel's 32
+  ranks per kv head go from one 64-position tile each to two), in both
+  persistent kernels and in the per-phase graph, with the Qwen3-1.7B layer
+  shape (two layers, a 4,096-token vocabulary so the CPU oracle runs in
+  seconds).  The XCD kernel also at depths where a rank's split holds two,
+  three and four tiles (up to its 8,192-position limit).
 * C3: the batched engine at batch 32 over contexts of 4,000 .. 4,095 positions
   (ragged, the workload's depth), one layer at full width.
 
@@ -73,14 +76,11 @@ def c2_weights():
     return synthetic_weights(C2_SHAPE, seed=3, norms="ones")
 
 
-@pytest.mark.parametrize("mode", ["persistent", "xcd", "graph"])
-@pytest.mark.parametrize("P", [2070, 2078])
-def test_c2_step_at_depth(gpu_device, c2_weights, mode, P):
-    cfg, w = C2_SHAPE, c2_weights
+def _step_at_depth(device, cfg, w, mode, P, max_new=2048, prompt_room=64):
     print(f"[deep] c2 mode={mode} position={P}", flush=True)
     ks, vs = _caches(cfg, P, seed=P)
     token = 1234
-    eng = Engine(cfg, w, device=gpu_device, max_new=2048, prompt_room=64, mode=mode)
+    eng = Engine(cfg, w, device=device, max_new=max_new, prompt_room=prompt_room, mode=mode)
     eng.place_context(ks, vs, token)
     eng.run_steps(1)
     torch.cuda.synchronize()
@@ -91,6 +91,19 @@ def test_c2_step_at_depth(gpu_device, c2_weights, mode, P):
     print(f"  {r}", flush=True)
     # the step appended this token's K/V at position P and advanced the position
     assert int(eng.pos.item()) == P + 1
+
+
+@pytest.mark.parametrize("mode", ["persistent", "xcd", "graph"])
+@pytest.mark.parametrize("P", [2047, 2048, 2049, 2070, 2078])
+def test_c2_step_at_depth(gpu_device, c2_weights, mode, P):
+    _step_at_depth(gpu_device, C2_SHAPE, c2_weights, mode, P)
+
+
+# tiles per rank's split: 4,095 two (the last such depth); 4,097 and 6,100
+# three; 8,100 four (the engine's cache sized to 8,192 positions)
+@pytest.mark.parametrize("P", [4095, 4097, 6100, 8100])
+def test_c2_xcd_step_past_two_tiles_per_rank(gpu_device, c2_weights, P):
+    _step_at_depth(gpu_device, C2_SHAPE, c2_weights, "xcd", P, max_new=8192 - 64)
 
 
 def test_c3_batch32_step_at_4096_contexts(gpu_device):

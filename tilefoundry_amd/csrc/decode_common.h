@@ -140,8 +140,16 @@ __device__ __forceinline__ u32x4 load16_stream(const bf16* p) {
 // ---------------------------------------------------------------------------
 constexpr int kCoherent = 16;  // buffer cache-policy bits: device scope (sc1)
 
+// The base is read through readfirstlane: a pointer the kernel loaded from
+// memory (the per-layer weight table) sits in vector registers, and a buffer
+// descriptor the compiler must treat as divergent costs a loop around every
+// access (one pass per distinct descriptor value among the lanes).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, -1, 0x00020000);
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  void* u = (void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, -1, 0x00020000);
 }
 __device__ __forceinline__ u32x4 coh_ld16(const void* base, uint32_t byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), byte_off, 0, kCoherent);

@@ -731,6 +731,12 @@ __device__ __forceinline__ void qk_gammas(const bf16* __restrict__ gq, const bf1
 // bits in every block) and its own positions of the prior context,
 //   s_j = bf16( sum_d bf16(q_s[d] * K[j][d]) ),
 // and records the split's max per query head.
+//
+// A split is `chunks` tiles of 64 positions.  Per-phase launches keep the
+// scores in global rows of s_stride; the flag-in-data kernels keep a block's
+// own scores in LDS, G rows of chunks * 64.  `kt` holds the split's first tile
+// (loaded by the caller); with kt1 the caller has also loaded the second, so
+// a two-tile split waits on no load issued inside this phase.
 // ---------------------------------------------------------------------------
 template <int D, int G, bool kLL, int kPol = kCoherent, class Grp = BlockGrp>
 __device__ __forceinline__ void attn_scores_phase(
@@ -738,7 +744,7 @@ __device__ __forceinline__ void attn_scores_phase(
     const int* __restrict__ page_table, int max_pages, bf16* __restrict__ kpool, bf16* __restrict__ vpool, int num_pages,
     int kv_heads, float scale, float eps, float* __restrict__ S, int s_stride,
     float* __restrict__ smax, float* __restrict__ snew, const AttnLL& ll, const KTile<D>& kt,
-    int* err, int chunks = 1) {
+    int* err, int chunks = 1, const KTile<D>* kt1 = nullptr) {
   using A = AttnShape<D>;
   constexpr int kHalf = D / 2;
   static_assert(kHalf <= kWave, "one wave holds a head as (d, d + D/2) lane pairs");
@@ -891,7 +897,7 @@ __device__ __forceinline__ void attn_scores_phase(
         if (valid) {
           if (part == 0) {
             if (kLL)
-              S[g * kSplit + (j - j0)] = sc;
+              S[g * chunks * kSplit + (j - j0)] = sc;
             else
               S[(int64_t)(h * G + g) * s_stride + j] = sc;
           }
@@ -902,6 +908,16 @@ __device__ __forceinline__ void attn_scores_phase(
   };
   KTile<D> ka = kt, kb;
   int c = 0;
+  if (kt1 != nullptr && ntl >= 2) {
+    // tile 1 came with the caller's loads; tile 2 (if any) loads during tile 1
+    kb = *kt1;
+    tile(0, ka, kb, std::false_type{});
+    if (ntl > 2)
+      tile(1, kb, ka, std::true_type{});
+    else
+      tile(1, kb, ka, std::false_type{});
+    c = 2;
+  }
   for (; c + 2 < ntl; c += 2) {
     tile(c, ka, kb, std::true_type{});
     tile(c + 1, kb, ka, std::true_type{});
@@ -973,7 +989,7 @@ __device__ __forceinline__ void attn_pv_phase(
     const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
     float* part_out, int* counters, bf16* __restrict__ attn_out, const AttnLL& ll,
     const VTile<D>& vt, int* err, int chunks = 1, const Hook& polled = Hook(),
-    const OutMap& omap = OutMap()) {
+    const OutMap& omap = OutMap(), const VTile<D>* vt1 = nullptr) {
   using A = AttnShape<D>;
   constexpr int kLpp = A::kLpp;
   constexpr int kGroups = A::kGroups;
@@ -998,8 +1014,9 @@ __device__ __forceinline__ void attn_pv_phase(
   const int wg = wave < G ? wave : 0;
   // the persistent kernel passes this block's own scores and new-key scores (LDS)
   const float sn = kLL ? snew[wg] : snew[h * G + wg];
+  // flag-in-data kernels: this block's scores in LDS, G rows of slen
   const float sj_first =
-      kLL ? S[wg * kSplit + lane] : S[(int64_t)(h * G + wg) * s_stride + j0 + lane];
+      kLL ? S[wg * slen + lane] : S[(int64_t)(h * G + wg) * s_stride + j0 + lane];
   float mx = kNegInf;
   for (int s0 = 0; s0 < nact; s0 += kWave) {
     const int s = s0 + lane;
@@ -1046,10 +1063,13 @@ __device__ __forceinline__ void attn_pv_phase(
   auto tile = [&](int c, const VTile<D>& cur, float sj, VTile<D>& nxt, float& sj_next,
                   auto issue) {
     const int jc = j0 + c * kSplit;
+    if (kLL && c > 0) sj = S[wg * slen + (jc - j0) + lane];   // LDS: no prefetch needed
     if (decltype(issue)::value) {
-      // lanes past jend read a score of this row (in bounds, unused)
-      const int jn = jc + kSplit + lane;
-      sj_next = S[(int64_t)(h * G + wg) * s_stride + (jn < jend ? jn : jend - 1)];
+      if (!kLL) {
+        // lanes past jend read a score of this row (in bounds, unused)
+        const int jn = jc + kSplit + lane;
+        sj_next = S[(int64_t)(h * G + wg) * s_stride + (jn < jend ? jn : jend - 1)];
+      }
       v_tile_load_at<D, kLL, Grp>(jc + kSplit, h, page_table, max_pages, vpool, num_pages, kv_heads,
                              nxt);
     }
@@ -1095,6 +1115,16 @@ __device__ __forceinline__ void attn_pv_phase(
   VTile<D> va = vt, vb;
   float sa = sj_first, sb = 0.f;
   int c = 0;
+  if (kLL && vt1 != nullptr && ntl >= 2) {
+    // tile 1 came with the caller's loads; tile 2 (if any) loads during tile 1
+    vb = *vt1;
+    tile(0, va, sa, vb, sb, std::false_type{});
+    if (ntl > 2)
+      tile(1, vb, sb, va, sa, std::true_type{});
+    else
+      tile(1, vb, sb, va, sa, std::false_type{});
+    c = 2;
+  }
   for (; c + 2 < ntl; c += 2) {
     tile(c, va, sa, vb, sb, std::true_type{});
     tile(c + 1, vb, sb, va, sa, std::true_type{});
@@ -1201,18 +1231,20 @@ __device__ __forceinline__ void attn_pv_phase(
 // the same arithmetic as the last-block merge above.  Up to kChunk splits at a
 // time, every word of a chunk (partial sums, maxima, partial outputs and the
 // new key's values) polled in one round: a thread holds at most one of each.
+// Splits are `chunks` tiles of 64 positions, as in parts 1 and 2.
 // ---------------------------------------------------------------------------
 template <int D, int G, class Hook = NoHook, int kPol = kCoherent, class Grp = BlockGrp>
 __device__ __forceinline__ void attn_merge_ll(int split, int h, int P, int max_pages,
                                               int kv_heads, const float* snew, const AttnLL& ll,
-                                              int* err, const Hook& polled = Hook()) {
+                                              int* err, const Hook& polled = Hook(),
+                                              int chunks = 1) {
   constexpr int kPairs = G * D / 2;
   constexpr int kChunk = 32;                          // splits staged at a time
   static_assert(kChunk * G <= kBlock && kPairs + kChunk <= kBlock, "one word of a kind per thread");
   const int heads = kv_heads * G;
   const int tid = Grp::tid();
   if (P < 0 || P >= max_pages * kPage) P = 0;
-  const int nact = (P + kSplit - 1) / kSplit;
+  const int nact = (P + chunks * kSplit - 1) / (chunks * kSplit);
   const int participants = nact > 0 ? nact : 1;
   if (split >= participants) return;
   const int q0 = split * kPairs / participants, q1 = (split + 1) * kPairs / participants;

@@ -19,8 +19,10 @@
 // heads 2x, 2x + 1 (the Qwen3-1.7B shape: 16 q heads, 8 kv heads, head_dim 128,
 // hidden 2048, intermediate 6144):
 //   qkv     the XCD's 512 q/k/v rows (16 per block, full rows of 2048)
-//   attn    kv head x over the context, 64-position splits s = r, r + 32, ...:
-//           scores, the split maxima, P.V partials and the merge all exchange
+//   attn    kv head x over the context in at most 32 contiguous splits of ct
+//           64-position tiles, ct = ceil(tiles / 32): split r is rank r's, so
+//           a rank's share grows by one tile only when every rank's does.
+//           Scores, the split maxima, P.V partials and the merge all exchange
 //           inside the XCD (model.py:172-212, the two-pass softmax as authored)
 //   o       K split: the XCD's 256 attention outputs against W_o[:, 256x..+256];
 //           block r makes rows 64r..64r+63 of that partial product
@@ -229,10 +231,11 @@ __device__ __forceinline__ void lm_head_grid(const u32x4 (&xr)[kCmax], const bf1
 
 // ---------------------------------------------------------------------------
 // The kernel (Qwen3-1.7B shape only: H 2048, 16 q / 8 kv heads of 128, I 6144;
-// the host entry checks it).  kMaxItems attention splits per block.
+// the host entry checks it).  A rank's split holds at most kMaxTiles tiles of
+// 64 positions: the context holds at most kRanks * kMaxTiles * 64 positions.
 // ---------------------------------------------------------------------------
 constexpr int kH = 2048, kQD = 2048, kI = 6144, kD = 128, kG = 2;
-constexpr int kMaxItems = 4;
+constexpr int kMaxTiles = 4;
 constexpr int kXO = kG * kD;                 // 256: an XCD's attention outputs (o's K slice)
 constexpr int kXI = kI / kXcds;              // 768: an XCD's intermediate columns (down's K slice)
 
@@ -248,8 +251,8 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
   __shared__ __attribute__((aligned(16))) uint32_t hid_s[kH / 2];
   __shared__ __attribute__((aligned(16))) uint32_t h1_s[kH / 2];
   __shared__ __attribute__((aligned(16))) uint32_t hs[(kG + 2) * kD / 2];
-  __shared__ float s_sc[kMaxItems][kG * kSplit];
-  __shared__ float s_new[kMaxItems][kG];
+  __shared__ float s_sc[kG * kMaxTiles * kSplit];    // the split's scores, G rows of ct * 64
+  __shared__ float s_new[kG];
   __shared__ float red[kXcds * 64];
   __shared__ __attribute__((aligned(16))) uint32_t nrm_s[kH / 2];   // the shared input norms
   const int xcc = xcc_id();
@@ -302,16 +305,27 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
         *reinterpret_cast<u32x4*>(hid_s + 4 * i) = *reinterpret_cast<const u32x4*>(row + 4 * i);
     }
     const int Pc = (P >= 0 && P < a.max_pages * kPage) ? P : 0;
-    const int nact = (Pc + kSplit - 1) / kSplit;
+    // the prior context in at most kRanks splits of ct tiles; rank r < parts
+    // owns split r (the host bounds the context so ct <= kMaxTiles)
+    const int ntile = (Pc + kSplit - 1) / kSplit;
+    const int ct = ntile > kRanks ? (ntile + kRanks - 1) / kRanks : 1;
+    const int slen = ct * kSplit;
+    const int nact = (Pc + slen - 1) / slen;
     const int parts = nact > 0 ? nact : 1;
-    // what the first K / V tiles and the q/k operands read depends on the
+    // what the first two K / V tiles and the q/k operands read depends on the
     // position only: the pages, the rope rows and the new position's page are
-    // looked up once per step, so no layer's tile addresses wait on a load
+    // looked up once per step, so no layer's tile addresses wait on a load.
+    // A one-tile split's "second" tile is its first again: those loads hit
+    // the lines the first brought into the L2, and loads that are always
+    // issued keep every later wait count exact.
     const int s0 = r < parts ? r : parts;
-    KTile<kD> kt0;
-    VTile<kD> vt0;
-    k_tile_pages<kD>(s0 * kSplit, a.page_table, a.max_pages, kt0);
-    v_tile_pages<kD>(s0 * kSplit, a.page_table, a.max_pages, vt0);
+    const int j0 = s0 * slen, j1 = ct > 1 ? j0 + kSplit : j0;
+    KTile<kD> kt0, kt1p;
+    VTile<kD> vt0, vt1p;
+    k_tile_pages<kD>(j0, a.page_table, a.max_pages, kt0);
+    v_tile_pages<kD>(j0, a.page_table, a.max_pages, vt0);
+    k_tile_pages<kD>(j1, a.page_table, a.max_pages, kt1p);
+    v_tile_pages<kD>(j1, a.page_table, a.max_pages, vt1p);
     const QKPre pre0 = qk_prefetch<kD, kG>(P, P, (const bf16*)a.layers[0].gamma_q,
                                            (const bf16*)a.layers[0].gamma_k,
                                            (const bf16*)a.cos_table, (const bf16*)a.sin_table,
@@ -328,14 +342,22 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
       // load unconditionally (a tile past P reads valid rows the attention
       // masks): loads under a branch make the wait for the qkv rows also wait
       // for them.
-      KTile<kD> kt;
-      VTile<kD> vt;
+      KTile<kD> kt, kt1;
+      VTile<kD> vt, vt1;
 #pragma unroll
-      for (int p = 0; p < AttnShape<kD>::kKPasses; ++p) kt.pg[p] = kt0.pg[p];
+      for (int p = 0; p < AttnShape<kD>::kKPasses; ++p) {
+        kt.pg[p] = kt0.pg[p];
+        kt1.pg[p] = kt1p.pg[p];
+      }
 #pragma unroll
-      for (int p = 0; p < AttnShape<kD>::kVPasses; ++p) vt.pg[p] = vt0.pg[p];
-      k_tile_load_pages<kD, true>(s0 * kSplit, x, (const bf16*)w.k_pool, a.num_pages, 8, kt);
-      v_tile_load_pages<kD, true>(s0 * kSplit, x, (const bf16*)w.v_pool, a.num_pages, 8, vt);
+      for (int p = 0; p < AttnShape<kD>::kVPasses; ++p) {
+        vt.pg[p] = vt0.pg[p];
+        vt1.pg[p] = vt1p.pg[p];
+      }
+      k_tile_load_pages<kD, true>(j0, x, (const bf16*)w.k_pool, a.num_pages, 8, kt);
+      v_tile_load_pages<kD, true>(j0, x, (const bf16*)w.v_pool, a.num_pages, 8, vt);
+      k_tile_load_pages<kD, true>(j1, x, (const bf16*)w.k_pool, a.num_pages, 8, kt1);
+      v_tile_load_pages<kD, true>(j1, x, (const bf16*)w.v_pool, a.num_pages, 8, vt1);
       QKPre pre = pre0;
       qk_gammas<kD, kG>((const bf16*)w.gamma_q, (const bf16*)w.gamma_k, pre);
       slab_issue<1>((const bf16*)w.w_o, kQD, 64 * r, kXO * x, wo);
@@ -345,44 +367,33 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
                                                            nrm_s);
       stamp(tl);
       const AttnLL ll{a.x_qkv, smax_x, psum_x, pout_x, a.x_attn, tag};
-      if (r >= parts)
+      if (r >= parts) {
         rows_issue<kCH, kRgu, kEarly>(vb_gu, (const bf16*)w.w_gu, kH, 0, we);
-      // ---- attention part 1: scores (splits r, r + 32, ... of kv head x)
-      for (int sp = r, j = 0; sp < parts && j < kMaxItems; sp += kRanks, ++j) {
-        if (j > 0)
-          k_tile_issue<kD, true>(sp, x, P, a.page_table, a.max_pages, (const bf16*)w.k_pool,
-                                 a.num_pages, 8, kt);
+        stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl);
+      } else {
+        // ---- attention part 1: scores over split r of kv head x
         stage_head_ll<kD, kG, kXcdLocal>(x, 8 * kG, 8, ll, hs, err);
         __syncthreads();
-        if (j == 0) rows_issue<kCH, kRgu, kEarly>(vb_gu, (const bf16*)w.w_gu, kH, 0, we);
-        if (j == 0) stamp(tl);
-        attn_scores_phase<kD, kG, true, kXcdLocal>(sp, x, hs, pre, a.rope_rows, P, P,
-                                                   a.page_table, a.max_pages, (bf16*)w.k_pool,
-                                                   (bf16*)w.v_pool, a.num_pages, 8, a.scale, eps,
-                                                   s_sc[j], 0, nullptr, s_new[j], ll, kt, err);
-        if (j == 0) stamp(tl);
-      }
-      // ---- part 2: P.V partials
-      for (int sp = r, j = 0; sp < parts && j < kMaxItems; sp += kRanks, ++j) {
-        if (j > 0)
-          v_tile_issue<kD, true>(sp, x, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
-                                 a.num_pages, 8, vt);
-        if (j == 0) stamp(tl);
+        rows_issue<kCH, kRgu, kEarly>(vb_gu, (const bf16*)w.w_gu, kH, 0, we);
+        stamp(tl);
+        attn_scores_phase<kD, kG, true, kXcdLocal>(r, x, hs, pre, a.rope_rows, P, P, a.page_table,
+                                                   a.max_pages, (bf16*)w.k_pool, (bf16*)w.v_pool,
+                                                   a.num_pages, 8, a.scale, eps, s_sc, 0, nullptr,
+                                                   s_new, ll, kt, err, ct, &kt1);
+        stamp(tl);
+        // ---- part 2: P.V partials
+        stamp(tl);
         attn_pv_phase<kD, kG, true, NoHook, RowOut, kXcdLocal>(
-            sp, x, a.nsplit, nullptr, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
-            a.num_pages, 8, s_sc[j], 0, nullptr, s_new[j], nullptr, nullptr, nullptr, nullptr,
-            ll, vt, err);
-        if (j == 0) stamp(tl);
-      }
-      // ---- part 3: merge
-      for (int sp = r, j = 0; sp < parts && j < kMaxItems; sp += kRanks, ++j) {
-        if (j == 0) stamp(tl);
-        attn_merge_ll<kD, kG, NoHook, kXcdLocal>(sp, x, P, a.max_pages, 8, s_new[j], ll, err);
+            r, x, a.nsplit, nullptr, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
+            a.num_pages, 8, s_sc, 0, nullptr, s_new, nullptr, nullptr, nullptr, nullptr, ll, vt,
+            err, ct, NoHook{}, RowOut{}, &vt1);
+        stamp(tl);
+        // ---- part 3: merge
+        stamp(tl);
+        attn_merge_ll<kD, kG, NoHook, kXcdLocal>(r, x, P, a.max_pages, 8, s_new, ll, err, NoHook{},
+                                                 ct);
         __syncthreads();
-        if (j == 0) stamp(tl);
-      }
-      if (r >= parts) {
-        stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl);
+        stamp(tl);
       }
       // ---- o: this XCD's 256 attention outputs against the o slab
       ll_stage<kXcdLocal>(attn_x, kXO, tag, xs, err);
@@ -468,9 +479,9 @@ int tfd_decode_xcd(const TfdDecodeArgs* args, const TfdXcdArgs* xcd, int steps, 
     return fail(kBadArg, "decode_xcd: epoch %u + %d steps passes 2^32: zero the exchange "
                 "buffers and restart the epoch at 0", a.epoch, steps);
   if ((int64_t)a.nsplit * kSplit < (int64_t)a.max_pages * kPage || a.num_pages <= 0 ||
-      a.nsplit > kRanks * kMaxItems)
+      a.nsplit > kRanks * kMaxTiles)
     return fail(kBadShape, "decode_xcd: nsplit=%d must cover max_pages=%d and be at most %d",
-                a.nsplit, a.max_pages, kRanks * kMaxItems);
+                a.nsplit, a.max_pages, kRanks * kMaxTiles);
   int dev = 0, cus = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
