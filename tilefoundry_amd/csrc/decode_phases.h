@@ -735,8 +735,9 @@ __device__ __forceinline__ void qk_gammas(const bf16* __restrict__ gq, const bf1
 // A split is `chunks` tiles of 64 positions.  Per-phase launches keep the
 // scores in global rows of s_stride; the flag-in-data kernels keep a block's
 // own scores in LDS, G rows of chunks * 64.  `kt` holds the split's first tile
-// (loaded by the caller); with kt1 the caller has also loaded the second, so
-// a two-tile split waits on no load issued inside this phase.
+// (loaded by the caller); with kt1 (and kt2) the caller has also loaded the
+// second (and third), so a split of up to that many tiles waits on no load
+// issued inside this phase.
 // ---------------------------------------------------------------------------
 template <int D, int G, bool kLL, int kPol = kCoherent, class Grp = BlockGrp>
 __device__ __forceinline__ void attn_scores_phase(
@@ -744,7 +745,7 @@ __device__ __forceinline__ void attn_scores_phase(
     const int* __restrict__ page_table, int max_pages, bf16* __restrict__ kpool, bf16* __restrict__ vpool, int num_pages,
     int kv_heads, float scale, float eps, float* __restrict__ S, int s_stride,
     float* __restrict__ smax, float* __restrict__ snew, const AttnLL& ll, const KTile<D>& kt,
-    int* err, int chunks = 1, const KTile<D>* kt1 = nullptr) {
+    int* err, int chunks = 1, const KTile<D>* kt1 = nullptr, const KTile<D>* kt2 = nullptr) {
   using A = AttnShape<D>;
   constexpr int kHalf = D / 2;
   static_assert(kHalf <= kWave, "one wave holds a head as (d, d + D/2) lane pairs");
@@ -906,27 +907,33 @@ __device__ __forceinline__ void attn_scores_phase(
       }
     }
   };
+  // tiles c, c + 1, ... from `cur`, the buffers alternating
+  auto run = [&](int c, KTile<D>& cur, KTile<D>& oth) {
+    for (; c + 2 < ntl; c += 2) {
+      tile(c, cur, oth, std::true_type{});
+      tile(c + 1, oth, cur, std::true_type{});
+    }
+    if (c + 1 < ntl) {
+      tile(c, cur, oth, std::true_type{});
+      tile(c + 1, oth, cur, std::false_type{});
+    } else if (c < ntl) {
+      tile(c, cur, oth, std::false_type{});
+    }
+  };
   KTile<D> ka = kt, kb;
-  int c = 0;
   if (kt1 != nullptr && ntl >= 2) {
-    // tile 1 came with the caller's loads; tile 2 (if any) loads during tile 1
+    // tile 1 (and 2) came with the caller's loads; later tiles load in turn
     kb = *kt1;
     tile(0, ka, kb, std::false_type{});
-    if (ntl > 2)
-      tile(1, kb, ka, std::true_type{});
-    else
+    if (kt2 != nullptr && ntl >= 3) {
+      ka = *kt2;
       tile(1, kb, ka, std::false_type{});
-    c = 2;
-  }
-  for (; c + 2 < ntl; c += 2) {
-    tile(c, ka, kb, std::true_type{});
-    tile(c + 1, kb, ka, std::true_type{});
-  }
-  if (c + 1 < ntl) {
-    tile(c, ka, kb, std::true_type{});
-    tile(c + 1, kb, ka, std::false_type{});
-  } else if (c < ntl) {
-    tile(c, ka, kb, std::false_type{});
+      run(2, ka, kb);
+    } else {
+      run(1, kb, ka);
+    }
+  } else {
+    run(0, ka, kb);
   }
   if (!page_ok) raise_error(err, kErrPageRange);
 #pragma unroll
@@ -989,7 +996,8 @@ __device__ __forceinline__ void attn_pv_phase(
     const float* __restrict__ smax, const float* __restrict__ snew, float* part_sum,
     float* part_out, int* counters, bf16* __restrict__ attn_out, const AttnLL& ll,
     const VTile<D>& vt, int* err, int chunks = 1, const Hook& polled = Hook(),
-    const OutMap& omap = OutMap(), const VTile<D>* vt1 = nullptr) {
+    const OutMap& omap = OutMap(), const VTile<D>* vt1 = nullptr,
+    const VTile<D>* vt2 = nullptr) {
   using A = AttnShape<D>;
   constexpr int kLpp = A::kLpp;
   constexpr int kGroups = A::kGroups;
@@ -1112,28 +1120,35 @@ __device__ __forceinline__ void attn_pv_phase(
     }
     Grp::sync();                        // p is rewritten by the next tile
   };
+  // tiles c, c + 1, ... from `cur`, the buffers alternating
+  auto run = [&](int c, VTile<D>& cur, float& scur, VTile<D>& oth, float& soth) {
+    for (; c + 2 < ntl; c += 2) {
+      tile(c, cur, scur, oth, soth, std::true_type{});
+      tile(c + 1, oth, soth, cur, scur, std::true_type{});
+    }
+    if (c + 1 < ntl) {
+      tile(c, cur, scur, oth, soth, std::true_type{});
+      tile(c + 1, oth, soth, cur, scur, std::false_type{});
+    } else if (c < ntl) {
+      tile(c, cur, scur, oth, soth, std::false_type{});
+    }
+  };
   VTile<D> va = vt, vb;
   float sa = sj_first, sb = 0.f;
-  int c = 0;
   if (kLL && vt1 != nullptr && ntl >= 2) {
-    // tile 1 came with the caller's loads; tile 2 (if any) loads during tile 1
+    // tile 1 (and 2) came with the caller's loads; later tiles load in turn
+    // (flag-in-data kernels read each tile's scores from LDS)
     vb = *vt1;
     tile(0, va, sa, vb, sb, std::false_type{});
-    if (ntl > 2)
-      tile(1, vb, sb, va, sa, std::true_type{});
-    else
+    if (vt2 != nullptr && ntl >= 3) {
+      va = *vt2;
       tile(1, vb, sb, va, sa, std::false_type{});
-    c = 2;
-  }
-  for (; c + 2 < ntl; c += 2) {
-    tile(c, va, sa, vb, sb, std::true_type{});
-    tile(c + 1, vb, sb, va, sa, std::true_type{});
-  }
-  if (c + 1 < ntl) {
-    tile(c, va, sa, vb, sb, std::true_type{});
-    tile(c + 1, vb, sb, va, sa, std::false_type{});
-  } else if (c < ntl) {
-    tile(c, va, sa, vb, sb, std::false_type{});
+      run(2, va, sa, vb, sb);
+    } else {
+      run(1, vb, sb, va, sa);
+    }
+  } else {
+    run(0, va, sa, vb, sb);
   }
   if (!page_ok) raise_error(err, kErrPageRange);
   if (wave < G && lane == 0) {

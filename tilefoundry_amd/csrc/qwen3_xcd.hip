@@ -160,6 +160,70 @@ __device__ __forceinline__ void allreduce_residual(const uint32_t* part, int H, 
   __syncthreads();
 }
 
+// The all-reduce's sum for rows kRows q .. kRows q + kRows - 1 of an H-long
+// f32 product held as one partial per XCD (part: [8][H] words): sum in XCD
+// order, out = bf16(res + bf16(sum)), published to this XCD's copy (bf16
+// pairs).  Readers stage the whole vector from there.  The same arithmetic as
+// allreduce_residual.
+template <int kRows>
+__device__ __forceinline__ void allreduce_publish(const uint32_t* part, int H, int q,
+                                                  const uint32_t* res, uint32_t* mine_xcd,
+                                                  uint32_t tag, float* red, int* err) {
+  constexpr int kPairs = kRows / 2;                 // word pairs per XCD partial
+  static_assert(kXcds * kPairs % kBlock == 0 && kPairs <= kBlock, "whole passes");
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int k = 0; k < kXcds * kPairs / kBlock; ++k) {
+    const int i = tid + k * kBlock, y = i / kPairs, i2 = i % kPairs;
+    const u32x2 v = ll_get2<kCoherent>(part, (uint32_t)(y * H + kRows * q + 2 * i2), tag, err);
+    red[y * kRows + 2 * i2] = __uint_as_float(v.x);
+    red[y * kRows + 2 * i2 + 1] = __uint_as_float(v.y);
+  }
+  __syncthreads();
+  if (tid < kPairs) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int y = 0; y < kXcds; ++y) {
+      s0 += red[y * kRows + 2 * tid];
+      s1 += red[y * kRows + 2 * tid + 1];
+    }
+    const int w = kPairs * q + tid;                  // word of rows kRows q + 2 tid, +1
+    const uint32_t rw = res[w];
+    const uint32_t pr = bf_pair(f2bf(bf_lo(rw) + rbf(s0)), f2bf(bf_hi(rw) + rbf(s1)));
+    ll_put<kXcdLocal>(mine_xcd, (uint32_t)w, pr, tag);
+  }
+}
+
+// A slab (slab_issue's lanes and rows) requested straight into LDS: load (p, j)
+// of wave w lands as 1 KB at block ((w * 8 + p) * kC + j), lane l's 16 bytes at
+// l.  Only for a block that waits on no other block until the data is used:
+// a barrier after these loads waits for every load issued before it.
+template <int kC>
+__device__ __forceinline__ void slab_to_lds(const bf16* __restrict__ W, int ld, int row0, int col0,
+                                            u32x4* lds) {
+  typedef __attribute__((address_space(1))) void g_void;
+  typedef __attribute__((address_space(3))) void l_void;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int half = lane >> 5, c = lane & 31;
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int64_t row = row0 + 16 * wave + 2 * p + half;
+#pragma unroll
+    for (int j = 0; j < kC; ++j)
+      __builtin_amdgcn_global_load_lds((g_void*)(W + row * ld + col0 + 8 * (c + 32 * j)),
+                                       (l_void*)(lds + ((wave * 8 + p) * kC + j) * kWave), 16, 0,
+                                       2 /* nt: streamed once */);
+  }
+}
+template <int kC>
+__device__ __forceinline__ void slab_from_lds(const u32x4* lds, u32x4 (&w)[8][kC]) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+#pragma unroll
+  for (int p = 0; p < 8; ++p)
+#pragma unroll
+    for (int j = 0; j < kC; ++j) w[p][j] = lds[((wave * 8 + p) * kC + j) * kWave + lane];
+}
+
 __device__ __forceinline__ void stamp(uint64_t*& tl) {
   if (tl && threadIdx.x == 0) *tl++ = wall_clock64();
 }
@@ -231,47 +295,91 @@ __device__ __forceinline__ void lm_head_grid(const u32x4 (&xr)[kCmax], const bf1
 
 // ---------------------------------------------------------------------------
 // The kernel (Qwen3-1.7B shape only: H 2048, 16 q / 8 kv heads of 128, I 6144;
-// the host entry checks it).  A rank's split holds at most kMaxTiles tiles of
-// 64 positions: the context holds at most kRanks * kMaxTiles * 64 positions.
+// the host entry checks it).
+//
+// Two roles per XCD, each with its own step loop (one loop holding both
+// roles' registers live at once would spill):
+//   attention ranks r < 16   the attention (split r of the context when r is
+//                            below the step's split count), 8 gate/up rows per
+//                            wave, and the down all-reduce (128 rows each)
+//   streaming ranks r >= 16  the XCD's qkv rows (8 per wave), 16 gate/up rows
+//                            per wave and the down slab requested as soon as
+//                            their qkv rows are out -- the rows into registers,
+//                            the slab into LDS -- so they stream while the
+//                            attention chain runs, when HBM would otherwise
+//                            idle; and the o all-reduce (128 rows each)
+// Every rank makes 64 rows of the o and down partial products.  Loads retire
+// in issue order, so each all-reduce is done by the ranks with no loads in
+// flight at that point: the streaming ranks' rows have landed by the o sum,
+// and only the streaming ranks request the next layer's qkv rows in front of
+// the down sum.  An attention rank requests two of its gate/up rows before
+// the scores arithmetic and the rest after its o partials.
+//
+// A split holds at most kMaxTiles tiles of 64 positions: the context holds at
+// most kAttnRanks * kMaxTiles * 64 positions.  Up to three tiles of a split are
+// requested at the layer start.
 // ---------------------------------------------------------------------------
 constexpr int kH = 2048, kQD = 2048, kI = 6144, kD = 128, kG = 2;
-constexpr int kMaxTiles = 4;
 constexpr int kXO = kG * kD;                 // 256: an XCD's attention outputs (o's K slice)
 constexpr int kXI = kI / kXcds;              // 768: an XCD's intermediate columns (down's K slice)
+constexpr int kAttnRanks = 16, kStrmRanks = kRanks - kAttnRanks;
+constexpr int kMaxTiles = 8;
+constexpr int kRguA = 8, kRguS = 16;         // gate/up rows per wave: attention, streaming ranks
+constexpr int kRqkv = 8;                     // qkv rows per wave of a streaming rank
+constexpr int kRedRows = kH / kAttnRanks;    // 128: rows each reducer sums
+static_assert(kAttnRanks * kRguA + kStrmRanks * kRguS == 2 * kXI / kWavesPerBlock,
+              "the roles' gate/up rows cover the XCD's columns");
+static_assert(kStrmRanks * kWavesPerBlock * kRqkv == kXO + 2 * kD, "the XCD's q, k and v rows");
+static_assert(kAttnRanks == kStrmRanks, "each role's ranks sum an all-reduce's rows");
+constexpr int kCH = kH / 512;                // 16-byte chunks per lane of a 2048 row
+constexpr int kRhead = 4;
+constexpr int kDownLds = 8 * 3 * kWavesPerBlock * kWave;   // u32x4: a streaming rank's down slab
 
-__global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdArgs xa, int steps) {
-  constexpr int kCH = kH / 512;              // 16-byte chunks per lane of a 2048 row
-  constexpr int kRqkv = 4, kRgu = 12, kRhead = 4;
-  // gate/up rows requested before the scores arithmetic, which waits on no
-  // other block: they land while it runs instead of in front of the o sum
-  // (measured: 2, 4 and 6 rows early all gain ~2.5%; 8 rows gain less, the
-  // scores and P.V hand-offs slowing as much as the o sum speeds up)
-  constexpr int kEarly = 2, kLate = kRgu - kEarly;
-  __shared__ __attribute__((aligned(16))) uint32_t xs[kXI / 2];   // o / down input slice
-  __shared__ __attribute__((aligned(16))) uint32_t hid_s[kH / 2];
-  __shared__ __attribute__((aligned(16))) uint32_t h1_s[kH / 2];
-  __shared__ __attribute__((aligned(16))) uint32_t hs[(kG + 2) * kD / 2];
-  __shared__ float s_sc[kG * kMaxTiles * kSplit];    // the split's scores, G rows of ct * 64
-  __shared__ float s_new[kG];
-  __shared__ float red[kXcds * 64];
-  __shared__ __attribute__((aligned(16))) uint32_t nrm_s[kH / 2];   // the shared input norms
-  const int xcc = xcc_id();
-  const int x = xcc & (kXcds - 1), r = (int)blockIdx.x / kXcds;
+// The block's LDS (declared once in the kernel; both roles use it).
+struct XcdLds {
+  uint32_t* xs;      // o / down input slice (kXI / 2 words)
+  uint32_t* hid_s;   // the hidden state (kH / 2)
+  uint32_t* h1_s;    // h1 (kH / 2)
+  uint32_t* hs;      // the staged head slice ((kG + 2) * kD / 2)
+  float* s_sc;       // the split's scores, G rows of ct * 64
+  float* s_new;      // [kG]
+  float* red;        // all-reduce staging [kXcds * kRedRows]
+  uint32_t* nrm_s;   // the shared input norms (kH / 2)
+  u32x4* down;       // a streaming rank's down slab (kDownLds, dynamic)
+};
+
+template <bool kAttn>
+__device__ __forceinline__ void xcd_steps(const TfdDecodeArgs& a, const TfdXcdArgs& xa, int steps,
+                                          int x, int r, const XcdLds& sm) {
+  constexpr int kRgu = kAttn ? kRguA : kRguS;
+  // attention ranks: gate/up rows requested before the scores arithmetic,
+  // which waits on no other block, so they land while it runs
+  constexpr int kEarly = kAttn ? 2 : kRgu, kLate = kRgu - kEarly;
+  uint32_t* const xs = sm.xs;
+  uint32_t* const hid_s = sm.hid_s;
+  uint32_t* const h1_s = sm.h1_s;
+  uint32_t* const nrm_s = sm.nrm_s;
   const int nb = gridDim.x;
   const int V = a.vocab;
   const float eps = a.eps;
   int* const err = a.err;
-  if (threadIdx.x == 0 && xcc != x) raise_error(err, kErrPlacement | kErrSync);
   int P = coh_ldi(a.pos);
   int tok = (int)__hip_atomic_load(a.ids, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int lane = threadIdx.x & (kWave - 1);
 
-  // this block's rows: qkv (16 full rows), gate/up (48), o and down (64 of the K slice)
-  const int qkv_row0 = r < 16 ? kXO * x + 16 * r
-                              : (r < 24 ? kQD + kD * x + 16 * (r - 16)
-                                        : kQD + 8 * kD + kD * x + 16 * (r - 24));
+  // a streaming rank's qkv rows: 32 of XCD x's q (256), k (128) or v (128) rows
+  const int sr = r - kAttnRanks;
+  const int qkv_row0 = sr < 8 ? kXO * x + 32 * sr
+                              : (sr < 12 ? kQD + kD * x + 32 * (sr - 8)
+                                         : kQD + 8 * kD + kD * x + 32 * (sr - 12));
   const int vb_qkv = qkv_row0 / (kWavesPerBlock * kRqkv);
-  const int vb_gu = kRanks * x + r;
+  // gate/up rows of XCD x: 2 kXI from row 2 kXI x; the attention ranks' first
+  const int vb_gu = kAttn ? (2 * kXI * x) / (kWavesPerBlock * kRgu) + r
+                          : (2 * kXI * x + kWavesPerBlock * kAttnRanks * kRguA) /
+                                    (kWavesPerBlock * kRgu) + sr;
+  // the rows this rank sums in its role's all-reduce (down for attention
+  // ranks, o for streaming ranks)
+  const int red_q = kAttn ? r : sr;
   const int qkv_n = kQD + 2 * 8 * kD;
   // this XCD's exchange arenas
   uint32_t* const hid_x = word_at(xa.hid, (int64_t)x * (kH / 2));
@@ -285,10 +393,14 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
   uint32_t* const opart_x = word_at(xa.opart, (int64_t)x * kH);
   uint32_t* const dpart_x = word_at(xa.dpart, (int64_t)x * kH);
 
-  u32x4 wq[kRqkv][kCH], we[kEarly][kCH], wl[kLate][kCH], wo[8][1], wd[8][3];
+  u32x4 we[kEarly][kCH], wo[8][1], wd[8][3];
+  u32x4 wl[kLate > 0 ? kLate : 1][kCH];
+  u32x4 wq[kAttn ? 1 : kRqkv][kCH];
   u32x4 gq_in[kCH], gq_post[kCH];
-  gemv_issue<kCH, kRqkv>(vb_qkv, (const bf16*)a.layers[0].w_qkv, kH, qkv_n, wq);
-  load_x<kCH>((const bf16*)a.layers[0].gamma_in, kH / 8, lane, gq_in);
+  if constexpr (!kAttn) {
+    gemv_issue<kCH, kRqkv>(vb_qkv, (const bf16*)a.layers[0].w_qkv, kH, qkv_n, wq);
+    load_x<kCH>((const bf16*)a.layers[0].gamma_in, kH / 8, lane, gq_in);
+  }
   // the layer table's entry for the next layer is read a layer ahead, so no
   // layer's first loads wait on the read of their addresses
   TfdLayer wn = a.layers[0];
@@ -305,95 +417,114 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
         *reinterpret_cast<u32x4*>(hid_s + 4 * i) = *reinterpret_cast<const u32x4*>(row + 4 * i);
     }
     const int Pc = (P >= 0 && P < a.max_pages * kPage) ? P : 0;
-    // the prior context in at most kRanks splits of ct tiles; rank r < parts
-    // owns split r (the host bounds the context so ct <= kMaxTiles)
+    // the prior context in at most kAttnRanks splits of ct tiles; rank r <
+    // parts owns split r (the host bounds the context so ct <= kMaxTiles)
     const int ntile = (Pc + kSplit - 1) / kSplit;
-    const int ct = ntile > kRanks ? (ntile + kRanks - 1) / kRanks : 1;
+    const int ct = ntile > kAttnRanks ? (ntile + kAttnRanks - 1) / kAttnRanks : 1;
     const int slen = ct * kSplit;
     const int nact = (Pc + slen - 1) / slen;
     const int parts = nact > 0 ? nact : 1;
-    // what the first two K / V tiles and the q/k operands read depends on the
-    // position only: the pages, the rope rows and the new position's page are
-    // looked up once per step, so no layer's tile addresses wait on a load.
-    // A one-tile split's "second" tile is its first again: those loads hit
-    // the lines the first brought into the L2, and loads that are always
+    // what the first three K / V tiles and the q/k operands read depends on
+    // the position only: the pages, the rope rows and the new position's page
+    // are looked up once per step, so no layer's tile addresses wait on a
+    // load.  A split's tiles past its last are its first again: those loads
+    // hit the lines the first brought into the L2, and loads that are always
     // issued keep every later wait count exact.
     const int s0 = r < parts ? r : parts;
-    const int j0 = s0 * slen, j1 = ct > 1 ? j0 + kSplit : j0;
-    KTile<kD> kt0, kt1p;
-    VTile<kD> vt0, vt1p;
-    k_tile_pages<kD>(j0, a.page_table, a.max_pages, kt0);
-    v_tile_pages<kD>(j0, a.page_table, a.max_pages, vt0);
-    k_tile_pages<kD>(j1, a.page_table, a.max_pages, kt1p);
-    v_tile_pages<kD>(j1, a.page_table, a.max_pages, vt1p);
-    const QKPre pre0 = qk_prefetch<kD, kG>(P, P, (const bf16*)a.layers[0].gamma_q,
-                                           (const bf16*)a.layers[0].gamma_k,
-                                           (const bf16*)a.cos_table, (const bf16*)a.sin_table,
-                                           a.rope_rows, a.page_table, a.max_pages);
+    const int j0 = s0 * slen, j1 = ct > 1 ? j0 + kSplit : j0, j2 = ct > 2 ? j0 + 2 * kSplit : j0;
+    KTile<kD> kt0, kt1p, kt2p;
+    VTile<kD> vt0, vt1p, vt2p;
+    QKPre pre0{};
+    if constexpr (kAttn) {
+      k_tile_pages<kD>(j0, a.page_table, a.max_pages, kt0);
+      v_tile_pages<kD>(j0, a.page_table, a.max_pages, vt0);
+      k_tile_pages<kD>(j1, a.page_table, a.max_pages, kt1p);
+      v_tile_pages<kD>(j1, a.page_table, a.max_pages, vt1p);
+      k_tile_pages<kD>(j2, a.page_table, a.max_pages, kt2p);
+      v_tile_pages<kD>(j2, a.page_table, a.max_pages, vt2p);
+      pre0 = qk_prefetch<kD, kG>(P, P, (const bf16*)a.layers[0].gamma_q,
+                                 (const bf16*)a.layers[0].gamma_k, (const bf16*)a.cos_table,
+                                 (const bf16*)a.sin_table, a.rope_rows, a.page_table,
+                                 a.max_pages);
+    }
     __syncthreads();
     for (int l = 0; l < a.n_layers; ++l) {
       const TfdLayer w = wn;
       wn = a.layers[(l + 1) % a.n_layers];
       const uint32_t tag = tag0 + (uint32_t)l + 1u;
+      const bool last = l + 1 == a.n_layers;
       stamp(tl);
-      // this block's first K / V tiles, the q/k norm scales and the o slab
-      // depend on no other block: requested before the qkv arithmetic, they
-      // land while it runs and while the QKV projection arrives.  The tiles
-      // load unconditionally (a tile past P reads valid rows the attention
-      // masks): loads under a branch make the wait for the qkv rows also wait
-      // for them.
-      KTile<kD> kt, kt1;
-      VTile<kD> vt, vt1;
+      if constexpr (kAttn) {
+        // the split's first K / V tiles, the q/k norm scales and the o slab
+        // depend on no other block: requested first, they land while the
+        // streaming ranks make the QKV projection.  The tiles load
+        // unconditionally (a tile past P reads valid rows the attention
+        // masks): loads under a branch make a later wait also wait for them.
+        KTile<kD> kt, kt1, kt2;
+        VTile<kD> vt, vt1, vt2;
+        QKPre pre = pre0;
 #pragma unroll
-      for (int p = 0; p < AttnShape<kD>::kKPasses; ++p) {
-        kt.pg[p] = kt0.pg[p];
-        kt1.pg[p] = kt1p.pg[p];
-      }
+        for (int p = 0; p < AttnShape<kD>::kKPasses; ++p) {
+          kt.pg[p] = kt0.pg[p];
+          kt1.pg[p] = kt1p.pg[p];
+          kt2.pg[p] = kt2p.pg[p];
+        }
 #pragma unroll
-      for (int p = 0; p < AttnShape<kD>::kVPasses; ++p) {
-        vt.pg[p] = vt0.pg[p];
-        vt1.pg[p] = vt1p.pg[p];
-      }
-      k_tile_load_pages<kD, true>(j0, x, (const bf16*)w.k_pool, a.num_pages, 8, kt);
-      v_tile_load_pages<kD, true>(j0, x, (const bf16*)w.v_pool, a.num_pages, 8, vt);
-      k_tile_load_pages<kD, true>(j1, x, (const bf16*)w.k_pool, a.num_pages, 8, kt1);
-      v_tile_load_pages<kD, true>(j1, x, (const bf16*)w.v_pool, a.num_pages, 8, vt1);
-      QKPre pre = pre0;
-      qk_gammas<kD, kG>((const bf16*)w.gamma_q, (const bf16*)w.gamma_k, pre);
-      slab_issue<1>((const bf16*)w.w_o, kQD, 64 * r, kXO * x, wo);
-      // ---- qkv (the hidden state is in hid_s)
-      gemv_finish_ll<kCH, kRqkv, kNorm, kStore, kXcdLocal>(vb_qkv, hid_s, gq_in, nullptr,
-                                                           a.x_qkv, tag, kH, qkv_n, eps, wq,
-                                                           nrm_s);
-      stamp(tl);
-      const AttnLL ll{a.x_qkv, smax_x, psum_x, pout_x, a.x_attn, tag};
-      if (r >= parts) {
-        rows_issue<kCH, kRgu, kEarly>(vb_gu, (const bf16*)w.w_gu, kH, 0, we);
-        stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl);
+        for (int p = 0; p < AttnShape<kD>::kVPasses; ++p) {
+          vt.pg[p] = vt0.pg[p];
+          vt1.pg[p] = vt1p.pg[p];
+          vt2.pg[p] = vt2p.pg[p];
+        }
+        k_tile_load_pages<kD, true>(j0, x, (const bf16*)w.k_pool, a.num_pages, 8, kt);
+        v_tile_load_pages<kD, true>(j0, x, (const bf16*)w.v_pool, a.num_pages, 8, vt);
+        k_tile_load_pages<kD, true>(j1, x, (const bf16*)w.k_pool, a.num_pages, 8, kt1);
+        v_tile_load_pages<kD, true>(j1, x, (const bf16*)w.v_pool, a.num_pages, 8, vt1);
+        k_tile_load_pages<kD, true>(j2, x, (const bf16*)w.k_pool, a.num_pages, 8, kt2);
+        v_tile_load_pages<kD, true>(j2, x, (const bf16*)w.v_pool, a.num_pages, 8, vt2);
+        qk_gammas<kD, kG>((const bf16*)w.gamma_q, (const bf16*)w.gamma_k, pre);
+        slab_issue<1>((const bf16*)w.w_o, kQD, 64 * r, kXO * x, wo);
+        stamp(tl);
+        if (r >= parts) {
+          rows_issue<kCH, kRgu, kEarly>(vb_gu, (const bf16*)w.w_gu, kH, 0, we);
+          stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl);
+        } else {
+          const AttnLL ll{a.x_qkv, smax_x, psum_x, pout_x, a.x_attn, tag};
+          // ---- attention part 1: scores over split r of kv head x
+          stage_head_ll<kD, kG, kXcdLocal>(x, 8 * kG, 8, ll, sm.hs, err);
+          __syncthreads();
+          rows_issue<kCH, kRgu, kEarly>(vb_gu, (const bf16*)w.w_gu, kH, 0, we);
+          stamp(tl);
+          attn_scores_phase<kD, kG, true, kXcdLocal>(r, x, sm.hs, pre, a.rope_rows, P, P,
+                                                     a.page_table, a.max_pages, (bf16*)w.k_pool,
+                                                     (bf16*)w.v_pool, a.num_pages, 8, a.scale,
+                                                     eps, sm.s_sc, 0, nullptr, sm.s_new, ll, kt,
+                                                     err, ct, &kt1, &kt2);
+          stamp(tl);
+          // ---- part 2: P.V partials
+          stamp(tl);
+          attn_pv_phase<kD, kG, true, NoHook, RowOut, kXcdLocal>(
+              r, x, a.nsplit, nullptr, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
+              a.num_pages, 8, sm.s_sc, 0, nullptr, sm.s_new, nullptr, nullptr, nullptr, nullptr,
+              ll, vt, err, ct, NoHook{}, RowOut{}, &vt1, &vt2);
+          stamp(tl);
+          // ---- part 3: merge
+          stamp(tl);
+          attn_merge_ll<kD, kG, NoHook, kXcdLocal>(r, x, P, a.max_pages, 8, sm.s_new, ll, err,
+                                                   NoHook{}, ct);
+          __syncthreads();
+          stamp(tl);
+        }
       } else {
-        // ---- attention part 1: scores over split r of kv head x
-        stage_head_ll<kD, kG, kXcdLocal>(x, 8 * kG, 8, ll, hs, err);
-        __syncthreads();
+        slab_issue<1>((const bf16*)w.w_o, kQD, 64 * r, kXO * x, wo);
+        // ---- qkv (the hidden state is in hid_s)
+        gemv_finish_ll<kCH, kRqkv, kNorm, kStore, kXcdLocal>(vb_qkv, hid_s, gq_in, nullptr,
+                                                             a.x_qkv, tag, kH, qkv_n, eps, wq,
+                                                             nrm_s);
+        stamp(tl);
+        // every gate/up row and the down slab: they land during the attention
         rows_issue<kCH, kRgu, kEarly>(vb_gu, (const bf16*)w.w_gu, kH, 0, we);
-        stamp(tl);
-        attn_scores_phase<kD, kG, true, kXcdLocal>(r, x, hs, pre, a.rope_rows, P, P, a.page_table,
-                                                   a.max_pages, (bf16*)w.k_pool, (bf16*)w.v_pool,
-                                                   a.num_pages, 8, a.scale, eps, s_sc, 0, nullptr,
-                                                   s_new, ll, kt, err, ct, &kt1);
-        stamp(tl);
-        // ---- part 2: P.V partials
-        stamp(tl);
-        attn_pv_phase<kD, kG, true, NoHook, RowOut, kXcdLocal>(
-            r, x, a.nsplit, nullptr, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
-            a.num_pages, 8, s_sc, 0, nullptr, s_new, nullptr, nullptr, nullptr, nullptr, ll, vt,
-            err, ct, NoHook{}, RowOut{}, &vt1);
-        stamp(tl);
-        // ---- part 3: merge
-        stamp(tl);
-        attn_merge_ll<kD, kG, NoHook, kXcdLocal>(r, x, P, a.max_pages, 8, s_new, ll, err, NoHook{},
-                                                 ct);
-        __syncthreads();
-        stamp(tl);
+        slab_to_lds<3>((const bf16*)w.w_down, kI, 64 * r, kXI * x, sm.down);
+        stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl); stamp(tl);
       }
       // ---- o: this XCD's 256 attention outputs against the o slab
       ll_stage<kXcdLocal>(attn_x, kXO, tag, xs, err);
@@ -401,35 +532,53 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
       stamp(tl);
       slab_finish<1>(xs, wo, opart_x, 64 * r, tag);
       stamp(tl);
-      // gate/up weights stream while the o partials are summed
-      rows_issue<kCH, kRgu, kLate>(vb_gu, (const bf16*)w.w_gu, kH, kEarly, wl);
-      load_x<kCH>((const bf16*)w.gamma_post, kH / 8, lane, gq_post);
-      allreduce_residual(xa.opart, kH, r, hid_s, h1_x, h1_s, tag, red, err);
+      if constexpr (kAttn) {
+        // the remaining gate/up rows stream while the streaming ranks sum o
+        rows_issue<kCH, kRgu, kLate>(vb_gu, (const bf16*)w.w_gu, kH, kEarly, wl);
+        load_x<kCH>((const bf16*)w.gamma_post, kH / 8, lane, gq_post);
+      } else {
+        load_x<kCH>((const bf16*)w.gamma_post, kH / 8, lane, gq_post);
+        allreduce_publish<kRedRows>(xa.opart, kH, red_q, hid_s, h1_x, tag, sm.red, err);
+      }
+      ll_stage<kXcdLocal>(h1_x, kH, tag, h1_s, err);
+      __syncthreads();
       stamp(tl);
-      // ---- gate/up + SwiGLU: this XCD's 768 columns
+      // ---- gate/up + SwiGLU: this block's share of the XCD's 768 columns
       {
         u32x4 wg[kRgu][kCH];
 #pragma unroll
         for (int i = 0; i < kRgu; ++i)
 #pragma unroll
-          for (int c = 0; c < kCH; ++c) wg[i][c] = i < kEarly ? we[i][c] : wl[i - kEarly][c];
+          for (int c = 0; c < kCH; ++c)
+            wg[i][c] = i < kEarly ? we[i][c] : wl[(i - kEarly) % (kLate > 0 ? kLate : 1)][c];
         gemv_finish_ll<kCH, kRgu, kNorm, kSwiglu, kXcdLocal>(vb_gu, h1_s, gq_post, nullptr,
                                                              a.x_mid, tag, kH, 2 * kI, eps, wg,
                                                              nrm_s);
       }
       stamp(tl);
-      slab_issue<3>((const bf16*)w.w_down, kI, 64 * r, kXI * x, wd);
+      if constexpr (kAttn) slab_issue<3>((const bf16*)w.w_down, kI, 64 * r, kXI * x, wd);
       // ---- down: this XCD's 768 SwiGLU values against the down slab
       ll_stage<kXcdLocal>(mid_x, kXI, tag, xs, err);
       __syncthreads();
       stamp(tl);
+      if constexpr (!kAttn) slab_from_lds<3>(sm.down, wd);
       slab_finish<3>(xs, wd, dpart_x, 64 * r, tag);
-      // the next layer's qkv weights -- after the last layer, layer 0's for the
-      // next step -- stream while the down partials are summed
-      gemv_issue<kCH, kRqkv>(vb_qkv, (const bf16*)wn.w_qkv, kH,
-                             qkv_n, wq);
-      load_x<kCH>((const bf16*)wn.gamma_in, kH / 8, lane, gq_in);
-      allreduce_residual(xa.dpart, kH, r, h1_s, hid_x, hid_s, tag, red, err);
+      if constexpr (kAttn) {
+        allreduce_publish<kRedRows>(xa.dpart, kH, red_q, h1_s, hid_x, tag, sm.red, err);
+        // the layer output is the next layer's input only for the streaming
+        // ranks (the qkv rows); an attention rank reads it for the head
+        if (last) {
+          ll_stage<kXcdLocal>(hid_x, kH, tag, hid_s, err);
+          __syncthreads();
+        }
+      } else {
+        // the next layer's qkv weights -- after the last layer, layer 0's for
+        // the next step -- stream while the attention ranks sum down
+        gemv_issue<kCH, kRqkv>(vb_qkv, (const bf16*)wn.w_qkv, kH, qkv_n, wq);
+        load_x<kCH>((const bf16*)wn.gamma_in, kH / 8, lane, gq_in);
+        ll_stage<kXcdLocal>(hid_x, kH, tag, hid_s, err);
+        __syncthreads();
+      }
       stamp(tl);
     }
     // ---- head: final norm, logits, block pick
@@ -452,6 +601,26 @@ __global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdAr
     stamp(tl);
     if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSync) break;
   }
+}
+
+__global__ __launch_bounds__(kBlock) void k_decode_xcd(TfdDecodeArgs a, TfdXcdArgs xa, int steps) {
+  __shared__ __attribute__((aligned(16))) uint32_t xs[kXI / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t hid_s[kH / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t h1_s[kH / 2];
+  __shared__ __attribute__((aligned(16))) uint32_t hs[(kG + 2) * kD / 2];
+  __shared__ float s_sc[kG * kMaxTiles * kSplit];
+  __shared__ float s_new[kG];
+  __shared__ float red[kXcds * kRedRows];
+  __shared__ __attribute__((aligned(16))) uint32_t nrm_s[kH / 2];
+  extern __shared__ __attribute__((aligned(16))) u32x4 dyn_lds[];   // kDownLds
+  const int xcc = xcc_id();
+  const int x = xcc & (kXcds - 1), r = (int)blockIdx.x / kXcds;
+  if (threadIdx.x == 0 && xcc != x) raise_error(a.err, kErrPlacement | kErrSync);
+  const XcdLds sm{xs, hid_s, h1_s, hs, s_sc, s_new, red, nrm_s, dyn_lds};
+  if (r < kAttnRanks)
+    xcd_steps<true>(a, xa, steps, x, r, sm);
+  else
+    xcd_steps<false>(a, xa, steps, x, r, sm);
 }
 
 }  // namespace
@@ -479,9 +648,9 @@ int tfd_decode_xcd(const TfdDecodeArgs* args, const TfdXcdArgs* xcd, int steps, 
     return fail(kBadArg, "decode_xcd: epoch %u + %d steps passes 2^32: zero the exchange "
                 "buffers and restart the epoch at 0", a.epoch, steps);
   if ((int64_t)a.nsplit * kSplit < (int64_t)a.max_pages * kPage || a.num_pages <= 0 ||
-      a.nsplit > kRanks * kMaxTiles)
+      a.nsplit > kAttnRanks * kMaxTiles)
     return fail(kBadShape, "decode_xcd: nsplit=%d must cover max_pages=%d and be at most %d",
-                a.nsplit, a.max_pages, kRanks * kMaxTiles);
+                a.nsplit, a.max_pages, kAttnRanks * kMaxTiles);
   int dev = 0, cus = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -492,7 +661,12 @@ int tfd_decode_xcd(const TfdDecodeArgs* args, const TfdXcdArgs* xcd, int steps, 
                 grid, cus);
   int per_cu = 0;
   const void* fn = reinterpret_cast<const void*>(&k_decode_xcd);
-  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kBlock, 0);
+  const size_t dyn = kDownLds * sizeof(u32x4);
+  static const hipError_t lds_ok =
+      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn);
+  if (lds_ok != hipSuccess)
+    return fail((int)lds_ok, "decode_xcd: %zu bytes of dynamic LDS refused", dyn);
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kBlock, dyn);
   if (e != hipSuccess) return fail((int)e, "decode_xcd: occupancy query failed");
   if (per_cu < 1)
     return fail(kUnsupported, "decode_xcd: a block does not fit a compute unit");
@@ -505,9 +679,10 @@ int tfd_decode_xcd(const TfdDecodeArgs* args, const TfdXcdArgs* xcd, int steps, 
     return v && v[0] == '1';
   }();
   if (plain)
-    e = hipLaunchKernel(fn, dim3(grid), dim3(kBlock), kargs, 0, (hipStream_t)stream);
+    e = hipLaunchKernel(fn, dim3(grid), dim3(kBlock), kargs, dyn, (hipStream_t)stream);
   else
-    e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kBlock), kargs, 0, (hipStream_t)stream);
+    e = hipLaunchCooperativeKernel(fn, dim3(grid), dim3(kBlock), kargs, (unsigned)dyn,
+                                   (hipStream_t)stream);
   if (e != hipSuccess) return fail((int)e, "decode_xcd: launch failed: %s", hipGetErrorString(e));
   return launched("decode_xcd");
 }
