@@ -94,7 +94,12 @@ __device__ __forceinline__ float group_sum(float v) {
   if (kWidth >= 4) v += dpp_f<kDppXor2>(v);
   if (kWidth >= 8) v += dpp_f<kDppHalfMirror>(v);
   if (kWidth >= 16) v += dpp_f<kDppMirror>(v);
-  if (kWidth >= 32) v += __shfl_xor(v, 16, kWave);
+  if (kWidth >= 32) {
+    // v_i + v_(i^16), the pair's two members in either order (the same bits)
+    float lo, hi;
+    pair16(v, lo, hi);
+    v = lo + hi;
+  }
   if (kWidth >= 64) {
     float lo, hi;
     pair32(v, lo, hi);
@@ -110,8 +115,9 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<kDppXor2>(v));
   v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
   v = fmaxf(v, dpp_f<kDppMirror>(v));
-  v = fmaxf(v, __shfl_xor(v, 16, kWave));
   float lo, hi;
+  pair16(v, lo, hi);
+  v = fmaxf(lo, hi);
   pair32(v, lo, hi);
   return fmaxf(lo, hi);
 }
