@@ -142,7 +142,12 @@ def traffic_for(kernel: str, positions, algorithmic_bytes: float):
     if not path.exists():
         return None, None
     try:
-        entry = json.loads(path.read_text()).get(kernel)
+        entries = json.loads(path.read_text()).get(kernel)
+        if isinstance(entries, dict):
+            entries = [entries]
+        # the committed launch over the same positions, else the first one
+        entry = next((e for e in entries
+                      if list(e.get("timed_positions", [])) == list(positions)), entries[0])
         hbm, alg = float(entry["hbm_bytes"]), float(entry["algorithmic_bytes"])
         counted = entry.get("launch", "a committed counter run")
         if list(entry.get("timed_positions", [])) == list(positions):
@@ -151,7 +156,7 @@ def traffic_for(kernel: str, positions, algorithmic_bytes: float):
         return (round(ratio * algorithmic_bytes),
                 f"committed counter ratio {ratio:.4f} (HBM bytes per algorithmic byte, counted "
                 f"on {counted}) times this launch's algorithmic bytes")
-    except (ValueError, KeyError, TypeError, ZeroDivisionError, AttributeError):
+    except (ValueError, KeyError, TypeError, ZeroDivisionError, AttributeError, IndexError):
         return None, None
 
 
@@ -302,6 +307,64 @@ def bench_c3(args) -> int:
     return 0
 
 
+# What each of the XCD kernel's 14 per-layer stamps marks, per role (the
+# attention ranks are blocks 0..127, rank = block / 8 < 16; the streaming
+# ranks the rest)
+TIMELINE_STAMPS = {
+    "attention": ["layer start", "tiles, q/k scales, o slab requested", "qkv staged",
+                  "scores done", "(P.V start)", "P.V partials out", "(merge start)",
+                  "merged outputs out", "o input staged", "o partials out", "h1 staged",
+                  "gate/up out", "SwiGLU staged", "down partials out, down sums published"],
+    "streaming": ["layer start", "qkv out", "gate/up rows + down slab requested", "", "", "",
+                  "", "", "o input staged", "o partials out", "o sums published, h1 staged",
+                  "gate/up out", "SwiGLU staged", "down partials out, layer output staged"],
+}
+
+
+def timeline(ctxs) -> int:
+    """Per-role device-clock stamps of the XCD kernel on the C2 model: one
+    step after walking a random prompt of each context length; for each stamp,
+    min / median / max over the role's blocks of (stamp - the layer's earliest
+    start) in us, averaged over layers 2 .. L-2; then the head's stamps."""
+    import torch
+
+    from tilefoundry_amd.qwen3 import QWEN3_1_7B, synthetic_weights
+    from tilefoundry_amd.qwen3.engine import Engine
+
+    cfg = QWEN3_1_7B
+    weights = synthetic_weights(cfg, seed=0)
+    eng = Engine(cfg, weights, device="cuda:0", max_new=max(ctxs) + 8, prompt_room=8,
+                 mode="xcd")
+    L, per = cfg.num_hidden_layers, 14
+    n_attn = 16 * 8
+    for ctx in ctxs:
+        g = torch.Generator().manual_seed(0)
+        prompt = torch.randint(0, cfg.vocab_size, (ctx,), generator=g).tolist()
+        st = eng.phase_timeline(prompt, 3)[1:]                # drop the first step
+        S, B = st.shape[0], st.shape[1]
+        step_us = (st[-1, :, -1, 1].median() - st[0, :, -1, 1].median()).item() / (S - 1)
+        s = st[0].reshape(B, -1)
+        print(f"== ctx {ctx}: step {step_us:.1f} us", flush=True)
+        for role, sel in (("attention", slice(0, n_attn)), ("streaming", slice(n_attn, B))):
+            print(f"  {role} ranks: stamp  min  median  max", flush=True)
+            for k in range(per):
+                if not TIMELINE_STAMPS[role][k]:
+                    continue
+                v = [(s[sel, l * per + k] - s[:, l * per].min()) for l in range(2, L - 1)]
+                mn = sum(x.min().item() for x in v) / len(v)
+                md = sum(x.median().item() for x in v) / len(v)
+                mx = sum(x.max().item() for x in v) / len(v)
+                print(f"    {k:2d} {mn:6.2f} {md:6.2f} {mx:6.2f}  {TIMELINE_STAMPS[role][k]}",
+                      flush=True)
+        h = s[:, L * per:]
+        t0 = s[:, L * per - 1].median()
+        names = ["head start", "head done", "(pick start)", "pick done"]
+        print("  head (us after the last layer's median end, median / max): " + ", ".join(
+            f"{names[k]} {(h[:, k] - t0).median().item():.1f} / {(h[:, k] - t0).max().item():.1f}"
+            for k in range(h.shape[1])), flush=True)
+    return 0
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__,
                                  formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -317,6 +380,9 @@ def main(argv=None) -> int:
                     help="persistent: one cooperative launch per run of steps; xcd: the same "
                          "with each layer split over the 8 XCDs; graph: a captured graph of "
                          "per-phase launches replayed per token")
+    ap.add_argument("--timeline", default=None, metavar="CTX[,CTX...]",
+                    help="only print the XCD kernel's per-role phase timeline on the C2 model "
+                         "at these context lengths and exit")
     ap.add_argument("--config", default="c2", choices=("c2", "c3"),
                     help="c2: the headline batch-1 workload; c3: batch 32 over 4096-token "
                          "contexts")
@@ -324,6 +390,8 @@ def main(argv=None) -> int:
     args.steps_given = any(a == "--steps" or a.startswith("--steps=") for a in (argv or sys.argv))
     if args.copy_probe:
         return copy_probe()
+    if args.timeline:
+        return timeline([int(c) for c in args.timeline.split(",")])
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (every box here "
               "has one MI355X); run with --gpus 1", file=sys.stderr)

@@ -139,6 +139,49 @@ def test_qwen3_5_checkpoint_reproduces_the_engine_weights(tmp_path):
     _same(got, w)
 
 
+def _without_head(tmp_path, tie: bool):
+    """A Qwen3.5 checkpoint with lm_head.weight removed and tie_word_embeddings
+    set to *tie*."""
+    import json
+
+    from safetensors import safe_open
+    from tests.test_oracle_hybrid_models import QWEN35_TINY, qwen35_hf
+
+    cfg = QWEN35_TINY
+    w = Q.synthetic_weights(cfg, seed=2, device="cpu", std=0.1)
+    qwen35_hf(cfg, w).to(torch.bfloat16).save_pretrained(tmp_path)
+    for path in tmp_path.glob("*.safetensors"):
+        with safe_open(str(path), "pt") as f:
+            sd = {k: f.get_tensor(k) for k in f.keys() if k != "lm_head.weight"}
+        save_file(sd, str(path))
+    index = tmp_path / "model.safetensors.index.json"
+    if index.exists():
+        d = json.loads(index.read_text())
+        d["weight_map"].pop("lm_head.weight", None)
+        index.write_text(json.dumps(d))
+    conf = tmp_path / "config.json"
+    d = json.loads(conf.read_text())
+    if "text_config" in d:
+        d["text_config"]["tie_word_embeddings"] = tie
+    d["tie_word_embeddings"] = tie
+    conf.write_text(json.dumps(d))
+    return cfg, w
+
+
+def test_qwen3_5_missing_head_is_refused_unless_tied(tmp_path):
+    """Qwen3.5-MoE does not tie its embeddings: a checkpoint without
+    lm_head.weight is an error, unless its config says the embeddings are tied
+    (then the head is the embedding table)."""
+    (tmp_path / "untied").mkdir()
+    _without_head(tmp_path / "untied", tie=False)
+    with pytest.raises(KeyError, match="not tied"):
+        C.load_qwen3_5(tmp_path / "untied")
+    (tmp_path / "tied").mkdir()
+    _, w = _without_head(tmp_path / "tied", tie=True)
+    _, got = C.load_qwen3_5(tmp_path / "tied")
+    assert torch.equal(got["head"], got["embed"])
+
+
 def test_qwen3_5_gamma_converter_is_one_plus_the_stored_delta():
     stored = torch.tensor([-0.5, -0.0078125, 0.0, 0.25, 0.9921875], dtype=torch.bfloat16)
     assert torch.equal(C._plus_one(stored),

@@ -191,9 +191,17 @@ def load_qwen3_5(path, cfg: Qwen35Config | None = None) -> tuple[Qwen35Config,
     pre = "model.language_model." if "model.language_model.embed_tokens.weight" in ck else "model."
     g = ck.get
     E, I, IS = cfg.experts, cfg.moe_inter, cfg.shared_inter
+    d = ck.config()
+    tied = bool(d.get("text_config", d).get("tie_word_embeddings",
+                                            d.get("tie_word_embeddings", False)))
+    if "lm_head.weight" in ck:
+        head = g("lm_head.weight")
+    elif tied:
+        head = g(pre + "embed_tokens.weight")
+    else:
+        raise KeyError(f"{path}: no lm_head.weight and the embeddings are not tied")
     w = {"embed": g(pre + "embed_tokens.weight"),
-         "gamma_final": _plus_one(g(pre + "norm.weight")),
-         "head": g("lm_head.weight") if "lm_head.weight" in ck else g(pre + "embed_tokens.weight")}
+         "gamma_final": _plus_one(g(pre + "norm.weight")), "head": head}
     for i in range(cfg.layers):
         p, k = f"layer{i}.", f"{pre}layers.{i}."
         w[p + "gamma_in"] = _plus_one(g(k + "input_layernorm.weight"))
