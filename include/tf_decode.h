@@ -181,7 +181,9 @@ int tfd_gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int 
  * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  Its K-split
  * work (TFD_SKINNY_COUNTERS tile counters + 2^21 f32 partials, about 8 MiB) is a
  * device array inside the library, one per GPU, held until the process ends; the
- * first call on a device looks it up and clears its counters on `stream`.  The same
+ * first call on a device looks up its address.  The array is zero when the library
+ * loads and every call leaves its counters at zero, so nothing is enqueued besides
+ * the GEMM itself, also on a first call under stream capture.  The same
  * shapes and epilogues as tfd_gemm_skinny_bf16 (TFD_EPI_*), the results of that entry
  * with a work buffer of the same size (a K split across blocks is planned within the
  * scratch, with fewer slices where more would not fit).  Calls that overlap on one GPU

@@ -1,6 +1,6 @@
 """Regenerate the committed golden fixtures (CPU, minutes at C2 size).
 
-    python tests/golden/make_golden.py [c1] [c2]
+    python tests/golden/make_golden.py [c1] [c2] [c2x] [c2xs]
 
 c1_tiny_fp32.json   workload C1: tiny Qwen3 (2 layers, hidden 256, 4q/2kv,
                     head_dim 64, I 768, V 4096), fp32, every parameter N(0, 0.02)
@@ -20,6 +20,8 @@ c2_*_exact_step*.npy  (target c2x) the same two steps teacher-forced on the
                     f32 sums sit from these: the noise floor of f32 summation
                     order at this depth, which bounds what any correct
                     implementation can be asked to match.
+c2_*_exact_steps.npz  (target c2xs) the exact-sum logits at steps 0, 8, ...,
+                    56 and 63 of the same teacher-forced walk (keys step<k>).
 
 The fixtures are data (inputs and expected outputs), regenerated from seeds.
 """
@@ -134,8 +136,38 @@ def make_c2x():
     (HERE / "c2_order_noise.json").write_text(json.dumps(noise, indent=1))
 
 
+EXACT_STEPS = (0, 8, 16, 24, 32, 40, 48, 56, 63)
+
+
+def make_c2xs():
+    """c2_*_exact_steps.npz: the exact-sum logits (as make_c2x) at every 8th of
+    the 64 steps and the last, raw bf16 bits under keys step<k>; steps 0 and 63
+    must reproduce c2_*_exact_step{0,63}.npy bit for bit."""
+    fx = json.loads((HERE / "c2_qwen3_1p7b.json").read_text())
+    prompt = fx["prompt"]
+    pl = len(prompt)
+    for norms in ("random", "ones"):
+        t0 = time.time()
+        w = synthetic_weights(QWEN3_1_7B, seed=0, norms=norms)
+        seq = prompt + fx[norms]["tokens"][:63]
+        with O.exact_sums():
+            ex = forced_logits(O.Qwen3Oracle(O.C2, w), seq, {pl - 1 + k for k in EXACT_STEPS})
+        arrays = {}
+        for k in EXACT_STEPS:
+            arrays[f"step{k}"] = (ex[pl - 1 + k].to(torch.bfloat16).view(torch.int16).numpy()
+                                  .astype(np.uint16))
+        for k in (0, 63):
+            same = np.load(HERE / f"c2_{norms}_exact_step{k}.npy")
+            assert np.array_equal(same, arrays[f"step{k}"]), (norms, k)
+        np.savez_compressed(HERE / f"c2_{norms}_exact_steps.npz", **arrays)
+        print(f"c2xs {norms}: {time.time() - t0:.0f}s", flush=True)
+        del w
+
+
 if __name__ == "__main__":
     which = sys.argv[1:] or ["c1", "c2", "c2x"]
+    if "c2xs" in which:
+        make_c2xs()
     if "c1" in which:
         make_c1()
     if "c2" in which:

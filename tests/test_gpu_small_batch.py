@@ -55,10 +55,15 @@ def _check_gemv(got, w, xb, name, min_cos=0.99999):
     assert r["within_1ulp"] >= 0.999, (name, r)
 
 
-@pytest.mark.parametrize("rows,K", [(1, 2048), (3, 2048), (4, 2048), (1, 4096), (2, 4096)])
-def test_rowgemv_norm_prologue(gpu_device, rows, K):
-    g = torch.Generator().manual_seed(rows * K)
-    N = 1001                                   # not a multiple of the rows per wave
+# N = 1,001: not a multiple of the rows per wave.  N <= 512 at K = 2,048 takes
+# the one-row-per-wave kernel (the C4 router's 256 rows; 509 leaves a ragged
+# last block of waves)
+@pytest.mark.parametrize("rows,K,N", [(1, 2048, 1001), (3, 2048, 1001), (4, 2048, 1001),
+                                      (1, 4096, 1001), (2, 4096, 1001),
+                                      (1, 2048, 256), (2, 2048, 256), (4, 2048, 256),
+                                      (1, 2048, 509), (3, 2048, 509), (4, 2048, 509)])
+def test_rowgemv_norm_prologue(gpu_device, rows, K, N):
+    g = torch.Generator().manual_seed(rows * K + N)
     x = (torch.randn(rows, K + 8, generator=g) * 3).to(DEV)
     gamma = (1 + 0.2 * torch.randn(K, generator=g)).to(BF).to(DEV)
     w = (torch.randn(N, K, generator=g) * 0.03).to(BF).to(DEV)

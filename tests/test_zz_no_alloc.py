@@ -71,3 +71,38 @@ def test_noalloc_gemm_rejects_bad_shapes(gpu_device):
     with pytest.raises(_lib.TFDError, match="K=100"):
         L.tfd_gemm_skinny_bf16_noalloc(ptr(dummy), ptr(dummy), 4, 100, 16, _lib.EPI_STORE,
                                        None, 0, ptr(dummy), 16, s)
+
+
+def test_noalloc_gemm_replays_in_a_captured_graph(gpu_device):
+    """The entry enqueues nothing but the GEMM, so a graph captured around it
+    replays it; the K-split counters it leaves at zero make every replay the
+    same.  Three replays with eager work and a synchronisation between them,
+    each against the work-buffer entry's eager result."""
+    M, K, N, epi = 32, 6144, 2048, _lib.EPI_RESID          # splits across blocks
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn(M, K, generator=g) * 0.5).to(torch.bfloat16).to(gpu_device)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(gpu_device)
+    r = torch.randn(M, N, generator=g).to(torch.bfloat16).to(gpu_device)
+    wp, xo = _packed(w), operand_order(x)
+    work = torch.zeros(_lib.NOALLOC_SCRATCH_FLOATS, device=gpu_device, dtype=torch.float32)
+    want = _out(M, N, epi, gpu_device)
+    L = lib()
+    L.tfd_gemm_skinny_bf16(ptr(xo), ptr(wp), M, K, N, epi, ptr(r), N, ptr(want), N,
+                           ptr(work), work.numel(), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    got = _out(M, N, epi, gpu_device)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            L.tfd_gemm_skinny_bf16_noalloc(ptr(xo), ptr(wp), M, K, N, epi, ptr(r), N, ptr(got),
+                                           N, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for k in range(3):
+        got.zero_()
+        _ = (x.float() @ w.float().t()).sum().item()           # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), k

@@ -1159,11 +1159,12 @@ int tfd_embed_rows_bf16(const void* table, const int64_t* ids, void* out, int ld
 // counters and f32 partial tiles -- lives in a file-scope device array instead
 // of a caller-supplied buffer.  Each device holds its own copy of the array for
 // the life of the process; its address on the current device is looked up once
-// (hipGetSymbolAddress: the array's name is not a device address in host code)
-// and its counters are cleared once by a fill kernel on the caller's stream
-// (not a memset: such nodes misbehave under graph replay).  Every call leaves
-// the counters it used at zero, as with a caller's buffer.  Calls that overlap
-// on one device share the array and race.
+// (hipGetSymbolAddress: the array's name is not a device address in host code).
+// The array is zero when the code object loads (a __device__ array without an
+// initializer), and every call leaves the tile counters it used at zero, as
+// with a caller's buffer, so nothing is ever enqueued to clear it: a first call
+// made under stream capture behaves as any other.  Calls that overlap on one
+// device share the array and race.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -1176,13 +1177,9 @@ constexpr int kScratchDevices = 64;
 float* g_scratch[kScratchDevices] = {};
 std::mutex g_scratch_lock;
 
-__global__ __launch_bounds__(kBlock) void k_zero_words(float* __restrict__ p, int n) {
-  for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) p[i] = 0.f;
-}
-
-// The current device's scratch, set up on first use; nullptr (rc set by fail())
-// when that fails.
-float* scratch_on_device(hipStream_t s, int& rc) {
+// The current device's scratch, looked up on first use; nullptr (rc set by
+// fail()) when that fails.
+float* scratch_on_device(int& rc) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
@@ -1203,10 +1200,6 @@ float* scratch_on_device(hipStream_t s, int& rc) {
                 "gemm_skinny_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
       return nullptr;
     }
-    hipLaunchKernelGGL(k_zero_words, dim3((kSkCounters + kBlock - 1) / kBlock), dim3(kBlock), 0,
-                       s, (float*)p, (int)kSkCounters);
-    rc = launched("gemm_skinny_noalloc: counter clear");
-    if (rc) return nullptr;
     g_scratch[dev] = (float*)p;
   }
   return g_scratch[dev];
@@ -1228,7 +1221,7 @@ int tfd_gemm_skinny_bf16_noalloc(const void* x, const void* w, int M, int K, int
   // the work-buffer entry plans within its caller's buffer.
   if (epilogue == kEpiLogitsDiv) return fail(kBadArg, "gemm_skinny_noalloc: epilogue %d", epilogue);
   int rc = 0;
-  float* work = scratch_on_device((hipStream_t)stream, rc);
+  float* work = scratch_on_device(rc);
   if (!work) return rc;
   return gemm_skinny_bf16(x, w, M, K, N, epilogue, resid, ldr, out, ldo, work, kScratchFloats,
                           1.f, stream);
