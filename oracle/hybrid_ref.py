@@ -103,6 +103,57 @@ def route_topk_softmax(logits: torch.Tensor, k: int):
     return bf(torch.softmax(vals, dim=-1)), idx
 
 
+def _over_set(scores: torch.Tensor, idx: torch.Tensor):
+    """The entries of *scores* [B][E] at the index sets *idx* [B][k], ordered as
+    topk_ordered orders them (largest first, equal values by ascending index)."""
+    asc = idx.sort(dim=-1).values
+    vals = scores.gather(-1, asc)
+    order = torch.sort(vals, dim=-1, descending=True, stable=True).indices
+    return vals.gather(-1, order), asc.gather(-1, order)
+
+
+def route_softmax_over(logits: torch.Tensor, idx: torch.Tensor):
+    """route_softmax_topk's weights for a given expert set per row."""
+    vals, idx = _over_set(torch.softmax(logits.float(), dim=-1), idx)
+    return vals / vals.sum(dim=-1, keepdim=True), idx
+
+
+def route_topk_softmax_over(logits: torch.Tensor, idx: torch.Tensor):
+    """route_topk_softmax's weights for a given expert set per row."""
+    vals, idx = _over_set(logits.float(), idx)
+    return bf(torch.softmax(vals, dim=-1)), idx
+
+
+def follow_near_ties(rlog: torch.Tensor, own: torch.Tensor, engine: torch.Tensor, k: int,
+                     slack: float = 2.0):
+    """Routing teacher-forced at near-ties, for whole-step parity tests.  Where a
+    row's engine top-k set differs from the oracle's (*own*), the engine's set is
+    taken if every expert it adds has an oracle logit at most *slack* bf16 ulps
+    (of the k-th logit) below the k-th, and every expert it drops at most *slack*
+    ulps above it: a near-tie that another f32 summation order settles the other
+    way.  A difference past the slack is not followed and is reported.
+    -> (index sets [B][k] i64, rows followed bool [B], rows past the slack bool [B])"""
+    B = rlog.shape[0]
+    r = rlog.float()
+    kth = r.sort(dim=-1, descending=True).values[:, k - 1]
+    ulp = torch.exp2(torch.floor(torch.log2(kth.abs().clamp(min=2.0 ** -126))) - 7)
+    out = own.clone().long()
+    followed = torch.zeros(B, dtype=torch.bool)
+    far = torch.zeros(B, dtype=torch.bool)
+    for b in range(B):
+        mine, theirs = set(own[b].tolist()), set(engine[b].tolist())
+        if mine == theirs:
+            continue
+        lo, hi = kth[b] - slack * ulp[b], kth[b] + slack * ulp[b]
+        if (all(r[b, j] >= lo for j in theirs - mine)
+                and all(r[b, j] <= hi for j in mine - theirs)):
+            followed[b] = True
+            out[b] = torch.tensor(sorted(theirs), dtype=torch.long)
+        else:
+            far[b] = True
+    return out, followed, far
+
+
 # ---------------------------------------------------------------------------
 # Experts (a18, a22)
 # ---------------------------------------------------------------------------
@@ -442,10 +493,18 @@ class Qwen35Oracle:
         #: and (k+1)-th router logit, in bf16 ulps of the k-th (a gap of an ulp or
         #: two may pick another expert under any other summation order)
         self.route_gaps: list[torch.Tensor] = []
+        #: per step, per sequence: the layers whose routing followed the engine's
+        #: at a near-tie, and those whose engine set lay past the slack
+        self.route_followed: list[torch.Tensor] = []
+        self.route_far: list[torch.Tensor] = []
 
-    def step(self, tokens, positions) -> torch.Tensor:
-        """One token per sequence at `positions` -> bf16-valued f32 logits [B][V]."""
+    def step(self, tokens, positions, routes=None) -> torch.Tensor:
+        """One token per sequence at `positions` -> bf16-valued f32 logits [B][V].
+        *routes*: the engine's top-k indices of this step [layers][B][k], followed
+        at near-ties (follow_near_ties)."""
         c, B = self.cfg, self.B
+        nfol = torch.zeros(B, dtype=torch.int64)
+        nfar = torch.zeros(B, dtype=torch.int64)
         hidden = self.w["embed"][torch.tensor(tokens)].float()
         pos = torch.tensor(positions)
         for i in range(c.layers):
@@ -476,11 +535,19 @@ class Qwen35Oracle:
             gap = (srt[:, c.top_k - 1] - srt[:, c.top_k]) / torch.exp2(torch.floor(torch.log2(kth)) - 7)
             gaps = gap if i == 0 else torch.minimum(gaps, gap)
             rw, ridx = route_softmax_topk(rlog, c.top_k)
+            if routes is not None:
+                use, fol, far = follow_near_ties(rlog, ridx, routes[i], c.top_k)
+                if fol.any():
+                    rw, ridx = route_softmax_over(rlog, use)
+                nfol += fol
+                nfar += far
             IS = c.shared_inter
             hidden = hidden + moe_c4(xm, rw, ridx, W("w_gate"), W("w_up"), W("w_down"),
                                      W("w_shared_in")[:IS], W("w_shared_in")[IS:],
                                      W("w_shared_out"), W("w_shared_scale")[None])
         self.route_gaps.append(gaps)
+        self.route_followed.append(nfol)
+        self.route_far.append(nfar)
         hn = bf(_rms_flat(hidden, self.w["gamma_final"], c.eps))
         return bf(mm_rows(self.w["head"].float(), hn))
 
@@ -524,9 +591,14 @@ class GraniteOracle:
         self.v_past = {i: [torch.zeros(0, c.kv_heads, c.head_dim)] * rows
                        for i in range(c.layers) if c.is_attention(i)}
         self.route_gaps: list[torch.Tensor] = []
+        self.route_followed: list[torch.Tensor] = []
+        self.route_far: list[torch.Tensor] = []
 
-    def step(self, tokens) -> torch.Tensor:
+    def step(self, tokens, routes=None) -> torch.Tensor:
+        """One token per sequence -> logits [B][V]; *routes* as Qwen35Oracle.step."""
         c, B = self.cfg, self.B
+        nfol = torch.zeros(B, dtype=torch.int64)
+        nfar = torch.zeros(B, dtype=torch.int64)
         E, I, H = c.experts, c.moe_inter, c.hidden
         hidden = bf(self.w["embed"][torch.tensor(tokens)].float() * c.embedding_multiplier)
         gaps = None
@@ -558,6 +630,12 @@ class GraniteOracle:
             gap = _route_gap_ulps(rlog, c.top_k)
             gaps = gap if gaps is None else torch.minimum(gaps, gap)
             rw, ridx = route_topk_softmax(rlog, c.top_k)
+            if routes is not None:
+                use, fol, far = follow_near_ties(rlog, ridx, routes[i], c.top_k)
+                if fol.any():
+                    rw, ridx = route_topk_softmax_over(rlog, use)
+                nfol += fol
+                nfar += far
             moe = moe_c5(xm, rw, ridx, W("w_gate").view(E, I, H), W("s_gate").view(E, I),
                          W("w_up").view(E, I, H), W("s_up").view(E, I),
                          W("w_down").view(E, H, I), W("s_down").view(E, H),
@@ -565,5 +643,7 @@ class GraniteOracle:
                          W("w_shared_out_scale"))
             hidden = bf(hidden + bf(moe * c.residual_multiplier))
         self.route_gaps.append(gaps)
+        self.route_followed.append(nfol)
+        self.route_far.append(nfar)
         hn = rms_norm_tf(hidden, self.w["gamma_final"], c.eps)
         return bf(bf(mm_rows(self.w["embed"].float(), hn)) / c.logits_scaling)

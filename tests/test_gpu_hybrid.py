@@ -598,14 +598,20 @@ def _rope_rows(rows, rot, theta):
     return H.bf(emb.cos().float()), H.bf(emb.sin().float())
 
 
+# the last rows reach the C4 workload's depth (a 32-token prompt + 2,048 new
+# tokens: positions up to 2,079) at the engine's 64-position splits, at batch 1
+# and 16
 @pytest.mark.parametrize("pos,split_len", [([0], 128), ([511], 128), ([700], 512),
                                            ([0, 15, 16, 17, 127, 128, 129, 300, 511, 512, 640,
-                                             700, 701, 750, 3, 64], 128)])
+                                             700, 701, 750, 3, 64], 128),
+                                           ([2040], 64), ([2079], 64),
+                                           ([2040 + 3 * i for i in range(13)] + [2078, 2079,
+                                                                                 2047], 64)])
 def test_gqa_decode_c4(gpu_device, pos, split_len):
     """Qwen3.5 full attention: 16 q / 2 kv heads of 256, RoPE on 64 dims."""
     g = torch.Generator().manual_seed(len(pos) * 1000 + pos[0] + split_len)
     B, HQ, HKV, D, rot = len(pos), 16, 2, 256, 64
-    max_pages = 48
+    max_pages = max(48, -(-(max(pos) + 1) // 16))
     qg = H.bf(torch.randn(B, HQ, 2 * D, generator=g))
     k = H.bf(torch.randn(B, HKV, D, generator=g))
     v = H.bf(torch.randn(B, HKV, D, generator=g))
@@ -613,7 +619,7 @@ def test_gqa_decode_c4(gpu_device, pos, split_len):
              for p in pos]
     gq = H.bf(1 + 0.2 * torch.randn(D, generator=g))
     gk = H.bf(1 + 0.2 * torch.randn(D, generator=g))
-    cos, sin = _rope_rows(1024, rot, 1e7)
+    cos, sin = _rope_rows(max(1024, max(pos) + 1), rot, 1e7)
     scale = D ** -0.5
     ldq = HQ * 2 * D + 2 * HKV * D + 8
     qkv = torch.zeros(B, ldq)

@@ -1,19 +1,37 @@
 """The Qwen3.5-style hybrid decode engine (workload C4) against the oracle's
 whole-step composition, on the GPU, at the model's real widths with fewer layers
-(3 gated-DeltaNet + 1 full-attention), 16 experts and a 4,096-token vocabulary so
-the CPU oracle runs in seconds.  Teacher-forced on the engine's own tokens: every
-step's logits within 2e-2 of max |logit| (the workload's bound), and the greedy
-pick equal wherever the oracle's top-2 margin exceeds twice the step's error.
-A sequence whose router saw its k-th and (k+1)-th logits within two bf16 ulps at
-some layer (a near-tie the f32 summation order may settle either way, picking a
-different expert from then on) is held to 1e-1 from that step on."""
+(3 gated-DeltaNet + 1 full-attention) and a 4,096-token vocabulary so the CPU
+oracle runs in seconds: 16 experts, and the workload's 256 (softmax top 8).
+Teacher-forced on the engine's own tokens and, at router near-ties, on its
+routing (tests/_hybrid_steps.py): every step's logits within 2e-2 of max |logit|
+(the workload's bound), the greedy pick equal wherever the oracle's top-2 margin
+exceeds twice the step's error."""
 import pytest
 import torch
 
 from oracle import hybrid_ref as H
+from tests._hybrid_steps import check_steps, feed_of
 from tilefoundry_amd.hybrid.qwen3_5 import Qwen35Config, Qwen35Engine, synthetic_weights
 
 pytestmark = pytest.mark.gpu
+
+
+def _run(dev, cfg, rows, *, seed, prompt_seed, new, small=None):
+    w = synthetic_weights(cfg, seed=seed, device=dev)
+    eng = Qwen35Engine(cfg, w, rows=rows, device=dev, max_steps=64, split_len=16, small=small,
+                       record_routes=True)
+    if small is not None:
+        assert eng.small == small
+    g = torch.Generator().manual_seed(prompt_seed)
+    prompts = [torch.randint(0, cfg.vocab, (3 + b,), generator=g).tolist() for b in range(rows)]
+    tokens, _, logits = eng.generate(prompts, new, record_logits=True)
+    steps = max(len(p) for p in prompts) - 1 + new
+    assert logits.shape[0] == steps
+    feed = feed_of(eng, prompts, steps)
+    assert all(tokens[b] == feed[b][len(p):len(p) + new] for b, p in enumerate(prompts))
+    orc = H.Qwen35Oracle(cfg, {k: v.cpu() for k, v in w.items()}, rows, max_pos=64)
+    return check_steps(orc, lambda t, tok, r: orc.step(tok, [t] * rows, routes=r), logits,
+                       eng.route_history, feed, prompts, 2e-2)
 
 
 @pytest.mark.parametrize("small", [True, False], ids=["small", "mfma"])
@@ -22,35 +40,17 @@ def test_qwen35_engine_matches_oracle_steps(gpu_device, rows, small):
     """small: the small-batch kernels (row GEMVs, the delta rule over value
     columns, the two-launch experts); mfma: the batched path at the same rows."""
     cfg = Qwen35Config(layers=4, experts=16, vocab=4096)
-    w = synthetic_weights(cfg, seed=3, device=gpu_device)
-    eng = Qwen35Engine(cfg, w, rows=rows, device=gpu_device, max_steps=64, split_len=16,
-                       small=small)
-    assert eng.small == small
-    g = torch.Generator().manual_seed(rows)
-    prompts = [torch.randint(0, cfg.vocab, (3 + b,), generator=g).tolist() for b in range(rows)]
-    new = 5
-    tokens, _, logits = eng.generate(prompts, new, record_logits=True)
-    wc = {k: v.cpu() for k, v in w.items()}
-    orc = H.Qwen35Oracle(cfg, wc, rows, max_pos=64)
-    steps = max(len(p) for p in prompts) - 1 + new
-    assert logits.shape[0] == steps
-    # the engine's input at step t: prompt token while the prompt lasts, else its
-    # own pick of step t - 1 (recorded at sam[b][t - 1])
-    sam = eng.sam.cpu()
-    feed = [list(p) + sam[b, len(p) - 1:steps].tolist() for b, p in enumerate(prompts)]
-    assert all(tokens[b] == feed[b][len(p):len(p) + new] for b, p in enumerate(prompts))
-    for t in range(steps):
-        want = orc.step([feed[b][t] for b in range(rows)], [t] * rows)
-        got = logits[t]
-        err = (got - want).abs().max(dim=1).values
-        scale = want.abs().max(dim=1).values
-        gaps = torch.stack(orc.route_gaps).min(dim=0).values     # ulps, up to this step
-        print(f"step {t}: rel err {(err / scale).tolist()} route gap (ulps) {gaps.tolist()}")
-        bound = torch.where(gaps <= 2, 1e-1, 2e-2)
-        assert (err <= bound * scale).all(), (t, err, scale, gaps)
-        top2 = want.topk(2, dim=1).values
-        for b in range(rows):
-            if (t >= len(prompts[b]) - 1 and gaps[b] > 2 and
-                    top2[b, 0] - top2[b, 1] > 2 * err[b]):
-                assert int(got[b].argmax()) == int(want[b].argmax()), (t, b)
-                assert feed[b][t + 1] == int(want[b].argmax()), (t, b)
+    _run(gpu_device, cfg, rows, seed=3, prompt_seed=rows, new=5, small=small)
+
+
+@pytest.mark.parametrize("rows", [1, 2])
+def test_qwen35_engine_at_full_expert_width(gpu_device, rows):
+    """The workload's MoE width: 256 experts, softmax top 8 plus the shared
+    expert, over 8 generated steps after the prompt.  At this width the k-th and
+    (k+1)-th router logits are often within an ulp or two, so routing is followed
+    at near-ties many times per run (the count is printed); the logits bound stays
+    the workload's at every step."""
+    cfg = Qwen35Config(layers=4, experts=256, vocab=4096)
+    assert cfg.top_k == 8
+    _, picks, _ = _run(gpu_device, cfg, rows, seed=11, prompt_seed=30 + rows, new=8)
+    assert picks >= rows * 2

@@ -117,6 +117,39 @@ def test_routers_rank_like_brute_force():
             assert idx[b].tolist() == order
 
 
+def test_routers_over_their_own_set_are_the_routers():
+    """Weights over the set a router picked are that router's, bit for bit."""
+    logits = H.bf(_logits(6, 72, 5))
+    for full, over in ((H.route_softmax_topk, H.route_softmax_over),
+                       (H.route_topk_softmax, H.route_topk_softmax_over)):
+        w, idx = full(logits, 8)
+        w2, idx2 = over(logits, idx.flip(-1))          # any order in, router order out
+        assert torch.equal(idx2, idx) and torch.equal(w2, w)
+
+
+def test_follow_near_ties_takes_only_swaps_within_the_slack():
+    """k = 3 over logits with the k-th at 1.0 (bf16 ulp 2^-7): an engine set that
+    swaps the 4th for the 3rd (1 ulp apart) or the 5th (2 ulps) is followed; one
+    that swaps in the 6th (3 ulps) or drops the clear 1st is not."""
+    u = 2.0 ** -7
+    rlog = torch.tensor([[4.0, 2.0, 1.0, 1.0 - u, 1.0 - 2 * u, 1.0 - 3 * u, -1.0]] * 5)
+    own = torch.tensor([[0, 1, 2]] * 5)
+    engine = torch.tensor([[1, 0, 2],          # same set, other order
+                           [0, 1, 3],          # 4th for 3rd: 1 ulp
+                           [4, 0, 1],          # 5th for 3rd: 2 ulps
+                           [0, 1, 5],          # 6th for 3rd: 3 ulps
+                           [3, 1, 2]])         # 4th for the 1st: far above the 3rd
+    use, fol, far = H.follow_near_ties(rlog, own, engine, 3)
+    assert fol.tolist() == [False, True, True, False, False]
+    assert far.tolist() == [False, False, False, True, True]
+    assert use[0].tolist() == [0, 1, 2] and use[3].tolist() == [0, 1, 2]
+    assert sorted(use[1].tolist()) == [0, 1, 3] and sorted(use[2].tolist()) == [0, 1, 4]
+    w, idx = H.route_topk_softmax_over(rlog, use)
+    assert idx[1].tolist() == [0, 1, 3] and idx[2].tolist() == [0, 1, 4]
+    top = torch.softmax(torch.tensor([4.0, 2.0, 1.0 - u]), dim=0)
+    assert torch.equal(w[1], H.bf(top))
+
+
 def _bf_param(module, std, gen):
     with torch.no_grad():
         for p in module.parameters():

@@ -196,7 +196,7 @@ class GraniteEngine:
 
     def __init__(self, cfg: GraniteConfig, weights: dict[str, torch.Tensor], *, rows: int,
                  device: str = "cuda:0", max_steps: int = 1024, page_seed: int = 0,
-                 split_len: int = 256, graph: bool = True):
+                 split_len: int = 256, graph: bool = True, record_routes: bool = False):
         if not 1 <= rows <= 32:
             raise ValueError("rows: 1..32 sequences")
         self.cfg, self.B, self.device = cfg, rows, device
@@ -205,6 +205,13 @@ class GraniteEngine:
         self.split_len = split_len
         self._pack(weights)
         self._buffers(page_seed)
+        # record_routes: each layer's top-k expert indices are copied into
+        # routes[layer] as the step runs (a device copy inside the step's graph);
+        # generate() keeps one [layers][rows][k] snapshot per step in
+        # route_history, for tests that follow the engine's routing at near-ties
+        self.routes = (torch.zeros(cfg.layers, rows, cfg.top_k, dtype=I32, device=device)
+                       if record_routes else None)
+        self.route_history = None
         self.graphs = None
         self._cur = 0
         if graph:
@@ -380,6 +387,8 @@ class GraniteEngine:
         self._gemm8(self.xn, w["w_router"], w["w_router_scale"], H, cfg.experts,
                     _lib.EPI_LOGITS, self.rlog, cfg.experts, s)
         self._moe(w, s)                    # routes inside the call, adds into the stream
+        if self.routes is not None:
+            self.routes[i].copy_(self.ridx)
 
     def _step(self, cur):
         s = self._stream()
@@ -490,20 +499,27 @@ class GraniteEngine:
         self._load_prompts(prompts)
         steps = longest - 1 + max_new
         hist = [] if record_logits else None
+        rhist = [] if self.routes is not None else None
         torch.cuda.synchronize(self.device)
         for _ in range(longest - 1):
             self.replay()
             if hist is not None:
                 hist.append(self.logits.clone())
+            if rhist is not None:
+                rhist.append(self.routes.clone())
         torch.cuda.synchronize(self.device)
         t0 = perf_counter()
         for _ in range(longest - 1, steps):
             self.replay()
             if hist is not None:
                 hist.append(self.logits.clone())
+            if rhist is not None:
+                rhist.append(self.routes.clone())
         torch.cuda.synchronize(self.device)
         seconds = perf_counter() - t0
         self.check_errors()
+        if rhist is not None:
+            self.route_history = torch.stack(rhist).cpu()
         sam = self.sam.cpu()
         tokens = [sam[b, len(p) - 1: len(p) - 1 + max_new].tolist()
                   for b, p in enumerate(prompts)]
