@@ -11,9 +11,9 @@ steps are exact bf16 ties; there f32 summation order decides the pick, so a
 step may differ only where the recorded margin is within the measured logit
 error.
 
-Logits at steps 0 and 63 are held against the exact-sum evaluation of the same
-HIR (c2_*_exact_step*.npy: every matmul and attention sum in f64, rounded where
-the HIR rounds).  The oracle's own f32 sums sit `noise` away from it
+Logits at steps 0, 8, 16, ..., 56 and 63 are held against the exact-sum
+evaluation of the same HIR (c2_*_exact_steps.npz, c2_*_exact_step{0,63}.npy:
+every matmul and attention sum in f64, rounded where the HIR rounds).  The oracle's own f32 sums sit `noise` away from it
 (c2_order_noise.json); at 28 layers with unit norm scales that is 2.5% of the
 largest logit, above the 2e-2 bar, because every layer's bf16 roundings
 amplify one-ulp flips.  So the bound is max(2e-2 * max|logit|, 2 * noise): the
@@ -63,6 +63,7 @@ def test_c2_full_depth_against_golden(gpu_device, norms):
         print(f"[golden] norms={norms} mode={mode}", flush=True)
 
         # full logits of steps 0 and 63 (teacher-forced on the golden tokens)
+        # against the exact sums and the oracle's f32 ones
         noise_max = 0.0
         for k in (0, STEPS - 1):
             ref = _golden_logits(norms, k)
@@ -76,6 +77,24 @@ def test_c2_full_depth_against_golden(gpu_device, norms):
             print(f"  step {k}: max|engine-exact| {err_exact:.4g}, max|oracle-exact| {noise:.4g}, "
                   f"max|engine-oracle| {err_oracle:.4g}; bound {bound:.4g}", flush=True)
             assert err_exact <= bound, (mode, k, err_exact, bound)
+        # every 8th step against the exact sums, the bound as above with the
+        # oracle's noise of steps 0 and 63
+        with np.load(GOLDEN / f"c2_{norms}_exact_steps.npz") as z:
+            exact_steps = {int(n[4:]): torch.from_numpy(z[n].astype(np.int16))
+                           .view(torch.bfloat16).float() for n in z.files}
+        for k in sorted(exact_steps):
+            exact = exact_steps[k]
+            got = eng.logits_for(prompt + gold["tokens"][:k]).float().cpu()
+            err = float((got - exact).abs().max())
+            scale = float(exact.abs().max())
+            bound = max(TOL * scale, 2 * noise_max)
+            same = int(got.argmax()) == int(exact.argmax())
+            print(f"  exact step {k:2d}: max|engine-exact| {err:.4g} = {err / scale:.4f} of "
+                  f"max|logit| {scale:.4g}; bound {bound:.4g}; argmax equal {same}", flush=True)
+            assert err <= bound, (mode, k, err, bound)
+            # a different argmax only where the exact top logit and the
+            # engine's pick are within twice the measured error
+            assert same or float(exact.max() - exact[int(got.argmax())]) <= 2 * err, (mode, k)
 
         # teacher-forced: every step's pick and its top-8 logits.  A pick that
         # differs from the golden one is allowed only where the golden gap
