@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TFD_ABI_VERSION 14
+#define TFD_ABI_VERSION 15
 
 /* gemv prologues / epilogues */
 #define TFD_PRO_PLAIN 0  /* x used as given */

@@ -136,6 +136,19 @@ typedef struct {
 } TfdMoeArgs;
 int tfd_moe_experts(const TfdMoeArgs* args, void* stream);
 
+/* tfd_moe_experts over packed weights for rows <= 16, on the matrix cores, in
+ * three launches (routing + grouping, gate/up, down + mix); same arguments and
+ * outputs (partial is not used and may be NULL).  Each weight matrix is packed
+ * as tfd_pack_skinny_bf16 / tfd_pack_skinny_fp8 pack a [rows][K] matrix, the
+ * experts' matrices stacked: w_gate and w_up as one [E I][H] matrix each, w_down
+ * as [E H][I], w_shared_in as [2 IS][H], w_shared_out as [H][IS]; the row scales
+ * keep their order.  Needs k <= 16, H a multiple of 1024, I and IS multiples of
+ * 256, IS <= 2048 and rows (k + 1) I / 256 <= 1024 (kBadShape otherwise).  The
+ * sums of the products run in another order than tfd_moe_experts' (MFMA
+ * accumulators over K instead of lane sums), so results agree to the f32
+ * rounding of each sum before its bf16 rounding. */
+int tfd_moe_experts_packed(const TfdMoeArgs* args, void* stream);
+
 /* Gated DeltaNet at one token per sequence, everything between the in- and
  * out-projections of Qwen3_5LinearAttention.linear_attention: conv_step,
  * l2_normalise, beta/g, delta_step and the gated RMS norm

@@ -132,7 +132,8 @@ def follow_near_ties(rlog: torch.Tensor, own: torch.Tensor, engine: torch.Tensor
     (of the k-th logit) below the k-th, and every expert it drops at most *slack*
     ulps above it: a near-tie that another f32 summation order settles the other
     way.  A difference past the slack is not followed and is reported.
-    -> (index sets [B][k] i64, rows followed bool [B], rows past the slack bool [B])"""
+    -> (index sets [B][k] i64, rows followed bool [B], rows past the slack bool [B],
+    the largest distance of a swapped expert from the k-th logit in its ulps [B])"""
     B = rlog.shape[0]
     r = rlog.float()
     kth = r.sort(dim=-1, descending=True).values[:, k - 1]
@@ -140,18 +141,20 @@ def follow_near_ties(rlog: torch.Tensor, own: torch.Tensor, engine: torch.Tensor
     out = own.clone().long()
     followed = torch.zeros(B, dtype=torch.bool)
     far = torch.zeros(B, dtype=torch.bool)
+    dist = torch.zeros(B)
     for b in range(B):
         mine, theirs = set(own[b].tolist()), set(engine[b].tolist())
         if mine == theirs:
             continue
-        lo, hi = kth[b] - slack * ulp[b], kth[b] + slack * ulp[b]
-        if (all(r[b, j] >= lo for j in theirs - mine)
-                and all(r[b, j] <= hi for j in mine - theirs)):
+        swapped = [float(kth[b] - r[b, j]) for j in theirs - mine] + \
+            [float(r[b, j] - kth[b]) for j in mine - theirs]
+        dist[b] = max(swapped) / float(ulp[b])
+        if dist[b] <= slack:
             followed[b] = True
             out[b] = torch.tensor(sorted(theirs), dtype=torch.long)
         else:
             far[b] = True
-    return out, followed, far
+    return out, followed, far, dist
 
 
 # ---------------------------------------------------------------------------
@@ -497,6 +500,10 @@ class Qwen35Oracle:
         #: at a near-tie, and those whose engine set lay past the slack
         self.route_followed: list[torch.Tensor] = []
         self.route_far: list[torch.Tensor] = []
+        #: per step, per sequence: the widest swap of the engine's routing, in
+        #: ulps of the k-th logit, and the widest followed (follow_near_ties)
+        self.route_dist: list[torch.Tensor] = []
+        self.route_slack = 2.0
 
     def step(self, tokens, positions, routes=None) -> torch.Tensor:
         """One token per sequence at `positions` -> bf16-valued f32 logits [B][V].
@@ -505,6 +512,7 @@ class Qwen35Oracle:
         c, B = self.cfg, self.B
         nfol = torch.zeros(B, dtype=torch.int64)
         nfar = torch.zeros(B, dtype=torch.int64)
+        ndist = torch.zeros(B)
         hidden = self.w["embed"][torch.tensor(tokens)].float()
         pos = torch.tensor(positions)
         for i in range(c.layers):
@@ -536,11 +544,13 @@ class Qwen35Oracle:
             gaps = gap if i == 0 else torch.minimum(gaps, gap)
             rw, ridx = route_softmax_topk(rlog, c.top_k)
             if routes is not None:
-                use, fol, far = follow_near_ties(rlog, ridx, routes[i], c.top_k)
+                use, fol, far, dist = follow_near_ties(rlog, ridx, routes[i], c.top_k,
+                                                       self.route_slack)
                 if fol.any():
                     rw, ridx = route_softmax_over(rlog, use)
                 nfol += fol
                 nfar += far
+                ndist = torch.maximum(ndist, dist)
             IS = c.shared_inter
             hidden = hidden + moe_c4(xm, rw, ridx, W("w_gate"), W("w_up"), W("w_down"),
                                      W("w_shared_in")[:IS], W("w_shared_in")[IS:],
@@ -548,6 +558,7 @@ class Qwen35Oracle:
         self.route_gaps.append(gaps)
         self.route_followed.append(nfol)
         self.route_far.append(nfar)
+        self.route_dist.append(ndist)
         hn = bf(_rms_flat(hidden, self.w["gamma_final"], c.eps))
         return bf(mm_rows(self.w["head"].float(), hn))
 
@@ -593,12 +604,17 @@ class GraniteOracle:
         self.route_gaps: list[torch.Tensor] = []
         self.route_followed: list[torch.Tensor] = []
         self.route_far: list[torch.Tensor] = []
+        #: per step, per sequence: the widest swap of the engine's routing, in
+        #: ulps of the k-th logit, and the widest followed (follow_near_ties)
+        self.route_dist: list[torch.Tensor] = []
+        self.route_slack = 2.0
 
     def step(self, tokens, routes=None) -> torch.Tensor:
         """One token per sequence -> logits [B][V]; *routes* as Qwen35Oracle.step."""
         c, B = self.cfg, self.B
         nfol = torch.zeros(B, dtype=torch.int64)
         nfar = torch.zeros(B, dtype=torch.int64)
+        ndist = torch.zeros(B)
         E, I, H = c.experts, c.moe_inter, c.hidden
         hidden = bf(self.w["embed"][torch.tensor(tokens)].float() * c.embedding_multiplier)
         gaps = None
@@ -631,11 +647,13 @@ class GraniteOracle:
             gaps = gap if gaps is None else torch.minimum(gaps, gap)
             rw, ridx = route_topk_softmax(rlog, c.top_k)
             if routes is not None:
-                use, fol, far = follow_near_ties(rlog, ridx, routes[i], c.top_k)
+                use, fol, far, dist = follow_near_ties(rlog, ridx, routes[i], c.top_k,
+                                                       self.route_slack)
                 if fol.any():
                     rw, ridx = route_topk_softmax_over(rlog, use)
                 nfol += fol
                 nfar += far
+                ndist = torch.maximum(ndist, dist)
             moe = moe_c5(xm, rw, ridx, W("w_gate").view(E, I, H), W("s_gate").view(E, I),
                          W("w_up").view(E, I, H), W("s_up").view(E, I),
                          W("w_down").view(E, H, I), W("s_down").view(E, H),
@@ -645,5 +663,6 @@ class GraniteOracle:
         self.route_gaps.append(gaps)
         self.route_followed.append(nfol)
         self.route_far.append(nfar)
+        self.route_dist.append(ndist)
         hn = rms_norm_tf(hidden, self.w["gamma_final"], c.eps)
         return bf(bf(mm_rows(self.w["embed"].float(), hn)) / c.logits_scaling)

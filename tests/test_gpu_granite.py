@@ -5,7 +5,12 @@ GPU, at the model's real widths with three layers (Mamba2, GQA, Mamba2) and a
 and the workload's 72 (top 10) at batch 1 and 8.  Teacher-forced on the engine's
 own tokens and, at router near-ties, on its routing (tests/_hybrid_steps.py):
 every step's logits within 5e-2 of max |logit| (the workload's fp8 bound), greedy
-picks equal where the oracle's top-2 margin exceeds twice the step's error."""
+picks equal where the oracle's top-2 margin exceeds twice the step's error.
+C5's residual stream is bf16 with every op rounded (the HIR policy), so the
+engine's router inputs sit a bf16 ulp from the oracle's wherever a rounding went
+the other way; a router logit, a 4,096-long sum of them, then moves by up to a
+few ulps, and routing is followed for swaps within 4 ulps of the k-th logit (2
+for C4's f32 stream).  The widest swap of each run is printed."""
 import pytest
 import torch
 
@@ -26,6 +31,7 @@ def _run(dev, cfg, rows, *, seed, prompts, new):
     feed = feed_of(eng, prompts, steps)
     assert all(tokens[b] == feed[b][len(p):len(p) + new] for b, p in enumerate(prompts))
     orc = H.GraniteOracle(cfg, {k: v.cpu() for k, v in w.items()}, rows)
+    orc.route_slack = 4.0
     return check_steps(orc, lambda t, tok, r: orc.step(tok, routes=r), logits,
                        eng.route_history, feed, prompts, 5e-2)
 

@@ -250,10 +250,22 @@ def test_route_rejects_bad_shapes(gpu_device):
 # ---------------------------------------------------------------------------
 # MoE experts
 # ---------------------------------------------------------------------------
+def _pack_rows(w):
+    """A [rows][K] weight matrix packed as the skinny GEMMs pack it (bf16 or fp8
+    codes), on the GPU."""
+    w = w.to("cuda:0").contiguous()
+    N, K = w.shape
+    out = torch.empty(-(-N // 16) * 16 * K, dtype=w.dtype, device=w.device)
+    fn = lib().tfd_pack_skinny_fp8 if w.dtype == torch.uint8 else lib().tfd_pack_skinny_bf16
+    fn(ptr(w), K, N, K, ptr(out), _stream())
+    return out
+
+
 def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w_sscale=None,
-              fp8=False, policy, expect_err=0, route=None, resid=None):
+              fp8=False, policy, expect_err=0, route=None, resid=None, packed=False):
     """resid = (stream, multiplier): the call adds its scaled output into a copy of
-    the bf16 stream, which is returned instead of `out`."""
+    the bf16 stream, which is returned instead of `out`.  packed: the weights
+    packed and tfd_moe_experts_packed called (no partials)."""
     dev = "cuda:0"
     rows, hs = x.shape
     k = idx.shape[1]
@@ -276,13 +288,18 @@ def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w
     err = torch.zeros(1, dtype=torch.int32, device=dev)
     a = _lib.TfdMoeArgs()
     a.x, a.weights, a.idx = d(x.to(BF)), d(weights.float()), d(idx.to(torch.int32))
+    if packed:
+        w_gate, w_up = w_gate.reshape(-1, hs), w_up.reshape(-1, hs)
+        w_down = w_down.reshape(-1, inter)
+        w_gate, w_up, w_down, w_sin, w_sout = (_pack_rows(w) for w in
+                                               (w_gate, w_up, w_down, w_sin, w_sout))
     a.w_gate, a.w_up, a.w_down = d(w_gate), d(w_up), d(w_down)
     a.w_shared_in, a.w_shared_out = d(w_sin), d(w_sout)
     if fp8:
         a.s_gate, a.s_up, a.s_down, a.s_shared_in, a.s_shared_out = [d(v) for v in s]
     a.w_shared_scale = None if w_sscale is None else d(w_sscale)
     a.hidden, a.shared_scale, a.out = ptr(hidden), ptr(sscale), ptr(out)
-    a.partial, a.groups = ptr(partial), ptr(groups)
+    a.partial, a.groups = (None if packed else ptr(partial)), ptr(groups)
     a.rows, a.k, a.experts, a.hidden_size = rows, k, experts, hs
     a.inter, a.shared_inter, a.hidden_ld = inter, sh, ld
     a.fp8, a.policy, a.err = int(fp8), policy, ptr(err)
@@ -292,7 +309,8 @@ def _moe_call(x, weights, idx, *, w_gate, w_up, w_down, w_sin, w_sout, s=None, w
     if resid is not None:
         stream = resid[0].to(dev, BF).contiguous()
         a.out, a.resid, a.resid_mult = None, ptr(stream), resid[1]
-    lib().tfd_moe_experts(ctypes.addressof(a), _stream())
+    (lib().tfd_moe_experts_packed if packed else lib().tfd_moe_experts)(ctypes.addressof(a),
+                                                                         _stream())
     torch.cuda.synchronize()
     if route is not None:
         idx = keep[2].cpu()                  # the call wrote the ids
@@ -397,6 +415,92 @@ def test_moe_experts_c5_fp8(gpu_device, rows):
                       s=(gs, us, ds, sis, sos), fp8=True, policy=_lib.POLICY_BF16,
                       resid=(h, 0.22))
     assert torch.equal(added, h + got.to(BF) * 0.22)
+
+
+def _packed_vs_rowmajor(got, ref, name, f32=False):
+    """The packed entry's sums run in another order (MFMA accumulators over K):
+    with bf16 outputs they equal the row-major entry's up to a one-ulp flip of a
+    bf16 rounding, and only rarely; with the f32 policy an output is an f32 sum
+    of bf16-rounded slot values, so a flip in any slot moves it by about a bf16
+    ulp of that slot -- held within 2^-8 of the largest output."""
+    d = (got - ref).abs()
+    flips = int((d > 0).sum())
+    rel = float(d.max() / ref.abs().max())
+    print(f"{name}: {flips} of {d.numel()} outputs differ from the row-major entry, max "
+          f"{float(d.max()):.4g} ({rel:.2e} of the largest)", flush=True)
+    if f32:
+        assert rel <= 2.0 ** -8, (name, rel)
+    else:
+        assert flips <= max(8, d.numel() // 200), (name, flips)
+
+
+@pytest.mark.parametrize("rows,same", [(1, False), (5, False), (16, False), (16, True)])
+def test_moe_experts_packed_c4_bf16(gpu_device, rows, same):
+    """tfd_moe_experts_packed at the Qwen3.5 widths (H 2048, I 512, shared 512, top
+    8, shared-expert gate, f32 policy, accumulate off), against the oracle and
+    the row-major entry."""
+    g = torch.Generator().manual_seed(300 + rows + 100 * same)
+    hs, inter, sh, E, k = 2048, 512, 512, 16, 8
+    rnd = lambda *s, std=0.03: H.bf(torch.randn(*s, generator=g) * std)
+    x = rnd(rows, hs, std=1.0)
+    weights, idx = _routing(rows, E, k, g)
+    if same:
+        idx = idx[:1].repeat(rows, 1)
+    w_gate, w_up, w_down = rnd(E, inter, hs), rnd(E, inter, hs), rnd(E, hs, inter)
+    ws_gate, ws_up, ws_down, ws_scale = rnd(sh, hs), rnd(sh, hs), rnd(hs, sh), rnd(1, hs)
+    kw = dict(w_gate=w_gate.to(BF), w_up=w_up.to(BF), w_down=w_down.to(BF),
+              w_sin=torch.cat([ws_gate, ws_up]).to(BF), w_sout=ws_down.to(BF),
+              w_sscale=ws_scale.to(BF), policy=_lib.POLICY_F32)
+    got = _moe_call(x, weights, idx, packed=True, **kw)
+    want = H.moe_c4(x, weights, idx, w_gate, w_up, w_down, ws_gate, ws_up, ws_down, ws_scale)
+    assert_close_bf16(got, want, max_rel=1e-2, min_cos=0.99999, name="moe c4 packed")
+    _packed_vs_rowmajor(got, _moe_call(x, weights, idx, **kw), "moe c4 packed", f32=True)
+
+
+@pytest.mark.parametrize("rows", [1, 8, 16])
+def test_moe_experts_packed_c5_fp8(gpu_device, rows):
+    """tfd_moe_experts_packed at the Granite workload's widths: H 4096, 72 experts
+    of I 768, shared 1536, top 10, fp8 with row scales, against the oracle and
+    the row-major entry; then routed inside the call (top 10 then softmax) and
+    added into a bf16 stream, against the row-major entry doing the same."""
+    g = torch.Generator().manual_seed(400 + rows)
+    hs, inter, sh, E, k = 4096, 768, 1536, 72, 10
+    x = H.bf(torch.randn(rows, hs, generator=g))
+    weights, idx = _routing(rows, E, k, g)
+    weights = H.bf(weights)
+    sc = lambda *s: torch.rand(*s, generator=g) * 0.004 + 0.002
+    gc, uc, dc = _fp8_codes((E, inter, hs), g), _fp8_codes((E, inter, hs), g), \
+        _fp8_codes((E, hs, inter), g)
+    gs, us, ds = sc(E, inter), sc(E, inter), sc(E, hs)
+    sic, soc = _fp8_codes((2 * sh, hs), g), _fp8_codes((hs, sh), g)
+    sis, sos = sc(2 * sh), sc(hs)
+    kw = dict(w_gate=gc, w_up=uc, w_down=dc, w_sin=sic, w_sout=soc, s=(gs, us, ds, sis, sos),
+              fp8=True, policy=_lib.POLICY_BF16)
+    got = _moe_call(x, weights, idx, packed=True, **kw)
+    want = H.moe_c5(x, weights, idx, gc, gs, uc, us, dc, ds, sic, sis, soc, sos)
+    assert torch.equal(got, got.to(BF).float())
+    assert_close_bf16(got, want, max_rel=2e-2, min_cos=0.9999, name="moe c5 packed")
+    _packed_vs_rowmajor(got, _moe_call(x, weights, idx, **kw), "moe c5 packed")
+    logits = H.bf(torch.randn(rows, E, generator=g))
+    h = H.bf(torch.randn(rows, hs, generator=g)).to(BF)
+    zw, zi = torch.zeros(rows, k), torch.zeros(rows, k, dtype=torch.long)
+    kw.update(route=(logits, _lib.MOE_ROUTE_TOPK_SOFTMAX), resid=(h, 0.22))
+    _packed_vs_rowmajor(_moe_call(x, zw, zi, packed=True, **kw).float(),
+                        _moe_call(x, zw, zi, **kw).float(), "moe c5 packed, routed, resid")
+
+
+def test_moe_experts_packed_rejects_bad_shapes(gpu_device):
+    """More than 16 sequences, a hidden size off the 1024 grid, more than 16
+    experts per sequence: kBadShape before anything is launched."""
+    g = torch.Generator().manual_seed(5)
+    inter, sh, E = 256, 256, 32
+    rnd = lambda *s: torch.randn(*s, generator=g).to(BF)
+    for rows, hs, k in ((17, 1024, 2), (2, 512, 2), (2, 1024, 17)):
+        weights, idx = _routing(rows, E, k, g)
+        with pytest.raises(_lib.TFDError, match="moe_experts_packed"):
+            _moe_call(rnd(rows, hs), weights, idx, w_gate=rnd(E, inter, hs),
+                      w_up=rnd(E, inter, hs), w_down=rnd(E, hs, inter), w_sin=rnd(2 * sh, hs),
+                      w_sout=rnd(hs, sh), policy=_lib.POLICY_BF16, packed=True)
 
 
 # ---------------------------------------------------------------------------

@@ -139,9 +139,10 @@ def test_follow_near_ties_takes_only_swaps_within_the_slack():
                            [4, 0, 1],          # 5th for 3rd: 2 ulps
                            [0, 1, 5],          # 6th for 3rd: 3 ulps
                            [3, 1, 2]])         # 4th for the 1st: far above the 3rd
-    use, fol, far = H.follow_near_ties(rlog, own, engine, 3)
+    use, fol, far, dist = H.follow_near_ties(rlog, own, engine, 3)
     assert fol.tolist() == [False, True, True, False, False]
     assert far.tolist() == [False, False, False, True, True]
+    assert dist.tolist() == [0.0, 1.0, 2.0, 3.0, 384.0]
     assert use[0].tolist() == [0, 1, 2] and use[3].tolist() == [0, 1, 2]
     assert sorted(use[1].tolist()) == [0, 1, 3] and sorted(use[2].tolist()) == [0, 1, 4]
     w, idx = H.route_topk_softmax_over(rlog, use)

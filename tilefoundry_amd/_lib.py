@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS, EPI_RESID_F32 = 0, 1, 2, 3, 4
@@ -35,6 +35,15 @@ POLICY_F32, POLICY_BF16 = 0, 1
 ROWX_NORM_F32, ROWX_GATED_F32, ROWX_OPERAND, ROWX_ROWS = 0, 1, 2, 3
 SMALL_ROWS = 4              # rows of the small-batch entries (tfd_rowgemv_bf16 and the rest)
 MOE_ROUTE_GIVEN, MOE_ROUTE_SOFTMAX_TOPK, MOE_ROUTE_TOPK_SOFTMAX = 0, 1, 2
+
+
+def moe_packed_fits(rows: int, k: int, hidden: int, inter: int, shared_inter: int) -> bool:
+    """Whether tfd_moe_experts_packed takes this shape (its kBadShape check,
+    include/tf_hybrid.h): rows <= 16, k <= 16, H a multiple of 1024, I and IS of
+    256 with IS <= 2048, rows (k + 1) I / 256 <= 1024."""
+    return (rows <= 16 and k <= 16 and hidden % 1024 == 0 and inter % 256 == 0 and
+            shared_inter % 256 == 0 and shared_inter <= 2048 and
+            rows * (k + 1) * (inter // 256) <= 1024)
 
 P = c_void_p
 I = c_int
@@ -75,6 +84,7 @@ SIGNATURES: dict[str, list] = {
     "tfd_gemm_skinny_fp8_resid_scaled": [P, P, P, I, I, I, P, I, F, P, I, P],
     "tfd_route_topk": [P, I, I, I, I, I, P, P, P],
     "tfd_moe_experts": [P, P],
+    "tfd_moe_experts_packed": [P, P],
     "tfd_gdn_step": [P, P],
     "tfd_mamba_step": [P, P],
     "tfd_gqa_decode": [P, P],

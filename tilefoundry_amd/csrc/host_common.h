@@ -18,6 +18,8 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int launched(const char* what);
 // 16-byte chunks per lane (1, 2, 4, 8, 12, 16) for a length-K vector over a wave; 0 if too long.
 int cmax_for(int K);
+// compute units of the current device (256 if the query fails), cached per device
+int compute_units();
 
 }  // namespace tfd_host
 

@@ -16,6 +16,8 @@
 #include "host_common.h"
 #include "tf_hybrid.h"
 
+#include <type_traits>
+
 using namespace tfd;
 using namespace tfd_host;
 using namespace tfd_hybrid;
@@ -336,6 +338,393 @@ __global__ __launch_bounds__(kBlock) void k_moe_mix(MoeArgs a) {
   }
   const float dsh = pb[(int64_t)a.k * a.H];
   const int64_t at = (int64_t)b * a.H + n;
+  if (kF32) {
+    const float y = acc + dsh * (a.w_sscale ? a.sscale[b] : 1.f);
+    a.out[at] = a.accumulate ? a.out[at] + y : y;
+  } else {
+    const float y = rbf(rbf(acc) + dsh);
+    if (a.resid)
+      a.resid[at] = f2bf(bf2f(a.resid[at]) + rbf(y * a.resid_mult));
+    else
+      a.out[at] = y;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Experts for at most 16 sequences, on the matrix cores, over weights packed
+// as the skinny GEMMs pack them (tfd_pack_skinny_bf16 / _fp8 of each [rows][K]
+// matrix, the experts' matrices stacked: expert e's rows e * I ..).  The
+// entries of a group (the sequences that picked its expert) are the rows of
+// one 16-row MFMA tile, rows past the count zero, so each (entry, weight row)
+// sum stays in the accumulators -- no wave sum per pair -- and every weight
+// byte of a picked expert is read once per launch, a wave's load of a 32-wide
+// K step being one contiguous packed block.  fp8 codes are decoded to bf16 in
+// registers, exactly, as in the skinny GEMMs.  The group lists of k_moe_group
+// are staged into LDS first; a wave decodes an item once, when its loads
+// reach it, so a step costs its loads, its decode and its MFMAs.
+//   gate/up  items of 16 gate + 16 up rows of the shared expert or of a picked
+//            one over the whole hidden size, dealt to the blocks in turn; the
+//            four waves of a block split K, their sums meet in LDS (two
+//            buffers, one barrier per item) and one wave, in turn, writes the
+//            SwiGLU of each (entry, row)
+//   down     a block per 16 output columns: its waves take the items in turn --
+//            the shared expert's K halves of the routed width, then the picked
+//            experts -- each a 16-column tile against the hidden vectors of the
+//            item's entries, into LDS; then per sequence the slots are mixed in
+//            slot order and the result goes into the stream, as k_moe_mix does
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8_m __attribute__((ext_vector_type(8)));
+typedef float f32x4_m __attribute__((ext_vector_type(4)));
+constexpr int kM8 = 16;          // entries of a group at most: the tile's rows
+constexpr int kM8Slots = 17;     // k + 1 at most
+constexpr int kM8Depth = 8;      // 32-wide K steps in flight per wave
+
+struct M8Meta {
+  int n;                         // experts picked
+  int picked[kMaxExperts];
+  int count[kMaxExperts];
+  uint16_t ent[kMaxExperts][kM8];   // entry t of expert e: (sequence << 8) | slot
+};
+
+__device__ __forceinline__ void m8_stage(const MoeArgs& a, M8Meta& m) {
+  for (int i = threadIdx.x; i < a.E; i += blockDim.x) {
+    m.picked[i] = grp_picked(a)[i];
+    m.count[i] = grp_count(a)[i];
+  }
+  const int* ent = grp_entries(a);
+  for (int i = threadIdx.x; i < a.E * a.B; i += blockDim.x) {
+    // entries past an expert's count are stale and never read
+    const unsigned v = (unsigned)ent[i];
+    m.ent[i / a.B][i % a.B] = (uint16_t)((((v / a.k) & 0xffu) << 8) | ((v % a.k) & 0xffu));
+  }
+  if (threadIdx.x == 0) m.n = a.groups[0];
+  __syncthreads();
+}
+
+// lane l's B operand of packed block `blk`: W[16 t + l % 16][32 s + 8 (l / 16) .. +7]
+template <bool kFp8>
+struct M8W {
+  using Raw = u32x2;
+  static __device__ __forceinline__ Raw load(const void* w, int64_t blk, int lane) {
+    return __builtin_nontemporal_load(
+        reinterpret_cast<const u32x2*>((const uint8_t*)w + blk * 512 + lane * 8));
+  }
+  static __device__ __forceinline__ bf16x8_m value(const Raw& r) {
+    typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+    const bf16x2_v p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.x, 1.0f, false);
+    const bf16x2_v p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.x, 1.0f, true);
+    const bf16x2_v p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.y, 1.0f, false);
+    const bf16x2_v p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r.y, 1.0f, true);
+    return bf16x8_m{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+  }
+};
+template <>
+struct M8W<false> {
+  using Raw = u32x4;
+  static __device__ __forceinline__ Raw load(const void* w, int64_t blk, int lane) {
+    return load16_stream((const bf16*)w + blk * 512 + lane * 8);
+  }
+  static __device__ __forceinline__ bf16x8_m value(const Raw& r) {
+    return __builtin_bit_cast(bf16x8_m, r);
+  }
+};
+
+// A operands through a buffer descriptor of `bytes` bytes: a lane whose row is
+// past the group's count reads at kM8Off, out of range, which returns zeros
+// without a memory access (the rows of the sequences that did not pick the
+// expert cost nothing)
+constexpr uint32_t kM8Off = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t m8_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  void* u = (void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ bf16x8_m m8_a(const u32x4& x) { return __builtin_bit_cast(bf16x8_m, x); }
+
+template <bool kFp8, bool kF32>
+__global__ __launch_bounds__(kBlock) void k_moe8_gateup(MoeArgs a) {
+  using W = M8W<kFp8>;
+  constexpr int kD = kM8Depth;
+  __shared__ M8Meta meta;
+  __shared__ f32x4_m red[2][kWavesPerBlock][2][kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  if (a.w_sscale && blockIdx.x == gridDim.x - 1 && wave == kWavesPerBlock - 1) {
+    // C4's shared-expert gate, sigmoid(bf16(w . x)) per sequence, summed as
+    // k_moe_gateup sums it
+    for (int b = 0; b < a.B; ++b) {
+      const bf16* xr = a.x + (int64_t)b * a.H;
+      float acc = 0.f;
+      for (int c = lane; c < a.H / 8; c += kWave)
+        acc = dot8(load16(a.w_sscale + (int64_t)c * 8), load16(xr + (int64_t)c * 8), acc);
+      const float d = rbf(wave_sum(acc));
+      if (lane == 0) a.sscale[b] = sigmoid_f(d);
+    }
+  }
+  m8_stage(a, meta);
+  const int nS = a.IS / 16, nT = a.I / 16;
+  const int items = nS + meta.n * nT;
+  const int G = (int)gridDim.x, me = (int)blockIdx.x;
+  if (me >= items) return;
+  const int mine = (items - 1 - me) / G + 1;
+  const int ksteps = a.H / 32;                    // packed blocks per tile
+  const int ns = ksteps / kWavesPerBlock;         // this wave's steps per item (>= kD)
+  const int k0 = wave * ns;                       // this wave's first step
+  const int nl = lane & 15, kq = lane >> 4;       // tile row / A row, K octet of a step
+  // an item as its loads see it: the first packed blocks of its gate and up
+  // rows for this wave, the A row of this lane and its validity
+  struct Item {
+    const void *wg, *wu;
+    int64_t gblk, ublk;
+    uint32_t xo;                                  // this lane's A bytes, or kM8Off
+  };
+  const auto xrs = m8_rsrc(a.x, (uint32_t)a.B * a.H * 2u);
+  auto decode = [&](int j) {
+    const int it = me + j * G;
+    Item d;
+    if (it < nS) {
+      d.wg = a.w_sin;
+      d.wu = a.w_sin;
+      d.gblk = (int64_t)it * ksteps + k0;
+      d.ublk = (int64_t)(nS + it) * ksteps + k0;
+      d.xo = nl < a.B ? ((uint32_t)nl * a.H + k0 * 32 + kq * 8) * 2u : kM8Off;
+    } else {
+      const int r = it - nS, e = meta.picked[r / nT];
+      const int64_t t = (int64_t)e * nT + r % nT;
+      d.wg = a.w_gate;
+      d.wu = a.w_up;
+      d.gblk = t * ksteps + k0;
+      d.ublk = d.gblk;
+      d.xo = nl < meta.count[e]
+                 ? ((uint32_t)(meta.ent[e][nl] >> 8) * a.H + k0 * 32 + kq * 8) * 2u
+                 : kM8Off;
+    }
+    return d;
+  };
+  typename W::Raw gw[kD], uw[kD];
+  u32x4 xs[kD];
+  Item nx = decode(0);
+  int jn = 0, sn = 0;                             // the next step to load
+  auto issue = [&](int u) {
+    gw[u] = W::load(nx.wg, nx.gblk + sn, lane);
+    uw[u] = W::load(nx.wu, nx.ublk + sn, lane);
+    xs[u] = __builtin_amdgcn_raw_buffer_load_b128(xrs, nx.xo + sn * 64u, 0, 0);
+    if (++sn == ns && jn + 1 < mine) {
+      sn = 0;
+      nx = decode(++jn);
+    }
+  };
+  f32x4_m cg = {0.f, 0.f, 0.f, 0.f}, cu = cg;
+  int jc = 0, sc = 0;                             // the step being computed
+  auto compute = [&](int u) {
+    const bf16x8_m x = m8_a(xs[u]);
+    cg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, W::value(gw[u]), cg, 0, 0, 0);
+    cu = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, W::value(uw[u]), cu, 0, 0, 0);
+    if (++sc < ns) return;
+    // item jc done: the four K quarters meet in LDS, one wave writes the rows
+    const int j = jc++;
+    sc = 0;
+    red[j & 1][wave][0][lane] = cg;
+    red[j & 1][wave][1][lane] = cu;
+    cg = f32x4_m{0.f, 0.f, 0.f, 0.f};
+    cu = cg;
+    __syncthreads();
+    if (wave != (j & (kWavesPerBlock - 1))) return;
+    const int it = me + j * G;
+    const bool sh = it < nS;
+    const int r = it - nS, e = sh ? 0 : meta.picked[r / nT];
+    const int cnt = sh ? a.B : meta.count[e];
+    const int row = (sh ? it : r % nT) * 16 + nl;
+    const int64_t grow = sh ? row : (int64_t)e * a.I + row;
+    const int64_t urow = sh ? (int64_t)a.IS + row : grow;
+    float gs = 1.f, us = 1.f;
+    if (kFp8) {
+      gs = sh ? a.s_sin[grow] : a.s_gate[grow];
+      us = sh ? a.s_sin[urow] : a.s_up[urow];
+    }
+    f32x4_m sg = red[j & 1][0][0][lane], su = red[j & 1][0][1][lane];
+#pragma unroll
+    for (int w = 1; w < kWavesPerBlock; ++w) {
+      const f32x4_m vg = red[j & 1][w][0][lane], vu = red[j & 1][w][1][lane];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sg[i] += vg[i];
+        su[i] += vu[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * kq + i;
+      if (m >= cnt) continue;
+      const int bs = sh ? (m << 8) | a.k : meta.ent[e][m];
+      float gv = sg[i], uv = su[i];
+      if (kFp8) {
+        gv *= gs;
+        uv *= us;
+      }
+      gv = rbf(gv);
+      uv = rbf(uv);
+      const float h = kF32 ? silu_f(gv) * uv : rbf(silu_f(gv)) * uv;
+      a.hidden[((int64_t)(bs >> 8) * (a.k + 1) + (bs & 0xff)) * a.IM + row] = f2bf(h);
+    }
+  };
+  const int total = mine * ns;                    // a multiple of kD
+#pragma unroll
+  for (int u = 0; u < kD; ++u) issue(u);
+  int q0 = 0;
+  for (; q0 + kD < total; q0 += kD) {
+#pragma unroll
+    for (int u = 0; u < kD; ++u) {
+      compute(u);
+      issue(u);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kD; ++u) compute(u);
+}
+
+// The down kernel's units: kM8Depth 32-wide steps (256 of K) of one item, so
+// every unit is as long as every other and the waves of a block finish
+// together; each unit's sums have their own place in LDS and the mix adds a
+// slot's units in K order.
+constexpr int kM8Unit = 32 * kM8Depth;
+constexpr int kM8Parts = 1024;       // (sequence, slot, unit) sums of the routed experts
+constexpr int kM8SharedUnits = 8;    // units of the shared expert's width
+
+template <bool kFp8, bool kF32, int kWv, int kD = kM8Depth>
+__global__ __launch_bounds__(kWv * kWave) void k_moe8_down(MoeArgs a) {
+  using W = M8W<kFp8>;
+  constexpr int kUnit = 32 * kD;                  // K of a unit
+  __shared__ M8Meta meta;
+  __shared__ float part[kM8Parts * 16];              // [sequence][slot][unit][column]
+  __shared__ float shp[kM8SharedUnits * kM8 * 16];   // [unit][sequence][column]
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int nl = lane & 15, kq = lane >> 4;
+  const int ct = (int)blockIdx.x;                 // 16-column tile of the output
+  const int uS = a.IS / kUnit, uR = a.I / kUnit;
+  struct Unit {
+    const void* w;
+    int64_t blk;
+    uint32_t ho;                                  // this lane's A bytes, or kM8Off
+  };
+  const auto hrs = m8_rsrc(a.hidden, (uint32_t)a.B * (a.k + 1) * a.IM * 2u);
+  auto decode = [&](int j) {
+    const int u = wave + j * kWv;
+    Unit d;
+    if (u < uS) {
+      d.w = a.w_sout;
+      d.blk = (int64_t)ct * (a.IS / 32) + u * kD;
+      d.ho = nl < a.B ? (((uint32_t)nl * (a.k + 1) + a.k) * a.IM + u * kUnit + kq * 8) * 2u
+                      : kM8Off;
+    } else {
+      const int r = u - uS, e = meta.picked[r / uR], pt = r % uR;
+      d.w = a.w_down;
+      d.blk = ((int64_t)e * (a.H / 16) + ct) * (a.I / 32) + pt * kD;
+      const int bs = meta.ent[e][nl];
+      d.ho = nl < meta.count[e] ? (((uint32_t)(bs >> 8) * (a.k + 1) + (bs & 0xff)) * a.IM +
+                                   pt * kUnit + kq * 8) * 2u
+                                : kM8Off;
+    }
+    return d;
+  };
+  typename W::Raw dw[kD];
+  u32x4 xs[kD];
+  auto issue = [&](const Unit& d) {
+#pragma unroll
+    for (int t = 0; t < kD; ++t) {
+      dw[t] = W::load(d.w, d.blk + t, lane);
+      xs[t] = __builtin_amdgcn_raw_buffer_load_b128(hrs, d.ho + t * 64u, 0, 0);
+    }
+  };
+  // a wave whose first unit is the shared expert's needs no group list for
+  // it: its loads go out before the lists are staged
+  const bool early = wave < uS;
+  Unit first;
+  if (early) {
+    first = decode(0);
+    issue(first);
+  }
+  m8_stage(a, meta);
+  const int nU = uS + meta.n * uR;
+  const int mine = wave < nU ? (nU - 1 - wave) / kWv + 1 : 0;
+  // the mix threads' slot weights and row scales, requested now and used at
+  // the end
+  const int t = threadIdx.x;
+  const bool mixer = t < a.B * 16;
+  const int b = mixer ? t / 16 : 0, n = t % 16, col = ct * 16 + n;
+  float wslot[kM8Slots - 1], sslot[kM8Slots - 1];
+#pragma unroll
+  for (int s = 0; s < kM8Slots - 1; ++s) {
+    const int ss = s < a.k ? s : 0;
+    wslot[s] = a.weights[(int64_t)b * a.k + ss];
+    if (kFp8) {
+      // an id out of range is served as expert 0, as k_moe_group groups it
+      const int e = a.idx[(int64_t)b * a.k + ss];
+      sslot[s] = a.s_down[(int64_t)((unsigned)e < (unsigned)a.E ? e : 0) * a.H + col];
+    } else {
+      sslot[s] = 1.f;
+    }
+  }
+  const float s_sh = kFp8 ? a.s_sout[col] : 1.f;
+  // unit j's steps, each slot refilled with the next unit's step right after
+  // its use (the last unit has none: a separate copy, so no branch sits
+  // between a load and its use)
+  auto unit = [&](int j, const Unit& nx, auto refill) {
+    f32x4_m c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < kD; ++t) {
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(m8_a(xs[t]), W::value(dw[t]), c, 0, 0, 0);
+      if (decltype(refill)::value) {
+        dw[t] = W::load(nx.w, nx.blk + t, lane);
+        xs[t] = __builtin_amdgcn_raw_buffer_load_b128(hrs, nx.ho + t * 64u, 0, 0);
+      }
+    }
+    const int u = wave + j * kWv;
+    const bool sh = u < uS;
+    const int r = u - uS, e = sh ? 0 : meta.picked[r / uR], pt = sh ? 0 : r % uR;
+    const int cnt = sh ? a.B : meta.count[e];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 4 * kq + i;
+      if (m >= cnt) continue;
+      if (sh) {
+        shp[(u * kM8 + m) * 16 + nl] = c[i];
+      } else {
+        const int bs = meta.ent[e][m];
+        part[(((bs >> 8) * (a.k + 1) + (bs & 0xff)) * uR + pt) * 16 + nl] = c[i];
+      }
+    }
+  };
+  if (mine > 0) {
+    if (!early) {
+      first = decode(0);
+      issue(first);
+    }
+    for (int j = 0; j + 1 < mine; ++j) unit(j, decode(j + 1), std::true_type{});
+    unit(mine - 1, first, std::false_type{});
+  }
+  __syncthreads();
+  // mix, as k_moe_down's rounding and k_moe_mix: each slot's units in K order,
+  // times its row scale, rounded to bf16; the slots in slot order, then the
+  // shared expert
+  if (!mixer) return;
+  float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < kM8Slots - 1; ++s) {
+    if (s >= a.k) break;
+    const float* ps = part + ((b * (a.k + 1) + s) * uR) * 16 + n;
+    float raw = ps[0];
+    for (int pt = 1; pt < uR; ++pt) raw += ps[pt * 16];
+    const float d = rbf(kFp8 ? raw * sslot[s] : raw);
+    acc += kF32 ? d * wslot[s] : rbf(d * wslot[s]);
+  }
+  float sraw = shp[b * 16 + n];
+  for (int u = 1; u < uS; ++u) sraw += shp[(u * kM8 + b) * 16 + n];
+  const float dsh = rbf(kFp8 ? sraw * s_sh : sraw);
+  const int64_t at = (int64_t)b * a.H + col;
   if (kF32) {
     const float y = acc + dsh * (a.w_sscale ? a.sscale[b] : 1.f);
     a.out[at] = a.accumulate ? a.out[at] + y : y;
@@ -717,17 +1106,60 @@ int launch_moe_down(const MoeArgs& a, int width, int ny, hipStream_t s) {
   return 0;
 }
 
-template <bool kFp8, bool kF32>
-int launch_moe(const MoeArgs& a, hipStream_t s) {
-  // picked experts at most min(E, B k), plus the shared one
-  const int np = a.E < a.B * a.k ? a.E : a.B * a.k;
-  const dim3 g3((a.H + kBlock - 1) / kBlock, a.B);
+// the matrix-core expert pair's limits: a group fits one 16-row tile, a wave's
+// share of K in the gate/up (a quarter of the hidden size) is a whole number of
+// kM8Depth 32-wide steps, both expert widths are whole numbers of the down's
+// units, and the down's unit sums fit its LDS
+bool moe8_fits(const MoeArgs& a) {
+  return a.B <= kM8 && a.k + 1 <= kM8Slots && a.E <= kMaxExperts &&
+         a.H % (32 * kWavesPerBlock * kM8Depth) == 0 && a.I % kM8Unit == 0 &&
+         a.IS % kM8Unit == 0 && a.IS / kM8Unit <= kM8SharedUnits &&
+         a.B * (a.k + 1) * (a.I / kM8Unit) <= kM8Parts;
+}
+
+// route (when asked) and group the entries by expert
+void launch_group(const MoeArgs& a, hipStream_t s) {
   if (a.route == TFD_ROUTE_SOFTMAX_TOPK)
     hipLaunchKernelGGL((k_moe_group<0>), dim3(1), dim3(kGroupThreads), 0, s, a);
   else if (a.route == TFD_ROUTE_TOPK_SOFTMAX)
     hipLaunchKernelGGL((k_moe_group<1>), dim3(1), dim3(kGroupThreads), 0, s, a);
   else
     hipLaunchKernelGGL((k_moe_group<-1>), dim3(1), dim3(kGroupThreads), 0, s, a);
+}
+
+// packed weights, at most 16 sequences: group, gate/up, down + mix
+template <bool kFp8, bool kF32>
+int launch_moe8(const MoeArgs& a, hipStream_t s) {
+  const int np = a.E < a.B * a.k ? a.E : a.B * a.k;
+  const int items = a.IS / 16 + np * (a.I / 16);
+  // as many gate/up blocks as are resident at once (one round, no tail)
+  static int per_cu[2][2] = {{0, 0}, {0, 0}};
+  int& pc = per_cu[kFp8][kF32];
+  if (!pc && (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                  &pc, reinterpret_cast<const void*>(&k_moe8_gateup<kFp8, kF32>), kBlock, 0) !=
+                  hipSuccess ||
+              pc <= 0))
+    pc = 2;
+  const int cap = pc * compute_units();
+  launch_group(a, s);
+  hipLaunchKernelGGL((k_moe8_gateup<kFp8, kF32>), dim3(items < cap ? items : cap), dim3(kBlock),
+                     0, s, a);
+  // whole 768-wide experts as units (C5's width) measured 5% faster than
+  // 256-wide units over 16 waves
+  if (a.I % 768 == 0 && a.IS % 768 == 0 && a.IS / 768 <= kM8SharedUnits)
+    hipLaunchKernelGGL((k_moe8_down<kFp8, kF32, 8, 24>), dim3(a.H / 16), dim3(8 * kWave), 0, s,
+                       a);
+  else
+    hipLaunchKernelGGL((k_moe8_down<kFp8, kF32, 16>), dim3(a.H / 16), dim3(16 * kWave), 0, s, a);
+  return launched("moe_experts_packed");
+}
+
+template <bool kFp8, bool kF32>
+int launch_moe(const MoeArgs& a, hipStream_t s) {
+  // picked experts at most min(E, B k), plus the shared one
+  const int np = a.E < a.B * a.k ? a.E : a.B * a.k;
+  const dim3 g3((a.H + kBlock - 1) / kBlock, a.B);
+  launch_group(a, s);
   // gate/up in one launch; the down projections in one launch when the shared
   // expert is as wide as the routed ones, else one for each width (a lane's
   // chunk registers are sized by the width)
@@ -761,22 +1193,27 @@ int tfd_route_topk(const float* logits, int ldl, int rows, int experts, int k, i
   return launched("route_topk");
 }
 
-int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
-  if (!args) return fail(kBadArg, "moe_experts: null args");
+}  // extern "C"
+
+namespace {
+
+// the checks and the device-side arguments shared by the two expert entries
+// (the packed one keeps no partials)
+int moe_args(const TfdMoeArgs* args, bool partials, const char* who, MoeArgs& a) {
+  if (!args) return fail(kBadArg, "%s: null args", who);
   const TfdMoeArgs& t = *args;
   if (!t.x || !t.weights || !t.idx || !t.w_gate || !t.w_up || !t.w_down || !t.w_shared_in ||
-      !t.w_shared_out || !t.hidden || !t.partial || !t.groups || (!t.out && !t.resid) ||
+      !t.w_shared_out || !t.hidden || (partials && !t.partial) || !t.groups || (!t.out && !t.resid) ||
       (t.fp8 && (!t.s_gate || !t.s_up || !t.s_down || !t.s_shared_in || !t.s_shared_out)) ||
       (t.w_shared_scale && (!t.shared_scale || t.fp8)))
-    return fail(kBadArg, "moe_experts: null pointer or a shared-expert gate with fp8 weights");
+    return fail(kBadArg, "%s: null pointer or a shared-expert gate with fp8 weights", who);
   if (t.rows <= 0 || t.rows > 65535 || t.k <= 0 || t.k > 64 || t.experts <= 0 ||
       t.experts > kMaxExperts || t.hidden_size % 64 || t.hidden_size > 4096 || t.inter % 64 ||
       t.inter > 2048 || t.shared_inter % 64 || t.shared_inter > 2048 ||
       t.hidden_ld < t.inter || t.hidden_ld < t.shared_inter || t.hidden_ld % 8)
-    return fail(kBadShape, "moe_experts: rows=%d k=%d experts=%d (<= 256) H=%d (<= 4096) "
-                "I=%d IS=%d (<= 2048) ld=%d", t.rows, t.k, t.experts, t.hidden_size, t.inter,
+    return fail(kBadShape, "%s: rows=%d k=%d experts=%d (<= 256) H=%d (<= 4096) "
+                "I=%d IS=%d (<= 2048) ld=%d", who, t.rows, t.k, t.experts, t.hidden_size, t.inter,
                 t.shared_inter, t.hidden_ld);
-  MoeArgs a;
   a.x = (const bf16*)t.x;
   a.weights = t.weights;
   a.idx = (const int*)t.idx;
@@ -814,17 +1251,43 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
   a.err = t.err;
   if (t.route < TFD_MOE_ROUTE_GIVEN || t.route > TFD_MOE_ROUTE_TOPK_SOFTMAX ||
       (t.route != TFD_MOE_ROUTE_GIVEN && (!t.logits || t.ldl < t.experts || t.k > kWave)))
-    return fail(kBadArg, "moe_experts: route %d (0..2) needs logits with ldl >= experts and "
-                "k <= 64", t.route);
+    return fail(kBadArg, "%s: route %d (0..2) needs logits with ldl >= experts and "
+                "k <= 64", who, t.route);
   if (t.accumulate && t.policy != TFD_POLICY_F32)
-    return fail(kUnsupported, "moe_experts: accumulate needs the f32 policy");
+    return fail(kUnsupported, "%s: accumulate needs the f32 policy", who);
   if (t.resid && t.policy != TFD_POLICY_BF16)
-    return fail(kUnsupported, "moe_experts: resid needs the bf16 policy");
+    return fail(kUnsupported, "%s: resid needs the bf16 policy", who);
+  if (t.policy != TFD_POLICY_F32 && t.policy != TFD_POLICY_BF16)
+    return fail(kBadArg, "%s: policy %d", who, t.policy);
+  if (t.fp8 && t.policy != TFD_POLICY_BF16)
+    return fail(kUnsupported, "%s: fp8 weights with the f32 policy are not built", who);
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
+  MoeArgs a;
+  if (int rc = moe_args(args, true, "moe_experts", a)) return rc;
   auto s = (hipStream_t)stream;
-  if (t.fp8 && t.policy == TFD_POLICY_BF16) return launch_moe<true, false>(a, s);
-  if (!t.fp8 && t.policy == TFD_POLICY_F32) return launch_moe<false, true>(a, s);
-  if (!t.fp8 && t.policy == TFD_POLICY_BF16) return launch_moe<false, false>(a, s);
-  return fail(kUnsupported, "moe_experts: fp8 weights with the f32 policy are not built");
+  if (args->fp8) return launch_moe<true, false>(a, s);
+  if (args->policy == TFD_POLICY_F32) return launch_moe<false, true>(a, s);
+  return launch_moe<false, false>(a, s);
+}
+
+int tfd_moe_experts_packed(const TfdMoeArgs* args, void* stream) {
+  MoeArgs a;
+  if (int rc = moe_args(args, false, "moe_experts_packed", a)) return rc;
+  if (!moe8_fits(a))
+    return fail(kBadShape, "moe_experts_packed: rows=%d (<= 16) k=%d (<= 16) H=%d (a multiple "
+                "of 1024) I=%d IS=%d (multiples of 256, IS <= 2048, rows (k + 1) I / 256 <= 1024)",
+                a.B, a.k, a.H, a.I, a.IS);
+  auto s = (hipStream_t)stream;
+  if (args->fp8) return launch_moe8<true, false>(a, s);
+  if (args->policy == TFD_POLICY_F32) return launch_moe8<false, true>(a, s);
+  return launch_moe8<false, false>(a, s);
 }
 
 int tfd_gdn_step(const TfdGdnArgs* args, void* stream) {

@@ -769,19 +769,6 @@ struct SkinnyPlan {
   int64_t work_floats;      // counters + partials
 };
 
-int compute_units() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0)
-      n = 256;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
 
 // The work buffer starts with kSkCounters tile counters (zero before first use;
 // every call leaves the ones it used at zero) at a fixed place, so GEMMs of

@@ -445,6 +445,20 @@ int launched(const char* what) {
   return 0;
 }
 
+int compute_units() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 int cmax_for(int K) {
   const int per_lane = (K / 8 + kWave - 1) / kWave;
   if (per_lane <= 1) return 1;

@@ -203,6 +203,13 @@ class GraniteEngine:
         self._lib = lib()
         self.nsteps = max_steps
         self.split_len = split_len
+        # up to 16 sequences: the fp8 experts packed for the matrix-core pair
+        # (tfd_moe_experts_packed, 98 us against 128 us per layer at batch 8);
+        # more: row-major, the lane-sum kernels.  (At C4's bf16 widths the
+        # lane-sum kernels already stream at 0.75-0.8 of HBM, and the pair's down
+        # has only hidden / 16 = 128 blocks there: that engine keeps them.)
+        self.moe_packed = _lib.moe_packed_fits(rows, cfg.top_k, cfg.hidden, cfg.moe_inter,
+                                               cfg.shared_inter)
         self._pack(weights)
         self._buffers(page_seed)
         # record_routes: each layer's top-k expert indices are copied into
@@ -236,6 +243,9 @@ class GraniteEngine:
             d = {k[len(p):]: v for k, v in w.items() if k.startswith(p)}
             for name in ("w_in", "w_out", "w_router"):
                 d[name] = self._packed8(d[name])
+            if self.moe_packed:
+                for name in ("w_gate", "w_up", "w_down", "w_shared_in", "w_shared_out"):
+                    d[name] = self._packed8(d[name])
             self.layers.append(d)
         self.embed = w["embed"]
         self.gamma_final = w["gamma_final"]
@@ -265,7 +275,7 @@ class GraniteEngine:
         ld = max(cfg.moe_inter, cfg.shared_inter)
         self.moe_hidden = z(B, k + 1, ld, dtype=BF)
         self.moe_sscale = z(B)
-        self.moe_partial = z(B, k + 1, H)
+        self.moe_partial = None if self.moe_packed else z(B, k + 1, H)
         self.moe_groups = z(_lib.moe_group_words(cfg.experts, B), dtype=I32)
         self.moe_ld = ld
         self.state, self.conv = {}, {}
@@ -355,8 +365,8 @@ class GraniteEngine:
         a.s_gate, a.s_up, a.s_down = ptr(w["s_gate"]), ptr(w["s_up"]), ptr(w["s_down"])
         a.w_shared_in, a.w_shared_out = ptr(w["w_shared_in"]), ptr(w["w_shared_out"])
         a.s_shared_in, a.s_shared_out = ptr(w["w_shared_in_scale"]), ptr(w["w_shared_out_scale"])
-        a.hidden, a.shared_scale, a.partial = ptr(self.moe_hidden), ptr(self.moe_sscale), \
-            ptr(self.moe_partial)
+        a.hidden, a.shared_scale = ptr(self.moe_hidden), ptr(self.moe_sscale)
+        a.partial = None if self.moe_partial is None else ptr(self.moe_partial)
         # the experts' output goes straight into the residual stream, scaled
         a.groups, a.out = ptr(self.moe_groups), None
         a.resid, a.resid_mult = ptr(self.hidden), cfg.residual_multiplier
@@ -364,7 +374,10 @@ class GraniteEngine:
         a.inter, a.shared_inter, a.hidden_ld = cfg.moe_inter, cfg.shared_inter, self.moe_ld
         a.fp8, a.policy, a.err = 1, _lib.POLICY_BF16, ptr(self.err)
         a.logits, a.ldl, a.route = ptr(self.rlog), cfg.experts, _lib.MOE_ROUTE_TOPK_SOFTMAX
-        self._lib.tfd_moe_experts(ctypes_addr(a), s)
+        if self.moe_packed:
+            self._lib.tfd_moe_experts_packed(ctypes_addr(a), s)
+        else:
+            self._lib.tfd_moe_experts(ctypes_addr(a), s)
 
     def _layer(self, i, s, cur):
         cfg, L, w, B, H = self.cfg, self._lib, self.layers[i], self.B, self.cfg.hidden
