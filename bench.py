@@ -206,8 +206,10 @@ def cpu_baseline(weights, prompt, budget_s: float) -> dict:
 
 def bench_c3(args) -> int:
     """Workload C3: the same model at batch 32, every sequence with a
-    4096-token random context (walked by batched decode steps, untimed), then
-    `--steps` (default 256) timed steps of 32 tokens each."""
+    4096-token random context (built untimed: by default prefilled one
+    sequence at a time, 32 positions per pass; `--c3-context walk` walks the
+    contexts with batched decode steps instead), then `--steps` (default 256)
+    timed steps of 32 tokens each."""
     import torch
 
     from tilefoundry_amd import _lib
@@ -226,11 +228,15 @@ def bench_c3(args) -> int:
     for b in range(batch):
         g = torch.Generator().manual_seed(1000 + b)
         prompts.append(torch.randint(0, cfg.vocab_size, (ctx,), generator=g).tolist())
-    eng._load_prompts(prompts)
-    eng.run_steps(ctx - 1)                      # the contexts, untimed
+    t1 = time.perf_counter()
+    if args.c3_context == "prefill":
+        eng.prefill(prompts)                    # the contexts, untimed
+    else:
+        eng._load_prompts(prompts)
+        eng.run_steps(ctx - 1)
     torch.cuda.synchronize()
-    print(f"[bench] c3 setup + {ctx - 1} context steps {time.perf_counter() - t0:.1f}s",
-          file=sys.stderr, flush=True)
+    print(f"[bench] c3 setup {t1 - t0:.1f}s, contexts ({args.c3_context}, {batch} x {ctx - 1} "
+          f"positions) {time.perf_counter() - t1:.1f}s", file=sys.stderr, flush=True)
     stream = torch.cuda.current_stream()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start = time.perf_counter()
@@ -291,7 +297,8 @@ def bench_c3(args) -> int:
         "data": "synthetic (random-init N(0,0.02) weights seed 0, 32 random 4096-id contexts)",
         "config": {"workload": "C3: Qwen3-1.7B-arch bf16 decode, batch 32, 4096-token contexts, "
                                f"{steps} new tokens per sequence, 16-token KV pages",
-                   "batch": batch, "context": ctx, "new_tokens": steps},
+                   "batch": batch, "context": ctx, "new_tokens": steps,
+                   "context_built_by": args.c3_context},
         "step_roofline": {"bound": "hbm", "bytes_per_step": int(step_bytes),
                           "achieved": round(step_bw / 1e9, 1), "peak": HBM_PEAK / 1e9,
                           "unit": "GB/s", "frac": round(step_bw / HBM_PEAK, 4),
@@ -383,6 +390,9 @@ def main(argv=None) -> int:
     ap.add_argument("--timeline", default=None, metavar="CTX[,CTX...]",
                     help="only print the XCD kernel's per-role phase timeline on the C2 model "
                          "at these context lengths and exit")
+    ap.add_argument("--c3-context", default="prefill", choices=("prefill", "walk"),
+                    help="c3: build the 4096-token contexts by prefill (default) or by "
+                         "walking them with batched decode steps")
     ap.add_argument("--config", default="c2", choices=("c2", "c3"),
                     help="c2: the headline batch-1 workload; c3: batch 32 over 4096-token "
                          "contexts")

@@ -287,6 +287,24 @@ class BatchEngine:
         self._lib.tfd_embed_rows_bf16(ptr(self.w_embed), ptr(self.ids), ptr(self.hid), self.H,
                                       self.B, self.H, self.V, ptr(self.err), self._stream())
 
+    def prefill(self, prompts: list[list[int]]):
+        """Fill sequence b's cache at positions 0 .. len(prompts[b]) - 2 in batched
+        passes (``qwen3.prefill``, through b's page-table row), so that the next
+        step decodes every prompt's last token at its own position."""
+        if len(prompts) != self.B or any(len(p) < 1 for p in prompts):
+            raise ValueError(f"need {self.B} non-empty prompts")
+        if getattr(self, "_prefiller", None) is None:
+            from .prefill import Prefill
+            self._prefiller = Prefill(self, packed=True)
+        self._load_prompts(prompts)
+        for b, p in enumerate(prompts):
+            if len(p) > 1:
+                self._prefiller.run(list(p[:-1]), 0, seq=b)
+        self.pos.copy_(torch.tensor([len(p) - 1 for p in prompts], dtype=torch.int32))
+        self.ids.copy_(torch.tensor([p[-1] for p in prompts], dtype=torch.int64))
+        self._lib.tfd_embed_rows_bf16(ptr(self.w_embed), ptr(self.ids), ptr(self.hid), self.H,
+                                      self.B, self.H, self.V, ptr(self.err), self._stream())
+
     def check_errors(self):
         e = int(self.err.item())
         if e:
@@ -294,12 +312,15 @@ class BatchEngine:
                                       (8, "step")) if e & bit]
             raise RuntimeError(f"decode kernels flagged an out-of-range {', '.join(names)}")
 
-    def generate(self, prompts: list[list[int]], max_new: int,
-                 record_logits: bool = False) -> BatchGenerated:
+    def generate(self, prompts: list[list[int]], max_new: int, record_logits: bool = False,
+                 prefill: bool = False) -> BatchGenerated:
         """Walk every prompt, then continue for *max_new* greedy tokens per
         sequence.  Sequence b's continuation starts after its own prompt; all
         sequences step together, so the step count is max(prompt) - 1 + max_new,
-        and the timing covers the steps after the longest prompt."""
+        and the timing covers the steps after the longest prompt.  With
+        *prefill*, every prompt but its last token goes through ``prefill`` and
+        all sequences decode their last prompt token in the first step: max_new
+        steps, all timed."""
         if len(prompts) != self.B:
             raise ValueError(f"engine holds {self.B} sequences, got {len(prompts)} prompts")
         if any(len(p) < 1 for p in prompts):
@@ -310,9 +331,18 @@ class BatchEngine:
                              f"{self.nsteps} steps")
         if any(not 0 <= int(t) < self.V for p in prompts for t in p):
             raise ValueError(f"prompt ids must lie in [0, {self.V})")
-        self._load_prompts(prompts)
-        steps = longest - 1 + max_new
-        warm = longest - 1
+        torch.cuda.synchronize(self.device)
+        t_pre = perf_counter()
+        if prefill:
+            self.prefill(prompts)
+            starts = [0] * self.B                      # step of each sequence's first pick
+        else:
+            self._load_prompts(prompts)
+            starts = [len(p) - 1 for p in prompts]
+        torch.cuda.synchronize(self.device)
+        t_pre = perf_counter() - t_pre
+        steps = max(starts) + max_new
+        warm = max(starts)
         hist = (torch.empty(steps, self.B, self.V, device=self.device, dtype=torch.float32)
                 if record_logits else None)
         torch.cuda.synchronize(self.device)
@@ -336,9 +366,9 @@ class BatchEngine:
         logits = None
         if hist is not None:
             h = hist.cpu()
-            # logits at each sequence's own picks: step len(p) - 1 + j
-            logits = [h[len(p) - 1: len(p) - 1 + max_new, b] for b, p in enumerate(prompts)]
-        return BatchGenerated(tokens, t2 - t1, t1 - t0, max_new, logits)
+            # logits at each sequence's own picks: step starts[b] + j
+            logits = [h[st: st + max_new, b] for b, st in enumerate(starts)]
+        return BatchGenerated(tokens, t2 - t1, t1 - t0 + t_pre, max_new, logits)
 
     # ------------------------------------------------------------ accounting
     def weight_bytes_per_step(self) -> int:

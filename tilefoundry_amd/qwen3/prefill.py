@@ -22,6 +22,10 @@ second one reads the cache, and the second launch writes the same bits again.
 Prefill fills the cache for positions start .. start + n - 1 and leaves the
 hidden states of those rows unused: the last prompt token is then decoded as
 before, by the decode step, which produces the first new token.
+
+The same pass serves a batch engine (``batch_engine.py``): its sequences share
+one pool of pages, each with its own page-table row, and a prompt is prefilled
+one sequence at a time through that sequence's row.
 """
 from __future__ import annotations
 
@@ -37,12 +41,13 @@ class Prefill:
     """The batched prompt pass over an engine's weights, pools and page table.
 
     *engine* is a ``qwen3.engine.Engine`` (or anything with its attributes:
-    ``layers`` (row-major weights), ``kpool``/``vpool`` [L][pages][HKV][16][D],
-    ``page_table`` [pages], ``cos``/``sin``, ``cap``).  The projections are
+    ``layers``, ``kpool``/``vpool`` [L][pages][HKV][16][D], ``page_table``
+    ([max_pages], or [sequences][max_pages] with ``num_pages`` pages in the
+    pool), ``cos``/``sin``, ``cap``).  With *packed* False the projections are
     re-laid once into the skinny GEMMs' operand blocks (one more copy of the
-    layer weights in HBM)."""
+    layer weights in HBM); a batch engine's layers are already in that order."""
 
-    def __init__(self, engine):
+    def __init__(self, engine, packed: bool = False):
         e = engine
         self.e = e
         self._lib = lib()
@@ -53,6 +58,8 @@ class Prefill:
         self.qkv_n = e.cfg.qkv_size
         self.eps, self.scale = e.eps, e.scale
         self.max_pages = e.max_pages
+        self.num_pages = getattr(e, "num_pages", e.max_pages)
+        self.rows = e.page_table.reshape(-1, self.max_pages)      # [sequences][max_pages]
         tiles = e.cap // _lib.ATTN_SPLIT
         self.split_tiles = max(1, round(tiles / 16))
         self.nsplit = -(-tiles // self.split_tiles)
@@ -60,10 +67,11 @@ class Prefill:
         s = torch.cuda.current_stream(self.dev).cuda_stream
         self.layers = []
         for w in e.layers:
-            packed = dict(w)
-            for n in ("w_qkv", "w_o", "w_gu", "w_down"):
-                packed[n] = self._mfma_order(w[n], s)
-            self.layers.append(packed)
+            lw = dict(w)
+            if not packed:
+                for n in ("w_qkv", "w_o", "w_gu", "w_down"):
+                    lw[n] = self._mfma_order(w[n], s)
+            self.layers.append(lw)
         torch.cuda.synchronize(self.dev)
         self._buffers()
 
@@ -94,7 +102,7 @@ class Prefill:
         self.counters = z(R, self.HKV, dtype=i32)
         self.pos = z(R, dtype=i32)
         self.ids = z(R, dtype=torch.int64)
-        self.table = self.e.page_table.reshape(1, -1).expand(R, -1).contiguous()
+        self.table = self.rows[:1].expand(R, -1).contiguous()
         self.work = z(1 << 21, dtype=f32)
 
     def _gemm(self, x, w, R, K, N, epi, resid, out, ldo, s):
@@ -116,12 +124,12 @@ class Prefill:
             L.tfd_attn_rope_scores_paged_batched(
                 ptr(self.qkv), self.qkv_n, ptr(w["gamma_q"]), ptr(w["gamma_k"]), ptr(e.cos),
                 ptr(e.sin), e.cap, ptr(self.pos), ptr(self.table), self.max_pages,
-                ptr(e.kpool[i]), ptr(e.vpool[i]), self.max_pages, R, self.HQ, self.HKV, D,
+                ptr(e.kpool[i]), ptr(e.vpool[i]), self.num_pages, R, self.HQ, self.HKV, D,
                 self.scale, self.eps, ptr(self.scores), self.score_stride, ptr(self.smax),
                 ptr(self.snew), self.nsplit, self.split_tiles, ptr(e.err), s)
         L.tfd_attn_pv_combine_paged_batched(
             ptr(self.qkv), self.qkv_n, ptr(self.pos), ptr(self.table), self.max_pages,
-            ptr(e.vpool[i]), self.max_pages, R, self.HQ, self.HKV, D, ptr(self.scores),
+            ptr(e.vpool[i]), self.num_pages, R, self.HQ, self.HKV, D, ptr(self.scores),
             self.score_stride, ptr(self.smax), ptr(self.snew), ptr(self.psum), ptr(self.pout),
             self.nsplit, self.split_tiles, ptr(self.counters), ptr(self.attn), ptr(e.err), s)
         self._gemm(self.attn, w["w_o"], R, self.QD, H, _lib.EPI_RESID, x_in, self.h1, H, s)
@@ -130,15 +138,19 @@ class Prefill:
         self._gemm(self.xn, w["w_gu"], R, H, 2 * I, _lib.EPI_SWIGLU, None, self.hmid, 0, s)
         self._gemm(self.hmid, w["w_down"], R, I, H, _lib.EPI_RESID, self.h1, x_out, H, s)
 
-    def run(self, tokens: list[int], start: int = 0):
+    def run(self, tokens: list[int], start: int = 0, seq: int = 0):
         """Fill every layer's cache at positions start .. start + len(tokens) - 1
-        from those tokens (chunks of up to 32 rows)."""
+        of sequence *seq* (its page-table row) from those tokens (chunks of up to
+        32 rows)."""
         e = self.e
         if start < 0 or start + len(tokens) > e.cap:
             raise ValueError(f"prefill: positions {start}..{start + len(tokens) - 1} outside the "
                              f"cache ({e.cap} positions)")
         if any(not 0 <= int(t) < e.V for t in tokens):
             raise ValueError(f"prefill: token ids must lie in [0, {e.V})")
+        if not 0 <= seq < self.rows.shape[0]:
+            raise ValueError(f"prefill: sequence {seq} outside [0, {self.rows.shape[0]})")
+        self.table.copy_(self.rows[seq:seq + 1].expand(MAX_ROWS, -1))
         s = torch.cuda.current_stream(self.dev).cuda_stream
         for c0 in range(0, len(tokens), MAX_ROWS):
             chunk = tokens[c0:c0 + MAX_ROWS]
