@@ -163,7 +163,18 @@ def bench_mamba(config, rows, reps, gen):
     return _line(config, "mamba_step", rows, sec, nbytes)
 
 
-def bench_moe(config, rows, reps, gen, *, hs, inter, sh, experts, k, fp8):
+def _pack_rows(w):
+    """[rows][K] weights in the skinny GEMMs' operand blocks (bf16 or fp8 codes)."""
+    N, K = w.shape
+    out = torch.empty(-(-N // 16) * 16 * K, dtype=w.dtype, device=DEV)
+    fn = lib().tfd_pack_skinny_fp8 if w.dtype == torch.uint8 else lib().tfd_pack_skinny_bf16
+    fn(ptr(w), K, N, K, ptr(out), _stream())
+    return out
+
+
+def bench_moe(config, rows, reps, gen, *, hs, inter, sh, experts, k, fp8, packed=False):
+    """tfd_moe_experts over row-major weights, or with *packed* the matrix-core
+    entry tfd_moe_experts_packed over packed weights (no partials)."""
     bpw = 1 if fp8 else 2
     if fp8:
         w_gate, w_up = _fp8((experts, inter, hs), gen), _fp8((experts, inter, hs), gen)
@@ -179,6 +190,8 @@ def bench_moe(config, rows, reps, gen, *, hs, inter, sh, experts, k, fp8):
         scales = [None] * 5
     dev = [t.to(DEV) if t is not None else None for t in
            (w_gate, w_up, w_down, w_sin, w_sout, *scales)]
+    if packed:
+        dev[:5] = [_pack_rows(t.reshape(-1, t.shape[-1])) for t in dev[:5]]
     w_sscale = None if fp8 else (_rn(hs, gen=gen) * 0.03).to(BF).to(DEV)
     x = _rn(rows, hs, gen=gen).to(BF).to(DEV)
     ld = max(inter, sh)
@@ -205,13 +218,14 @@ def bench_moe(config, rows, reps, gen, *, hs, inter, sh, experts, k, fp8):
         a.s_gate, a.s_up, a.s_down, a.s_shared_in, a.s_shared_out = [ptr(t) for t in dev[5:]]
         a.w_shared_scale = ptr(w_sscale)
         a.hidden, a.shared_scale, a.out = ptr(hidden), ptr(sscale), ptr(out)
-        a.partial, a.groups = ptr(partial), ptr(groups)
+        a.partial, a.groups = (None if packed else ptr(partial)), ptr(groups)
         a.rows, a.k, a.experts, a.hidden_size = rows, k, experts, hs
         a.inter, a.shared_inter, a.hidden_ld = inter, sh, ld
         a.fp8, a.policy, a.err = int(fp8), _lib.POLICY_BF16 if fp8 else _lib.POLICY_F32, ptr(err)
         args.append(a)
     L = lib()
-    calls = [lambda a=a: L.tfd_moe_experts(ctypes.addressof(a), _stream()) for a in args]
+    entry = L.tfd_moe_experts_packed if packed else L.tfd_moe_experts
+    calls = [lambda a=a: entry(ctypes.addressof(a), _stream()) for a in args]
     sec = time_graph(calls, reps)
     union = sum(unions) / len(unions)
     wbytes = union * 3 * inter * hs * bpw + 3 * sh * hs * bpw
@@ -220,8 +234,9 @@ def bench_moe(config, rows, reps, gen, *, hs, inter, sh, experts, k, fp8):
     else:
         wbytes += hs * 2
     nbytes = (wbytes + rows * hs * 2 + rows * hs * 4 + rows * (k + 1) * ld * 2 * 2 +
-              rows * (k + 1) * hs * 4 * 2)
-    return _line(config, "moe_experts", rows, sec, nbytes, experts_touched=round(union, 1))
+              (0 if packed else rows * (k + 1) * hs * 4 * 2))
+    return _line(config, "moe_experts_packed" if packed else "moe_experts", rows, sec, nbytes,
+                 experts_touched=round(union, 1))
 
 
 def bench_route(config, rows, reps, gen, *, experts, k, mode):
@@ -373,6 +388,9 @@ def run(config: str, reps: int) -> list[dict]:
                                mode=_lib.ROUTE_SOFTMAX_TOPK))
         res.append(bench_moe(config, rows, reps, gen, hs=2048, inter=512, sh=512, experts=256,
                              k=8, fp8=False))
+        if rows > 1:
+            res.append(bench_moe(config, rows, reps, gen, hs=2048, inter=512, sh=512,
+                                 experts=256, k=8, fp8=False, packed=True))
         res.append(bench_gqa(config, rows, reps, gen, heads=16, kv_heads=2, d=256, ctx=1024,
                              f32=True, split_len=64))
     elif config == "c5":
@@ -380,8 +398,9 @@ def run(config: str, reps: int) -> list[dict]:
         res.append(bench_mamba(config, rows, reps, gen))
         res.append(bench_route(config, rows, reps, gen, experts=72, k=10,
                                mode=_lib.ROUTE_TOPK_SOFTMAX))
-        res.append(bench_moe(config, rows, reps, gen, hs=4096, inter=768, sh=1536, experts=72,
-                             k=10, fp8=True))
+        for packed in (False, True):
+            res.append(bench_moe(config, rows, reps, gen, hs=4096, inter=768, sh=1536,
+                                 experts=72, k=10, fp8=True, packed=packed))
         res.append(bench_gqa(config, rows, reps, gen, heads=32, kv_heads=8, d=128, ctx=8192,
                              f32=False, split_len=256))
         res.append(bench_gemm_fp8(config, rows, reps, gen, K=4096, N=8512, name="in_proj"))
