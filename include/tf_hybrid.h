@@ -149,6 +149,32 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream);
  * rounding of each sum before its bf16 rounding. */
 int tfd_moe_experts_packed(const TfdMoeArgs* args, void* stream);
 
+/* An fp8 projection of C5 with the HIR's RMSNorm as its prologue (replaces
+ * GraniteDecoderLayer's input_layernorm / post_attention_layernorm followed by
+ * the in-projection or the router, examples/granite_4_0_h_small-cuda/
+ * model.py:480-523 with rms_norm at ir/hir/nn/rms_norm.py:103-110): for rows
+ * <= 8 and K = 4096, xn = bf16(x * rsqrt(mean(x^2) + eps) * gamma) from the bf16
+ * rows x [rows][ldx] (f32 arithmetic, one rounding), then out[r][n] =
+ * bf16(scale[n] sum_k xn[r][k] e4m3(W[n][k])) with W packed by
+ * tfd_pack_skinny_fp8: TFD_EPI_STORE bf16 [rows][ldo], TFD_EPI_LOGITS f32 (bf16
+ * values) [rows][ldo].  With x_rows set the normalised rows are also written
+ * there ([rows][ldxr] bf16: the experts' input).  One launch instead of a norm
+ * and a GEMM; kBadShape outside those sizes. */
+typedef struct {
+  const void* x;
+  int ldx;
+  const void* gamma;
+  float eps;
+  void* x_rows;
+  int ldxr;
+  const void* w;
+  const float* scale;
+  int rows, K, N;
+  void* out;
+  int ldo, epilogue;
+} TfdProj8NormArgs;
+int tfd_proj8_norm(const TfdProj8NormArgs* args, void* stream);
+
 /* Gated DeltaNet at one token per sequence, everything between the in- and
  * out-projections of Qwen3_5LinearAttention.linear_attention: conv_step,
  * l2_normalise, beta/g, delta_step and the gated RMS norm

@@ -157,6 +157,72 @@ def test_tf_rmsnorm_rows_rounds_once(gpu_device, rows):
     assert (got == want).float().mean() >= 0.99
 
 
+def _proj8_norm(x, gamma, codes, scale, epi, rows_out=True):
+    """tfd_proj8_norm over bf16 rows x [M][4096]: (out, normalised rows)."""
+    M, K = x.shape
+    N = codes.shape[0]
+    dev = "cuda:0"
+    w = _packed_fp8(codes.to(dev))
+    xd, gd, sd = x.to(BF).to(dev), gamma.to(BF).to(dev), scale.to(dev)
+    out = torch.zeros(M, N, device=dev, dtype=BF if epi == _lib.EPI_STORE else torch.float32)
+    xr = torch.zeros(M, K, device=dev, dtype=BF)
+    a = _lib.TfdProj8NormArgs()
+    a.x, a.ldx, a.gamma, a.eps = ptr(xd), K, ptr(gd), 1e-5
+    a.x_rows, a.ldxr = (ptr(xr), K) if rows_out else (None, 0)
+    a.w, a.scale, a.rows, a.K, a.N = ptr(w), ptr(sd), M, K, N
+    a.out, a.ldo, a.epilogue = ptr(out), N, epi
+    lib().tfd_proj8_norm(ctypes.addressof(a), _stream())
+    torch.cuda.synchronize()
+    return out.float().cpu(), xr.float().cpu()
+
+
+@pytest.mark.parametrize("M", [1, 5, 8])
+@pytest.mark.parametrize("N,epi", [(72, _lib.EPI_LOGITS), (8512, _lib.EPI_STORE),
+                                   (6144, _lib.EPI_STORE)])
+def test_proj8_norm_is_the_norm_then_the_fp8_gemm(gpu_device, M, N, epi):
+    """tfd_proj8_norm (the HIR RMSNorm as the prologue of an fp8 projection; C5's
+    post norm + router) equals tfd_tf_rmsnorm_rows_bf16 followed by
+    tfd_gemm_skinny_fp8 bit for bit -- the normalised rows it hands on too -- and
+    is within one bf16 ulp plus the f32 bound of the exact product of the
+    oracle's normalised rows (rms_norm_tf) with gemv_fp8."""
+    g = torch.Generator().manual_seed(7 * M + N)
+    K = 4096
+    x = H.bf(torch.randn(M, K, generator=g) * 2)
+    gamma = H.bf(1 + 0.2 * torch.randn(K, generator=g))
+    codes = _fp8_codes((N, K), g)
+    scale = torch.rand(N, generator=g) * 0.02 + 0.005
+    got, rows = _proj8_norm(x, gamma, codes, scale, epi)
+    dev = "cuda:0"
+    xd, gd = x.to(BF).to(dev), gamma.to(BF).to(dev)
+    o_rows = torch.zeros(M, K, dtype=BF, device=dev)
+    o_pk = torch.zeros(32 * K, dtype=BF, device=dev)
+    lib().tfd_tf_rmsnorm_rows_bf16(ptr(xd), K, ptr(gd), ptr(o_rows), K, ptr(o_pk), M, K, 1e-5,
+                                   _stream())
+    torch.cuda.synchronize()
+    assert torch.equal(rows, o_rows.float().cpu())
+    two = _gemm_fp8(o_rows.float().cpu().to(BF), codes, scale, epi).float()
+    assert torch.equal(got, two)
+    xn = H.rms_norm_tf(x, gamma, 1e-5)
+    exact = H.gemv_fp8(codes, scale, xn).double()
+    raw = codes.view(torch.float8_e4m3fn).double()
+    acc_bound = K * 2.0 ** -24 * (xn.double().abs() @ raw.abs().t()) * scale.double()
+    # the norm may round one input an ulp away from the oracle's (f32 sums in
+    # another order): that input's term is bounded by an ulp of it times |w|
+    norm_bound = (ulp_bf16(xn).double() @ raw.abs().t()) * scale.double()
+    bound = ulp_bf16(exact.float()).double() + acc_bound + norm_bound
+    bad = (got.double() - exact).abs() > bound
+    assert not bad.any(), (int(bad.sum()), got[bad][:4], exact[bad][:4])
+
+
+def test_proj8_norm_rejects_bad_shapes(gpu_device):
+    g = torch.Generator().manual_seed(3)
+    for M, K in ((9, 4096), (4, 2048)):
+        x = H.bf(torch.randn(M, K, generator=g))
+        with pytest.raises(_lib.TFDError, match="proj8_norm"):
+            _proj8_norm(x, torch.ones(K), _fp8_codes((72, K), g), torch.ones(72),
+                        _lib.EPI_LOGITS)
+
+
 @pytest.mark.parametrize("M,V", [(1, 4096), (8, 100352)])
 def test_head_logits_divided_by_logits_scaling(gpu_device, M, V):
     """tfd_gemm_skinny_bf16_logits_div (Granite's lm_head / logits_scaling):

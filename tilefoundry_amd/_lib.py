@@ -37,6 +37,10 @@ SMALL_ROWS = 4              # rows of the small-batch entries (tfd_rowgemv_bf16 
 MOE_ROUTE_GIVEN, MOE_ROUTE_SOFTMAX_TOPK, MOE_ROUTE_TOPK_SOFTMAX = 0, 1, 2
 
 
+#: tfd_proj8_norm's sizes: rows <= PROJ8_ROWS, K == PROJ8_K
+PROJ8_ROWS, PROJ8_K = 8, 4096
+
+
 def moe_packed_fits(rows: int, k: int, hidden: int, inter: int, shared_inter: int) -> bool:
     """Whether tfd_moe_experts_packed takes this shape (its kBadShape check,
     include/tf_hybrid.h): rows <= 16, k <= 16, H a multiple of 1024, I and IS of
@@ -85,6 +89,7 @@ SIGNATURES: dict[str, list] = {
     "tfd_route_topk": [P, I, I, I, I, I, P, P, P],
     "tfd_moe_experts": [P, P],
     "tfd_moe_experts_packed": [P, P],
+    "tfd_proj8_norm": [P, P],
     "tfd_gdn_step": [P, P],
     "tfd_mamba_step": [P, P],
     "tfd_gqa_decode": [P, P],
@@ -127,6 +132,17 @@ class TfdMoeArgs(ctypes.Structure):
                                 "hidden_ld", "fp8", "policy", "accumulate")],
         ("logits", c_void_p), ("ldl", c_int), ("route", c_int),
         ("err", c_void_p), ("resid", c_void_p), ("resid_mult", c_float),
+    ]
+
+
+class TfdProj8NormArgs(ctypes.Structure):
+    """``TfdProj8NormArgs`` of include/tf_hybrid.h, field for field."""
+
+    _fields_ = [
+        ("x", c_void_p), ("ldx", c_int), ("gamma", c_void_p), ("eps", c_float),
+        ("x_rows", c_void_p), ("ldxr", c_int), ("w", c_void_p), ("scale", c_void_p),
+        *[(n, c_int) for n in ("rows", "K", "N")],
+        ("out", c_void_p), ("ldo", c_int), ("epilogue", c_int),
     ]
 
 

@@ -157,6 +157,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
   void* u = (void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
   return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, -1, 0x00020000);
 }
+// A descriptor of `bytes` bytes: a load at an offset past them returns zeros
+// without a memory access (kOutOfRange is such an offset for any buffer under
+// 2 GiB, with room to add steps to it).
+constexpr uint32_t kOutOfRange = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_bounded(const void* base, uint32_t bytes) {
+  const uint64_t b = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  void* u = (void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, (int)bytes, 0x00020000);
+}
 __device__ __forceinline__ u32x4 coh_ld16(const void* base, uint32_t byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), byte_off, 0, kCoherent);
 }

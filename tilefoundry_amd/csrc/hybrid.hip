@@ -14,6 +14,7 @@
 
 #include "hybrid_common.h"
 #include "host_common.h"
+#include "tf_decode.h"
 #include "tf_hybrid.h"
 
 #include <type_traits>
@@ -429,17 +430,13 @@ struct M8W<false> {
   }
 };
 
-// A operands through a buffer descriptor of `bytes` bytes: a lane whose row is
-// past the group's count reads at kM8Off, out of range, which returns zeros
-// without a memory access (the rows of the sequences that did not pick the
-// expert cost nothing)
-constexpr uint32_t kM8Off = 0x80000000u;
+// A operands through a range-limited descriptor (rsrc_bounded): a lane whose
+// row is past the group's count reads at kM8Off, out of range, which returns
+// zeros without a memory access (the rows of the sequences that did not pick
+// the expert cost nothing)
+constexpr uint32_t kM8Off = kOutOfRange;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t m8_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t b = (uint64_t)(uintptr_t)base;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
-  void* u = (void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-  return __builtin_amdgcn_make_buffer_rsrc(u, (short)0, (int)bytes, 0x00020000);
+  return rsrc_bounded(base, bytes);
 }
 __device__ __forceinline__ bf16x8_m m8_a(const u32x4& x) { return __builtin_bit_cast(bf16x8_m, x); }
 
@@ -735,6 +732,137 @@ __global__ __launch_bounds__(kWv * kWave) void k_moe8_down(MoeArgs a) {
     else
       a.out[at] = y;
   }
+}
+
+// ---------------------------------------------------------------------------
+// An fp8 projection with the HIR's RMSNorm as its prologue, for at most eight
+// rows (C5: the input norm + in-projection, the post norm + router, which also
+// hands the normalised rows to the experts).  A separate norm launch costs the
+// ramp and tail every launch pays (about 4 us); here a block normalises the
+// rows itself, into LDS, while its first weight loads are in flight:
+//   prologue  wave r normalises row r as tfd_tf_rmsnorm_rows_bf16 does (the
+//             same sums in the same order: the same bits) into LDS (block 0
+//             also to x_rows)
+//   tiles     the block takes a run of `tiles` 16-column tiles; its eight
+//             waves split K, read the A operand from LDS and stream the packed
+//             fp8 blocks kD steps ahead across tile boundaries; the waves'
+//             sums meet in LDS (one buffer, two barriers per tile, so that two
+//             blocks fit a compute unit) and one wave in turn applies the scale
+//             and the epilogue (bf16 rows, or bf16-valued f32 logits)
+// ---------------------------------------------------------------------------
+struct Proj8Args {
+  const bf16* x;            // [M][ldx] bf16 rows
+  int ldx;
+  const bf16* gamma;        // [K]
+  float eps;
+  bf16* x_rows;             // optional [M][ldxr]: the normalised rows
+  int ldxr;
+  const void* w;            // packed fp8 [N][K] (tfd_pack_skinny_fp8)
+  const float* scale;       // [N]
+  int M, K, N;
+  void* out;                // kEpi 0: bf16 [M][ldo]; 1: f32 [M][ldo]
+  int ldo, tiles;
+};
+constexpr int kP8Waves = 8;
+constexpr int kP8Rows = 8;
+constexpr int kP8K = 4096;                 // the prologue's chunk map: K = 8 x 512
+constexpr int kP8Ld = kP8K + 8;            // LDS row stride (bf16), 16 bytes of pad
+// under 80 KB, so that two blocks fit a compute unit
+constexpr size_t kP8Lds = (size_t)kP8Rows * kP8Ld * 2 + kP8Waves * kWave * 16;
+
+template <int kEpi, int kD>
+__global__ __launch_bounds__(kP8Waves * kWave) void k_proj8_norm(Proj8Args a) {
+  using W = M8W<true>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t p8_lds[];
+  bf16* xs = reinterpret_cast<bf16*>(p8_lds);
+  f32x4_m* red = reinterpret_cast<f32x4_m*>(p8_lds + (size_t)kP8Rows * kP8Ld * 2);
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int nl = lane & 15, kq = lane >> 4;
+  const int ntiles = (a.N + 15) / 16, ksteps = kP8K / 32;
+  constexpr int ns = kP8K / 32 / kP8Waves;        // this wave's steps per tile
+  const int t0 = (int)blockIdx.x * a.tiles;
+  if (t0 >= ntiles) return;
+  const int mine = min(a.tiles, ntiles - t0), total = mine * ns;
+  const int k0 = wave * ns;
+  typename W::Raw b[kD];
+  int jn = 0, sn = 0;
+  auto issue = [&](int u) {
+    b[u] = W::load(a.w, (int64_t)(t0 + jn) * ksteps + k0 + sn, lane);
+    if (++sn == ns && jn + 1 < mine) {
+      sn = 0;
+      ++jn;
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < kD; ++u) issue(u);
+  // ---- prologue: the rows' norm into LDS.  Wave r normalises row r exactly
+  // as tfd_tf_rmsnorm_rows_bf16 does (rms_norm_x: lane l holds chunks l, l + 64,
+  // ..., the squares summed in that order, then the wave's sum), so the rows
+  // are that kernel's bit for bit.
+  if (wave < a.M) {
+    u32x4 xr[kP8K / 512];
+    rms_norm_x<kP8K / 512, true>(a.x + (int64_t)wave * a.ldx, a.gamma, kP8K, a.eps, lane, xr);
+#pragma unroll
+    for (int i = 0; i < kP8K / 512; ++i) {
+      const int c = i * kWave + lane;
+      *reinterpret_cast<u32x4*>(xs + wave * kP8Ld + c * 8) = xr[i];
+      if (a.x_rows && blockIdx.x == 0)
+        *reinterpret_cast<u32x4*>(a.x_rows + (int64_t)wave * a.ldxr + c * 8) = xr[i];
+    }
+  }
+  __syncthreads();
+  // ---- the tiles
+  const bool valid = nl < a.M;
+  const bf16* arow = xs + (valid ? nl : 0) * kP8Ld + k0 * 32 + kq * 8;
+  f32x4_m c = {0.f, 0.f, 0.f, 0.f};
+  int jc = 0, sc = 0;
+  auto compute = [&](int u) {
+    const u32x4 av = valid ? *reinterpret_cast<const u32x4*>(arow + sc * 32)
+                           : u32x4{0u, 0u, 0u, 0u};
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_m, av),
+                                                W::value(b[u]), c, 0, 0, 0);
+    if (++sc < ns) return;
+    const int j = jc++;
+    sc = 0;
+    red[wave * kWave + lane] = c;
+    c = f32x4_m{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+    f32x4_m sum = red[lane];
+    const bool mine_ep = wave == (j & (kP8Waves - 1));
+    if (mine_ep) {
+#pragma unroll
+      for (int w = 1; w < kP8Waves; ++w) {
+        const f32x4_m v = red[w * kWave + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum[e] += v[e];
+      }
+    }
+    __syncthreads();                               // the sums read: LDS free for the next tile
+    const int n = (t0 + j) * 16 + nl;
+    if (!mine_ep || n >= a.N) return;
+    const float sc_n = a.scale[n];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 4 * kq + e;
+      if (m >= a.M) continue;
+      const float y = rbf(sum[e] * sc_n);
+      if (kEpi == 0)
+        ((bf16*)a.out)[(int64_t)m * a.ldo + n] = f2bf(y);
+      else
+        ((float*)a.out)[(int64_t)m * a.ldo + n] = y;
+    }
+  };
+  int q0 = 0;
+  for (; q0 + kD < total; q0 += kD) {
+#pragma unroll
+    for (int u = 0; u < kD; ++u) {
+      compute(u);
+      issue(u);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kD; ++u) compute(u);
 }
 
 // ---------------------------------------------------------------------------
@@ -1275,6 +1403,57 @@ int tfd_moe_experts(const TfdMoeArgs* args, void* stream) {
   if (args->fp8) return launch_moe<true, false>(a, s);
   if (args->policy == TFD_POLICY_F32) return launch_moe<false, true>(a, s);
   return launch_moe<false, false>(a, s);
+}
+
+int tfd_proj8_norm(const TfdProj8NormArgs* args, void* stream) {
+  if (!args) return fail(kBadArg, "proj8_norm: null args");
+  const TfdProj8NormArgs& t = *args;
+  if (!t.x || !t.gamma || !t.w || !t.scale || !t.out)
+    return fail(kBadArg, "proj8_norm: null pointer");
+  if (t.rows <= 0 || t.rows > kP8Rows || t.K != kP8K || t.N <= 0 || t.ldx < t.K ||
+      t.ldo < t.N || (t.x_rows && t.ldxr < t.K) ||
+      (t.epilogue != TFD_EPI_STORE && t.epilogue != TFD_EPI_LOGITS))
+    return fail(kBadShape, "proj8_norm: rows=%d (1..%d) K=%d (%d) N=%d ldx=%d ldo=%d "
+                "epilogue=%d (store or logits)", t.rows, kP8Rows, t.K, kP8K, t.N, t.ldx, t.ldo,
+                t.epilogue);
+  Proj8Args a;
+  a.x = (const bf16*)t.x;
+  a.ldx = t.ldx;
+  a.gamma = (const bf16*)t.gamma;
+  a.eps = t.eps;
+  a.x_rows = (bf16*)t.x_rows;
+  a.ldxr = t.ldxr;
+  a.w = t.w;
+  a.scale = t.scale;
+  a.M = t.rows;
+  a.K = t.K;
+  a.N = t.N;
+  a.out = t.out;
+  a.ldo = t.ldo;
+  const int ntiles = (t.N + 15) / 16;
+  const void* k = t.epilogue == TFD_EPI_STORE
+                      ? reinterpret_cast<const void*>(&k_proj8_norm<0, 16>)
+                      : reinterpret_cast<const void*>(&k_proj8_norm<1, 16>);
+  // as many blocks as are resident at once, each the same number of tiles
+  static int per_cu[2] = {0, 0};
+  int& pc = per_cu[t.epilogue == TFD_EPI_STORE ? 0 : 1];
+  if (!pc) {
+    if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kP8Lds) !=
+        hipSuccess)
+      return fail(kUnsupported, "proj8_norm: %d bytes of LDS refused", (int)kP8Lds);
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&pc, k, kP8Waves * kWave, kP8Lds) !=
+            hipSuccess || pc <= 0)
+      pc = 1;
+  }
+  const int cap = pc * compute_units();
+  a.tiles = (ntiles + cap - 1) / cap;
+  const dim3 grid((ntiles + a.tiles - 1) / a.tiles);
+  auto s = (hipStream_t)stream;
+  if (t.epilogue == TFD_EPI_STORE)
+    hipLaunchKernelGGL((k_proj8_norm<0, 16>), grid, dim3(kP8Waves * kWave), kP8Lds, s, a);
+  else
+    hipLaunchKernelGGL((k_proj8_norm<1, 16>), grid, dim3(kP8Waves * kWave), kP8Lds, s, a);
+  return launched("proj8_norm");
 }
 
 int tfd_moe_experts_packed(const TfdMoeArgs* args, void* stream) {
