@@ -56,3 +56,23 @@ def test_granite_engine_at_full_expert_width(gpu_device, rows):
                for b in range(rows)]
     _, picks, _ = _run(gpu_device, cfg, rows, seed=13, prompts=prompts, new=8)
     assert picks >= rows * 2
+
+
+def test_granite_prefill_is_the_walk(gpu_device):
+    """GraniteEngine.prefill walks equal-length prompts to their last token: the
+    greedy continuation after it equals generate's (which walks the same
+    prompts), and unequal lengths are refused."""
+    cfg = GraniteConfig(layers=3, attention_layers=(1,), experts=12, top_k=4, vocab=4096)
+    w = synthetic_weights(cfg, seed=5, device=gpu_device)
+    eng = GraniteEngine(cfg, w, rows=2, device=gpu_device, max_steps=64, split_len=16)
+    g = torch.Generator().manual_seed(9)
+    prompts = [torch.randint(0, cfg.vocab, (7,), generator=g).tolist() for _ in range(2)]
+    tokens, _, _ = eng.generate(prompts, 6)
+    eng.prefill(prompts)
+    for _ in range(6):
+        eng.replay()
+    eng.check_errors()
+    sam = eng.sam.cpu()
+    assert [sam[b, 6:12].tolist() for b in range(2)] == tokens
+    with pytest.raises(ValueError, match="one length"):
+        eng.prefill([prompts[0], prompts[1][:5]])

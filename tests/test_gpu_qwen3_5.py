@@ -54,3 +54,20 @@ def test_qwen35_engine_at_full_expert_width(gpu_device, rows):
     assert cfg.top_k == 8
     _, picks, _ = _run(gpu_device, cfg, rows, seed=11, prompt_seed=30 + rows, new=8)
     assert picks >= rows * 2
+
+
+def test_qwen35_prefill_is_the_walk(gpu_device):
+    """Qwen35Engine.prefill walks equal-length prompts to their last token: the
+    greedy continuation after it equals generate's."""
+    cfg = Qwen35Config(layers=4, experts=16, vocab=4096)
+    w = synthetic_weights(cfg, seed=3, device=gpu_device)
+    eng = Qwen35Engine(cfg, w, rows=2, device=gpu_device, max_steps=64, split_len=16)
+    g = torch.Generator().manual_seed(9)
+    prompts = [torch.randint(0, cfg.vocab, (7,), generator=g).tolist() for _ in range(2)]
+    tokens, _, _ = eng.generate(prompts, 6)
+    eng.prefill(prompts)
+    for _ in range(6):
+        eng.replay()
+    eng.check_errors()
+    sam = eng.sam.cpu()
+    assert [sam[b, 6:12].tolist() for b in range(2)] == tokens

@@ -442,22 +442,30 @@ def bench_c4_step(rows: int, steps: int, prompt: int = 32, small: bool | None = 
     return out
 
 
-def bench_c5_step(rows: int, steps: int, ctx: int = 8192) -> dict:
+def bench_c5_step(rows: int, steps: int, ctx: int = 8192, context: str = "drawn") -> dict:
     """Whole C5 decode steps (Granite-4.0-H-style, 40 layers, fp8 weights, batch
-    `rows`) after a `ctx`-token context per sequence that is drawn at random into
-    the caches and states rather than walked (GraniteEngine.synthetic_context:
-    the work of each later step is that of a real context of that length)."""
+    `rows`) after a `ctx`-token context per sequence: drawn at random into the
+    caches and states (GraniteEngine.synthetic_context: the work of each later
+    step is that of a real context of that length), or with *context* "walk"
+    built from a random prompt by GraniteEngine.prefill (ctx - 1 decode steps,
+    untimed)."""
     from .granite import GraniteConfig, GraniteEngine, synthetic_weights
 
     cfg = GraniteConfig()
     t0 = time.perf_counter()
     w = synthetic_weights(cfg, seed=0, device=DEV)
     eng = GraniteEngine(cfg, w, rows=rows, device=DEV, max_steps=ctx + steps + 32)
-    eng.synthetic_context(ctx)
+    if context == "walk":
+        g = torch.Generator().manual_seed(5)
+        eng.prefill([torch.randint(0, cfg.vocab, (ctx + 1,), generator=g).tolist()
+                     for _ in range(rows)])
+    else:
+        eng.synthetic_context(ctx)
     for _ in range(4):
         eng.replay()
     torch.cuda.synchronize()
-    print(f"[bench] c5 weights + engine + capture {time.perf_counter() - t0:.1f}s", flush=True)
+    print(f"[bench] c5 weights + engine + capture + context ({context}) "
+          f"{time.perf_counter() - t0:.1f}s", flush=True)
     t1 = time.perf_counter()
     for _ in range(steps):
         eng.replay()
@@ -469,7 +477,8 @@ def bench_c5_step(rows: int, steps: int, ctx: int = 8192) -> dict:
     positions = range(ctx + 4, ctx + 4 + steps)
     sbytes = sum(eng.state_bytes_per_step([p] * rows) for p in positions) / steps
     step_s = seconds / steps
-    out = {"config": f"c5 step b{rows} ctx{ctx}", "tok_s": round(rows * steps / seconds, 1),
+    out = {"config": f"c5 step b{rows} ctx{ctx}", "context": context,
+           "tok_s": round(rows * steps / seconds, 1),
            "ms_per_step": round(step_s * 1e3, 4), "steps": steps,
            "bytes_per_step": int(wbytes + sbytes), "experts_touched_sample": touched,
            "GB/s": round((wbytes + sbytes) / step_s / 1e9, 1),
@@ -486,6 +495,10 @@ def main(argv=None) -> int:
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--rows", type=int, default=1, help="c4-step / c5-step: sequences")
     ap.add_argument("--steps", type=int, default=256, help="c4-step / c5-step: timed steps")
+    ap.add_argument("--context", choices=("drawn", "walk"), default="drawn",
+                    help="c5-step: the contexts drawn into the caches and states (default) or "
+                         "built by prefill from random prompts (about 53 s at 8,192 tokens)")
+    ap.add_argument("--ctx", type=int, default=8192, help="c5-step: context length")
     ap.add_argument("--path", choices=("auto", "small", "mfma"), default="auto",
                     help="c4-step: the small-batch kernels (rows <= 4, the default there) or "
                          "the batched MFMA path")
@@ -497,7 +510,7 @@ def main(argv=None) -> int:
                       small=None if args.path == "auto" else args.path == "small")
         return 0
     if args.config == "c5-step":
-        bench_c5_step(args.rows, args.steps)
+        bench_c5_step(args.rows, args.steps, ctx=args.ctx, context=args.context)
         return 0
     if args.config == "gemm":
         run_gemm(args.reps)

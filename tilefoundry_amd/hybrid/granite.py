@@ -484,6 +484,24 @@ class GraniteEngine:
                                       self.cfg.hidden, self.B, self.cfg.hidden, self.cfg.vocab,
                                       ptr(self.err), self._stream())
 
+    def prefill(self, prompts: list[list[int]]):
+        """Bring every sequence to its prompt's last token: the prompts (all of one
+        length) are walked through the decode step, one position per step, so
+        that the next step decodes each last prompt token.  The recurrent state
+        of the mixers has no batched form here (each position's state is the
+        previous one's update), so this is the walk ``generate`` makes, taken out
+        of it."""
+        if len(prompts) != self.B or any(len(p) < 1 for p in prompts):
+            raise ValueError(f"need {self.B} non-empty prompts")
+        if len({len(p) for p in prompts}) != 1:
+            raise ValueError("prefill: the prompts must have one length (the walk moves "
+                             "every sequence one position per step)")
+        if len(prompts[0]) > self.nsteps:
+            raise ValueError(f"prompt {len(prompts[0])} exceeds {self.nsteps} steps")
+        self._load_prompts(prompts)
+        for _ in range(len(prompts[0]) - 1):
+            self.replay()
+
     def synthetic_context(self, ctx: int, seed: int = 0):
         """Stand in for a walked `ctx`-token context without walking it: every
         sequence's first `ctx` cache rows, conv windows and SSM states are drawn at
