@@ -1434,9 +1434,13 @@ int tfd_proj8_norm(const TfdProj8NormArgs* args, void* stream) {
   const void* k = t.epilogue == TFD_EPI_STORE
                       ? reinterpret_cast<const void*>(&k_proj8_norm<0, 16>)
                       : reinterpret_cast<const void*>(&k_proj8_norm<1, 16>);
-  // as many blocks as are resident at once, each the same number of tiles
-  static int per_cu[2] = {0, 0};
-  int& pc = per_cu[t.epilogue == TFD_EPI_STORE ? 0 : 1];
+  // as many blocks as are resident at once, each the same number of tiles (the
+  // LDS attribute and the occupancy are set per device)
+  static int per_cu[64][2] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(kUnsupported, "proj8_norm: device %d", dev);
+  int& pc = per_cu[dev][t.epilogue == TFD_EPI_STORE ? 0 : 1];
   if (!pc) {
     if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kP8Lds) !=
         hipSuccess)
