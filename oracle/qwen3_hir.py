@@ -44,6 +44,9 @@ class _Sums:
     the results -- the noise floor a correct implementation must stay within."""
 
     exact = False
+    #: ``exact_products()``: attention's elementwise products are not rounded
+    #: to the model dtype before their sum (see ``_prod_sum``)
+    products = False
 
     def matmul(self, a, b):
         if self.exact:
@@ -68,6 +71,34 @@ def exact_sums():
         yield
     finally:
         _ops.exact = prev
+
+
+@contextmanager
+def exact_products():
+    """Inside the block, attention's q.k and p.v products enter their sums
+    unrounded (taken in f32, where every bf16 x bf16 product is exact) instead of
+    rounded to the model dtype one by one; the sums are rounded to the model
+    dtype as before, and every other op keeps its HIR rounding.  This is the
+    arithmetic of a matrix-core product -- the reference's fast path computes
+    both attention products with ``T.gemm``
+    (``examples/qwen3_1_7b-tilelang/fast/kernels.py:418-501``) -- and the XCD
+    decode kernel's."""
+    prev = _ops.products
+    _ops.products = True
+    try:
+        yield
+    finally:
+        _ops.products = prev
+
+
+def _prod_sum(a, b, dim, keepdim=False):
+    """``_ops.sum(a * b, dim)`` of the HIR (bf16 products, each rounded, summed
+    in f32 and rounded once); under ``exact_products()`` the products are exact
+    and only the sum is rounded to the operands' dtype."""
+    if not _ops.products:
+        return _ops.sum(a * b, dim=dim, keepdim=keepdim)
+    wide = torch.float64 if _ops.exact else torch.float32
+    return (a.to(wide) * b.to(wide)).sum(dim=dim, keepdim=keepdim).to(a.dtype)
 
 
 @dataclass(frozen=True)
@@ -172,8 +203,8 @@ def self_attention(dims: Qwen3Dims, hidden, gamma_in, w_q, w_k, w_v, gamma_q, ga
     v_new = torch.repeat_interleave(v, g, dim=2)
 
     q_e = q_s.reshape(1, 1, hq, 1, d)
-    score_ctx = _ops.sum(q_e * k_ctx, dim=-1, keepdim=True)            # (1,1,hq,ctx,1)
-    score_new = _ops.sum(q_s * k_new, dim=-1, keepdim=True)            # (1,1,hq,1)
+    score_ctx = _prod_sum(q_e, k_ctx, dim=-1, keepdim=True)            # (1,1,hq,ctx,1)
+    score_new = _prod_sum(q_s, k_new, dim=-1, keepdim=True)            # (1,1,hq,1)
     if ctx == 0:
         # reduce.py:124-133: an empty max is the dtype's least representable value
         ctx_max = torch.full((1, 1, hq, 1), float("-inf"), dtype=dt)
@@ -184,7 +215,7 @@ def self_attention(dims: Qwen3Dims, hidden, gamma_in, w_q, w_k, w_v, gamma_q, ga
     p_ctx = torch.exp(score_ctx - peak_e)
     p_new = torch.exp(score_new - peak)
     total = _ops.sum(p_ctx, dim=-2) + p_new
-    weighted = _ops.sum(p_ctx * v_ctx, dim=-2) + p_new * v_new
+    weighted = _prod_sum(p_ctx, v_ctx, dim=-2) + p_new * v_new
     attn = weighted / total
     out = _ops.matmul(attn.reshape(1, 1, hq * d), w_o)
     return out, k_rope, v

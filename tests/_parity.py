@@ -1,5 +1,15 @@
 """Comparison helpers shared by the GPU parity tests (not collected)."""
+import contextlib
+
 import torch
+
+
+def oracle_arith(mode: str):
+    """The oracle arithmetic a Qwen3 engine mode computes: the XCD kernel takes
+    attention's products exactly (``qwen3_hir.exact_products``), the other modes
+    round each one as the HIR does."""
+    from oracle import qwen3_hir as O
+    return O.exact_products() if mode == "xcd" else contextlib.nullcontext()
 
 
 def ulp_bf16(x: torch.Tensor) -> torch.Tensor:

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import qwen3_hir as O
-from tests._parity import report
+from tests._parity import oracle_arith, report
 from tilefoundry_amd.qwen3 import QWEN3_1_7B, TINY, synthetic_weights
 from tilefoundry_amd.qwen3.engine import Engine
 
@@ -177,13 +177,15 @@ def test_persistent_kernel_equals_per_phase_launches(gpu_device, shape):
 
 def test_xcd_kernel_matches_oracle_at_the_layer_shape(gpu_device):
     """The XCD-partitioned persistent kernel (two layers of the Qwen3-1.7B shape)
-    against the oracle's greedy loop: logits within the bf16 bar, free-running
-    tokens identical until a near-tie the measured error explains, teacher-forced
-    picks bounded by each step's error."""
+    against the oracle's greedy loop in the kernel's arithmetic (attention's
+    products exact): logits within the bf16 bar, free-running tokens identical
+    until a near-tie the measured error explains, teacher-forced picks bounded by
+    each step's error."""
     cfg = QWEN3_1_7B.with_(num_hidden_layers=2)
     w = synthetic_weights(cfg, seed=0, norms="ones")
     prompt = _prompt(8, cfg.vocab_size)
-    orc = O.decode(O.Qwen3Oracle(_dims(cfg), w), prompt, 64)
+    with oracle_arith("xcd"):
+        orc = O.decode(O.Qwen3Oracle(_dims(cfg), w), prompt, 64)
     eng = Engine(cfg, w, device=gpu_device, max_new=64, prompt_room=8, mode="xcd")
     run = eng.generate(prompt, 64, record_logits=True)
     k = _check_run(run, orc, 64, strict=False)
@@ -193,10 +195,13 @@ def test_xcd_kernel_matches_oracle_at_the_layer_shape(gpu_device):
 
 
 def test_xcd_kernel_tracks_the_persistent_kernel(gpu_device):
-    """Same weights and prompt: the XCD kernel differs from the chip-wide one only
-    in the f32 order of the o and down sums, so the logits agree to a few bf16
-    ulps of max |logit| and the tokens agree wherever no near-tie is hit; one
-    launch of n steps equals n launches of one step bit for bit."""
+    """Same weights and prompt: the XCD kernel differs from the chip-wide one in
+    the f32 order of the o and down sums and in taking attention's products
+    exactly (the chip-wide kernel rounds each one, as the HIR does), so the
+    logits agree to the north-star bar (2e-2 of max |logit|; cosine >= 0.999,
+    the two arithmetics being a bf16 rounding per product apart) and the tokens
+    agree wherever no near-tie is hit; one launch of n steps equals n launches of
+    one step bit for bit."""
     cfg = QWEN3_1_7B.with_(num_hidden_layers=2)
     w = synthetic_weights(cfg, seed=6, norms="ones")
     prompt = _prompt(12, cfg.vocab_size, seed=9)
@@ -208,7 +213,7 @@ def test_xcd_kernel_tracks_the_persistent_kernel(gpu_device):
     upto = 48 if k is None else k + 1
     for j in range(upto):
         r = report(b.logits[j], a.logits[j])
-        assert r["max_rel"] <= 2e-2 and r["cos"] >= 0.9999, (j, r)
+        assert r["max_rel"] <= 2e-2 and r["cos"] >= 0.999, (j, r)
     c = xcd.generate(prompt, 48)                    # two launches: prompt walk, continuation
     assert c.tokens == b.tokens
     one = [xcd.generate(prompt, 1)]

@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from oracle import qwen3_hir as O
-from tests._parity import assert_close_bf16
+from tests._parity import assert_close_bf16, oracle_arith
 from tests.test_gpu_engine import SMALL, _check_run, _dims, _prompt
 from tilefoundry_amd import _lib
 from tilefoundry_amd.qwen3 import QWEN3_1_7B, synthetic_weights
@@ -87,7 +87,8 @@ def test_prefill_at_the_layer_shape(gpu_device, mode):
     cfg = QWEN3_1_7B.with_(num_hidden_layers=2)
     w = synthetic_weights(cfg, seed=0, norms="ones")
     prompt = _prompt(70, cfg.vocab_size, seed=2)
-    orc = O.decode(O.Qwen3Oracle(_dims(cfg), w), prompt, 32)
+    with oracle_arith(mode):
+        orc = O.decode(O.Qwen3Oracle(_dims(cfg), w), prompt, 32)
     eng = Engine(cfg, w, device=gpu_device, max_new=32, prompt_room=70, mode=mode)
     run = eng.generate(prompt, 32, record_logits=True, prefill=True)
     eng.check_errors()

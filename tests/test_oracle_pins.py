@@ -6,6 +6,9 @@
   (tests/models/decode_oracle.py:126-137, qwen3_1_7b/reference.py:44-70);
 * bf16 attention within bf16 noise of an f64 brute-force softmax
   (fast/arbitrate.py:22-56);
+* the exact-products arithmetic (``exact_products``): equal to the HIR's bit for
+  bit where every product is a bf16 value, within bf16 noise of the HIR on
+  random inputs and not equal to it there (the switch is live);
 * argmax tie rule: first maximal index (tests/ops/test_argmax.py:70-73);
 * RoPE: rotation preserves each pair's norm; position 0 is the identity;
 * cache growth: append_cache grows every layer by one position per step.
@@ -113,6 +116,68 @@ def test_bf16_attention_core_close_to_f64():
     assert rel < 3e-2, rel
     cos_sim = torch.nn.functional.cosine_similarity(got.flatten(), ref.flatten(), 0).item()
     assert cos_sim > 0.999, cos_sim
+
+
+def _attention_case(seed, kc, vc, *, zero_new_key=False):
+    """One layer's self_attention (o_proj the identity) over the given caches."""
+    torch.manual_seed(seed)
+    hq, hkv, d = 4, 2, 64
+    ctx = kc.shape[1]
+    dims = O.Qwen3Dims(hidden=hq * d, heads=hq, kv_heads=hkv, head_dim=d, intermediate=64,
+                       vocab=16, layers=1, dtype=torch.bfloat16)
+    w = synthetic_weights(TINY.with_(dtype=torch.bfloat16, hidden_size=hq * d,
+                                     num_hidden_layers=1, intermediate_size=64, vocab_size=16),
+                          seed=5, norms="ones")
+    w_k = w["layer0.w_k"] * 0 if zero_new_key else w["layer0.w_k"]
+    hidden = (torch.randn(1, 1, hq * d) * 0.5).to(torch.bfloat16)
+    cos, sin = O.generation_rope(dims, 128)
+    pos = torch.tensor([ctx], dtype=torch.int32)
+    scale = torch.full((1, 1, 1, 1), d ** -0.5, dtype=torch.bfloat16)
+    eye = torch.eye(hq * d, dtype=torch.bfloat16).unsqueeze(0)
+    g = lambda n: w[f"layer0.{n}"]  # noqa: E731
+    out, _, _ = O.self_attention(dims, hidden, g("gamma_in"), g("w_q"), w_k, g("w_v"),
+                                 g("gamma_q"), g("gamma_k"), cos, sin, pos, kc, vc, scale, eye)
+    return out
+
+
+def _pow2(shape, gen):
+    """bf16 entries +-2^e (e in -3..2): a bf16 value times one is a bf16 value."""
+    e = torch.randint(-3, 3, shape, generator=gen).float()
+    sign = torch.randint(0, 2, shape, generator=gen).float() * 2 - 1
+    return (sign * torch.exp2(e)).to(torch.bfloat16)
+
+
+def test_exact_products_equal_the_hir_where_products_are_bf16():
+    """With every cache entry a power of two and the new key zero, each q.k and
+    p.v product is itself a bf16 value, so not rounding the products changes
+    nothing: under exact sums the two arithmetics agree bit for bit (a dropped
+    term, a wrong axis or a wrong operand would not)."""
+    gen = torch.Generator().manual_seed(11)
+    kc, vc = _pow2((1, 53, 2, 64), gen), _pow2((1, 53, 2, 64), gen)
+    with O.exact_sums():
+        hir = _attention_case(4, kc, vc, zero_new_key=True)
+        with O.exact_products():
+            ex = _attention_case(4, kc, vc, zero_new_key=True)
+    assert torch.equal(hir, ex)
+    assert hir.abs().max() > 0
+
+
+def test_exact_products_close_to_f64_and_not_the_hir():
+    """On random caches the exact-products chain stays within bf16 noise of the
+    HIR's (which test_bf16_attention_core_close_to_f64 holds to the f64
+    softmax), and differs from it somewhere: the products' rounding is what it
+    leaves out."""
+    gen = torch.Generator().manual_seed(12)
+    kc = torch.randn(1, 61, 2, 64, generator=gen).to(torch.bfloat16)
+    vc = torch.randn(1, 61, 2, 64, generator=gen).to(torch.bfloat16)
+    hir = _attention_case(6, kc, vc).double()
+    with O.exact_products():
+        ex = _attention_case(6, kc, vc).double()
+    assert not torch.equal(hir, ex)
+    rel = ((ex - hir).abs().max() / hir.abs().max()).item()
+    assert rel < 2e-2, rel
+    cos_sim = torch.nn.functional.cosine_similarity(ex.flatten(), hir.flatten(), 0).item()
+    assert cos_sim > 0.9999, cos_sim
 
 
 def test_argmax_first_index_on_ties():

@@ -738,8 +738,15 @@ __device__ __forceinline__ void qk_gammas(const bf16* __restrict__ gq, const bf1
 // (loaded by the caller); with kt1 (and kt2) the caller has also loaded the
 // second (and third), so a split of up to that many tiles waits on no load
 // issued inside this phase.
+//
+// kExact: the products of q_s and K are not rounded one by one; they are taken
+// exactly (bf16 x bf16 fits f32) and summed in f32, as a matrix-core product
+// does (the reference's fast path computes both attention products with
+// T.gemm, examples/qwen3_1_7b-tilelang/fast/kernels.py:418-501).  Every other
+// rounding point stays.  A pair of products is then one bf16 dot instruction
+// on the cache word as loaded, where the rounded form takes five.
 // ---------------------------------------------------------------------------
-template <int D, int G, bool kLL, int kPol = kCoherent, class Grp = BlockGrp>
+template <int D, int G, bool kLL, int kPol = kCoherent, class Grp = BlockGrp, bool kExact = false>
 __device__ __forceinline__ void attn_scores_phase(
     int split, int h, const uint32_t* hs, const QKPre& pre, int rope_rows, int rp, int P,
     const int* __restrict__ page_table, int max_pages, bf16* __restrict__ kpool, bf16* __restrict__ vpool, int num_pages,
@@ -839,8 +846,13 @@ __device__ __forceinline__ void attn_scores_phase(
   if (wave < G) {
     float a = 0.f;
     if (lane < kHalf) {
-      a = rbf(qs[wave][lane] * kn[lane]);
-      a += rbf(qs[wave][lane + kHalf] * kn[lane + kHalf]);
+      if (kExact) {
+        a = qs[wave][lane] * kn[lane];
+        a += qs[wave][lane + kHalf] * kn[lane + kHalf];
+      } else {
+        a = rbf(qs[wave][lane] * kn[lane]);
+        a += rbf(qs[wave][lane + kHalf] * kn[lane + kHalf]);
+      }
     }
     a = wave_sum(a);
     if (lane == 0) {
@@ -856,12 +868,16 @@ __device__ __forceinline__ void attn_scores_phase(
   constexpr int kKL = A::kKLanes;
   const int part = lane % kKL;
   float qv[G][A::kKChunks][8];
+  uint32_t qp[G][A::kKChunks][4];          // kExact: the same dims as bf16 pairs
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int i = 0; i < A::kKChunks; ++i)
+    for (int i = 0; i < A::kKChunks; ++i) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) qv[g][i][e] = qs[g][8 * (kKL * i + part) + e];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qp[g][i][e] = pack2(qv[g][i][2 * e], qv[g][i][2 * e + 1]);
+    }
   float mymax[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) mymax[g] = kNegInf;
@@ -890,8 +906,9 @@ __device__ __forceinline__ void attn_scores_phase(
           const uint32_t kw[4] = {cur.t[p][i].x, cur.t[p][i].y, cur.t[p][i].z, cur.t[p][i].w};
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            a = add_rounded2(a, qv[g][i][2 * e] * bf_lo(kw[e]),
-                             qv[g][i][2 * e + 1] * bf_hi(kw[e]));
+            a = kExact ? dot2(qp[g][i][e], kw[e], a)
+                       : add_rounded2(a, qv[g][i][2 * e] * bf_lo(kw[e]),
+                                      qv[g][i][2 * e + 1] * bf_hi(kw[e]));
         }
         a = group_sum<kKL>(a);
         const float sc = rbf(a);
@@ -987,8 +1004,13 @@ struct RowOut {
 // `polled` runs once this block's waits of the phase are over (the persistent
 // kernel issues weight loads there: memory counters retire in order, so loads
 // issued before a wait would hold it up)
+//
+// kExact: sum_j p_j * V[j][d] with the products exact and summed in f32 (no
+// per-product rounding; see attn_scores_phase): the two positions of a pass
+// pair meet in one bf16 dot instruction, their p_j and their V entries each
+// packed as a pair by one byte permute.
 template <int D, int G, bool kLL, class Hook = NoHook, class OutMap = RowOut,
-          int kPol = kCoherent, class Grp = BlockGrp>
+          int kPol = kCoherent, class Grp = BlockGrp, bool kExact = false>
 __device__ __forceinline__ void attn_pv_phase(
     int split, int h, int nsplit, const bf16* __restrict__ qkv, int P,
     const int* __restrict__ page_table, int max_pages, const bf16* __restrict__ vpool,
@@ -1107,14 +1129,35 @@ __device__ __forceinline__ void attn_pv_phase(
 #pragma unroll
         for (int g = 0; g < G; ++g) pj[u][g] = p[g][jj];   // 0 past the end: exact zeros
       }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
+      if constexpr (kExact) {
+        // (V[j0][d], V[j1][d]) and (V[j0][d+1], V[j1][d+1]) from the two words;
+        // (p_j0, p_j1) from the high halves of the two bf16-valued floats
+        uint32_t vl[4], vh[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          acc[g][2 * e] = add_rounded2(acc[g][2 * e], pj[0][g] * bf_lo(vw[0][e]),
-                                       pj[1][g] * bf_lo(vw[1][e]));
-          acc[g][2 * e + 1] = add_rounded2(acc[g][2 * e + 1], pj[0][g] * bf_hi(vw[0][e]),
-                                           pj[1][g] * bf_hi(vw[1][e]));
+          vl[e] = __builtin_amdgcn_perm(vw[1][e], vw[0][e], 0x05040100u);
+          vh[e] = __builtin_amdgcn_perm(vw[1][e], vw[0][e], 0x07060302u);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const uint32_t pp = __builtin_amdgcn_perm(__float_as_uint(pj[1][g]),
+                                                    __float_as_uint(pj[0][g]), 0x07060302u);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            acc[g][2 * e] = dot2(pp, vl[e], acc[g][2 * e]);
+            acc[g][2 * e + 1] = dot2(pp, vh[e], acc[g][2 * e + 1]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            acc[g][2 * e] = add_rounded2(acc[g][2 * e], pj[0][g] * bf_lo(vw[0][e]),
+                                         pj[1][g] * bf_lo(vw[1][e]));
+            acc[g][2 * e + 1] = add_rounded2(acc[g][2 * e + 1], pj[0][g] * bf_hi(vw[0][e]),
+                                             pj[1][g] * bf_hi(vw[1][e]));
+          }
         }
       }
     }

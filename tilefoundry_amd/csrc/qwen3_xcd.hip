@@ -494,7 +494,7 @@ __device__ __forceinline__ void xcd_steps(const TfdDecodeArgs& a, const TfdXcdAr
           __syncthreads();
           rows_issue<kCH, kRgu, kEarly>(vb_gu, (const bf16*)w.w_gu, kH, 0, we);
           stamp(tl);
-          attn_scores_phase<kD, kG, true, kXcdLocal>(r, x, sm.hs, pre, a.rope_rows, P, P,
+          attn_scores_phase<kD, kG, true, kXcdLocal, BlockGrp, true>(r, x, sm.hs, pre, a.rope_rows, P, P,
                                                      a.page_table, a.max_pages, (bf16*)w.k_pool,
                                                      (bf16*)w.v_pool, a.num_pages, 8, a.scale,
                                                      eps, sm.s_sc, 0, nullptr, sm.s_new, ll, kt,
@@ -502,7 +502,7 @@ __device__ __forceinline__ void xcd_steps(const TfdDecodeArgs& a, const TfdXcdAr
           stamp(tl);
           // ---- part 2: P.V partials
           stamp(tl);
-          attn_pv_phase<kD, kG, true, NoHook, RowOut, kXcdLocal>(
+          attn_pv_phase<kD, kG, true, NoHook, RowOut, kXcdLocal, BlockGrp, true>(
               r, x, a.nsplit, nullptr, P, a.page_table, a.max_pages, (const bf16*)w.v_pool,
               a.num_pages, 8, sm.s_sc, 0, nullptr, sm.s_new, nullptr, nullptr, nullptr, nullptr,
               ll, vt, err, ct, NoHook{}, RowOut{}, &vt1, &vt2);
