@@ -213,10 +213,15 @@ __global__ __launch_bounds__(kBlock) void k_gqa_scores(GqaArgs a) {
 #pragma unroll
       for (int g = 0; g < kG; ++g) {
         acc[g] = 0.f;
+        if constexpr (kF32) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float prod = qr[g][e] * kv[e];
-          acc[g] += kF32 ? prod : rbf(prod);
+          for (int e = 0; e < 8; ++e) acc[g] += qr[g][e] * kv[e];
+        } else {
+          // each product rounded to bf16, two at a time by one convert, and
+          // both added by one bf16 dot against (1, 1)
+#pragma unroll
+          for (int e = 0; e < 8; e += 2)
+            acc[g] = add_rounded2(acc[g], qr[g][e] * kv[e], qr[g][e + 1] * kv[e + 1]);
         }
         acc[g] = group_sum<kLpp>(acc[g]);
       }
@@ -297,20 +302,38 @@ __global__ __launch_bounds__(kBlock) void k_gqa_pv(GqaArgs a) {
       const int jj = min(jb + u * kPpi + pg, n - 1);
       vw[u] = load16(a.vpool + page_row(pg_s[jj / kPage], j0 + jj, a.hkv, kvh, kD) + li * 8);
     }
+    if constexpr (kF32) {
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int jj = jb + u * kPpi + pg;
-      if (jj < n) {
-        float v[8];
-        unpack8(vw[u], v);
+      for (int u = 0; u < kU; ++u) {
+        const int jj = jb + u * kPpi + pg;
+        if (jj < n) {
+          float v[8];
+          unpack8(vw[u], v);
+#pragma unroll
+          for (int g = 0; g < kG; ++g) {
+            const float p = p_s[g][jj];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[g][e] += p * v[e];
+          }
+        }
+      }
+    } else {
+      // positions u and u + 1 in pairs: their rounded products p * v meet in
+      // one convert and one bf16 dot; a position past the split has p = 0
+      // (its row, a re-read of the split's last, is finite)
+      static_assert(kU % 2 == 0, "positions pair up");
+#pragma unroll
+      for (int u = 0; u < kU; u += 2) {
+        const int ja = jb + u * kPpi + pg, jb2 = ja + kPpi;
+        float va[8], vb[8];
+        unpack8(vw[u], va);
+        unpack8(vw[u + 1], vb);
 #pragma unroll
         for (int g = 0; g < kG; ++g) {
-          const float p = p_s[g][jj];
+          const float pa = ja < n ? p_s[g][ja] : 0.f;
+          const float pb = jb2 < n ? p_s[g][jb2] : 0.f;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float prod = p * v[e];
-            acc[g][e] += kF32 ? prod : rbf(prod);
-          }
+          for (int e = 0; e < 8; ++e) acc[g][e] = add_rounded2(acc[g][e], pa * va[e], pb * vb[e]);
         }
       }
     }
