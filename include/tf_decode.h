@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TFD_ABI_VERSION 15
+#define TFD_ABI_VERSION 16
 
 /* gemv prologues / epilogues */
 #define TFD_PRO_PLAIN 0  /* x used as given */
@@ -214,6 +214,33 @@ int tfd_attn_pv_combine_paged_batched(
     const float* scores, int score_stride, const float* split_max, const float* score_new,
     float* part_sum, float* part_out, int nsplit, int split_tiles, int32_t* counters,
     void* attn_out, int32_t* err, void* stream);
+
+/* Sampling a token per row of f32 logits (rows <= 65535, vocab <= TFD_SAMPLE_MAX_VOCAB),
+ * on the device, in place of tfd_argmax_rows.  Replaces the reference's two samplers:
+ *   top_k in 1..TFD_SAMPLE_MAX_K: the top k logits (ties to the lower index), divided by
+ *     `temperature`, softmax over the k, the nucleus of mass `top_p` inside them (the
+ *     tokens up to and including the one that crosses it, at least one), then one
+ *     categorical draw (examples/qwen3_5_35b_a3b-tilelang/run.py:145-180);
+ *   top_k = 0 (top_p must be 1): softmax(logits / temperature) over the whole row, by
+ *     Gumbel-max (examples/granite_4_0_h_small-cuda/kernels/granite.cu:716-800).
+ * The random numbers are a counter-based hash of (seed, row, counter[row], element):
+ * pass each row's position (a device array the step advances) so that a captured graph
+ * draws anew on every replay; NULL counts as 0.  NaN logits are never picked (an all-NaN
+ * row picks 0).  `work`: tfd_sample_work_bytes(rows, vocab, top_k) bytes of device
+ * memory, contents free.  Errors: kBadArg (null pointer, temperature <= 0, top_k out
+ * of range, top_p outside (0, 1], or top_p < 1 with top_k = 0), kBadShape. */
+#define TFD_SAMPLE_MAX_K 64
+#define TFD_SAMPLE_MAX_VOCAB 262144
+typedef struct TfdSampling {
+  float temperature;
+  int top_k;
+  float top_p;
+  uint64_t seed;
+} TfdSampling;
+int64_t tfd_sample_work_bytes(int rows, int vocab, int top_k);
+int tfd_sample_rows(const float* logits, int ldl, int rows, int vocab,
+                    const TfdSampling* sampling, const int32_t* counter, int32_t* pick,
+                    void* work, int64_t work_bytes, void* stream);
 
 /* Greedy pick per row: the first maximal logit (ref_src/generation.py:24-26).  With
  * `work` (rows * TFD_ARGMAX_WORK int32) the rows are scanned by 64 blocks each and the

@@ -13,6 +13,15 @@ Qwen3.5-MoE or Granite-4.0-H).  Without a checkpoint, ``--synthetic`` builds
 random-init weights of a benchmark configuration (C1/C2 for Qwen3, C4, C5) and
 the prompt comes as ids (``--prompt-ids``) or a seeded random draw
 (``--random-prompt``); the continuation is then printed as ids.
+
+Tokens are greedy unless ``--sample`` is given: then they are drawn on the device
+(``tilefoundry_amd.sampling``) with the reference runtimes' defaults -- Qwen3.5's
+published top-k 20 / top-p 0.95 at temperature 1.0
+(``examples/qwen3_5_35b_a3b-tilelang/run.py:145-180``), Granite's softmax over
+the whole vocabulary at temperature 1.0 (``examples/granite_4_0_h_small-cuda/
+run.py:21-28``) -- which ``--temperature``, ``--top-k`` (0: the whole
+vocabulary), ``--top-p`` and ``--sample-seed`` override.  Qwen3 (greedy only in
+its reference) samples through the batched engine with one sequence.
 """
 from __future__ import annotations
 
@@ -100,11 +109,29 @@ def xcd_fits(cfg, device) -> bool:
     return shape and torch.cuda.get_device_properties(device).multi_processor_count == 256
 
 
+#: --sample's defaults per model (the reference runtimes' own)
+SAMPLE_DEFAULTS = {"qwen3": (1.0, 20, 0.95), "qwen3_5": (1.0, 20, 0.95),
+                   "granite": (1.0, 0, 1.0)}
+
+
+def sampling_of(args, model: str):
+    """The Sampling the flags ask for, or None (greedy)."""
+    if not args.sample:
+        return None
+    from tilefoundry_amd.sampling import Sampling
+
+    t, k, p = SAMPLE_DEFAULTS[model]
+    return Sampling(temperature=t if args.temperature is None else args.temperature,
+                    top_k=k if args.top_k is None else args.top_k,
+                    top_p=p if args.top_p is None else args.top_p, seed=args.sample_seed)
+
+
 def build(args, model: str, device: str):
     """(make(prompt_len) -> engine, run(engine, prompt) -> (tokens, seconds of the
     continuation, seconds of the prompt walk), vocab, step mode)."""
     import torch
 
+    sampling = sampling_of(args, model)
     if model == "qwen3":
         from tilefoundry_amd.qwen3 import QWEN3_1_7B, TINY, synthetic_weights
         from tilefoundry_amd.qwen3.engine import Engine
@@ -117,8 +144,20 @@ def build(args, model: str, device: str):
             # C1 is the reference's small CPU case; the engine computes in bf16
             cfg = QWEN3_1_7B if args.synthetic == "c2" else TINY.with_(dtype=torch.bfloat16)
             w = synthetic_weights(cfg, seed=args.seed)
-        mode = args.mode or ("xcd" if xcd_fits(cfg, device) else "persistent")
         room = args.prompt_room
+        if sampling is not None:
+            from tilefoundry_amd.qwen3.batch_engine import BatchEngine
+
+            def make_batch(prompt_len):
+                return BatchEngine(cfg, w, batch=1, device=device, max_new=args.max_new_tokens,
+                                   prompt_room=max(room, prompt_len + 8), sampling=sampling)
+
+            def run_batch(eng, prompt):
+                r = eng.generate([prompt], args.max_new_tokens, prefill=args.prefill)
+                return r.tokens[0], r.seconds, r.prefill_seconds
+
+            return make_batch, run_batch, cfg.vocab_size, "batch, sampled"
+        mode = args.mode or ("xcd" if xcd_fits(cfg, device) else "persistent")
 
         def make(prompt_len):
             return Engine(cfg, w, device=device, max_new=args.max_new_tokens,
@@ -154,14 +193,14 @@ def build(args, model: str, device: str):
 
     def make(prompt_len):
         return engine_cls(cfg, w, rows=1, device=device,
-                          max_steps=prompt_len + args.max_new_tokens + 8)
+                          max_steps=prompt_len + args.max_new_tokens + 8, sampling=sampling)
 
     def run(eng, prompt):
         t0 = perf_counter()
         tokens, seconds, _ = eng.generate([prompt], args.max_new_tokens)
         return tokens[0], seconds, perf_counter() - t0 - seconds
 
-    return make, run, cfg.vocab, "graph"
+    return make, run, cfg.vocab, "graph" if sampling is None else "graph, sampled"
 
 
 def main(argv: list[str] | None = None) -> int:
@@ -188,7 +227,19 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--prefill", action="store_true",
                     help="Qwen3: fill the prompt's cache in batched passes (32 positions per "
                          "pass) instead of walking it one decode step per token")
+    ap.add_argument("--sample", action="store_true",
+                    help="draw tokens instead of taking the largest logit (the model's "
+                         "reference defaults unless the flags below say otherwise)")
+    ap.add_argument("--temperature", type=float, default=None, help="--sample: temperature")
+    ap.add_argument("--top-k", type=int, default=None,
+                    help="--sample: candidates (1..64; 0: the whole vocabulary)")
+    ap.add_argument("--top-p", type=float, default=None,
+                    help="--sample: nucleus mass inside the top k")
+    ap.add_argument("--sample-seed", type=int, default=0, help="--sample: seed of the draws")
     args = ap.parse_args(argv)
+    if not args.sample and any(v is not None for v in (args.temperature, args.top_k,
+                                                       args.top_p)):
+        raise SystemExit("--temperature / --top-k / --top-p need --sample")
     if args.max_new_tokens < 1:
         raise SystemExit("--max-new-tokens must be at least 1")
     if args.synthetic in ("c4", "c5"):

@@ -41,7 +41,8 @@ def test_header_constants_match_binding():
              "EPI_LOGITS", "ERR_TOKEN_RANGE", "ERR_POS_RANGE", "ERR_PAGE_RANGE",
              "ERR_STEP_RANGE", "ERR_SYNC", "ERR_PLACEMENT", "PAGE_SIZE", "ATTN_SPLIT", "SKINNY_COUNTERS", "EPI_RESID_F32",
              "ROUTE_SOFTMAX_TOPK", "ROUTE_TOPK_SOFTMAX", "POLICY_F32", "POLICY_BF16",
-             "MOE_ROUTE_GIVEN", "MOE_ROUTE_SOFTMAX_TOPK", "MOE_ROUTE_TOPK_SOFTMAX"}
+             "MOE_ROUTE_GIVEN", "MOE_ROUTE_SOFTMAX_TOPK", "MOE_ROUTE_TOPK_SOFTMAX",
+             "SAMPLE_MAX_K", "SAMPLE_MAX_VOCAB"}
     assert names <= set(defines), names - set(defines)
     for name in names:
         assert getattr(_lib, name) == int(defines[name]), name
@@ -62,7 +63,8 @@ STRUCTS = {"TfdDecodeArgs": _lib.TfdDecodeArgs, "TfdLayer": _lib.TfdLayer,
            "TfdXcdArgs": _lib.TfdXcdArgs, "TfdConvStepArgs": _lib.TfdConvStepArgs,
            "TfdDeltaStepArgs": _lib.TfdDeltaStepArgs, "TfdPartialRopeArgs": _lib.TfdPartialRopeArgs,
            "TfdSsmStepArgs": _lib.TfdSsmStepArgs, "TfdGatedNormArgs": _lib.TfdGatedNormArgs,
-           "TfdRowGemvArgs": _lib.TfdRowGemvArgs}
+           "TfdRowGemvArgs": _lib.TfdRowGemvArgs, "TfdProj8NormArgs": _lib.TfdProj8NormArgs,
+           "TfdSampling": _lib.TfdSampling}
 
 
 @pytest.mark.skipif(shutil.which("gcc") is None, reason="no C compiler")

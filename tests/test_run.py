@@ -82,3 +82,46 @@ def test_synthetic_weights_and_random_prompt(gpu_device, capsys):
     out = capsys.readouterr().out.splitlines()
     assert len(out[0].split()) == 16 and all(0 <= int(t) < CFG.vocab_size for t in out[0].split())
     assert "qwen3 (persistent)" in out[3]          # C1's shape is not the XCD kernel's
+
+
+def test_sampling_flags():
+    """--temperature / --top-k / --top-p need --sample; --sample takes each model's
+    reference defaults, which the flags override; out-of-range values refuse."""
+    with pytest.raises(SystemExit, match="need --sample"):
+        R.main(["--synthetic", "c1", "--random-prompt", "4", "--top-k", "5"])
+
+    class A:
+        sample, temperature, top_k, top_p, sample_seed = True, None, None, None, 3
+    s = R.sampling_of(A, "qwen3_5")
+    assert (s.temperature, s.top_k, s.top_p, s.seed) == (1.0, 20, 0.95, 3)
+    s = R.sampling_of(A, "granite")
+    assert (s.top_k, s.top_p) == (0, 1.0)
+    A.temperature, A.top_k = 0.5, 8
+    s = R.sampling_of(A, "granite")
+    assert (s.temperature, s.top_k) == (0.5, 8)
+    A.top_k = 65
+    with pytest.raises(ValueError):
+        R.sampling_of(A, "qwen3")
+    A.sample = False
+    assert R.sampling_of(A, "qwen3") is None
+
+
+@pytest.mark.gpu
+def test_sampled_run_is_the_batch_engine_with_one_sequence(gpu_device, capsys):
+    """--sample on Qwen3 runs the batched engine with one sequence: its tokens are
+    those BatchEngine gives with the same sampling, and a second seed differs."""
+    from tilefoundry_amd.qwen3.batch_engine import BatchEngine
+    from tilefoundry_amd.sampling import Sampling
+
+    argv = ["--synthetic", "c1", "--prompt-ids", "5,17,300,9", "--max-new-tokens", "16",
+            "--device", gpu_device, "--sample", "--top-k", "20", "--temperature", "1.3"]
+    assert R.main(argv + ["--sample-seed", "7"]) == 0
+    out = capsys.readouterr().out.splitlines()
+    got = [int(t) for t in out[0].split()]
+    assert "qwen3 (batch, sampled)" in out[3]
+    w = synthetic_weights(CFG, seed=0)
+    eng = BatchEngine(CFG, w, batch=1, device=gpu_device, max_new=16, prompt_room=64,
+                      sampling=Sampling(temperature=1.3, top_k=20, top_p=0.95, seed=7))
+    assert got == eng.generate([[5, 17, 300, 9]], 16).tokens[0]
+    assert R.main(argv + ["--sample-seed", "8"]) == 0
+    assert [int(t) for t in capsys.readouterr().out.splitlines()[0].split()] != got

@@ -13,7 +13,7 @@ from pathlib import Path
 
 from .build import LIB
 
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 PRO_PLAIN, PRO_NORM = 0, 1
 EPI_STORE, EPI_RESID, EPI_SWIGLU, EPI_LOGITS, EPI_RESID_F32 = 0, 1, 2, 3, 4
@@ -39,6 +39,8 @@ MOE_ROUTE_GIVEN, MOE_ROUTE_SOFTMAX_TOPK, MOE_ROUTE_TOPK_SOFTMAX = 0, 1, 2
 
 #: tfd_proj8_norm's sizes: rows <= PROJ8_ROWS, K == PROJ8_K
 PROJ8_ROWS, PROJ8_K = 8, 4096
+#: tfd_sample_rows' limits: top_k <= SAMPLE_MAX_K, vocab <= SAMPLE_MAX_VOCAB
+SAMPLE_MAX_K, SAMPLE_MAX_VOCAB = 64, 262144
 
 
 def moe_packed_fits(rows: int, k: int, hidden: int, inter: int, shared_inter: int) -> bool:
@@ -76,6 +78,8 @@ SIGNATURES: dict[str, list] = {
                                            F, P, I, P, P, I, I, P, P],
     "tfd_attn_pv_combine_paged_batched": [P, I, P, P, I, P, I, I, I, I, I, P, I, P, P, P, P, I,
                                           I, P, P, P, P],
+    "tfd_sample_work_bytes": [I, I, I],
+    "tfd_sample_rows": [P, I, I, I, P, P, P, P, L, P],
     "tfd_argmax_rows": [P, I, I, I, P, P, P],
     "tfd_finalize_rows": [P, I, P, I, P, P, P, P, I, I, P, P, I, I, I, P, P],
     "tfd_embed_rows_bf16": [P, P, P, I, I, I, I, P, P],
@@ -109,7 +113,7 @@ SIGNATURES: dict[str, list] = {
     "tfd_gdn_step_cols": [P, P, I, P],
     "tfd_moe_experts_small": [P, P],
 }
-RESTYPES = {"tfd_last_error": ctypes.c_char_p}
+RESTYPES = {"tfd_last_error": ctypes.c_char_p, "tfd_sample_work_bytes": ctypes.c_int64}
 UNCHECKED = {"tfd_abi_version", "tfd_decode_persistent_grid"}
 
 
@@ -133,6 +137,13 @@ class TfdMoeArgs(ctypes.Structure):
         ("logits", c_void_p), ("ldl", c_int), ("route", c_int),
         ("err", c_void_p), ("resid", c_void_p), ("resid_mult", c_float),
     ]
+
+
+class TfdSampling(ctypes.Structure):
+    """include/tf_decode.h TfdSampling (tfd_sample_rows): top_k 0 samples the whole
+    row by Gumbel-max, 1..SAMPLE_MAX_K the top k with the top_p nucleus."""
+    _fields_ = [("temperature", c_float), ("top_k", c_int), ("top_p", c_float),
+                ("seed", ctypes.c_uint64)]
 
 
 class TfdProj8NormArgs(ctypes.Structure):

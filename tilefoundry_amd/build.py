@@ -20,7 +20,7 @@ ARCH = "gfx950"
 #: Sources linked into the library; every header under csrc/ and include/ is a
 #: dependency of all of them.
 SOURCES = ["qwen3_decode.hip", "qwen3_xcd.hip", "qwen3_batch.hip", "hybrid.hip",
-           "gqa_hybrid.hip", "twin_ops.hip", "hybrid_small.hip"]
+           "gqa_hybrid.hip", "twin_ops.hip", "hybrid_small.hip", "sample.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

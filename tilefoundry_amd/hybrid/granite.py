@@ -32,6 +32,7 @@ import torch
 
 from .. import _lib
 from .._lib import lib, ptr
+from ..sampling import Picker, Sampling
 from .qwen3_5 import ctypes_addr
 
 BF = torch.bfloat16
@@ -196,11 +197,13 @@ class GraniteEngine:
 
     def __init__(self, cfg: GraniteConfig, weights: dict[str, torch.Tensor], *, rows: int,
                  device: str = "cuda:0", max_steps: int = 1024, page_seed: int = 0,
-                 split_len: int = 256, graph: bool = True, record_routes: bool = False):
+                 split_len: int = 256, graph: bool = True, record_routes: bool = False,
+                 sampling: Sampling | None = None):
         if not 1 <= rows <= 32:
             raise ValueError("rows: 1..32 sequences")
         self.cfg, self.B, self.device = cfg, rows, device
         self._lib = lib()
+        self.sampling = sampling                # the token choice (None: greedy)
         self.nsteps = max_steps
         self.split_len = split_len
         # up to 16 sequences: the fp8 experts packed for the matrix-core pair
@@ -309,7 +312,7 @@ class GraniteEngine:
         self.counters = z(B * cfg.kv_heads, dtype=I32)
         self.logits = z(B, V)
         self.pick = z(B, dtype=I32)
-        self.argmax_work = z(B * _lib.ARGMAX_WORK, dtype=I32)
+        self.picker = Picker(self.sampling, B, V, dev)
         self.ids = z(B, dtype=torch.int64)
         self.pos = z(B, dtype=I32)
         self.inp = z(B, self.nsteps, dtype=I32)
@@ -430,7 +433,7 @@ class GraniteEngine:
         L.tfd_gemm_skinny_bf16_logits_div(ptr(self.xn), ptr(self.head), B, H, V,
                                           cfg.logits_scaling, ptr(self.logits), V,
                                           ptr(self.work), self.work.numel(), s)
-        L.tfd_argmax_rows(ptr(self.logits), V, B, V, ptr(self.pick), ptr(self.argmax_work), s)
+        self.picker(self.logits, V, self.pick, self.pos, s)
         L.tfd_finalize_rows(ptr(self.pick), B, ptr(self.inp), self.nsteps, ptr(self.plen),
                             ptr(self.ids), ptr(self.pos), ptr(self.sam), self.nsteps,
                             self.nsteps, ptr(self.embed), ptr(self.emb), H, H, V, ptr(self.err),
@@ -535,8 +538,9 @@ class GraniteEngine:
             raise RuntimeError(f"hybrid decode kernels raised error bits {e:#x}")
 
     def generate(self, prompts: list[list[int]], max_new: int, record_logits: bool = False):
-        """Walk every prompt and continue for *max_new* greedy tokens per sequence
-        (the walk untimed) -> (tokens per sequence, seconds, logits per step)."""
+        """Walk every prompt and continue for *max_new* tokens per sequence
+        (greedy, or drawn as the engine's ``sampling`` says; the walk untimed)
+        -> (tokens per sequence, seconds, logits per step)."""
         if len(prompts) != self.B or any(len(p) < 1 for p in prompts):
             raise ValueError(f"need {self.B} non-empty prompts")
         longest = max(len(p) for p in prompts)

@@ -35,6 +35,7 @@ import torch
 
 from .. import _lib
 from .._lib import lib, ptr
+from ..sampling import Picker, Sampling
 
 BF = torch.bfloat16
 F32 = torch.float32
@@ -184,11 +185,13 @@ class Qwen35Engine:
     def __init__(self, cfg: Qwen35Config, weights: dict[str, torch.Tensor], *, rows: int,
                  device: str = "cuda:0", max_steps: int = 2112, page_seed: int = 0,
                  split_len: int = 64, graph: bool = True, small: bool | None = None,
-                 record_routes: bool = False):
+                 record_routes: bool = False,
+                 sampling: Sampling | None = None):
         if not 1 <= rows <= 32:
             raise ValueError("rows: 1..32 sequences")
         self.cfg, self.B, self.device = cfg, rows, device
         self._lib = lib()
+        self.sampling = sampling                # the token choice (None: greedy)
         # the small-batch path (rows <= 4): row GEMVs on row-major weights with
         # the norms as prologues, the delta rule over value columns, the
         # experts in two launches (tfd_rowgemv_bf16, tfd_gdn_step_cols,
@@ -294,7 +297,7 @@ class Qwen35Engine:
         # head, pick, token feed
         self.logits = z(B, V)
         self.pick = z(B, dtype=I32)
-        self.argmax_work = z(B * _lib.ARGMAX_WORK, dtype=I32)
+        self.picker = Picker(self.sampling, B, V, dev)
         self.ids = z(B, dtype=torch.int64)
         self.pos = z(B, dtype=I32)
         self.inp = z(B, self.nsteps, dtype=I32)
@@ -442,7 +445,7 @@ class Qwen35Engine:
             L.tfd_rmsnorm_f32_rows(ptr(self.hidden), H, ptr(self.gamma_final), None, 0,
                                    ptr(self.xn), B, H, cfg.eps, s)
             self._gemm(self.xn, self.head, H, V, self.logits, V, s)
-        L.tfd_argmax_rows(ptr(self.logits), V, B, V, ptr(self.pick), ptr(self.argmax_work), s)
+        self.picker(self.logits, V, self.pick, self.pos, s)
         L.tfd_finalize_rows(ptr(self.pick), B, ptr(self.inp), self.nsteps, ptr(self.plen),
                             ptr(self.ids), ptr(self.pos), ptr(self.sam), self.nsteps,
                             self.nsteps, ptr(self.embed), ptr(self.emb), H, H, V, ptr(self.err),
@@ -520,9 +523,10 @@ class Qwen35Engine:
             raise RuntimeError(f"hybrid decode kernels raised error bits {e:#x}")
 
     def generate(self, prompts: list[list[int]], max_new: int, record_logits: bool = False):
-        """Walk every prompt and continue for *max_new* greedy tokens per sequence
-        (the prompt walk is untimed).  -> (tokens per sequence, seconds of the
-        timed steps, logits [steps][rows][V] when recorded)."""
+        """Walk every prompt and continue for *max_new* tokens per sequence
+        (greedy, or drawn as the engine's ``sampling`` says; the prompt walk is
+        untimed).  -> (tokens per sequence, seconds of the timed steps, logits
+        [steps][rows][V] when recorded)."""
         if len(prompts) != self.B or any(len(p) < 1 for p in prompts):
             raise ValueError(f"need {self.B} non-empty prompts")
         longest = max(len(p) for p in prompts)

@@ -22,6 +22,7 @@ import torch
 
 from .. import _lib
 from .._lib import lib, ptr
+from ..sampling import Picker, Sampling
 from .config import Qwen3Config
 from .engine import bf16_scale, scatter_cache
 from .weights import head_rows, pack_layer, validate
@@ -54,9 +55,11 @@ class BatchEngine:
 
     def __init__(self, cfg: Qwen3Config, weights: dict[str, torch.Tensor], *, batch: int,
                  device: str = "cuda:0", max_new: int = 256, prompt_room: int = 4096,
-                 page_seed: int | None = 0, graph: bool = True, split_tiles: int | None = None):
+                 page_seed: int | None = 0, graph: bool = True, split_tiles: int | None = None,
+                 sampling: Sampling | None = None):
         """*split_tiles*: 64-position tiles per attention split (default: about 16
-        splits per sequence and kv head at full capacity)."""
+        splits per sequence and kv head at full capacity).  *sampling*: the
+        token choice (``tilefoundry_amd.sampling.Sampling``; None: greedy)."""
         if cfg.dtype != torch.bfloat16:
             raise ValueError(f"the HIP engine runs bf16 weights; config has {cfg.dtype}")
         if not 1 <= batch <= MAX_BATCH:
@@ -85,6 +88,7 @@ class BatchEngine:
             raise ValueError(f"capacity {self.cap} exceeds the rope table "
                              f"({cfg.max_position_embeddings} positions)")
         self._lib = lib()
+        self.sampling = sampling
         self._pack(weights, page_seed)
         self._buffers()
         self.graph = None
@@ -151,7 +155,7 @@ class BatchEngine:
         self.counters = z(B, self.HKV, dtype=i32)
         self.logits = z(B, self.V, dtype=f32)
         self.pick = z(B, dtype=i32)
-        self.argmax_work = z(B * _lib.ARGMAX_WORK, dtype=i32)
+        self.picker = Picker(self.sampling, B, self.V, self.device)
         self.pos = z(B, dtype=i32)
         self.ids = z(B, dtype=torch.int64)
         self.inp = z(B, self.nsteps, dtype=i32)
@@ -210,8 +214,7 @@ class BatchEngine:
                                 ptr(self.xn), 0, B, H, self.eps, 1, s)
         self._gemm(self.xn, self.w_head, H, self.V, _lib.EPI_LOGITS, None, self.logits,
                    self.V, s)
-        L.tfd_argmax_rows(ptr(self.logits), self.V, B, self.V, ptr(self.pick),
-                          ptr(self.argmax_work), s)
+        self.picker(self.logits, self.V, self.pick, self.pos, s)
         L.tfd_finalize_rows(ptr(self.pick), B, ptr(self.inp), self.nsteps, ptr(self.plen),
                             ptr(self.ids), ptr(self.pos), ptr(self.sam), self.nsteps,
                             self.nsteps, ptr(self.w_embed), ptr(self.hid), H, H, self.V,
@@ -314,9 +317,10 @@ class BatchEngine:
 
     def generate(self, prompts: list[list[int]], max_new: int, record_logits: bool = False,
                  prefill: bool = False) -> BatchGenerated:
-        """Walk every prompt, then continue for *max_new* greedy tokens per
-        sequence.  Sequence b's continuation starts after its own prompt; all
-        sequences step together, so the step count is max(prompt) - 1 + max_new,
+        """Walk every prompt, then continue for *max_new* tokens per sequence
+        (greedy, or drawn as the engine's ``sampling`` says).  Sequence b's
+        continuation starts after its own prompt; all sequences step together,
+        so the step count is max(prompt) - 1 + max_new,
         and the timing covers the steps after the longest prompt.  With
         *prefill*, every prompt but its last token goes through ``prefill`` and
         all sequences decode their last prompt token in the first step: max_new
