@@ -1,6 +1,6 @@
 """Regenerate the committed golden fixtures (CPU, minutes at C2 size).
 
-    python tests/golden/make_golden.py [c1] [c2] [c2x] [c2xs]
+    python tests/golden/make_golden.py [c1] [c2] [c2x] [c2xs] [c2xp]
 
 c1_tiny_fp32.json   workload C1: tiny Qwen3 (2 layers, hidden 256, 4q/2kv,
                     head_dim 64, I 768, V 4096), fp32, every parameter N(0, 0.02)
@@ -22,6 +22,12 @@ c2_*_exact_step*.npy  (target c2x) the same two steps teacher-forced on the
                     implementation can be asked to match.
 c2_*_exact_steps.npz  (target c2xs) the exact-sum logits at steps 0, 8, ...,
                     56 and 63 of the same teacher-forced walk (keys step<k>).
+c2_*_exactprod_steps.npz  (target c2xp) the same steps of the same walk in the
+                    exact-products arithmetic (oracle.exact_products: attention's
+                    q.k and p.v products not rounded before their sums, the XCD
+                    kernel's), with exact sums; c2_order_noise_exactprod.json
+                    records how far that arithmetic's own f32 sums sit from it at
+                    steps 0 and 63.
 
 The fixtures are data (inputs and expected outputs), regenerated from seeds.
 """
@@ -164,8 +170,45 @@ def make_c2xs():
         del w
 
 
+def make_c2xp():
+    """c2_*_exactprod_steps.npz and c2_order_noise_exactprod.json: the walk of
+    make_c2xs in the exact-products arithmetic, with exact sums (the reference
+    values) and with the oracle's f32 sums at steps 0 and 63 (their distance from
+    the reference values is that arithmetic's summation-order noise)."""
+    fx = json.loads((HERE / "c2_qwen3_1p7b.json").read_text())
+    prompt = fx["prompt"]
+    pl = len(prompt)
+    noise = {}
+    for norms in ("random", "ones"):
+        t0 = time.time()
+        w = synthetic_weights(QWEN3_1_7B, seed=0, norms=norms)
+        seq = prompt + fx[norms]["tokens"][:63]
+        with O.exact_products():
+            with O.exact_sums():
+                ex = forced_logits(O.Qwen3Oracle(O.C2, w), seq,
+                                   {pl - 1 + k for k in EXACT_STEPS})
+            f32 = forced_logits(O.Qwen3Oracle(O.C2, w), seq, {pl - 1, pl - 1 + 63})
+        arrays = {}
+        for k in EXACT_STEPS:
+            arrays[f"step{k}"] = (ex[pl - 1 + k].to(torch.bfloat16).view(torch.int16).numpy()
+                                  .astype(np.uint16))
+        np.savez_compressed(HERE / f"c2_{norms}_exactprod_steps.npz", **arrays)
+        noise[norms] = {}
+        for k in (0, 63):
+            ref = ex[pl - 1 + k].to(torch.bfloat16).float()
+            orc = f32[pl - 1 + k].to(torch.bfloat16).float()
+            d = (orc - ref).abs()
+            noise[norms][f"step{k}"] = {"max_abs": float(d.max()), "mean_abs": float(d.mean()),
+                                       "max_logit": float(ref.abs().max())}
+        print(f"c2xp {norms}: {time.time() - t0:.0f}s {noise[norms]}", flush=True)
+        del w
+    (HERE / "c2_order_noise_exactprod.json").write_text(json.dumps(noise, indent=1))
+
+
 if __name__ == "__main__":
     which = sys.argv[1:] or ["c1", "c2", "c2x"]
+    if "c2xp" in which:
+        make_c2xp()
     if "c2xs" in which:
         make_c2xs()
     if "c1" in which:

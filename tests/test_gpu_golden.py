@@ -19,6 +19,11 @@ largest logit, above the 2e-2 bar, because every layer's bf16 roundings
 amplify one-ulp flips.  So the bound is max(2e-2 * max|logit|, 2 * noise): the
 engine must be as close to the exact result as the torch evaluator is, within a
 factor of two, and never worse than the bar where the noise is below it.
+
+The XCD kernel takes attention's products exactly (oracle.exact_products): it
+is held to the exact-sum evaluation of that arithmetic
+(c2_*_exactprod_steps.npz) at twice that arithmetic's own f32 noise
+(c2_order_noise_exactprod.json), and to the HIR's exact sums at the HIR's bound.
 """
 import json
 from pathlib import Path
@@ -45,6 +50,12 @@ def _golden_logits(norms, k):
 def _bf16_npy(name):
     raw = np.load(GOLDEN / name)
     return torch.from_numpy(raw.astype(np.int16)).view(torch.bfloat16).float()
+
+
+def _exact_steps(norms, kind):
+    with np.load(GOLDEN / f"c2_{norms}_{kind}_steps.npz") as z:
+        return {int(n[4:]): torch.from_numpy(z[n].astype(np.int16)).view(torch.bfloat16).float()
+                for n in z.files}
 
 
 def _top8_error(logits, top8):
@@ -77,24 +88,30 @@ def test_c2_full_depth_against_golden(gpu_device, norms):
             print(f"  step {k}: max|engine-exact| {err_exact:.4g}, max|oracle-exact| {noise:.4g}, "
                   f"max|engine-oracle| {err_oracle:.4g}; bound {bound:.4g}", flush=True)
             assert err_exact <= bound, (mode, k, err_exact, bound)
-        # every 8th step against the exact sums, the bound as above with the
-        # oracle's noise of steps 0 and 63
-        with np.load(GOLDEN / f"c2_{norms}_exact_steps.npz") as z:
-            exact_steps = {int(n[4:]): torch.from_numpy(z[n].astype(np.int16))
-                           .view(torch.bfloat16).float() for n in z.files}
-        for k in sorted(exact_steps):
-            exact = exact_steps[k]
-            got = eng.logits_for(prompt + gold["tokens"][:k]).float().cpu()
-            err = float((got - exact).abs().max())
-            scale = float(exact.abs().max())
-            bound = max(TOL * scale, 2 * noise_max)
-            same = int(got.argmax()) == int(exact.argmax())
-            print(f"  exact step {k:2d}: max|engine-exact| {err:.4g} = {err / scale:.4f} of "
-                  f"max|logit| {scale:.4g}; bound {bound:.4g}; argmax equal {same}", flush=True)
-            assert err <= bound, (mode, k, err, bound)
-            # a different argmax only where the exact top logit and the
-            # engine's pick are within twice the measured error
-            assert same or float(exact.max() - exact[int(got.argmax())]) <= 2 * err, (mode, k)
+        # every 8th step against the exact sums of the arithmetic the mode
+        # computes (and, for the XCD kernel, the HIR's too), the bound as above
+        # with that arithmetic's noise at steps 0 and 63
+        kinds = [("exact", noise_max)]
+        if mode == "xcd":
+            prod = json.loads((GOLDEN / "c2_order_noise_exactprod.json").read_text())[norms]
+            kinds.insert(0, ("exactprod", max(v["max_abs"] for v in prod.values())))
+        for kind, nz in kinds:
+            exact_steps = _exact_steps(norms, kind)
+            for k in sorted(exact_steps):
+                exact = exact_steps[k]
+                got = eng.logits_for(prompt + gold["tokens"][:k]).float().cpu()
+                err = float((got - exact).abs().max())
+                scale = float(exact.abs().max())
+                bound = max(TOL * scale, 2 * nz)
+                same = int(got.argmax()) == int(exact.argmax())
+                print(f"  {kind} step {k:2d}: max|engine-exact| {err:.4g} = {err / scale:.4f} of "
+                      f"max|logit| {scale:.4g}; bound {bound:.4g}; argmax equal {same}",
+                      flush=True)
+                assert err <= bound, (mode, kind, k, err, bound)
+                # a different argmax only where the exact top logit and the
+                # engine's pick are within twice the measured error
+                assert same or float(exact.max() - exact[int(got.argmax())]) <= 2 * err, \
+                    (mode, kind, k)
 
         # teacher-forced: every step's pick and its top-8 logits.  A pick that
         # differs from the golden one is allowed only where the golden gap
