@@ -662,10 +662,15 @@ int tfd_decode_xcd(const TfdDecodeArgs* args, const TfdXcdArgs* xcd, int steps, 
   int per_cu = 0;
   const void* fn = reinterpret_cast<const void*>(&k_decode_xcd);
   const size_t dyn = kDownLds * sizeof(u32x4);
-  static const hipError_t lds_ok =
-      hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn);
-  if (lds_ok != hipSuccess)
-    return fail((int)lds_ok, "decode_xcd: %zu bytes of dynamic LDS refused", dyn);
+  // the dynamic-LDS attribute is set once per device (with that device current)
+  static bool lds_set[64] = {};
+  if (dev < 0 || dev >= 64) return fail(kUnsupported, "decode_xcd: device %d", dev);
+  if (!lds_set[dev]) {
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn);
+    if (e != hipSuccess)
+      return fail((int)e, "decode_xcd: %zu bytes of dynamic LDS refused", dyn);
+    lds_set[dev] = true;
+  }
   e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kBlock, dyn);
   if (e != hipSuccess) return fail((int)e, "decode_xcd: occupancy query failed");
   if (per_cu < 1)
