@@ -287,6 +287,9 @@ def bench_c3(args) -> int:
         return e0.elapsed_time(e1) / 1e3 / rounds
 
     sc_s, pv_s = time_it(scores), time_it(pv)
+    # tiles per split at the final position (split_tiles 0: derived from it)
+    tiles_now = (pos_now + 63) // 64
+    split_tiles = eng.split_tiles or (tiles_now + eng.nsplit - 1) // eng.nsplit
     att_bw = 2 * kv_read / (sc_s + pv_s)
     line = {
         "metric": "decode tok/s bs=32 Qwen3-1.7B-arch bf16, 4096-token contexts "
@@ -308,7 +311,8 @@ def bench_c3(args) -> int:
                      "achieved": round(att_bw / 1e9, 1), "peak": HBM_PEAK / 1e9, "unit": "GB/s",
                      "frac": round(att_bw / HBM_PEAK, 4), "traffic": None,
                      "bytes_per_launch": kv_read, "scores_us": round(sc_s * 1e6, 2),
-                     "pv_us": round(pv_s * 1e6, 2), "split_positions": 64 * eng.split_tiles},
+                     "pv_us": round(pv_s * 1e6, 2), "splits": eng.nsplit,
+                     "split_positions": 64 * split_tiles},
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -214,15 +214,19 @@ def test_batch_engine_qwen3_layer_shape(gpu_device):
         print(f"sequence {b}: identical for {16 if k is None else k} of 16 steps")
 
 
-@pytest.mark.parametrize("split_tiles", [1, 2, 3, 4, 8])
-def test_batch_engine_long_splits(gpu_device, split_tiles):
+@pytest.mark.parametrize("split_tiles,splits", [(1, None), (2, None), (3, None), (4, None),
+                                               (8, None), (None, None), (None, 1), (None, 2),
+                                               (None, 3)])
+def test_batch_engine_long_splits(gpu_device, split_tiles, splits):
     """Splits of several 64-position tiles (the long-context partition) against
-    the oracle, with contexts past several splits."""
+    the oracle, with contexts past several splits: fixed split lengths, and
+    lengths derived from each sequence's position over 1, 2, 3 or the default
+    number of splits."""
     cfg = QWEN3_1_7B.with_(num_hidden_layers=2)
     w = synthetic_weights(cfg, seed=1, norms="ones")
     prompts = [_prompt(n, cfg.vocab_size, seed=20 + n) for n in (230, 150, 400)]
     eng = BatchEngine(cfg, w, batch=3, device=gpu_device, max_new=8, prompt_room=400,
-                      split_tiles=split_tiles)
+                      split_tiles=split_tiles, splits=splits)
     run = eng.generate(prompts, 8, record_logits=True)
     for b, orc in enumerate(_oracle_runs(cfg, w, prompts, 8)):
         seq = type("Run", (), {"tokens": run.tokens[b], "logits": run.logits[b]})

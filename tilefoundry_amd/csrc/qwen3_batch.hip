@@ -487,6 +487,17 @@ __global__ __launch_bounds__(kKW * kWave) void k_gemm_ksplit(
 // own position, page-table row, QKV row and workspaces.  The phase bodies are
 // the batch-1 ones.
 // ---------------------------------------------------------------------------
+// Tiles per split: `chunks` when positive; when 0, derived from the sequence's
+// position so that its prior context spreads evenly over the nsplit splits
+// (both launches of a step read the same position, so they agree on it).
+__device__ __forceinline__ int split_chunks(int chunks, int P, int max_pages, int nsplit) {
+  if (chunks > 0) return chunks;
+  const int Pc = (P >= 0 && P < max_pages * kPage) ? P : 0;
+  const int tiles = (Pc + kSplit - 1) / kSplit;
+  const int c = (tiles + nsplit - 1) / nsplit;
+  return c > 0 ? c : 1;
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(kBlock) void k_attn_scores_b(
     const bf16* __restrict__ qkv, int ldq, const bf16* __restrict__ gq,
@@ -498,6 +509,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_scores_b(
   const int b = blockIdx.z, heads = kv_heads * G, nsplit = gridDim.x;
   const int P = coh_ldi(pos + b);
   const int* pt = page_table + (int64_t)b * max_pages;
+  chunks = split_chunks(chunks, P, max_pages, nsplit);
   KTile<D> kt;
   k_tile_issue_at<D, false>(blockIdx.x * chunks * kSplit, blockIdx.y, P, pt, max_pages, kpool,
                      num_pages, kv_heads, kt);
@@ -529,6 +541,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_pv_b(
   int P = coh_ldi(pos + b);
   if (P < 0 || P >= max_pages * kPage) P = 0;
   const int* pt = page_table + (int64_t)b * max_pages;
+  chunks = split_chunks(chunks, P, max_pages, nsplit);
   VTile<D> vt;
   v_tile_issue_at<D, false>(blockIdx.x * chunks * kSplit, blockIdx.y, P, pt, max_pages, vpool,
                      num_pages, kv_heads, vt);
@@ -1018,6 +1031,16 @@ int gemm_skinny_bf16(const void* x, const void* w, int M, int K, int N, int epil
   return launched("gemm_skinny");
 }
 
+// The splits reach every cached position and the score rows hold them: fixed
+// splits cover nsplit x split_tiles x 64 positions; derived ones (split_tiles
+// 0) always cover the prior context, whose scores go at their positions.
+bool batched_splits_cover(int max_pages, int nsplit, int split_tiles, int score_stride) {
+  const int64_t cap = (int64_t)max_pages * kPage;
+  if (split_tiles == 0) return score_stride >= (cap + kSplit - 1) / kSplit * kSplit;
+  const int64_t slen = (int64_t)split_tiles * kSplit;
+  return nsplit * slen >= cap && score_stride >= nsplit * slen;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1048,11 +1071,10 @@ int tfd_attn_rope_scores_paged_batched(
       !k_pool || !v_pool || !scores || !split_max || !score_new)
     return fail(kBadArg, "attn_rope_scores_batched: null pointer");
   if (batch <= 0 || batch > 65535 || kv_heads <= 0 || heads % kv_heads || nsplit <= 0 ||
-      max_pages <= 0 || num_pages <= 0 || split_tiles <= 0)
+      max_pages <= 0 || num_pages <= 0 || split_tiles < 0)
     return fail(kBadShape, "attn_rope_scores_batched: batch=%d heads=%d kv_heads=%d nsplit=%d "
                 "split_tiles=%d", batch, heads, kv_heads, nsplit, split_tiles);
-  const int64_t slen = (int64_t)split_tiles * kSplit;
-  if (nsplit * slen < (int64_t)max_pages * kPage || score_stride < nsplit * slen ||
+  if (!batched_splits_cover(max_pages, nsplit, split_tiles, score_stride) ||
       ldq < (heads + 2 * kv_heads) * head_dim)
     return fail(kBadShape, "attn_rope_scores_batched: nsplit=%d / score_stride=%d / ldq=%d do "
                 "not cover the cache", nsplit, score_stride, ldq);
@@ -1079,11 +1101,10 @@ int tfd_attn_pv_combine_paged_batched(
       !part_sum || !part_out || !counters || !attn_out)
     return fail(kBadArg, "attn_pv_combine_batched: null pointer");
   if (batch <= 0 || batch > kMaxRows || kv_heads <= 0 || heads % kv_heads || nsplit <= 0 ||
-      max_pages <= 0 || num_pages <= 0 || (heads * head_dim) % 32 || split_tiles <= 0)
+      max_pages <= 0 || num_pages <= 0 || (heads * head_dim) % 32 || split_tiles < 0)
     return fail(kBadShape, "attn_pv_combine_batched: batch=%d (1..32) heads=%d kv_heads=%d "
                 "nsplit=%d split_tiles=%d", batch, heads, kv_heads, nsplit, split_tiles);
-  const int64_t slen = (int64_t)split_tiles * kSplit;
-  if (nsplit * slen < (int64_t)max_pages * kPage || score_stride < nsplit * slen)
+  if (!batched_splits_cover(max_pages, nsplit, split_tiles, score_stride))
     return fail(kBadShape, "attn_pv_combine_batched: nsplit=%d does not cover the cache", nsplit);
   const int G = heads / kv_heads;
   const dim3 grid(nsplit, kv_heads, batch);

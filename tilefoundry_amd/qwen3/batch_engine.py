@@ -25,6 +25,7 @@ from .._lib import lib, ptr
 from ..sampling import Picker, Sampling
 from .config import Qwen3Config
 from .engine import bf16_scale, scatter_cache
+from .prefill import attention_splits
 from .weights import head_rows, pack_layer, validate
 
 MAX_BATCH = 32
@@ -56,10 +57,12 @@ class BatchEngine:
     def __init__(self, cfg: Qwen3Config, weights: dict[str, torch.Tensor], *, batch: int,
                  device: str = "cuda:0", max_new: int = 256, prompt_room: int = 4096,
                  page_seed: int | None = 0, graph: bool = True, split_tiles: int | None = None,
-                 sampling: Sampling | None = None):
-        """*split_tiles*: 64-position tiles per attention split (default: about 16
-        splits per sequence and kv head at full capacity).  *sampling*: the
-        token choice (``tilefoundry_amd.sampling.Sampling``; None: greedy)."""
+                 splits: int | None = None, sampling: Sampling | None = None):
+        """*split_tiles*: 64-position tiles per attention split (default: split
+        lengths that follow each sequence's position, over *splits* splits per
+        sequence and kv head, by default ``prefill.attention_splits``).
+        *sampling*: the token choice (``tilefoundry_amd.sampling.Sampling``;
+        None: greedy)."""
         if cfg.dtype != torch.bfloat16:
             raise ValueError(f"the HIP engine runs bf16 weights; config has {cfg.dtype}")
         if not 1 <= batch <= MAX_BATCH:
@@ -79,11 +82,19 @@ class BatchEngine:
         self.cap = _round_up(self.nsteps, _lib.ATTN_SPLIT)
         self.max_pages = self.cap // _lib.PAGE_SIZE
         tiles = self.cap // _lib.ATTN_SPLIT
-        self.split_tiles = split_tiles or max(1, round(tiles / 16))
-        if self.split_tiles < 1:
-            raise ValueError(f"split_tiles must be positive, got {split_tiles}")
-        self.nsplit = -(-tiles // self.split_tiles)
-        self.score_stride = self.nsplit * self.split_tiles * _lib.ATTN_SPLIT
+        if split_tiles is None:
+            if splits is not None and not 1 <= splits <= tiles:
+                raise ValueError(f"splits must lie in [1, {tiles}], got {splits}")
+            self.nsplit = splits or attention_splits(batch, self.HKV, self.cap)
+            self.split_tiles = 0              # derived from each sequence's position
+            self.score_stride = self.cap
+        else:
+            if split_tiles < 1 or splits is not None:
+                raise ValueError(f"split_tiles must be positive and given without splits, "
+                                 f"got {split_tiles} / {splits}")
+            self.split_tiles = split_tiles
+            self.nsplit = -(-tiles // self.split_tiles)
+            self.score_stride = self.nsplit * self.split_tiles * _lib.ATTN_SPLIT
         if self.cap > cfg.max_position_embeddings:
             raise ValueError(f"capacity {self.cap} exceeds the rope table "
                              f"({cfg.max_position_embeddings} positions)")
