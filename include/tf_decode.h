@@ -207,7 +207,10 @@ int tfd_attn_rope_scores_paged_batched(
  * zero; the output rows go to attn_out in operand order, 32 x heads * head_dim, for
  * the o projection).  A split covers split_tiles x 64 positions in
  * both entries (long contexts: fewer, longer splits; one tile's loads are in flight
- * while the previous one is reduced); nsplit x split_tiles x 64 >= max_pages x 16. */
+ * while the previous one is reduced); nsplit x split_tiles x 64 >= max_pages x 16.
+ * split_tiles 0: each sequence's split length follows its position, ceil(ceil(pos /
+ * 64) / nsplit) tiles, so its prior context spreads evenly over the nsplit splits at
+ * every depth (score_stride >= max_pages x 16 rounded up to 64). */
 int tfd_attn_pv_combine_paged_batched(
     const void* qkv, int ldq, const int32_t* pos, const int32_t* page_table, int max_pages,
     const void* v_pool, int num_pages, int batch, int heads, int kv_heads, int head_dim,

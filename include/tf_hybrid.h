@@ -242,7 +242,9 @@ int tfd_mamba_step(const TfdMambaArgs* args, void* stream);
  * scores f32 [rows][heads][score_stride >= max_pages * 16], stats f32
  * [rows][heads][nsplit][2], part f32 [rows][heads][nsplit][head_dim], counters
  * int32 [rows][kv_heads] (zero; left zero).  A split covers split_len positions
- * (a multiple of 16, <= 512); nsplit * split_len >= max_pages * 16.  A position
+ * (a multiple of 16, <= 512); nsplit * split_len >= max_pages * 16.  split_len 0:
+ * each row's split length follows its position, ceil((pos + 1) / nsplit) rounded up
+ * to 16, between 64 and 512 (nsplit * 512 >= max_pages * 16).  A position
  * outside the page (or rope) table raises TFD_ERR_POS_RANGE in err, a page
  * outside the pool TFD_ERR_PAGE_RANGE. */
 typedef struct {

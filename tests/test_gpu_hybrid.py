@@ -20,6 +20,7 @@ from tests._parity import assert_close_bf16, report, ulp_bf16
 from tests.test_gpu_batch import from_operand_order, operand_order
 from tilefoundry_amd import _lib
 from tilefoundry_amd._lib import lib, ptr
+from tilefoundry_amd.hybrid.qwen3_5 import attention_splits
 
 pytestmark = pytest.mark.gpu
 
@@ -720,11 +721,16 @@ def _paged_pool(pasts, hkv, d, max_pages, gen):
 
 
 def _gqa_call(qkv, pos, table, kpool, vpool, *, heads, kv_heads, head_dim, scale, split_len,
-              policy, gamma_q=None, gamma_k=None, cos=None, sin=None, eps=1e-6):
+              policy, gamma_q=None, gamma_k=None, cos=None, sin=None, eps=1e-6, nsplit=None):
+    """split_len 0: lengths derived from each row's position over nsplit splits
+    (default: the engines' choice)."""
     dev = "cuda:0"
     rows = qkv.shape[0]
     max_pages = table.shape[1]
-    nsplit = -(-max_pages * 16 // split_len)
+    if split_len == 0:
+        nsplit = nsplit or attention_splits(rows, kv_heads, max_pages * 16)
+    else:
+        nsplit = -(-max_pages * 16 // split_len)
     stride = max_pages * 16
     keep = []
 
@@ -769,15 +775,18 @@ def _rope_rows(rows, rot, theta):
 
 
 # the last rows reach the C4 workload's depth (a 32-token prompt + 2,048 new
-# tokens: positions up to 2,079) at the engine's 64-position splits, at batch 1
-# and 16
-@pytest.mark.parametrize("pos,split_len", [([0], 128), ([511], 128), ([700], 512),
-                                           ([0, 15, 16, 17, 127, 128, 129, 300, 511, 512, 640,
-                                             700, 701, 750, 3, 64], 128),
-                                           ([2040], 64), ([2079], 64),
-                                           ([2040 + 3 * i for i in range(13)] + [2078, 2079,
-                                                                                 2047], 64)])
-def test_gqa_decode_c4(gpu_device, pos, split_len):
+# tokens: positions up to 2,079) at batch 1 and 16, with fixed split lengths and
+# with lengths derived from each row's position (split_len 0: the engines'
+# default, over the engines' split count or over 2)
+_C4_ROWS16 = [2040 + 3 * i for i in range(13)] + [2078, 2079, 2047]
+_C4_MIXED = [0, 15, 16, 17, 127, 128, 129, 300, 511, 512, 640, 700, 701, 750, 3, 64]
+
+
+@pytest.mark.parametrize("pos,split_len,nsplit", [
+    ([0], 128, None), ([511], 128, None), ([700], 512, None), (_C4_MIXED, 128, None),
+    ([2040], 64, None), ([2079], 64, None), (_C4_ROWS16, 64, None),
+    ([2079], 0, None), (_C4_ROWS16, 0, None), (_C4_MIXED, 0, None), (_C4_MIXED, 0, 2)])
+def test_gqa_decode_c4(gpu_device, pos, split_len, nsplit):
     """Qwen3.5 full attention: 16 q / 2 kv heads of 256, RoPE on 64 dims."""
     g = torch.Generator().manual_seed(len(pos) * 1000 + pos[0] + split_len)
     B, HQ, HKV, D, rot = len(pos), 16, 2, 256, 64
@@ -800,7 +809,7 @@ def test_gqa_decode_c4(gpu_device, pos, split_len):
     got, kp, vp, err = _gqa_call(qkv, torch.tensor(pos), table, kpool, vpool, heads=HQ,
                                  kv_heads=HKV, head_dim=D, scale=scale, split_len=split_len,
                                  policy=_lib.POLICY_F32, gamma_q=gq, gamma_k=gk, cos=cos,
-                                 sin=sin)
+                                 sin=sin, nsplit=nsplit)
     assert err == 0
     P = torch.tensor(pos)
     want, k_rope = H.qwen35_attend(qg, k, v, [p[0] for p in pasts], [p[1] for p in pasts], gq,
@@ -812,11 +821,16 @@ def test_gqa_decode_c4(gpu_device, pos, split_len):
     assert torch.equal(vp[pg, :, P % 16].float(), v)
 
 
-@pytest.mark.parametrize("pos,split_len", [([0, 1, 2, 100, 255, 256, 1000, 2000], 256),
-                                           ([1999], 16), ([37], 512),
-                                           ([8191, 8192, 8000, 4095, 8191, 6000, 8190, 7777],
-                                            256)])
-def test_gqa_decode_c5(gpu_device, pos, split_len):
+_C5_DEEP = [8191, 8192, 8000, 4095, 8191, 6000, 8190, 7777]
+_C5_MIXED = [0, 1, 2, 100, 255, 256, 1000, 2000]
+
+
+# split_len 0: lengths derived from each row's position over the engines'
+# split count, or over 16 at 8,192 positions (512-position splits, the longest)
+@pytest.mark.parametrize("pos,split_len,nsplit", [
+    (_C5_MIXED, 256, None), ([1999], 16, None), ([37], 512, None), (_C5_DEEP, 256, None),
+    (_C5_MIXED, 0, None), (_C5_DEEP, 0, None), ([8191, 1, 511, 4000], 0, 16)])
+def test_gqa_decode_c5(gpu_device, pos, split_len, nsplit):
     """Granite attention: 32 q / 8 kv heads of 128, no RoPE, HIR rounding; up to
     the workload's depth (8 rows at 8,192-token contexts)."""
     g = torch.Generator().manual_seed(len(pos) * 100 + pos[0] + split_len)
@@ -832,7 +846,7 @@ def test_gqa_decode_c5(gpu_device, pos, split_len):
     kpool, vpool, table = _paged_pool(pasts, HKV, D, max_pages, g)
     got, kp, vp, err = _gqa_call(qkv, torch.tensor(pos), table, kpool, vpool, heads=HQ,
                                  kv_heads=HKV, head_dim=D, scale=scale, split_len=split_len,
-                                 policy=_lib.POLICY_BF16)
+                                 policy=_lib.POLICY_BF16, nsplit=nsplit)
     assert err == 0
     want = H.granite_attend(q, k, v, [p[0] for p in pasts], [p[1] for p in pasts], scale)
     r = assert_close_bf16(got, want, max_rel=2e-2, min_cos=0.9999, name="gqa c5")

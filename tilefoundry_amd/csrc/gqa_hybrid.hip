@@ -92,6 +92,20 @@ __device__ __forceinline__ void stage_pages(const GqaArgs& a, int b, int j0, int
   }
 }
 
+// Positions per split: split_len when positive; when 0, derived from the
+// sequence's position so that its context spreads evenly over the nsplit
+// splits -- ceil((P + 1) / nsplit) rounded up to a page, at least kMinSplitLen
+// (the host guarantees nsplit * kMaxSplitLen covers the cache, so it never
+// exceeds kMaxSplitLen).  Both launches of a layer read the same position.
+constexpr int kMinSplitLen = 64;
+__device__ __forceinline__ int split_len_of(const GqaArgs& a, int P) {
+  if (a.split_len > 0) return a.split_len;
+  int n = (P + a.nsplit) / a.nsplit;                  // ceil((P + 1) / nsplit)
+  n = (n + kPage - 1) / kPage * kPage;
+  n = n > kMinSplitLen ? n : kMinSplitLen;
+  return n < kMaxSplitLen ? n : kMaxSplitLen;
+}
+
 // Positions are walked kU passes at a time: every load of the batch is issued
 // before the first is used (positions past the split re-read its last row).
 constexpr int kU = 4;
@@ -113,9 +127,10 @@ __global__ __launch_bounds__(kBlock) void k_gqa_scores(GqaArgs a) {
     if (split == 0 && kvh == 0 && tid == 0) raise_error(a.err, kErrPosRange);
     return;
   }
-  const int j0 = split * a.split_len;
+  const int slen = split_len_of(a, P);
+  const int j0 = split * slen;
   if (j0 > P) return;
-  const int j1 = min(j0 + a.split_len, P + 1), n = j1 - j0;
+  const int j1 = min(j0 + slen, P + 1), n = j1 - j0;
   const bool owner = P < j1;            // this split appends the token's K/V
   const int nrows = kG + (owner ? 1 : 0);
   // ---- this token's query heads (and key head): C4 normalises them per head
@@ -267,9 +282,10 @@ __global__ __launch_bounds__(kBlock) void k_gqa_pv(GqaArgs a) {
   __shared__ int is_last;
   const int P = a.pos[b];
   if (!pos_ok(a, P, kF32)) return;      // raised by the scores launch
-  const int nlive = P / a.split_len + 1;
+  const int slen = split_len_of(a, P);
+  const int nlive = P / slen + 1;
   if (split >= nlive) return;
-  const int j0 = split * a.split_len, j1 = min(j0 + a.split_len, P + 1), n = j1 - j0;
+  const int j0 = split * slen, j1 = min(j0 + slen, P + 1), n = j1 - j0;
   const int hq0 = kvh * kG;
   if (tid < kG) {
     const float* st = a.stats + ((int64_t)b * a.hq + hq0 + tid) * a.nsplit * 2;
@@ -432,8 +448,10 @@ extern "C" int tfd_gqa_decode(const TfdGqaArgs* args, void* stream) {
   if (t.rows <= 0 || t.rows > kMaxRowsG || t.kv_heads <= 0 || t.heads % t.kv_heads ||
       !((D == 128 && G == 4) || (D == 256 && G == 8)) ||
       t.ldq < t.heads * qw + 2 * t.kv_heads * D || t.max_pages <= 0 || t.num_pages <= 0 ||
-      t.split_len < kPage || t.split_len > kMaxSplitLen || t.split_len % kPage ||
-      (int64_t)t.nsplit * t.split_len < (int64_t)t.max_pages * kPage ||
+      t.nsplit <= 0 || t.split_len < 0 || t.split_len > kMaxSplitLen ||
+      t.split_len % kPage ||
+      (int64_t)t.nsplit * (t.split_len > 0 ? t.split_len : kMaxSplitLen) <
+          (int64_t)t.max_pages * kPage ||
       t.score_stride < t.max_pages * kPage ||
       (f32 && (t.rot_dim <= 0 || t.rot_dim % 2 || t.rot_dim > D || t.rope_rows <= 0)))
     return fail(kBadShape, "gqa_decode: rows=%d (1..32) heads=%d kv_heads=%d head_dim=%d "

@@ -264,7 +264,11 @@ def bench_gqa(config, rows, reps, gen, *, heads, kv_heads, d, ctx, f32, split_le
     ldq = heads * qw + 2 * kv_heads * d
     qkv = (_rn(rows, ldq, gen=gen).to(DEV) if f32 else
            _rn(rows, ldq, gen=gen).to(BF).to(DEV))
-    nsplit = -(-max_pages * 16 // split_len)
+    if split_len is None:           # the engines' choice: lengths follow the position
+        from .qwen3_5 import attention_splits
+        nsplit, split_len = attention_splits(rows, kv_heads, max_pages * 16), 0
+    else:
+        nsplit = -(-max_pages * 16 // split_len)
     stride = max_pages * 16
     scores = torch.empty(rows * heads * stride, device=DEV)
     stats = torch.empty(rows * heads * nsplit * 2, device=DEV)
@@ -392,7 +396,7 @@ def run(config: str, reps: int) -> list[dict]:
             res.append(bench_moe(config, rows, reps, gen, hs=2048, inter=512, sh=512,
                                  experts=256, k=8, fp8=False, packed=True))
         res.append(bench_gqa(config, rows, reps, gen, heads=16, kv_heads=2, d=256, ctx=1024,
-                             f32=True, split_len=64))
+                             f32=True, split_len=None))
     elif config == "c5":
         rows = 8
         res.append(bench_mamba(config, rows, reps, gen))
@@ -402,7 +406,7 @@ def run(config: str, reps: int) -> list[dict]:
             res.append(bench_moe(config, rows, reps, gen, hs=4096, inter=768, sh=1536,
                                  experts=72, k=10, fp8=True, packed=packed))
         res.append(bench_gqa(config, rows, reps, gen, heads=32, kv_heads=8, d=128, ctx=8192,
-                             f32=False, split_len=256))
+                             f32=False, split_len=None))
         res.append(bench_gemm_fp8(config, rows, reps, gen, K=4096, N=8512, name="in_proj"))
         res.append(bench_gemm_fp8(config, rows, reps, gen, K=4096, N=4096, name="out_proj"))
     else:

@@ -33,7 +33,7 @@ import torch
 from .. import _lib
 from .._lib import lib, ptr
 from ..sampling import Picker, Sampling
-from .qwen3_5 import ctypes_addr
+from .qwen3_5 import attention_splits, ctypes_addr
 
 BF = torch.bfloat16
 F32 = torch.float32
@@ -197,7 +197,7 @@ class GraniteEngine:
 
     def __init__(self, cfg: GraniteConfig, weights: dict[str, torch.Tensor], *, rows: int,
                  device: str = "cuda:0", max_steps: int = 1024, page_seed: int = 0,
-                 split_len: int = 256, graph: bool = True, record_routes: bool = False,
+                 split_len: int | None = None, graph: bool = True, record_routes: bool = False,
                  sampling: Sampling | None = None):
         if not 1 <= rows <= 32:
             raise ValueError("rows: 1..32 sequences")
@@ -304,7 +304,10 @@ class GraniteEngine:
                 shape = (self.num_pages, cfg.kv_heads, 16, cfg.head_dim)
                 self.kpool[i] = z(*shape, dtype=BF)
                 self.vpool[i] = z(*shape, dtype=BF)
-        self.nsplit = -(-self.max_pages * 16 // self.split_len)
+        if self.split_len is None:              # lengths follow each row's position
+            self.nsplit = attention_splits(B, cfg.kv_heads, self.max_pages * 16)
+        else:
+            self.nsplit = -(-self.max_pages * 16 // self.split_len)
         self.stride = self.max_pages * 16
         self.scores = z(B * cfg.heads * self.stride)
         self.stats = z(B * cfg.heads * self.nsplit * 2)
@@ -360,7 +363,7 @@ class GraniteEngine:
         a.scale, a.eps = cfg.attention_multiplier, cfg.eps
         a.scores, a.score_stride, a.stats, a.part = ptr(self.scores), self.stride, \
             ptr(self.stats), ptr(self.part)
-        a.counters, a.nsplit, a.split_len = ptr(self.counters), self.nsplit, self.split_len
+        a.counters, a.nsplit, a.split_len = ptr(self.counters), self.nsplit, self.split_len or 0
         a.out, a.policy, a.err = ptr(self.mix), _lib.POLICY_BF16, ptr(self.err)
         self._lib.tfd_gqa_decode(ctypes_addr(a), s)
 
