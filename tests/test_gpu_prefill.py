@@ -110,11 +110,15 @@ def _batch_cache(eng, layer, b, n):
     return eng.kpool[layer][page, :, row].float().cpu(), eng.vpool[layer][page, :, row].float().cpu()
 
 
-def test_batch_prefill_caches_match_the_oracle_walks(gpu_device):
+# room 4,096: the prefill's score rows are an allocation of megabytes, whose
+# first row is sequence 0's at position 0 -- a split with no prior position,
+# which still prefetches its next tile's scores from inside that row
+@pytest.mark.parametrize("room", [72, 4096])
+def test_batch_prefill_caches_match_the_oracle_walks(gpu_device, room):
     w = synthetic_weights(SMALL, seed=1, norms="random")
     lens = [5, 40, 71]
     prompts = [_prompt(n, SMALL.vocab_size, seed=10 + n) for n in lens]
-    eng = BatchEngine(SMALL, w, batch=3, device=gpu_device, max_new=8, prompt_room=72)
+    eng = BatchEngine(SMALL, w, batch=3, device=gpu_device, max_new=8, prompt_room=room)
     eng.prefill(prompts)
     eng.check_errors()
     assert eng.pos.tolist() == [n - 1 for n in lens]
