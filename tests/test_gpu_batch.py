@@ -214,21 +214,29 @@ def test_batch_engine_qwen3_layer_shape(gpu_device):
         print(f"sequence {b}: identical for {16 if k is None else k} of 16 steps")
 
 
+@pytest.fixture(scope="module")
+def long_split_case():
+    """Weights, prompts and the oracle's runs of the long-split tests, computed
+    once for all their partitions (the oracle decodes on its own)."""
+    cfg = QWEN3_1_7B.with_(num_hidden_layers=2)
+    w = synthetic_weights(cfg, seed=1, norms="ones")
+    prompts = [_prompt(n, cfg.vocab_size, seed=20 + n) for n in (230, 150, 400)]
+    return cfg, w, prompts, _oracle_runs(cfg, w, prompts, 8)
+
+
 @pytest.mark.parametrize("split_tiles,splits", [(1, None), (2, None), (3, None), (4, None),
                                                (8, None), (None, None), (None, 1), (None, 2),
                                                (None, 3)])
-def test_batch_engine_long_splits(gpu_device, split_tiles, splits):
+def test_batch_engine_long_splits(gpu_device, long_split_case, split_tiles, splits):
     """Splits of several 64-position tiles (the long-context partition) against
     the oracle, with contexts past several splits: fixed split lengths, and
     lengths derived from each sequence's position over 1, 2, 3 or the default
     number of splits."""
-    cfg = QWEN3_1_7B.with_(num_hidden_layers=2)
-    w = synthetic_weights(cfg, seed=1, norms="ones")
-    prompts = [_prompt(n, cfg.vocab_size, seed=20 + n) for n in (230, 150, 400)]
+    cfg, w, prompts, oracle_runs = long_split_case
     eng = BatchEngine(cfg, w, batch=3, device=gpu_device, max_new=8, prompt_room=400,
                       split_tiles=split_tiles, splits=splits)
     run = eng.generate(prompts, 8, record_logits=True)
-    for b, orc in enumerate(_oracle_runs(cfg, w, prompts, 8)):
+    for b, orc in enumerate(oracle_runs):
         seq = type("Run", (), {"tokens": run.tokens[b], "logits": run.logits[b]})
         _check_run(seq, orc, 8, strict=False)
 
