@@ -144,6 +144,95 @@ __device__ __forceinline__ uint32_t bf_pair(bf16 lo, bf16 hi) {
   return (uint32_t)lo | ((uint32_t)hi << 16);
 }
 
+// ---------------------------------------------------------------------------
+// The row sums of kR (8 or 16) rows at once: lane l holds a partial sum of every
+// row, and exchanges halve the rows a lane carries at each step -- lanes l and
+// l ^ 32 (a lane swap: lanes below 32 keep rows 0 .. kR/2 - 1, the others the
+// rest), l ^ 16 (lane swap), then within 16 lanes by mirrors, each pairing a
+// lane with one of the other half -- until every lane holds one row, which the
+// rest of its group then completes.  kR 16: lane l ends with row l / 4; kR 8:
+// row l / 8; every lane of a row's group holds the same bits.  About 35 VALU
+// operations for 16 rows against 16 wave sums of 12.  (A row's f32 sum is taken
+// in another order than wave_sum's.)
+// ---------------------------------------------------------------------------
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtrl, 0xF, 0xF, false);
+}
+constexpr int kDppRor8 = 0x128;       // lane i <-> i + 8 (mod 16) within 16
+
+template <int kR>
+__device__ __forceinline__ float rows_sum(const float (&a)[kR], int lane) {
+  static_assert(kR == 8 || kR == 16, "8 or 16 rows");
+  constexpr int kH = kR / 2, kQ = kR / 4;
+  float b[kH];
+#pragma unroll
+  for (int j = 0; j < kH; ++j) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[j]),
+                                                    __float_as_uint(a[j + kH]), false, false);
+    b[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  float c[kQ];
+#pragma unroll
+  for (int j = 0; j < kQ; ++j) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(b[j]),
+                                                    __float_as_uint(b[j + kQ]), false, false);
+    c[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  // within 16 lanes: lanes with bit 3 set keep the upper value of each pair;
+  // the mirror (i <-> 15 - i) pairs every lane with one across bit 3
+  const bool b3 = lane & 8;
+  if constexpr (kR == 16) {
+    float d[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float keep = b3 ? c[k + 2] : c[k], give = b3 ? c[k] : c[k + 2];
+      d[k] = keep + dpp_f<kDppMirror>(give);
+    }
+    const bool b2 = lane & 4;
+    const float keep = b2 ? d[1] : d[0], give = b2 ? d[0] : d[1];
+    float v = keep + dpp_f<kDppHalfMirror>(give);        // i <-> 7 - i: across bit 2
+    v += dpp_f<kDppXor2>(v);
+    v += dpp_f<kDppXor1>(v);
+    return v;
+  } else {
+    const float keep = b3 ? c[1] : c[0], give = b3 ? c[0] : c[1];
+    float v = keep + dpp_f<kDppMirror>(give);
+    v += dpp_f<kDppXor1>(v);
+    v += dpp_f<kDppXor2>(v);
+    v += dpp_f<kDppHalfMirror>(v);
+    return v;
+  }
+}
+
+// The SwiGLU epilogue on rows_sum's layout (rows are (gate_n, up_n) pairs,
+// model.py:230-233): every lane of a gate row's group takes the up row's sum
+// from the next group, one silu for all pairs at once, and the pairs' words go
+// out from one lane per word in one store.
+template <int kR, int kPol>
+__device__ __forceinline__ void swiglu_rows_out(const float (&part)[kR], int64_t row0,
+                                                int nvalid, uint32_t* out, uint32_t tag,
+                                                int lane) {
+  const float y = rbf(rows_sum<kR>(part, lane));
+  // the up row sits across bit 2 (16 rows) or bit 3 (8 rows) of the lane
+  const float u = kR == 16 ? dpp_f<kDppHalfMirror>(y) : __uint_as_float(dpp_u<kDppRor8>(
+                                                            __float_as_uint(y)));
+  const uint32_t o = (uint32_t)f2bf(rbf(silu_f(y)) * u);
+  // word q = (pair 2q, pair 2q + 1): 16 rows -- lanes 16q and 16q + 8; 8 rows
+  // -- lanes 32q and 32q + 16
+  uint32_t hi;
+  if constexpr (kR == 16) {
+    hi = dpp_u<kDppRor8>(o);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(o, o, false, false);
+    hi = r[1];
+  }
+  constexpr int kLanesPerWord = kWave / (kR / 4);
+  const int q = lane / kLanesPerWord;
+  if (lane % kLanesPerWord == 0 && 4 * q + 3 < nvalid)
+    ll_put<kPol>(out, (uint32_t)(row0 / 4 + q), (o & 0xffffu) | (hi << 16), tag);
+}
+
 // nbuf: the norm is shared by the block's waves through this LDS buffer
 // (rms_norm_apply_block); then every wave of the block must call this with
 // rows of its own (the caller's partition guarantees it).
@@ -171,6 +260,18 @@ __device__ __forceinline__ void gemv_finish_ll(int vb, const uint32_t* xs,
     rms_norm_apply<kCmax>(xr, gr, K, eps);
   }
   if (row0 >= N) return;
+  if constexpr (kEpi == kSwiglu && (kR == 8 || kR == 16)) {
+    float part[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < kCmax; ++i) a = dot8(w[r][i], xr[i], a);
+      part[r] = a;
+    }
+    swiglu_rows_out<kR, kPol>(part, row0, nvalid, out, tag, lane);
+    return;
+  }
   float acc[kR];
   dot_loaded<kCmax, kR>(w, xr, acc);
   if (kEpi == kSwiglu) {
