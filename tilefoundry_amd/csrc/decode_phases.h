@@ -151,7 +151,7 @@ __device__ __forceinline__ uint32_t bf_pair(bf16 lo, bf16 hi) {
 // rest), l ^ 16 (lane swap), then within 16 lanes by mirrors, each pairing a
 // lane with one of the other half -- until every lane holds one row, which the
 // rest of its group then completes.  kR 16: lane l ends with row l / 4; kR 8:
-// row l / 8; every lane of a row's group holds the same bits.  About 35 VALU
+// row l / 8; kR 4: row l / 16; every lane of a row's group holds the same bits.  About 35 VALU
 // operations for 16 rows against 16 wave sums of 12.  (A row's f32 sum is taken
 // in another order than wave_sum's.)
 // ---------------------------------------------------------------------------
@@ -163,7 +163,20 @@ constexpr int kDppRor8 = 0x128;       // lane i <-> i + 8 (mod 16) within 16
 
 template <int kR>
 __device__ __forceinline__ float rows_sum(const float (&a)[kR], int lane) {
-  static_assert(kR == 8 || kR == 16, "8 or 16 rows");
+  static_assert(kR == 4 || kR == 8 || kR == 16, "4, 8 or 16 rows");
+  if constexpr (kR == 4) {
+    // kR 4: lane l ends with row l / 16
+    float b[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[j]),
+                                                      __float_as_uint(a[j + 2]), false, false);
+      b[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(b[0]), __float_as_uint(b[1]),
+                                                    false, false);
+    return group_sum<16>(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+  }
   constexpr int kH = kR / 2, kQ = kR / 4;
   float b[kH];
 #pragma unroll
@@ -179,6 +192,7 @@ __device__ __forceinline__ float rows_sum(const float (&a)[kR], int lane) {
                                                     __float_as_uint(b[j + kQ]), false, false);
     c[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
+  if constexpr (kR == 4) return 0.f;      // (returned above)
   // within 16 lanes: lanes with bit 3 set keep the upper value of each pair;
   // the mirror (i <-> 15 - i) pairs every lane with one across bit 3
   const bool b3 = lane & 8;
@@ -270,6 +284,33 @@ __device__ __forceinline__ void gemv_finish_ll(int vb, const uint32_t* xs,
       part[r] = a;
     }
     swiglu_rows_out<kR, kPol>(part, row0, nvalid, out, tag, lane);
+    return;
+  } else if constexpr ((kEpi == kStore || kEpi == kResid) && (kR == 8 || kR == 16)) {
+    float part[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < kCmax; ++i) a = dot8(w[r][i], xr[i], a);
+      part[r] = a;
+    }
+    // rows_sum's layout: row 2q + 1 sits across bit 2 (16 rows) or bit 3 (8)
+    // of row 2q's lanes; word q leaves from the first lane of row 2q
+    const float y0 = rbf(rows_sum<kR>(part, lane));
+    const float y1 = kR == 16 ? dpp_f<kDppHalfMirror>(y0)
+                              : __uint_as_float(dpp_u<kDppRor8>(__float_as_uint(y0)));
+    constexpr int kLanesPerWord = kWave / (kR / 2);
+    const int q = lane / kLanesPerWord;
+    if (lane % kLanesPerWord == 0 && 2 * q + 1 < nvalid) {
+      uint32_t pr;
+      if (kEpi == kResid) {
+        const uint32_t r = resid_s[(row0 + 2 * q) / 2];
+        pr = bf_pair(f2bf(bf_lo(r) + y0), f2bf(bf_hi(r) + y1));
+      } else {
+        pr = bf_pair(f2bf(y0), f2bf(y1));
+      }
+      ll_put<kPol>(out, (uint32_t)((row0 + 2 * q) / 2), pr, tag);
+    }
     return;
   }
   float acc[kR];

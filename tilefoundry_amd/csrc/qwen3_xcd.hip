@@ -233,19 +233,26 @@ __device__ __forceinline__ void lm_head_rows(int64_t row0, int V, int lane,
                                              const u32x4 (&xr)[kCmax],
                                              const u32x4 (&w)[kR][kCmax], float* logits,
                                              float& best, int& besti) {
+  static_assert(kR == 4, "rows_sum<4>: lane l holds row l / 16");
   if (row0 >= V) return;
   const int nvalid = (int)((V - row0) < kR ? (V - row0) : kR);
-  float acc[kR];
-  dot_loaded<kCmax, kR>(w, xr, acc);
+  float part[kR];
 #pragma unroll
   for (int r = 0; r < kR; ++r) {
-    if (r < nvalid) {
-      const float y = rbf(acc[r]);
-      if (lane == r) logits[row0 + r] = y;
-      if (better(y, (int)(row0 + r), best, besti)) {
-        best = y;
-        besti = (int)(row0 + r);
-      }
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < kCmax; ++i) a = dot8(w[r][i], xr[i], a);
+    part[r] = a;
+  }
+  // every lane keeps the best of its own row slot; the wave's four slots
+  // meet once, after the last rows (lm_head_grid)
+  const int r = lane / 16;
+  const float y = rbf(rows_sum<kR>(part, lane));
+  if (r < nvalid) {
+    if ((lane & 15) == 0) logits[row0 + r] = y;
+    if (better(y, (int)(row0 + r), best, besti)) {
+      best = y;
+      besti = (int)(row0 + r);
     }
   }
 }
@@ -272,6 +279,16 @@ __device__ __forceinline__ void lm_head_grid(const u32x4 (&xr)[kCmax], const bf1
     gemv_issue<kCmax, kR>((int)(r2 / (kWavesPerBlock * kR)), W, K, V, wa);
     lm_head_rows<kCmax, kR>(r1, V, lane, xr, wb, logits, best, besti);
     r0 = r2;
+  }
+  // the wave's four row slots (lanes 0, 16, 32, 48 hold them)
+#pragma unroll
+  for (int m = 16; m <= 32; m <<= 1) {
+    const float ob = __shfl_xor(best, m, kWave);
+    const int oi = __shfl_xor(besti, m, kWave);
+    if (better(ob, oi, best, besti)) {
+      best = ob;
+      besti = oi;
+    }
   }
   __shared__ float sv[kWavesPerBlock];
   __shared__ int si[kWavesPerBlock];
