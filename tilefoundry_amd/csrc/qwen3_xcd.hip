@@ -98,19 +98,35 @@ __device__ __forceinline__ void slab_finish(const uint32_t* xs, const u32x4 (&w)
   u32x4 xr[kC];
 #pragma unroll
   for (int j = 0; j < kC; ++j) xr[j] = *reinterpret_cast<const u32x4*>(xs + 4 * (c + 32 * j));
-  float mine = 0.f;
+  float a[8];
 #pragma unroll
   for (int p = 0; p < 8; ++p) {
-    float a = 0.f;
+    a[p] = 0.f;
 #pragma unroll
-    for (int j = 0; j < kC; ++j) a = dot8(w[p][j], xr[j], a);
-    a = group_sum<32>(a);
-    // lane 2p (row of half 0) and lane 32 + 2p (half 1) keep pass p's sums
-    if ((lane & 31) == 2 * p) mine = a;
+    for (int j = 0; j < kC; ++j) a[p] = dot8(w[p][j], xr[j], a[p]);
   }
-  // lanes 0, 2, .., 14 and 32, 34, .., 46 hold rows 2p + half: one word each
-  if ((lane & 31) < 16 && (lane & 1) == 0) {
-    const int p = (lane & 31) >> 1;
+  // the eight passes' sums over each 32-lane half at once (rows_sum's
+  // exchanges without the first): lane l ends with pass (l / 4) % 8 of its half
+  float b[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[j]),
+                                                    __float_as_uint(a[j + 4]), false, false);
+    b[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  const bool b3 = lane & 8, b2 = lane & 4;
+  float d[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const float keep = b3 ? b[k + 2] : b[k], give = b3 ? b[k] : b[k + 2];
+    d[k] = keep + dpp_f<kDppMirror>(give);
+  }
+  float mine = (b2 ? d[1] : d[0]) + dpp_f<kDppHalfMirror>(b2 ? d[0] : d[1]);
+  mine += dpp_f<kDppXor2>(mine);
+  mine += dpp_f<kDppXor1>(mine);
+  // the first lane of each group of four holds row 2p + half: one word each
+  if ((lane & 3) == 0) {
+    const int p = (lane >> 2) & 7;
     ll_put<kCoherent>(part, (uint32_t)(row0 + 16 * wave + 2 * p + half), __float_as_uint(mine),
                       tag);
   }
