@@ -164,19 +164,6 @@ constexpr int kDppRor8 = 0x128;       // lane i <-> i + 8 (mod 16) within 16
 template <int kR>
 __device__ __forceinline__ float rows_sum(const float (&a)[kR], int lane) {
   static_assert(kR == 4 || kR == 8 || kR == 16, "4, 8 or 16 rows");
-  if constexpr (kR == 4) {
-    // kR 4: lane l ends with row l / 16
-    float b[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[j]),
-                                                      __float_as_uint(a[j + 2]), false, false);
-      b[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(b[0]), __float_as_uint(b[1]),
-                                                    false, false);
-    return group_sum<16>(__uint_as_float(r[0]) + __uint_as_float(r[1]));
-  }
   constexpr int kH = kR / 2, kQ = kR / 4;
   float b[kH];
 #pragma unroll
@@ -192,11 +179,19 @@ __device__ __forceinline__ float rows_sum(const float (&a)[kR], int lane) {
                                                     __float_as_uint(b[j + kQ]), false, false);
     c[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
-  if constexpr (kR == 4) return 0.f;      // (returned above)
   // within 16 lanes: lanes with bit 3 set keep the upper value of each pair;
   // the mirror (i <-> 15 - i) pairs every lane with one across bit 3
   const bool b3 = lane & 8;
-  if constexpr (kR == 16) {
+  if constexpr (kR == 4) {
+    return group_sum<16>(c[0]);
+  } else if constexpr (kR == 8) {
+    const float keep = b3 ? c[1] : c[0], give = b3 ? c[0] : c[1];
+    float v = keep + dpp_f<kDppMirror>(give);
+    v += dpp_f<kDppXor1>(v);
+    v += dpp_f<kDppXor2>(v);
+    v += dpp_f<kDppHalfMirror>(v);
+    return v;
+  } else {
     float d[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -208,13 +203,6 @@ __device__ __forceinline__ float rows_sum(const float (&a)[kR], int lane) {
     float v = keep + dpp_f<kDppHalfMirror>(give);        // i <-> 7 - i: across bit 2
     v += dpp_f<kDppXor2>(v);
     v += dpp_f<kDppXor1>(v);
-    return v;
-  } else {
-    const float keep = b3 ? c[1] : c[0], give = b3 ? c[0] : c[1];
-    float v = keep + dpp_f<kDppMirror>(give);
-    v += dpp_f<kDppXor1>(v);
-    v += dpp_f<kDppXor2>(v);
-    v += dpp_f<kDppHalfMirror>(v);
     return v;
   }
 }
