@@ -223,7 +223,7 @@ def bench_c3(args) -> int:
     t0 = time.perf_counter()
     weights = synthetic_weights(cfg, seed=0)
     eng = BatchEngine(cfg, weights, batch=batch, device="cuda:0", max_new=steps,
-                      prompt_room=ctx)
+                      prompt_room=ctx, splits=args.c3_splits)
     prompts = []
     for b in range(batch):
         g = torch.Generator().manual_seed(1000 + b)
@@ -397,6 +397,9 @@ def main(argv=None) -> int:
     ap.add_argument("--c3-context", default="prefill", choices=("prefill", "walk"),
                     help="c3: build the 4096-token contexts by prefill (default) or by "
                          "walking them with batched decode steps")
+    ap.add_argument("--c3-splits", type=int, default=None, metavar="N",
+                    help="c3: attention splits per (sequence, kv head), each split's length "
+                         "following its sequence's position (default: the engine's choice)")
     ap.add_argument("--config", default="c2", choices=("c2", "c3"),
                     help="c2: the headline batch-1 workload; c3: batch 32 over 4096-token "
                          "contexts")

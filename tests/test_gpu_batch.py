@@ -226,12 +226,13 @@ def long_split_case():
 
 @pytest.mark.parametrize("split_tiles,splits", [(1, None), (2, None), (3, None), (4, None),
                                                (8, None), (None, None), (None, 1), (None, 2),
-                                               (None, 3)])
+                                               (None, 3), (None, 7)])
 def test_batch_engine_long_splits(gpu_device, long_split_case, split_tiles, splits):
     """Splits of several 64-position tiles (the long-context partition) against
     the oracle, with contexts past several splits: fixed split lengths, and
-    lengths derived from each sequence's position over 1, 2, 3 or the default
-    number of splits."""
+    lengths derived from each sequence's position over 1, 2, 3, 7 (one per
+    tile of the cache, so the last splits are empty) or the default number of
+    splits."""
     cfg, w, prompts, oracle_runs = long_split_case
     eng = BatchEngine(cfg, w, batch=3, device=gpu_device, max_new=8, prompt_room=400,
                       split_tiles=split_tiles, splits=splits)
